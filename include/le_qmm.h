@@ -1,0 +1,94 @@
+/*
+ * le_qmm.h -- C ABI of the MI355X-native GGUF quantized-matmul hot path.
+ *
+ * This is the drop-in boundary for the reference's quantized-matmul launch surface: the named
+ * kernel table `f: HashMap<&str, CudaFunction>` of src/gpu.rs:30,70-75 reached through
+ * Gpu::qx/mv_ptrs/mv (src/gpu.rs:223-238), prefill::mm/dense (src/gpu/prefill.rs:44-60) and
+ * DenseGpu::mvq/bmm (src/gpu/dense.rs:150-199). A Rust host binds these functions through FFI
+ * (see INTEGRATION.md for the extern block).
+ *
+ * Conventions
+ *   - Every entry returns an int status: LE_OK (0) or a negative LE_ERR_* code. The reference
+ *     panics on the same conditions (src/gpu.rs:221,233); a binding maps codes to its own errors.
+ *   - All pointers named w, x, y, out, logits, h, ws, ptrs, off, in_idx, out_idx are DEVICE
+ *     pointers owned by the caller. Weights are raw GGUF row bytes (src/gpu.rs:79-83), row-major:
+ *     `rows` rows of le_row_bytes(ty, cols) bytes; an expert slab e of a 3D tensor starts at
+ *     e * rows * row_bytes (src/cpu_ref.rs:110-115).
+ *   - `stream` is a hipStream_t (NULL = the null stream). Calls are asynchronous on it.
+ *   - A context is thread-compatible, not thread-safe: use one per host thread or lock around
+ *     it, as the reference drives one engine from one thread (src/local.rs:20,217).
+ *   - Nothing allocates device memory after le_init except le_init itself; entries that need
+ *     scratch take a caller-sized workspace.
+ *   - Activations are fp32; results are fp32 with fp32 accumulation (see DESIGN.md for the
+ *     error bound of the in-kernel 15-bit activation split).
+ *
+ * Supported types (GGML ids, src/quant.rs:13-20): Q8_0=8, Q4_K=12, Q6_K=14, IQ2_XXS=16, IQ3_XXS=18.
+ */
+#ifndef LE_QMM_H
+#define LE_QMM_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+typedef struct le_ctx le_ctx;
+typedef void *le_stream_t; /* hipStream_t */
+
+enum le_type { LE_Q8_0 = 8, LE_Q4_K = 12, LE_Q6_K = 14, LE_IQ2_XXS = 16, LE_IQ3_XXS = 18 };
+
+enum le_status {
+    LE_OK = 0,
+    LE_ERR_ARG = -1,    /* null pointer / bad count */
+    LE_ERR_TYPE = -2,   /* unsupported quant type (reference: panic!("no kernel for type"), src/gpu.rs:233) */
+    LE_ERR_SHAPE = -3,  /* cols not a multiple of 256, or rows/cols out of range */
+    LE_ERR_ALIGN = -4,  /* activation/output pointer or stride not 16-byte aligned */
+    LE_ERR_HIP = -5,    /* a HIP runtime call failed (reference: .expect("launch"), src/gpu.rs:221) */
+    LE_ERR_MODULE = -6, /* code object missing / unloadable, or device is not gfx950 */
+    LE_ERR_WORKSPACE = -7 /* workspace too small */
+};
+
+/* ---- geometry (src/quant.rs:24-35) ---- */
+
+/* Values and bytes per block of `ty`; returns LE_OK or LE_ERR_TYPE. (src/quant.rs:24-31) */
+int le_block_info(int ty, int *values, int *bytes);
+/* Bytes of one row of n values, 0 for an unsupported type. (src/quant.rs:35) */
+size_t le_row_bytes(int ty, size_t n);
+/* Human-readable text for a status code. */
+const char *le_status_str(int status);
+
+/* ---- context / module load (replaces the NVRTC compile + module load, src/gpu.rs:65-76) ---- */
+
+/* Loads the gfx950 code objects from `lib_dir` (NULL = the directory holding this library) on the
+ * current HIP device. */
+int le_init(const char *lib_dir, le_ctx **out);
+void le_destroy(le_ctx *ctx);
+/* Text of the last error raised on ctx (HIP error string or argument check). */
+const char *le_last_error(const le_ctx *ctx);
+
+/* ---- bit-exact dequantization (the device twin of quant::dequant_row, src/quant.rs:59-170) ---- */
+
+/* out[r * cols + c] = dequant(W[r])[c] for r < rows. */
+int le_dequant_rows(le_ctx *ctx, int ty, const void *w, float *out, int rows, int cols, le_stream_t stream);
+
+/* ---- batch-1 decode matvec (replaces matvec_<ty> + Gpu::mv_ptrs, src/cuda/kernels.cu:371-392,
+ *      src/gpu.rs:228-237) ----
+ * For slot s < slots: y[s * rows + r] = W_s[r,:] . x_s with W_s = ptrs[s] (device array of
+ * `slots` weight pointers) or, when ptrs is NULL, w + s * rows * row_bytes; x_s = x + s * xstride
+ * (xstride = 0 shares one activation, as the fused gate+up launch of src/gpu.rs:589 does). */
+int le_matvec(le_ctx *ctx, int ty, const void *const *ptrs, const void *w, const float *x, long long xstride,
+              float *y, int rows, int cols, int slots, le_stream_t stream);
+
+/* ---- small-M GEMM for speculative verify / prefill (replaces mmq*_<ty> + DenseGpu::bmm,
+ *      src/cuda/kernels.cu:965-1223, src/gpu/dense.rs:181-199; CPU twin cpu_ref::matmat,
+ *      src/cpu_ref.rs:266-276) ----
+ * Y[t * rows + r] = W[r,:] . X[t * cols ...] for t < m. */
+int le_gemm(le_ctx *ctx, int ty, const void *w, const float *x, int m, float *y, int rows, int cols,
+            le_stream_t stream);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* LE_QMM_H */

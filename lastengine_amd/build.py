@@ -1,0 +1,67 @@
+"""Build recipe for the native parts (run on the CPU build host; hipcc cross-compiles gfx950).
+
+Outputs (git-ignored, shipped with the tree):
+  lastengine_amd/lib/le_qmm_<part>.hsaco   gfx950 code objects, one per kernel part
+  lastengine_amd/lib/lible_qmm.so          host C-ABI library (include/le_qmm.h, include/le_quant.h)
+"""
+import os
+import subprocess
+import sys
+from concurrent.futures import ThreadPoolExecutor
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+REPO = os.path.dirname(HERE)
+CSRC = os.path.join(HERE, "csrc")
+LIB = os.path.join(HERE, "lib")
+ROCM = os.environ.get("ROCM_PATH", "/opt/rocm")
+HIPCC = os.environ.get("HIPCC", ROCM + "/bin/hipcc")
+
+# Packed FP32 instructions are disabled for all device code (they are not trusted on this pool).
+DEVICE_FLAGS = ["--offload-arch=gfx950", "-O3", "-std=c++17", "-Xclang", "-target-feature", "-Xclang",
+                "-packed-fp32-ops", "-I" + CSRC]
+PARTS = {"deq": ["-DLE_PART_DEQ"]}
+for _ty in (8, 12, 14, 16, 18):
+    PARTS["mv%d" % _ty] = ["-DLE_PART_MV=%d" % _ty]
+
+HOST_SOURCES = ["le_qmm.cpp", "le_quant.cpp"]
+
+
+def _run(cmd):
+    r = subprocess.run(cmd, stdout=subprocess.PIPE, stderr=subprocess.STDOUT, text=True)
+    out = "\n".join(l for l in r.stdout.splitlines() if "packed-fp32-ops" not in l and l.strip())
+    if r.returncode != 0:
+        raise RuntimeError("build step failed: %s\n%s" % (" ".join(cmd), out))
+    return out
+
+
+def code_object_cmd(part):
+    return [HIPCC, "--genco"] + DEVICE_FLAGS + PARTS[part] + [
+        os.path.join(CSRC, "le_qmm_kernels.hip"), "-o", os.path.join(LIB, "le_qmm_%s.hsaco" % part)]
+
+
+def host_lib_cmd():
+    # Host-only C++: the HIP runtime API is used through its C headers, no device pass.
+    return ["g++", "-O2", "-std=c++17", "-fPIC", "-shared", "-Wall", "-D__HIP_PLATFORM_AMD__",
+            "-I" + ROCM + "/include", "-I" + CSRC, "-I" + os.path.join(REPO, "include")] + [
+        os.path.join(CSRC, s) for s in HOST_SOURCES] + [
+        "-o", os.path.join(LIB, "lible_qmm.so"), "-L" + ROCM + "/lib", "-Wl,-rpath," + ROCM + "/lib",
+        "-lamdhip64", "-lpthread", "-ldl"]
+
+
+def oracle_cmd():
+    return ["make", "-s", "-C", os.path.join(REPO, "oracle")]
+
+
+def build(jobs=8, with_oracle=True, parts=None):
+    os.makedirs(LIB, exist_ok=True)
+    cmds = [code_object_cmd(p) for p in (parts or PARTS)] + [host_lib_cmd()]
+    if with_oracle:
+        cmds.append(oracle_cmd())
+    with ThreadPoolExecutor(max_workers=jobs) as ex:
+        for out in ex.map(_run, cmds):
+            if out:
+                print(out)
+
+
+if __name__ == "__main__":
+    build(parts=sys.argv[1:] or None)

@@ -1,0 +1,276 @@
+/* Host side of the C ABI in include/le_qmm.h.
+ *
+ * The context owns the gfx950 code objects (hipModuleLoad) and a name -> hipFunction_t table,
+ * the MI355X counterpart of the reference's NVRTC module and kernel map (src/gpu.rs:65-76).
+ * Launch policy (grid, LDS, kernel variant) mirrors the role of Gpu::mv_ptrs / prefill::mm /
+ * DenseGpu::bmm (src/gpu.rs:228-237, src/gpu/prefill.rs:44-56, src/gpu/dense.rs:181-199), with
+ * the shapes chosen for 256 CUs and wave64 instead of 32-lane warps.
+ */
+#include <dlfcn.h>
+#include <hip/hip_runtime.h>
+
+#include <cstdarg>
+#include <cstdio>
+#include <cstring>
+#include <map>
+#include <string>
+#include <vector>
+
+#include "../../include/le_qmm.h"
+#include "le_formats.h"
+
+namespace {
+
+const char *kParts[] = {"le_qmm_deq", "le_qmm_mv8", "le_qmm_mv12", "le_qmm_mv14", "le_qmm_mv16", "le_qmm_mv18"};
+
+/* Kernel argument block of le_mv_* (mirrors MvArgs in le_qmm_kernels.hip). */
+struct MvArgs {
+    const void *const *ptrs;
+    const void *w0;
+    unsigned long long w_slot_bytes;
+    const float *x;
+    long long x_slot, x_tok;
+    float *y;
+    long long y_slot, y_tok;
+    int rows, cols, ntok, pad;
+};
+
+int xtok_bytes(int K) { return (K / 8) * 16 + (K / 8) * 4 + (K / 32) * 4; }
+int table_bytes(int ty) {
+    if (ty == LE_TYPE_IQ2_XXS) return 4 * (256 + 512);
+    if (ty == LE_TYPE_IQ3_XXS) return 4 * (256 + 256);
+    return 0;
+}
+
+}  // namespace
+
+struct le_ctx {
+    int device = 0;
+    int cus = 256;
+    size_t lds_limit = 65536;
+    std::vector<hipModule_t> mods;
+    std::map<std::string, hipFunction_t> fns;
+    std::string err;
+
+    int fail(int code, const char *fmt, ...) {
+        char buf[512];
+        va_list ap;
+        va_start(ap, fmt);
+        vsnprintf(buf, sizeof buf, fmt, ap);
+        va_end(ap);
+        err = buf;
+        return code;
+    }
+    int hip(hipError_t e, const char *what) {
+        if (e == hipSuccess) return LE_OK;
+        return fail(LE_ERR_HIP, "%s: %s", what, hipGetErrorString(e));
+    }
+    hipFunction_t fn(const std::string &name) {
+        auto it = fns.find(name);
+        if (it != fns.end()) return it->second;
+        for (hipModule_t m : mods) {
+            hipFunction_t f = nullptr;
+            if (hipModuleGetFunction(&f, m, name.c_str()) == hipSuccess && f) {
+                fns[name] = f;
+                return f;
+            }
+        }
+        (void)hipGetLastError();
+        return nullptr;
+    }
+    int launch(const std::string &name, dim3 grid, int block, size_t lds, hipStream_t st, void **args) {
+        hipFunction_t f = fn(name);
+        if (!f) return fail(LE_ERR_MODULE, "kernel %s not found in the loaded code objects", name.c_str());
+        return hip(hipModuleLaunchKernel(f, grid.x, grid.y, grid.z, block, 1, 1, (unsigned)lds, st, args, nullptr),
+                   name.c_str());
+    }
+};
+
+namespace {
+
+bool supported(int ty) {
+    return ty == LE_TYPE_Q8_0 || ty == LE_TYPE_Q4_K || ty == LE_TYPE_Q6_K || ty == LE_TYPE_IQ2_XXS ||
+           ty == LE_TYPE_IQ3_XXS;
+}
+int sb_bytes(int ty) {
+    switch (ty) {
+    case LE_TYPE_Q8_0: return LE_SB_BYTES_Q8_0;
+    case LE_TYPE_Q4_K: return LE_SB_BYTES_Q4_K;
+    case LE_TYPE_Q6_K: return LE_SB_BYTES_Q6_K;
+    case LE_TYPE_IQ2_XXS: return LE_SB_BYTES_IQ2_XXS;
+    case LE_TYPE_IQ3_XXS: return LE_SB_BYTES_IQ3_XXS;
+    }
+    return 0;
+}
+bool al16(const void *p) { return ((uintptr_t)p & 15) == 0; }
+
+std::string lib_dir_of_this_so() {
+    Dl_info info;
+    if (dladdr((void *)&lib_dir_of_this_so, &info) && info.dli_fname) {
+        std::string p = info.dli_fname;
+        size_t s = p.rfind('/');
+        if (s != std::string::npos) return p.substr(0, s);
+    }
+    return ".";
+}
+
+/* Lanes per row: G groups of 8 lanes share a row; G is the largest of 8,4,2,1 dividing the
+ * super-block count, so every lane group gets the same number of super-blocks. */
+int pick_g(int nsb) {
+    for (int g = 8; g > 1; g >>= 1)
+        if (nsb % g == 0) return g;
+    return 1;
+}
+
+/* Matvec/matmul launcher: T tokens per pass, grid (workers, slots, ceil(ntok/T)). */
+int mv_launch(le_ctx *c, int ty, const void *const *ptrs, const void *w, const float *x, long long x_slot,
+              long long x_tok, float *y, long long y_slot, long long y_tok, int rows, int cols, int ntok, int slots,
+              hipStream_t st) {
+    if (!supported(ty)) return c->fail(LE_ERR_TYPE, "no kernel for type %d", ty);
+    if (rows <= 0 || cols <= 0 || ntok <= 0 || slots <= 0) return c->fail(LE_ERR_SHAPE, "empty shape");
+    if (cols % 256) return c->fail(LE_ERR_SHAPE, "cols=%d is not a multiple of 256", cols);
+    if (!x || !y || (!ptrs && !w)) return c->fail(LE_ERR_ARG, "null pointer");
+    if (!al16(x) || (x_slot % 4) || (x_tok % 4)) return c->fail(LE_ERR_ALIGN, "activations must be 16-byte aligned");
+    const int nsb = cols / 256, G = pick_g(nsb);
+    const int xb = xtok_bytes(cols), tb = table_bytes(ty);
+    int T = 1;
+    const int want = ntok >= 8 ? 8 : ntok >= 4 ? 4 : ntok >= 2 ? 2 : 1;
+    for (int t = want; t >= 1; t >>= 1)
+        if ((size_t)(t * xb + tb) <= c->lds_limit) { T = t; break; }
+    if ((size_t)(xb + tb) > c->lds_limit) return c->fail(LE_ERR_SHAPE, "cols=%d exceeds the LDS activation budget", cols);
+    const int rpw = 8 / G;
+    const long long nrb = (rows + rpw - 1) / rpw;
+    const long long need = (nrb + 3) / 4; /* 4 waves per block */
+    const long long cap = (long long)c->cus * 4;
+    long long gx = need;
+    if (need > cap) {
+        const long long iters = (need + cap - 1) / cap;
+        gx = (need + iters - 1) / iters;
+    }
+    MvArgs a{};
+    a.ptrs = ptrs;
+    a.w0 = w;
+    a.w_slot_bytes = (unsigned long long)rows * (unsigned long long)nsb * sb_bytes(ty);
+    a.x = x;
+    a.x_slot = x_slot;
+    a.x_tok = x_tok;
+    a.y = y;
+    a.y_slot = y_slot;
+    a.y_tok = y_tok;
+    a.rows = rows;
+    a.cols = cols;
+    a.ntok = ntok;
+    void *args[] = {&a};
+    char name[64];
+    snprintf(name, sizeof name, "le_mv_%d_g%d_t%d", ty, G, T);
+    return c->launch(name, dim3((unsigned)gx, (unsigned)slots, (unsigned)((ntok + T - 1) / T)), 256,
+                     (size_t)(T * xb + tb), st, args);
+}
+
+}  // namespace
+
+extern "C" {
+
+int le_block_info(int ty, int *values, int *bytes) {
+    int v, b;
+    if (!le_block_geometry(ty, &v, &b)) return LE_ERR_TYPE;
+    if (values) *values = v;
+    if (bytes) *bytes = b;
+    return LE_OK;
+}
+
+size_t le_row_bytes(int ty, size_t n) {
+    int v, b;
+    if (!le_block_geometry(ty, &v, &b)) return 0;
+    return n / (size_t)v * (size_t)b;
+}
+
+const char *le_status_str(int s) {
+    switch (s) {
+    case LE_OK: return "ok";
+    case LE_ERR_ARG: return "invalid argument";
+    case LE_ERR_TYPE: return "unsupported quant type";
+    case LE_ERR_SHAPE: return "unsupported shape";
+    case LE_ERR_ALIGN: return "misaligned pointer or stride";
+    case LE_ERR_HIP: return "HIP runtime error";
+    case LE_ERR_MODULE: return "code object missing or device unsupported";
+    case LE_ERR_WORKSPACE: return "workspace too small";
+    }
+    return "unknown status";
+}
+
+int le_init(const char *lib_dir, le_ctx **out) {
+    if (!out) return LE_ERR_ARG;
+    *out = nullptr;
+    le_ctx *c = new le_ctx();
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess) {
+        delete c;
+        return LE_ERR_HIP;
+    }
+    c->device = dev;
+    hipDeviceProp_t prop;
+    if (hipGetDeviceProperties(&prop, dev) != hipSuccess) {
+        delete c;
+        return LE_ERR_HIP;
+    }
+    if (strncmp(prop.gcnArchName, "gfx950", 6) != 0) {
+        delete c;
+        return LE_ERR_MODULE;
+    }
+    c->cus = prop.multiProcessorCount;
+    c->lds_limit = prop.sharedMemPerBlock;
+    const std::string dir = lib_dir ? lib_dir : lib_dir_of_this_so();
+    for (const char *part : kParts) {
+        hipModule_t m = nullptr;
+        const std::string path = dir + "/" + part + ".hsaco";
+        if (hipModuleLoad(&m, path.c_str()) != hipSuccess) {
+            for (hipModule_t mm : c->mods) (void)hipModuleUnload(mm);
+            delete c;
+            return LE_ERR_MODULE;
+        }
+        c->mods.push_back(m);
+    }
+    *out = c;
+    return LE_OK;
+}
+
+void le_destroy(le_ctx *c) {
+    if (!c) return;
+    for (hipModule_t m : c->mods) (void)hipModuleUnload(m);
+    delete c;
+}
+
+const char *le_last_error(const le_ctx *c) { return c ? c->err.c_str() : "null context"; }
+
+int le_dequant_rows(le_ctx *c, int ty, const void *w, float *out, int rows, int cols, le_stream_t stream) {
+    if (!c) return LE_ERR_ARG;
+    if (!supported(ty)) return c->fail(LE_ERR_TYPE, "no kernel for type %d", ty);
+    if (!w || !out) return c->fail(LE_ERR_ARG, "null pointer");
+    int v = 1, b = 0;
+    le_block_geometry(ty, &v, &b);
+    if (rows <= 0 || cols <= 0 || cols % v || cols % 32) return c->fail(LE_ERR_SHAPE, "bad shape %dx%d", rows, cols);
+    if (!al16(out) || (cols % 4)) return c->fail(LE_ERR_ALIGN, "output must be 16-byte aligned");
+    unsigned long long rb = (unsigned long long)(cols / v) * b;
+    const long long units = (long long)rows * (cols / 32);
+    long long blocks = (units + 255) / 256;
+    if (blocks > (long long)c->cus * 16) blocks = (long long)c->cus * 16;
+    char name[32];
+    snprintf(name, sizeof name, "le_dequant_%d", ty);
+    void *args[] = {(void *)&w, (void *)&out, (void *)&rows, (void *)&cols, (void *)&rb};
+    return c->launch(name, dim3((unsigned)blocks), 256, 0, (hipStream_t)stream, args);
+}
+
+int le_matvec(le_ctx *c, int ty, const void *const *ptrs, const void *w, const float *x, long long xstride, float *y,
+              int rows, int cols, int slots, le_stream_t stream) {
+    if (!c) return LE_ERR_ARG;
+    return mv_launch(c, ty, ptrs, w, x, xstride, 0, y, (long long)rows, 0, rows, cols, 1, slots, (hipStream_t)stream);
+}
+
+int le_gemm(le_ctx *c, int ty, const void *w, const float *x, int m, float *y, int rows, int cols,
+            le_stream_t stream) {
+    if (!c) return LE_ERR_ARG;
+    return mv_launch(c, ty, nullptr, w, x, 0, cols, y, 0, rows, rows, cols, m, 1, (hipStream_t)stream);
+}
+
+}  // extern "C"

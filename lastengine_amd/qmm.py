@@ -1,0 +1,169 @@
+"""ctypes binding of lible_qmm.so (include/le_qmm.h, include/le_quant.h).
+
+`Engine` mirrors the reference's launch surface for this path (src/gpu.rs:223-238 `mv_ptrs`/`mv`,
+src/gpu/prefill.rs:44-60 `mm`/`dense`, src/gpu/dense.rs:181-199 `bmm`): a context over the loaded
+gfx950 code objects whose methods take device buffers and launch on the current stream. Errors
+come back as LeError carrying the C status code (the reference panics on the same conditions,
+src/gpu.rs:221,233).
+
+Device buffers may be passed as torch tensors (their data_ptr is used) or as raw integer
+addresses. There is no CPU fallback: without the built library or a gfx950 device every entry
+raises.
+"""
+import ctypes
+import os
+
+import numpy as np
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_DIR = os.path.join(HERE, "lib")
+
+Q8_0, Q4_K, Q6_K, IQ2_XXS, IQ3_XXS = 8, 12, 14, 16, 18
+TYPES = {"Q8_0": Q8_0, "Q4_K": Q4_K, "Q6_K": Q6_K, "IQ2_XXS": IQ2_XXS, "IQ3_XXS": IQ3_XXS}
+
+_STATUS = {0: "ok", -1: "invalid argument", -2: "unsupported quant type", -3: "unsupported shape",
+           -4: "misaligned pointer or stride", -5: "HIP runtime error",
+           -6: "code object missing or device unsupported", -7: "workspace too small"}
+
+
+class LeError(RuntimeError):
+    def __init__(self, code, msg=""):
+        self.code = code
+        super().__init__("le_qmm error %d (%s)%s" % (code, _STATUS.get(code, "?"), (": " + msg) if msg else ""))
+
+
+def library_path():
+    return os.path.join(LIB_DIR, "lible_qmm.so")
+
+
+_lib = None
+
+
+def lib():
+    """Load lible_qmm.so once and declare the C signatures."""
+    global _lib
+    if _lib is not None:
+        return _lib
+    path = library_path()
+    if not os.path.exists(path):
+        raise LeError(-6, "%s is not built; run __graft_entry__.build() or lastengine_amd/build.py" % path)
+    L = ctypes.CDLL(path)
+    P, I, LL, S, F, D = ctypes.c_void_p, ctypes.c_int, ctypes.c_longlong, ctypes.c_size_t, ctypes.c_float, ctypes.c_double
+    sig = {
+        "le_block_info": (I, [I, ctypes.POINTER(I), ctypes.POINTER(I)]),
+        "le_row_bytes": (S, [I, S]),
+        "le_status_str": (ctypes.c_char_p, [I]),
+        "le_init": (I, [ctypes.c_char_p, ctypes.POINTER(P)]),
+        "le_destroy": (None, [P]),
+        "le_last_error": (ctypes.c_char_p, [P]),
+        "le_dequant_rows": (I, [P, I, P, P, I, I, P]),
+        "le_matvec": (I, [P, I, P, P, P, LL, P, I, I, I, P]),
+        "le_gemm": (I, [P, I, P, P, I, P, I, I, P]),
+        "le_fill_normal": (None, [P, S, ctypes.c_uint64, ctypes.c_uint64, D, D, I]),
+        "le_quantize_rows": (I, [I, P, P, S, S, I]),
+        "le_f32_to_f16": (ctypes.c_uint16, [F]),
+    }
+    for name, (res, args) in sig.items():
+        fn = getattr(L, name)
+        fn.restype = res
+        fn.argtypes = args
+    _lib = L
+    return L
+
+
+def _threads():
+    return max(1, min(16, os.cpu_count() or 1))
+
+
+def block_info(ty):
+    v, b = ctypes.c_int(), ctypes.c_int()
+    rc = lib().le_block_info(ty, ctypes.byref(v), ctypes.byref(b))
+    if rc:
+        raise LeError(rc)
+    return v.value, b.value
+
+
+def row_bytes(ty, n):
+    return int(lib().le_row_bytes(ty, n))
+
+
+def f32_to_f16(x):
+    return int(lib().le_f32_to_f16(float(x)))
+
+
+def fill_normal(n, seed, std=1.0, mean=0.0, offset=0):
+    """Seeded N(mean, std) float32 vector (splitmix64 + Box-Muller, see include/le_quant.h)."""
+    out = np.empty(int(n), dtype=np.float32)
+    lib().le_fill_normal(out.ctypes.data, out.size, ctypes.c_uint64(seed), ctypes.c_uint64(offset),
+                         float(mean), float(std), _threads())
+    return out
+
+
+def quantize_rows(ty, x):
+    """Quantize a (rows, cols) float32 array into GGUF blocks -> uint8 array (rows, row_bytes)."""
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    rows, cols = x.shape
+    out = np.empty((rows, row_bytes(ty, cols)), dtype=np.uint8)
+    rc = lib().le_quantize_rows(ty, x.ctypes.data, out.ctypes.data, rows, cols, _threads())
+    if rc:
+        raise LeError(rc)
+    return out
+
+
+def _ptr(t):
+    if t is None:
+        return None
+    if isinstance(t, int):
+        return t
+    return t.data_ptr()
+
+
+def _stream(stream):
+    if stream is None:
+        import torch
+        return torch.cuda.current_stream().cuda_stream
+    if isinstance(stream, int):
+        return stream
+    return stream.cuda_stream
+
+
+class Engine:
+    """One le_ctx: the gfx950 code objects loaded on the current device."""
+
+    def __init__(self, lib_dir=None):
+        self._L = lib()
+        self._ctx = ctypes.c_void_p()
+        rc = self._L.le_init(lib_dir.encode() if lib_dir else None, ctypes.byref(self._ctx))
+        if rc:
+            raise LeError(rc, "le_init (needs a gfx950 device and the built code objects in %s)" % (lib_dir or LIB_DIR))
+
+    def close(self):
+        if self._ctx:
+            self._L.le_destroy(self._ctx)
+            self._ctx = ctypes.c_void_p()
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+    def _check(self, rc):
+        if rc:
+            raise LeError(rc, (self._L.le_last_error(self._ctx) or b"").decode())
+
+    def dequant_rows(self, ty, w, out, rows, cols, stream=None):
+        self._check(self._L.le_dequant_rows(self._ctx, ty, _ptr(w), _ptr(out), rows, cols, _stream(stream)))
+
+    def mv_ptrs(self, ty, ptrs, x, out, rows, cols, xstride, slots, w=None, stream=None):
+        """Gpu::mv_ptrs (src/gpu.rs:228): out[s*rows + r] = W_s[r] . x[s*xstride:]."""
+        self._check(self._L.le_matvec(self._ctx, ty, _ptr(ptrs), _ptr(w), _ptr(x), int(xstride), _ptr(out), rows,
+                                      cols, slots, _stream(stream)))
+
+    def mv(self, ty, w, x, out, rows, cols, stream=None):
+        """Gpu::mv (src/gpu.rs:238): one matrix, one activation."""
+        self.mv_ptrs(ty, None, x, out, rows, cols, 0, 1, w=w, stream=stream)
+
+    def gemm(self, ty, w, x, m, out, rows, cols, stream=None):
+        """DenseGpu::bmm (src/gpu/dense.rs:181): out[t*rows + r] = W[r] . x[t] for t < m."""
+        self._check(self._L.le_gemm(self._ctx, ty, _ptr(w), _ptr(x), m, _ptr(out), rows, cols, _stream(stream)))

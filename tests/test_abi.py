@@ -1,0 +1,96 @@
+"""Host-side checks of the C ABI that need no GPU: the library loads, exports every function the
+headers declare, computes geometry like src/quant.rs:24-35, and rejects bad arguments with status
+codes instead of crashing."""
+import ctypes
+import os
+import re
+
+import numpy as np
+import pytest
+
+import lastengine_amd as le
+from lastengine_amd import qmm
+from tests.conftest import REPO
+
+HEADERS = [os.path.join(REPO, "include", h) for h in ("le_qmm.h", "le_quant.h")]
+
+
+def declared_functions():
+    names = []
+    for h in HEADERS:
+        txt = open(h).read()
+        txt = re.sub(r"/\*.*?\*/", "", txt, flags=re.S)
+        names += re.findall(r"^\s*(?:const\s+)?[a-z_0-9]+\s*\**\s*(le_[a-z_0-9]+)\s*\(", txt, flags=re.M)
+    return sorted(set(names))
+
+
+def test_library_exports_every_declared_symbol():
+    names = declared_functions()
+    assert "le_matvec" in names and "le_init" in names and "le_quantize_rows" in names
+    L = ctypes.CDLL(qmm.library_path())
+    missing = [n for n in names if not hasattr(L, n)]
+    assert not missing, missing
+
+
+def test_code_objects_built():
+    for part in ("deq", "mv8", "mv12", "mv14", "mv16", "mv18"):
+        assert os.path.getsize(os.path.join(qmm.LIB_DIR, "le_qmm_%s.hsaco" % part)) > 1000
+
+
+@pytest.mark.parametrize("ty,cols,want", [(8, 4096, 4352), (12, 4096, 2304), (14, 14336, 11760),
+                                          (16, 4096, 1056), (18, 14336, 5488), (12, 2048, 1152),
+                                          (14, 768, 630)])
+def test_row_bytes(ty, cols, want):
+    assert le.row_bytes(ty, cols) == want
+
+
+def test_block_info_and_bad_type():
+    assert le.block_info(le.Q4_K) == (256, 144)
+    assert le.block_info(le.Q8_0) == (32, 34)
+    with pytest.raises(le.LeError) as e:
+        le.block_info(99)
+    assert e.value.code == -2
+    assert le.row_bytes(99, 256) == 0
+
+
+def test_quantize_errors():
+    L = qmm.lib()
+    x = np.zeros(300, dtype=np.float32)
+    out = np.zeros(1024, dtype=np.uint8)
+    assert L.le_quantize_rows(12, x.ctypes.data, out.ctypes.data, 1, 300, 1) == -3  # not a block multiple
+    assert L.le_quantize_rows(7, x.ctypes.data, out.ctypes.data, 1, 256, 1) == -2
+    assert L.le_quantize_rows(12, None, out.ctypes.data, 1, 256, 1) == -1
+
+
+def test_fill_normal_deterministic_and_threaded():
+    a = le.fill_normal(100003, 42)
+    L = qmm.lib()
+    b = np.empty_like(a)
+    L.le_fill_normal(b.ctypes.data, b.size, ctypes.c_uint64(42), ctypes.c_uint64(0), 0.0, 1.0, 1)
+    assert np.array_equal(a, b)
+    c = le.fill_normal(1000, 42, offset=500)
+    assert np.array_equal(c, a[500:1500])
+    assert abs(a.mean()) < 0.02 and abs(a.std() - 1) < 0.02
+
+
+def test_f32_to_f16_matches_numpy():
+    rng = np.random.default_rng(5)
+    vals = np.concatenate([rng.normal(size=2000).astype(np.float32) * 10.0 ** rng.integers(-9, 6, size=2000),
+                           np.array([0.0, -0.0, 65504.0, 65520.0, 1e-8, 5.96e-8, 2.98e-8, np.inf, -np.inf],
+                                    dtype=np.float32)])
+    for v in vals:
+        assert le.f32_to_f16(v) == int(np.array(v, dtype=np.float16).view(np.uint16)), v
+
+
+def test_quantizer_is_deterministic():
+    src = le.fill_normal(4 * 1024, 7, std=0.02).reshape(4, 1024)
+    for ty in le.TYPES.values():
+        assert np.array_equal(le.quantize_rows(ty, src), le.quantize_rows(ty, src))
+
+
+def test_init_without_gpu_fails_cleanly():
+    import torch
+    if torch.cuda.is_available():
+        pytest.skip("GPU present")
+    with pytest.raises(le.LeError):
+        le.Engine()

@@ -1,0 +1,182 @@
+"""GPU parity: the HIP path (through the C ABI) against the CPU oracle on identical seeded inputs.
+
+Bars: dequantized weights bit-exact; matvec/GEMM outputs within max|d|/max|want| <= 1e-3 and
+|d| <= 1e-3 * sum|w*x| per output (tests/util.py)."""
+import numpy as np
+import pytest
+
+import lastengine_amd as le
+import oracle
+from tests.util import weights, acts, check_close
+
+pytestmark = pytest.mark.gpu
+
+NAMES = list(le.TYPES)
+
+
+def dev(a):
+    import torch
+    return torch.from_numpy(np.ascontiguousarray(a)).cuda()
+
+
+def sync():
+    import torch
+    torch.cuda.synchronize()
+
+
+def absmag(ty, q, rows, cols, xs):
+    w = oracle.dequant_rows(ty, q, rows, cols).astype(np.float64)
+    return np.abs(np.atleast_2d(xs).astype(np.float64)) @ np.abs(w).T
+
+
+# ------------------------------------------------------------------ dequant
+
+@pytest.mark.parametrize("name", NAMES)
+@pytest.mark.parametrize("rows,cols", [(8, 1024), (37, 2048), (3, 4096)])
+def test_dequant_bit_exact(engine, name, rows, cols):
+    import torch
+    ty = le.TYPES[name]
+    q, _ = weights(ty, rows, cols, seed=rows * 1000 + cols)
+    out = torch.empty(rows, cols, dtype=torch.float32, device="cuda")
+    engine.dequant_rows(ty, dev(q), out, rows, cols)
+    sync()
+    want = oracle.dequant_rows(ty, q, rows, cols)
+    assert np.array_equal(out.cpu().numpy().view(np.uint32), want.view(np.uint32))
+
+
+@pytest.mark.parametrize("name", NAMES)
+def test_dequant_random_bytes_bit_exact(engine, name):
+    """Arbitrary block bytes, including f16 scales that are subnormal, Inf or NaN."""
+    import torch
+    ty = le.TYPES[name]
+    rows, cols = 16, 1024
+    rng = np.random.default_rng(ty)
+    q = rng.integers(0, 256, size=(rows, le.row_bytes(ty, cols)), dtype=np.uint8)
+    out = torch.empty(rows, cols, dtype=torch.float32, device="cuda")
+    engine.dequant_rows(ty, dev(q), out, rows, cols)
+    sync()
+    want = oracle.dequant_rows(ty, q, rows, cols)
+    assert np.array_equal(out.cpu().numpy().view(np.uint32), want.view(np.uint32))
+
+
+# ------------------------------------------------------------------ matvec
+
+@pytest.mark.parametrize("name", NAMES)
+@pytest.mark.parametrize("rows,cols", [(64, 256), (100, 1024), (333, 4096), (77, 768), (40, 14336), (1, 512)])
+def test_matvec_parity(engine, name, rows, cols):
+    import torch
+    ty = le.TYPES[name]
+    q, _ = weights(ty, rows, cols, seed=rows + cols + ty)
+    x = acts(cols, seed=cols + 7)
+    y = torch.empty(rows, dtype=torch.float32, device="cuda")
+    engine.mv(ty, dev(q), dev(x), y, rows, cols)
+    sync()
+    want = oracle.matvec(ty, q, rows, cols, x)
+    check_close(y.cpu().numpy(), want, absmag(ty, q, rows, cols, x)[0])
+
+
+def test_matvec_slots_ptr_table(engine):
+    """mv_ptrs semantics: slot s reads ptrs[s] and x + s*xstride, writes y[s*rows:]."""
+    import torch
+    ty, rows, cols, slots = le.Q4_K, 96, 2048, 3
+    qs = [weights(ty, rows, cols, seed=500 + s)[0] for s in range(slots)]
+    xs = np.stack([acts(cols, 600 + s) for s in range(slots)])
+    bufs = [dev(q) for q in qs]
+    ptrs = torch.tensor([b.data_ptr() for b in bufs], dtype=torch.int64, device="cuda")
+    y = torch.empty(slots * rows, dtype=torch.float32, device="cuda")
+    engine.mv_ptrs(ty, ptrs, dev(xs), y, rows, cols, cols, slots)
+    sync()
+    got = y.cpu().numpy().reshape(slots, rows)
+    for s in range(slots):
+        check_close(got[s], oracle.matvec(ty, qs[s], rows, cols, xs[s]), absmag(ty, qs[s], rows, cols, xs[s])[0])
+    # shared activation (xstride = 0) over a contiguous slab (no pointer table)
+    slab = np.concatenate(qs, axis=0)
+    y2 = torch.empty(slots * rows, dtype=torch.float32, device="cuda")
+    engine.mv_ptrs(ty, None, dev(xs[0]), y2, rows, cols, 0, slots, w=dev(slab))
+    sync()
+    got = y2.cpu().numpy().reshape(slots, rows)
+    for s in range(slots):
+        check_close(got[s], oracle.matvec(ty, qs[s], rows, cols, xs[0]), absmag(ty, qs[s], rows, cols, xs[0])[0])
+
+
+# configs 1, 2 and 5 at their full sizes
+FULL = [("Q4_K", 4096, 4096), ("Q4_K", 14336, 4096), ("Q4_K", 1024, 4096), ("Q6_K", 4096, 14336),
+        ("Q8_0", 32000, 4096), ("IQ2_XXS", 14336, 4096), ("IQ3_XXS", 4096, 14336)]
+
+
+@pytest.mark.parametrize("name,rows,cols", FULL)
+def test_matvec_config_sizes(engine, name, rows, cols):
+    import torch
+    ty = le.TYPES[name]
+    q, _ = weights(ty, rows, cols, seed=rows * 7 + cols)
+    x = acts(cols, seed=cols)
+    y = torch.empty(rows, dtype=torch.float32, device="cuda")
+    engine.mv(ty, dev(q), dev(x), y, rows, cols)
+    sync()
+    want = oracle.matvec(ty, q, rows, cols, x)
+    check_close(y.cpu().numpy(), want, absmag(ty, q, rows, cols, x)[0])
+
+
+# ------------------------------------------------------------------ small-M GEMM
+
+@pytest.mark.parametrize("name", NAMES)
+@pytest.mark.parametrize("m", [1, 2, 3, 4, 5, 8, 13, 16])
+def test_gemm_small_m(engine, name, m):
+    import torch
+    ty = le.TYPES[name]
+    rows, cols = 200, 1024
+    q, _ = weights(ty, rows, cols, seed=900 + ty)
+    xs = np.stack([acts(cols, 1000 + t) for t in range(m)])
+    y = torch.empty(m, rows, dtype=torch.float32, device="cuda")
+    engine.gemm(ty, dev(q), dev(xs), m, y, rows, cols)
+    sync()
+    want = oracle.matmat(ty, q, rows, cols, xs)
+    check_close(y.cpu().numpy(), want, absmag(ty, q, rows, cols, xs))
+
+
+@pytest.mark.parametrize("m", [4, 8, 16, 64])
+def test_gemm_config3(engine, m):
+    import torch
+    ty, rows, cols = le.Q4_K, 14336, 4096
+    q, _ = weights(ty, rows, cols, seed=3)
+    xs = np.stack([acts(cols, 2000 + t) for t in range(m)])
+    y = torch.empty(m, rows, dtype=torch.float32, device="cuda")
+    engine.gemm(ty, dev(q), dev(xs), m, y, rows, cols)
+    sync()
+    want = oracle.matmat(ty, q, rows, cols, xs)
+    check_close(y.cpu().numpy(), want, absmag(ty, q, rows, cols, xs))
+
+
+# ------------------------------------------------------------------ edge cases and errors
+
+def test_zero_activation_and_zero_weights(engine):
+    import torch
+    ty, rows, cols = le.Q4_K, 64, 1024
+    q, _ = weights(ty, rows, cols, seed=1)
+    y = torch.full((rows,), 7.0, dtype=torch.float32, device="cuda")
+    engine.mv(ty, dev(q), dev(np.zeros(cols, np.float32)), y, rows, cols)
+    sync()
+    assert np.all(y.cpu().numpy() == 0.0)
+    zq = np.zeros_like(q)
+    engine.mv(ty, dev(zq), dev(acts(cols, 2)), y, rows, cols)
+    sync()
+    assert np.all(y.cpu().numpy() == 0.0)
+
+
+def test_error_codes(engine):
+    import torch
+    x = torch.zeros(1024 + 4, dtype=torch.float32, device="cuda")
+    w = torch.zeros(64 * 1024, dtype=torch.uint8, device="cuda")
+    y = torch.zeros(64, dtype=torch.float32, device="cuda")
+    with pytest.raises(le.LeError) as e:
+        engine.mv(99, w, x, y, 8, 1024)
+    assert e.value.code == -2
+    with pytest.raises(le.LeError) as e:
+        engine.mv(le.Q4_K, w, x, y, 8, 1000)
+    assert e.value.code == -3
+    with pytest.raises(le.LeError) as e:
+        engine.mv(le.Q4_K, w, x.data_ptr() + 4, y, 8, 1024)
+    assert e.value.code == -4
+    with pytest.raises(le.LeError) as e:
+        engine.mv(le.Q4_K, w, x, y, 0, 1024)
+    assert e.value.code == -3
