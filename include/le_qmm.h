@@ -4,8 +4,8 @@
  * This is the drop-in boundary for the reference's quantized-matmul launch surface: the named
  * kernel table `f: HashMap<&str, CudaFunction>` of src/gpu.rs:30,70-75 reached through
  * Gpu::qx/mv_ptrs/mv (src/gpu.rs:223-238), prefill::mm/dense (src/gpu/prefill.rs:44-60) and
- * DenseGpu::mvq/bmm (src/gpu/dense.rs:150-199). A Rust host binds these functions through FFI
- * (see INTEGRATION.md for the extern block).
+ * DenseGpu::mvq/bmm (src/gpu/dense.rs:150-199). A Rust host binds these functions through an
+ * `extern "C"` FFI block.
  *
  * Conventions
  *   - Every entry returns an int status: LE_OK (0) or a negative LE_ERR_* code. The reference
@@ -17,10 +17,10 @@
  *   - `stream` is a hipStream_t (NULL = the null stream). Calls are asynchronous on it.
  *   - A context is thread-compatible, not thread-safe: use one per host thread or lock around
  *     it, as the reference drives one engine from one thread (src/local.rs:20,217).
- *   - Nothing allocates device memory after le_init except le_init itself; entries that need
- *     scratch take a caller-sized workspace.
- *   - Activations are fp32; results are fp32 with fp32 accumulation (see DESIGN.md for the
- *     error bound of the in-kernel 15-bit activation split).
+ *   - No entry allocates device memory; entries that need scratch take a caller-sized workspace.
+ *   - Activations are fp32; results are fp32 with fp32 accumulation. Inside the kernels each
+ *     32-value activation block is held as a 15-bit integer split into two int8 planes with an
+ *     fp32 scale (error <= 3.1e-5 of the block maximum per value); weight codes are exact.
  *
  * Supported types (GGML ids, src/quant.rs:13-20): Q8_0=8, Q4_K=12, Q6_K=14, IQ2_XXS=16, IQ3_XXS=18.
  */
@@ -67,6 +67,11 @@ int le_init(const char *lib_dir, le_ctx **out);
 void le_destroy(le_ctx *ctx);
 /* Text of the last error raised on ctx (HIP error string or argument check). */
 const char *le_last_error(const le_ctx *ctx);
+/* Launch-policy knobs (the counterpart of the reference's LE_MMQ* / LE_TMAX env switches,
+ * src/gpu/dense.rs:182-192): "mv_block" threads per decode block (512, 1024), "mv_blocks_per_cu" grid cap,
+ * "mv_shape" rows x super-blocks in flight per lane and step (0 auto, 1: 1x2, 2: 2x1, 3: 2x2,
+ * 4: 4x1). */
+int le_set_option(le_ctx *ctx, const char *name, int value);
 
 /* ---- bit-exact dequantization (the device twin of quant::dequant_row, src/quant.rs:59-170) ---- */
 

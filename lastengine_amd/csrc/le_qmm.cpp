@@ -35,7 +35,7 @@ struct MvArgs {
     int rows, cols, ntok, pad;
 };
 
-int xtok_bytes(int K) { return (K / 8) * 16 + (K / 8) * 4 + (K / 32) * 4; }
+int xtok_bytes(int K) { return (K / 8) * 24; }
 int table_bytes(int ty) {
     if (ty == LE_TYPE_IQ2_XXS) return 4 * (256 + 512);
     if (ty == LE_TYPE_IQ3_XXS) return 4 * (256 + 256);
@@ -48,6 +48,13 @@ struct le_ctx {
     int device = 0;
     int cus = 256;
     size_t lds_limit = 65536;
+    /* launch-policy options (le_set_option) */
+    int mv_block = 1024;      /* threads per decode (T = 1) matvec block: 512 or 1024 */
+    int mv_blocks_per_cu = 1; /* grid cap = CUs * this */
+    int mv_shape = 0;        /* (rows, steps) per lane: 0 auto, 1 (1,2), 2 (2,1), 3 (2,2), 4 (4,1) */
+    int mq = 1;              /* decode matvec on MFMA where available */
+    int mq_waves = 4, mq_steps = 2, mq_blocks_per_cu = 4;
+    int ms = 1, ms_p = 2;    /* staged MFMA variant and its super-blocks per row and step */
     std::vector<hipModule_t> mods;
     std::map<std::string, hipFunction_t> fns;
     std::string err;
@@ -70,12 +77,14 @@ struct le_ctx {
         if (it != fns.end()) return it->second;
         for (hipModule_t m : mods) {
             hipFunction_t f = nullptr;
-            if (hipModuleGetFunction(&f, m, name.c_str()) == hipSuccess && f) {
+            const hipError_t e = hipModuleGetFunction(&f, m, name.c_str());
+            /* a miss in one module must not leave a sticky error behind for the caller */
+            (void)hipGetLastError();
+            if (e == hipSuccess && f) {
                 fns[name] = f;
                 return f;
             }
         }
-        (void)hipGetLastError();
         return nullptr;
     }
     int launch(const std::string &name, dim3 grid, int block, size_t lds, hipStream_t st, void **args) {
@@ -122,6 +131,42 @@ int pick_g(int nsb) {
     return 1;
 }
 
+/* MFMA decode matvec (Q4_K): one block of mq_waves waves per 16-row tile at a time. */
+int mq_launch(le_ctx *c, const void *const *ptrs, const void *w, const float *x, long long x_slot, float *y,
+              long long y_slot, int rows, int cols, int slots, hipStream_t st) {
+    const int nsb = cols / 256, NW = c->mq_waves, U = c->mq_steps;
+    const long long ntile = (rows + 15) / 16;
+    long long gx = ntile, cap = (long long)c->cus * c->mq_blocks_per_cu;
+    if (gx > cap) {
+        const long long it = (gx + cap - 1) / cap;
+        gx = (gx + it - 1) / it;
+    }
+    MvArgs a{};
+    a.ptrs = ptrs;
+    a.w0 = w;
+    a.w_slot_bytes = (unsigned long long)rows * nsb * 144ull;
+    a.x = x;
+    a.x_slot = x_slot;
+    a.y = y;
+    a.y_slot = y_slot;
+    a.rows = rows;
+    a.cols = cols;
+    a.ntok = 1;
+    void *args[] = {&a};
+    char name[64];
+    size_t lds = (size_t)nsb * 608 + (size_t)NW * 64;
+    int P = c->ms_p;
+    while (P > 1 && nsb % P) P >>= 1;
+    if (c->ms) {
+        const int cpr = 9 * P + 1, ni = (16 * cpr + 63) / 64;
+        snprintf(name, sizeof name, "le_ms_12_p%d_w%d", P, NW);
+        lds += (size_t)NW * ni * 64 * 16 + (size_t)NW * 64;
+        return c->launch(name, dim3((unsigned)gx, (unsigned)slots), NW * 64, lds, st, args);
+    }
+    snprintf(name, sizeof name, "le_mq_12_w%d_u%d", NW, U);
+    return c->launch(name, dim3((unsigned)gx, (unsigned)slots), NW * 64, lds, st, args);
+}
+
 /* Matvec/matmul launcher: T tokens per pass, grid (workers, slots, ceil(ntok/T)). */
 int mv_launch(le_ctx *c, int ty, const void *const *ptrs, const void *w, const float *x, long long x_slot,
               long long x_tok, float *y, long long y_slot, long long y_tok, int rows, int cols, int ntok, int slots,
@@ -131,17 +176,25 @@ int mv_launch(le_ctx *c, int ty, const void *const *ptrs, const void *w, const f
     if (cols % 256) return c->fail(LE_ERR_SHAPE, "cols=%d is not a multiple of 256", cols);
     if (!x || !y || (!ptrs && !w)) return c->fail(LE_ERR_ARG, "null pointer");
     if (!al16(x) || (x_slot % 4) || (x_tok % 4)) return c->fail(LE_ERR_ALIGN, "activations must be 16-byte aligned");
-    const int nsb = cols / 256, G = pick_g(nsb);
+    const int nsb = cols / 256, G = pick_g(nsb), S = nsb / G;
+    if (ty == LE_TYPE_Q4_K && ntok == 1 && c->mq && (size_t)nsb * 608 + 1024 <= c->lds_limit)
+        return mq_launch(c, ptrs, w, x, x_slot, y, y_slot, rows, cols, slots, st);
     const int xb = xtok_bytes(cols), tb = table_bytes(ty);
     int T = 1;
     const int want = ntok >= 8 ? 8 : ntok >= 4 ? 4 : ntok >= 2 ? 2 : 1;
     for (int t = want; t >= 1; t >>= 1)
         if ((size_t)(t * xb + tb) <= c->lds_limit) { T = t; break; }
     if ((size_t)(xb + tb) > c->lds_limit) return c->fail(LE_ERR_SHAPE, "cols=%d exceeds the LDS activation budget", cols);
+    static const int kRW[5] = {0, 1, 2, 2, 4}, kCH[5] = {0, 2, 1, 2, 1};
+    int shape = c->mv_shape ? c->mv_shape : (S == 1 ? 4 : 3);
+    if (T > 1 && shape < 3) shape = 3;
+    const int RW = kRW[shape], CH = kCH[shape];
+    const int block = T == 1 ? c->mv_block : 256;
+    const int nwave = block / 64;
     const int rpw = 8 / G;
-    const long long nrb = (rows + rpw - 1) / rpw;
-    const long long need = (nrb + 3) / 4; /* 4 waves per block */
-    const long long cap = (long long)c->cus * 4;
+    const long long nrb = (rows + rpw * RW - 1) / (rpw * RW);
+    const long long need = (nrb + nwave - 1) / nwave;
+    const long long cap = (long long)c->cus * c->mv_blocks_per_cu;
     long long gx = need;
     if (need > cap) {
         const long long iters = (need + cap - 1) / cap;
@@ -161,9 +214,9 @@ int mv_launch(le_ctx *c, int ty, const void *const *ptrs, const void *w, const f
     a.cols = cols;
     a.ntok = ntok;
     void *args[] = {&a};
-    char name[64];
-    snprintf(name, sizeof name, "le_mv_%d_g%d_t%d", ty, G, T);
-    return c->launch(name, dim3((unsigned)gx, (unsigned)slots, (unsigned)((ntok + T - 1) / T)), 256,
+    char name[96];
+    snprintf(name, sizeof name, "le_mv_%d_g%d_t%d_r%d_c%d_b%d", ty, G, T, RW, CH, block);
+    return c->launch(name, dim3((unsigned)gx, (unsigned)slots, (unsigned)((ntok + T - 1) / T)), block,
                      (size_t)(T * xb + tb), st, args);
 }
 
@@ -220,6 +273,7 @@ int le_init(const char *lib_dir, le_ctx **out) {
     }
     c->cus = prop.multiProcessorCount;
     c->lds_limit = prop.sharedMemPerBlock;
+
     const std::string dir = lib_dir ? lib_dir : lib_dir_of_this_so();
     for (const char *part : kParts) {
         hipModule_t m = nullptr;
@@ -242,6 +296,40 @@ void le_destroy(le_ctx *c) {
 }
 
 const char *le_last_error(const le_ctx *c) { return c ? c->err.c_str() : "null context"; }
+
+int le_set_option(le_ctx *c, const char *name, int value) {
+    if (!c || !name) return LE_ERR_ARG;
+    const std::string n = name;
+    if (n == "mv_block") {
+        if (value != 512 && value != 1024) return c->fail(LE_ERR_ARG, "mv_block must be 512 or 1024");
+        c->mv_block = value;
+    } else if (n == "mv_blocks_per_cu") {
+        if (value < 1 || value > 64) return c->fail(LE_ERR_ARG, "mv_blocks_per_cu must be 1..64");
+        c->mv_blocks_per_cu = value;
+    } else if (n == "mq") {
+        c->mq = value ? 1 : 0;
+    } else if (n == "ms") {
+        c->ms = value ? 1 : 0;
+    } else if (n == "ms_p") {
+        if (value != 1 && value != 2 && value != 4) return c->fail(LE_ERR_ARG, "ms_p must be 1, 2 or 4");
+        c->ms_p = value;
+    } else if (n == "mq_waves") {
+        if (value != 2 && value != 4 && value != 8) return c->fail(LE_ERR_ARG, "mq_waves must be 2, 4 or 8");
+        c->mq_waves = value;
+    } else if (n == "mq_steps") {
+        if (value != 1 && value != 2 && value != 4) return c->fail(LE_ERR_ARG, "mq_steps must be 1, 2 or 4");
+        c->mq_steps = value;
+    } else if (n == "mq_blocks_per_cu") {
+        if (value < 1 || value > 32) return c->fail(LE_ERR_ARG, "mq_blocks_per_cu must be 1..32");
+        c->mq_blocks_per_cu = value;
+    } else if (n == "mv_shape") {
+        if (value < 0 || value > 4) return c->fail(LE_ERR_ARG, "mv_shape must be 0..4");
+        c->mv_shape = value;
+    } else {
+        return c->fail(LE_ERR_ARG, "unknown option %s", name);
+    }
+    return LE_OK;
+}
 
 int le_dequant_rows(le_ctx *c, int ty, const void *w, float *out, int rows, int cols, le_stream_t stream) {
     if (!c) return LE_ERR_ARG;

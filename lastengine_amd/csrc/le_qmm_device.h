@@ -1,21 +1,23 @@
 /* Device-side building blocks of the quantized matmul kernels (gfx950, wave64).
  *
  * Work decomposition. Every type is handled in 256-value super-blocks (one K-quant/IQ block, or
- * eight Q8_0 blocks). Eight lanes cooperate on one super-block; each lane owns 32 of its values,
- * split into four groups of 8 consecutive activation positions. A lane decodes its 32 weights into
- * eight packed int8x4 words plus, per group, a float weight scale `sig` and (K-quants with an
- * offset) a float offset scale `mu`, so that
+ * eight Q8_0 blocks). Eight lanes cooperate on one super-block; each lane owns 32 of its values.
+ * A lane decodes its 32 weights into eight packed int8x4 words organised as NSEG segments of
+ * WPS words (4*WPS consecutive activation positions sharing one weight scale). Per segment the
+ * lane holds a float weight scale `sig` and, for K-quants with an offset, a float offset scale
+ * `mu`, so that
  *
- *     sum_{8 values} w * x  ==  sig * (dx * sum q*v) - mu * (dx * sum v)
+ *     sum_{segment} w * x  ==  sig * dx * sum(q * v)  -  mu * sum(dx * v)
  *
  * where x ~= dx * v is the activation held in LDS as a 15-bit integer v = 128*xh + xl split into
- * two int8 planes (xh, xl) with one fp32 scale dx per 32 values. The integer dot is exact
+ * two int8 planes (xh, xl), with one fp32 scale dx per 32 values. The integer dot is exact
  * (v_dot4_i32_i8 on both planes), so the only approximation is the activation rounding,
- * |x - dx*v| <= dx/2 with dx = amax32 / 16256 (relative 3e-5 of the 32-value block maximum).
+ * |x - dx*v| <= dx/2 with dx = amax32 / 16256 (3.1e-5 of the 32-value block maximum).
  *
  * Weight bytes are read straight from the raw GGUF rows (the reference uploads raw GGUF bytes,
- * src/gpu.rs:79-83): Q4_K super-blocks are 16-byte aligned and are read with 128-bit loads; the
- * other types are only 2-byte aligned and use unaligned 64/128-bit loads.
+ * src/gpu.rs:79-83) through global-address-space loads: Q4_K super-blocks are 16-byte aligned and
+ * use 128-bit loads; the other types are only 2-byte aligned and use unaligned 32/64/128-bit
+ * loads, which gfx950 serves in one request per cache line.
  */
 #pragma once
 #include <hip/hip_runtime.h>
@@ -26,14 +28,31 @@
 typedef uint8_t u8;
 typedef uint32_t u32;
 
+#if defined(__HIP_DEVICE_COMPILE__)
+#define LE_GLOBAL __attribute__((address_space(1)))
+#else
+#define LE_GLOBAL /* host pass of a mixed host/device translation unit */
+#endif
 #define LE_XSPLIT 16256.0f /* 127 * 128: |v| <= 16256 so xh = (v+64)>>7 in [-127,127], xl in [-64,63] */
 
-template <typename T>
-__device__ __forceinline__ T ldu(const u8 *p) {
-    T v;
-    __builtin_memcpy(&v, p, sizeof(T));
-    return v;
+typedef uint2 __attribute__((aligned(2))) le_uint2_a2;
+typedef uint4 __attribute__((aligned(2))) le_uint4_a2;
+typedef u32 __attribute__((aligned(2))) le_u32_a2;
+typedef u32 le_v4u __attribute__((ext_vector_type(4)));
+
+/* Global loads (never flat: flat loads also count against the LDS wait counter). */
+__device__ __forceinline__ uint4 ldg16(const u8 *p) { /* 16-byte aligned, streamed once */
+    const le_v4u v = __builtin_nontemporal_load((const LE_GLOBAL le_v4u *)p);
+    return make_uint4(v.x, v.y, v.z, v.w);
 }
+__device__ __forceinline__ uint4 ldg16c(const u8 *p) { /* 16-byte aligned, cached (shared by 8 lanes) */
+    const le_v4u v = *(const LE_GLOBAL le_v4u *)p;
+    return make_uint4(v.x, v.y, v.z, v.w);
+}
+__device__ __forceinline__ uint4 ldg16u(const u8 *p) { return *(const LE_GLOBAL le_uint4_a2 *)p; }
+__device__ __forceinline__ uint2 ldg8u(const u8 *p) { return *(const LE_GLOBAL le_uint2_a2 *)p; }
+__device__ __forceinline__ u32 ldg4u(const u8 *p) { return *(const LE_GLOBAL le_u32_a2 *)p; }
+__device__ __forceinline__ u32 ldg2(const u8 *p) { return *(const LE_GLOBAL uint16_t *)p; }
 
 __device__ __forceinline__ float h2f(u32 bits16) {
     return (float)__builtin_bit_cast(_Float16, (uint16_t)bits16);
@@ -44,71 +63,140 @@ __device__ __forceinline__ int dot4(u32 a, u32 b, int c) {
 }
 
 /* LDS image of one token's activations: per 8-value group p, xq[p] = {xh word0, xh word1,
- * xl word0, xl word1}, fs[p] = dx * sum(v); per 32-value unit u, dx[u]. */
+ * xl word0, xl word1} and xs[p] = {dx of the group's 32-value unit, dx * sum(v) over the group}. */
 struct XTok {
     const uint4 *xq;
-    const float *fs;
-    const float *dx;
+    const float2 *xs;
 };
 
-/* Bytes of LDS needed for one token's activation image of K values. */
-__host__ __device__ inline int le_xtok_bytes(int K) { return (K / 8) * 16 + (K / 8) * 4 + (K / 32) * 4; }
+/* Bytes of LDS for one token's activation image of K values. */
+__host__ __device__ inline int le_xtok_bytes(int K) { return (K / 8) * (16 + 8); }
+
+/* LDS record order of the activation image. Lane li of a super-block's 8-lane group reads its
+ * c-th 8-value group (c = 0..3, segment-major) from record 32*sb + 8*(c ^ (sb & 3)) + li, so
+ * each 8-lane read touches 8 distinct 16-byte bank groups and neighbouring super-blocks differ in
+ * bits 3-4. The per-type maps from a natural group (unit uu of the super-block, group gw of the
+ * unit) to (li, c) follow each format's lane split:
+ *   XL_Q4K: li = 2*(uu>>1) + (gw>>1), c = 2*(uu&1) + (gw&1)
+ *   XL_Q6K: li = 4*(uu>>2) + gw,      c = uu & 3
+ *   XL_ROW: li = uu,                  c = gw          (Q8_0, IQ2_XXS, IQ3_XXS) */
+#define XL_ROW 0
+#define XL_Q4K 1
+#define XL_Q6K 2
+template <int XL>
+__device__ __forceinline__ int le_xpos(int p) {
+    const int u = p >> 2, gw = p & 3, sb = u >> 3, uu = u & 7;
+    int li, c;
+    if (XL == XL_Q4K) { li = 2 * (uu >> 1) + (gw >> 1); c = 2 * (uu & 1) + (gw & 1); }
+    else if (XL == XL_Q6K) { li = 4 * (uu >> 2) + gw; c = uu & 3; }
+    else { li = uu; c = gw; }
+    return 32 * sb + 8 * (c ^ (sb & 3)) + li;
+}
+
+/* Quantize 8 activations (one group) given the amax of their 32-value unit; record q. */
+__device__ __forceinline__ void le_quant_group(float4 a, float4 b, float am, uint4 *xq, float2 *xs, int p) {
+    const float inv = am > 0.f ? LE_XSPLIT / am : 0.f;
+    const float d = am / LE_XSPLIT;
+    const int v[8] = {(int)rintf(a.x * inv), (int)rintf(a.y * inv), (int)rintf(a.z * inv), (int)rintf(a.w * inv),
+                      (int)rintf(b.x * inv), (int)rintf(b.y * inv), (int)rintf(b.z * inv), (int)rintf(b.w * inv)};
+    u32 hw[2] = {0, 0}, lw[2] = {0, 0};
+    int s = 0;
+#pragma unroll
+    for (int i = 0; i < 8; i++) {
+        const int h = (v[i] + 64) >> 7;
+        const int l = v[i] - (h << 7);
+        hw[i >> 2] |= ((u32)h & 255u) << (8 * (i & 3));
+        lw[i >> 2] |= ((u32)l & 255u) << (8 * (i & 3));
+        s += v[i];
+    }
+    xq[p] = make_uint4(hw[0], hw[1], lw[0], lw[1]);
+    xs[p] = make_float2(d, d * (float)s);
+}
+
+__device__ __forceinline__ float amax8(float4 a, float4 b) {
+    return fmaxf(fmaxf(fmaxf(fabsf(a.x), fabsf(a.y)), fmaxf(fabsf(a.z), fabsf(a.w))),
+                 fmaxf(fmaxf(fabsf(b.x), fabsf(b.y)), fmaxf(fabsf(b.z), fabsf(b.w))));
+}
 
 /* Quantize one token's K activations (K % 32 == 0) into the LDS image. Called by all threads of
  * the block; 4 consecutive threads share a 32-value unit. */
-__device__ __forceinline__ void le_quant_x_lds(const float *__restrict__ x, int K, uint4 *xq, float *fs, float *dx) {
+template <int XL>
+__device__ __forceinline__ void le_quant_x_lds(const float *__restrict__ x, int K, uint4 *xq, float2 *xs) {
     const int ng = K >> 3;
+    const LE_GLOBAL float *xg = (const LE_GLOBAL float *)x;
     for (int p = threadIdx.x; p < ((ng + 3) & ~3); p += blockDim.x) {
         const bool ok = p < ng;
         float4 a = make_float4(0.f, 0.f, 0.f, 0.f), b = a;
         if (ok) {
-            a = *(const float4 *)(x + 8 * p);
-            b = *(const float4 *)(x + 8 * p + 4);
+            a = *(const LE_GLOBAL float4 *)(xg + 8 * p);
+            b = *(const LE_GLOBAL float4 *)(xg + 8 * p + 4);
         }
-        float am = fmaxf(fmaxf(fmaxf(fabsf(a.x), fabsf(a.y)), fmaxf(fabsf(a.z), fabsf(a.w))),
-                         fmaxf(fmaxf(fabsf(b.x), fabsf(b.y)), fmaxf(fabsf(b.z), fabsf(b.w))));
+        float am = amax8(a, b);
         am = fmaxf(am, __shfl_xor(am, 1));
         am = fmaxf(am, __shfl_xor(am, 2));
-        const float inv = am > 0.f ? LE_XSPLIT / am : 0.f;
-        const float d = am / LE_XSPLIT;
-        int v[8] = {(int)rintf(a.x * inv), (int)rintf(a.y * inv), (int)rintf(a.z * inv), (int)rintf(a.w * inv),
-                    (int)rintf(b.x * inv), (int)rintf(b.y * inv), (int)rintf(b.z * inv), (int)rintf(b.w * inv)};
-        u32 hw[2] = {0, 0}, lw[2] = {0, 0};
-        int s = 0;
-#pragma unroll
-        for (int i = 0; i < 8; i++) {
-            const int h = (v[i] + 64) >> 7;
-            const int l = v[i] - (h << 7);
-            hw[i >> 2] |= ((u32)h & 255u) << (8 * (i & 3));
-            lw[i >> 2] |= ((u32)l & 255u) << (8 * (i & 3));
-            s += v[i];
-        }
-        if (ok) {
-            xq[p] = make_uint4(hw[0], hw[1], lw[0], lw[1]);
-            fs[p] = d * (float)s;
-            if ((p & 3) == 0) dx[p >> 2] = d;
-        }
+        if (ok) le_quant_group(a, b, am, xq, xs, le_xpos<XL>(p));
     }
 }
 
-/* One lane's decoded share of a super-block: 8 int8x4 words (group k uses w[2k], w[2k+1]),
- * the activation group index p[k], and the scales of each group. */
-struct Dec {
-    u32 w[8];
-    int p[4];
-    float sig[4];
-    float mu[4];
+/* The same in two phases for one token with a compile-time block of BLOCK threads and at most
+ * XR groups per thread: load() issues the activation loads (before the weight loads, so they
+ * return first; addresses are clamped instead of predicated so the wait counters stay exact),
+ * store() quantizes into LDS. */
+template <int BLOCK, int XR>
+struct XLoad {
+    float4 a[XR], b[XR];
+    __device__ __forceinline__ void load(const float *__restrict__ x, int K) {
+        const int ng = K >> 3;
+        const LE_GLOBAL float *xg = (const LE_GLOBAL float *)x;
+#pragma unroll
+        for (int r = 0; r < XR; r++) {
+            const int p = min((int)threadIdx.x + r * BLOCK, ng - 1);
+            a[r] = *(const LE_GLOBAL float4 *)(xg + 8 * p);
+            b[r] = *(const LE_GLOBAL float4 *)(xg + 8 * p + 4);
+        }
+    }
+    template <int XL>
+    __device__ __forceinline__ void store(int K, uint4 *xq, float2 *xs) {
+        const int ng = K >> 3;
+#pragma unroll
+        for (int r = 0; r < XR; r++) {
+            if (r * BLOCK >= ng) break;
+            const int p = threadIdx.x + r * BLOCK;
+            float am = amax8(a[r], b[r]);
+            am = fmaxf(am, __shfl_xor(am, 1));
+            am = fmaxf(am, __shfl_xor(am, 2));
+            if (p < ng) le_quant_group(a[r], b[r], am, xq, xs, le_xpos<XL>(p));
+        }
+    }
 };
 
-/* Integer dot of one decoded group against one token's LDS image, returned already scaled. */
-template <bool HAS_MU>
-__device__ __forceinline__ float group_dot(const Dec &d, int k, const XTok &x) {
-    const uint4 q = x.xq[d.p[k]];
-    const int hi = dot4(d.w[2 * k], q.x, dot4(d.w[2 * k + 1], q.y, 0));
-    const int lo = dot4(d.w[2 * k], q.z, dot4(d.w[2 * k + 1], q.w, 0));
-    const float a = (float)((hi << 7) + lo) * x.dx[d.p[k] >> 2];
-    if (HAS_MU) return d.sig[k] * a - d.mu[k] * x.fs[d.p[k]];
-    return d.sig[k] * a;
+/* One lane's decoded share of a super-block: NSEG segments of WPS int8x4 words each; the lane's
+ * activation groups c = 0..3 are taken in segment order (segment k owns groups
+ * k*WPS/2 .. (k+1)*WPS/2 - 1). */
+template <int NSEG, int WPS>
+struct Dec {
+    u32 w[NSEG * WPS];
+    float sig[NSEG];
+    float mu[NSEG];
+};
+
+/* Sum over aligned groups of N lanes (N = 8, 16, 32 or 64) with DPP / swizzle; the full sum is
+ * valid in the first lane of each group. */
+template <int CTRL>
+__device__ __forceinline__ float dpp_f(float x) {
+    return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, x), CTRL, 0xF, 0xF, true));
+}
+
+template <int N>
+__device__ __forceinline__ float group_sum(float v) {
+    v += dpp_f<0xB1>(v);  /* quad_perm [1,0,3,2] */
+    v += dpp_f<0x4E>(v);  /* quad_perm [2,3,0,1] */
+    v += dpp_f<0x141>(v); /* row_half_mirror: 8-lane sums */
+    if constexpr (N >= 16) v += dpp_f<0x140>(v); /* row_mirror: 16-lane sums */
+    if constexpr (N >= 32) /* xor 16 within each 32 lanes */
+        v += __builtin_bit_cast(float, __builtin_amdgcn_ds_swizzle(__builtin_bit_cast(int, v), 0x401F));
+    if constexpr (N >= 64) v += __shfl_xor(v, 32);
+    return v;
 }
 
 template <int TY>
@@ -116,52 +204,54 @@ struct Fmt;
 
 /* ---------------- Q4_K: 144 B = d f16, dmin f16, 12 B packed 6-bit scales/mins, 128 B nibbles.
  * Lane li: pair g = li>>1 of 64 values (low nibbles -> sub-block 2g, high -> 2g+1, per
- * src/quant.rs:74-80), half hh = li&1 of the 32 nibble bytes. */
+ * src/quant.rs:74-80), half hh = li&1 of the 32 nibble bytes -> two 16-value segments. */
 template <>
 struct Fmt<LE_TYPE_Q4_K> {
     static constexpr int SB = LE_SB_BYTES_Q4_K;
     static constexpr bool HAS_MU = true;
     static constexpr bool TABLES = false;
+    static constexpr int NSEG = 2, WPS = 4, XL = XL_Q4K;
     struct Raw {
         uint4 h, q;
     };
     __device__ static __forceinline__ Raw load(const u8 *p, int li) {
         Raw r;
-        r.h = *(const uint4 *)p;
-        r.q = *(const uint4 *)(p + 16 + 16 * li);
+        r.h = ldg16c(p);
+        r.q = ldg16(p + 16 + 16 * li);
         return r;
     }
-    __device__ static __forceinline__ void decode(const Raw &r, int li, int sb, const u32 *, Dec &d) {
+    __device__ static __forceinline__ void decode(const Raw &r, int li, int sb, const u32 *, Dec<NSEG, WPS> &d) {
         const int g = li >> 1, hh = li & 1;
         const u32 q[4] = {r.q.x, r.q.y, r.q.z, r.q.w};
 #pragma unroll
         for (int i = 0; i < 4; i++) {
-            d.w[i] = q[i] & 0x0F0F0F0Fu;              /* groups 0,1: low nibbles */
-            d.w[4 + i] = (q[i] >> 4) & 0x0F0F0F0Fu;   /* groups 2,3: high nibbles */
+            d.w[i] = q[i] & 0x0F0F0F0Fu;            /* segment 0: low nibbles, sub-block 2g */
+            d.w[4 + i] = (q[i] >> 4) & 0x0F0F0F0Fu; /* segment 1: high nibbles, sub-block 2g+1 */
         }
-        /* scale_min_k4 (src/quant.rs:52-55) for j = 2g, 2g+1, four bytes at a time */
-        const u32 sy = r.h.y, sz = r.h.z, sw = r.h.w;
-        const u32 tsc = g < 2 ? sy : ((sw & 0x0F0F0F0Fu) | ((sy >> 2) & 0x30303030u));
-        const u32 tm = g < 2 ? sz : (((sw >> 4) & 0x0F0F0F0Fu) | ((sz >> 2) & 0x30303030u));
-        const int sh = (g & 1) * 16;
-        const float dd = h2f(r.h.x & 0xFFFFu), dm = h2f(r.h.x >> 16);
-        const float sa = dd * (float)((tsc >> sh) & 63u), sb2 = dd * (float)((tsc >> (sh + 8)) & 63u);
-        const float ma = dm * (float)((tm >> sh) & 63u), mb = dm * (float)((tm >> (sh + 8)) & 63u);
-        const int pa = (sb * 8 + 2 * g) * 4 + 2 * hh;
-        d.p[0] = pa; d.p[1] = pa + 1; d.p[2] = pa + 4; d.p[3] = pa + 5;
-        d.sig[0] = sa; d.sig[1] = sa; d.sig[2] = sb2; d.sig[3] = sb2;
-        d.mu[0] = ma; d.mu[1] = ma; d.mu[2] = mb; d.mu[3] = mb;
+        /* scale_min_k4 (src/quant.rs:52-55): lane li decodes sub-block j = li, then the pair
+         * (2g, 2g+1) it needs comes from lanes li&~1 and li|1 of its quad. */
+        const int sh8 = 8 * (li & 3);
+        const u32 a = r.h.y >> sh8, b = r.h.z >> sh8, c = r.h.w >> sh8;
+        const u32 sc = li < 4 ? (a & 63u) : ((c & 15u) | ((a >> 2) & 0x30u));
+        const u32 mn = li < 4 ? (b & 63u) : (((c >> 4) & 15u) | ((b >> 2) & 0x30u));
+        const float sj = h2f(r.h.x & 0xFFFFu) * (float)sc, mj = h2f(r.h.x >> 16) * (float)mn;
+        d.sig[0] = dpp_f<0xA0>(sj); /* quad_perm [0,0,2,2] */
+        d.sig[1] = dpp_f<0xF5>(sj); /* quad_perm [1,1,3,3] */
+        d.mu[0] = dpp_f<0xA0>(mj);
+        d.mu[1] = dpp_f<0xF5>(mj);
     }
 };
 
 /* ---------------- Q6_K: 210 B = ql[128], qh[64], int8 scales[16], d f16 (src/quant.rs:96-112).
- * Lane li: half n = li>>2 (128 values), l-range [8t, 8t+8) with t = li&3, all four quadrants.
- * The stored 6-bit code q is used unsigned; the -32 offset goes into mu = 32*d*sc. */
+ * Lane li: half n = li>>2 (128 values), l-range [8t, 8t+8) with t = li&3, all four quadrants
+ * (four 8-value segments). The stored 6-bit code q is used unsigned; the -32 offset goes into
+ * mu = 32*d*sc. */
 template <>
 struct Fmt<LE_TYPE_Q6_K> {
     static constexpr int SB = LE_SB_BYTES_Q6_K;
     static constexpr bool HAS_MU = true;
     static constexpr bool TABLES = false;
+    static constexpr int NSEG = 4, WPS = 2, XL = XL_Q6K;
     struct Raw {
         uint2 la, lb, qh, sc;
         u32 d;
@@ -169,14 +259,14 @@ struct Fmt<LE_TYPE_Q6_K> {
     __device__ static __forceinline__ Raw load(const u8 *p, int li) {
         const int n = li >> 2, t = li & 3;
         Raw r;
-        r.la = ldu<uint2>(p + n * 64 + 8 * t);
-        r.lb = ldu<uint2>(p + n * 64 + 32 + 8 * t);
-        r.qh = ldu<uint2>(p + 128 + n * 32 + 8 * t);
-        r.sc = ldu<uint2>(p + 192 + n * 8);
-        r.d = ldu<uint16_t>(p + 208);
+        r.la = ldg8u(p + n * 64 + 8 * t);
+        r.lb = ldg8u(p + n * 64 + 32 + 8 * t);
+        r.qh = ldg8u(p + 128 + n * 32 + 8 * t);
+        r.sc = ldg8u(p + 192 + n * 8);
+        r.d = ldg2(p + 208);
         return r;
     }
-    __device__ static __forceinline__ void decode(const Raw &r, int li, int sb, const u32 *, Dec &d) {
+    __device__ static __forceinline__ void decode(const Raw &r, int li, int sb, const u32 *, Dec<NSEG, WPS> &d) {
         const int n = li >> 2, t = li & 3, is = t >> 1;
         const u32 la[2] = {r.la.x, r.la.y}, lb[2] = {r.lb.x, r.lb.y}, qh[2] = {r.qh.x, r.qh.y};
 #pragma unroll
@@ -187,27 +277,25 @@ struct Fmt<LE_TYPE_Q6_K> {
             d.w[6 + k] = ((lb[k] >> 4) & 0x0F0F0F0Fu) | ((qh[k] >> 2) & 0x30303030u);
         }
         const float dd = h2f(r.d);
-        const u32 scw = is ? (r.sc.x >> 8) | (r.sc.y << 24) : r.sc.x; /* bytes is, is+1, ... */
-        const u32 scw2 = is ? (r.sc.y >> 8) : r.sc.y;
-        /* quadrant qd uses sc[is + 2*qd]: qd 0,1 -> scw bytes 0,2; qd 2,3 -> scw2 bytes 0,2 */
-        const int s0 = (int)(int8_t)(scw & 255u), s1 = (int)(int8_t)((scw >> 16) & 255u);
-        const int s2 = (int)(int8_t)(scw2 & 255u), s3 = (int)(int8_t)((scw2 >> 16) & 255u);
-        const int ub = sb * 8 + n * 4;
-#pragma unroll
-        for (int k = 0; k < 4; k++) d.p[k] = (ub + k) * 4 + t;
-        d.sig[0] = dd * (float)s0; d.sig[1] = dd * (float)s1; d.sig[2] = dd * (float)s2; d.sig[3] = dd * (float)s3;
+        /* quadrant qd uses sc[is + 2*qd] of this half: bytes is, is+2 of word x and of word y */
+        const u32 sx = r.sc.x >> (8 * is), sy = r.sc.y >> (8 * is);
+        d.sig[0] = dd * (float)(int)(int8_t)(sx & 255u);
+        d.sig[1] = dd * (float)(int)(int8_t)((sx >> 16) & 255u);
+        d.sig[2] = dd * (float)(int)(int8_t)(sy & 255u);
+        d.sig[3] = dd * (float)(int)(int8_t)((sy >> 16) & 255u);
 #pragma unroll
         for (int k = 0; k < 4; k++) d.mu[k] = 32.0f * d.sig[k];
     }
 };
 
 /* ---------------- Q8_0 (8 blocks of 34 B = d f16 + 32 int8 per 256 values, src/quant.rs:68-71).
- * Lane li owns block li of the super-block. */
+ * Lane li owns block li of the super-block: one 32-value segment. */
 template <>
 struct Fmt<LE_TYPE_Q8_0> {
     static constexpr int SB = LE_SB_BYTES_Q8_0;
     static constexpr bool HAS_MU = false;
     static constexpr bool TABLES = false;
+    static constexpr int NSEG = 1, WPS = 8, XL = XL_ROW;
     struct Raw {
         uint4 a, b;
         u32 d;
@@ -215,18 +303,16 @@ struct Fmt<LE_TYPE_Q8_0> {
     __device__ static __forceinline__ Raw load(const u8 *p, int li) {
         const u8 *bp = p + 34 * li;
         Raw r;
-        r.d = ldu<uint16_t>(bp);
-        r.a = ldu<uint4>(bp + 2);
-        r.b = ldu<uint4>(bp + 18);
+        r.d = ldg2(bp);
+        r.a = ldg16u(bp + 2);
+        r.b = ldg16u(bp + 18);
         return r;
     }
-    __device__ static __forceinline__ void decode(const Raw &r, int li, int sb, const u32 *, Dec &d) {
+    __device__ static __forceinline__ void decode(const Raw &r, int li, int sb, const u32 *, Dec<NSEG, WPS> &d) {
         d.w[0] = r.a.x; d.w[1] = r.a.y; d.w[2] = r.a.z; d.w[3] = r.a.w;
         d.w[4] = r.b.x; d.w[5] = r.b.y; d.w[6] = r.b.z; d.w[7] = r.b.w;
-        const float dd = h2f(r.d);
-        const int u = sb * 8 + li;
-#pragma unroll
-        for (int k = 0; k < 4; k++) { d.p[k] = u * 4 + k; d.sig[k] = dd; d.mu[k] = 0.f; }
+        d.sig[0] = h2f(r.d);
+        d.mu[0] = 0.f;
     }
 };
 
@@ -248,19 +334,19 @@ struct Fmt<LE_TYPE_IQ2_XXS> {
     static constexpr bool HAS_MU = false;
     static constexpr bool TABLES = true;
     static constexpr int GRID_WORDS = 512;
+    static constexpr int NSEG = 1, WPS = 8, XL = XL_ROW;
     struct Raw {
         uint2 q;
         u32 d;
     };
     __device__ static __forceinline__ Raw load(const u8 *p, int li) {
         Raw r;
-        r.d = ldu<uint16_t>(p);
-        r.q = ldu<uint2>(p + 2 + 8 * li);
+        r.d = ldg2(p);
+        r.q = ldg8u(p + 2 + 8 * li);
         return r;
     }
-    __device__ static __forceinline__ void decode(const Raw &r, int li, int sb, const u32 *tab, Dec &d) {
+    __device__ static __forceinline__ void decode(const Raw &r, int li, int sb, const u32 *tab, Dec<NSEG, WPS> &d) {
         const u32 aux = r.q.y;
-        const float db = h2f(r.d) * (0.5f + (float)(aux >> 28)) * 0.25f;
         const u32 *grid = tab + LE_TAB_GRID, *sg = tab + LE_TAB_SIGN;
 #pragma unroll
         for (int l = 0; l < 4; l++) {
@@ -270,9 +356,8 @@ struct Fmt<LE_TYPE_IQ2_XXS> {
             d.w[2 * l] = apply_sign(g.x, m.x);
             d.w[2 * l + 1] = apply_sign(g.y, m.y);
         }
-        const int u = sb * 8 + li;
-#pragma unroll
-        for (int k = 0; k < 4; k++) { d.p[k] = u * 4 + k; d.sig[k] = db; d.mu[k] = 0.f; }
+        d.sig[0] = h2f(r.d) * (0.5f + (float)(aux >> 28)) * 0.25f;
+        d.mu[0] = 0.f;
     }
 };
 
@@ -283,20 +368,20 @@ struct Fmt<LE_TYPE_IQ3_XXS> {
     static constexpr bool HAS_MU = false;
     static constexpr bool TABLES = true;
     static constexpr int GRID_WORDS = 256;
+    static constexpr int NSEG = 1, WPS = 8, XL = XL_ROW;
     struct Raw {
         uint2 q;
         u32 aux, d;
     };
     __device__ static __forceinline__ Raw load(const u8 *p, int li) {
         Raw r;
-        r.d = ldu<uint16_t>(p);
-        r.q = ldu<uint2>(p + 2 + 8 * li);
-        r.aux = ldu<u32>(p + 66 + 4 * li);
+        r.d = ldg2(p);
+        r.q = ldg8u(p + 2 + 8 * li);
+        r.aux = ldg4u(p + 66 + 4 * li);
         return r;
     }
-    __device__ static __forceinline__ void decode(const Raw &r, int li, int sb, const u32 *tab, Dec &d) {
+    __device__ static __forceinline__ void decode(const Raw &r, int li, int sb, const u32 *tab, Dec<NSEG, WPS> &d) {
         const u32 aux = r.aux;
-        const float db = h2f(r.d) * (0.5f + (float)(aux >> 28)) * 0.5f;
         const u32 *grid = tab + LE_TAB_GRID, *sg = tab + LE_TAB_SIGN;
         const u32 qw[2] = {r.q.x, r.q.y};
 #pragma unroll
@@ -307,8 +392,7 @@ struct Fmt<LE_TYPE_IQ3_XXS> {
             d.w[2 * l] = apply_sign(grid[q & 255u], m.x);
             d.w[2 * l + 1] = apply_sign(grid[(q >> 8) & 255u], m.y);
         }
-        const int u = sb * 8 + li;
-#pragma unroll
-        for (int k = 0; k < 4; k++) { d.p[k] = u * 4 + k; d.sig[k] = db; d.mu[k] = 0.f; }
+        d.sig[0] = h2f(r.d) * (0.5f + (float)(aux >> 28)) * 0.5f;
+        d.mu[0] = 0.f;
     }
 };

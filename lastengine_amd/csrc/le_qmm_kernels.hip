@@ -166,7 +166,7 @@ LE_DEQ(LE_TYPE_IQ3_XXS, le_dequant_18)
 /* ===================================================================================== */
 
 /* Launch contract (checked by the host):
- *   cols % 256 == 0; G divides cols/256; x rows 16-byte aligned; blockDim = 256 (4 waves);
+ *   cols % 256 == 0; G divides cols/256; x rows 16-byte aligned; blockDim a multiple of 64;
  *   dynamic LDS = T * le_xtok_bytes(cols) + (IQ types) 4 * (256 + GRID_WORDS).
  * Grid: x = row-block workers, y = slot, z = token chunk of T tokens.
  * Slot s uses weights (ptrs ? ptrs[s] : w0 + s * w_slot_bytes), activations x + s*x_slot + t*x_tok,
@@ -201,91 +201,484 @@ __device__ __forceinline__ void load_tables(u32 *tab) {
     }
 }
 
-template <int TY, int G, int T>
-__device__ __forceinline__ void mv_body(const MvArgs &a) {
-    using F = Fmt<TY>;
-    extern __shared__ uint4 smem[];
-    const int K = a.cols, nsb = K >> 8, ng = K >> 3, nu = K >> 5;
-    const int slot = blockIdx.y, t0 = blockIdx.z * T;
-    const int nt = min(T, a.ntok - t0);
-    const u8 *W = a.ptrs ? a.ptrs[slot] : a.w0 + (size_t)slot * a.w_slot_bytes;
-    const size_t rb = (size_t)nsb * F::SB;
-
-    /* LDS carve-up: T token images, then the IQ tables */
-    XTok xt[T];
-    {
-        uint4 *xq = smem;
-        float *fs = (float *)(smem + T * ng);
-        float *dx = fs + T * ng;
+/* Dot of RW decoded rows (same columns) against one token: the LDS reads are shared by the rows.
+ * The integer chain runs over the xh plane, is scaled by 128, and continues over the xl plane,
+ * giving sum(q * v) with v = 128*xh + xl in one int32. */
+template <int NSEG, int WPS, bool HAS_MU, int RW>
+__device__ __forceinline__ void rows_dot(const Dec<NSEG, WPS> (&d)[RW], const XTok &x, int sb, int li, float (&c)[RW]) {
+    const int base = 32 * sb + li, xr = sb & 3;
 #pragma unroll
-        for (int t = 0; t < T; t++) {
-            xt[t].xq = xq + t * ng;
-            xt[t].fs = fs + t * ng;
-            xt[t].dx = dx + t * nu;
-            if (t < nt)
-                le_quant_x_lds(a.x + a.x_slot * slot + a.x_tok * (t0 + t), K, xq + t * ng, fs + t * ng, dx + t * nu);
+    for (int k = 0; k < NSEG; k++) {
+        uint4 q[WPS / 2];
+        float fs = 0.f, dx = 0.f;
+#pragma unroll
+        for (int g = 0; g < WPS / 2; g++) {
+            const int pos = base + 8 * ((k * (WPS / 2) + g) ^ xr);
+            q[g] = x.xq[pos];
+            const float2 s = x.xs[pos];
+            dx = s.x;
+            if (HAS_MU) fs += s.y;
         }
-    }
-    u32 *tab = (u32 *)((float *)(smem + T * ng) + T * ng + T * nu);
-    load_tables<TY>(tab);
-    __syncthreads();
-
-    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-    constexpr int RPW = 8 / G; /* rows per wave per step */
-    const int li = lane & 7, g = (lane >> 3) % G, rsub = lane / (8 * G);
-    const int S = nsb / G; /* super-blocks per lane per row */
-    const int nrb = (a.rows + RPW - 1) / RPW;
-    constexpr int U = 4;
-    for (int rbk = blockIdx.x * 4 + wave; rbk < nrb; rbk += gridDim.x * 4) {
-        const int row = rbk * RPW + rsub;
-        const bool rok = row < a.rows;
-        const u8 *wr = W + (size_t)(rok ? row : a.rows - 1) * rb;
-        float acc[T];
 #pragma unroll
-        for (int t = 0; t < T; t++) acc[t] = 0.f;
-        for (int s0 = 0; s0 < S; s0 += U) {
-            typename F::Raw raw[U];
+        for (int i = 0; i < RW; i++) {
+            int acc = 0;
 #pragma unroll
-            for (int u = 0; u < U; u++) {
-                const int s = min(s0 + u, S - 1);
-                raw[u] = F::load(wr + (size_t)(g + G * s) * F::SB, li);
+            for (int g = 0; g < WPS / 2; g++) {
+                acc = dot4(d[i].w[k * WPS + 2 * g], q[g].x, acc);
+                acc = dot4(d[i].w[k * WPS + 2 * g + 1], q[g].y, acc);
             }
+            acc <<= 7;
 #pragma unroll
-            for (int u = 0; u < U; u++) {
-                if (s0 + u < S) {
-                    Dec d;
-                    F::decode(raw[u], li, g + G * (s0 + u), tab, d);
-#pragma unroll
-                    for (int t = 0; t < T; t++) {
-                        if (t < nt) {
-                            float c = 0.f;
-#pragma unroll
-                            for (int k = 0; k < 4; k++) c += group_dot<F::HAS_MU>(d, k, xt[t]);
-                            acc[t] += c;
-                        }
-                    }
-                }
+            for (int g = 0; g < WPS / 2; g++) {
+                acc = dot4(d[i].w[k * WPS + 2 * g], q[g].z, acc);
+                acc = dot4(d[i].w[k * WPS + 2 * g + 1], q[g].w, acc);
             }
-        }
-#pragma unroll
-        for (int t = 0; t < T; t++) {
-#pragma unroll
-            for (int off = 1; off < 8 * G; off <<= 1) acc[t] += __shfl_xor(acc[t], off);
-        }
-        if (rok && (lane & (8 * G - 1)) == 0) {
-#pragma unroll
-            for (int t = 0; t < T; t++)
-                if (t < nt) a.y[a.y_slot * slot + a.y_tok * (t0 + t) + row] = acc[t];
+            c[i] = __builtin_fmaf(d[i].sig[k], (float)acc * dx, c[i]);
+            if (HAS_MU) c[i] = __builtin_fmaf(-d[i].mu[k], fs, c[i]);
         }
     }
 }
 
-#define LE_MV(TY, G, T)                                                                                    \
-    extern "C" __global__ void __launch_bounds__(256) le_mv_##TY##_g##G##_t##T(MvArgs a) { mv_body<TY, G, T>(a); }
-#define LE_MV_G(TY, G) LE_MV(TY, G, 1) LE_MV(TY, G, 2) LE_MV(TY, G, 4) LE_MV(TY, G, 8)
+/* Each wave owns row-blocks of RW*RPW rows (RPW = 8/G rows side by side, G lane groups of 8 per
+ * row) and walks them in steps of CH super-blocks per lane and row. Steps are double-buffered:
+ * the loads of step n+1 are in flight while step n is decoded and multiplied, and the first
+ * step's loads are issued before the activation prologue so HBM latency overlaps it. */
+template <int TY, int G, int T, int RW, int CH, int BLOCK>
+__device__ __forceinline__ void mv_body(const MvArgs &a) {
+    using F = Fmt<TY>;
+    using D = Dec<F::NSEG, F::WPS>;
+    using Raw = typename F::Raw;
+    extern __shared__ uint4 smem[];
+    const int K = a.cols, nsb = K >> 8, ng = K >> 3;
+    const int slot = blockIdx.y, t0 = blockIdx.z * T;
+    const int nt = min(T, a.ntok - t0);
+    const u8 *W = a.ptrs ? a.ptrs[slot] : a.w0 + (size_t)slot * a.w_slot_bytes;
+    const size_t rb = (size_t)nsb * F::SB;
+    constexpr int nwave = BLOCK / 64;
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    constexpr int RPW = 8 / G;
+    const int li = lane & 7, g = (lane >> 3) % G, rsub = lane / (8 * G);
+    const int S = nsb / G, nch = (S + CH - 1) / CH;
+    const int nrb = (a.rows + RPW * RW - 1) / (RPW * RW);
+    const int rstride = gridDim.x * nwave;
+
+    auto issue = [&](Raw (&raw)[RW][CH], int rbk, int c) {
+#pragma unroll
+        for (int i = 0; i < RW; i++) {
+            const int row = min((rbk * RW + i) * RPW + rsub, a.rows - 1);
+            const u8 *wr = W + (size_t)row * rb;
+#pragma unroll
+            for (int u = 0; u < CH; u++) {
+                const int s = c * CH + u;
+                if (s < S) raw[i][u] = F::load(wr + (size_t)(g + G * s) * F::SB, li);
+            }
+        }
+    };
+
+    Raw ra[RW][CH], rb2[RW][CH];
+    int rbk = blockIdx.x * nwave + wave, c = 0;
+
+    /* LDS: T token images, then the IQ tables. For one token whose groups fit in registers
+     * (K/8 <= 4 * blockDim), the activation loads go out before the weight loads. */
+    XTok xt[T];
+    uint4 *xq = smem;
+    float2 *xs = (float2 *)(smem + T * ng);
+#pragma unroll
+    for (int t = 0; t < T; t++) {
+        xt[t].xq = xq + t * ng;
+        xt[t].xs = xs + t * ng;
+    }
+    constexpr int XR = 16384 / 8 / BLOCK; /* register-staged activations up to K = 16384 */
+    if (T == 1 && ng <= XR * BLOCK) {
+        XLoad<BLOCK, XR> xl;
+        xl.load(a.x + a.x_slot * slot + a.x_tok * t0, K);
+        if (rbk < nrb) issue(ra, rbk, 0);
+        xl.template store<F::XL>(K, xq, xs);
+    } else {
+        if (rbk < nrb) issue(ra, rbk, 0);
+        for (int t = 0; t < nt; t++)
+            le_quant_x_lds<F::XL>(a.x + a.x_slot * slot + a.x_tok * (t0 + t), K, xq + t * ng, xs + t * ng);
+    }
+    u32 *tab = (u32 *)((float2 *)(smem + T * ng) + T * ng);
+    load_tables<TY>(tab);
+    __syncthreads();
+
+    float acc[T][RW];
+#pragma unroll
+    for (int t = 0; t < T; t++)
+#pragma unroll
+        for (int i = 0; i < RW; i++) acc[t][i] = 0.f;
+
+    auto consume = [&](Raw (&raw)[RW][CH], int rbk, int c) {
+#pragma unroll
+        for (int u = 0; u < CH; u++) {
+            const int s = c * CH + u;
+            if (s < S) {
+                D d[RW];
+#pragma unroll
+                for (int i = 0; i < RW; i++) F::decode(raw[i][u], li, g + G * s, tab, d[i]);
+#pragma unroll
+                for (int t = 0; t < T; t++)
+                    if (t < nt) rows_dot<F::NSEG, F::WPS, F::HAS_MU, RW>(d, xt[t], g + G * s, li, acc[t]);
+            }
+        }
+        if (c == nch - 1) {
+#pragma unroll
+            for (int t = 0; t < T; t++)
+#pragma unroll
+                for (int i = 0; i < RW; i++) acc[t][i] = group_sum<8 * G>(acc[t][i]);
+            if ((lane & (8 * G - 1)) == 0) {
+#pragma unroll
+                for (int i = 0; i < RW; i++) {
+                    const int row = (rbk * RW + i) * RPW + rsub;
+                    if (row < a.rows) {
+#pragma unroll
+                        for (int t = 0; t < T; t++)
+                            if (t < nt) a.y[a.y_slot * slot + a.y_tok * (t0 + t) + row] = acc[t][i];
+                    }
+                }
+            }
+#pragma unroll
+            for (int t = 0; t < T; t++)
+#pragma unroll
+                for (int i = 0; i < RW; i++) acc[t][i] = 0.f;
+        }
+    };
+
+    /* ping-pong over the wave's (row-block, step) sequence */
+    while (rbk < nrb) {
+        int r1 = rbk, c1 = c + 1;
+        if (c1 == nch) { c1 = 0; r1 += rstride; }
+        if (r1 < nrb) issue(rb2, r1, c1);
+        consume(ra, rbk, c);
+        rbk = r1;
+        c = c1;
+        if (rbk >= nrb) break;
+        int r2 = rbk, c2 = c + 1;
+        if (c2 == nch) { c2 = 0; r2 += rstride; }
+        if (r2 < nrb) issue(ra, r2, c2);
+        consume(rb2, rbk, c);
+        rbk = r2;
+        c = c2;
+    }
+}
+
+#define LE_MV(TY, G, T, RW, CH, BLOCK)                                                                        \
+    extern "C" __global__ void __launch_bounds__(BLOCK) le_mv_##TY##_g##G##_t##T##_r##RW##_c##CH##_b##BLOCK(   \
+        MvArgs a) {                                                                                           \
+        mv_body<TY, G, T, RW, CH, BLOCK>(a);                                                                  \
+    }
+/* T = 1 (decode): four (rows, steps) shapes at 512 and 1024 threads; T > 1: two shapes at 256. */
+#define LE_MV_T1B(TY, G, B) LE_MV(TY, G, 1, 1, 2, B) LE_MV(TY, G, 1, 2, 1, B) LE_MV(TY, G, 1, 2, 2, B) LE_MV(TY, G, 1, 4, 1, B)
+#define LE_MV_T1(TY, G) LE_MV_T1B(TY, G, 512) LE_MV_T1B(TY, G, 1024)
+#define LE_MV_TN(TY, G, T) LE_MV(TY, G, T, 2, 2, 256) LE_MV(TY, G, T, 4, 1, 256)
+#define LE_MV_G(TY, G) LE_MV_T1(TY, G) LE_MV_TN(TY, G, 2) LE_MV_TN(TY, G, 4) LE_MV_TN(TY, G, 8)
 #define LE_MV_ALL(TY) LE_MV_G(TY, 1) LE_MV_G(TY, 2) LE_MV_G(TY, 4) LE_MV_G(TY, 8)
+
+/* ===================================================================================== */
+/* MFMA matvec (decode, one token).                                                          */
+/* ===================================================================================== */
+/* v_mfma_i32_16x16x64_i8 computes D[16x16] += A[16x64] . B[64x16]; lane l holds A row l%16 and B
+ * column l%16 over K-slice l/16 (16 int8 each), and D[4*(l/16)+i][l%16] for i < 4. The matvec
+ * uses B = 16 weight rows (one tile) and A rows m = (plane p, sub-block j), m = 8p + j, holding
+ * the activation plane p (0: xh, 1: xl) only in the K-slices that belong to sub-block j and zero
+ * elsewhere. Four MFMAs cover a 256-value super-block and leave D[(p,j)][n] = sum over sub-block
+ * j of q * x_p for every row n, so the per-sub-block scales are applied once per super-block in a
+ * short epilogue instead of per weight.
+ *
+ * Q4_K K-slices: lane (n, s) loads qs bytes 16s..16s+15 (load 0) and 64+16s.. (load 1) of its
+ * row's super-block. MFMA b uses the low nibbles (b even) or high nibbles (b odd) of load b/2, so
+ * slice s of MFMA b is sub-block j(b,s) = 4*(b>>1) + 2*(s>>1) + (b&1), positions 16*(s&1)..+15. */
+typedef int le_v4i __attribute__((ext_vector_type(4)));
+
+__device__ __forceinline__ int mq_j(int b, int s) { return 4 * (b >> 1) + 2 * (s >> 1) + (b & 1); }
+
+/* LDS activation image of the MFMA path, per super-block: 16 records of 32 B (record 4b+s holds
+ * slice s of MFMA b: 16 B xh, 16 B xl), then dxp[16] (m = 8p+j: dx_j * (p ? 1 : 128)) and fs[8]
+ * (dx_j * sum v over sub-block j). */
+__host__ __device__ inline int le_mq_x_bytes(int K) { return (K / 256) * (512 + 64 + 32); }
+
+/* Segment e = 16 activations: load, then quantize (partner segments e, e^1 share a sub-block). */
+__device__ __forceinline__ void mq_load_seg(const float *__restrict__ x, int e, float4 (&v4)[4]) {
+    const LE_GLOBAL float4 *xg = (const LE_GLOBAL float4 *)x;
+#pragma unroll
+    for (int i = 0; i < 4; i++) v4[i] = xg[4 * e + i];
+}
+__device__ __forceinline__ void mq_quant_seg(int e, bool store, const float4 (&v4)[4], uint4 *rec, float *dxp, float *fsv) {
+    float am = fmaxf(amax8(v4[0], v4[1]), amax8(v4[2], v4[3]));
+    am = fmaxf(am, __shfl_xor(am, 1));
+    const float inv = am > 0.f ? LE_XSPLIT / am : 0.f;
+    const float d = am / LE_XSPLIT;
+    u32 hw[4] = {0, 0, 0, 0}, lw[4] = {0, 0, 0, 0};
+    int sum = 0;
+#pragma unroll
+    for (int i = 0; i < 16; i++) {
+        const float xv = i % 4 == 0 ? v4[i / 4].x : i % 4 == 1 ? v4[i / 4].y : i % 4 == 2 ? v4[i / 4].z : v4[i / 4].w;
+        const int v = (int)rintf(xv * inv);
+        const int h = (v + 64) >> 7;
+        const int lo = v - (h << 7);
+        hw[i >> 2] |= ((u32)h & 255u) << (8 * (i & 3));
+        lw[i >> 2] |= ((u32)lo & 255u) << (8 * (i & 3));
+        sum += v;
+    }
+    sum += __shfl_xor(sum, 1);
+    if (!store) return;
+    const int sb = e >> 4, j = (e & 15) >> 1, c = e & 1;
+    const int b = 2 * (j >> 2) + (j & 1), s = 2 * ((j & 3) >> 1) + c;
+    const int r = (sb * 16 + b * 4 + s) * 2;
+    rec[r] = make_uint4(hw[0], hw[1], hw[2], hw[3]);
+    rec[r + 1] = make_uint4(lw[0], lw[1], lw[2], lw[3]);
+    if (c == 0) {
+        dxp[sb * 16 + j] = d * 128.0f;
+        dxp[sb * 16 + 8 + j] = d;
+        fsv[sb * 8 + j] = d * (float)sum;
+    }
+}
+__device__ __forceinline__ void mq_quant_x(const float *__restrict__ x, int K, uint4 *rec, float *dxp, float *fsv) {
+    const int nseg = K >> 4; /* even: partners share trips */
+    for (int e = threadIdx.x; e < nseg; e += blockDim.x) {
+        float4 v4[4];
+        mq_load_seg(x, e, v4);
+        mq_quant_seg(e, true, v4, rec, dxp, fsv);
+    }
+}
+
+/* One block = NW waves on one 16-row tile at a time; wave w takes super-blocks w, w+NW, ... (U
+ * per step) and the block sums the waves' partial rows through LDS. */
+template <int NW, int U>
+__device__ __forceinline__ void mq_q4k_body(const MvArgs &a) {
+    extern __shared__ uint4 smem[];
+    const int K = a.cols, nsb = K >> 8;
+    const int slot = blockIdx.y;
+    const u8 *W = a.ptrs ? a.ptrs[slot] : a.w0 + (size_t)slot * a.w_slot_bytes;
+    const size_t rb = (size_t)nsb * 144;
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int n = lane & 15, sq = lane >> 4;
+    uint4 *rec = smem;
+    float *dxp = (float *)(smem + nsb * 32);
+    float *fsv = dxp + nsb * 16;
+    float *red = fsv + nsb * 8; /* NW * 16 partial rows */
+    const int ntile = (a.rows + 15) >> 4;
+
+    mq_quant_x(a.x + a.x_slot * slot, K, rec, dxp, fsv);
+    __syncthreads();
+
+    /* exec-masked A operands: lane (m = l%16, s = l/16) of MFMA b is live iff m%8 == j(b, s) */
+    const int m = lane & 15, p = m >> 3, jm = m & 7;
+    bool live[4];
+#pragma unroll
+    for (int b = 0; b < 4; b++) live[b] = jm == mq_j(b, sq);
+    le_v4i A[4];
+#pragma unroll
+    for (int b = 0; b < 4; b++) A[b] = (le_v4i){0, 0, 0, 0};
+
+    const int pe = sq >> 1, jb = 4 * (sq & 1);
+    for (int tile = blockIdx.x; tile < ntile; tile += gridDim.x) {
+        const int row = min(tile * 16 + n, a.rows - 1);
+        const u8 *wr = W + (size_t)row * rb;
+        float y = 0.f;
+        for (int s0 = wave; s0 < nsb; s0 += NW * U) {
+            uint4 hd[U], l0[U], l1[U];
+#pragma unroll
+            for (int u = 0; u < U; u++) {
+                const int sb = min(s0 + u * NW, nsb - 1);
+                const u8 *pb = wr + (size_t)sb * 144;
+                hd[u] = ldg16c(pb);
+                l0[u] = ldg16(pb + 16 + 16 * sq);
+                l1[u] = ldg16(pb + 80 + 16 * sq);
+            }
+#pragma unroll
+            for (int u = 0; u < U; u++) {
+                const int sb = s0 + u * NW;
+                if (sb < nsb) {
+#pragma unroll
+                    for (int b = 0; b < 4; b++)
+                        if (live[b]) {
+                            const uint4 v = rec[(sb * 16 + b * 4 + sq) * 2 + p];
+                            A[b] = (le_v4i){(int)v.x, (int)v.y, (int)v.z, (int)v.w};
+                        }
+                    const le_v4i B0 = {(int)(l0[u].x & 0x0F0F0F0Fu), (int)(l0[u].y & 0x0F0F0F0Fu),
+                                       (int)(l0[u].z & 0x0F0F0F0Fu), (int)(l0[u].w & 0x0F0F0F0Fu)};
+                    const le_v4i B1 = {(int)((l0[u].x >> 4) & 0x0F0F0F0Fu), (int)((l0[u].y >> 4) & 0x0F0F0F0Fu),
+                                       (int)((l0[u].z >> 4) & 0x0F0F0F0Fu), (int)((l0[u].w >> 4) & 0x0F0F0F0Fu)};
+                    const le_v4i B2 = {(int)(l1[u].x & 0x0F0F0F0Fu), (int)(l1[u].y & 0x0F0F0F0Fu),
+                                       (int)(l1[u].z & 0x0F0F0F0Fu), (int)(l1[u].w & 0x0F0F0F0Fu)};
+                    const le_v4i B3 = {(int)((l1[u].x >> 4) & 0x0F0F0F0Fu), (int)((l1[u].y >> 4) & 0x0F0F0F0Fu),
+                                       (int)((l1[u].z >> 4) & 0x0F0F0F0Fu), (int)((l1[u].w >> 4) & 0x0F0F0F0Fu)};
+                    le_v4i D = __builtin_amdgcn_mfma_i32_16x16x64_i8(A[0], B0, (le_v4i){0, 0, 0, 0}, 0, 0, 0);
+                    D = __builtin_amdgcn_mfma_i32_16x16x64_i8(A[1], B1, D, 0, 0, 0);
+                    D = __builtin_amdgcn_mfma_i32_16x16x64_i8(A[2], B2, D, 0, 0, 0);
+                    D = __builtin_amdgcn_mfma_i32_16x16x64_i8(A[3], B3, D, 0, 0, 0);
+                    /* epilogue: lane (n, sq) holds D[(pe, jb+i)][n], i < 4 */
+                    const u32 sy = hd[u].y, sz = hd[u].z, sw = hd[u].w;
+                    const u32 tsc = (sq & 1) ? ((sw & 0x0F0F0F0Fu) | ((sy >> 2) & 0x30303030u)) : (sy & 0x3F3F3F3Fu);
+                    const u32 tm = (sq & 1) ? (((sw >> 4) & 0x0F0F0F0Fu) | ((sz >> 2) & 0x30303030u)) : (sz & 0x3F3F3F3Fu);
+                    const float4 dq = *(const float4 *)(dxp + sb * 16 + pe * 8 + jb);
+                    const float t = (float)(tsc & 255u) * dq.x * (float)D[0] + (float)((tsc >> 8) & 255u) * dq.y * (float)D[1] +
+                                    (float)((tsc >> 16) & 255u) * dq.z * (float)D[2] + (float)(tsc >> 24) * dq.w * (float)D[3];
+                    const float2 f2 = *(const float2 *)(fsv + sb * 8 + jb + 2 * pe);
+                    const u32 mm = tm >> (16 * pe);
+                    const float mt = (float)(mm & 255u) * f2.x + (float)((mm >> 8) & 255u) * f2.y;
+                    y += h2f(hd[u].x & 0xFFFFu) * t - h2f(hd[u].x >> 16) * mt;
+                }
+            }
+        }
+        /* sum the four slices of row n, then the NW waves */
+        y += __builtin_bit_cast(float, __builtin_amdgcn_ds_swizzle(__builtin_bit_cast(int, y), 0x401F));
+        y += __shfl_xor(y, 32);
+        if (lane < 16) red[wave * 16 + lane] = y;
+        __syncthreads();
+        if (wave == 0 && lane < 16) {
+            float acc = 0.f;
+#pragma unroll
+            for (int w = 0; w < NW; w++) acc += red[w * 16 + lane];
+            const int r = tile * 16 + lane;
+            if (r < a.rows) a.y[a.y_slot * slot + r] = acc;
+        }
+        __syncthreads();
+    }
+}
+
+/* Staged variant: each wave streams its tile's P super-blocks per row as consecutive 16-byte
+ * chunks (consecutive lanes take consecutive chunks of a row, so every load instruction reads
+ * long contiguous runs), prefetched into registers one item ahead and written to a wave-private
+ * LDS buffer where one pad chunk per row keeps the 16 rows of a read in distinct banks. MFMA
+ * operands then come from LDS. Barriers wait on LDS traffic only, so weight loads in flight are
+ * not drained at a barrier. */
+template <int P, int NW>
+__device__ __forceinline__ void ms_q4k_body(const MvArgs &a) {
+    extern __shared__ uint4 smem[];
+    constexpr int CPR = 9 * P + 1, NCH = 16 * CPR, NI = (NCH + 63) / 64;
+    const int K = a.cols, nsb = K >> 8;
+    const int slot = blockIdx.y;
+    const u8 *W = a.ptrs ? a.ptrs[slot] : a.w0 + (size_t)slot * a.w_slot_bytes;
+    const size_t rb = (size_t)nsb * 144;
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int n = lane & 15, sq = lane >> 4;
+    uint4 *rec = smem;
+    float *dxp = (float *)(smem + nsb * 32);
+    float *fsv = dxp + nsb * 16;
+    uint4 *wb = (uint4 *)(fsv + nsb * 8) + wave * (NI * 64);
+    float *red = (float *)((uint4 *)(fsv + nsb * 8) + NW * NI * 64); /* [2][NW][16] */
+    const int ntile = (a.rows + 15) >> 4;
+
+    /* chunk i of this lane: row ri[i] of the tile, byte cb[i] of the row's P-super-block run */
+    int ri[NI], cb[NI];
+#pragma unroll
+    for (int i = 0; i < NI; i++) {
+        const int c = min(64 * i + lane, NCH - 1);
+        const int col = c % CPR;
+        ri[i] = c / CPR;
+        cb[i] = (col == 9 * P ? 0 : col) * 16;
+    }
+    /* register staging: the chunks of the next item are loaded while the current one computes */
+    uint4 R[NI];
+    auto issue = [&](int tile, int s0) {
+#pragma unroll
+        for (int i = 0; i < NI; i++) {
+            const int row = min(tile * 16 + ri[i], a.rows - 1);
+            R[i] = ldg16(W + (size_t)row * rb + (size_t)s0 * 144 + cb[i]);
+        }
+    };
+    const int sfirst = wave * P, sstep = NW * P;
+    const bool active = sfirst < nsb;
+    /* activations of the first segment round go out first (clamped, unpredicated), then the
+     * first weight item, so the quantization waits only for the activations */
+    const float *xs = a.x + a.x_slot * slot;
+    const int nseg = K >> 4, e0 = threadIdx.x;
+    float4 xv[4];
+    mq_load_seg(xs, min(e0, nseg - 1), xv);
+    issue(min((int)blockIdx.x, ntile - 1), active ? sfirst : 0); /* unpredicated: exact wait counts */
+    mq_quant_seg(e0, e0 < nseg, xv, rec, dxp, fsv);
+    for (int e = e0 + NW * 64; e < nseg; e += NW * 64) {
+        mq_load_seg(xs, e, xv);
+        mq_quant_seg(e, true, xv, rec, dxp, fsv);
+    }
+    __builtin_amdgcn_s_waitcnt(0xC07F); /* lgkmcnt(0): this wave's LDS writes are done */
+    __builtin_amdgcn_s_barrier();
+
+    const int m = lane & 15, p = m >> 3, jm = m & 7;
+    bool live[4];
+#pragma unroll
+    for (int b = 0; b < 4; b++) live[b] = jm == mq_j(b, sq);
+    le_v4i A[4];
+#pragma unroll
+    for (int b = 0; b < 4; b++) A[b] = (le_v4i){0, 0, 0, 0};
+    const int pe = sq >> 1, jb = 4 * (sq & 1);
+
+    int par = 0;
+    for (int tile = blockIdx.x; tile < ntile; tile += gridDim.x) {
+        float y = 0.f;
+        if (active) {
+            for (int s0 = sfirst; s0 < nsb; s0 += sstep) {
+                int nt = tile, ns = s0 + sstep;
+                if (ns >= nsb) { ns = sfirst; nt += gridDim.x; }
+#pragma unroll
+                for (int i = 0; i < NI; i++) wb[64 * i + lane] = R[i];
+                if (nt < ntile) issue(nt, ns);
+#pragma unroll
+                for (int q = 0; q < P; q++) {
+                    const int sb = s0 + q;
+                    const uint4 *rowp = wb + n * CPR + 9 * q;
+                    const uint4 hd = rowp[0], l0 = rowp[1 + sq], l1 = rowp[5 + sq];
+#pragma unroll
+                    for (int b = 0; b < 4; b++)
+                        if (live[b]) {
+                            const uint4 v = rec[(sb * 16 + b * 4 + sq) * 2 + p];
+                            A[b] = (le_v4i){(int)v.x, (int)v.y, (int)v.z, (int)v.w};
+                        }
+                    const le_v4i B0 = {(int)(l0.x & 0x0F0F0F0Fu), (int)(l0.y & 0x0F0F0F0Fu), (int)(l0.z & 0x0F0F0F0Fu), (int)(l0.w & 0x0F0F0F0Fu)};
+                    const le_v4i B1 = {(int)((l0.x >> 4) & 0x0F0F0F0Fu), (int)((l0.y >> 4) & 0x0F0F0F0Fu),
+                                       (int)((l0.z >> 4) & 0x0F0F0F0Fu), (int)((l0.w >> 4) & 0x0F0F0F0Fu)};
+                    const le_v4i B2 = {(int)(l1.x & 0x0F0F0F0Fu), (int)(l1.y & 0x0F0F0F0Fu), (int)(l1.z & 0x0F0F0F0Fu), (int)(l1.w & 0x0F0F0F0Fu)};
+                    const le_v4i B3 = {(int)((l1.x >> 4) & 0x0F0F0F0Fu), (int)((l1.y >> 4) & 0x0F0F0F0Fu),
+                                       (int)((l1.z >> 4) & 0x0F0F0F0Fu), (int)((l1.w >> 4) & 0x0F0F0F0Fu)};
+                    le_v4i D = __builtin_amdgcn_mfma_i32_16x16x64_i8(A[0], B0, (le_v4i){0, 0, 0, 0}, 0, 0, 0);
+                    D = __builtin_amdgcn_mfma_i32_16x16x64_i8(A[1], B1, D, 0, 0, 0);
+                    D = __builtin_amdgcn_mfma_i32_16x16x64_i8(A[2], B2, D, 0, 0, 0);
+                    D = __builtin_amdgcn_mfma_i32_16x16x64_i8(A[3], B3, D, 0, 0, 0);
+                    const u32 sy = hd.y, sz = hd.z, sw = hd.w;
+                    const u32 tsc = (sq & 1) ? ((sw & 0x0F0F0F0Fu) | ((sy >> 2) & 0x30303030u)) : (sy & 0x3F3F3F3Fu);
+                    const u32 tm = (sq & 1) ? (((sw >> 4) & 0x0F0F0F0Fu) | ((sz >> 2) & 0x30303030u)) : (sz & 0x3F3F3F3Fu);
+                    const float4 dq = *(const float4 *)(dxp + sb * 16 + pe * 8 + jb);
+                    const float t = (float)(tsc & 255u) * dq.x * (float)D[0] + (float)((tsc >> 8) & 255u) * dq.y * (float)D[1] +
+                                    (float)((tsc >> 16) & 255u) * dq.z * (float)D[2] + (float)(tsc >> 24) * dq.w * (float)D[3];
+                    const float2 f2 = *(const float2 *)(fsv + sb * 8 + jb + 2 * pe);
+                    const u32 mm = tm >> (16 * pe);
+                    const float mt = (float)(mm & 255u) * f2.x + (float)((mm >> 8) & 255u) * f2.y;
+                    y += h2f(hd.x & 0xFFFFu) * t - h2f(hd.x >> 16) * mt;
+                }
+            }
+        }
+        y += __builtin_bit_cast(float, __builtin_amdgcn_ds_swizzle(__builtin_bit_cast(int, y), 0x401F));
+        y += __shfl_xor(y, 32);
+        float *rp = red + par * (NW * 16);
+        if (lane < 16) rp[wave * 16 + lane] = y;
+        __builtin_amdgcn_s_waitcnt(0xC07F);
+        __builtin_amdgcn_s_barrier();
+        if (wave == 0 && lane < 16) {
+            float acc = 0.f;
+#pragma unroll
+            for (int w = 0; w < NW; w++) acc += rp[w * 16 + lane];
+            const int r = tile * 16 + lane;
+            if (r < a.rows) a.y[a.y_slot * slot + r] = acc;
+        }
+        par ^= 1;
+    }
+}
+
+#define LE_MS12(P, NW)                                                                                     \
+    extern "C" __global__ void __launch_bounds__(NW * 64) le_ms_12_p##P##_w##NW(MvArgs a) { ms_q4k_body<P, NW>(a); }
+
+#define LE_MQ12(NW, U)                                                                                     \
+    extern "C" __global__ void __launch_bounds__(NW * 64) le_mq_12_w##NW##_u##U(MvArgs a) { mq_q4k_body<NW, U>(a); }
+
 /* Each code object carries the kernels of one part (the build compiles this file once per part,
  * in parallel): LE_PART_DEQ, or LE_PART_MV=<type id>. */
 #if defined(LE_PART_MV)
 LE_MV_ALL(LE_PART_MV)
+#if LE_PART_MV == 12
+LE_MQ12(4, 1) LE_MQ12(4, 2) LE_MQ12(4, 4) LE_MQ12(8, 1) LE_MQ12(8, 2) LE_MQ12(2, 4)
+LE_MS12(1, 4) LE_MS12(1, 8) LE_MS12(2, 4) LE_MS12(2, 8) LE_MS12(4, 2) LE_MS12(4, 4)
+#endif
 #endif

@@ -56,6 +56,7 @@ def lib():
         "le_init": (I, [ctypes.c_char_p, ctypes.POINTER(P)]),
         "le_destroy": (None, [P]),
         "le_last_error": (ctypes.c_char_p, [P]),
+        "le_set_option": (I, [P, ctypes.c_char_p, I]),
         "le_dequant_rows": (I, [P, I, P, P, I, I, P]),
         "le_matvec": (I, [P, I, P, P, P, LL, P, I, I, I, P]),
         "le_gemm": (I, [P, I, P, P, I, P, I, I, P]),
@@ -151,6 +152,9 @@ class Engine:
     def _check(self, rc):
         if rc:
             raise LeError(rc, (self._L.le_last_error(self._ctx) or b"").decode())
+
+    def set_option(self, name, value):
+        self._check(self._L.le_set_option(self._ctx, name.encode(), int(value)))
 
     def dequant_rows(self, ty, w, out, rows, cols, stream=None):
         self._check(self._L.le_dequant_rows(self._ctx, ty, _ptr(w), _ptr(out), rows, cols, _stream(stream)))
