@@ -53,7 +53,7 @@ struct le_ctx {
     int mv_blocks_per_cu = 1; /* grid cap = CUs * this */
     int mv_shape = 0;        /* (rows, steps) per lane: 0 auto, 1 (1,2), 2 (2,1), 3 (2,2), 4 (4,1) */
     int mq = 1;              /* decode matvec on MFMA where available */
-    int mq_waves = 4, mq_steps = 2, mq_blocks_per_cu = 4;
+    int mq_waves = 4, mq_steps = 2, mq_blocks_per_cu = 2;
     int ms = 1, ms_p = 2;    /* staged MFMA variant and its super-blocks per row and step */
     std::vector<hipModule_t> mods;
     std::map<std::string, hipFunction_t> fns;
@@ -155,13 +155,16 @@ int mq_launch(le_ctx *c, const void *const *ptrs, const void *w, const float *x,
     void *args[] = {&a};
     char name[64];
     size_t lds = (size_t)nsb * 608 + (size_t)NW * 64;
-    int P = c->ms_p;
+    int P = c->ms_p, NWs = NW;
     while (P > 1 && nsb % P) P >>= 1;
-    if (c->ms) {
+    while (NWs > 1 && nsb % (NWs * P)) NWs >>= 1;
+    if (c->ms && nsb % (NWs * P) == 0) {
         const int cpr = 9 * P + 1, ni = (16 * cpr + 63) / 64;
-        snprintf(name, sizeof name, "le_ms_12_p%d_w%d", P, NW);
-        lds += (size_t)NW * ni * 64 * 16 + (size_t)NW * 64;
-        return c->launch(name, dim3((unsigned)gx, (unsigned)slots), NW * 64, lds, st, args);
+        snprintf(name, sizeof name, "le_ms_12_p%d_w%d", P, NWs);
+        lds = (size_t)NWs * ((size_t)(nsb / NWs) * 608 + (size_t)ni * 1024) + (size_t)NWs * 128;
+        if (lds <= c->lds_limit)
+            return c->launch(name, dim3((unsigned)gx, (unsigned)slots), NWs * 64, lds, st, args);
+        lds = (size_t)nsb * 608 + (size_t)NW * 64;
     }
     snprintf(name, sizeof name, "le_mq_12_w%d_u%d", NW, U);
     return c->launch(name, dim3((unsigned)gx, (unsigned)slots), NW * 64, lds, st, args);

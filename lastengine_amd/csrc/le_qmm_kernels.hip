@@ -17,6 +17,19 @@
 #include "le_iq_tables.h"
 #include "le_qmm_device.h"
 
+/* Optional per-block timestamps for diagnostic builds (-DLE_TRACE): slot i of block b at
+ * le_trace_buf[b * 4 + i]. Compiled out otherwise. */
+#if defined(LE_TRACE)
+__device__ unsigned long long le_trace_buf[1 << 16];
+#define LE_TRACE_POINT(i)                                                                                  \
+    do {                                                                                                   \
+        if (threadIdx.x == 0 && blockIdx.y == 0 && blockIdx.x < (1 << 14))                                 \
+            le_trace_buf[blockIdx.x * 4 + (i)] = __builtin_amdgcn_s_memrealtime();                         \
+    } while (0)
+#else
+#define LE_TRACE_POINT(i) do { } while (0)
+#endif
+
 __device__ const u32 le_iq2xxs_grid[512] = LE_IQ2XXS_GRID_WORDS;
 __device__ const u32 le_iq3xxs_grid[256] = LE_IQ3XXS_GRID_WORDS;
 
@@ -555,11 +568,15 @@ __device__ __forceinline__ void ms_q4k_body(const MvArgs &a) {
     const size_t rb = (size_t)nsb * 144;
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int n = lane & 15, sq = lane >> 4;
-    uint4 *rec = smem;
-    float *dxp = (float *)(smem + nsb * 32);
-    float *fsv = dxp + nsb * 16;
-    uint4 *wb = (uint4 *)(fsv + nsb * 8) + wave * (NI * 64);
-    float *red = (float *)((uint4 *)(fsv + nsb * 8) + NW * NI * 64); /* [2][NW][16] */
+    /* wave-private LDS: the activation image of this wave's super-blocks (local index ls, global
+     * super-block (ls/P)*NW*P + wave*P + ls%P), then the staging buffer; the host guarantees
+     * nsb % (NW*P) == 0 */
+    const int nsbw = nsb / NW;
+    uint4 *rec = smem + wave * (nsbw * 38 + NI * 64);
+    float *dxp = (float *)(rec + nsbw * 32);
+    float *fsv = dxp + nsbw * 16;
+    uint4 *wb = (uint4 *)(fsv + nsbw * 8);
+    float *red = (float *)(smem + NW * (nsbw * 38 + NI * 64)); /* [2][NW][16] */
     const int ntile = (a.rows + 15) >> 4;
 
     /* chunk i of this lane: row ri[i] of the tile, byte cb[i] of the row's P-super-block run */
@@ -580,22 +597,26 @@ __device__ __forceinline__ void ms_q4k_body(const MvArgs &a) {
             R[i] = ldg16(W + (size_t)row * rb + (size_t)s0 * 144 + cb[i]);
         }
     };
+    LE_TRACE_POINT(0);
     const int sfirst = wave * P, sstep = NW * P;
     const bool active = sfirst < nsb;
     /* activations of the first segment round go out first (clamped, unpredicated), then the
      * first weight item, so the quantization waits only for the activations */
     const float *xs = a.x + a.x_slot * slot;
-    const int nseg = K >> 4, e0 = threadIdx.x;
+    const int nsegw = nsbw * 16;
+    auto gseg = [&](int el) { /* local segment -> global segment */
+        const int ls = el >> 4;
+        return ((ls / P) * sstep + sfirst + ls % P) * 16 + (el & 15);
+    };
     float4 xv[4];
-    mq_load_seg(xs, min(e0, nseg - 1), xv);
+    mq_load_seg(xs, gseg(min(lane, nsegw - 1)), xv);
     issue(min((int)blockIdx.x, ntile - 1), active ? sfirst : 0); /* unpredicated: exact wait counts */
-    mq_quant_seg(e0, e0 < nseg, xv, rec, dxp, fsv);
-    for (int e = e0 + NW * 64; e < nseg; e += NW * 64) {
-        mq_load_seg(xs, e, xv);
-        mq_quant_seg(e, true, xv, rec, dxp, fsv);
+    mq_quant_seg(lane, lane < nsegw, xv, rec, dxp, fsv);
+    for (int el = lane + 64; el < nsegw; el += 64) {
+        mq_load_seg(xs, gseg(el), xv);
+        mq_quant_seg(el, true, xv, rec, dxp, fsv);
     }
-    __builtin_amdgcn_s_waitcnt(0xC07F); /* lgkmcnt(0): this wave's LDS writes are done */
-    __builtin_amdgcn_s_barrier();
+    LE_TRACE_POINT(1);
 
     const int m = lane & 15, p = m >> 3, jm = m & 7;
     bool live[4];
@@ -610,7 +631,7 @@ __device__ __forceinline__ void ms_q4k_body(const MvArgs &a) {
     for (int tile = blockIdx.x; tile < ntile; tile += gridDim.x) {
         float y = 0.f;
         if (active) {
-            for (int s0 = sfirst; s0 < nsb; s0 += sstep) {
+            for (int s0 = sfirst, lb = 0; s0 < nsb; s0 += sstep, lb += P) {
                 int nt = tile, ns = s0 + sstep;
                 if (ns >= nsb) { ns = sfirst; nt += gridDim.x; }
 #pragma unroll
@@ -618,7 +639,7 @@ __device__ __forceinline__ void ms_q4k_body(const MvArgs &a) {
                 if (nt < ntile) issue(nt, ns);
 #pragma unroll
                 for (int q = 0; q < P; q++) {
-                    const int sb = s0 + q;
+                    const int sb = lb + q; /* local super-block of this wave's image */
                     const uint4 *rowp = wb + n * CPR + 9 * q;
                     const uint4 hd = rowp[0], l0 = rowp[1 + sq], l1 = rowp[5 + sq];
 #pragma unroll
@@ -665,6 +686,7 @@ __device__ __forceinline__ void ms_q4k_body(const MvArgs &a) {
         }
         par ^= 1;
     }
+    LE_TRACE_POINT(2);
 }
 
 #define LE_MS12(P, NW)                                                                                     \
@@ -679,6 +701,6 @@ __device__ __forceinline__ void ms_q4k_body(const MvArgs &a) {
 LE_MV_ALL(LE_PART_MV)
 #if LE_PART_MV == 12
 LE_MQ12(4, 1) LE_MQ12(4, 2) LE_MQ12(4, 4) LE_MQ12(8, 1) LE_MQ12(8, 2) LE_MQ12(2, 4)
-LE_MS12(1, 4) LE_MS12(1, 8) LE_MS12(2, 4) LE_MS12(2, 8) LE_MS12(4, 2) LE_MS12(4, 4)
+LE_MS12(1, 1) LE_MS12(1, 2) LE_MS12(1, 4) LE_MS12(1, 8) LE_MS12(2, 1) LE_MS12(2, 2) LE_MS12(2, 4) LE_MS12(2, 8) LE_MS12(4, 1) LE_MS12(4, 2) LE_MS12(4, 4)
 #endif
 #endif
