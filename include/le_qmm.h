@@ -93,6 +93,23 @@ int le_matvec(le_ctx *ctx, int ty, const void *const *ptrs, const void *w, const
 int le_gemm(le_ctx *ctx, int ty, const void *w, const float *x, int m, float *y, int rows, int cols,
             le_stream_t stream);
 
+/* ---- MoE expert layer, routed part (replaces the decode chain router_topk -> host read-back ->
+ *      build_ptrs -> matvec gate/up -> swiglu -> quant_x -> matvec down -> moe_combine,
+ *      src/gpu.rs:560-597, and the prefill expert grouping of src/gpu/prefill.rs:153-215; CPU twin
+ *      cpu_ref::moe, src/cpu_ref.rs:242-259) ----
+ * For each token t < n_tok: softmax over logits[t*n_exp ...], top-k (ties keep the lower expert),
+ * weights renormalised over the k, out[t*hidden ...] = sum_s w_s * down_e(silu(gate_e h_t) * up_e h_t).
+ * gate/up: n_exp slabs of ff x hidden (types ty_gate, ty_up), down: n_exp slabs of hidden x ff
+ * (ty_down), slab e at e * rows * row_bytes. Routing and grouping by expert run on the device
+ * (no host synchronisation); each routed expert's weights are read once per call. idx_out/w_out
+ * (n_tok*k, optional) receive the selection. ws: device workspace of le_moe_workspace_size bytes.
+ * Limits: n_tok <= 64, k <= 16, n_exp <= 256, hidden and ff multiples of 256. */
+size_t le_moe_workspace_size(int n_tok, int k, int ff);
+int le_moe_layer(le_ctx *ctx, int ty_gate, int ty_up, int ty_down, const void *gate, const void *up,
+                 const void *down, int n_exp, int k, int hidden, int ff, const float *logits, const float *h,
+                 int n_tok, float *out, int *idx_out, float *w_out, void *ws, size_t ws_bytes,
+                 le_stream_t stream);
+
 #ifdef __cplusplus
 }
 #endif

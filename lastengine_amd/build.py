@@ -19,7 +19,7 @@ HIPCC = os.environ.get("HIPCC", ROCM + "/bin/hipcc")
 # Packed FP32 instructions are disabled for all device code (they are not trusted on this pool).
 DEVICE_FLAGS = ["--offload-arch=gfx950", "-O3", "-std=c++17", "-Xclang", "-target-feature", "-Xclang",
                 "-packed-fp32-ops", "-I" + CSRC]
-PARTS = {"deq": ["-DLE_PART_DEQ"]}
+PARTS = {"deq": ["-DLE_PART_DEQ"], "moe": ["-DLE_PART_MOE"]}
 for _ty in (8, 12, 14, 16, 18):
     PARTS["mv%d" % _ty] = ["-DLE_PART_MV=%d" % _ty]
 

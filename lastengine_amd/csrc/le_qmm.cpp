@@ -21,7 +21,7 @@
 
 namespace {
 
-const char *kParts[] = {"le_qmm_deq", "le_qmm_mv8", "le_qmm_mv12", "le_qmm_mv14", "le_qmm_mv16", "le_qmm_mv18"};
+const char *kParts[] = {"le_qmm_deq", "le_qmm_moe", "le_qmm_mv8", "le_qmm_mv12", "le_qmm_mv14", "le_qmm_mv16", "le_qmm_mv18"};
 
 /* Kernel argument block of le_mv_* (mirrors MvArgs in le_qmm_kernels.hip). */
 struct MvArgs {
@@ -36,6 +36,17 @@ struct MvArgs {
 };
 
 int xtok_bytes(int K) { return (K / 8) * 24; }
+
+/* Kernel argument block of le_moe_* (mirrors MoeArgs in le_qmm_kernels.hip). */
+struct MoeArgs {
+    const void *gate, *up, *down;
+    const float *logits, *h;
+    float *out;
+    void *ws;
+    int *idx_out;
+    float *w_out;
+    int n_tok, n_exp, k, hidden, ff;
+};
 int table_bytes(int ty) {
     if (ty == LE_TYPE_IQ2_XXS) return 4 * (256 + 512);
     if (ty == LE_TYPE_IQ3_XXS) return 4 * (256 + 256);
@@ -356,6 +367,41 @@ int le_matvec(le_ctx *c, int ty, const void *const *ptrs, const void *w, const f
               int rows, int cols, int slots, le_stream_t stream) {
     if (!c) return LE_ERR_ARG;
     return mv_launch(c, ty, ptrs, w, x, xstride, 0, y, (long long)rows, 0, rows, cols, 1, slots, (hipStream_t)stream);
+}
+
+size_t le_moe_workspace_size(int n_tok, int k, int ff) {
+    if (n_tok <= 0 || k <= 0 || ff <= 0) return 0;
+    return (size_t)n_tok * (size_t)k * (size_t)xtok_bytes(ff);
+}
+
+int le_moe_layer(le_ctx *c, int ty_gate, int ty_up, int ty_down, const void *gate, const void *up, const void *down,
+                 int n_exp, int k, int hidden, int ff, const float *logits, const float *h, int n_tok, float *out,
+                 int *idx_out, float *w_out, void *ws, size_t ws_bytes, le_stream_t stream) {
+    if (!c) return LE_ERR_ARG;
+    if (!gate || !up || !down || !logits || !h || !out || !ws) return c->fail(LE_ERR_ARG, "null pointer");
+    if (ty_gate != ty_up) return c->fail(LE_ERR_TYPE, "gate and up must share a type");
+    if (!supported(ty_gate) || !supported(ty_down)) return c->fail(LE_ERR_TYPE, "no kernel for types %d/%d", ty_gate, ty_down);
+    static const int combos[][2] = {{12, 14}, {12, 12}, {14, 14}, {8, 8}, {16, 18}, {16, 16}, {18, 18}};
+    bool have = false;
+    for (auto &cb : combos) have |= cb[0] == ty_gate && cb[1] == ty_down;
+    if (!have) return c->fail(LE_ERR_TYPE, "no MoE kernel for gate/up type %d with down type %d", ty_gate, ty_down);
+    if (n_tok <= 0 || n_tok > 64 || k <= 0 || k > 16 || n_exp <= 0 || n_exp > 256 || k > n_exp)
+        return c->fail(LE_ERR_SHAPE, "MoE limits: n_tok <= 64, k <= 16, k <= n_exp <= 256");
+    if (hidden <= 0 || ff <= 0 || hidden % 256 || ff % 256) return c->fail(LE_ERR_SHAPE, "hidden and ff must be multiples of 256");
+    if (ws_bytes < le_moe_workspace_size(n_tok, k, ff)) return c->fail(LE_ERR_WORKSPACE, "workspace needs %zu bytes", le_moe_workspace_size(n_tok, k, ff));
+    if (!al16(h) || !al16(ws)) return c->fail(LE_ERR_ALIGN, "h and ws must be 16-byte aligned");
+    const size_t lds = (size_t)8 * xtok_bytes(hidden);
+    if (lds + 16384 > c->lds_limit) return c->fail(LE_ERR_SHAPE, "hidden=%d exceeds the LDS budget", hidden);
+    MoeArgs a{gate, up, down, logits, h, out, ws, idx_out, w_out, n_tok, n_exp, k, hidden, ff};
+    void *args[] = {&a};
+    char name[64];
+    const int g8 = (hidden / 256) % 8 == 0;
+    snprintf(name, sizeof name, "le_moe_gu_%d_%d_g%d", ty_gate, ty_down, g8 ? 8 : 1);
+    const int groups = n_tok * k < n_exp ? n_tok * k : n_exp;
+    int rc = c->launch(name, dim3((unsigned)(ff / 32), (unsigned)groups), 256, lds, (hipStream_t)stream, args);
+    if (rc) return rc;
+    snprintf(name, sizeof name, "le_moe_down_%d", ty_down);
+    return c->launch(name, dim3((unsigned)(hidden / 8)), 256, 0, (hipStream_t)stream, args);
 }
 
 int le_gemm(le_ctx *c, int ty, const void *w, const float *x, int m, float *y, int rows, int cols,

@@ -704,3 +704,306 @@ LE_MQ12(4, 1) LE_MQ12(4, 2) LE_MQ12(4, 4) LE_MQ12(8, 1) LE_MQ12(8, 2) LE_MQ12(2,
 LE_MS12(1, 1) LE_MS12(1, 2) LE_MS12(1, 4) LE_MS12(1, 8) LE_MS12(2, 1) LE_MS12(2, 2) LE_MS12(2, 4) LE_MS12(2, 8) LE_MS12(4, 1) LE_MS12(4, 2) LE_MS12(4, 4)
 #endif
 #endif
+
+/* ===================================================================================== */
+/* MoE expert layer: routing, grouped gate/up + SwiGLU, grouped down + weighted combine.    */
+/* ===================================================================================== */
+#if defined(LE_PART_MOE)
+/* Semantics of the routed part of cpu_ref::moe (src/cpu_ref.rs:242-259) for n_tok tokens:
+ * softmax over the router logits, top-k (ties keep the lower expert first), weights renormalised
+ * over the selected k, out = sum_s w_s * down_e(silu(gate_e h) * up_e h).
+ *
+ * Two launches instead of the reference's per-layer chain of router_topk, host read-back of the
+ * indices (src/gpu.rs:579), build_ptrs, fused gate+up matvec, swiglu, quant_x, down matvec and
+ * moe_combine (src/gpu.rs:560-597). Every block recomputes the routing from the logits (a few
+ * hundred values), so nothing crosses to the host. (token, expert) pairs are grouped by expert:
+ * group z is the z-th selected expert in ascending id order, its members the tokens that chose it
+ * in ascending order, so each expert's weights are read once per launch whatever the batch.
+ *   le_moe_gu_*:   grid (ff/32, groups). Gate and up rows of one 32-row unit for all members,
+ *                  SwiGLU, and the down projection's activation image of that unit written to the
+ *                  workspace already quantized (pair p = token*k + slot).
+ *   le_moe_down_*: grid (hidden/8). The block's 8 output rows for every group; waves take groups
+ *                  round-robin and the four partial sums are added in a fixed order. */
+struct MoeArgs {
+    const u8 *gate, *up, *down;
+    const float *logits, *h;
+    float *out;
+    u8 *ws;
+    int *idx_out;
+    float *w_out;
+    int n_tok, n_exp, k, hidden, ff;
+};
+#define LE_MOE_MAXTOK 64
+#define LE_MOE_MAXK 16
+#define LE_MOE_MAXEXP 256
+
+/* LDS routing state shared by both kernels. */
+struct MoeRoute {
+    int topi[LE_MOE_MAXTOK * LE_MOE_MAXK];
+    float topw[LE_MOE_MAXTOK * LE_MOE_MAXK];
+    unsigned long long mask[LE_MOE_MAXEXP];
+    int grp_e[LE_MOE_MAXEXP];
+    int U;
+};
+
+__device__ __forceinline__ float wave_max(float v) {
+    for (int o = 32; o; o >>= 1) v = fmaxf(v, __shfl_xor(v, o));
+    return v;
+}
+__device__ __forceinline__ float wave_sum(float v) {
+    for (int o = 32; o; o >>= 1) v += __shfl_xor(v, o);
+    return v;
+}
+
+/* All threads: route every token (one wave per token), then list the groups. */
+__device__ void moe_route(const MoeArgs &a, MoeRoute &R) {
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, nwave = blockDim.x >> 6;
+    for (int e = threadIdx.x; e < a.n_exp; e += blockDim.x) R.mask[e] = 0ull;
+    __syncthreads();
+    for (int t = wave; t < a.n_tok; t += nwave) {
+        const float *lg = a.logits + (size_t)t * a.n_exp;
+        float v[4];
+        bool taken[4];
+#pragma unroll
+        for (int j = 0; j < 4; j++) {
+            const int e = lane + 64 * j;
+            v[j] = e < a.n_exp ? lg[e] : -INFINITY;
+            taken[j] = e >= a.n_exp;
+        }
+        const float m = wave_max(fmaxf(fmaxf(v[0], v[1]), fmaxf(v[2], v[3])));
+        float ex[4], ls = 0.f;
+#pragma unroll
+        for (int j = 0; j < 4; j++) {
+            ex[j] = lane + 64 * j < a.n_exp ? expf(v[j] - m) : 0.f;
+            ls += ex[j];
+        }
+        const float s = wave_sum(ls);
+        float tot = 0.f;
+        for (int r = 0; r < a.k; r++) {
+            /* best = largest logit, lower index on ties (the stable descending sort) */
+            float bv = -INFINITY;
+            int bi = 0x7fffffff;
+#pragma unroll
+            for (int j = 0; j < 4; j++)
+                if (!taken[j] && (v[j] > bv || (v[j] == bv && lane + 64 * j < bi))) { bv = v[j]; bi = lane + 64 * j; }
+            for (int o = 32; o; o >>= 1) {
+                const float ov = __shfl_xor(bv, o);
+                const int oi = __shfl_xor(bi, o);
+                if (ov > bv || (ov == bv && oi < bi)) { bv = ov; bi = oi; }
+            }
+#pragma unroll
+            for (int j = 0; j < 4; j++)
+                if (lane + 64 * j == bi) taken[j] = true;
+            const float pr = expf(bv - m) / s;
+            tot += pr;
+            if (lane == 0) {
+                R.topi[t * a.k + r] = bi;
+                R.topw[t * a.k + r] = pr;
+                atomicOr(&R.mask[bi], 1ull << t);
+            }
+        }
+        if (lane == 0)
+            for (int r = 0; r < a.k; r++) R.topw[t * a.k + r] /= tot;
+    }
+    __syncthreads();
+    if (wave == 0) {
+        int base = 0;
+        for (int c = 0; c < a.n_exp; c += 64) {
+            const int e = c + lane;
+            const bool nz = e < a.n_exp && R.mask[e] != 0ull;
+            const unsigned long long bal = __ballot(nz);
+            if (nz) R.grp_e[base + __popcll(bal & ((1ull << lane) - 1ull))] = e;
+            base += __popcll(bal);
+        }
+        if (lane == 0) R.U = base;
+    }
+    __syncthreads();
+}
+
+/* Member i (token order) of group z: its token, pair index and routing weight. */
+__device__ __forceinline__ void moe_member(const MoeArgs &a, const MoeRoute &R, int e, int i, int &t, int &pair, float &w) {
+    unsigned long long msk = R.mask[e];
+    for (int q = 0; q < i; q++) msk &= msk - 1ull;
+    t = __ffsll((long long)msk) - 1;
+    int s = 0;
+    while (R.topi[t * a.k + s] != e) s++;
+    pair = t * a.k + s;
+    w = R.topw[pair];
+}
+
+/* Launch 1: gate/up rows of unit blockIdx.x (32 rows) of group blockIdx.y for up to 8 members at
+ * a time; block of 4 waves, wave w owns rows 8w..8w+7 of the unit. */
+template <int TG, int TD, int G>
+__device__ void moe_gu_body(const MoeArgs &a) {
+    using F = Fmt<TG>;
+    using D = Dec<F::NSEG, F::WPS>;
+    __shared__ MoeRoute R;
+    __shared__ float asv[8][32];
+    __shared__ u32 tab[F::TABLES ? 256 + 512 : 1];
+    extern __shared__ uint4 smem[];
+    load_tables<TG>(tab);
+    moe_route(a, R);
+    const int z = blockIdx.y;
+    if (z >= R.U) return; /* uniform across the block */
+    const int e = R.grp_e[z];
+    const int nmem = __popcll(R.mask[e]);
+    if (blockIdx.x == 0 && z == 0) { /* routing outputs */
+        for (int i = threadIdx.x; i < a.n_tok * a.k; i += blockDim.x) {
+            if (a.idx_out) a.idx_out[i] = R.topi[i];
+            if (a.w_out) a.w_out[i] = R.topw[i];
+        }
+    }
+    const int K = a.hidden, nsb = K >> 8, ng = K >> 3;
+    const size_t rbg = (size_t)nsb * F::SB;
+    const u8 *Wg = a.gate + (size_t)e * a.ff * rbg, *Wu = a.up + (size_t)e * a.ff * rbg;
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    constexpr int RPW = 8 / G;
+    const int li = lane & 7, g = (lane >> 3) % G, rsub = lane / (8 * G);
+    const int S = nsb / G;
+    const int ux = blockIdx.x;
+    const int ngd = a.ff >> 3; /* groups of the down image */
+    const int img_bytes = le_xtok_bytes(a.ff);
+    for (int m0 = 0; m0 < nmem; m0 += 8) {
+        const int nt = min(8, nmem - m0);
+        XTok xt[8];
+        for (int i = 0; i < nt; i++) {
+            int t, pair;
+            float w;
+            moe_member(a, R, e, m0 + i, t, pair, w);
+            le_quant_x_lds<F::XL>(a.h + (size_t)t * K, K, smem + i * ng, (float2 *)(smem + 8 * ng) + i * ng);
+        }
+#pragma unroll
+        for (int i = 0; i < 8; i++) {
+            xt[i].xq = smem + i * ng;
+            xt[i].xs = (float2 *)(smem + 8 * ng) + i * ng;
+        }
+        __syncthreads();
+        for (int st = 0; st < 8 / RPW; st++) {
+            const int rl = 8 * wave + st * RPW + rsub; /* row within the 32-row unit */
+            const int row = 32 * ux + rl;
+            float ag[8], au[8];
+#pragma unroll
+            for (int i = 0; i < 8; i++) ag[i] = au[i] = 0.f;
+            for (int s = 0; s < S; s++) {
+                const int sb = g + G * s;
+                D d[2];
+                F::decode(F::load(Wg + (size_t)row * rbg + (size_t)sb * F::SB, li), li, sb, tab, d[0]);
+                F::decode(F::load(Wu + (size_t)row * rbg + (size_t)sb * F::SB, li), li, sb, tab, d[1]);
+#pragma unroll
+                for (int i = 0; i < 8; i++) {
+                    if (i < nt) {
+                        float c[2] = {0.f, 0.f};
+                        rows_dot<F::NSEG, F::WPS, F::HAS_MU, 2>(d, xt[i], sb, li, c);
+                        ag[i] += c[0];
+                        au[i] += c[1];
+                    }
+                }
+            }
+#pragma unroll
+            for (int i = 0; i < 8; i++) {
+                if (i < nt) {
+                    const float gg = group_sum<8 * G>(ag[i]), uu = group_sum<8 * G>(au[i]);
+                    if ((lane & (8 * G - 1)) == 0) asv[i][rl] = gg / (1.0f + __expf(-gg)) * uu;
+                }
+            }
+        }
+        __syncthreads();
+        /* quantize each member's 32 values into its pair image: 4 threads per member */
+        if (threadIdx.x < 4 * 8) {
+            const int i = threadIdx.x >> 2, gw = threadIdx.x & 3;
+            const bool ok = i < nt;
+            float4 va = make_float4(0.f, 0.f, 0.f, 0.f), vb = va;
+            if (ok) {
+                va = make_float4(asv[i][8 * gw], asv[i][8 * gw + 1], asv[i][8 * gw + 2], asv[i][8 * gw + 3]);
+                vb = make_float4(asv[i][8 * gw + 4], asv[i][8 * gw + 5], asv[i][8 * gw + 6], asv[i][8 * gw + 7]);
+            }
+            float am = amax8(va, vb);
+            am = fmaxf(am, __shfl_xor(am, 1));
+            am = fmaxf(am, __shfl_xor(am, 2));
+            if (ok) {
+                int t, pair;
+                float w;
+                moe_member(a, R, e, m0 + i, t, pair, w);
+                uint4 *img = (uint4 *)(a.ws + (size_t)pair * img_bytes);
+                le_quant_group(va, vb, am, img, (float2 *)(img + ngd), le_xpos<Fmt<TD>::XL>(4 * ux + gw));
+            }
+        }
+        __syncthreads();
+    }
+}
+
+/* Launch 2: output rows 8*blockIdx.x .. +7 (one row per 8-lane group) over all groups. */
+template <int TD>
+__device__ void moe_down_body(const MoeArgs &a) {
+    using F = Fmt<TD>;
+    using D = Dec<F::NSEG, F::WPS>;
+    __shared__ MoeRoute R;
+    __shared__ float red[4][LE_MOE_MAXTOK][8];
+    __shared__ u32 tab[F::TABLES ? 256 + 512 : 1];
+    load_tables<TD>(tab);
+    moe_route(a, R);
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    for (int i = threadIdx.x; i < 4 * LE_MOE_MAXTOK * 8; i += blockDim.x) (&red[0][0][0])[i] = 0.f;
+    __syncthreads();
+    const int K = a.ff, nsb = K >> 8, ng = K >> 3;
+    const size_t rbd = (size_t)nsb * F::SB;
+    const int li = lane & 7, rr = lane >> 3, row = 8 * blockIdx.x + rr;
+    const int img_bytes = le_xtok_bytes(K);
+    for (int z = wave; z < R.U; z += 4) {
+        const int e = R.grp_e[z];
+        const int nmem = __popcll(R.mask[e]);
+        const u8 *Wd = a.down + (size_t)e * a.hidden * rbd + (size_t)row * rbd;
+        for (int m0 = 0; m0 < nmem; m0 += 8) {
+            const int nt = min(8, nmem - m0);
+            XTok xt[8];
+            int tt[8];
+            float ww[8];
+#pragma unroll
+            for (int i = 0; i < 8; i++) {
+                int pair = 0;
+                tt[i] = 0;
+                ww[i] = 0.f;
+                if (i < nt) moe_member(a, R, e, m0 + i, tt[i], pair, ww[i]);
+                const uint4 *img = (const uint4 *)(a.ws + (size_t)pair * img_bytes);
+                xt[i].xq = img;
+                xt[i].xs = (const float2 *)(img + ng);
+            }
+            float acc[8];
+#pragma unroll
+            for (int i = 0; i < 8; i++) acc[i] = 0.f;
+            for (int sb = 0; sb < nsb; sb++) {
+                D d[1];
+                F::decode(F::load(Wd + (size_t)sb * F::SB, li), li, sb, tab, d[0]);
+#pragma unroll
+                for (int i = 0; i < 8; i++) {
+                    if (i < nt) {
+                        float c[1] = {0.f};
+                        rows_dot<F::NSEG, F::WPS, F::HAS_MU, 1>(d, xt[i], sb, li, c);
+                        acc[i] += c[0];
+                    }
+                }
+            }
+#pragma unroll
+            for (int i = 0; i < 8; i++) {
+                if (i < nt) {
+                    const float v = group_sum<8>(acc[i]);
+                    if (li == 0) red[wave][tt[i]][rr] += ww[i] * v;
+                }
+            }
+        }
+    }
+    __syncthreads();
+    for (int i = threadIdx.x; i < a.n_tok * 8; i += blockDim.x) {
+        const int t = i >> 3, r = i & 7;
+        a.out[(size_t)t * a.hidden + 8 * blockIdx.x + r] = ((red[0][t][r] + red[1][t][r]) + red[2][t][r]) + red[3][t][r];
+    }
+}
+
+#define LE_MOE(TG, TD)                                                                                       \
+    extern "C" __global__ void __launch_bounds__(256) le_moe_gu_##TG##_##TD##_g8(MoeArgs a) { moe_gu_body<TG, TD, 8>(a); } \
+    extern "C" __global__ void __launch_bounds__(256) le_moe_gu_##TG##_##TD##_g1(MoeArgs a) { moe_gu_body<TG, TD, 1>(a); }
+#define LE_MOE_DOWN(TD) \
+    extern "C" __global__ void __launch_bounds__(256) le_moe_down_##TD(MoeArgs a) { moe_down_body<TD>(a); }
+LE_MOE(12, 14) LE_MOE(12, 12) LE_MOE(14, 14) LE_MOE(8, 8) LE_MOE(16, 18) LE_MOE(16, 16) LE_MOE(18, 18)
+LE_MOE_DOWN(8) LE_MOE_DOWN(12) LE_MOE_DOWN(14) LE_MOE_DOWN(16) LE_MOE_DOWN(18)
+#endif /* LE_PART_MOE */

@@ -60,6 +60,8 @@ def lib():
         "le_dequant_rows": (I, [P, I, P, P, I, I, P]),
         "le_matvec": (I, [P, I, P, P, P, LL, P, I, I, I, P]),
         "le_gemm": (I, [P, I, P, P, I, P, I, I, P]),
+        "le_moe_workspace_size": (S, [I, I, I]),
+        "le_moe_layer": (I, [P, I, I, I, P, P, P, I, I, I, I, P, P, I, P, P, P, P, S, P]),
         "le_fill_normal": (None, [P, S, ctypes.c_uint64, ctypes.c_uint64, D, D, I]),
         "le_quantize_rows": (I, [I, P, P, S, S, I]),
         "le_f32_to_f16": (ctypes.c_uint16, [F]),
@@ -167,6 +169,21 @@ class Engine:
     def mv(self, ty, w, x, out, rows, cols, stream=None):
         """Gpu::mv (src/gpu.rs:238): one matrix, one activation."""
         self.mv_ptrs(ty, None, x, out, rows, cols, 0, 1, w=w, stream=stream)
+
+    def moe_workspace_size(self, n_tok, k, ff):
+        return int(self._L.le_moe_workspace_size(n_tok, k, ff))
+
+    def moe(self, ty_gate, ty_up, ty_down, gate, up, down, n_exp, k, hidden, ff, logits, h, n_tok, out,
+            idx_out=None, w_out=None, ws=None, ws_bytes=None, stream=None):
+        """Routed MoE layer (cpu_ref::moe, src/cpu_ref.rs:242-259) for n_tok tokens."""
+        if ws is None:
+            import torch
+            ws = torch.empty(max(16, self.moe_workspace_size(n_tok, k, ff)), dtype=torch.uint8, device="cuda")
+        if ws_bytes is None:
+            ws_bytes = ws.numel() if hasattr(ws, "numel") else 0
+        self._check(self._L.le_moe_layer(self._ctx, ty_gate, ty_up, ty_down, _ptr(gate), _ptr(up), _ptr(down), n_exp,
+                                         k, hidden, ff, _ptr(logits), _ptr(h), n_tok, _ptr(out), _ptr(idx_out),
+                                         _ptr(w_out), _ptr(ws), ws_bytes, _stream(stream)))
 
     def gemm(self, ty, w, x, m, out, rows, cols, stream=None):
         """DenseGpu::bmm (src/gpu/dense.rs:181): out[t*rows + r] = W[r] . x[t] for t < m."""

@@ -1,0 +1,93 @@
+"""GPU parity of the routed MoE layer against the oracle's cpu_ref::moe restatement."""
+import numpy as np
+import pytest
+
+import lastengine_amd as le
+import oracle
+from tests.util import weights, acts, check_close
+
+pytestmark = pytest.mark.gpu
+
+
+def dev(a):
+    import torch
+    return torch.from_numpy(np.ascontiguousarray(a)).cuda()
+
+
+def reference(tg, td, g, u, d, n_exp, k, hidden, ff, h, lg):
+    """Oracle output plus the condition number sum_s w_s * sum_c |down[r,c] * a_c| per output."""
+    out, idx, w = oracle.moe(tg, tg, td, g, u, d, n_exp, k, hidden, ff, h, lg)
+    rbg, rbd = le.row_bytes(tg, hidden), le.row_bytes(td, ff)
+    mag = np.zeros_like(out, dtype=np.float64)
+    for t in range(h.shape[0]):
+        for s in range(k):
+            e = idx[t, s]
+            gg = oracle.matvec(tg, g.reshape(-1)[e * ff * rbg:(e + 1) * ff * rbg], ff, hidden, h[t])
+            uu = oracle.matvec(tg, u.reshape(-1)[e * ff * rbg:(e + 1) * ff * rbg], ff, hidden, h[t])
+            a = gg / (1 + np.exp(-gg.astype(np.float64))) * uu
+            dw = oracle.dequant_rows(td, d.reshape(-1)[e * hidden * rbd:(e + 1) * hidden * rbd], hidden, ff)
+            mag[t] += w[t, s] * (np.abs(dw).astype(np.float64) @ np.abs(a))
+    return out, idx, w, mag
+
+
+def run(engine, tg, td, n_exp, k, hidden, ff, n_tok, seed, lg=None):
+    import torch
+    g, _ = weights(tg, n_exp * ff, hidden, seed)
+    u, _ = weights(tg, n_exp * ff, hidden, seed + 1)
+    d, _ = weights(td, n_exp * hidden, ff, seed + 2)
+    h = acts(n_tok * hidden, seed + 3).reshape(n_tok, hidden)
+    if lg is None:
+        lg = acts(n_tok * n_exp, seed + 4).reshape(n_tok, n_exp)
+    out = torch.empty(n_tok, hidden, dtype=torch.float32, device="cuda")
+    idx = torch.empty(n_tok, k, dtype=torch.int32, device="cuda")
+    w = torch.empty(n_tok, k, dtype=torch.float32, device="cuda")
+    engine.moe(tg, tg, td, dev(g), dev(u), dev(d), n_exp, k, hidden, ff, dev(lg), dev(h), n_tok, out, idx, w)
+    torch.cuda.synchronize()
+    want, widx, ww, mag = reference(tg, td, g, u, d, n_exp, k, hidden, ff, h, lg)
+    assert np.array_equal(idx.cpu().numpy(), widx)
+    np.testing.assert_allclose(w.cpu().numpy(), ww, rtol=2e-6, atol=1e-7)
+    check_close(out.cpu().numpy(), want, mag)
+
+
+@pytest.mark.parametrize("n_tok", [1, 3, 8])
+def test_moe_small(engine, n_tok):
+    run(engine, le.Q4_K, le.Q6_K, 16, 4, 256, 256, n_tok, seed=10 + n_tok)
+
+
+@pytest.mark.parametrize("tg,td", [(le.Q8_0, le.Q8_0), (le.IQ2_XXS, le.IQ3_XXS), (le.Q4_K, le.Q4_K)])
+def test_moe_type_combos(engine, tg, td):
+    run(engine, tg, td, 8, 2, 512, 256, 2, seed=40 + tg)
+
+
+@pytest.mark.parametrize("n_tok", [1, 8])
+def test_moe_config4(engine, n_tok):
+    """Qwen3-30B-A3B shape: 128 experts, top-8, hidden 2048, ff 768, Q4_K gate/up, Q6_K down."""
+    run(engine, le.Q4_K, le.Q6_K, 128, 8, 2048, 768, n_tok, seed=100 + n_tok)
+
+
+def test_moe_many_tokens_shared_experts(engine):
+    """More tokens than fit one member pass (8), so expert groups loop over member chunks."""
+    run(engine, le.Q4_K, le.Q6_K, 4, 2, 256, 256, 20, seed=77)
+
+
+def test_moe_tied_logits_lower_index_first(engine):
+    n_tok, n_exp, k = 2, 16, 4
+    lg = np.zeros((n_tok, n_exp), dtype=np.float32)
+    lg[0, [3, 9, 12]] = 1.5  # a three-way tie at the top
+    lg[1, :] = 0.25          # every expert tied
+    run(engine, le.Q4_K, le.Q6_K, n_exp, k, 256, 256, n_tok, seed=5, lg=lg)
+
+
+def test_moe_errors(engine):
+    import torch
+    z = torch.zeros(1 << 20, dtype=torch.uint8, device="cuda")
+    f = torch.zeros(4096, dtype=torch.float32, device="cuda")
+    with pytest.raises(le.LeError) as e:
+        engine.moe(le.Q4_K, le.Q8_0, le.Q6_K, z, z, z, 8, 2, 256, 256, f, f, 1, f)
+    assert e.value.code == -2
+    with pytest.raises(le.LeError) as e:
+        engine.moe(le.Q4_K, le.Q4_K, le.Q6_K, z, z, z, 8, 2, 256, 256, f, f, 65, f)
+    assert e.value.code == -3
+    with pytest.raises(le.LeError) as e:
+        engine.moe(le.Q4_K, le.Q4_K, le.Q6_K, z, z, z, 8, 2, 256, 256, f, f, 1, f, ws=z, ws_bytes=16)
+    assert e.value.code == -7
