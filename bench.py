@@ -1,13 +1,17 @@
 """Benchmark of the GGUF quantized-matmul hot path on one MI355X.
 
-Headline (BASELINE.json metric "Q4_K matvec GB/s (% HBM peak) @14336x4096"): one step = one batch-1
-Q4_K matvec over a 14336x4096 weight (33,030,144 B) with fp32 activations, weights already resident
-in HBM. Weight copies are rotated so the streamed footprint exceeds 512 MB and the 256 MB Infinity
-Cache cannot serve them. `value` = algorithmic bytes (weights + x + y) per step / measured time.
+Headline (BASELINE.json metric "Q4_K matvec GB/s (% HBM peak) @14336x4096; MoE layer us/token
+decode"): one step = one batch-1 Q4_K matvec over a 14336x4096 weight (33,030,144 B) with fp32
+activations, weights resident in HBM. Copies of the weight are rotated so the streamed footprint
+exceeds 512 MB and the 256 MB Infinity Cache cannot serve repeats. The steps are recorded once into
+a HIP graph (one launch per weight copy) and the graph is replayed; HIP events on that stream
+bracket the timed replays. `value` = algorithmic bytes (weights + x + y) per step / time per step.
 
-Secondary lines (same JSON object, "secondary"): the other BASELINE configs timed the same way.
-The CPU baseline times the oracle (a C restatement of the reference's cpu_ref::matvec) on a bounded
-sample of the same workload on the host's cores.
+Secondary measurements (same JSON object, "secondary"): the MoE expert layer (config 4) in
+us/token at 1 and 8 tokens, the Llama-3-8B layer matvecs and Q8_0 head (config 2), the IQ2_XXS /
+IQ3_XXS matvecs (config 5), Q4_K 4096x4096 (config 1) and the small-M GEMM (config 3).
+The CPU baseline times the oracle (a C restatement of the reference's cpu_ref::matvec) on a
+bounded sample of the headline workload on the host's cores.
 
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-secondary] [--no-cpu]
 """
@@ -30,61 +34,139 @@ def log(*a):
     print(*a, file=sys.stderr, flush=True)
 
 
-class Matrix:
-    """A quantized matrix replicated `copies` times in HBM (rotated per step)."""
-
-    def __init__(self, ty, rows, cols, seed, min_bytes=ROTATE_BYTES):
-        import torch
-        import lastengine_amd as le
-        self.ty, self.rows, self.cols = ty, rows, cols
-        src = le.fill_normal(rows * cols, seed, std=0.02).reshape(rows, cols)
-        self.host = le.quantize_rows(ty, src)
-        self.nbytes = self.host.nbytes
-        self.copies = max(1, -(-min_bytes // self.nbytes))
-        first = torch.from_numpy(self.host).cuda()
-        self.bufs = [first] + [first.clone() for _ in range(self.copies - 1)]
-
-    def __getitem__(self, i):
-        return self.bufs[i % self.copies]
-
-
-def time_steps(step, steps, warmup):
-    """Run `step(i)` warmup times, then time `steps` calls between events on the current stream
-    (the stream the library launches on). Returns ms per step."""
+def device_copies(host, min_bytes=ROTATE_BYTES):
     import torch
-    for i in range(warmup):
-        step(i)
+    first = torch.from_numpy(np.ascontiguousarray(host)).cuda()
+    n = max(1, -(-min_bytes // first.numel()))
+    return [first] + [first.clone() for _ in range(n - 1)]
+
+
+def quantized(ty, rows, cols, seed):
+    import lastengine_amd as le
+    return le.quantize_rows(ty, le.fill_normal(rows * cols, seed, std=0.02).reshape(rows, cols))
+
+
+def graph_time(record, n_launch, steps, warmup):
+    """Capture record() (n_launch steps) into a HIP graph, replay it, and time `steps` steps with
+    HIP events on the replay stream. Returns ms per step."""
+    import torch
+    s = torch.cuda.Stream()
+    with torch.cuda.stream(s):
+        record()  # eager warm-up outside capture (loads code objects)
     torch.cuda.synchronize()
-    s, e = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    s.record()
-    for i in range(steps):
-        step(warmup + i)
-    e.record()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        record()
+    reps = max(1, -(-steps // n_launch))
+    for _ in range(max(1, -(-warmup // n_launch))):
+        g.replay()
     torch.cuda.synchronize()
-    return s.elapsed_time(e) / steps
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record()
+    for _ in range(reps):
+        g.replay()
+    e1.record()
+    torch.cuda.synchronize()
+    return e0.elapsed_time(e1) / (reps * n_launch)
 
 
 def bench_matvec(eng, ty, rows, cols, steps, warmup, seed=1):
     import torch
     import lastengine_amd as le
-    m = Matrix(ty, rows, cols, seed)
+    host = quantized(ty, rows, cols, seed)
+    bufs = device_copies(host)
     x = torch.from_numpy(le.fill_normal(cols, seed + 1)).cuda()
     y = torch.empty(rows, dtype=torch.float32, device="cuda")
-    ms = time_steps(lambda i: eng.mv(ty, m[i], x, y, rows, cols), steps, warmup)
-    alg = m.nbytes + 4 * cols + 4 * rows
-    return {"ms": ms, "us": ms * 1e3, "bytes": alg, "gbs": alg / (ms * 1e-3) / 1e9}, m
+
+    def record():
+        for b in bufs:
+            eng.mv(ty, b, x, y, rows, cols)
+    ms = graph_time(record, len(bufs), steps, warmup)
+    alg = host.nbytes + 4 * cols + 4 * rows
+    return {"us": ms * 1e3, "ms": ms, "bytes": alg, "gbs": alg / (ms * 1e-3) / 1e9, "copies": len(bufs)}, host
+
+
+def bench_layer(eng, mats, steps, warmup):
+    """One step = every matvec of `mats` [(name, ty, rows, cols)] in sequence."""
+    import torch
+    import lastengine_amd as le
+    hosts = [quantized(ty, r, c, 50 + i) for i, (_, ty, r, c) in enumerate(mats)]
+    total = sum(h.nbytes for h in hosts)
+    ncopy = max(1, -(-ROTATE_BYTES // total))
+    devs = [device_copies(h, min_bytes=ncopy * h.nbytes) for h in hosts]
+    xs = {c: torch.from_numpy(le.fill_normal(c, c)).cuda() for (_, _, _, c) in mats}
+    ys = [torch.empty(r, dtype=torch.float32, device="cuda") for (_, _, r, _) in mats]
+
+    def record():
+        for k in range(ncopy):
+            for i, (_, ty, r, c) in enumerate(mats):
+                eng.mv(ty, devs[i][k], xs[c], ys[i], r, c)
+    ms = graph_time(record, ncopy, steps, warmup)
+    alg = total + sum(4 * (r + c) for (_, _, r, c) in mats)
+    return {"us": round(ms * 1e3, 3), "GB/s": round(alg / (ms * 1e-3) / 1e9, 1),
+            "frac_hbm": round(alg / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4), "weight_bytes": total}
 
 
 def bench_gemm(eng, ty, rows, cols, mtok, steps, warmup, seed=3):
     import torch
     import lastengine_amd as le
-    m = Matrix(ty, rows, cols, seed)
+    host = quantized(ty, rows, cols, seed)
+    bufs = device_copies(host)
     x = torch.from_numpy(le.fill_normal(mtok * cols, seed + 1)).cuda()
     y = torch.empty(mtok * rows, dtype=torch.float32, device="cuda")
-    ms = time_steps(lambda i: eng.gemm(ty, m[i], x, mtok, y, rows, cols), steps, warmup)
-    flops = 2.0 * mtok * rows * cols
-    alg = m.nbytes + 4 * mtok * (cols + rows)
-    return {"m": mtok, "us": ms * 1e3, "gbs": alg / (ms * 1e-3) / 1e9, "tflops": flops / (ms * 1e-3) / 1e12}
+
+    def record():
+        for b in bufs:
+            eng.gemm(ty, b, x, mtok, y, rows, cols)
+    ms = graph_time(record, len(bufs), steps, warmup)
+    alg = host.nbytes + 4 * mtok * (cols + rows)
+    return {"us": round(ms * 1e3, 2), "GB/s": round(alg / (ms * 1e-3) / 1e9, 1),
+            "TFLOP/s": round(2.0 * mtok * rows * cols / (ms * 1e-3) / 1e12, 2)}
+
+
+def unique_experts(logits, k):
+    top = np.argsort(-logits, axis=1, kind="stable")[:, :k]
+    return len(np.unique(top))
+
+
+def bench_moe(eng, n_tok, steps, warmup, n_exp=128, k=8, hidden=2048, ff=768, copies=4, variants=8):
+    """Config 4: Qwen3-30B-A3B expert layer. Rotates `copies` full expert sets (each 392 MB) and
+    `variants` router-logit draws so repeated steps stream different experts."""
+    import torch
+    import lastengine_amd as le
+    tg, td = le.Q4_K, le.Q6_K
+    g = quantized(tg, n_exp * ff, hidden, 201)
+    u = quantized(tg, n_exp * ff, hidden, 202)
+    d = quantized(td, n_exp * hidden, ff, 203)
+    per_expert = (g.nbytes + u.nbytes + d.nbytes) // n_exp
+    sets = []
+    for c in range(copies):
+        if c == 0:
+            sets.append(tuple(torch.from_numpy(a).cuda() for a in (g, u, d)))
+        else:
+            sets.append(tuple(t.clone() for t in sets[0]))
+    del g, u, d
+    lgs = [le.fill_normal(n_tok * n_exp, 300 + i).reshape(n_tok, n_exp) for i in range(variants)]
+    dlg = [torch.from_numpy(l).cuda() for l in lgs]
+    h = torch.from_numpy(le.fill_normal(n_tok * hidden, 299)).cuda()
+    out = torch.empty(n_tok * hidden, dtype=torch.float32, device="cuda")
+    ws = torch.empty(eng.moe_workspace_size(n_tok, k, ff), dtype=torch.uint8, device="cuda")
+    n_launch = copies * variants
+
+    def record():
+        for i in range(n_launch):
+            gs, us_, ds = sets[i % copies]
+            eng.moe(tg, tg, td, gs, us_, ds, n_exp, k, hidden, ff, dlg[i % variants], h, n_tok, out, ws=ws)
+    ms = graph_time(record, n_launch, steps, warmup)
+    uniq = float(np.mean([unique_experts(l, k) for l in lgs]))
+    wbytes = uniq * per_expert
+    res = {"n_tok": n_tok, "us_per_layer": round(ms * 1e3, 3), "us_per_token": round(ms * 1e3 / n_tok, 3),
+           "unique_experts": uniq, "weight_bytes": int(wbytes), "GB/s": round(wbytes / (ms * 1e-3) / 1e9, 1),
+           "roofline_us": round(wbytes / (HBM_PEAK_GBS * 1e9) * 1e6, 3)}
+    res["x_roofline"] = round(res["us_per_layer"] / res["roofline_us"], 2)
+    del sets
+    torch.cuda.empty_cache()
+    return res
 
 
 def cpu_baseline(ty, host_q, rows, cols, budget_s=2.0):
@@ -104,8 +186,8 @@ def cpu_baseline(ty, host_q, rows, cols, budget_s=2.0):
     per = el / reps
     gbs = (host_q.nbytes + 4 * cols + 4 * rows) / per / 1e9
     return {"value": round(gbs, 3), "unit": "GB/s", "cores": threads, "kind": "port",
-            "sample": "%d full %dx%d Q4_K matvecs (oracle, %d threads), %.1f ms each" % (reps, rows, cols, threads,
-                                                                                     per * 1e3)}
+            "sample": "%d full %dx%d Q4_K matvecs by the oracle on %d host threads, %.1f ms each" % (
+                reps, rows, cols, threads, per * 1e3)}
 
 
 def main():
@@ -117,8 +199,8 @@ def main():
     ap.add_argument("--no-cpu", action="store_true")
     args = ap.parse_args()
     if args.gpus != 1:
-        print("bench.py measures one GPU only: this build has no multi-GPU path (every box here has one "
-              "GPU); run with --gpus 1", file=sys.stderr)
+        print("bench.py measures one GPU: this build has no multi-GPU path (each box has one GPU); "
+              "run with --gpus 1", file=sys.stderr)
         sys.exit(2)
 
     import torch
@@ -129,8 +211,8 @@ def main():
     log("device:", props.name, getattr(props, "gcnArchName", ""), "CUs", props.multi_processor_count)
 
     rows, cols = 14336, 4096
-    head, m = bench_matvec(eng, le.Q4_K, rows, cols, args.steps, args.warmup)
-    log("headline Q4_K %dx%d: %.2f us, %.1f GB/s" % (rows, cols, head["us"], head["gbs"]))
+    head, host = bench_matvec(eng, le.Q4_K, rows, cols, args.steps, args.warmup)
+    log("headline Q4_K %dx%d: %.3f us, %.1f GB/s" % (rows, cols, head["us"], head["gbs"]))
 
     out = {
         "metric": "Q4_K matvec GB/s (% HBM peak) @14336x4096; MoE layer us/token decode",
@@ -143,38 +225,57 @@ def main():
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
-        "dtype": "q4_k weights x fp32 activations, fp32 accumulate",
-        "data": "synthetic: seeded N(0,0.02) weights quantized by this repo's Q4_K quantizer, N(0,1) activations",
-        "config": {"workload": "Q4_K batch-1 matvec 14336x4096 (gate/up of a Llama-3-8B layer)", "rows": rows,
-                   "cols": cols, "weight_bytes": m.nbytes, "rotated_copies": m.copies,
-                   "parallelism": "single GPU"},
-        "roofline": {"bound": "hbm", "kernel": "le_mv_12_g8_t1", "achieved": round(head["gbs"], 2),
+        "dtype": "q4_k",
+        "data": "synthetic: seeded N(0,0.02) weights quantized by this repo's quantizer, N(0,1) activations",
+        "config": {"workload": "Q4_K batch-1 matvec 14336x4096 (config 2 gate/up shape)", "rows": rows,
+                   "cols": cols, "weight_bytes": int(host.nbytes), "rotated_copies": head["copies"],
+                   "activations": "fp32 in, fp32 out, fp32 accumulation"},
+        "roofline": {"bound": "hbm", "kernel": "le_ms_12_p2_w4", "achieved": round(head["gbs"], 2),
                      "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": round(head["gbs"] / HBM_PEAK_GBS, 4),
                      "traffic": None},
     }
+    tr = os.path.join(REPO, "profiles", "traffic_le_ms_12_14336x4096.json")
+    if os.path.exists(tr):
+        out["roofline"]["traffic"] = json.load(open(tr)).get("hbm_bytes_per_launch")
 
     if not args.no_secondary:
         sec = {}
-        steps2 = max(50, args.steps // 4)
-        for name, ty, r, c in [("cfg1_q4k_4096x4096", le.Q4_K, 4096, 4096),
-                               ("q6k_4096x14336", le.Q6_K, 4096, 14336),
-                               ("q8_0_head_32000x4096", le.Q8_0, 32000, 4096),
-                               ("iq2xxs_14336x4096", le.IQ2_XXS, 14336, 4096),
-                               ("iq3xxs_4096x14336", le.IQ3_XXS, 4096, 14336)]:
-            r_, _ = bench_matvec(eng, ty, r, c, steps2, args.warmup // 4)
-            sec[name] = {"us": round(r_["us"], 3), "GB/s": round(r_["gbs"], 1),
-                         "frac_hbm": round(r_["gbs"] / HBM_PEAK_GBS, 4)}
+        steps2 = max(100, args.steps // 4)
+        for nt in (1, 8):
+            r = bench_moe(eng, nt, max(64, steps2 // 4), 32)
+            sec["moe_config4_ntok%d" % nt] = r
+            log("moe", r)
+        r, _ = bench_matvec(eng, le.Q4_K, 4096, 4096, steps2, args.warmup // 4)
+        sec["config1_q4k_4096x4096"] = {"us": round(r["us"], 3), "GB/s": round(r["gbs"], 1),
+                                        "frac_hbm": round(r["gbs"] / HBM_PEAK_GBS, 4)}
+        log("config1", sec["config1_q4k_4096x4096"])
+        layer = [("wq", le.Q4_K, 4096, 4096), ("wk", le.Q4_K, 1024, 4096), ("wv", le.Q4_K, 1024, 4096),
+                 ("wo", le.Q4_K, 4096, 4096), ("gate", le.Q4_K, 14336, 4096), ("up", le.Q4_K, 14336, 4096),
+                 ("down", le.Q6_K, 4096, 14336)]
+        sec["config2_llama3_8b_layer"] = bench_layer(eng, layer, max(40, steps2 // 8), 8)
+        log("config2 layer", sec["config2_llama3_8b_layer"])
+        sec["config2_q8_0_head_32000x4096"] = bench_layer(eng, [("head", le.Q8_0, 32000, 4096)], max(40, steps2 // 8), 8)
+        log("config2 head", sec["config2_q8_0_head_32000x4096"])
+        for name, ty, r_, c_ in [("q6k_down_4096x14336", le.Q6_K, 4096, 14336),
+                                 ("iq2xxs_14336x4096", le.IQ2_XXS, 14336, 4096),
+                                 ("iq3xxs_4096x14336", le.IQ3_XXS, 4096, 14336)]:
+            r, _ = bench_matvec(eng, ty, r_, c_, steps2, args.warmup // 4)
+            sec[name] = {"us": round(r["us"], 3), "GB/s": round(r["gbs"], 1), "frac_hbm": round(r["gbs"] / HBM_PEAK_GBS, 4)}
             log(name, sec[name])
             torch.cuda.empty_cache()
+        sec["config5_iq_gate_up_down"] = bench_layer(
+            eng, [("gate", le.IQ2_XXS, 14336, 4096), ("up", le.IQ2_XXS, 14336, 4096), ("down", le.IQ3_XXS, 4096, 14336)],
+            max(40, steps2 // 8), 8)
+        log("config5", sec["config5_iq_gate_up_down"])
         for mt in (4, 8, 16, 64, 512):
-            g = bench_gemm(eng, le.Q4_K, 14336, 4096, mt, max(20, steps2 // (1 + mt // 16)), 5)
-            sec["gemm_q4k_14336x4096_m%d" % mt] = {"us": round(g["us"], 2), "GB/s": round(g["gbs"], 1),
-                                                  "TFLOP/s": round(g["tflops"], 2)}
-            log("gemm m=%d" % mt, sec["gemm_q4k_14336x4096_m%d" % mt])
+            g = bench_gemm(eng, le.Q4_K, 14336, 4096, mt, max(20, steps2 // (1 + mt // 8)), 4)
+            sec["config3_gemm_q4k_14336x4096_m%d" % mt] = g
+            log("gemm m=%d" % mt, g)
+            torch.cuda.empty_cache()
         out["secondary"] = sec
 
     if not args.no_cpu:
-        out["cpu_baseline"] = cpu_baseline(le.Q4_K, m.host, rows, cols)
+        out["cpu_baseline"] = cpu_baseline(le.Q4_K, host, rows, cols)
         log("cpu baseline", out["cpu_baseline"])
     print(json.dumps(out), flush=True)
 

@@ -66,6 +66,7 @@ struct le_ctx {
     int mq = 1;              /* decode matvec on MFMA where available */
     int mq_waves = 4, mq_steps = 2, mq_blocks_per_cu = 2;
     int ms = 1, ms_p = 2;    /* staged MFMA variant and its super-blocks per row and step */
+    int moe_fast = 1;        /* decode-shaped MoE kernels */
     std::vector<hipModule_t> mods;
     std::map<std::string, hipFunction_t> fns;
     std::string err;
@@ -322,6 +323,8 @@ int le_set_option(le_ctx *c, const char *name, int value) {
         c->mv_blocks_per_cu = value;
     } else if (n == "mq") {
         c->mq = value ? 1 : 0;
+    } else if (n == "moe_fast") {
+        c->moe_fast = value ? 1 : 0;
     } else if (n == "ms") {
         c->ms = value ? 1 : 0;
     } else if (n == "ms_p") {
@@ -395,13 +398,18 @@ int le_moe_layer(le_ctx *c, int ty_gate, int ty_up, int ty_down, const void *gat
     MoeArgs a{gate, up, down, logits, h, out, ws, idx_out, w_out, n_tok, n_exp, k, hidden, ff};
     void *args[] = {&a};
     char name[64];
-    const int g8 = (hidden / 256) % 8 == 0;
-    snprintf(name, sizeof name, "le_moe_gu_%d_%d_g%d", ty_gate, ty_down, g8 ? 8 : 1);
+    const int nsb = hidden / 256, g8 = nsb % 8 == 0;
+    const int S = g8 ? nsb / 8 : nsb;
     const int groups = n_tok * k < n_exp ? n_tok * k : n_exp;
-    int rc = c->launch(name, dim3((unsigned)(ff / 32), (unsigned)groups), 256, lds, (hipStream_t)stream, args);
+    /* decode-shaped fast paths: few tokens, short rows */
+    const bool fast_gu = c->moe_fast && n_tok <= 8 && S <= 2 && n_tok * (hidden / 8) <= 4096;
+    const bool fast_dn = c->moe_fast && n_tok <= 8 && ff <= 1024;
+    snprintf(name, sizeof name, fast_gu ? "le_moe_guf_%d_%d_g%d" : "le_moe_gu_%d_%d_g%d", ty_gate, ty_down, g8 ? 8 : 1);
+    int rc = c->launch(name, dim3((unsigned)(ff / 32), (unsigned)groups), fast_gu ? 1024 : 256, lds,
+                       (hipStream_t)stream, args);
     if (rc) return rc;
-    snprintf(name, sizeof name, "le_moe_down_%d", ty_down);
-    return c->launch(name, dim3((unsigned)(hidden / 8)), 256, 0, (hipStream_t)stream, args);
+    snprintf(name, sizeof name, fast_dn ? "le_moe_downf_%d" : "le_moe_down_%d", ty_down);
+    return c->launch(name, dim3((unsigned)(hidden / 8)), fast_dn ? 512 : 256, fast_dn ? 49152 : 0, (hipStream_t)stream, args);
 }
 
 int le_gemm(le_ctx *c, int ty, const void *w, const float *x, int m, float *y, int rows, int cols,

@@ -17,17 +17,23 @@
 #include "le_iq_tables.h"
 #include "le_qmm_device.h"
 
-/* Optional per-block timestamps for diagnostic builds (-DLE_TRACE): slot i of block b at
- * le_trace_buf[b * 4 + i]. Compiled out otherwise. */
+/* Optional per-block timestamps for diagnostic builds (-DLE_TRACE): LE_TRACE_DECL at kernel
+ * entry, LE_TRACE_POINT(i) keeps s_memrealtime in registers (no store between barriers, which
+ * would make the next barrier wait for it), LE_TRACE_FLUSH writes slot i of block b to
+ * le_trace_buf[b * 8 + i]. Compiled out otherwise. */
 #if defined(LE_TRACE)
 __device__ unsigned long long le_trace_buf[1 << 16];
-#define LE_TRACE_POINT(i)                                                                                  \
+#define LE_TRACE_DECL unsigned long long le_tr_[8] = {0, 0, 0, 0, 0, 0, 0, 0}
+#define LE_TRACE_POINT(i) do { le_tr_[i] = __builtin_amdgcn_s_memrealtime(); } while (0)
+#define LE_TRACE_FLUSH                                                                                     \
     do {                                                                                                   \
-        if (threadIdx.x == 0 && blockIdx.y == 0 && blockIdx.x < (1 << 14))                                 \
-            le_trace_buf[blockIdx.x * 4 + (i)] = __builtin_amdgcn_s_memrealtime();                         \
+        if (threadIdx.x == 0 && blockIdx.y == 0 && blockIdx.x < (1 << 13))                                 \
+            for (int i_ = 0; i_ < 8; i_++) le_trace_buf[blockIdx.x * 8 + i_] = le_tr_[i_];                 \
     } while (0)
 #else
+#define LE_TRACE_DECL do { } while (0)
 #define LE_TRACE_POINT(i) do { } while (0)
+#define LE_TRACE_FLUSH do { } while (0)
 #endif
 
 __device__ const u32 le_iq2xxs_grid[512] = LE_IQ2XXS_GRID_WORDS;
@@ -597,6 +603,7 @@ __device__ __forceinline__ void ms_q4k_body(const MvArgs &a) {
             R[i] = ldg16(W + (size_t)row * rb + (size_t)s0 * 144 + cb[i]);
         }
     };
+    LE_TRACE_DECL;
     LE_TRACE_POINT(0);
     const int sfirst = wave * P, sstep = NW * P;
     const bool active = sfirst < nsb;
@@ -687,6 +694,7 @@ __device__ __forceinline__ void ms_q4k_body(const MvArgs &a) {
         par ^= 1;
     }
     LE_TRACE_POINT(2);
+    LE_TRACE_FLUSH;
 }
 
 #define LE_MS12(P, NW)                                                                                     \
@@ -746,67 +754,153 @@ struct MoeRoute {
     int U;
 };
 
+/* Wave-wide max / sum: DPP within 16-lane rows, then the four row results through readlane, so the
+ * result is uniform (no LDS-routed shuffles on the routing critical path). */
 __device__ __forceinline__ float wave_max(float v) {
-    for (int o = 32; o; o >>= 1) v = fmaxf(v, __shfl_xor(v, o));
-    return v;
+    v = fmaxf(v, dpp_f<0xB1>(v));
+    v = fmaxf(v, dpp_f<0x4E>(v));
+    v = fmaxf(v, dpp_f<0x141>(v));
+    v = fmaxf(v, dpp_f<0x140>(v));
+    const int b = __builtin_bit_cast(int, v);
+    return fmaxf(fmaxf(__builtin_bit_cast(float, __builtin_amdgcn_readlane(b, 0)), __builtin_bit_cast(float, __builtin_amdgcn_readlane(b, 16))),
+                 fmaxf(__builtin_bit_cast(float, __builtin_amdgcn_readlane(b, 32)), __builtin_bit_cast(float, __builtin_amdgcn_readlane(b, 48))));
 }
 __device__ __forceinline__ float wave_sum(float v) {
-    for (int o = 32; o; o >>= 1) v += __shfl_xor(v, o);
-    return v;
+    v += dpp_f<0xB1>(v);
+    v += dpp_f<0x4E>(v);
+    v += dpp_f<0x141>(v);
+    v += dpp_f<0x140>(v);
+    const int b = __builtin_bit_cast(int, v);
+    return (__builtin_bit_cast(float, __builtin_amdgcn_readlane(b, 0)) + __builtin_bit_cast(float, __builtin_amdgcn_readlane(b, 16))) +
+           (__builtin_bit_cast(float, __builtin_amdgcn_readlane(b, 32)) + __builtin_bit_cast(float, __builtin_amdgcn_readlane(b, 48)));
 }
 
-/* All threads: route every token (one wave per token), then list the groups. */
+/* All threads: route every token (one wave per token), then list the groups. Lane l holds
+ * experts l*per .. l*per+per-1 (per <= 4), so among lanes tied on the best logit the lowest lane
+ * holds the lowest expert index: the ballot's first set bit is the winner (the stable descending
+ * sort of src/cpu_ref.rs:248 keeps the lower index first). */
 __device__ void moe_route(const MoeArgs &a, MoeRoute &R) {
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, nwave = blockDim.x >> 6;
-    for (int e = threadIdx.x; e < a.n_exp; e += blockDim.x) R.mask[e] = 0ull;
-    __syncthreads();
+    const int per = (a.n_exp + 63) >> 6;
     for (int t = wave; t < a.n_tok; t += nwave) {
         const float *lg = a.logits + (size_t)t * a.n_exp;
         float v[4];
         bool taken[4];
 #pragma unroll
         for (int j = 0; j < 4; j++) {
-            const int e = lane + 64 * j;
-            v[j] = e < a.n_exp ? lg[e] : -INFINITY;
-            taken[j] = e >= a.n_exp;
+            const int e = lane * per + j;
+            const bool ok = j < per && e < a.n_exp;
+            v[j] = ok ? lg[e] : -INFINITY;
+            taken[j] = !ok;
         }
         const float m = wave_max(fmaxf(fmaxf(v[0], v[1]), fmaxf(v[2], v[3])));
-        float ex[4], ls = 0.f;
+        float ls = 0.f;
 #pragma unroll
-        for (int j = 0; j < 4; j++) {
-            ex[j] = lane + 64 * j < a.n_exp ? expf(v[j] - m) : 0.f;
-            ls += ex[j];
-        }
+        for (int j = 0; j < 4; j++) ls += taken[j] ? 0.f : expf(v[j] - m);
         const float s = wave_sum(ls);
         float tot = 0.f;
         for (int r = 0; r < a.k; r++) {
-            /* best = largest logit, lower index on ties (the stable descending sort) */
             float bv = -INFINITY;
-            int bi = 0x7fffffff;
+            int bj = -1;
 #pragma unroll
             for (int j = 0; j < 4; j++)
-                if (!taken[j] && (v[j] > bv || (v[j] == bv && lane + 64 * j < bi))) { bv = v[j]; bi = lane + 64 * j; }
-            for (int o = 32; o; o >>= 1) {
-                const float ov = __shfl_xor(bv, o);
-                const int oi = __shfl_xor(bi, o);
-                if (ov > bv || (ov == bv && oi < bi)) { bv = ov; bi = oi; }
+                if (!taken[j] && (bj < 0 || v[j] > bv)) { bv = v[j]; bj = j; }
+            const float mx = wave_max(bj >= 0 ? bv : -INFINITY);
+            const unsigned long long cand = __ballot(bj >= 0 && bv == mx);
+            const int wl = __ffsll((long long)cand) - 1;
+            const int wj = __builtin_amdgcn_readlane(bj, wl);
+            if (lane == wl) {
+#pragma unroll
+                for (int j = 0; j < 4; j++)
+                    if (j == wj) taken[j] = true;
             }
-#pragma unroll
-            for (int j = 0; j < 4; j++)
-                if (lane + 64 * j == bi) taken[j] = true;
-            const float pr = expf(bv - m) / s;
+            const float pr = expf(mx - m) / s;
             tot += pr;
             if (lane == 0) {
-                R.topi[t * a.k + r] = bi;
+                R.topi[t * a.k + r] = wl * per + wj;
                 R.topw[t * a.k + r] = pr;
-                atomicOr(&R.mask[bi], 1ull << t);
             }
         }
         if (lane == 0)
             for (int r = 0; r < a.k; r++) R.topw[t * a.k + r] /= tot;
     }
     __syncthreads();
+    /* expert masks from the top-k table (no atomics, no zeroing pass) */
+    const int nsel = a.n_tok * a.k;
+    for (int e = threadIdx.x; e < a.n_exp; e += blockDim.x) {
+        unsigned long long msk = 0ull;
+        for (int i = 0; i < nsel; i++)
+            if (R.topi[i] == e) msk |= 1ull << (i / a.k);
+        R.mask[e] = msk;
+    }
+    __syncthreads();
     if (wave == 0) {
+        int base = 0;
+        for (int c = 0; c < a.n_exp; c += 64) {
+            const int e = c + lane;
+            const bool nz = e < a.n_exp && R.mask[e] != 0ull;
+            const unsigned long long bal = __ballot(nz);
+            if (nz) R.grp_e[base + __popcll(bal & ((1ull << lane) - 1ull))] = e;
+            base += __popcll(bal);
+        }
+        if (lane == 0) R.U = base;
+    }
+    __syncthreads();
+}
+
+/* Parallel routing for the decode-shaped kernels (n_exp <= 256): one thread per (token, expert).
+ * An expert's rank is the number of experts with a larger logit, or an equal logit and a lower
+ * index, i.e. its position in the stable descending sort of src/cpu_ref.rs:248; rank < k selects
+ * it. With ex = exp(logit - max), the renormalised weight pr/sum(pr over the k) equals
+ * ex/sum(ex over the k) (the softmax denominator cancels); the k-sum runs in selection order. */
+__device__ void moe_route_par(const MoeArgs &a, MoeRoute &R, float *lv /* [n_tok][n_exp] LDS */, float *sx /* [n_tok][k] */) {
+    const int tpt = a.n_exp <= 128 ? 128 : 256;
+    const int tpp = blockDim.x / tpt; /* tokens per pass */
+    for (int t0 = 0; t0 < a.n_tok; t0 += tpp) {
+        const int t = t0 + threadIdx.x / tpt, e = threadIdx.x % tpt;
+        const bool ok = t < a.n_tok && e < a.n_exp;
+        const float v = ok ? a.logits[(size_t)t * a.n_exp + e] : 0.f;
+        if (ok) lv[t * a.n_exp + e] = v;
+        __syncthreads();
+        if (ok) {
+            const float4 *row = (const float4 *)(lv + t * a.n_exp);
+            int rank = 0;
+            float m = v;
+            /* a compact loop: this runs once per launch, so code size (instruction fetch) costs
+             * more than loop overhead */
+#pragma unroll 1
+            for (int j4 = 0; j4 < (a.n_exp >> 2); j4++) {
+                const float4 u = row[j4];
+                const int j = 4 * j4;
+                rank += (u.x > v) || (u.x == v && j < e);
+                rank += (u.y > v) || (u.y == v && j + 1 < e);
+                rank += (u.z > v) || (u.z == v && j + 2 < e);
+                rank += (u.w > v) || (u.w == v && j + 3 < e);
+                m = fmaxf(fmaxf(m, fmaxf(u.x, u.y)), fmaxf(u.z, u.w));
+            }
+            if (rank < a.k) {
+                R.topi[t * a.k + rank] = e;
+                sx[t * a.k + rank] = expf(v - m);
+            }
+        }
+        __syncthreads();
+    }
+    for (int i = threadIdx.x; i < a.n_tok * a.k; i += blockDim.x) {
+        const int t = i / a.k;
+        float tot = 0.f;
+        for (int r = 0; r < a.k; r++) tot += sx[t * a.k + r];
+        R.topw[i] = sx[i] / tot;
+    }
+    const int nsel = a.n_tok * a.k;
+    for (int e = threadIdx.x; e < a.n_exp; e += blockDim.x) {
+        unsigned long long msk = 0ull;
+        for (int i = 0; i < nsel; i++)
+            if (R.topi[i] == e) msk |= 1ull << (i / a.k);
+        R.mask[e] = msk;
+    }
+    __syncthreads();
+    const int lane = threadIdx.x & 63;
+    if (threadIdx.x < 64) {
         int base = 0;
         for (int c = 0; c < a.n_exp; c += 64) {
             const int e = c + lane;
@@ -999,11 +1093,281 @@ __device__ void moe_down_body(const MoeArgs &a) {
     }
 }
 
+/* Decode-shaped fast paths (n_tok <= 8): every wave issues all of its weight loads at once, the
+ * activations and router logits go out before anything waits, and the down projection reads the
+ * quantized SwiGLU images from LDS when they fit. */
+#define LE_MOE_FAST_TOK 8
+template <int TG, int TD, int G>
+__device__ void moe_gu_fast(const MoeArgs &a) {
+    using F = Fmt<TG>;
+    using D = Dec<F::NSEG, F::WPS>;
+    using Raw = typename F::Raw;
+    constexpr int NW = 16, RPW = 8 / G, JS = (32 / RPW + NW - 1) / NW, XR = 4;
+    __shared__ MoeRoute R;
+    __shared__ float asv[8][32];
+    __shared__ __attribute__((aligned(16))) float lv[LE_MOE_FAST_TOK * LE_MOE_MAXEXP];
+    __shared__ float sx[LE_MOE_FAST_TOK * LE_MOE_MAXK];
+    __shared__ u32 tab[F::TABLES ? 256 + 512 : 1];
+    extern __shared__ uint4 smem[];
+    const int K = a.hidden, nsb = K >> 8, ng = K >> 3;
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    /* 1. every token's activations (n_tok * ng <= XR * 1024 groups), clamped and unpredicated */
+    LE_TRACE_DECL;
+    LE_TRACE_POINT(0);
+#if defined(LE_TRACE)
+    le_tr_[6] = __builtin_amdgcn_s_memtime();
+#endif
+    float4 ha[XR], hb[XR];
+    const int ngt = a.n_tok * ng;
+#pragma unroll
+    for (int r = 0; r < XR; r++) {
+        const int gp = min((int)threadIdx.x + 1024 * r, ngt - 1);
+        const float *src = a.h + (size_t)(gp / ng) * K + 8 * (gp % ng);
+        ha[r] = *(const LE_GLOBAL float4 *)src;
+        hb[r] = *(const LE_GLOBAL float4 *)(src + 4);
+    }
+    load_tables<TG>(tab);
+    moe_route_par(a, R, lv, sx);
+    LE_TRACE_POINT(1);
+    const int z = blockIdx.y;
+    if (z >= R.U) return;
+    const int e = R.grp_e[z];
+    const int nmem = __popcll(R.mask[e]);
+    if (blockIdx.x == 0 && z == 0) {
+        for (int i = threadIdx.x; i < a.n_tok * a.k; i += blockDim.x) {
+            if (a.idx_out) a.idx_out[i] = R.topi[i];
+            if (a.w_out) a.w_out[i] = R.topw[i];
+        }
+    }
+    /* 2. weight loads of this wave's rows: wave-step ws = wave + NW*j covers rows ws*RPW .. */
+    const size_t rbg = (size_t)nsb * F::SB;
+    const u8 *Wg = a.gate + (size_t)e * a.ff * rbg, *Wu = a.up + (size_t)e * a.ff * rbg;
+    const int li = lane & 7, g = (lane >> 3) % G, rsub = lane / (8 * G);
+    const int S = nsb / G; /* <= 2 on this path */
+    const int ux = blockIdx.x;
+    Raw rg[JS][2], ru[JS][2];
+#pragma unroll
+    for (int j = 0; j < JS; j++) {
+        const int rl = min((wave + NW * j) * RPW + rsub, 31);
+        const size_t ro = (size_t)(32 * ux + rl) * rbg;
+#pragma unroll
+        for (int s = 0; s < 2; s++) {
+            const int sb = g + G * min(s, S - 1);
+            rg[j][s] = F::load(Wg + ro + (size_t)sb * F::SB, li);
+            ru[j][s] = F::load(Wu + ro + (size_t)sb * F::SB, li);
+        }
+    }
+    /* 3. quantize the activations into token images */
+    uint4 *xq = smem;
+    float2 *xs = (float2 *)(smem + LE_MOE_FAST_TOK * ng);
+#pragma unroll
+    for (int r = 0; r < XR; r++) {
+        const int gp = (int)threadIdx.x + 1024 * r;
+        if (r * 1024 >= ngt) break;
+        float am = amax8(ha[r], hb[r]);
+        am = fmaxf(am, __shfl_xor(am, 1));
+        am = fmaxf(am, __shfl_xor(am, 2));
+        if (gp < ngt) {
+            const int t = gp / ng, p = gp % ng;
+            le_quant_group(ha[r], hb[r], am, xq + t * ng, xs + t * ng, le_xpos<F::XL>(p));
+        }
+    }
+    int tokm[8], pairm[8];
+    float wm[8];
+#pragma unroll
+    for (int i = 0; i < 8; i++) {
+        tokm[i] = 0;
+        pairm[i] = 0;
+        if (i < nmem) moe_member(a, R, e, i, tokm[i], pairm[i], wm[i]);
+    }
+    __syncthreads();
+    LE_TRACE_POINT(2);
+    /* 4. gate and up rows for every member; the wave's JS rows go through one dot so their
+     * chains interleave */
+    float ag[JS][8], au[JS][8];
+#pragma unroll
+    for (int j = 0; j < JS; j++)
+#pragma unroll
+        for (int i = 0; i < 8; i++) ag[j][i] = au[j][i] = 0.f;
+#pragma unroll
+    for (int s = 0; s < 2; s++) {
+        if (s < S) {
+            const int sb = g + G * s;
+            D d[2 * JS];
+#pragma unroll
+            for (int j = 0; j < JS; j++) {
+                F::decode(rg[j][s], li, sb, tab, d[2 * j]);
+                F::decode(ru[j][s], li, sb, tab, d[2 * j + 1]);
+            }
+#pragma unroll
+            for (int i = 0; i < 8; i++) {
+                if (i < nmem) {
+                    XTok xt;
+                    xt.xq = xq + tokm[i] * ng;
+                    xt.xs = xs + tokm[i] * ng;
+                    float c[2 * JS];
+#pragma unroll
+                    for (int q = 0; q < 2 * JS; q++) c[q] = 0.f;
+                    rows_dot<F::NSEG, F::WPS, F::HAS_MU, 2 * JS>(d, xt, sb, li, c);
+#pragma unroll
+                    for (int j = 0; j < JS; j++) {
+                        ag[j][i] += c[2 * j];
+                        au[j][i] += c[2 * j + 1];
+                    }
+                }
+            }
+        }
+    }
+#pragma unroll
+    for (int j = 0; j < JS; j++) {
+        const int wsj = wave + NW * j;
+        if (wsj * RPW >= 32) break; /* wave-uniform */
+        const int rl = wsj * RPW + rsub;
+#pragma unroll
+        for (int i = 0; i < 8; i++) {
+            if (i < nmem) {
+                const float gg = group_sum<8 * G>(ag[j][i]), uu = group_sum<8 * G>(au[j][i]);
+                if ((lane & (8 * G - 1)) == 0) asv[i][rl] = gg / (1.0f + __expf(-gg)) * uu;
+            }
+        }
+    }
+    __syncthreads();
+    LE_TRACE_POINT(4);
+    /* 5. the unit's SwiGLU values, quantized into each member's down image */
+    if (threadIdx.x < 32) {
+        const int i = threadIdx.x >> 2, gw = threadIdx.x & 3;
+        const bool ok = i < nmem;
+        float4 va = make_float4(0.f, 0.f, 0.f, 0.f), vb = va;
+        if (ok) {
+            va = make_float4(asv[i][8 * gw], asv[i][8 * gw + 1], asv[i][8 * gw + 2], asv[i][8 * gw + 3]);
+            vb = make_float4(asv[i][8 * gw + 4], asv[i][8 * gw + 5], asv[i][8 * gw + 6], asv[i][8 * gw + 7]);
+        }
+        float am = amax8(va, vb);
+        am = fmaxf(am, __shfl_xor(am, 1));
+        am = fmaxf(am, __shfl_xor(am, 2));
+        if (ok) {
+            const int pair = pairm[0] * 0 + (i == 0 ? pairm[0] : i == 1 ? pairm[1] : i == 2 ? pairm[2] : i == 3 ? pairm[3]
+                                              : i == 4 ? pairm[4] : i == 5 ? pairm[5] : i == 6 ? pairm[6] : pairm[7]);
+            uint4 *img = (uint4 *)(a.ws + (size_t)pair * le_xtok_bytes(a.ff));
+            le_quant_group(va, vb, am, img, (float2 *)(img + (a.ff >> 3)), le_xpos<Fmt<TD>::XL>(4 * ux + gw));
+        }
+    }
+    LE_TRACE_POINT(3);
+#if defined(LE_TRACE)
+    le_tr_[5] = __builtin_amdgcn_s_memtime();
+#endif
+    LE_TRACE_FLUSH;
+}
+
+/* Launch 2 fast path: 8 output rows per block, 8 waves take the groups round-robin (one group in
+ * flight per wave, the next one prefetched); ff <= 1024 so a lane's row needs at most 4
+ * super-blocks. */
+template <int TD>
+__device__ void moe_down_fast(const MoeArgs &a) {
+    using F = Fmt<TD>;
+    using D = Dec<F::NSEG, F::WPS>;
+    using Raw = typename F::Raw;
+    constexpr int NW = 8, SM = 4;
+    __shared__ MoeRoute R;
+    __shared__ float red[NW][LE_MOE_FAST_TOK][8];
+    __shared__ __attribute__((aligned(16))) float lv[LE_MOE_FAST_TOK * LE_MOE_MAXEXP];
+    __shared__ float sx[LE_MOE_FAST_TOK * LE_MOE_MAXK];
+    __shared__ u32 tab[F::TABLES ? 256 + 512 : 1];
+    extern __shared__ uint4 smem[];
+    load_tables<TD>(tab);
+    moe_route_par(a, R, lv, sx);
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int K = a.ff, nsb = K >> 8, ng = K >> 3;
+    const int img_bytes = le_xtok_bytes(K);
+    const int npair = a.n_tok * a.k;
+    const bool in_lds = (size_t)npair * img_bytes <= 49152;
+    if (in_lds) {
+        const int n16 = npair * img_bytes / 16;
+        const LE_GLOBAL uint4 *src = (const LE_GLOBAL uint4 *)a.ws;
+        for (int i = threadIdx.x; i < n16; i += blockDim.x) smem[i] = src[i];
+    }
+    for (int i = threadIdx.x; i < NW * LE_MOE_FAST_TOK * 8; i += blockDim.x) (&red[0][0][0])[i] = 0.f;
+    __syncthreads();
+    const u8 *img0 = in_lds ? (const u8 *)smem : a.ws;
+    const size_t rbd = (size_t)nsb * F::SB;
+    const int li = lane & 7, rr = lane >> 3, row = 8 * blockIdx.x + rr;
+    Raw ra[SM], rb2[SM];
+    auto issue = [&](int z, Raw (&r)[SM]) {
+        const u8 *Wd = a.down + (size_t)R.grp_e[z] * a.hidden * rbd + (size_t)row * rbd;
+#pragma unroll
+        for (int s = 0; s < SM; s++) r[s] = F::load(Wd + (size_t)min(s, nsb - 1) * F::SB, li);
+    };
+    auto consume = [&](int z, Raw (&r)[SM]) {
+        const int e = R.grp_e[z];
+        const int nmem = __popcll(R.mask[e]);
+        int tt[8];
+        float ww[8];
+        XTok xt[8];
+#pragma unroll
+        for (int i = 0; i < 8; i++) {
+            int pair = 0;
+            tt[i] = 0;
+            ww[i] = 0.f;
+            if (i < nmem) moe_member(a, R, e, i, tt[i], pair, ww[i]);
+            const uint4 *img = (const uint4 *)(img0 + (size_t)pair * img_bytes);
+            xt[i].xq = img;
+            xt[i].xs = (const float2 *)(img + ng);
+        }
+        float acc[8];
+#pragma unroll
+        for (int i = 0; i < 8; i++) acc[i] = 0.f;
+#pragma unroll
+        for (int s = 0; s < SM; s++) {
+            if (s < nsb) {
+                D d[1];
+                F::decode(r[s], li, s, tab, d[0]);
+#pragma unroll
+                for (int i = 0; i < 8; i++) {
+                    if (i < nmem) {
+                        float c[1] = {0.f};
+                        rows_dot<F::NSEG, F::WPS, F::HAS_MU, 1>(d, xt[i], s, li, c);
+                        acc[i] += c[0];
+                    }
+                }
+            }
+        }
+#pragma unroll
+        for (int i = 0; i < 8; i++) {
+            if (i < nmem) {
+                const float v = group_sum<8>(acc[i]);
+                if (li == 0) red[wave][tt[i]][rr] += ww[i] * v;
+            }
+        }
+    };
+    int z = wave;
+    if (z < R.U) issue(z, ra);
+    while (z < R.U) {
+        if (z + NW < R.U) issue(z + NW, rb2);
+        consume(z, ra);
+        z += NW;
+        if (z >= R.U) break;
+        if (z + NW < R.U) issue(z + NW, ra);
+        consume(z, rb2);
+        z += NW;
+    }
+    __syncthreads();
+    for (int i = threadIdx.x; i < a.n_tok * 8; i += blockDim.x) {
+        const int t = i >> 3, r = i & 7;
+        float acc = 0.f;
+#pragma unroll
+        for (int w = 0; w < NW; w++) acc += red[w][t][r];
+        a.out[(size_t)t * a.hidden + 8 * blockIdx.x + r] = acc;
+    }
+}
+
 #define LE_MOE(TG, TD)                                                                                       \
     extern "C" __global__ void __launch_bounds__(256) le_moe_gu_##TG##_##TD##_g8(MoeArgs a) { moe_gu_body<TG, TD, 8>(a); } \
-    extern "C" __global__ void __launch_bounds__(256) le_moe_gu_##TG##_##TD##_g1(MoeArgs a) { moe_gu_body<TG, TD, 1>(a); }
+    extern "C" __global__ void __launch_bounds__(256) le_moe_gu_##TG##_##TD##_g1(MoeArgs a) { moe_gu_body<TG, TD, 1>(a); } \
+    extern "C" __global__ void __launch_bounds__(1024) le_moe_guf_##TG##_##TD##_g8(MoeArgs a) { moe_gu_fast<TG, TD, 8>(a); } \
+    extern "C" __global__ void __launch_bounds__(1024) le_moe_guf_##TG##_##TD##_g1(MoeArgs a) { moe_gu_fast<TG, TD, 1>(a); }
 #define LE_MOE_DOWN(TD) \
-    extern "C" __global__ void __launch_bounds__(256) le_moe_down_##TD(MoeArgs a) { moe_down_body<TD>(a); }
+    extern "C" __global__ void __launch_bounds__(256) le_moe_down_##TD(MoeArgs a) { moe_down_body<TD>(a); } \
+    extern "C" __global__ void __launch_bounds__(512) le_moe_downf_##TD(MoeArgs a) { moe_down_fast<TD>(a); }
 LE_MOE(12, 14) LE_MOE(12, 12) LE_MOE(14, 14) LE_MOE(8, 8) LE_MOE(16, 18) LE_MOE(16, 16) LE_MOE(18, 18)
 LE_MOE_DOWN(8) LE_MOE_DOWN(12) LE_MOE_DOWN(14) LE_MOE_DOWN(16) LE_MOE_DOWN(18)
 #endif /* LE_PART_MOE */

@@ -134,6 +134,9 @@ class Engine:
     """One le_ctx: the gfx950 code objects loaded on the current device."""
 
     def __init__(self, lib_dir=None):
+        import torch  # torch must bring up its HIP context before this library touches the runtime
+        if torch.cuda.is_available():
+            torch.cuda.init()
         self._L = lib()
         self._ctx = ctypes.c_void_p()
         rc = self._L.le_init(lib_dir.encode() if lib_dir else None, ctypes.byref(self._ctx))
