@@ -190,6 +190,27 @@ def cpu_baseline(ty, host_q, rows, cols, budget_s=2.0):
                 reps, rows, cols, threads, per * 1e3)}
 
 
+def probe(eng, ty, rows, cols, launches=100, copy_bytes=256 << 20):
+    """Workload for rocprofv3 --pmc passes: `launches` eager headline matvecs over rotated weight
+    copies, then 10 copies of a `copy_bytes` buffer (torch's elementwise copy kernel) whose
+    FETCH_SIZE / WRITE_SIZE per dispatch calibrate the counters against known traffic."""
+    import torch
+    import lastengine_amd as le
+    host = quantized(ty, rows, cols, 1)
+    bufs = device_copies(host)
+    x = torch.from_numpy(le.fill_normal(cols, 2)).cuda()
+    y = torch.empty(rows, dtype=torch.float32, device="cuda")
+    for i in range(launches):
+        eng.mv(ty, bufs[i % len(bufs)], x, y, rows, cols)
+    src = torch.ones(copy_bytes // 4, dtype=torch.float32, device="cuda")
+    dst = torch.empty_like(src)
+    for _ in range(10):
+        dst.copy_(src)
+    torch.cuda.synchronize()
+    print(json.dumps({"probe": "done", "matvec_launches": launches, "copy_bytes": copy_bytes,
+                      "weight_bytes": int(host.nbytes)}))
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -197,6 +218,8 @@ def main():
     ap.add_argument("--warmup", type=int, default=200)
     ap.add_argument("--no-secondary", action="store_true")
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--probe", action="store_true",
+                    help="counter-pass workload: eager headline launches plus a 256 MiB copy kernel")
     args = ap.parse_args()
     if args.gpus != 1:
         print("bench.py measures one GPU: this build has no multi-GPU path (each box has one GPU); "
@@ -211,6 +234,9 @@ def main():
     log("device:", props.name, getattr(props, "gcnArchName", ""), "CUs", props.multi_processor_count)
 
     rows, cols = 14336, 4096
+    if args.probe:
+        probe(eng, le.Q4_K, rows, cols)
+        return
     head, host = bench_matvec(eng, le.Q4_K, rows, cols, args.steps, args.warmup)
     log("headline Q4_K %dx%d: %.3f us, %.1f GB/s" % (rows, cols, head["us"], head["gbs"]))
 
