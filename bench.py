@@ -169,7 +169,7 @@ def bench_moe(eng, n_tok, steps, warmup, n_exp=128, k=8, hidden=2048, ff=768, co
     return res
 
 
-def cpu_baseline(ty, host_q, rows, cols, budget_s=2.0):
+def cpu_baseline(ty, host_q, rows, cols, budget_s=10.0):
     """Oracle matvec (C restatement of cpu_ref::matvec) on the host cores, bounded sample."""
     import lastengine_amd as le
     import oracle
