@@ -20,20 +20,24 @@
 /* Optional per-block timestamps for diagnostic builds (-DLE_TRACE): LE_TRACE_DECL at kernel
  * entry, LE_TRACE_POINT(i) keeps s_memrealtime in registers (no store between barriers, which
  * would make the next barrier wait for it), LE_TRACE_FLUSH writes slot i of block b to
- * le_trace_buf[b * 8 + i]. Compiled out otherwise. */
+ * le_trace_buf[b * 16 + i]. Compiled out otherwise. */
 #if defined(LE_TRACE)
 __device__ unsigned long long le_trace_buf[1 << 16];
-#define LE_TRACE_DECL unsigned long long le_tr_[8] = {0, 0, 0, 0, 0, 0, 0, 0}
+#define LE_TRACE_DECL unsigned long long le_tr_[16] = {}
+#define LE_TRACE_PARAM , unsigned long long *le_tr_
+#define LE_TRACE_ARG , le_tr_
 #define LE_TRACE_POINT(i) do { le_tr_[i] = __builtin_amdgcn_s_memrealtime(); } while (0)
 #define LE_TRACE_FLUSH                                                                                     \
     do {                                                                                                   \
-        if (threadIdx.x == 0 && blockIdx.y == 0 && blockIdx.x < (1 << 13))                                 \
-            for (int i_ = 0; i_ < 8; i_++) le_trace_buf[blockIdx.x * 8 + i_] = le_tr_[i_];                 \
+        if (threadIdx.x == 0 && blockIdx.y == 0 && blockIdx.x < (1 << 12))                                 \
+            for (int i_ = 0; i_ < 16; i_++) le_trace_buf[blockIdx.x * 16 + i_] = le_tr_[i_];               \
     } while (0)
 #else
 #define LE_TRACE_DECL do { } while (0)
 #define LE_TRACE_POINT(i) do { } while (0)
 #define LE_TRACE_FLUSH do { } while (0)
+#define LE_TRACE_PARAM
+#define LE_TRACE_ARG
 #endif
 
 __device__ const u32 le_iq2xxs_grid[512] = LE_IQ2XXS_GRID_WORDS;
@@ -849,58 +853,65 @@ __device__ void moe_route(const MoeArgs &a, MoeRoute &R) {
 }
 
 /* Parallel routing for the decode-shaped kernels (n_exp <= 256): one thread per (token, expert).
- * An expert's rank is the number of experts with a larger logit, or an equal logit and a lower
- * index, i.e. its position in the stable descending sort of src/cpu_ref.rs:248; rank < k selects
- * it. With ex = exp(logit - max), the renormalised weight pr/sum(pr over the k) equals
- * ex/sum(ex over the k) (the softmax denominator cancels); the k-sum runs in selection order. */
-__device__ void moe_route_par(const MoeArgs &a, MoeRoute &R, float *lv /* [n_tok][n_exp] LDS */, float *sx /* [n_tok][k] */) {
+ * Each logit becomes a 64-bit key, the float's order-preserving bits above the inverted expert
+ * index, so "larger logit, or equal logit and lower index" is one unsigned compare. An expert's
+ * rank (the number of larger keys) is its position in the stable descending sort of
+ * src/cpu_ref.rs:248; rank < k selects it. With ex = exp(logit - top logit), the renormalised
+ * weight pr/sum(pr over the k) equals ex/sum(ex over the k) (the softmax denominator cancels); the
+ * k-sum runs in selection order. */
+__device__ __forceinline__ unsigned long long moe_key(float v, int e) {
+    u32 b = __float_as_uint(v == 0.f ? 0.f : v); /* -0 ties with +0, as the float compare does */
+    b = (b & 0x80000000u) ? ~b : (b | 0x80000000u);
+    return ((unsigned long long)b << 32) | (u32)(0xFFFFFFFFu - (u32)e);
+}
+
+__device__ __forceinline__ void moe_route_par(const MoeArgs &a, MoeRoute &R, unsigned long long *lv /* [n_tok][n_exp] LDS */,
+                                              float *sx /* [n_tok][k] */ LE_TRACE_PARAM) {
+    /* C lanes share one (token, expert): lane c of the group compares against key pairs
+     * c, c + C, ... (adjacent lanes read adjacent 16 bytes); C shrinks as tokens grow so that one
+     * pass covers as many tokens as the block has threads for. */
     const int tpt = a.n_exp <= 128 ? 128 : 256;
-    const int tpp = blockDim.x / tpt; /* tokens per pass */
+    int C = 8;
+    while (C > 1 && C * tpt * a.n_tok > (int)blockDim.x) C >>= 1;
+    const int tpp = blockDim.x / (tpt * C); /* tokens per pass */
+    /* n_tok <= 64 on every caller, so a token's bit fits the 64-bit expert mask; the first pass's
+     * barrier orders this clear before the atomics below */
+    for (int e = threadIdx.x; e < a.n_exp; e += blockDim.x) R.mask[e] = 0ull;
+    const int c = threadIdx.x % C;
     for (int t0 = 0; t0 < a.n_tok; t0 += tpp) {
-        const int t = t0 + threadIdx.x / tpt, e = threadIdx.x % tpt;
+        const int t = t0 + threadIdx.x / (tpt * C), e = (threadIdx.x / C) % tpt;
         const bool ok = t < a.n_tok && e < a.n_exp;
         const float v = ok ? a.logits[(size_t)t * a.n_exp + e] : 0.f;
-        if (ok) lv[t * a.n_exp + e] = v;
+        const unsigned long long key = moe_key(v, e);
+        if (ok && c == 0) lv[t * a.n_exp + e] = key;
+        LE_TRACE_POINT(8);
         __syncthreads();
+        LE_TRACE_POINT(9);
+        int rank = 0;
         if (ok) {
-            const float4 *row = (const float4 *)(lv + t * a.n_exp);
-            int rank = 0;
-            float m = v;
-            /* a compact loop: this runs once per launch, so code size (instruction fetch) costs
-             * more than loop overhead */
-#pragma unroll 1
-            for (int j4 = 0; j4 < (a.n_exp >> 2); j4++) {
-                const float4 u = row[j4];
-                const int j = 4 * j4;
-                rank += (u.x > v) || (u.x == v && j < e);
-                rank += (u.y > v) || (u.y == v && j + 1 < e);
-                rank += (u.z > v) || (u.z == v && j + 2 < e);
-                rank += (u.w > v) || (u.w == v && j + 3 < e);
-                m = fmaxf(fmaxf(m, fmaxf(u.x, u.y)), fmaxf(u.z, u.w));
-            }
-            if (rank < a.k) {
-                R.topi[t * a.k + rank] = e;
-                sx[t * a.k + rank] = expf(v - m);
+            const ulonglong2 *row = (const ulonglong2 *)(lv + t * a.n_exp);
+#pragma unroll 4
+            for (int j2 = c; j2 < (a.n_exp >> 1); j2 += C) {
+                const ulonglong2 u = row[j2];
+                rank += u.x > key;
+                rank += u.y > key;
             }
         }
+        for (int o = 1; o < C; o <<= 1) rank += __shfl_xor(rank, o); /* groups are lane-aligned */
+        if (ok && c == 0 && rank < a.k) {
+            R.topi[t * a.k + rank] = e;
+            sx[t * a.k + rank] = v;
+            atomicOr(&R.mask[e], 1ull << t);
+        }
+        LE_TRACE_POINT(10);
         __syncthreads();
+        LE_TRACE_POINT(11);
     }
-    for (int i = threadIdx.x; i < a.n_tok * a.k; i += blockDim.x) {
-        const int t = i / a.k;
-        float tot = 0.f;
-        for (int r = 0; r < a.k; r++) tot += sx[t * a.k + r];
-        R.topw[i] = sx[i] / tot;
-    }
-    const int nsel = a.n_tok * a.k;
-    for (int e = threadIdx.x; e < a.n_exp; e += blockDim.x) {
-        unsigned long long msk = 0ull;
-        for (int i = 0; i < nsel; i++)
-            if (R.topi[i] == e) msk |= 1ull << (i / a.k);
-        R.mask[e] = msk;
-    }
-    __syncthreads();
-    const int lane = threadIdx.x & 63;
+    LE_TRACE_POINT(12);
+    LE_TRACE_POINT(13);
+    const int lane = threadIdx.x & 63, nsel = a.n_tok * a.k;
     if (threadIdx.x < 64) {
+        /* wave 0: list the experts with members in ascending order */
         int base = 0;
         for (int c = 0; c < a.n_exp; c += 64) {
             const int e = c + lane;
@@ -910,6 +921,19 @@ __device__ void moe_route_par(const MoeArgs &a, MoeRoute &R, float *lv /* [n_tok
             base += __popcll(bal);
         }
         if (lane == 0) R.U = base;
+    } else {
+        /* the other waves: renormalised weights, summed in selection order */
+        for (int i = threadIdx.x - 64; i < nsel; i += blockDim.x - 64) {
+            const int t = i / a.k;
+            const float top = sx[t * a.k];
+            float tot = 0.f, mine = 0.f;
+            for (int r = 0; r < a.k; r++) {
+                const float ex = expf(sx[t * a.k + r] - top);
+                tot += ex;
+                if (t * a.k + r == i) mine = ex;
+            }
+            R.topw[i] = mine / tot;
+        }
     }
     __syncthreads();
 }
@@ -1105,7 +1129,7 @@ __device__ void moe_gu_fast(const MoeArgs &a) {
     constexpr int NW = 16, RPW = 8 / G, JS = (32 / RPW + NW - 1) / NW, XR = 4;
     __shared__ MoeRoute R;
     __shared__ float asv[8][32];
-    __shared__ __attribute__((aligned(16))) float lv[LE_MOE_FAST_TOK * LE_MOE_MAXEXP];
+    __shared__ __attribute__((aligned(16))) unsigned long long lv[LE_MOE_FAST_TOK * LE_MOE_MAXEXP];
     __shared__ float sx[LE_MOE_FAST_TOK * LE_MOE_MAXK];
     __shared__ u32 tab[F::TABLES ? 256 + 512 : 1];
     extern __shared__ uint4 smem[];
@@ -1127,7 +1151,7 @@ __device__ void moe_gu_fast(const MoeArgs &a) {
         hb[r] = *(const LE_GLOBAL float4 *)(src + 4);
     }
     load_tables<TG>(tab);
-    moe_route_par(a, R, lv, sx);
+    moe_route_par(a, R, lv, sx LE_TRACE_ARG);
     LE_TRACE_POINT(1);
     const int z = blockIdx.y;
     if (z >= R.U) return;
@@ -1270,12 +1294,13 @@ __device__ void moe_down_fast(const MoeArgs &a) {
     constexpr int NW = 8, SM = 4;
     __shared__ MoeRoute R;
     __shared__ float red[NW][LE_MOE_FAST_TOK][8];
-    __shared__ __attribute__((aligned(16))) float lv[LE_MOE_FAST_TOK * LE_MOE_MAXEXP];
+    __shared__ __attribute__((aligned(16))) unsigned long long lv[LE_MOE_FAST_TOK * LE_MOE_MAXEXP];
     __shared__ float sx[LE_MOE_FAST_TOK * LE_MOE_MAXK];
     __shared__ u32 tab[F::TABLES ? 256 + 512 : 1];
     extern __shared__ uint4 smem[];
     load_tables<TD>(tab);
-    moe_route_par(a, R, lv, sx);
+    LE_TRACE_DECL;
+    moe_route_par(a, R, lv, sx LE_TRACE_ARG);
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int K = a.ff, nsb = K >> 8, ng = K >> 3;
     const int img_bytes = le_xtok_bytes(K);
