@@ -22,6 +22,8 @@ DEVICE_FLAGS = ["--offload-arch=gfx950", "-O3", "-std=c++17", "-Xclang", "-targe
 PARTS = {"deq": ["-DLE_PART_DEQ"], "moe": ["-DLE_PART_MOE"]}
 for _ty in (8, 12, 14, 16, 18):
     PARTS["mv%d" % _ty] = ["-DLE_PART_MV=%d" % _ty]
+PARTS["gm"] = []
+SOURCES = {"gm": "le_gemm_kernels.hip"}  # parts not listed here compile le_qmm_kernels.hip
 
 HOST_SOURCES = ["le_qmm.cpp", "le_quant.cpp"]
 
@@ -36,7 +38,7 @@ def _run(cmd):
 
 def code_object_cmd(part):
     return [HIPCC, "--genco"] + DEVICE_FLAGS + PARTS[part] + [
-        os.path.join(CSRC, "le_qmm_kernels.hip"), "-o", os.path.join(LIB, "le_qmm_%s.hsaco" % part)]
+        os.path.join(CSRC, SOURCES.get(part, "le_qmm_kernels.hip")), "-o", os.path.join(LIB, "le_qmm_%s.hsaco" % part)]
 
 
 def host_lib_cmd():

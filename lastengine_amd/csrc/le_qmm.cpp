@@ -21,7 +21,7 @@
 
 namespace {
 
-const char *kParts[] = {"le_qmm_deq", "le_qmm_moe", "le_qmm_mv8", "le_qmm_mv12", "le_qmm_mv14", "le_qmm_mv16", "le_qmm_mv18"};
+const char *kParts[] = {"le_qmm_deq", "le_qmm_moe", "le_qmm_mv8", "le_qmm_mv12", "le_qmm_mv14", "le_qmm_mv16", "le_qmm_mv18", "le_qmm_gm"};
 
 /* Kernel argument block of le_mv_* (mirrors MvArgs in le_qmm_kernels.hip). */
 struct MvArgs {
@@ -67,6 +67,8 @@ struct le_ctx {
     int mq_waves = 4, mq_steps = 2, mq_blocks_per_cu = 2;
     int ms = 1, ms_p = 2;    /* staged MFMA variant and its super-blocks per row and step */
     int moe_fast = 1;        /* decode-shaped MoE kernels */
+    int gm_min_m = 16;       /* le_gemm uses the MFMA kernels from this many tokens on */
+    int gm_tile = 0;         /* MFMA GEMM tile: 0 auto, else 10*TM + TN (TM, TN in 1..2) */
     std::vector<hipModule_t> mods;
     std::map<std::string, hipFunction_t> fns;
     std::string err;
@@ -323,6 +325,12 @@ int le_set_option(le_ctx *c, const char *name, int value) {
         c->mv_blocks_per_cu = value;
     } else if (n == "mq") {
         c->mq = value ? 1 : 0;
+    } else if (n == "gm_tile") {
+        if (value && (value / 10 < 1 || value / 10 > 2 || value % 10 < 1 || value % 10 > 2))
+            return c->fail(LE_ERR_ARG, "gm_tile must be 0, 11, 12, 21 or 22");
+        c->gm_tile = value;
+    } else if (n == "gm_min_m") {
+        c->gm_min_m = value;
     } else if (n == "moe_fast") {
         c->moe_fast = value ? 1 : 0;
     } else if (n == "ms") {
@@ -415,6 +423,33 @@ int le_moe_layer(le_ctx *c, int ty_gate, int ty_up, int ty_down, const void *gat
 int le_gemm(le_ctx *c, int ty, const void *w, const float *x, int m, float *y, int rows, int cols,
             le_stream_t stream) {
     if (!c) return LE_ERR_ARG;
+    if (ty == LE_TYPE_Q4_K && m >= c->gm_min_m && m > 0 && rows > 0 && cols > 0 && cols % 256 == 0 && w && x && y &&
+        al16(x)) {
+        /* MFMA tiles of 32*TM tokens x 128*TN rows; the row tiles are padded to a multiple of 8
+         * so that the token tiles of one row tile share blockIdx % 8 (one XCD) */
+        struct {
+            const void *w;
+            const float *x;
+            float *y;
+            int rows, cols, m;
+        } a{w, x, y, rows, cols, m};
+        void *args[] = {&a};
+        int TM = m > 32 ? 2 : 1, TN = 2;
+        if (c->gm_tile) {
+            TM = c->gm_tile / 10;
+            TN = c->gm_tile % 10;
+        } else if ((long long)((rows + 255) / 256) * ((m + 32 * TM - 1) / (32 * TM)) < c->cus) {
+            TN = 1; /* more, smaller row tiles when the grid would not fill the chip */
+        }
+        const int BM = 32 * TM, BN = 128 * TN;
+        const long long nt = (rows + BN - 1) / BN, mt = (m + BM - 1) / BM;
+        const long long grid = (nt + 7) / 8 * 8 * mt;
+        const size_t lds = (size_t)BN * (152 + 64 + 16 + 8) + (size_t)BM * (2 * 264 * 2 + 32);
+        if (grid > 0x7FFFFFFFLL) return c->fail(LE_ERR_SHAPE, "GEMM grid too large");
+        char name[48];
+        snprintf(name, sizeof name, "le_gm_12_m%d_n%d", TM, TN);
+        return c->launch(name, dim3((unsigned)grid), 256, lds, (hipStream_t)stream, args);
+    }
     return mv_launch(c, ty, nullptr, w, x, 0, cols, y, 0, rows, rows, cols, m, 1, (hipStream_t)stream);
 }
 

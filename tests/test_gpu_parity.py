@@ -152,6 +152,47 @@ def test_gemm_config3(engine, m):
     check_close(y.cpu().numpy(), want, absmag(ty, q, rows, cols, xs))
 
 
+@pytest.mark.parametrize("rows,cols,m", [(256, 256, 16), (300, 512, 17), (1000, 1024, 63), (513, 768, 65),
+                                          (2048, 2048, 130), (96, 4096, 40)])
+def test_gemm_mfma_tiles(engine, rows, cols, m):
+    """Ragged token and row tiles of the MFMA GEMM (64 tokens x 256 rows per block)."""
+    import torch
+    ty = le.Q4_K
+    q, _ = weights(ty, rows, cols, seed=rows + m)
+    xs = np.stack([acts(cols, 3000 + t) for t in range(m)])
+    y = torch.full((m, rows), float("nan"), dtype=torch.float32, device="cuda")
+    engine.gemm(ty, dev(q), dev(xs), m, y, rows, cols)
+    sync()
+    want = oracle.matmat(ty, q, rows, cols, xs)
+    check_close(y.cpu().numpy(), want, absmag(ty, q, rows, cols, xs))
+
+
+def test_gemm_mfma_large_activations(engine):
+    """Activations of magnitude ~1e3 exercise the fp16 high/low split away from unit scale."""
+    import torch
+    ty, rows, cols, m = le.Q4_K, 512, 1024, 32
+    q, _ = weights(ty, rows, cols, seed=17)
+    xs = np.stack([acts(cols, 4000 + t) * np.float32(1000.0) for t in range(m)])
+    y = torch.empty(m, rows, dtype=torch.float32, device="cuda")
+    engine.gemm(ty, dev(q), dev(xs), m, y, rows, cols)
+    sync()
+    want = oracle.matmat(ty, q, rows, cols, xs)
+    check_close(y.cpu().numpy(), want, absmag(ty, q, rows, cols, xs))
+
+
+def test_gemm_config3_m512(engine):
+    """Config 3's largest M on a 2048-row slice of the 14336x4096 weight (rows are independent)."""
+    import torch
+    ty, rows, cols, m = le.Q4_K, 2048, 4096, 512
+    q, _ = weights(ty, rows, cols, seed=3)
+    xs = np.stack([acts(cols, 5000 + t) for t in range(m)])
+    y = torch.empty(m, rows, dtype=torch.float32, device="cuda")
+    engine.gemm(ty, dev(q), dev(xs), m, y, rows, cols)
+    sync()
+    want = oracle.matmat(ty, q, rows, cols, xs)
+    check_close(y.cpu().numpy(), want, absmag(ty, q, rows, cols, xs))
+
+
 # ------------------------------------------------------------------ edge cases and errors
 
 def test_zero_activation_and_zero_weights(engine):
