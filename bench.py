@@ -114,10 +114,11 @@ def bench_gemm(eng, ty, rows, cols, mtok, steps, warmup, seed=3):
     bufs = device_copies(host)
     x = torch.from_numpy(le.fill_normal(mtok * cols, seed + 1)).cuda()
     y = torch.empty(mtok * rows, dtype=torch.float32, device="cuda")
+    ws = torch.empty(max(16, eng.gemm_workspace_size(ty, mtok, cols)), dtype=torch.uint8, device="cuda")
 
     def record():
         for b in bufs:
-            eng.gemm(ty, b, x, mtok, y, rows, cols)
+            eng.gemm(ty, b, x, mtok, y, rows, cols, ws=ws)
     ms = graph_time(record, len(bufs), steps, warmup)
     alg = host.nbytes + 4 * mtok * (cols + rows)
     return {"us": round(ms * 1e3, 2), "GB/s": round(alg / (ms * 1e-3) / 1e9, 1),

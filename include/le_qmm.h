@@ -89,9 +89,14 @@ int le_matvec(le_ctx *ctx, int ty, const void *const *ptrs, const void *w, const
 /* ---- small-M GEMM for speculative verify / prefill (replaces mmq*_<ty> + DenseGpu::bmm,
  *      src/cuda/kernels.cu:965-1223, src/gpu/dense.rs:181-199; CPU twin cpu_ref::matmat,
  *      src/cpu_ref.rs:266-276) ----
- * Y[t * rows + r] = W[r,:] . X[t * cols ...] for t < m. */
-int le_gemm(le_ctx *ctx, int ty, const void *w, const float *x, int m, float *y, int rows, int cols,
-            le_stream_t stream);
+ * Y[t * rows + r] = W[r,:] . X[t * cols ...] for t < m. ws: device workspace of
+ * le_gemm_workspace_size(ty, m, cols) bytes (may be 0 bytes / NULL when that size is 0), the
+ * counterpart of the reference's pre-quantized activation buffers (xqb/xdb/xsb, src/gpu.rs:210).
+ * Q4_K with m >= 16 runs on the matrix cores; activations must lie inside the fp16 range there
+ * (|x| < 65504), as each value is split into two fp16 halves. */
+size_t le_gemm_workspace_size(int ty, int m, int cols);
+int le_gemm(le_ctx *ctx, int ty, const void *w, const float *x, int m, float *y, int rows, int cols, void *ws,
+            size_t ws_bytes, le_stream_t stream);
 
 /* ---- MoE expert layer, routed part (replaces the decode chain router_topk -> host read-back ->
  *      build_ptrs -> matvec gate/up -> swiglu -> quant_x -> matvec down -> moe_combine,

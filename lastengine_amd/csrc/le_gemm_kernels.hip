@@ -93,21 +93,63 @@ __device__ __forceinline__ void gm_q4k_frag(uint2 w, uint4 k, le_v8h &lo, le_v8h
     hi = __builtin_bit_cast(le_v8h, make_uint4(h[0], h[1], h[2], h[3]));
 }
 
-#define GM_WS 152 /* LDS bytes per raw weight row: 144 + 8 (conflict-free 8-byte fragment reads) */
-#define GM_AS 264 /* fp16 per activation row: 256 + 8 */
+#define GM_WS 72  /* LDS bytes per row of a half super-block's quants: 64 + 8 */
+#define GM_AS 136 /* fp16 per activation row of a half super-block: 128 + 8 */
+
+/* Activation pre-pass: X fp32 [M][K] -> workspace planes Xh, Xl fp16 [M][K] (x = xh + xl, order
+ * 0,2,1,3 within each four) and per (token, super-block) a 32-byte record of the eight sub-block
+ * sums S_j as fp16 high halves then low halves. One wave per (token, super-block). */
+extern "C" __global__ void __launch_bounds__(256) le_gm_xprep(GmArgs a, u8 *ws) {
+    const int K = a.cols, nsb = K >> 8;
+    const int wid = blockIdx.x * 4 + (threadIdx.x >> 6); /* the host keeps m * nsb below 2^31 */
+    if (wid >= a.m * nsb) return;
+    const int lane = threadIdx.x & 63;
+    const int t = wid / nsb, sb = wid - t * nsb;
+    const size_t e = (size_t)t * K + 256 * sb + 4 * lane;
+    const float4 v = *(const LE_GLOBAL float4 *)(a.x + e);
+    u32 h0, h1, l0, l1;
+    gm_split2(v.x, v.z, h0, l0);
+    gm_split2(v.y, v.w, h1, l1);
+    _Float16 *Xh = (_Float16 *)ws, *Xl = Xh + (size_t)a.m * K;
+    *(LE_GLOBAL uint2 *)(Xh + e) = make_uint2(h0, h1);
+    *(LE_GLOBAL uint2 *)(Xl + e) = make_uint2(l0, l1);
+    const float sum = group_sum<8>((v.x + v.y) + (v.z + v.w));
+    const int si = __builtin_bit_cast(int, sum);
+    /* the lane reads run on the whole wave, outside the single-lane store below (a reduction
+     * moved under that branch would see inactive lanes) */
+    float sv[8];
+#pragma unroll
+    for (int q = 0; q < 8; q++) sv[q] = __builtin_bit_cast(float, __builtin_amdgcn_readlane(si, 8 * q));
+    __builtin_amdgcn_wave_barrier();
+    if (lane == 0) {
+        u32 hh[4], ll[4];
+#pragma unroll
+        for (int q = 0; q < 4; q++) gm_split2(sv[2 * q], sv[2 * q + 1], hh[q], ll[q]);
+        uint4 *rec = (uint4 *)(ws + (size_t)a.m * K * 4) + 2 * wid;
+        *(LE_GLOBAL uint4 *)rec = make_uint4(hh[0], hh[1], hh[2], hh[3]);
+        *(LE_GLOBAL uint4 *)(rec + 1) = make_uint4(ll[0], ll[1], ll[2], ll[3]);
+    }
+}
 
 template <int TM, int TN>
-__device__ __forceinline__ void gm_q4k_body(const GmArgs &a) {
-    constexpr int BM = 32 * TM, BN = 128 * TN, NWC = BN * 9 / 256 + (BN * 9 % 256 ? 1 : 0), NXC = BM / 4;
+struct GmLds {
+    static constexpr int BM = 32 * TM, BN = 128 * TN;
+    /* one pipeline buffer: the half super-block's quants, fragment constants of its two groups,
+     * offsets m_j, (d, dmin), activation halves */
+    static constexpr int W_OFF = 0, K_OFF = BN * GM_WS, M_OFF = K_OFF + BN * 32, D_OFF = M_OFF + BN * 16,
+                         AH_OFF = D_OFF + BN * 8, AL_OFF = AH_OFF + BM * GM_AS * 2, BUF = AL_OFF + BM * GM_AS * 2;
+    static constexpr int S_OFF = 2 * BUF, BYTES = S_OFF + 2 * BM * 32; /* + sum records [2][BM][32 B] */
+};
+
+template <int TM, int TN>
+__device__ __forceinline__ void gm_q4k_body(const GmArgs &a, const u8 *ws) {
+    using L = GmLds<TM, TN>;
+    constexpr int BM = L::BM, BN = L::BN;
+    constexpr int NQC = BN * 4 / 256, NHC = BN / 256 > 0 ? BN / 256 : 1, NXC = BM * 32 / 256;
     typedef float v16f __attribute__((ext_vector_type(16)));
     extern __shared__ uint4 smem[];
-    u8 *Wr = (u8 *)smem;                          /* [BN][GM_WS] raw super-block bytes */
-    uint4 *Wk = (uint4 *)(Wr + BN * GM_WS);       /* [BN][4] fragment constants per 64-value group */
-    uint4 *Bm = Wk + BN * 4;                      /* [BN] offsets m_0..7 (fp16) */
-    float2 *Dd = (float2 *)(Bm + BN);             /* [BN] (d, dmin) */
-    _Float16 *Ah = (_Float16 *)(Dd + BN);         /* [BM][GM_AS] activation high halves */
-    _Float16 *Al = Ah + BM * GM_AS;               /* [BM][GM_AS] low halves */
-    float *Sf = (float *)(Al + BM * GM_AS);       /* [BM][8] sub-block sums */
+    u8 *lds = (u8 *)smem;
+    uint4 *Sx = (uint4 *)(lds + L::S_OFF);
 
     const int K = a.cols, nsb = K >> 8, M = a.m;
     const int NT = (a.rows + BN - 1) / BN, MT = (M + BM - 1) / BM;
@@ -117,70 +159,75 @@ __device__ __forceinline__ void gm_q4k_body(const GmArgs &a) {
     const int nb = nt * BN, mb = mt * BM;
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const size_t rb = (size_t)nsb * 144;
+    const int nstep = 2 * nsb;
+    const _Float16 *Xh = (const _Float16 *)ws, *Xl = Xh + (size_t)M * K;
+    const uint4 *Xs = (const uint4 *)(ws + (size_t)M * K * 4);
 
-    /* staging: weight chunk c = tid + 256 i is (row c/9, 16-byte column c%9) of the super-block;
-     * activation float4 f = tid + 256 i is (token f/64, column f%64) */
-    uint4 wr[NWC];
-    float4 xr[NXC];
-    auto issue = [&](int sb) {
+    /* staging of step s (super-block s/2, half s&1), all copies of 16 bytes:
+     *   header of row tid (+256 i), decoded by this thread;
+     *   quant chunk c = tid + 256 i: row c/4, 16-byte column c%4 of the half's 64 bytes;
+     *   activation chunk c = tid + 256 i: token c/32, plane (c/16)&1, 8-value column c%16;
+     *   sum record chunk tid < 2*BM: token tid/2, half tid&1 (once per super-block) */
+    uint4 wh[NHC] = {}, wq[NQC] = {}, xa[NXC] = {}, xs = make_uint4(0u, 0u, 0u, 0u);
+    auto issue = [&](int s) {
+        const int sb = s >> 1, h = s & 1;
+        const u8 *w0 = a.w + (size_t)sb * 144;
 #pragma unroll
-        for (int i = 0; i < NWC; i++) {
-            const int c = min(tid + 256 * i, BN * 9 - 1), row = c / 9, col = c - 9 * row;
-            wr[i] = ldg16(a.w + (size_t)min(nb + row, a.rows - 1) * rb + (size_t)sb * 144 + 16 * col);
+        for (int i = 0; i < NHC; i++) wh[i] = ldg16(w0 + (size_t)min(nb + tid + 256 * i, a.rows - 1) * rb);
+#pragma unroll
+        for (int i = 0; i < NQC; i++) {
+            const int c = tid + 256 * i, row = c >> 2;
+            wq[i] = ldg16(w0 + (size_t)min(nb + row, a.rows - 1) * rb + 16 + 64 * h + 16 * (c & 3));
         }
 #pragma unroll
         for (int i = 0; i < NXC; i++) {
-            const int t = (tid >> 6) + 4 * i;
-            xr[i] = *(const LE_GLOBAL float4 *)(a.x + (size_t)min(mb + t, M - 1) * K + 256 * sb + 4 * lane);
+            const int c = tid + 256 * i, t = min(mb + (c >> 5), M - 1);
+            const _Float16 *src = ((c >> 4) & 1 ? Xl : Xh) + (size_t)t * K + 256 * sb + 128 * h + 8 * (c & 15);
+            xa[i] = ldg16c((const u8 *)src);
         }
+        if (h == 0 && tid < 2 * BM) xs = ldg16c((const u8 *)(Xs + 2 * ((size_t)min(mb + (tid >> 1), M - 1) * nsb + sb) + (tid & 1)));
     };
-    auto stage = [&]() {
+    auto stage = [&](int s) {
+        const int sb = s >> 1, h = s & 1;
+        u8 *B = lds + (s & 1) * L::BUF;
 #pragma unroll
-        for (int i = 0; i < NWC; i++) {
-            const int c = tid + 256 * i;
-            if (NWC * 256 > BN * 9 && c >= BN * 9) break;
-            const int row_ = c / 9;
-            uint2 *d = (uint2 *)(Wr + row_ * GM_WS + 16 * (c - 9 * row_));
-            d[0] = make_uint2(wr[i].x, wr[i].y);
-            d[1] = make_uint2(wr[i].z, wr[i].w);
-            if (c % 9 == 0) { /* the row's header: fragment constants, offsets, (d, dmin) */
-                const int row = c / 9;
-                const u32 sy = wr[i].y, sz = wr[i].z, sw = wr[i].w;
-                const u32 sc0 = sy & 0x3F3F3F3Fu, sc1 = (sw & 0x0F0F0F0Fu) | ((sy >> 2) & 0x30303030u);
-                const u32 m0 = sz & 0x3F3F3F3Fu, m1 = ((sw >> 4) & 0x0F0F0F0Fu) | ((sz >> 2) & 0x30303030u);
+        for (int i = 0; i < NHC; i++) {
+            const int row = tid + 256 * i;
+            if (row >= BN) break;
+            const u32 sy = wh[i].y, sz = wh[i].z, sw = wh[i].w;
+            const u32 scw = h ? ((sw & 0x0F0F0F0Fu) | ((sy >> 2) & 0x30303030u)) : (sy & 0x3F3F3F3Fu);
+            uint4 *kc = (uint4 *)(B + L::K_OFF) + 2 * row;
 #pragma unroll
-                for (int g = 0; g < 4; g++) {
-                    const u32 scw = (g < 2 ? sc0 : sc1) >> (16 * (g & 1));
-                    const float sl = (float)(scw & 255u), sh = (float)((scw >> 8) & 255u);
-                    const le_h2 v0 = {(_Float16)sl, (_Float16)sl}, v1 = {(_Float16)(-1024.f * sl), (_Float16)(-1024.f * sl)};
-                    const le_h2 v2 = {(_Float16)(0.0625f * sh), (_Float16)(0.0625f * sh)}, v3 = {(_Float16)(-64.f * sh), (_Float16)(-64.f * sh)};
-                    Wk[row * 4 + g] = make_uint4(as_u32(v0), as_u32(v1), as_u32(v2), as_u32(v3));
-                }
-                u32 mw[4];
-#pragma unroll
-                for (int q = 0; q < 4; q++) {
-                    const u32 mm = (q < 2 ? m0 : m1) >> (16 * (q & 1));
-                    const le_h2 v = {(_Float16)(float)(mm & 255u), (_Float16)(float)((mm >> 8) & 255u)};
-                    mw[q] = as_u32(v);
-                }
-                Bm[row] = make_uint4(mw[0], mw[1], mw[2], mw[3]);
-                Dd[row] = make_float2(h2f(wr[i].x & 0xFFFFu), h2f(wr[i].x >> 16));
+            for (int g = 0; g < 2; g++) {
+                const float sl = (float)((scw >> (16 * g)) & 255u), sh = (float)((scw >> (16 * g + 8)) & 255u);
+                const le_h2 v0 = {(_Float16)sl, (_Float16)sl}, v1 = {(_Float16)(-1024.f * sl), (_Float16)(-1024.f * sl)};
+                const le_h2 v2 = {(_Float16)(0.0625f * sh), (_Float16)(0.0625f * sh)}, v3 = {(_Float16)(-64.f * sh), (_Float16)(-64.f * sh)};
+                kc[g] = make_uint4(as_u32(v0), as_u32(v1), as_u32(v2), as_u32(v3));
             }
+            const u32 m0 = sz & 0x3F3F3F3Fu, m1 = ((sw >> 4) & 0x0F0F0F0Fu) | ((sz >> 2) & 0x30303030u);
+            u32 mw[4];
+#pragma unroll
+            for (int q = 0; q < 4; q++) {
+                const u32 mm = (q < 2 ? m0 : m1) >> (16 * (q & 1));
+                const le_h2 v = {(_Float16)(float)(mm & 255u), (_Float16)(float)((mm >> 8) & 255u)};
+                mw[q] = as_u32(v);
+            }
+            ((uint4 *)(B + L::M_OFF))[row] = make_uint4(mw[0], mw[1], mw[2], mw[3]);
+            ((float2 *)(B + L::D_OFF))[row] = make_float2(h2f(wh[i].x & 0xFFFFu), h2f(wh[i].x >> 16));
+        }
+#pragma unroll
+        for (int i = 0; i < NQC; i++) {
+            const int c = tid + 256 * i;
+            uint2 *d = (uint2 *)(B + L::W_OFF + (c >> 2) * GM_WS + 16 * (c & 3));
+            d[0] = make_uint2(wq[i].x, wq[i].y);
+            d[1] = make_uint2(wq[i].z, wq[i].w);
         }
 #pragma unroll
         for (int i = 0; i < NXC; i++) {
-            const int f = tid + 256 * i, t = f >> 6, c4 = f & 63;
-            float4 v = xr[i];
-            if (mb + t >= M) v = make_float4(0.f, 0.f, 0.f, 0.f);
-            u32 h0, h1, l0, l1;
-            gm_split2(v.x, v.z, h0, l0);
-            gm_split2(v.y, v.w, h1, l1);
-            *(uint2 *)(Ah + t * GM_AS + 4 * c4) = make_uint2(h0, h1);
-            *(uint2 *)(Al + t * GM_AS + 4 * c4) = make_uint2(l0, l1);
-            /* sub-block sum over the 8 lanes holding its 32 values */
-            const float sum = group_sum<8>((v.x + v.y) + (v.z + v.w)); /* DPP, no LDS round trips */
-            if ((c4 & 7) == 0) Sf[t * 8 + (c4 >> 3)] = sum;
+            const int c = tid + 256 * i;
+            *(uint4 *)(B + ((c >> 4) & 1 ? L::AL_OFF : L::AH_OFF) + ((c >> 5) * GM_AS + 8 * (c & 15)) * 2) = xa[i];
         }
+        if (h == 0 && tid < 2 * BM) Sx[((sb & 1) * BM + (tid >> 1)) * 2 + (tid & 1)] = xs;
     };
 
     v16f acc[TM][TN], d1[TM][TN];
@@ -193,94 +240,105 @@ __device__ __forceinline__ void gm_q4k_body(const GmArgs &a) {
     int brow[TN];
 #pragma unroll
     for (int k = 0; k < TN; k++) brow[k] = 32 * (wave * TN + k) + r32;
+
 #if defined(LE_TRACE)
     unsigned long long tr[8] = {};
 #endif
     GM_T(t_start);
     issue(0);
+    stage(0);
+    if (nstep > 1) issue(1);
     for (int sb = 0; sb < nsb; sb++) {
-        GM_T(ta);
-        gm_barrier(); /* the previous super-block's operand reads are done */
-        GM_T(tb);
-        stage();
-        GM_T(tc);
-        if (sb + 1 < nsb) issue(sb + 1);
-        GM_T(td);
-        gm_barrier();
-        GM_T(te);
-        GM_ADD(0, ta, tb);
-        GM_ADD(1, tb, tc);
-        GM_ADD(2, tc, td);
-        GM_ADD(3, td, te);
-#pragma unroll 1
-        for (int g = 0; g < 4; g++) {
-            uint4 kc[TN];
 #pragma unroll
-            for (int k = 0; k < TN; k++) kc[k] = Wk[brow[k] * 4 + g];
+        for (int h = 0; h < 2; h++) {
+            const int s = 2 * sb + h;
+            GM_T(ta);
+            gm_barrier(); /* step s is staged; every wave is done with step s-1's buffer */
+            GM_T(tb);
+            GM_ADD(0, ta, tb);
+            const u8 *B = lds + h * L::BUF; /* s & 1 == h */
+            const _Float16 *Ah = (const _Float16 *)(B + L::AH_OFF), *Al = (const _Float16 *)(B + L::AL_OFF);
 #pragma unroll
-            for (int c = 0; c < 2; c++) {
-                /* K slice: values 64g + 16c + 8hs .. +8 (low nibbles) and 64g + 32 + ... (high) */
-                le_v8h blo[TN], bhi[TN];
+            for (int gl = 0; gl < 2; gl++) {
+                uint4 kc[TN];
 #pragma unroll
-                for (int k = 0; k < TN; k++) {
-                    const uint2 w = *(const uint2 *)(Wr + brow[k] * GM_WS + 16 + 32 * g + 16 * c + 8 * hs);
-                    gm_q4k_frag(w, kc[k], blo[k], bhi[k]);
-                }
+                for (int k = 0; k < TN; k++) kc[k] = ((const uint4 *)(B + L::K_OFF))[2 * brow[k] + gl];
 #pragma unroll
-                for (int half = 0; half < 2; half++) {
-                    const int ko = 64 * g + 32 * half + 16 * c + 8 * hs;
-                    le_v8h ah[TM], al[TM];
+                for (int c = 0; c < 2; c++) {
+                    /* K slice: values 64gl + 16c + 8hs .. +8 (low nibbles) and 32 further (high) */
+                    le_v8h blo[TN], bhi[TN];
 #pragma unroll
-                    for (int i = 0; i < TM; i++) {
-                        ah[i] = __builtin_bit_cast(le_v8h, *(const uint4 *)(Ah + (32 * i + r32) * GM_AS + ko));
-                        al[i] = __builtin_bit_cast(le_v8h, *(const uint4 *)(Al + (32 * i + r32) * GM_AS + ko));
+                    for (int k = 0; k < TN; k++) {
+                        const uint2 w = *(const uint2 *)(B + L::W_OFF + brow[k] * GM_WS + 32 * gl + 16 * c + 8 * hs);
+                        gm_q4k_frag(w, kc[k], blo[k], bhi[k]);
                     }
 #pragma unroll
-                    for (int i = 0; i < TM; i++)
+                    for (int half = 0; half < 2; half++) {
+                        const int ko = 64 * gl + 32 * half + 16 * c + 8 * hs;
+                        le_v8h ah[TM], al[TM];
 #pragma unroll
-                        for (int k = 0; k < TN; k++)
-                            d1[i][k] = __builtin_amdgcn_mfma_f32_32x32x16_f16(ah[i], half ? bhi[k] : blo[k], d1[i][k], 0, 0, 0);
+                        for (int i = 0; i < TM; i++) {
+                            ah[i] = __builtin_bit_cast(le_v8h, *(const uint4 *)(Ah + (32 * i + r32) * GM_AS + ko));
+                            al[i] = __builtin_bit_cast(le_v8h, *(const uint4 *)(Al + (32 * i + r32) * GM_AS + ko));
+                        }
+                        /* the super-block's first MFMA starts from zero: no clearing pass */
+                        const bool first = h == 0 && gl == 0 && c == 0 && half == 0;
 #pragma unroll
-                    for (int i = 0; i < TM; i++)
+                        for (int i = 0; i < TM; i++)
 #pragma unroll
-                        for (int k = 0; k < TN; k++)
-                            d1[i][k] = __builtin_amdgcn_mfma_f32_32x32x16_f16(al[i], half ? bhi[k] : blo[k], d1[i][k], 0, 0, 0);
+                            for (int k = 0; k < TN; k++)
+                                d1[i][k] = __builtin_amdgcn_mfma_f32_32x32x16_f16(ah[i], half ? bhi[k] : blo[k],
+                                                                                  first ? (v16f){} : d1[i][k], 0, 0, 0);
+#pragma unroll
+                        for (int i = 0; i < TM; i++)
+#pragma unroll
+                            for (int k = 0; k < TN; k++)
+                                d1[i][k] = __builtin_amdgcn_mfma_f32_32x32x16_f16(al[i], half ? bhi[k] : blo[k], d1[i][k], 0, 0, 0);
+                    }
                 }
-            }
-        }
-        /* super-block epilogue: Y += d * D1 - dmin * D2 with D2 = sum_j m_j S_j from one more MFMA
-         * (K slice 0 carries the high halves of S_0..7, slice 1 the low halves, both against m) */
-        le_v8h a2[TM];
-#pragma unroll
-        for (int i = 0; i < TM; i++) {
-            const float4 s0 = *(const float4 *)(Sf + (32 * i + r32) * 8), s1 = *(const float4 *)(Sf + (32 * i + r32) * 8 + 4);
-            const float sv[8] = {s0.x, s0.y, s0.z, s0.w, s1.x, s1.y, s1.z, s1.w};
-            u32 pw[4];
-#pragma unroll
-            for (int q = 0; q < 4; q++) {
-                u32 hh, ll;
-                gm_split2(sv[2 * q], sv[2 * q + 1], hh, ll);
-                pw[q] = hs ? ll : hh;
-            }
-            a2[i] = __builtin_bit_cast(le_v8h, make_uint4(pw[0], pw[1], pw[2], pw[3]));
-        }
-#pragma unroll
-        for (int k = 0; k < TN; k++) {
-            const le_v8h b2 = __builtin_bit_cast(le_v8h, Bm[brow[k]]);
-            const float2 dm = Dd[brow[k]];
-#pragma unroll
-            for (int i = 0; i < TM; i++) {
-                const v16f d2 = __builtin_amdgcn_mfma_f32_32x32x16_f16(a2[i], b2, (v16f){}, 0, 0, 0);
-#pragma unroll
-                for (int e = 0; e < 16; e++) {
-                    acc[i][k][e] = __builtin_fmaf(dm.x, d1[i][k][e], acc[i][k][e]);
-                    acc[i][k][e] = __builtin_fmaf(-dm.y, d2[e], acc[i][k][e]);
+#if !defined(GM_DIAG_NOSTAGE)
+                /* the next step's staging and the loads two steps ahead run under this step's MFMAs */
+                if (gl == 0) {
+                    if (s + 1 < nstep) stage(s + 1);
+#if !defined(GM_DIAG_NOISSUE)
+                    if (s + 2 < nstep) issue(s + 2);
+#endif
                 }
-                d1[i][k] = (v16f){};
+#endif
+            }
+            GM_T(tc);
+            GM_ADD(1, tb, tc);
+        }
+        GM_T(td0);
+        /* super-block epilogue: Y += d * D1 - dmin * D2, D2 = sum_j m_j S_j by one more MFMA per
+         * tile (K slice 0: high halves of S_0..7, slice 1: low halves, both against m); all D2
+         * MFMAs are issued before their results are read */
+        {
+            const u8 *B = lds + L::BUF; /* the super-block's second half wrote m and (d, dmin) too */
+            le_v8h a2[TM];
+#pragma unroll
+            for (int i = 0; i < TM; i++) a2[i] = __builtin_bit_cast(le_v8h, Sx[((sb & 1) * BM + 32 * i + r32) * 2 + hs]);
+            v16f d2[TM][TN];
+#pragma unroll
+            for (int k = 0; k < TN; k++) {
+                const le_v8h b2 = __builtin_bit_cast(le_v8h, ((const uint4 *)(B + L::M_OFF))[brow[k]]);
+#pragma unroll
+                for (int i = 0; i < TM; i++) d2[i][k] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a2[i], b2, (v16f){}, 0, 0, 0);
+            }
+#pragma unroll
+            for (int k = 0; k < TN; k++) {
+                const float2 dm = ((const float2 *)(B + L::D_OFF))[brow[k]];
+#pragma unroll
+                for (int i = 0; i < TM; i++)
+#pragma unroll
+                    for (int e = 0; e < 16; e++) {
+                        acc[i][k][e] = __builtin_fmaf(dm.x, d1[i][k][e], acc[i][k][e]);
+                        acc[i][k][e] = __builtin_fmaf(-dm.y, d2[i][k][e], acc[i][k][e]);
+                    }
             }
         }
-        GM_T(tf);
-        GM_ADD(4, te, tf);
+        GM_T(td);
+        GM_ADD(2, td0, td);
     }
 #if defined(LE_TRACE)
     GM_T(t_end);
@@ -303,6 +361,8 @@ __device__ __forceinline__ void gm_q4k_body(const GmArgs &a) {
 }
 
 #define LE_GM(TM, TN)                                                                                      \
-    extern "C" __global__ void __launch_bounds__(256) le_gm_12_m##TM##_n##TN(GmArgs a) { gm_q4k_body<TM, TN>(a); }
+    extern "C" __global__ void __launch_bounds__(256) le_gm_12_m##TM##_n##TN(GmArgs a, const u8 *ws) {    \
+        gm_q4k_body<TM, TN>(a, ws);                                                                        \
+    }
 
 LE_GM(1, 1) LE_GM(1, 2) LE_GM(2, 1) LE_GM(2, 2)

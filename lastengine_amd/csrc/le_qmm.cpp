@@ -420,20 +420,35 @@ int le_moe_layer(le_ctx *c, int ty_gate, int ty_up, int ty_down, const void *gat
     return c->launch(name, dim3((unsigned)(hidden / 8)), fast_dn ? 512 : 256, fast_dn ? 49152 : 0, (hipStream_t)stream, args);
 }
 
-int le_gemm(le_ctx *c, int ty, const void *w, const float *x, int m, float *y, int rows, int cols,
-            le_stream_t stream) {
+size_t le_gemm_workspace_size(int ty, int m, int cols) {
+    if (ty != LE_TYPE_Q4_K || m <= 0 || cols <= 0 || cols % 256) return 0;
+    /* activation halves (2 x fp16 per value) and one 32-byte sum record per (token, super-block) */
+    return (size_t)m * cols * 4 + (size_t)m * (cols / 256) * 32;
+}
+
+int le_gemm(le_ctx *c, int ty, const void *w, const float *x, int m, float *y, int rows, int cols, void *ws,
+            size_t ws_bytes, le_stream_t stream) {
     if (!c) return LE_ERR_ARG;
-    if (ty == LE_TYPE_Q4_K && m >= c->gm_min_m && m > 0 && rows > 0 && cols > 0 && cols % 256 == 0 && w && x && y &&
-        al16(x)) {
-        /* MFMA tiles of 32*TM tokens x 128*TN rows; the row tiles are padded to a multiple of 8
-         * so that the token tiles of one row tile share blockIdx % 8 (one XCD) */
+    if (ty == LE_TYPE_Q4_K && m >= c->gm_min_m && m > 0 && rows > 0 && cols > 0 && cols % 256 == 0 && w && x && y) {
+        if (!ws) return c->fail(LE_ERR_ARG, "null workspace");
+        if (ws_bytes < le_gemm_workspace_size(ty, m, cols))
+            return c->fail(LE_ERR_WORKSPACE, "workspace needs %zu bytes", le_gemm_workspace_size(ty, m, cols));
+        if (!al16(x) || !al16(ws)) return c->fail(LE_ERR_ALIGN, "x and ws must be 16-byte aligned");
         struct {
             const void *w;
             const float *x;
             float *y;
             int rows, cols, m;
         } a{w, x, y, rows, cols, m};
-        void *args[] = {&a};
+        /* pass 1: activation halves and sub-block sums into the workspace, one wave per
+         * (token, super-block) */
+        void *pargs[] = {&a, &ws};
+        const long long waves = (long long)m * (cols / 256);
+        if (waves > 0x7FFFFFFFLL) return c->fail(LE_ERR_SHAPE, "GEMM activation size too large");
+        int rc = c->launch("le_gm_xprep", dim3((unsigned)((waves + 3) / 4)), 256, 0, (hipStream_t)stream, pargs);
+        if (rc) return rc;
+        /* pass 2: MFMA tiles of 32*TM tokens x 128*TN rows; the row tiles are padded to a multiple
+         * of 8 so that the token tiles of one row tile share blockIdx % 8 (one XCD) */
         int TM = m > 32 ? 2 : 1, TN = 2;
         if (c->gm_tile) {
             TM = c->gm_tile / 10;
@@ -444,10 +459,12 @@ int le_gemm(le_ctx *c, int ty, const void *w, const float *x, int m, float *y, i
         const int BM = 32 * TM, BN = 128 * TN;
         const long long nt = (rows + BN - 1) / BN, mt = (m + BM - 1) / BM;
         const long long grid = (nt + 7) / 8 * 8 * mt;
-        const size_t lds = (size_t)BN * (152 + 64 + 16 + 8) + (size_t)BM * (2 * 264 * 2 + 32);
+        /* two pipeline buffers of BN*(72+32+16+8) + BM*2*136*2 bytes, plus [2][BM] 32-byte sum records */
+        const size_t lds = 2 * ((size_t)BN * 128 + (size_t)BM * 544) + (size_t)BM * 64;
         if (grid > 0x7FFFFFFFLL) return c->fail(LE_ERR_SHAPE, "GEMM grid too large");
         char name[48];
         snprintf(name, sizeof name, "le_gm_12_m%d_n%d", TM, TN);
+        void *args[] = {&a, &ws};
         return c->launch(name, dim3((unsigned)grid), 256, lds, (hipStream_t)stream, args);
     }
     return mv_launch(c, ty, nullptr, w, x, 0, cols, y, 0, rows, rows, cols, m, 1, (hipStream_t)stream);

@@ -59,7 +59,8 @@ def lib():
         "le_set_option": (I, [P, ctypes.c_char_p, I]),
         "le_dequant_rows": (I, [P, I, P, P, I, I, P]),
         "le_matvec": (I, [P, I, P, P, P, LL, P, I, I, I, P]),
-        "le_gemm": (I, [P, I, P, P, I, P, I, I, P]),
+        "le_gemm_workspace_size": (S, [I, I, I]),
+        "le_gemm": (I, [P, I, P, P, I, P, I, I, P, S, P]),
         "le_moe_workspace_size": (S, [I, I, I]),
         "le_moe_layer": (I, [P, I, I, I, P, P, P, I, I, I, I, P, P, I, P, P, P, P, S, P]),
         "le_fill_normal": (None, [P, S, ctypes.c_uint64, ctypes.c_uint64, D, D, I]),
@@ -188,6 +189,17 @@ class Engine:
                                          k, hidden, ff, _ptr(logits), _ptr(h), n_tok, _ptr(out), _ptr(idx_out),
                                          _ptr(w_out), _ptr(ws), ws_bytes, _stream(stream)))
 
-    def gemm(self, ty, w, x, m, out, rows, cols, stream=None):
+    def gemm_workspace_size(self, ty, m, cols):
+        return int(self._L.le_gemm_workspace_size(ty, m, cols))
+
+    def gemm(self, ty, w, x, m, out, rows, cols, ws=None, ws_bytes=None, stream=None):
         """DenseGpu::bmm (src/gpu/dense.rs:181): out[t*rows + r] = W[r] . x[t] for t < m."""
-        self._check(self._L.le_gemm(self._ctx, ty, _ptr(w), _ptr(x), m, _ptr(out), rows, cols, _stream(stream)))
+        if ws is None:
+            n = self.gemm_workspace_size(ty, m, cols)
+            if n:
+                import torch
+                ws = torch.empty(n, dtype=torch.uint8, device="cuda")
+        if ws_bytes is None:
+            ws_bytes = ws.numel() if hasattr(ws, "numel") else 0
+        self._check(self._L.le_gemm(self._ctx, ty, _ptr(w), _ptr(x), m, _ptr(out), rows, cols, _ptr(ws), ws_bytes,
+                                    _stream(stream)))

@@ -33,7 +33,7 @@ def test_library_exports_every_declared_symbol():
 
 
 def test_code_objects_built():
-    for part in ("deq", "mv8", "mv12", "mv14", "mv16", "mv18"):
+    for part in ("deq", "moe", "gm", "mv8", "mv12", "mv14", "mv16", "mv18"):
         assert os.path.getsize(os.path.join(qmm.LIB_DIR, "le_qmm_%s.hsaco" % part)) > 1000
 
 
@@ -94,3 +94,13 @@ def test_init_without_gpu_fails_cleanly():
         pytest.skip("GPU present")
     with pytest.raises(le.LeError):
         le.Engine()
+
+
+def test_gemm_workspace_size():
+    L = qmm.lib()
+    # fp16 halves of every activation (4 bytes per value) + one 32-byte sum record per super-block
+    assert L.le_gemm_workspace_size(12, 512, 4096) == 512 * 4096 * 4 + 512 * 16 * 32
+    assert L.le_gemm_workspace_size(12, 1, 256) == 1024 + 32
+    assert L.le_gemm_workspace_size(14, 64, 4096) == 0  # no workspace for the other types
+    assert L.le_gemm_workspace_size(12, 0, 4096) == 0
+    assert L.le_gemm_workspace_size(12, 16, 100) == 0

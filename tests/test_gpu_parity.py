@@ -180,6 +180,21 @@ def test_gemm_mfma_large_activations(engine):
     check_close(y.cpu().numpy(), want, absmag(ty, q, rows, cols, xs))
 
 
+def test_gemm_workspace_errors(engine):
+    import torch
+    ty, rows, cols, m = le.Q4_K, 256, 512, 32
+    q, _ = weights(ty, rows, cols, seed=2)
+    xs = np.stack([acts(cols, 6000 + t) for t in range(m)])
+    y = torch.empty(m, rows, dtype=torch.float32, device="cuda")
+    small = torch.empty(64, dtype=torch.uint8, device="cuda")
+    with pytest.raises(le.LeError) as e:
+        engine.gemm(ty, dev(q), dev(xs), m, y, rows, cols, ws=small)
+    assert e.value.code == -7
+    with pytest.raises(le.LeError) as e:
+        engine.gemm(ty, dev(q), dev(xs), m, y, rows, cols, ws=0, ws_bytes=1 << 20)
+    assert e.value.code == -1
+
+
 def test_gemm_config3_m512(engine):
     """Config 3's largest M on a 2048-row slice of the 14336x4096 weight (rows are independent)."""
     import torch
