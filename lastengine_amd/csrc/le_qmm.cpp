@@ -66,6 +66,7 @@ struct le_ctx {
     int mq = 1;              /* decode matvec on MFMA where available */
     int mq_waves = 4, mq_steps = 2, mq_blocks_per_cu = 2;
     int ms = 1, ms_p = 2;    /* staged MFMA variant and its super-blocks per row and step */
+    int mq6 = 1, ms_p6 = 2;  /* Q6_K decode matvec on the staged MFMA kernels, super-blocks per step */
     int moe_fast = 1;        /* decode-shaped MoE kernels */
     int gm_min_m = 16;       /* le_gemm uses the MFMA kernels from this many tokens on */
     int gm_tile = 0;         /* MFMA GEMM tile: 0 auto, else 10*TM + TN (TM, TN in 1..2) */
@@ -145,8 +146,8 @@ int pick_g(int nsb) {
     return 1;
 }
 
-/* MFMA decode matvec (Q4_K): one block of mq_waves waves per 16-row tile at a time. */
-int mq_launch(le_ctx *c, const void *const *ptrs, const void *w, const float *x, long long x_slot, float *y,
+/* MFMA decode matvec (Q4_K, Q6_K): one block of mq_waves waves per 16-row tile at a time. */
+int mq_launch(le_ctx *c, int ty, const void *const *ptrs, const void *w, const float *x, long long x_slot, float *y,
               long long y_slot, int rows, int cols, int slots, hipStream_t st) {
     const int nsb = cols / 256, NW = c->mq_waves, U = c->mq_steps;
     const long long ntile = (rows + 15) / 16;
@@ -158,7 +159,7 @@ int mq_launch(le_ctx *c, const void *const *ptrs, const void *w, const float *x,
     MvArgs a{};
     a.ptrs = ptrs;
     a.w0 = w;
-    a.w_slot_bytes = (unsigned long long)rows * nsb * 144ull;
+    a.w_slot_bytes = (unsigned long long)rows * nsb * sb_bytes(ty);
     a.x = x;
     a.x_slot = x_slot;
     a.y = y;
@@ -169,17 +170,20 @@ int mq_launch(le_ctx *c, const void *const *ptrs, const void *w, const float *x,
     void *args[] = {&a};
     char name[64];
     size_t lds = (size_t)nsb * 608 + (size_t)NW * 64;
-    int P = c->ms_p, NWs = NW;
+    /* staged variant: P super-blocks per row and item, NWs waves splitting K evenly */
+    int P = ty == LE_TYPE_Q6_K ? c->ms_p6 : c->ms_p, NWs = NW;
     while (P > 1 && nsb % P) P >>= 1;
     while (NWs > 1 && nsb % (NWs * P)) NWs >>= 1;
     if (c->ms && nsb % (NWs * P) == 0) {
-        const int cpr = 9 * P + 1, ni = (16 * cpr + 63) / 64;
-        snprintf(name, sizeof name, "le_ms_12_p%d_w%d", P, NWs);
+        const int cps = ty == LE_TYPE_Q6_K ? 14 : 9;
+        const int cpr = cps * P + 1, ni = (16 * cpr + 63) / 64;
+        snprintf(name, sizeof name, "le_ms_%d_p%d_w%d", ty, P, NWs);
         lds = (size_t)NWs * ((size_t)(nsb / NWs) * 608 + (size_t)ni * 1024) + (size_t)NWs * 128;
         if (lds <= c->lds_limit)
             return c->launch(name, dim3((unsigned)gx, (unsigned)slots), NWs * 64, lds, st, args);
         lds = (size_t)nsb * 608 + (size_t)NW * 64;
     }
+    if (ty != LE_TYPE_Q4_K) return 1; /* no unstaged MFMA variant: the caller falls back */
     snprintf(name, sizeof name, "le_mq_12_w%d_u%d", NW, U);
     return c->launch(name, dim3((unsigned)gx, (unsigned)slots), NW * 64, lds, st, args);
 }
@@ -194,8 +198,11 @@ int mv_launch(le_ctx *c, int ty, const void *const *ptrs, const void *w, const f
     if (!x || !y || (!ptrs && !w)) return c->fail(LE_ERR_ARG, "null pointer");
     if (!al16(x) || (x_slot % 4) || (x_tok % 4)) return c->fail(LE_ERR_ALIGN, "activations must be 16-byte aligned");
     const int nsb = cols / 256, G = pick_g(nsb), S = nsb / G;
-    if (ty == LE_TYPE_Q4_K && ntok == 1 && c->mq && (size_t)nsb * 608 + 1024 <= c->lds_limit)
-        return mq_launch(c, ptrs, w, x, x_slot, y, y_slot, rows, cols, slots, st);
+    if ((ty == LE_TYPE_Q4_K || (ty == LE_TYPE_Q6_K && c->mq6)) && ntok == 1 && c->mq &&
+        (size_t)nsb * 608 + 1024 <= c->lds_limit) {
+        const int rc = mq_launch(c, ty, ptrs, w, x, x_slot, y, y_slot, rows, cols, slots, st);
+        if (rc != 1) return rc;
+    }
     const int xb = xtok_bytes(cols), tb = table_bytes(ty);
     int T = 1;
     const int want = ntok >= 8 ? 8 : ntok >= 4 ? 4 : ntok >= 2 ? 2 : 1;
@@ -325,6 +332,11 @@ int le_set_option(le_ctx *c, const char *name, int value) {
         c->mv_blocks_per_cu = value;
     } else if (n == "mq") {
         c->mq = value ? 1 : 0;
+    } else if (n == "mq6") {
+        c->mq6 = value ? 1 : 0;
+    } else if (n == "ms_p6") {
+        if (value != 1 && value != 2) return c->fail(LE_ERR_ARG, "ms_p6 must be 1 or 2");
+        c->ms_p6 = value;
     } else if (n == "gm_tile") {
         if (value && (value / 10 < 1 || value / 10 > 2 || value % 10 < 1 || value % 10 > 2))
             return c->fail(LE_ERR_ARG, "gm_tile must be 0, 11, 12, 21 or 22");

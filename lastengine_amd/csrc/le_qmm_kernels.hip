@@ -427,6 +427,10 @@ __device__ __forceinline__ void mq_load_seg(const float *__restrict__ x, int e, 
 #pragma unroll
     for (int i = 0; i < 4; i++) v4[i] = xg[4 * e + i];
 }
+/* MAP 0 (Q4_K): slice s of MFMA b is sub-block j(b,s) = 4*(b>>1) + 2*(s>>1) + (b&1), positions
+ * 16*(s&1)..; MAP 1 (Q6_K): MFMA b = (half b>>1, 16-value index b&1), slice s = quarter, so
+ * sub-block j = 4*(b>>1) + s, positions 16*(b&1)... */
+template <int MAP = 0>
 __device__ __forceinline__ void mq_quant_seg(int e, bool store, const float4 (&v4)[4], uint4 *rec, float *dxp, float *fsv) {
     float am = fmaxf(amax8(v4[0], v4[1]), amax8(v4[2], v4[3]));
     am = fmaxf(am, __shfl_xor(am, 1));
@@ -447,7 +451,7 @@ __device__ __forceinline__ void mq_quant_seg(int e, bool store, const float4 (&v
     sum += __shfl_xor(sum, 1);
     if (!store) return;
     const int sb = e >> 4, j = (e & 15) >> 1, c = e & 1;
-    const int b = 2 * (j >> 2) + (j & 1), s = 2 * ((j & 3) >> 1) + c;
+    const int b = MAP ? 2 * (j >> 2) + c : 2 * (j >> 2) + (j & 1), s = MAP ? (j & 3) : 2 * ((j & 3) >> 1) + c;
     const int r = (sb * 16 + b * 4 + s) * 2;
     rec[r] = make_uint4(hw[0], hw[1], hw[2], hw[3]);
     rec[r + 1] = make_uint4(lw[0], lw[1], lw[2], lw[3]);
@@ -701,6 +705,151 @@ __device__ __forceinline__ void ms_q4k_body(const MvArgs &a) {
     LE_TRACE_FLUSH;
 }
 
+/* Q6_K on the staged MFMA design. A super-block (210 B: ql[128], qh[64], sc[16] int8, d f16,
+ * src/quant.rs:96-112) is staged as 14 unaligned 16-byte chunks into a 224-byte LDS slot, so its
+ * fields are 16-byte aligned there. MFMA b = (half n = b>>1, 16-value index is = b&1); slice s of
+ * lane (row, s) is quarter s of the half: values 128n + 32s + 16is + (0..15), with
+ *     q = ((ql[64n + 32(s&1) + 16is + l] >> 4(s>>1)) & 15) | ((qh[32n + 16is + l] >> 2s) & 3) << 4
+ * and the int8 code q - 32 (exact, by a bytewise subtraction that cannot borrow across bytes).
+ * Sub-block j = 4n + s of 32 values has the two scales sc[2j], sc[2j+1] (its 16-value halves), so
+ * the MFMAs of is = 0 and is = 1 accumulate separately and the epilogue adds
+ *     d * sum_j dx_j (sc[2j] D0[j] + sc[2j+1] D1[j]). */
+__device__ __forceinline__ u32 q6_code(u32 ql, u32 qh, int s) {
+    const u32 q = ((ql >> (4 * (s >> 1))) & 0x0F0F0F0Fu) | (((qh >> (2 * s)) & 0x03030303u) << 4);
+    return ((q | 0x80808080u) - 0x20202020u) ^ 0x80808080u; /* q - 32 per byte */
+}
+
+template <int P, int NW>
+__device__ __forceinline__ void ms_q6k_body(const MvArgs &a) {
+    extern __shared__ uint4 smem[];
+    constexpr int CPS = 14, CPR = CPS * P + 1, NCH = 16 * CPR, NI = (NCH + 63) / 64;
+    const int K = a.cols, nsb = K >> 8;
+    const int slot = blockIdx.y;
+    const u8 *W = a.ptrs ? a.ptrs[slot] : a.w0 + (size_t)slot * a.w_slot_bytes;
+    const size_t rb = (size_t)nsb * 210;
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int n = lane & 15, sq = lane >> 4;
+    const int nsbw = nsb / NW;
+    uint4 *rec = smem + wave * (nsbw * 38 + NI * 64);
+    float *dxp = (float *)(rec + nsbw * 32);
+    float *fsv = dxp + nsbw * 16;
+    uint4 *wb = (uint4 *)(fsv + nsbw * 8);
+    float *red = (float *)(smem + NW * (nsbw * 38 + NI * 64)); /* [2][NW][16] */
+    const int ntile = (a.rows + 15) >> 4;
+
+    /* chunk i of this lane: row ri[i] of the tile, global byte gb[i] and LDS chunk index of the
+     * row's P-super-block run (the pad chunk re-reads chunk 0) */
+    int ri[NI], gb[NI];
+#pragma unroll
+    for (int i = 0; i < NI; i++) {
+        const int c = min(64 * i + lane, NCH - 1);
+        const int col = c % CPR, cc = col == CPS * P ? 0 : col;
+        ri[i] = c / CPR;
+        gb[i] = (cc / CPS) * 210 + (cc % CPS) * 16;
+    }
+    uint4 R[NI];
+    auto issue = [&](int tile, int s0) {
+#pragma unroll
+        for (int i = 0; i < NI; i++) {
+            const int row = min(tile * 16 + ri[i], a.rows - 1);
+            R[i] = ldg16u(W + (size_t)row * rb + (size_t)s0 * 210 + gb[i]);
+        }
+    };
+    const int sfirst = wave * P, sstep = NW * P;
+    const bool active = sfirst < nsb;
+    const float *xs = a.x + a.x_slot * slot;
+    const int nsegw = nsbw * 16;
+    auto gseg = [&](int el) {
+        const int ls = el >> 4;
+        return ((ls / P) * sstep + sfirst + ls % P) * 16 + (el & 15);
+    };
+    float4 xv[4];
+    mq_load_seg(xs, gseg(min(lane, nsegw - 1)), xv);
+    issue(min((int)blockIdx.x, ntile - 1), active ? sfirst : 0);
+    mq_quant_seg<1>(lane, lane < nsegw, xv, rec, dxp, fsv);
+    for (int el = lane + 64; el < nsegw; el += 64) {
+        mq_load_seg(xs, gseg(el), xv);
+        mq_quant_seg<1>(el, true, xv, rec, dxp, fsv);
+    }
+
+    const int m = lane & 15, p = m >> 3, jm = m & 7;
+    bool live[4];
+#pragma unroll
+    for (int b = 0; b < 4; b++) live[b] = jm == 4 * (b >> 1) + sq;
+    le_v4i A[4];
+#pragma unroll
+    for (int b = 0; b < 4; b++) A[b] = (le_v4i){0, 0, 0, 0};
+    const int pe = sq >> 1, jb = 4 * (sq & 1);
+
+    int par = 0;
+    for (int tile = blockIdx.x; tile < ntile; tile += gridDim.x) {
+        float y = 0.f;
+        if (active) {
+            for (int s0 = sfirst, lb = 0; s0 < nsb; s0 += sstep, lb += P) {
+                int nt = tile, ns = s0 + sstep;
+                if (ns >= nsb) { ns = sfirst; nt += gridDim.x; }
+#pragma unroll
+                for (int i = 0; i < NI; i++) wb[64 * i + lane] = R[i];
+                if (nt < ntile) issue(nt, ns);
+#pragma unroll
+                for (int q = 0; q < P; q++) {
+                    const int sb = lb + q;
+                    const uint4 *sbp = wb + n * CPR + CPS * q; /* 14 chunks: ql 0-7, qh 8-11, sc 12, d 13 */
+#pragma unroll
+                    for (int b = 0; b < 4; b++)
+                        if (live[b]) {
+                            const uint4 v = rec[(sb * 16 + b * 4 + sq) * 2 + p];
+                            A[b] = (le_v4i){(int)v.x, (int)v.y, (int)v.z, (int)v.w};
+                        }
+                    le_v4i D0 = {0, 0, 0, 0}, D1 = {0, 0, 0, 0};
+#pragma unroll
+                    for (int b = 0; b < 4; b++) {
+                        const int hn = b >> 1, is = b & 1;
+                        const uint4 l = sbp[4 * hn + 2 * (sq & 1) + is], h = sbp[8 + 2 * hn + is];
+                        const le_v4i B = {(int)q6_code(l.x, h.x, sq), (int)q6_code(l.y, h.y, sq), (int)q6_code(l.z, h.z, sq),
+                                          (int)q6_code(l.w, h.w, sq)};
+                        if (is)
+                            D1 = __builtin_amdgcn_mfma_i32_16x16x64_i8(A[b], B, D1, 0, 0, 0);
+                        else
+                            D0 = __builtin_amdgcn_mfma_i32_16x16x64_i8(A[b], B, D0, 0, 0, 0);
+                    }
+                    /* lane: row n, plane pe, sub-blocks jb..jb+3 -> scales sc[2j], sc[2j+1] */
+                    const uint4 scv = sbp[12];
+                    const u32 s0w = (sq & 1) ? scv.z : scv.x, s1w = (sq & 1) ? scv.w : scv.y;
+                    const float4 dq = *(const float4 *)(dxp + sb * 16 + pe * 8 + jb);
+                    const float dqa[4] = {dq.x, dq.y, dq.z, dq.w};
+                    float t = 0.f;
+#pragma unroll
+                    for (int i = 0; i < 4; i++) {
+                        const u32 sw = i < 2 ? s0w : s1w;
+                        const int sa = (int)(signed char)((sw >> (16 * (i & 1))) & 255u);
+                        const int sbb = (int)(signed char)((sw >> (16 * (i & 1) + 8)) & 255u);
+                        t += dqa[i] * ((float)sa * (float)D0[i] + (float)sbb * (float)D1[i]);
+                    }
+                    y += h2f(sbp[13].x & 0xFFFFu) * t;
+                }
+            }
+        }
+        y += __builtin_bit_cast(float, __builtin_amdgcn_ds_swizzle(__builtin_bit_cast(int, y), 0x401F));
+        y += __shfl_xor(y, 32);
+        float *rp = red + par * (NW * 16);
+        if (lane < 16) rp[wave * 16 + lane] = y;
+        __builtin_amdgcn_s_waitcnt(0xC07F);
+        __builtin_amdgcn_s_barrier();
+        if (wave == 0 && lane < 16) {
+            float acc = 0.f;
+#pragma unroll
+            for (int w = 0; w < NW; w++) acc += rp[w * 16 + lane];
+            const int r = tile * 16 + lane;
+            if (r < a.rows) a.y[a.y_slot * slot + r] = acc;
+        }
+        par ^= 1;
+    }
+}
+
+#define LE_MS14(P, NW)                                                                                     \
+    extern "C" __global__ void __launch_bounds__(NW * 64) le_ms_14_p##P##_w##NW(MvArgs a) { ms_q6k_body<P, NW>(a); }
+
 #define LE_MS12(P, NW)                                                                                     \
     extern "C" __global__ void __launch_bounds__(NW * 64) le_ms_12_p##P##_w##NW(MvArgs a) { ms_q4k_body<P, NW>(a); }
 
@@ -714,6 +863,9 @@ LE_MV_ALL(LE_PART_MV)
 #if LE_PART_MV == 12
 LE_MQ12(4, 1) LE_MQ12(4, 2) LE_MQ12(4, 4) LE_MQ12(8, 1) LE_MQ12(8, 2) LE_MQ12(2, 4)
 LE_MS12(1, 1) LE_MS12(1, 2) LE_MS12(1, 4) LE_MS12(1, 8) LE_MS12(2, 1) LE_MS12(2, 2) LE_MS12(2, 4) LE_MS12(2, 8) LE_MS12(4, 1) LE_MS12(4, 2) LE_MS12(4, 4)
+#endif
+#if LE_PART_MV == 14
+LE_MS14(1, 1) LE_MS14(1, 2) LE_MS14(1, 4) LE_MS14(1, 8) LE_MS14(2, 1) LE_MS14(2, 2) LE_MS14(2, 4) LE_MS14(4, 1) LE_MS14(4, 2)
 #endif
 #endif
 
