@@ -68,6 +68,7 @@ struct le_ctx {
     int ms = 1, ms_p = 2;    /* staged MFMA variant and its super-blocks per row and step */
     int mq6 = 1, ms_p6 = 2;  /* Q6_K decode matvec on the staged MFMA kernels, super-blocks per step */
     int moe_fast = 1;        /* decode-shaped MoE kernels */
+    int moe_mfma = 1;        /* decode-shaped MoE on the staged MFMA kernels where the types allow */
     int gm_min_m = 16;       /* le_gemm uses the MFMA kernels from this many tokens on */
     int gm_tile = 0;         /* MFMA GEMM tile: 0 auto, else 10*TM + TN (TM, TN in 1..2) */
     std::vector<hipModule_t> mods;
@@ -343,6 +344,8 @@ int le_set_option(le_ctx *c, const char *name, int value) {
         c->gm_tile = value;
     } else if (n == "gm_min_m") {
         c->gm_min_m = value;
+    } else if (n == "moe_mfma") {
+        c->moe_mfma = value ? 1 : 0;
     } else if (n == "moe_fast") {
         c->moe_fast = value ? 1 : 0;
     } else if (n == "ms") {
@@ -394,7 +397,9 @@ int le_matvec(le_ctx *c, int ty, const void *const *ptrs, const void *w, const f
 
 size_t le_moe_workspace_size(int n_tok, int k, int ff) {
     if (n_tok <= 0 || k <= 0 || ff <= 0) return 0;
-    return (size_t)n_tok * (size_t)k * (size_t)xtok_bytes(ff);
+    /* per (token, slot) the down projection's activation image, then (staged path) a routing record */
+    const size_t img = (size_t)xtok_bytes(ff) > (size_t)(ff / 256) * 608 ? (size_t)xtok_bytes(ff) : (size_t)(ff / 256) * 608;
+    return (size_t)n_tok * (size_t)k * img + 16 + 256 * 4 + 256 * 8 + 1024 * 4 + 1024 * 4;
 }
 
 int le_moe_layer(le_ctx *c, int ty_gate, int ty_up, int ty_down, const void *gate, const void *up, const void *down,
@@ -421,6 +426,21 @@ int le_moe_layer(le_ctx *c, int ty_gate, int ty_up, int ty_down, const void *gat
     const int nsb = hidden / 256, g8 = nsb % 8 == 0;
     const int S = g8 ? nsb / 8 : nsb;
     const int groups = n_tok * k < n_exp ? n_tok * k : n_exp;
+    /* decode-shaped staged-MFMA path: Q4_K gate/up, Q4_K or Q6_K down; gate/up blocks of 8 waves
+     * (hidden 2048) or 4 waves (hidden 1024, 3072), down blocks of 8 waves (ff 256, 512, 768) */
+    const int gw = hidden == 2048 ? 8 : 4, gp = hidden / (256 * gw), dp = ff / 256;
+    if (c->moe_mfma && ty_gate == LE_TYPE_Q4_K && (ty_down == LE_TYPE_Q6_K || ty_down == LE_TYPE_Q4_K) && n_tok <= 8 &&
+        (hidden == 1024 || hidden == 2048 || hidden == 3072) && dp >= 1 && dp <= 3) {
+        const int nig = 9 * gp + 1, cps = ty_down == LE_TYPE_Q6_K ? 14 : 9, nid = (16 * (cps * dp + 1) + 63) / 64;
+        const size_t img_g = (size_t)hidden / 256 * 608, img_d = (size_t)dp * 608;
+        snprintf(name, sizeof name, "le_moe_gum_12_%d_w%d_p%d", ty_down, gw, gp);
+        int rc = c->launch(name, dim3((unsigned)(ff / 32), (unsigned)groups), 64 * gw, 8 * img_g + (size_t)gw * nig * 1024,
+                           (hipStream_t)stream, args);
+        if (rc) return rc;
+        snprintf(name, sizeof name, "le_moe_dnm_%d_w8_p%d", ty_down, dp);
+        return c->launch(name, dim3((unsigned)(hidden / 16)), 512, 16 * img_d + 8 * (size_t)nid * 1024, (hipStream_t)stream,
+                         args);
+    }
     /* decode-shaped fast paths: few tokens, short rows */
     const bool fast_gu = c->moe_fast && n_tok <= 8 && S <= 2 && n_tok * (hidden / 8) <= 4096;
     const bool fast_dn = c->moe_fast && n_tok <= 8 && ff <= 1024;

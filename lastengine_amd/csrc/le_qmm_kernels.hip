@@ -566,6 +566,149 @@ __device__ __forceinline__ void mq_q4k_body(const MvArgs &a) {
     }
 }
 
+/* Per-super-block MFMA step of the staged kernels, shared by the decode matvec and the MoE
+ * kernels. Lane (row n = lane&15, slice sq = lane>>4); A[b] holds the activation image slice of
+ * MFMA b for the lane's A row m = lane&15 (plane m>>3, sub-block m&7) where that row is live, and
+ * zero elsewhere. Returns the lane's share of row n's dot product over the super-block (the four
+ * sq lanes of a row are summed by the caller). */
+struct MsLane {
+    int sq, p, pe, jb;
+    bool live[4];
+};
+template <int MAP>
+__device__ __forceinline__ MsLane ms_lane(int lane) {
+    MsLane L;
+    const int m = lane & 15;
+    L.sq = lane >> 4;
+    L.p = m >> 3;
+    L.pe = L.sq >> 1;
+    L.jb = 4 * (L.sq & 1);
+#pragma unroll
+    for (int b = 0; b < 4; b++) L.live[b] = (m & 7) == (MAP ? 4 * (b >> 1) + L.sq : mq_j(b, L.sq));
+    return L;
+}
+__device__ __forceinline__ void ms_load_a(const uint4 *rec_sb, const MsLane &L, le_v4i (&A)[4]) {
+#pragma unroll
+    for (int b = 0; b < 4; b++)
+        if (L.live[b]) {
+            const uint4 v = rec_sb[(b * 4 + L.sq) * 2 + L.p];
+            A[b] = (le_v4i){(int)v.x, (int)v.y, (int)v.z, (int)v.w};
+        }
+}
+/* Q4_K: sbp = the row's staged super-block (header chunk, then 8 quant chunks). */
+__device__ __forceinline__ float ms_sb_q4k(const uint4 *sbp, const le_v4i (&A)[4], const float *dxp_sb, const float *fsv_sb,
+                                           const MsLane &L) {
+    const int sq = L.sq;
+    const uint4 hd = sbp[0], l0 = sbp[1 + sq], l1 = sbp[5 + sq];
+    const le_v4i B0 = {(int)(l0.x & 0x0F0F0F0Fu), (int)(l0.y & 0x0F0F0F0Fu), (int)(l0.z & 0x0F0F0F0Fu), (int)(l0.w & 0x0F0F0F0Fu)};
+    const le_v4i B1 = {(int)((l0.x >> 4) & 0x0F0F0F0Fu), (int)((l0.y >> 4) & 0x0F0F0F0Fu), (int)((l0.z >> 4) & 0x0F0F0F0Fu),
+                       (int)((l0.w >> 4) & 0x0F0F0F0Fu)};
+    const le_v4i B2 = {(int)(l1.x & 0x0F0F0F0Fu), (int)(l1.y & 0x0F0F0F0Fu), (int)(l1.z & 0x0F0F0F0Fu), (int)(l1.w & 0x0F0F0F0Fu)};
+    const le_v4i B3 = {(int)((l1.x >> 4) & 0x0F0F0F0Fu), (int)((l1.y >> 4) & 0x0F0F0F0Fu), (int)((l1.z >> 4) & 0x0F0F0F0Fu),
+                       (int)((l1.w >> 4) & 0x0F0F0F0Fu)};
+    le_v4i D = __builtin_amdgcn_mfma_i32_16x16x64_i8(A[0], B0, (le_v4i){0, 0, 0, 0}, 0, 0, 0);
+    D = __builtin_amdgcn_mfma_i32_16x16x64_i8(A[1], B1, D, 0, 0, 0);
+    D = __builtin_amdgcn_mfma_i32_16x16x64_i8(A[2], B2, D, 0, 0, 0);
+    D = __builtin_amdgcn_mfma_i32_16x16x64_i8(A[3], B3, D, 0, 0, 0);
+    const u32 sy = hd.y, sz = hd.z, sw = hd.w;
+    const u32 tsc = (sq & 1) ? ((sw & 0x0F0F0F0Fu) | ((sy >> 2) & 0x30303030u)) : (sy & 0x3F3F3F3Fu);
+    const u32 tm = (sq & 1) ? (((sw >> 4) & 0x0F0F0F0Fu) | ((sz >> 2) & 0x30303030u)) : (sz & 0x3F3F3F3Fu);
+    const float4 dq = *(const float4 *)(dxp_sb + L.pe * 8 + L.jb);
+    const float t = (float)(tsc & 255u) * dq.x * (float)D[0] + (float)((tsc >> 8) & 255u) * dq.y * (float)D[1] +
+                    (float)((tsc >> 16) & 255u) * dq.z * (float)D[2] + (float)(tsc >> 24) * dq.w * (float)D[3];
+    const float2 f2 = *(const float2 *)(fsv_sb + L.jb + 2 * L.pe);
+    const u32 mm = tm >> (16 * L.pe);
+    const float mt = (float)(mm & 255u) * f2.x + (float)((mm >> 8) & 255u) * f2.y;
+    return h2f(hd.x & 0xFFFFu) * t - h2f(hd.x >> 16) * mt;
+}
+
+/* Q4_K for NT tiles that share the activation (rows sbp + ti * tstride chunks): the MFMAs of the
+ * tiles are interleaved, so NT accumulation chains are in flight instead of one. */
+template <int NT>
+__device__ __forceinline__ void ms_sb_q4k_n(const uint4 *sbp, int tstride, const le_v4i (&A)[4], const float *dxp_sb,
+                                            const float *fsv_sb, const MsLane &L, float (&y)[NT]) {
+    const int sq = L.sq;
+    uint4 hd[NT], l0[NT], l1[NT];
+#pragma unroll
+    for (int t = 0; t < NT; t++) {
+        const uint4 *p = sbp + t * tstride;
+        hd[t] = p[0];
+        l0[t] = p[1 + sq];
+        l1[t] = p[5 + sq];
+    }
+    le_v4i D[NT];
+#pragma unroll
+    for (int b = 0; b < 4; b++) {
+#pragma unroll
+        for (int t = 0; t < NT; t++) {
+            const uint4 w = b < 2 ? l0[t] : l1[t];
+            const int sh = (b & 1) * 4;
+            const le_v4i B = {(int)((w.x >> sh) & 0x0F0F0F0Fu), (int)((w.y >> sh) & 0x0F0F0F0Fu), (int)((w.z >> sh) & 0x0F0F0F0Fu),
+                              (int)((w.w >> sh) & 0x0F0F0F0Fu)};
+            D[t] = __builtin_amdgcn_mfma_i32_16x16x64_i8(A[b], B, b ? D[t] : (le_v4i){0, 0, 0, 0}, 0, 0, 0);
+        }
+    }
+    const float4 dq = *(const float4 *)(dxp_sb + L.pe * 8 + L.jb);
+    const float2 f2 = *(const float2 *)(fsv_sb + L.jb + 2 * L.pe);
+#pragma unroll
+    for (int t = 0; t < NT; t++) {
+        const u32 sy = hd[t].y, sz = hd[t].z, sw = hd[t].w;
+        const u32 tsc = (sq & 1) ? ((sw & 0x0F0F0F0Fu) | ((sy >> 2) & 0x30303030u)) : (sy & 0x3F3F3F3Fu);
+        const u32 tm = (sq & 1) ? (((sw >> 4) & 0x0F0F0F0Fu) | ((sz >> 2) & 0x30303030u)) : (sz & 0x3F3F3F3Fu);
+        const float tt = (float)(tsc & 255u) * dq.x * (float)D[t][0] + (float)((tsc >> 8) & 255u) * dq.y * (float)D[t][1] +
+                         (float)((tsc >> 16) & 255u) * dq.z * (float)D[t][2] + (float)(tsc >> 24) * dq.w * (float)D[t][3];
+        const u32 mm = tm >> (16 * L.pe);
+        const float mt = (float)(mm & 255u) * f2.x + (float)((mm >> 8) & 255u) * f2.y;
+        y[t] += h2f(hd[t].x & 0xFFFFu) * tt - h2f(hd[t].x >> 16) * mt;
+    }
+}
+
+/* Q6_K on the staged MFMA design. A super-block (210 B: ql[128], qh[64], sc[16] int8, d f16,
+ * src/quant.rs:96-112) is staged as 14 unaligned 16-byte chunks into a 224-byte LDS slot, so its
+ * fields are 16-byte aligned there. MFMA b = (half n = b>>1, 16-value index is = b&1); slice s of
+ * lane (row, s) is quarter s of the half: values 128n + 32s + 16is + (0..15), with
+ *     q = ((ql[64n + 32(s&1) + 16is + l] >> 4(s>>1)) & 15) | ((qh[32n + 16is + l] >> 2s) & 3) << 4
+ * and the int8 code q - 32 (exact, by a bytewise subtraction that cannot borrow across bytes).
+ * Sub-block j = 4n + s of 32 values has the two scales sc[2j], sc[2j+1] (its 16-value halves), so
+ * the MFMAs of is = 0 and is = 1 accumulate separately and the epilogue adds
+ *     d * sum_j dx_j (sc[2j] D0[j] + sc[2j+1] D1[j]). */
+__device__ __forceinline__ u32 q6_code(u32 ql, u32 qh, int s) {
+    const u32 q = ((ql >> (4 * (s >> 1))) & 0x0F0F0F0Fu) | (((qh >> (2 * s)) & 0x03030303u) << 4);
+    return ((q | 0x80808080u) - 0x20202020u) ^ 0x80808080u; /* q - 32 per byte */
+}
+
+/* Q6_K: sbp = the row's staged super-block (14 chunks: ql 0-7, qh 8-11, sc 12, d 13). A[b] is the
+ * image slice under the Q6_K map (MAP 1). */
+__device__ __forceinline__ float ms_sb_q6k(const uint4 *sbp, const le_v4i (&A)[4], const float *dxp_sb, const MsLane &L) {
+    const int sq = L.sq;
+    le_v4i D0 = {0, 0, 0, 0}, D1 = {0, 0, 0, 0};
+#pragma unroll
+    for (int b = 0; b < 4; b++) {
+        const int hn = b >> 1, is = b & 1;
+        const uint4 l = sbp[4 * hn + 2 * (sq & 1) + is], h = sbp[8 + 2 * hn + is];
+        const le_v4i B = {(int)q6_code(l.x, h.x, sq), (int)q6_code(l.y, h.y, sq), (int)q6_code(l.z, h.z, sq),
+                          (int)q6_code(l.w, h.w, sq)};
+        if (is)
+            D1 = __builtin_amdgcn_mfma_i32_16x16x64_i8(A[b], B, D1, 0, 0, 0);
+        else
+            D0 = __builtin_amdgcn_mfma_i32_16x16x64_i8(A[b], B, D0, 0, 0, 0);
+    }
+    /* lane: row n, plane pe, sub-blocks jb..jb+3 -> scales sc[2j], sc[2j+1] */
+    const uint4 scv = sbp[12];
+    const u32 s0w = (sq & 1) ? scv.z : scv.x, s1w = (sq & 1) ? scv.w : scv.y;
+    const float4 dq = *(const float4 *)(dxp_sb + L.pe * 8 + L.jb);
+    const float dqa[4] = {dq.x, dq.y, dq.z, dq.w};
+    float t = 0.f;
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+        const u32 sw = i < 2 ? s0w : s1w;
+        const int sa = (int)(signed char)((sw >> (16 * (i & 1))) & 255u);
+        const int sbb = (int)(signed char)((sw >> (16 * (i & 1) + 8)) & 255u);
+        t += dqa[i] * ((float)sa * (float)D0[i] + (float)sbb * (float)D1[i]);
+    }
+    return h2f(sbp[13].x & 0xFFFFu) * t;
+}
+
 /* Staged variant: each wave streams its tile's P super-blocks per row as consecutive 16-byte
  * chunks (consecutive lanes take consecutive chunks of a row, so every load instruction reads
  * long contiguous runs), prefetched into registers one item ahead and written to a wave-private
@@ -633,14 +776,10 @@ __device__ __forceinline__ void ms_q4k_body(const MvArgs &a) {
     }
     LE_TRACE_POINT(1);
 
-    const int m = lane & 15, p = m >> 3, jm = m & 7;
-    bool live[4];
-#pragma unroll
-    for (int b = 0; b < 4; b++) live[b] = jm == mq_j(b, sq);
+    const MsLane L = ms_lane<0>(lane);
     le_v4i A[4];
 #pragma unroll
     for (int b = 0; b < 4; b++) A[b] = (le_v4i){0, 0, 0, 0};
-    const int pe = sq >> 1, jb = 4 * (sq & 1);
 
     int par = 0;
     for (int tile = blockIdx.x; tile < ntile; tile += gridDim.x) {
@@ -655,34 +794,8 @@ __device__ __forceinline__ void ms_q4k_body(const MvArgs &a) {
 #pragma unroll
                 for (int q = 0; q < P; q++) {
                     const int sb = lb + q; /* local super-block of this wave's image */
-                    const uint4 *rowp = wb + n * CPR + 9 * q;
-                    const uint4 hd = rowp[0], l0 = rowp[1 + sq], l1 = rowp[5 + sq];
-#pragma unroll
-                    for (int b = 0; b < 4; b++)
-                        if (live[b]) {
-                            const uint4 v = rec[(sb * 16 + b * 4 + sq) * 2 + p];
-                            A[b] = (le_v4i){(int)v.x, (int)v.y, (int)v.z, (int)v.w};
-                        }
-                    const le_v4i B0 = {(int)(l0.x & 0x0F0F0F0Fu), (int)(l0.y & 0x0F0F0F0Fu), (int)(l0.z & 0x0F0F0F0Fu), (int)(l0.w & 0x0F0F0F0Fu)};
-                    const le_v4i B1 = {(int)((l0.x >> 4) & 0x0F0F0F0Fu), (int)((l0.y >> 4) & 0x0F0F0F0Fu),
-                                       (int)((l0.z >> 4) & 0x0F0F0F0Fu), (int)((l0.w >> 4) & 0x0F0F0F0Fu)};
-                    const le_v4i B2 = {(int)(l1.x & 0x0F0F0F0Fu), (int)(l1.y & 0x0F0F0F0Fu), (int)(l1.z & 0x0F0F0F0Fu), (int)(l1.w & 0x0F0F0F0Fu)};
-                    const le_v4i B3 = {(int)((l1.x >> 4) & 0x0F0F0F0Fu), (int)((l1.y >> 4) & 0x0F0F0F0Fu),
-                                       (int)((l1.z >> 4) & 0x0F0F0F0Fu), (int)((l1.w >> 4) & 0x0F0F0F0Fu)};
-                    le_v4i D = __builtin_amdgcn_mfma_i32_16x16x64_i8(A[0], B0, (le_v4i){0, 0, 0, 0}, 0, 0, 0);
-                    D = __builtin_amdgcn_mfma_i32_16x16x64_i8(A[1], B1, D, 0, 0, 0);
-                    D = __builtin_amdgcn_mfma_i32_16x16x64_i8(A[2], B2, D, 0, 0, 0);
-                    D = __builtin_amdgcn_mfma_i32_16x16x64_i8(A[3], B3, D, 0, 0, 0);
-                    const u32 sy = hd.y, sz = hd.z, sw = hd.w;
-                    const u32 tsc = (sq & 1) ? ((sw & 0x0F0F0F0Fu) | ((sy >> 2) & 0x30303030u)) : (sy & 0x3F3F3F3Fu);
-                    const u32 tm = (sq & 1) ? (((sw >> 4) & 0x0F0F0F0Fu) | ((sz >> 2) & 0x30303030u)) : (sz & 0x3F3F3F3Fu);
-                    const float4 dq = *(const float4 *)(dxp + sb * 16 + pe * 8 + jb);
-                    const float t = (float)(tsc & 255u) * dq.x * (float)D[0] + (float)((tsc >> 8) & 255u) * dq.y * (float)D[1] +
-                                    (float)((tsc >> 16) & 255u) * dq.z * (float)D[2] + (float)(tsc >> 24) * dq.w * (float)D[3];
-                    const float2 f2 = *(const float2 *)(fsv + sb * 8 + jb + 2 * pe);
-                    const u32 mm = tm >> (16 * pe);
-                    const float mt = (float)(mm & 255u) * f2.x + (float)((mm >> 8) & 255u) * f2.y;
-                    y += h2f(hd.x & 0xFFFFu) * t - h2f(hd.x >> 16) * mt;
+                    ms_load_a(rec + sb * 32, L, A);
+                    y += ms_sb_q4k(wb + n * CPR + 9 * q, A, dxp + sb * 16, fsv + sb * 8, L);
                 }
             }
         }
@@ -703,20 +816,6 @@ __device__ __forceinline__ void ms_q4k_body(const MvArgs &a) {
     }
     LE_TRACE_POINT(2);
     LE_TRACE_FLUSH;
-}
-
-/* Q6_K on the staged MFMA design. A super-block (210 B: ql[128], qh[64], sc[16] int8, d f16,
- * src/quant.rs:96-112) is staged as 14 unaligned 16-byte chunks into a 224-byte LDS slot, so its
- * fields are 16-byte aligned there. MFMA b = (half n = b>>1, 16-value index is = b&1); slice s of
- * lane (row, s) is quarter s of the half: values 128n + 32s + 16is + (0..15), with
- *     q = ((ql[64n + 32(s&1) + 16is + l] >> 4(s>>1)) & 15) | ((qh[32n + 16is + l] >> 2s) & 3) << 4
- * and the int8 code q - 32 (exact, by a bytewise subtraction that cannot borrow across bytes).
- * Sub-block j = 4n + s of 32 values has the two scales sc[2j], sc[2j+1] (its 16-value halves), so
- * the MFMAs of is = 0 and is = 1 accumulate separately and the epilogue adds
- *     d * sum_j dx_j (sc[2j] D0[j] + sc[2j+1] D1[j]). */
-__device__ __forceinline__ u32 q6_code(u32 ql, u32 qh, int s) {
-    const u32 q = ((ql >> (4 * (s >> 1))) & 0x0F0F0F0Fu) | (((qh >> (2 * s)) & 0x03030303u) << 4);
-    return ((q | 0x80808080u) - 0x20202020u) ^ 0x80808080u; /* q - 32 per byte */
 }
 
 template <int P, int NW>
@@ -772,14 +871,10 @@ __device__ __forceinline__ void ms_q6k_body(const MvArgs &a) {
         mq_quant_seg<1>(el, true, xv, rec, dxp, fsv);
     }
 
-    const int m = lane & 15, p = m >> 3, jm = m & 7;
-    bool live[4];
-#pragma unroll
-    for (int b = 0; b < 4; b++) live[b] = jm == 4 * (b >> 1) + sq;
+    const MsLane L = ms_lane<1>(lane);
     le_v4i A[4];
 #pragma unroll
     for (int b = 0; b < 4; b++) A[b] = (le_v4i){0, 0, 0, 0};
-    const int pe = sq >> 1, jb = 4 * (sq & 1);
 
     int par = 0;
     for (int tile = blockIdx.x; tile < ntile; tile += gridDim.x) {
@@ -794,39 +889,8 @@ __device__ __forceinline__ void ms_q6k_body(const MvArgs &a) {
 #pragma unroll
                 for (int q = 0; q < P; q++) {
                     const int sb = lb + q;
-                    const uint4 *sbp = wb + n * CPR + CPS * q; /* 14 chunks: ql 0-7, qh 8-11, sc 12, d 13 */
-#pragma unroll
-                    for (int b = 0; b < 4; b++)
-                        if (live[b]) {
-                            const uint4 v = rec[(sb * 16 + b * 4 + sq) * 2 + p];
-                            A[b] = (le_v4i){(int)v.x, (int)v.y, (int)v.z, (int)v.w};
-                        }
-                    le_v4i D0 = {0, 0, 0, 0}, D1 = {0, 0, 0, 0};
-#pragma unroll
-                    for (int b = 0; b < 4; b++) {
-                        const int hn = b >> 1, is = b & 1;
-                        const uint4 l = sbp[4 * hn + 2 * (sq & 1) + is], h = sbp[8 + 2 * hn + is];
-                        const le_v4i B = {(int)q6_code(l.x, h.x, sq), (int)q6_code(l.y, h.y, sq), (int)q6_code(l.z, h.z, sq),
-                                          (int)q6_code(l.w, h.w, sq)};
-                        if (is)
-                            D1 = __builtin_amdgcn_mfma_i32_16x16x64_i8(A[b], B, D1, 0, 0, 0);
-                        else
-                            D0 = __builtin_amdgcn_mfma_i32_16x16x64_i8(A[b], B, D0, 0, 0, 0);
-                    }
-                    /* lane: row n, plane pe, sub-blocks jb..jb+3 -> scales sc[2j], sc[2j+1] */
-                    const uint4 scv = sbp[12];
-                    const u32 s0w = (sq & 1) ? scv.z : scv.x, s1w = (sq & 1) ? scv.w : scv.y;
-                    const float4 dq = *(const float4 *)(dxp + sb * 16 + pe * 8 + jb);
-                    const float dqa[4] = {dq.x, dq.y, dq.z, dq.w};
-                    float t = 0.f;
-#pragma unroll
-                    for (int i = 0; i < 4; i++) {
-                        const u32 sw = i < 2 ? s0w : s1w;
-                        const int sa = (int)(signed char)((sw >> (16 * (i & 1))) & 255u);
-                        const int sbb = (int)(signed char)((sw >> (16 * (i & 1) + 8)) & 255u);
-                        t += dqa[i] * ((float)sa * (float)D0[i] + (float)sbb * (float)D1[i]);
-                    }
-                    y += h2f(sbp[13].x & 0xFFFFu) * t;
+                    ms_load_a(rec + sb * 32, L, A);
+                    y += ms_sb_q6k(wb + n * CPR + CPS * q, A, dxp + sb * 16, L);
                 }
             }
         }
@@ -1042,11 +1106,15 @@ __device__ __forceinline__ void moe_route_par(const MoeArgs &a, MoeRoute &R, uns
         int rank = 0;
         if (ok) {
             const ulonglong2 *row = (const ulonglong2 *)(lv + t * a.n_exp);
-#pragma unroll 4
-            for (int j2 = c; j2 < (a.n_exp >> 1); j2 += C) {
-                const ulonglong2 u = row[j2];
-                rank += u.x > key;
-                rank += u.y > key;
+            const int npair = a.n_exp >> 1;
+            /* eight reads issued before any compare, so LDS latency is paid once per batch */
+            for (int j0 = c; j0 < npair; j0 += 8 * C) {
+                ulonglong2 u[8];
+#pragma unroll
+                for (int q = 0; q < 8; q++) u[q] = row[min(j0 + q * C, npair - 1)];
+#pragma unroll
+                for (int q = 0; q < 8; q++)
+                    if (j0 + q * C < npair) rank += (int)(u[q].x > key) + (int)(u[q].y > key);
             }
         }
         for (int o = 1; o < C; o <<= 1) rank += __shfl_xor(rank, o); /* groups are lane-aligned */
@@ -1099,6 +1167,51 @@ __device__ __forceinline__ void moe_member(const MoeArgs &a, const MoeRoute &R, 
     while (R.topi[t * a.k + s] != e) s++;
     pair = t * a.k + s;
     w = R.topw[pair];
+}
+
+/* Routing record in the workspace, after the pair images (offset from the host): written by the
+ * gate/up launch, read by the down launch instead of routing again.
+ *   int U, 3 x pad; int grp_e[256]; u64 group mask[256]; int topi[1024]; float topw[1024] */
+#define LE_MOE_REC_BYTES (16 + 256 * 4 + 256 * 8 + 1024 * 4 + 1024 * 4)
+__device__ __forceinline__ void moe_rec_write(const MoeArgs &a, const MoeRoute &R, u8 *rec) {
+    const int nsel = a.n_tok * a.k;
+    int *ri = (int *)rec;
+    unsigned long long *rm = (unsigned long long *)(rec + 16 + 256 * 4);
+    int *rt = (int *)(rec + 16 + 256 * 12);
+    float *rw = (float *)(rec + 16 + 256 * 12 + 1024 * 4);
+    if (threadIdx.x == 0) ri[0] = R.U;
+    for (int z = threadIdx.x; z < R.U; z += blockDim.x) {
+        ri[4 + z] = R.grp_e[z];
+        rm[z] = R.mask[R.grp_e[z]];
+    }
+    for (int i = threadIdx.x; i < nsel; i += blockDim.x) {
+        rt[i] = R.topi[i];
+        rw[i] = R.topw[i];
+    }
+}
+__device__ __forceinline__ void moe_rec_read(const MoeArgs &a, MoeRoute &R, const u8 *rec) {
+    const int nsel = a.n_tok * a.k;
+    const int *ri = (const int *)rec;
+    const unsigned long long *rm = (const unsigned long long *)(rec + 16 + 256 * 4);
+    const int *rt = (const int *)(rec + 16 + 256 * 12);
+    const float *rw = (const float *)(rec + 16 + 256 * 12 + 1024 * 4);
+    const int U = *(const LE_GLOBAL int *)ri;
+    /* every thread issues its loads before any store */
+    const int z = threadIdx.x;
+    const int ge = z < U ? *(const LE_GLOBAL int *)(ri + 4 + z) : 0;
+    const unsigned long long gm = z < U ? *(const LE_GLOBAL unsigned long long *)(rm + z) : 0ull;
+    const int ti = z < nsel ? *(const LE_GLOBAL int *)(rt + z) : 0;
+    const float tw = z < nsel ? *(const LE_GLOBAL float *)(rw + z) : 0.f;
+    if (z == 0) R.U = U;
+    if (z < U) {
+        R.grp_e[z] = ge;
+        R.mask[ge] = gm;
+    }
+    if (z < nsel) {
+        R.topi[z] = ti;
+        R.topw[z] = tw;
+    }
+    __syncthreads();
 }
 
 /* Launch 1: gate/up rows of unit blockIdx.x (32 rows) of group blockIdx.y for up to 8 members at
@@ -1536,6 +1649,281 @@ __device__ void moe_down_fast(const MoeArgs &a) {
         a.out[(size_t)t * a.hidden + 8 * blockIdx.x + r] = acc;
     }
 }
+
+/* ===================== MoE on the staged MFMA kernels (decode-shaped: n_tok <= 8) =====================
+ * Launch 1 (le_moe_gum_12_<td>_p<P>): grid (ff/32, groups), four waves. Each block routes, builds the
+ * MFMA activation image of every token's h in LDS (one shared copy), and streams its expert's
+ * 32-row unit of gate and of up as four 16-row tiles; wave w owns super-blocks wP..wP+P-1 of each
+ * row (hidden = 1024 P). The SwiGLU values of the unit are one 32-value sub-block of the down
+ * projection's input, quantized straight into each member's down image in the workspace (the
+ * image format of the staged kernels, under the down type's slice map).
+ * Launch 2 (le_moe_dnm_<td>_p<P>): grid (hidden/16), four waves taking the expert groups
+ * round-robin; per group the 16 rows x P super-blocks (ff = 256 P) are staged like the matvec, the
+ * members' images are copied into the wave's LDS, and each member's dot is weighted and added to
+ * its token's rows. The waves' sums are added in a fixed order. */
+#define LE_MOE_IMG(K) ((K) / 256 * 608) /* bytes of one token's MFMA activation image */
+
+/* LDS layout of the staged MoE kernels: the routing keys (needed only until routing is done)
+ * share their bytes with the weight staging that follows. */
+#define LE_MOE_LV_BYTES (LE_MOE_FAST_TOK * LE_MOE_MAXEXP * 8)
+
+template <int TD, int NW, int P>
+__device__ __forceinline__ void moe_gum_body(const MoeArgs &a) {
+    constexpr int CPR = 9 * P + 1, NCH = 4 * 16 * CPR, NI = (NCH + 63) / 64, MAPD = TD == LE_TYPE_Q6_K ? 1 : 0;
+    constexpr int K = 256 * NW * P, NSB = NW * P, SEGT = K / 16, NT = 64 * NW; /* segments of 16 values per token */
+    constexpr int XR = (LE_MOE_FAST_TOK * SEGT + NT - 1) / NT;
+    __shared__ MoeRoute R;
+    __shared__ float sx[LE_MOE_FAST_TOK * LE_MOE_MAXK];
+    __shared__ float red[NW][LE_MOE_FAST_TOK][64];
+    __shared__ __attribute__((aligned(16))) float act[LE_MOE_FAST_TOK][32];
+    __shared__ int mtok[LE_MOE_FAST_TOK], mpair[LE_MOE_FAST_TOK];
+    extern __shared__ uint4 smem[];
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, n = lane & 15;
+    uint4 *img = smem;                                          /* [n_tok][image] */
+    uint4 *stg = smem + LE_MOE_FAST_TOK * LE_MOE_IMG(K) / 16;  /* [NW][NI*64] staging; routing keys first */
+    uint4 *wb = stg + wave * NI * 64;
+    LE_TRACE_DECL;
+    LE_TRACE_POINT(0);
+    /* 1. every token's activations, 16 values per (thread, r), clamped and unpredicated */
+    const int nseg = a.n_tok * SEGT;
+    float4 hv[XR][4];
+#pragma unroll
+    for (int r = 0; r < XR; r++) {
+        const int e = min((int)threadIdx.x + NT * r, nseg - 1);
+        mq_load_seg(a.h + (size_t)(e / SEGT) * K, e % SEGT, hv[r]);
+    }
+    moe_route_par(a, R, (unsigned long long *)stg, sx LE_TRACE_ARG);
+    LE_TRACE_POINT(1);
+    const int z = blockIdx.y;
+    if (z >= R.U) return; /* uniform over the block */
+    const int e = R.grp_e[z];
+    const int nmem = __popcll(R.mask[e]);
+    if (blockIdx.x == 0 && z == 0) {
+        for (int i = threadIdx.x; i < a.n_tok * a.k; i += blockDim.x) {
+            if (a.idx_out) a.idx_out[i] = R.topi[i];
+            if (a.w_out) a.w_out[i] = R.topw[i];
+        }
+        moe_rec_write(a, R, a.ws + (size_t)a.n_tok * a.k * LE_MOE_IMG(a.ff));
+    }
+    /* 2. the four tiles of this wave's super-blocks (gate rows 32ux.., +16, up rows 32ux.., +16),
+     * packed: chunk c = (tile, row, column) of 4 x 16 x CPR, all in flight at once */
+    const size_t rb = (size_t)NSB * 144;
+    const u8 *Wg = a.gate + (size_t)e * a.ff * rb, *Wu = a.up + (size_t)e * a.ff * rb;
+    const int ux = blockIdx.x;
+    uint4 Rg[NI];
+#pragma unroll
+    for (int i = 0; i < NI; i++) {
+        const int c = min(64 * i + lane, NCH - 1), ti = c / (16 * CPR), rem = c % (16 * CPR), col = rem % CPR;
+        Rg[i] = ldg16((ti < 2 ? Wg : Wu) + (size_t)(32 * ux + 16 * (ti & 1) + rem / CPR) * rb + (size_t)wave * P * 144 +
+                      (col == 9 * P ? 0 : col) * 16);
+    }
+    /* 3. token images (the Q4_K slice map) and the group's members */
+#pragma unroll
+    for (int r = 0; r < XR; r++) {
+        const int eg = (int)threadIdx.x + NT * r;
+        if (r * NT >= nseg) break;
+        const int t = min(eg, nseg - 1) / SEGT, el = min(eg, nseg - 1) % SEGT;
+        uint4 *rec = img + t * (LE_MOE_IMG(K) / 16);
+        float *dxp = (float *)(rec + NSB * 32), *fsv = dxp + NSB * 16;
+        mq_quant_seg<0>(el, eg < nseg, hv[r], rec, dxp, fsv);
+    }
+    if (threadIdx.x < nmem) {
+        int t, pair;
+        float w;
+        moe_member(a, R, e, threadIdx.x, t, pair, w);
+        mtok[threadIdx.x] = t;
+        mpair[threadIdx.x] = pair;
+    }
+#pragma unroll
+    for (int i = 0; i < NI; i++) wb[64 * i + lane] = Rg[i];
+    __syncthreads();
+    LE_TRACE_POINT(2);
+    /* 4. per member (a runtime loop: the code stays small), four tiles x this wave's super-blocks */
+    const MsLane L = ms_lane<0>(lane);
+    le_v4i A[4];
+#pragma unroll
+    for (int b = 0; b < 4; b++) A[b] = (le_v4i){0, 0, 0, 0};
+#pragma unroll 1
+    for (int i = 0; i < nmem; i++) {
+        const uint4 *rec = img + mtok[i] * (LE_MOE_IMG(K) / 16);
+        const float *dxp = (const float *)(rec + NSB * 32), *fsv = dxp + NSB * 16;
+        float y[4] = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int q = 0; q < P; q++) {
+            const int sb = wave * P + q;
+            ms_load_a(rec + sb * 32, L, A);
+            ms_sb_q4k_n<4>(wb + n * CPR + 9 * q, 16 * CPR, A, dxp + sb * 16, fsv + sb * 8, L, y);
+        }
+#pragma unroll
+        for (int ti = 0; ti < 4; ti++) {
+            float v = y[ti];
+            v += __builtin_bit_cast(float, __builtin_amdgcn_ds_swizzle(__builtin_bit_cast(int, v), 0x401F));
+            v += __shfl_xor(v, 32);
+            if (lane < 16) red[wave][i][16 * ti + lane] = v;
+        }
+    }
+    __syncthreads();
+    LE_TRACE_POINT(3);
+    /* 5. SwiGLU of the unit's 32 values = sub-block ux of the down input: thread (member i, row r)
+     * adds the waves for gate and up; then lanes 2i, 2i+1 of wave 0 quantize member i's two
+     * 16-value segments into its down image */
+    if (threadIdx.x < 32 * LE_MOE_FAST_TOK) {
+        const int i = threadIdx.x >> 5, r = threadIdx.x & 31;
+        if (i < nmem) {
+            float g = 0.f, u = 0.f;
+#pragma unroll
+            for (int w = 0; w < NW; w++) {
+                g += red[w][i][r];
+                u += red[w][i][32 + r];
+            }
+            act[i][r] = g / (1.0f + __expf(-g)) * u;
+        }
+    }
+    __syncthreads();
+    if (wave == 0 && lane < 2 * LE_MOE_FAST_TOK) {
+        const int i = lane >> 1, c = lane & 1;
+        const bool ok = i < nmem;
+        const float4 *av = (const float4 *)&act[ok ? i : 0][16 * c];
+        float4 v4[4];
+#pragma unroll
+        for (int q = 0; q < 4; q++) v4[q] = av[q];
+        const int nsbd = a.ff >> 8;
+        uint4 *rec = (uint4 *)(a.ws + (size_t)mpair[ok ? i : 0] * LE_MOE_IMG(a.ff));
+        float *dxp = (float *)(rec + nsbd * 32), *fsv = dxp + nsbd * 16;
+        mq_quant_seg<MAPD>(2 * ux + c, ok, v4, rec, dxp, fsv);
+    }
+    LE_TRACE_POINT(4);
+    LE_TRACE_FLUSH;
+}
+
+#define LE_MOE_DN_IMGS 16 /* pair images the down kernel keeps in LDS */
+template <int TD, int NW, int P>
+__device__ __forceinline__ void moe_dnm_body(const MoeArgs &a) {
+    constexpr int MAPD = TD == LE_TYPE_Q6_K ? 1 : 0, CPS = TD == LE_TYPE_Q6_K ? 14 : 9, SBB = TD == LE_TYPE_Q6_K ? 210 : 144;
+    constexpr int CPR = CPS * P + 1, NCH = 16 * CPR, NI = (NCH + 63) / 64, IMG = LE_MOE_IMG(256 * P), IMGC = IMG / 16;
+    constexpr int SLOTS = LE_MOE_DN_IMGS / NW; /* image slots per wave when the pairs do not all fit */
+    __shared__ MoeRoute R;
+    __shared__ float sx[LE_MOE_FAST_TOK * LE_MOE_MAXK];
+    __shared__ float red[NW][LE_MOE_FAST_TOK][16];
+    __shared__ int mtok[NW][LE_MOE_FAST_TOK], mpair[NW][LE_MOE_FAST_TOK];
+    __shared__ float mw[NW][LE_MOE_FAST_TOK];
+    extern __shared__ uint4 smem[];
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, n = lane & 15;
+    uint4 *imgs = smem;                          /* LE_MOE_DN_IMGS images */
+    uint4 *stg = smem + LE_MOE_DN_IMGS * IMGC;   /* [NW][NI*64] staging; routing keys first */
+    uint4 *wb = stg + wave * NI * 64;
+    LE_TRACE_DECL;
+    LE_TRACE_POINT(0);
+    for (int i = threadIdx.x; i < NW * LE_MOE_FAST_TOK * 16; i += blockDim.x) (&red[0][0][0])[i] = 0.f;
+    /* the routing of the gate/up launch (n_tok * k <= 64 <= blockDim.x, groups <= 64) */
+    moe_rec_read(a, R, a.ws + (size_t)a.n_tok * a.k * IMG);
+    LE_TRACE_POINT(1);
+    const int npair = a.n_tok * a.k;
+    const bool all_in = npair <= LE_MOE_DN_IMGS;
+    const size_t rb = (size_t)P * SBB;
+    const int row0 = 16 * blockIdx.x;
+    int roff[NI];
+#pragma unroll
+    for (int i = 0; i < NI; i++) {
+        const int c = min(64 * i + lane, NCH - 1), col = c % CPR, cc = col == CPS * P ? 0 : col;
+        roff[i] = (row0 + c / CPR) * (int)rb + (TD == LE_TYPE_Q6_K ? (cc / 14) * 210 + (cc % 14) * 16 : cc * 16);
+    }
+    /* weights of two groups in flight: R0 is the next group to compute, R1 the one after */
+    uint4 R0[NI], R1[NI];
+    auto issue = [&](int zz, uint4 (&r)[NI]) {
+        const u8 *W = a.down + (size_t)R.grp_e[zz] * a.hidden * rb;
+#pragma unroll
+        for (int i = 0; i < NI; i++) r[i] = TD == LE_TYPE_Q6_K ? ldg16u(W + roff[i]) : ldg16(W + roff[i]);
+    };
+    if (wave < R.U) issue(wave, R0);
+    if (wave + NW < R.U) issue(wave + NW, R1);
+    if (all_in) { /* every pair's down image */
+        const int nc = npair * IMGC;
+#pragma unroll 1
+        for (int c0 = threadIdx.x; c0 < nc; c0 += 4 * 64 * NW) {
+            uint4 v[4];
+#pragma unroll
+            for (int q = 0; q < 4; q++) v[q] = ldg16c(a.ws + 16 * (size_t)min(c0 + 64 * NW * q, nc - 1));
+#pragma unroll
+            for (int q = 0; q < 4; q++)
+                if (c0 + 64 * NW * q < nc) imgs[c0 + 64 * NW * q] = v[q];
+        }
+    }
+    __syncthreads(); /* the images, and the routing keys are no longer read before staging reuses them */
+    LE_TRACE_POINT(5);
+    const MsLane L = ms_lane<MAPD>(lane);
+    le_v4i A[4];
+#pragma unroll
+    for (int b = 0; b < 4; b++) A[b] = (le_v4i){0, 0, 0, 0};
+    uint4 *wimg = imgs + wave * SLOTS * IMGC;
+#pragma unroll 1
+    for (int z = wave; z < R.U; z += NW) {
+        const int e = R.grp_e[z];
+        const int nmem = __popcll(R.mask[e]);
+        if (lane < nmem) {
+            int t, pair;
+            float w;
+            moe_member(a, R, e, lane, t, pair, w);
+            mtok[wave][lane] = t;
+            mpair[wave][lane] = pair;
+            mw[wave][lane] = w;
+        }
+#pragma unroll
+        for (int i = 0; i < NI; i++) {
+            wb[64 * i + lane] = R0[i];
+            R0[i] = R1[i];
+        }
+        if (z + 2 * NW < R.U) issue(z + 2 * NW, R1);
+#pragma unroll 1
+        for (int i = 0; i < nmem; i++) {
+            const uint4 *rec;
+            if (all_in) {
+                rec = imgs + mpair[wave][i] * IMGC;
+            } else { /* this member's image into one of the wave's slots */
+                uint4 *slot = wimg + (i % SLOTS) * IMGC;
+                const int pr = mpair[wave][i];
+                for (int o = lane; o < IMGC; o += 64) slot[o] = ldg16c(a.ws + (size_t)pr * IMG + 16 * o);
+                rec = slot;
+            }
+            const float *dxp = (const float *)(rec + P * 32), *fsv = dxp + P * 16;
+            float y = 0.f;
+#pragma unroll
+            for (int q = 0; q < P; q++) {
+                ms_load_a(rec + q * 32, L, A);
+                if constexpr (TD == LE_TYPE_Q6_K)
+                    y += ms_sb_q6k(wb + n * CPR + CPS * q, A, dxp + q * 16, L);
+                else
+                    y += ms_sb_q4k(wb + n * CPR + CPS * q, A, dxp + q * 16, fsv + q * 8, L);
+            }
+            y += __builtin_bit_cast(float, __builtin_amdgcn_ds_swizzle(__builtin_bit_cast(int, y), 0x401F));
+            y += __shfl_xor(y, 32);
+            if (lane < 16) red[wave][mtok[wave][i]][lane] += mw[wave][i] * y;
+        }
+    }
+    LE_TRACE_POINT(2);
+    __syncthreads();
+    LE_TRACE_POINT(3);
+    for (int i = threadIdx.x; i < a.n_tok * 16; i += blockDim.x) {
+        const int t = i >> 4, r = i & 15;
+        float acc = 0.f;
+#pragma unroll
+        for (int w = 0; w < NW; w++) acc += red[w][t][r];
+        a.out[(size_t)t * a.hidden + row0 + r] = acc;
+    }
+    LE_TRACE_POINT(4);
+    LE_TRACE_FLUSH;
+}
+
+#define LE_MOE_GUM(TD, NW, P)                                                                               \
+    extern "C" __global__ void __launch_bounds__(64 * NW) le_moe_gum_12_##TD##_w##NW##_p##P(MoeArgs a) {  \
+        moe_gum_body<TD, NW, P>(a);                                                                        \
+    }
+#define LE_MOE_DNM(TD, NW, P)                                                                               \
+    extern "C" __global__ void __launch_bounds__(64 * NW) le_moe_dnm_##TD##_w##NW##_p##P(MoeArgs a) {      \
+        moe_dnm_body<TD, NW, P>(a);                                                                        \
+    }
+LE_MOE_GUM(14, 8, 1) LE_MOE_GUM(14, 4, 1) LE_MOE_GUM(14, 4, 3) LE_MOE_GUM(12, 8, 1) LE_MOE_GUM(12, 4, 1) LE_MOE_GUM(12, 4, 3)
+LE_MOE_DNM(14, 8, 1) LE_MOE_DNM(14, 8, 2) LE_MOE_DNM(14, 8, 3) LE_MOE_DNM(12, 8, 1) LE_MOE_DNM(12, 8, 2) LE_MOE_DNM(12, 8, 3)
 
 #define LE_MOE(TG, TD)                                                                                       \
     extern "C" __global__ void __launch_bounds__(256) le_moe_gu_##TG##_##TD##_g8(MoeArgs a) { moe_gu_body<TG, TD, 8>(a); } \
