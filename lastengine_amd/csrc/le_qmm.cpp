@@ -67,6 +67,7 @@ struct le_ctx {
     int mq_waves = 4, mq_steps = 2, mq_blocks_per_cu = 2;
     int ms = 1, ms_p = 2;    /* staged MFMA variant and its super-blocks per row and step */
     int mq6 = 1, ms_p6 = 2;  /* Q6_K decode matvec on the staged MFMA kernels, super-blocks per step */
+    int mqiq = 1, ms_piq = 2; /* IQ2_XXS / IQ3_XXS likewise */
     int moe_fast = 1;        /* decode-shaped MoE kernels */
     int moe_mfma = 1;        /* decode-shaped MoE on the staged MFMA kernels where the types allow */
     int gm_min_m = 16;       /* le_gemm uses the MFMA kernels from this many tokens on */
@@ -172,11 +173,11 @@ int mq_launch(le_ctx *c, int ty, const void *const *ptrs, const void *w, const f
     char name[64];
     size_t lds = (size_t)nsb * 608 + (size_t)NW * 64;
     /* staged variant: P super-blocks per row and item, NWs waves splitting K evenly */
-    int P = ty == LE_TYPE_Q6_K ? c->ms_p6 : c->ms_p, NWs = NW;
+    int P = ty == LE_TYPE_Q6_K ? c->ms_p6 : ty == LE_TYPE_Q4_K ? c->ms_p : c->ms_piq, NWs = NW;
     while (P > 1 && nsb % P) P >>= 1;
     while (NWs > 1 && nsb % (NWs * P)) NWs >>= 1;
     if (c->ms && nsb % (NWs * P) == 0) {
-        const int cps = ty == LE_TYPE_Q6_K ? 14 : 9;
+        const int cps = ty == LE_TYPE_Q6_K ? 14 : ty == LE_TYPE_IQ2_XXS ? 5 : ty == LE_TYPE_IQ3_XXS ? 7 : 9;
         const int cpr = cps * P + 1, ni = (16 * cpr + 63) / 64;
         snprintf(name, sizeof name, "le_ms_%d_p%d_w%d", ty, P, NWs);
         lds = (size_t)NWs * ((size_t)(nsb / NWs) * 608 + (size_t)ni * 1024) + (size_t)NWs * 128;
@@ -199,7 +200,8 @@ int mv_launch(le_ctx *c, int ty, const void *const *ptrs, const void *w, const f
     if (!x || !y || (!ptrs && !w)) return c->fail(LE_ERR_ARG, "null pointer");
     if (!al16(x) || (x_slot % 4) || (x_tok % 4)) return c->fail(LE_ERR_ALIGN, "activations must be 16-byte aligned");
     const int nsb = cols / 256, G = pick_g(nsb), S = nsb / G;
-    if ((ty == LE_TYPE_Q4_K || (ty == LE_TYPE_Q6_K && c->mq6)) && ntok == 1 && c->mq &&
+    const bool iq = ty == LE_TYPE_IQ2_XXS || ty == LE_TYPE_IQ3_XXS;
+    if ((ty == LE_TYPE_Q4_K || (ty == LE_TYPE_Q6_K && c->mq6) || (iq && c->mqiq)) && ntok == 1 && c->mq &&
         (size_t)nsb * 608 + 1024 <= c->lds_limit) {
         const int rc = mq_launch(c, ty, ptrs, w, x, x_slot, y, y_slot, rows, cols, slots, st);
         if (rc != 1) return rc;
@@ -333,6 +335,11 @@ int le_set_option(le_ctx *c, const char *name, int value) {
         c->mv_blocks_per_cu = value;
     } else if (n == "mq") {
         c->mq = value ? 1 : 0;
+    } else if (n == "mqiq") {
+        c->mqiq = value ? 1 : 0;
+    } else if (n == "ms_piq") {
+        if (value != 1 && value != 2 && value != 4) return c->fail(LE_ERR_ARG, "ms_piq must be 1, 2 or 4");
+        c->ms_piq = value;
     } else if (n == "mq6") {
         c->mq6 = value ? 1 : 0;
     } else if (n == "ms_p6") {

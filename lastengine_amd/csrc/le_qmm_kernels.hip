@@ -914,6 +914,169 @@ __device__ __forceinline__ void ms_q6k_body(const MvArgs &a) {
 #define LE_MS14(P, NW)                                                                                     \
     extern "C" __global__ void __launch_bounds__(NW * 64) le_ms_14_p##P##_w##NW(MvArgs a) { ms_q6k_body<P, NW>(a); }
 
+/* IQ2_XXS / IQ3_XXS on the staged MFMA design, under the Q4_K slice map (slice s of MFMA b is
+ * sub-block j = 4*(b>>1) + 2*(s>>1) + (b&1), values 16*(s&1)..+15). A super-block is staged from
+ * byte 2 (its quant bytes then start 16-byte aligned in LDS) plus one chunk from byte 0 holding d:
+ *   IQ2_XXS (66 B, src/quant.rs:142-154): chunks 0-3 = per sub-block j the grid indices (4 bytes at
+ *     8j) and aux (u32 at 8j+4: four 7-bit ksign indices, scale aux>>28); chunk 4 = d.
+ *   IQ3_XXS (98 B, src/quant.rs:127-141): chunks 0-3 = grid indices (8 per sub-block at 8j), chunks
+ *     4-5 = aux words (u32 at 64+4j), chunk 6 = d.
+ * The lane's 16 values are grid magnitudes from the LDS tables with the ksign masks applied, and
+ * the sub-block scale d * (2s+1) / 8 (IQ2) or / 4 (IQ3) comes in the epilogue. */
+template <int TY>
+struct MsIq;
+template <>
+struct MsIq<LE_TYPE_IQ2_XXS> {
+    static constexpr int CPS = 5, SBB = 66;
+    static constexpr float SCALE = 0.125f;
+    static __device__ __forceinline__ int goff(int c) { return c < 4 ? 2 + 16 * c : 0; }
+    /* B words of sub-block j, values 16h..16h+15 */
+    static __device__ __forceinline__ le_v4i bfrag(const u8 *sb, int j, int h, const u32 *tab) {
+        const uint2 q = *(const uint2 *)(sb + 8 * j);
+        const u32 *grid = tab + LE_TAB_GRID, *sg = tab + LE_TAB_SIGN;
+        u32 w[4];
+#pragma unroll
+        for (int l = 0; l < 2; l++) {
+            const int g = 2 * h + l;
+            const u32 gi = (q.x >> (8 * g)) & 255u, si = (q.y >> (7 * g)) & 127u;
+            const uint2 gv = *(const uint2 *)(grid + 2 * gi);
+            const uint2 m = *(const uint2 *)(sg + 2 * si);
+            w[2 * l] = apply_sign(gv.x, m.x);
+            w[2 * l + 1] = apply_sign(gv.y, m.y);
+        }
+        return (le_v4i){(int)w[0], (int)w[1], (int)w[2], (int)w[3]};
+    }
+    static __device__ __forceinline__ u32 aux(const u8 *sb, int j) { return *(const u32 *)(sb + 8 * j + 4); }
+    static __device__ __forceinline__ float d(const u8 *sb) { return h2f(*(const u32 *)(sb + 64) & 0xFFFFu); }
+};
+template <>
+struct MsIq<LE_TYPE_IQ3_XXS> {
+    static constexpr int CPS = 7, SBB = 98;
+    static constexpr float SCALE = 0.25f;
+    static __device__ __forceinline__ int goff(int c) { return c < 6 ? 2 + 16 * c : 0; }
+    static __device__ __forceinline__ le_v4i bfrag(const u8 *sb, int j, int h, const u32 *tab) {
+        const u32 q = *(const u32 *)(sb + 8 * j + 4 * h), ax = *(const u32 *)(sb + 64 + 4 * j);
+        const u32 *grid = tab + LE_TAB_GRID, *sg = tab + LE_TAB_SIGN;
+        const uint2 m0 = *(const uint2 *)(sg + 2 * ((ax >> (14 * h)) & 127u));
+        const uint2 m1 = *(const uint2 *)(sg + 2 * ((ax >> (14 * h + 7)) & 127u));
+        return (le_v4i){(int)apply_sign(grid[q & 255u], m0.x), (int)apply_sign(grid[(q >> 8) & 255u], m0.y),
+                        (int)apply_sign(grid[(q >> 16) & 255u], m1.x), (int)apply_sign(grid[q >> 24], m1.y)};
+    }
+    static __device__ __forceinline__ u32 aux(const u8 *sb, int j) { return *(const u32 *)(sb + 64 + 4 * j); }
+    static __device__ __forceinline__ float d(const u8 *sb) { return h2f(*(const u32 *)(sb + 96) & 0xFFFFu); }
+};
+
+template <int TY>
+__device__ __forceinline__ float ms_sb_iq(const u8 *sb, const le_v4i (&A)[4], const float *dxp_sb, const MsLane &L, const u32 *tab) {
+    using F = MsIq<TY>;
+    const int sq = L.sq;
+    le_v4i D = {0, 0, 0, 0};
+#pragma unroll
+    for (int b = 0; b < 4; b++) D = __builtin_amdgcn_mfma_i32_16x16x64_i8(A[b], F::bfrag(sb, mq_j(b, sq), sq & 1, tab), D, 0, 0, 0);
+    const float4 dq = *(const float4 *)(dxp_sb + L.pe * 8 + L.jb);
+    const float dqa[4] = {dq.x, dq.y, dq.z, dq.w};
+    float t = 0.f;
+#pragma unroll
+    for (int i = 0; i < 4; i++) t += (float)(2 * (F::aux(sb, L.jb + i) >> 28) + 1) * dqa[i] * (float)D[i];
+    return F::d(sb) * F::SCALE * t;
+}
+
+template <int TY, int P, int NW>
+__device__ __forceinline__ void ms_iq_body(const MvArgs &a) {
+    using F = MsIq<TY>;
+    extern __shared__ uint4 smem[];
+    constexpr int CPS = F::CPS, CPR = CPS * P + 1, NCH = 16 * CPR, NI = (NCH + 63) / 64;
+    __shared__ u32 tab[256 + 512];
+    load_tables<TY>(tab);
+    const int K = a.cols, nsb = K >> 8;
+    const int slot = blockIdx.y;
+    const u8 *W = a.ptrs ? a.ptrs[slot] : a.w0 + (size_t)slot * a.w_slot_bytes;
+    const size_t rb = (size_t)nsb * F::SBB;
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int n = lane & 15;
+    const int nsbw = nsb / NW;
+    uint4 *rec = smem + wave * (nsbw * 38 + NI * 64);
+    float *dxp = (float *)(rec + nsbw * 32);
+    float *fsv = dxp + nsbw * 16;
+    uint4 *wb = (uint4 *)(fsv + nsbw * 8);
+    float *red = (float *)(smem + NW * (nsbw * 38 + NI * 64)); /* [2][NW][16] */
+    const int ntile = (a.rows + 15) >> 4;
+    int ri[NI], gb[NI];
+#pragma unroll
+    for (int i = 0; i < NI; i++) {
+        const int c = min(64 * i + lane, NCH - 1);
+        const int col = c % CPR, cc = col == CPS * P ? 0 : col;
+        ri[i] = c / CPR;
+        gb[i] = (cc / CPS) * F::SBB + F::goff(cc % CPS);
+    }
+    uint4 R[NI];
+    auto issue = [&](int tile, int s0) {
+#pragma unroll
+        for (int i = 0; i < NI; i++) {
+            const int row = min(tile * 16 + ri[i], a.rows - 1);
+            R[i] = ldg16u(W + (size_t)row * rb + (size_t)s0 * F::SBB + gb[i]);
+        }
+    };
+    const int sfirst = wave * P, sstep = NW * P;
+    const bool active = sfirst < nsb;
+    const float *xs = a.x + a.x_slot * slot;
+    const int nsegw = nsbw * 16;
+    auto gseg = [&](int el) {
+        const int ls = el >> 4;
+        return ((ls / P) * sstep + sfirst + ls % P) * 16 + (el & 15);
+    };
+    float4 xv[4];
+    mq_load_seg(xs, gseg(min(lane, nsegw - 1)), xv);
+    issue(min((int)blockIdx.x, ntile - 1), active ? sfirst : 0);
+    mq_quant_seg<0>(lane, lane < nsegw, xv, rec, dxp, fsv);
+    for (int el = lane + 64; el < nsegw; el += 64) {
+        mq_load_seg(xs, gseg(el), xv);
+        mq_quant_seg<0>(el, true, xv, rec, dxp, fsv);
+    }
+    __syncthreads(); /* the tables */
+    const MsLane L = ms_lane<0>(lane);
+    le_v4i A[4];
+#pragma unroll
+    for (int b = 0; b < 4; b++) A[b] = (le_v4i){0, 0, 0, 0};
+    int par = 0;
+    for (int tile = blockIdx.x; tile < ntile; tile += gridDim.x) {
+        float y = 0.f;
+        if (active) {
+            for (int s0 = sfirst, lb = 0; s0 < nsb; s0 += sstep, lb += P) {
+                int nt = tile, ns = s0 + sstep;
+                if (ns >= nsb) { ns = sfirst; nt += gridDim.x; }
+#pragma unroll
+                for (int i = 0; i < NI; i++) wb[64 * i + lane] = R[i];
+                if (nt < ntile) issue(nt, ns);
+#pragma unroll
+                for (int q = 0; q < P; q++) {
+                    const int sb = lb + q;
+                    ms_load_a(rec + sb * 32, L, A);
+                    y += ms_sb_iq<TY>((const u8 *)(wb + n * CPR + CPS * q), A, dxp + sb * 16, L, tab);
+                }
+            }
+        }
+        y += __builtin_bit_cast(float, __builtin_amdgcn_ds_swizzle(__builtin_bit_cast(int, y), 0x401F));
+        y += __shfl_xor(y, 32);
+        float *rp = red + par * (NW * 16);
+        if (lane < 16) rp[wave * 16 + lane] = y;
+        __builtin_amdgcn_s_waitcnt(0xC07F);
+        __builtin_amdgcn_s_barrier();
+        if (wave == 0 && lane < 16) {
+            float acc = 0.f;
+#pragma unroll
+            for (int w = 0; w < NW; w++) acc += rp[w * 16 + lane];
+            const int r = tile * 16 + lane;
+            if (r < a.rows) a.y[a.y_slot * slot + r] = acc;
+        }
+        par ^= 1;
+    }
+}
+
+#define LE_MSIQ_(TY, P, NW)                                                                                \
+    extern "C" __global__ void __launch_bounds__(NW * 64) le_ms_##TY##_p##P##_w##NW(MvArgs a) { ms_iq_body<TY, P, NW>(a); }
+#define LE_MSIQ(TY, P, NW) LE_MSIQ_(TY, P, NW) /* expands TY before pasting */
+
 #define LE_MS12(P, NW)                                                                                     \
     extern "C" __global__ void __launch_bounds__(NW * 64) le_ms_12_p##P##_w##NW(MvArgs a) { ms_q4k_body<P, NW>(a); }
 
@@ -930,6 +1093,10 @@ LE_MS12(1, 1) LE_MS12(1, 2) LE_MS12(1, 4) LE_MS12(1, 8) LE_MS12(2, 1) LE_MS12(2,
 #endif
 #if LE_PART_MV == 14
 LE_MS14(1, 1) LE_MS14(1, 2) LE_MS14(1, 4) LE_MS14(1, 8) LE_MS14(2, 1) LE_MS14(2, 2) LE_MS14(2, 4) LE_MS14(4, 1) LE_MS14(4, 2)
+#endif
+#if LE_PART_MV == 16 || LE_PART_MV == 18
+LE_MSIQ(LE_PART_MV, 1, 1) LE_MSIQ(LE_PART_MV, 1, 2) LE_MSIQ(LE_PART_MV, 1, 4) LE_MSIQ(LE_PART_MV, 2, 1) LE_MSIQ(LE_PART_MV, 2, 2)
+LE_MSIQ(LE_PART_MV, 2, 4) LE_MSIQ(LE_PART_MV, 4, 1) LE_MSIQ(LE_PART_MV, 4, 2) LE_MSIQ(LE_PART_MV, 4, 4)
 #endif
 #endif
 
