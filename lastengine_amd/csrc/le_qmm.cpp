@@ -440,13 +440,15 @@ int le_moe_layer(le_ctx *c, int ty_gate, int ty_up, int ty_down, const void *gat
         (hidden == 1024 || hidden == 2048 || hidden == 3072) && dp >= 1 && dp <= 3) {
         const int nig = 9 * gp + 1, cps = ty_down == LE_TYPE_Q6_K ? 14 : 9, nid = (16 * (cps * dp + 1) + 63) / 64;
         const size_t img_g = (size_t)hidden / 256 * 608, img_d = (size_t)dp * 608;
-        snprintf(name, sizeof name, "le_moe_gum_12_%d_w%d_p%d", ty_down, gw, gp);
-        int rc = c->launch(name, dim3((unsigned)(ff / 32), (unsigned)groups), 64 * gw, 8 * img_g + (size_t)gw * nig * 1024,
-                           (hipStream_t)stream, args);
-        if (rc) return rc;
-        snprintf(name, sizeof name, "le_moe_dnm_%d_w8_p%d", ty_down, dp);
-        return c->launch(name, dim3((unsigned)(hidden / 16)), 512, 16 * img_d + 8 * (size_t)nid * 1024, (hipStream_t)stream,
-                         args);
+        const size_t lds_g = 8 * img_g + (size_t)gw * nig * 1024, lds_d = 16 * img_d + 8 * (size_t)nid * 1024;
+        /* dynamic LDS plus the kernels' static routing/reduction state (< 40 KB) must fit */
+        if (lds_g + 40960 <= c->lds_limit && lds_d + 40960 <= c->lds_limit) {
+            snprintf(name, sizeof name, "le_moe_gum_12_%d_w%d_p%d", ty_down, gw, gp);
+            int rc = c->launch(name, dim3((unsigned)(ff / 32), (unsigned)groups), 64 * gw, lds_g, (hipStream_t)stream, args);
+            if (rc) return rc;
+            snprintf(name, sizeof name, "le_moe_dnm_%d_w8_p%d", ty_down, dp);
+            return c->launch(name, dim3((unsigned)(hidden / 16)), 512, lds_d, (hipStream_t)stream, args);
+        }
     }
     /* decode-shaped fast paths: few tokens, short rows */
     const bool fast_gu = c->moe_fast && n_tok <= 8 && S <= 2 && n_tok * (hidden / 8) <= 4096;

@@ -91,3 +91,33 @@ def test_moe_errors(engine):
     with pytest.raises(le.LeError) as e:
         engine.moe(le.Q4_K, le.Q4_K, le.Q6_K, z, z, z, 8, 2, 256, 256, f, f, 1, f, ws=z, ws_bytes=16)
     assert e.value.code == -7
+
+
+@pytest.mark.parametrize("hidden,ff,td,n_tok", [(1024, 256, le.Q6_K, 2), (3072, 512, le.Q6_K, 1), (2048, 768, le.Q4_K, 3),
+                                                (2048, 256, le.Q6_K, 5), (1024, 768, le.Q4_K, 8)])
+def test_moe_staged_shapes(engine, hidden, ff, td, n_tok):
+    """The staged MFMA MoE kernels at each block shape they are built for (gate/up of 8 waves for
+    hidden 2048, 4 waves for 1024 / 3072; down super-blocks per row 1..3)."""
+    run(engine, le.Q4_K, td, 32, 4, hidden, ff, n_tok, seed=hidden + ff + n_tok)
+
+
+def test_moe_staged_matches_vector_path(engine):
+    """The staged MFMA kernels and the vector-ALU kernels agree on the same call."""
+    import torch
+    n_exp, k, hidden, ff, n_tok = 64, 8, 2048, 768, 4
+    g, _ = weights(le.Q4_K, n_exp * ff, hidden, 501)
+    u, _ = weights(le.Q4_K, n_exp * ff, hidden, 502)
+    d, _ = weights(le.Q6_K, n_exp * hidden, ff, 503)
+    h = acts(n_tok * hidden, 504).reshape(n_tok, hidden)
+    lg = acts(n_tok * n_exp, 505).reshape(n_tok, n_exp)
+    outs = []
+    for mfma in (1, 0):
+        engine.set_option("moe_mfma", mfma)
+        out = torch.empty(n_tok, hidden, dtype=torch.float32, device="cuda")
+        engine.moe(le.Q4_K, le.Q4_K, le.Q6_K, dev(g), dev(u), dev(d), n_exp, k, hidden, ff, dev(lg), dev(h), n_tok, out)
+        torch.cuda.synchronize()
+        outs.append(out.cpu().numpy())
+    engine.set_option("moe_mfma", 1)
+    want, _, _, mag = reference(le.Q4_K, le.Q6_K, g, u, d, n_exp, k, hidden, ff, h, lg)
+    check_close(outs[0], want, mag)
+    check_close(outs[1], want, mag)
