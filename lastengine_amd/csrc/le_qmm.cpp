@@ -70,6 +70,9 @@ struct le_ctx {
     int mqiq = 1, ms_piq = 2; /* IQ2_XXS / IQ3_XXS likewise */
     int moe_fast = 1;        /* decode-shaped MoE kernels */
     int moe_mfma = 1;        /* decode-shaped MoE on the staged MFMA kernels where the types allow */
+    int moe_fused = 1;       /* ... in one launch with a device-wide barrier where the grid fits */
+    int moe_fused_min_tok = 3; /* ... from this many tokens on (below, two launches are faster) */
+    std::map<std::string, int> occ; /* resident blocks per CU of the barrier kernels */
     int gm_min_m = 16;       /* le_gemm uses the MFMA kernels from this many tokens on */
     int gm_tile = 0;         /* MFMA GEMM tile: 0 auto, else 10*TM + TN (TM, TN in 1..2) */
     std::vector<hipModule_t> mods;
@@ -351,6 +354,10 @@ int le_set_option(le_ctx *c, const char *name, int value) {
         c->gm_tile = value;
     } else if (n == "gm_min_m") {
         c->gm_min_m = value;
+    } else if (n == "moe_fused_min_tok") {
+        c->moe_fused_min_tok = value;
+    } else if (n == "moe_fused") {
+        c->moe_fused = value ? 1 : 0;
     } else if (n == "moe_mfma") {
         c->moe_mfma = value ? 1 : 0;
     } else if (n == "moe_fast") {
@@ -433,6 +440,35 @@ int le_moe_layer(le_ctx *c, int ty_gate, int ty_up, int ty_down, const void *gat
     const int nsb = hidden / 256, g8 = nsb % 8 == 0;
     const int S = g8 ? nsb / 8 : nsb;
     const int groups = n_tok * k < n_exp ? n_tok * k : n_exp;
+    /* one launch with a device-wide barrier (hidden 2048): only with a grid that is resident at once */
+    if (c->moe_fused && n_tok >= c->moe_fused_min_tok && ty_gate == LE_TYPE_Q4_K &&
+        (ty_down == LE_TYPE_Q6_K || ty_down == LE_TYPE_Q4_K) && n_tok <= 8 &&
+        hidden == 2048 && ff % 256 == 0 && ff / 256 >= 1 && ff / 256 <= 3) {
+        const int pd = ff / 256, cps = ty_down == LE_TYPE_Q6_K ? 14 : 9, nid = (16 * (cps * pd + 1) + 63) / 64;
+        const size_t lds1 = 8 * (size_t)8 * 608 + 8 * (size_t)10 * 1024, lds2 = 16 * (size_t)pd * 608 + 8 * (size_t)nid * 1024;
+        const size_t lds = lds1 > lds2 ? lds1 : lds2;
+        snprintf(name, sizeof name, "le_moe_fus_12_%d_p%d", ty_down, pd);
+        hipFunction_t f = c->fn(name);
+        int per_cu = 0;
+        if (f) {
+            auto it = c->occ.find(name);
+            if (it != c->occ.end()) {
+                per_cu = it->second;
+            } else if (hipModuleOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, f, 512, lds) == hipSuccess) {
+                c->occ[name] = per_cu;
+            } else {
+                (void)hipGetLastError();
+                per_cu = 0;
+            }
+        }
+        const long long resident = (long long)c->cus * per_cu, ntile = hidden / 16;
+        const long long items = (long long)(ff / 32) * groups;
+        if (f && resident >= ntile && ntile <= 1024) { /* 1024: the kernel's arrival flags */
+            long long g = items > ntile ? (items < resident ? items : resident) : ntile;
+            if (g > 1024) g = 1024;
+            return c->launch(name, dim3((unsigned)g), 512, lds, (hipStream_t)stream, args);
+        }
+    }
     /* decode-shaped staged-MFMA path: Q4_K gate/up, Q4_K or Q6_K down; gate/up blocks of 8 waves
      * (hidden 2048) or 4 waves (hidden 1024, 3072), down blocks of 8 waves (ff 256, 512, 768) */
     const int gw = hidden == 2048 ? 8 : 4, gp = hidden / (256 * gw), dp = ff / 256;

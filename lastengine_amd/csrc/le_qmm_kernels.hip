@@ -430,7 +430,29 @@ __device__ __forceinline__ void mq_load_seg(const float *__restrict__ x, int e, 
 /* MAP 0 (Q4_K): slice s of MFMA b is sub-block j(b,s) = 4*(b>>1) + 2*(s>>1) + (b&1), positions
  * 16*(s&1)..; MAP 1 (Q6_K): MFMA b = (half b>>1, 16-value index b&1), slice s = quarter, so
  * sub-block j = 4*(b>>1) + s, positions 16*(b&1)... */
-template <int MAP = 0>
+/* Store helpers: COH = device-coherent stores (written through to where every XCD reads), for
+ * data another block reads in the same launch. */
+template <bool COH>
+__device__ __forceinline__ void st_u4(uint4 *p, uint4 v) {
+    if constexpr (COH) {
+        u32 *q = (u32 *)p;
+        __hip_atomic_store(q, v.x, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        __hip_atomic_store(q + 1, v.y, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        __hip_atomic_store(q + 2, v.z, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        __hip_atomic_store(q + 3, v.w, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    } else {
+        *p = v;
+    }
+}
+template <bool COH>
+__device__ __forceinline__ void st_f(float *p, float v) {
+    if constexpr (COH)
+        __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    else
+        *p = v;
+}
+
+template <int MAP = 0, bool COH = false>
 __device__ __forceinline__ void mq_quant_seg(int e, bool store, const float4 (&v4)[4], uint4 *rec, float *dxp, float *fsv) {
     float am = fmaxf(amax8(v4[0], v4[1]), amax8(v4[2], v4[3]));
     am = fmaxf(am, __shfl_xor(am, 1));
@@ -453,12 +475,12 @@ __device__ __forceinline__ void mq_quant_seg(int e, bool store, const float4 (&v
     const int sb = e >> 4, j = (e & 15) >> 1, c = e & 1;
     const int b = MAP ? 2 * (j >> 2) + c : 2 * (j >> 2) + (j & 1), s = MAP ? (j & 3) : 2 * ((j & 3) >> 1) + c;
     const int r = (sb * 16 + b * 4 + s) * 2;
-    rec[r] = make_uint4(hw[0], hw[1], hw[2], hw[3]);
-    rec[r + 1] = make_uint4(lw[0], lw[1], lw[2], lw[3]);
+    st_u4<COH>(rec + r, make_uint4(hw[0], hw[1], hw[2], hw[3]));
+    st_u4<COH>(rec + r + 1, make_uint4(lw[0], lw[1], lw[2], lw[3]));
     if (c == 0) {
-        dxp[sb * 16 + j] = d * 128.0f;
-        dxp[sb * 16 + 8 + j] = d;
-        fsv[sb * 8 + j] = d * (float)sum;
+        st_f<COH>(dxp + sb * 16 + j, d * 128.0f);
+        st_f<COH>(dxp + sb * 16 + 8 + j, d);
+        st_f<COH>(fsv + sb * 8 + j, d * (float)sum);
     }
 }
 __device__ __forceinline__ void mq_quant_x(const float *__restrict__ x, int K, uint4 *rec, float *dxp, float *fsv) {
@@ -2080,6 +2102,289 @@ __device__ __forceinline__ void moe_dnm_body(const MoeArgs &a) {
     LE_TRACE_POINT(4);
     LE_TRACE_FLUSH;
 }
+
+/* ===================== MoE in one launch: gate/up, a device-wide barrier, down =====================
+ * A persistent grid (the host launches no more blocks than fit on the device at once) of 8-wave
+ * blocks. Every block routes. Phase 1: blocks take the (32-row unit, expert group) items of the
+ * gate/up projection round-robin, as in le_moe_gum (hidden 2048). Before that, block b issues the
+ * weight loads of its first down group for row tile b (they depend on the routing only), so they
+ * arrive while phase 1 runs. A barrier over all blocks (arrival counter + generation word in device
+ * memory, self-resetting, bounded wait) separates the phases. Phase 2: block b computes row tile
+ * b of the down projection as in le_moe_dnm. If a wait ever exceeds its bound the block writes
+ * NaN to its outputs rather than waiting on. */
+#define LE_MOE_MAXGRID 1024
+__device__ unsigned int le_moe_bar_flag[LE_MOE_MAXGRID]; /* per block: the epoch it last arrived in */
+__device__ unsigned int le_moe_bar_gen;                  /* completed barriers */
+
+/* Arrival is a plain store of this barrier's epoch (gen + 1) to the block's own flag, so no
+ * arrival contends with another; block 0 polls all flags in parallel and then publishes the new
+ * generation. Callers store what other blocks read after the barrier with device-coherent stores
+ * (mq_quant_seg<.., true>). Every wait is bounded; false means a wait gave up. */
+__device__ __forceinline__ bool moe_grid_barrier(unsigned int nblocks) {
+    __shared__ unsigned int gen_s;
+    __shared__ int ok_s;
+    __builtin_amdgcn_s_waitcnt(0x0F70); /* vmcnt(0): this thread's coherent stores have completed */
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        const unsigned int gen = __hip_atomic_load(&le_moe_bar_gen, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        gen_s = gen;
+        ok_s = 1;
+        /* the data other blocks read was stored device-coherently and has completed (the block
+         * barrier above waits for it), so the arrival needs no L2 writeback */
+        __hip_atomic_store(&le_moe_bar_flag[blockIdx.x], gen + 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+    __syncthreads();
+    const unsigned int epoch = gen_s + 1u;
+    if (blockIdx.x == 0) {
+        for (unsigned int i = threadIdx.x; i < nblocks; i += blockDim.x) {
+            unsigned int spins = 0;
+            /* relaxed polls (an acquire per poll would invalidate L2 every time); one acquire after */
+            while (__hip_atomic_load(&le_moe_bar_flag[i], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) != epoch) {
+                __builtin_amdgcn_s_sleep(1);
+                if (++spins > (1u << 20)) { /* about a second of polling: give up instead of hanging */
+                    ok_s = 0;
+                    break;
+                }
+            }
+        }
+        __syncthreads();
+        if (threadIdx.x == 0) __hip_atomic_store(&le_moe_bar_gen, epoch, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    } else if (threadIdx.x == 0) {
+        unsigned int spins = 0;
+        while (__hip_atomic_load(&le_moe_bar_gen, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) != epoch) {
+            __builtin_amdgcn_s_sleep(1);
+            if (++spins > (1u << 20)) {
+                ok_s = 0;
+                break;
+            }
+        }
+    }
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
+    __syncthreads();
+    return ok_s != 0;
+}
+
+template <int TD, int PD>
+__device__ __forceinline__ void moe_fus_body(const MoeArgs &a) {
+    constexpr int NW = 8, P = 1, CPR = 9 * P + 1, NCH = 4 * 16 * CPR, NI = (NCH + 63) / 64, MAPD = TD == LE_TYPE_Q6_K ? 1 : 0;
+    constexpr int K = 2048, NSB = 8, SEGT = K / 16, NT = 512;
+    constexpr int XR = (LE_MOE_FAST_TOK * SEGT + NT - 1) / NT;
+    constexpr int DCPS = TD == LE_TYPE_Q6_K ? 14 : 9, DSBB = TD == LE_TYPE_Q6_K ? 210 : 144;
+    constexpr int DCPR = DCPS * PD + 1, DNCH = 16 * DCPR, DNI = (DNCH + 63) / 64, IMG = LE_MOE_IMG(256 * PD), IMGC = IMG / 16;
+    constexpr int SLOTS = LE_MOE_DN_IMGS / NW;
+    __shared__ MoeRoute R;
+    __shared__ float sx[LE_MOE_FAST_TOK * LE_MOE_MAXK];
+    __shared__ float red[NW][LE_MOE_FAST_TOK][64];
+    __shared__ __attribute__((aligned(16))) float act[LE_MOE_FAST_TOK][32];
+    __shared__ int mtok[NW][LE_MOE_FAST_TOK], mpair[NW][LE_MOE_FAST_TOK];
+    __shared__ float mw[NW][LE_MOE_FAST_TOK];
+    extern __shared__ uint4 smem[];
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, n = lane & 15;
+    uint4 *img = smem;                                         /* phase 1: [n_tok][image] */
+    uint4 *stg = smem + LE_MOE_FAST_TOK * LE_MOE_IMG(K) / 16; /* phase 1: [NW][NI*64] staging; routing keys first */
+    uint4 *wb = stg + wave * NI * 64;
+    LE_TRACE_DECL;
+    LE_TRACE_POINT(0);
+    /* every token's activations */
+    const int nseg = a.n_tok * SEGT;
+    float4 hv[XR][4];
+#pragma unroll
+    for (int r = 0; r < XR; r++) {
+        const int e = min((int)threadIdx.x + NT * r, nseg - 1);
+        mq_load_seg(a.h + (size_t)(e / SEGT) * K, e % SEGT, hv[r]);
+    }
+    moe_route_par(a, R, (unsigned long long *)stg, sx LE_TRACE_ARG);
+    LE_TRACE_POINT(1);
+    const int ngu = (a.ff >> 5) * R.U, ntile = a.hidden >> 4;
+    const int b = blockIdx.x, G = gridDim.x;
+    if (b == 0)
+        for (int i = threadIdx.x; i < a.n_tok * a.k; i += blockDim.x) {
+            if (a.idx_out) a.idx_out[i] = R.topi[i];
+            if (a.w_out) a.w_out[i] = R.topw[i];
+        }
+    /* the first down group of this block's tile, in flight through phase 1 */
+    const size_t drb = (size_t)PD * DSBB;
+    int roff[DNI];
+#pragma unroll
+    for (int i = 0; i < DNI; i++) {
+        const int c = min(64 * i + lane, DNCH - 1), col = c % DCPR, cc = col == DCPS * PD ? 0 : col;
+        roff[i] = (16 * b + c / DCPR) * (int)drb + (TD == LE_TYPE_Q6_K ? (cc / 14) * 210 + (cc % 14) * 16 : cc * 16);
+    }
+    uint4 R0[DNI];
+    auto dissue = [&](int zz, uint4 (&r)[DNI]) {
+        const u8 *W = a.down + (size_t)R.grp_e[zz] * a.hidden * drb;
+#pragma unroll
+        for (int i = 0; i < DNI; i++) r[i] = TD == LE_TYPE_Q6_K ? ldg16u(W + roff[i]) : ldg16(W + roff[i]);
+    };
+    if (b < ntile && wave < R.U) dissue(wave, R0);
+    /* ---- phase 1: gate/up items ---- */
+    if (b < ngu) {
+#pragma unroll
+        for (int r = 0; r < XR; r++) { /* token images (the Q4_K slice map) */
+            const int eg = (int)threadIdx.x + NT * r;
+            if (r * NT >= nseg) break;
+            const int t = min(eg, nseg - 1) / SEGT, el = min(eg, nseg - 1) % SEGT;
+            uint4 *rec = img + t * (LE_MOE_IMG(K) / 16);
+            float *dxp = (float *)(rec + NSB * 32), *fsv = dxp + NSB * 16;
+            mq_quant_seg<0>(el, eg < nseg, hv[r], rec, dxp, fsv);
+        }
+    }
+    const size_t rb = (size_t)NSB * 144;
+    const MsLane L0 = ms_lane<0>(lane);
+    le_v4i A[4];
+#pragma unroll
+    for (int q = 0; q < 4; q++) A[q] = (le_v4i){0, 0, 0, 0};
+#pragma unroll 1
+    for (int it = b; it < ngu; it += G) {
+        const int ux = it % (a.ff >> 5), z = it / (a.ff >> 5);
+        const int e = R.grp_e[z];
+        const int nmem = __popcll(R.mask[e]);
+        const u8 *Wg = a.gate + (size_t)e * a.ff * rb, *Wu = a.up + (size_t)e * a.ff * rb;
+        uint4 Rg[NI];
+#pragma unroll
+        for (int i = 0; i < NI; i++) {
+            const int c = min(64 * i + lane, NCH - 1), ti = c / (16 * CPR), rem = c % (16 * CPR), col = rem % CPR;
+            Rg[i] = ldg16((ti < 2 ? Wg : Wu) + (size_t)(32 * ux + 16 * (ti & 1) + rem / CPR) * rb + (size_t)wave * P * 144 +
+                          (col == 9 * P ? 0 : col) * 16);
+        }
+        if (threadIdx.x < nmem) {
+            int t, pair;
+            float w;
+            moe_member(a, R, e, threadIdx.x, t, pair, w);
+            mtok[0][threadIdx.x] = t;
+            mpair[0][threadIdx.x] = pair;
+        }
+        __syncthreads(); /* the previous item's readers of wb / act are done; images and members ready */
+#pragma unroll
+        for (int i = 0; i < NI; i++) wb[64 * i + lane] = Rg[i];
+#pragma unroll 1
+        for (int i = 0; i < nmem; i++) {
+            const uint4 *rec = img + mtok[0][i] * (LE_MOE_IMG(K) / 16);
+            const float *dxp = (const float *)(rec + NSB * 32), *fsv = dxp + NSB * 16;
+            float y[4] = {0.f, 0.f, 0.f, 0.f};
+            const int sb = wave;
+            ms_load_a(rec + sb * 32, L0, A);
+            ms_sb_q4k_n<4>(wb + n * CPR, 16 * CPR, A, dxp + sb * 16, fsv + sb * 8, L0, y);
+#pragma unroll
+            for (int ti = 0; ti < 4; ti++) {
+                float v = y[ti];
+                v += __builtin_bit_cast(float, __builtin_amdgcn_ds_swizzle(__builtin_bit_cast(int, v), 0x401F));
+                v += __shfl_xor(v, 32);
+                if (lane < 16) red[wave][i][16 * ti + lane] = v;
+            }
+        }
+        __syncthreads();
+        if (threadIdx.x < 32 * LE_MOE_FAST_TOK) {
+            const int i = threadIdx.x >> 5, r = threadIdx.x & 31;
+            if (i < nmem) {
+                float g = 0.f, u = 0.f;
+#pragma unroll
+                for (int w = 0; w < NW; w++) {
+                    g += red[w][i][r];
+                    u += red[w][i][32 + r];
+                }
+                act[i][r] = g / (1.0f + __expf(-g)) * u;
+            }
+        }
+        __syncthreads();
+        if (wave == 0 && lane < 2 * LE_MOE_FAST_TOK) {
+            const int i = lane >> 1, c = lane & 1;
+            const bool ok = i < nmem;
+            const float4 *av = (const float4 *)&act[ok ? i : 0][16 * c];
+            float4 v4[4];
+#pragma unroll
+            for (int q = 0; q < 4; q++) v4[q] = av[q];
+            uint4 *rec = (uint4 *)(a.ws + (size_t)mpair[0][ok ? i : 0] * IMG);
+            float *dxp = (float *)(rec + PD * 32), *fsv = dxp + PD * 16;
+            mq_quant_seg<MAPD, true>(2 * ux + c, ok, v4, rec, dxp, fsv); /* read by other blocks after the barrier */
+        }
+    }
+    /* ---- every down image written ---- */
+    LE_TRACE_POINT(2);
+    const bool ok = moe_grid_barrier(G);
+    LE_TRACE_POINT(3);
+    if (b >= ntile) return;
+    /* ---- phase 2: row tile b of the down projection ---- */
+    uint4 *imgs = smem;                        /* LE_MOE_DN_IMGS images */
+    uint4 *dwb = smem + LE_MOE_DN_IMGS * IMGC + wave * DNI * 64;
+    for (int i = threadIdx.x; i < NW * LE_MOE_FAST_TOK * 16; i += blockDim.x) (&red[0][0][0])[i] = 0.f;
+    const int npair = a.n_tok * a.k;
+    const bool all_in = npair <= LE_MOE_DN_IMGS;
+    if (all_in) {
+        const int nc = npair * IMGC;
+#pragma unroll 1
+        for (int c0 = threadIdx.x; c0 < nc; c0 += 4 * 512) {
+            uint4 v[4];
+#pragma unroll
+            for (int q = 0; q < 4; q++) v[q] = ldg16c(a.ws + 16 * (size_t)min(c0 + 512 * q, nc - 1));
+#pragma unroll
+            for (int q = 0; q < 4; q++)
+                if (c0 + 512 * q < nc) imgs[c0 + 512 * q] = v[q];
+        }
+    }
+    __syncthreads();
+    const MsLane L = ms_lane<MAPD>(lane);
+    /* the down map's dead A lanes must be zero: phase 1 filled the lanes live under the Q4_K map */
+#pragma unroll
+    for (int q = 0; q < 4; q++) A[q] = (le_v4i){0, 0, 0, 0};
+    uint4 *wimg = imgs + wave * SLOTS * IMGC;
+    float *redd = &red[0][0][0]; /* [NW][8][16] */
+#pragma unroll 1
+    for (int z = wave; z < R.U; z += NW) {
+        const int e = R.grp_e[z];
+        const int nmem = __popcll(R.mask[e]);
+        if (lane < nmem) {
+            int t, pair;
+            float w;
+            moe_member(a, R, e, lane, t, pair, w);
+            mtok[wave][lane] = t;
+            mpair[wave][lane] = pair;
+            mw[wave][lane] = w;
+        }
+#pragma unroll
+        for (int i = 0; i < DNI; i++) dwb[64 * i + lane] = R0[i];
+        if (z + NW < R.U) dissue(z + NW, R0);
+#pragma unroll 1
+        for (int i = 0; i < nmem; i++) {
+            const uint4 *rec;
+            if (all_in) {
+                rec = imgs + mpair[wave][i] * IMGC;
+            } else {
+                uint4 *slot = wimg + (i % SLOTS) * IMGC;
+                const int pr = mpair[wave][i];
+                for (int o = lane; o < IMGC; o += 64) slot[o] = ldg16c(a.ws + (size_t)pr * IMG + 16 * o);
+                rec = slot;
+            }
+            const float *dxp = (const float *)(rec + PD * 32), *fsv = dxp + PD * 16;
+            float y = 0.f;
+#pragma unroll
+            for (int q = 0; q < PD; q++) {
+                ms_load_a(rec + q * 32, L, A);
+                if constexpr (TD == LE_TYPE_Q6_K)
+                    y += ms_sb_q6k(dwb + n * DCPR + DCPS * q, A, dxp + q * 16, L);
+                else
+                    y += ms_sb_q4k(dwb + n * DCPR + DCPS * q, A, dxp + q * 16, fsv + q * 8, L);
+            }
+            y += __builtin_bit_cast(float, __builtin_amdgcn_ds_swizzle(__builtin_bit_cast(int, y), 0x401F));
+            y += __shfl_xor(y, 32);
+            if (lane < 16) redd[(wave * LE_MOE_FAST_TOK + mtok[wave][i]) * 16 + lane] += mw[wave][i] * y;
+        }
+    }
+    __syncthreads();
+    for (int i = threadIdx.x; i < a.n_tok * 16; i += blockDim.x) {
+        const int t = i >> 4, r = i & 15;
+        float acc = 0.f;
+#pragma unroll
+        for (int w = 0; w < NW; w++) acc += redd[(w * LE_MOE_FAST_TOK + t) * 16 + r];
+        a.out[(size_t)t * a.hidden + 16 * b + r] = ok ? acc : __builtin_nanf("");
+    }
+    LE_TRACE_POINT(4);
+    LE_TRACE_FLUSH;
+}
+
+#define LE_MOE_FUS(TD, PD)                                                                                  \
+    extern "C" __global__ void __launch_bounds__(512) le_moe_fus_12_##TD##_p##PD(MoeArgs a) { moe_fus_body<TD, PD>(a); }
+LE_MOE_FUS(14, 1) LE_MOE_FUS(14, 2) LE_MOE_FUS(14, 3) LE_MOE_FUS(12, 1) LE_MOE_FUS(12, 2) LE_MOE_FUS(12, 3)
 
 #define LE_MOE_GUM(TD, NW, P)                                                                               \
     extern "C" __global__ void __launch_bounds__(64 * NW) le_moe_gum_12_##TD##_w##NW##_p##P(MoeArgs a) {  \
