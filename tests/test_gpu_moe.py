@@ -121,3 +121,23 @@ def test_moe_staged_matches_vector_path(engine):
     want, _, _, mag = reference(le.Q4_K, le.Q6_K, g, u, d, n_exp, k, hidden, ff, h, lg)
     check_close(outs[0], want, mag)
     check_close(outs[1], want, mag)
+
+
+def test_moe_one_launch_repeated(engine):
+    """The single-launch path (3+ tokens) reuses its device-wide barrier across calls: twenty calls
+    in a row, every result checked."""
+    import torch
+    n_exp, k, hidden, ff, n_tok = 64, 8, 2048, 768, 6
+    g, _ = weights(le.Q4_K, n_exp * ff, hidden, 601)
+    u, _ = weights(le.Q4_K, n_exp * ff, hidden, 602)
+    d, _ = weights(le.Q6_K, n_exp * hidden, ff, 603)
+    h = acts(n_tok * hidden, 604).reshape(n_tok, hidden)
+    lg = acts(n_tok * n_exp, 605).reshape(n_tok, n_exp)
+    want, _, _, mag = reference(le.Q4_K, le.Q6_K, g, u, d, n_exp, k, hidden, ff, h, lg)
+    dg, du, dd, dh, dl = dev(g), dev(u), dev(d), dev(h), dev(lg)
+    out = torch.empty(n_tok, hidden, dtype=torch.float32, device="cuda")
+    for _ in range(20):
+        out.fill_(float("nan"))
+        engine.moe(le.Q4_K, le.Q4_K, le.Q6_K, dg, du, dd, n_exp, k, hidden, ff, dl, dh, n_tok, out)
+        torch.cuda.synchronize()
+        check_close(out.cpu().numpy(), want, mag)
