@@ -40,6 +40,8 @@ struct GmArgs {
     const float *x;
     float *y;
     int rows, cols, m;
+    int ksplit; /* K slices (blockIdx.y); with more than one, the slices add into y, which the
+                   pre-pass clears */
 };
 
 
@@ -101,6 +103,10 @@ __device__ __forceinline__ void gm_q4k_frag(uint2 w, uint4 k, le_v8h &lo, le_v8h
  * sums S_j as fp16 high halves then low halves. One wave per (token, super-block). */
 extern "C" __global__ void __launch_bounds__(256) le_gm_xprep(GmArgs a, u8 *ws) {
     const int K = a.cols, nsb = K >> 8;
+    if (a.ksplit > 1) { /* the K slices of the main pass add into y */
+        const size_t ny = (size_t)a.m * a.rows;
+        for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < ny; i += (size_t)gridDim.x * blockDim.x) a.y[i] = 0.f;
+    }
     const int wid = blockIdx.x * 4 + (threadIdx.x >> 6); /* the host keeps m * nsb below 2^31 */
     if (wid >= a.m * nsb) return;
     const int lane = threadIdx.x & 63;
@@ -159,7 +165,9 @@ __device__ __forceinline__ void gm_q4k_body(const GmArgs &a, const u8 *ws) {
     const int nb = nt * BN, mb = mt * BM;
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const size_t rb = (size_t)nsb * 144;
-    const int nstep = 2 * nsb;
+    /* K slice blockIdx.y: super-blocks sb0..sb1-1 (the host makes nsb a multiple of ksplit) */
+    const int sb0 = blockIdx.y * (nsb / a.ksplit), sb1 = sb0 + nsb / a.ksplit;
+    const int nstep = 2 * sb1;
     const _Float16 *Xh = (const _Float16 *)ws, *Xl = Xh + (size_t)M * K;
     const uint4 *Xs = (const uint4 *)(ws + (size_t)M * K * 4);
 
@@ -245,10 +253,10 @@ __device__ __forceinline__ void gm_q4k_body(const GmArgs &a, const u8 *ws) {
     unsigned long long tr[8] = {};
 #endif
     GM_T(t_start);
-    issue(0);
-    stage(0);
-    if (nstep > 1) issue(1);
-    for (int sb = 0; sb < nsb; sb++) {
+    issue(2 * sb0);
+    stage(2 * sb0);
+    issue(2 * sb0 + 1);
+    for (int sb = sb0; sb < sb1; sb++) {
 #pragma unroll
         for (int h = 0; h < 2; h++) {
             const int s = 2 * sb + h;
@@ -355,7 +363,12 @@ __device__ __forceinline__ void gm_q4k_body(const GmArgs &a, const u8 *ws) {
 #pragma unroll
             for (int e = 0; e < 16; e++) {
                 const int t = mb + 32 * i + 8 * (e >> 2) + 4 * hs + (e & 3);
-                if (t < M && r < a.rows) a.y[(size_t)t * a.rows + r] = acc[i][k][e];
+                if (t < M && r < a.rows) {
+                    if (a.ksplit > 1)
+                        unsafeAtomicAdd(a.y + (size_t)t * a.rows + r, acc[i][k][e]);
+                    else
+                        a.y[(size_t)t * a.rows + r] = acc[i][k][e];
+                }
             }
         }
 }

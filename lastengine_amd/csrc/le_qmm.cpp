@@ -73,8 +73,9 @@ struct le_ctx {
     int moe_fused = 1;       /* ... in one launch with a device-wide barrier where the grid fits */
     int moe_fused_min_tok = 3; /* ... from this many tokens on (below, two launches are faster) */
     std::map<std::string, int> occ; /* resident blocks per CU of the barrier kernels */
-    int gm_min_m = 16;       /* le_gemm uses the MFMA kernels from this many tokens on */
+    int gm_min_m = 4;        /* le_gemm uses the MFMA kernels from this many tokens on */
     int gm_tile = 0;         /* MFMA GEMM tile: 0 auto, else 10*TM + TN (TM, TN in 1..2) */
+    int gm_ksplit = 0;       /* MFMA GEMM K slices: 0 auto, else 1, 2, 4, 8 */
     std::vector<hipModule_t> mods;
     std::map<std::string, hipFunction_t> fns;
     std::string err;
@@ -348,6 +349,10 @@ int le_set_option(le_ctx *c, const char *name, int value) {
     } else if (n == "ms_p6") {
         if (value != 1 && value != 2) return c->fail(LE_ERR_ARG, "ms_p6 must be 1 or 2");
         c->ms_p6 = value;
+    } else if (n == "gm_ksplit") {
+        if (value != 0 && value != 1 && value != 2 && value != 4 && value != 8)
+            return c->fail(LE_ERR_ARG, "gm_ksplit must be 0, 1, 2, 4 or 8");
+        c->gm_ksplit = value;
     } else if (n == "gm_tile") {
         if (value && (value / 10 < 1 || value / 10 > 2 || value % 10 < 1 || value % 10 > 2))
             return c->fail(LE_ERR_ARG, "gm_tile must be 0, 11, 12, 21 or 22");
@@ -511,21 +516,8 @@ int le_gemm(le_ctx *c, int ty, const void *w, const float *x, int m, float *y, i
         if (ws_bytes < le_gemm_workspace_size(ty, m, cols))
             return c->fail(LE_ERR_WORKSPACE, "workspace needs %zu bytes", le_gemm_workspace_size(ty, m, cols));
         if (!al16(x) || !al16(ws)) return c->fail(LE_ERR_ALIGN, "x and ws must be 16-byte aligned");
-        struct {
-            const void *w;
-            const float *x;
-            float *y;
-            int rows, cols, m;
-        } a{w, x, y, rows, cols, m};
-        /* pass 1: activation halves and sub-block sums into the workspace, one wave per
-         * (token, super-block) */
-        void *pargs[] = {&a, &ws};
-        const long long waves = (long long)m * (cols / 256);
-        if (waves > 0x7FFFFFFFLL) return c->fail(LE_ERR_SHAPE, "GEMM activation size too large");
-        int rc = c->launch("le_gm_xprep", dim3((unsigned)((waves + 3) / 4)), 256, 0, (hipStream_t)stream, pargs);
-        if (rc) return rc;
-        /* pass 2: MFMA tiles of 32*TM tokens x 128*TN rows; the row tiles are padded to a multiple
-         * of 8 so that the token tiles of one row tile share blockIdx % 8 (one XCD) */
+        /* tiles: 32*TM tokens x 128*TN rows; K split into slices when the tiles alone would not
+         * fill the chip */
         int TM = m > 32 ? 2 : 1, TN = 2;
         if (c->gm_tile) {
             TM = c->gm_tile / 10;
@@ -533,16 +525,38 @@ int le_gemm(le_ctx *c, int ty, const void *w, const float *x, int m, float *y, i
         } else if ((long long)((rows + 255) / 256) * ((m + 32 * TM - 1) / (32 * TM)) < c->cus) {
             TN = 1; /* more, smaller row tiles when the grid would not fill the chip */
         }
-        const int BM = 32 * TM, BN = 128 * TN;
+        const int BM = 32 * TM, BN = 128 * TN, nsb = cols / 256;
         const long long nt = (rows + BN - 1) / BN, mt = (m + BM - 1) / BM;
         const long long grid = (nt + 7) / 8 * 8 * mt;
+        int ks = 1;
+        if (c->gm_ksplit > 0) {
+            ks = c->gm_ksplit;
+        } else {
+            while (ks < 8 && nt * mt * ks < c->cus && nsb % (2 * ks) == 0) ks *= 2;
+        }
+        if (nsb % ks) return c->fail(LE_ERR_SHAPE, "gm_ksplit=%d does not divide the %d super-blocks", ks, nsb);
+        struct {
+            const void *w;
+            const float *x;
+            float *y;
+            int rows, cols, m, ksplit;
+        } a{w, x, y, rows, cols, m, ks};
+        /* pass 1: activation halves and sub-block sums into the workspace, one wave per
+         * (token, super-block); clears y when K is split */
+        void *pargs[] = {&a, &ws};
+        const long long waves = (long long)m * (cols / 256);
+        if (waves > 0x7FFFFFFFLL) return c->fail(LE_ERR_SHAPE, "GEMM activation size too large");
+        int rc = c->launch("le_gm_xprep", dim3((unsigned)((waves + 3) / 4)), 256, 0, (hipStream_t)stream, pargs);
+        if (rc) return rc;
+        /* pass 2: the row tiles are padded to a multiple of 8 so that the token tiles of one row
+         * tile share blockIdx % 8 (one XCD); blockIdx.y is the K slice */
         /* two pipeline buffers of BN*(72+32+16+8) + BM*2*136*2 bytes, plus [2][BM] 32-byte sum records */
         const size_t lds = 2 * ((size_t)BN * 128 + (size_t)BM * 544) + (size_t)BM * 64;
         if (grid > 0x7FFFFFFFLL) return c->fail(LE_ERR_SHAPE, "GEMM grid too large");
         char name[48];
         snprintf(name, sizeof name, "le_gm_12_m%d_n%d", TM, TN);
         void *args[] = {&a, &ws};
-        return c->launch(name, dim3((unsigned)grid), 256, lds, (hipStream_t)stream, args);
+        return c->launch(name, dim3((unsigned)grid, (unsigned)ks), 256, lds, (hipStream_t)stream, args);
     }
     return mv_launch(c, ty, nullptr, w, x, 0, cols, y, 0, rows, rows, cols, m, 1, (hipStream_t)stream);
 }
