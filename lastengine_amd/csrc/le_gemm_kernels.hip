@@ -147,7 +147,10 @@ struct GmLds {
     static constexpr int S_OFF = 2 * BUF, BYTES = S_OFF + 2 * BM * 32; /* + sum records [2][BM][32 B] */
 };
 
-template <int TM, int TN>
+/* PC = producer/consumer blocks of 8 waves: waves 0-3 only compute (MFMAs, epilogues), waves
+ * 4-7 only load and stage the next step, so the staging work overlaps the MFMAs on other waves
+ * instead of alternating with them; otherwise 4 waves do both. */
+template <int TM, int TN, bool PC>
 __device__ __forceinline__ void gm_q4k_body(const GmArgs &a, const u8 *ws) {
     using L = GmLds<TM, TN>;
     constexpr int BM = L::BM, BN = L::BN;
@@ -164,6 +167,8 @@ __device__ __forceinline__ void gm_q4k_body(const GmArgs &a, const u8 *ws) {
     if (nt >= NT) return; /* uniform over the block */
     const int nb = nt * BN, mb = mt * BM;
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const bool producer = PC && wave >= 4;
+    const int st = PC ? (tid & 255) : tid; /* staging thread index */
     const size_t rb = (size_t)nsb * 144;
     /* K slice blockIdx.y: super-blocks sb0..sb1-1 (the host makes nsb a multiple of ksplit) */
     const int sb0 = blockIdx.y * (nsb / a.ksplit), sb1 = sb0 + nsb / a.ksplit;
@@ -181,26 +186,26 @@ __device__ __forceinline__ void gm_q4k_body(const GmArgs &a, const u8 *ws) {
         const int sb = s >> 1, h = s & 1;
         const u8 *w0 = a.w + (size_t)sb * 144;
 #pragma unroll
-        for (int i = 0; i < NHC; i++) wh[i] = ldg16(w0 + (size_t)min(nb + tid + 256 * i, a.rows - 1) * rb);
+        for (int i = 0; i < NHC; i++) wh[i] = ldg16(w0 + (size_t)min(nb + st + 256 * i, a.rows - 1) * rb);
 #pragma unroll
         for (int i = 0; i < NQC; i++) {
-            const int c = tid + 256 * i, row = c >> 2;
+            const int c = st + 256 * i, row = c >> 2;
             wq[i] = ldg16(w0 + (size_t)min(nb + row, a.rows - 1) * rb + 16 + 64 * h + 16 * (c & 3));
         }
 #pragma unroll
         for (int i = 0; i < NXC; i++) {
-            const int c = tid + 256 * i, t = min(mb + (c >> 5), M - 1);
+            const int c = st + 256 * i, t = min(mb + (c >> 5), M - 1);
             const _Float16 *src = ((c >> 4) & 1 ? Xl : Xh) + (size_t)t * K + 256 * sb + 128 * h + 8 * (c & 15);
             xa[i] = ldg16c((const u8 *)src);
         }
-        if (h == 0 && tid < 2 * BM) xs = ldg16c((const u8 *)(Xs + 2 * ((size_t)min(mb + (tid >> 1), M - 1) * nsb + sb) + (tid & 1)));
+        if (h == 0 && st < 2 * BM) xs = ldg16c((const u8 *)(Xs + 2 * ((size_t)min(mb + (st >> 1), M - 1) * nsb + sb) + (st & 1)));
     };
     auto stage = [&](int s) {
         const int sb = s >> 1, h = s & 1;
         u8 *B = lds + (s & 1) * L::BUF;
 #pragma unroll
         for (int i = 0; i < NHC; i++) {
-            const int row = tid + 256 * i;
+            const int row = st + 256 * i;
             if (row >= BN) break;
             const u32 sy = wh[i].y, sz = wh[i].z, sw = wh[i].w;
             const u32 scw = h ? ((sw & 0x0F0F0F0Fu) | ((sy >> 2) & 0x30303030u)) : (sy & 0x3F3F3F3Fu);
@@ -225,17 +230,17 @@ __device__ __forceinline__ void gm_q4k_body(const GmArgs &a, const u8 *ws) {
         }
 #pragma unroll
         for (int i = 0; i < NQC; i++) {
-            const int c = tid + 256 * i;
+            const int c = st + 256 * i;
             uint2 *d = (uint2 *)(B + L::W_OFF + (c >> 2) * GM_WS + 16 * (c & 3));
             d[0] = make_uint2(wq[i].x, wq[i].y);
             d[1] = make_uint2(wq[i].z, wq[i].w);
         }
 #pragma unroll
         for (int i = 0; i < NXC; i++) {
-            const int c = tid + 256 * i;
+            const int c = st + 256 * i;
             *(uint4 *)(B + ((c >> 4) & 1 ? L::AL_OFF : L::AH_OFF) + ((c >> 5) * GM_AS + 8 * (c & 15)) * 2) = xa[i];
         }
-        if (h == 0 && tid < 2 * BM) Sx[((sb & 1) * BM + (tid >> 1)) * 2 + (tid & 1)] = xs;
+        if (h == 0 && st < 2 * BM) Sx[((sb & 1) * BM + (st >> 1)) * 2 + (st & 1)] = xs;
     };
 
     v16f acc[TM][TN], d1[TM][TN];
@@ -253,9 +258,11 @@ __device__ __forceinline__ void gm_q4k_body(const GmArgs &a, const u8 *ws) {
     unsigned long long tr[8] = {};
 #endif
     GM_T(t_start);
-    issue(2 * sb0);
-    stage(2 * sb0);
-    issue(2 * sb0 + 1);
+    if (!PC || producer) {
+        issue(2 * sb0);
+        stage(2 * sb0);
+        issue(2 * sb0 + 1);
+    }
     for (int sb = sb0; sb < sb1; sb++) {
 #pragma unroll
         for (int h = 0; h < 2; h++) {
@@ -264,6 +271,11 @@ __device__ __forceinline__ void gm_q4k_body(const GmArgs &a, const u8 *ws) {
             gm_barrier(); /* step s is staged; every wave is done with step s-1's buffer */
             GM_T(tb);
             GM_ADD(0, ta, tb);
+            if (producer) { /* the next step's staging and the loads two steps ahead */
+                if (s + 1 < nstep) stage(s + 1);
+                if (s + 2 < nstep) issue(s + 2);
+                continue;
+            }
             const u8 *B = lds + h * L::BUF; /* s & 1 == h */
             const _Float16 *Ah = (const _Float16 *)(B + L::AH_OFF), *Al = (const _Float16 *)(B + L::AL_OFF);
 #pragma unroll
@@ -306,7 +318,7 @@ __device__ __forceinline__ void gm_q4k_body(const GmArgs &a, const u8 *ws) {
                 }
 #if !defined(GM_DIAG_NOSTAGE)
                 /* the next step's staging and the loads two steps ahead run under this step's MFMAs */
-                if (gl == 0) {
+                if (!PC && gl == 0) {
                     if (s + 1 < nstep) stage(s + 1);
 #if !defined(GM_DIAG_NOISSUE)
                     if (s + 2 < nstep) issue(s + 2);
@@ -317,6 +329,7 @@ __device__ __forceinline__ void gm_q4k_body(const GmArgs &a, const u8 *ws) {
             GM_T(tc);
             GM_ADD(1, tb, tc);
         }
+        if (producer) continue;
         GM_T(td0);
         /* super-block epilogue: Y += d * D1 - dmin * D2, D2 = sum_j m_j S_j by one more MFMA per
          * tile (K slice 0: high halves of S_0..7, slice 1: low halves, both against m); all D2
@@ -354,6 +367,7 @@ __device__ __forceinline__ void gm_q4k_body(const GmArgs &a, const u8 *ws) {
     if (tid == 0)
         for (int i = 0; i < 8; i++) le_gm_trace[blockIdx.x * 8 + i] = tr[i];
 #endif
+    if (producer) return;
     /* D lane l element e: token 8*(e/4) + 4*(l/32) + e%4 of the tile, weight row l%32 */
 #pragma unroll
     for (int i = 0; i < TM; i++)
@@ -375,7 +389,10 @@ __device__ __forceinline__ void gm_q4k_body(const GmArgs &a, const u8 *ws) {
 
 #define LE_GM(TM, TN)                                                                                      \
     extern "C" __global__ void __launch_bounds__(256) le_gm_12_m##TM##_n##TN(GmArgs a, const u8 *ws) {    \
-        gm_q4k_body<TM, TN>(a, ws);                                                                        \
+        gm_q4k_body<TM, TN, false>(a, ws);                                                                 \
+    }                                                                                                      \
+    extern "C" __global__ void __launch_bounds__(512) le_gm_12_m##TM##_n##TN##_pc(GmArgs a, const u8 *ws) { \
+        gm_q4k_body<TM, TN, true>(a, ws);                                                                  \
     }
 
 LE_GM(1, 1) LE_GM(1, 2) LE_GM(2, 1) LE_GM(2, 2)

@@ -76,6 +76,7 @@ struct le_ctx {
     int gm_min_m = 4;        /* le_gemm uses the MFMA kernels from this many tokens on */
     int gm_tile = 0;         /* MFMA GEMM tile: 0 auto, else 10*TM + TN (TM, TN in 1..2) */
     int gm_ksplit = 0;       /* MFMA GEMM K slices: 0 auto, else 1, 2, 4, 8 */
+    int gm_pc = 1;           /* MFMA GEMM with producer/consumer waves */
     std::vector<hipModule_t> mods;
     std::map<std::string, hipFunction_t> fns;
     std::string err;
@@ -349,6 +350,8 @@ int le_set_option(le_ctx *c, const char *name, int value) {
     } else if (n == "ms_p6") {
         if (value != 1 && value != 2) return c->fail(LE_ERR_ARG, "ms_p6 must be 1 or 2");
         c->ms_p6 = value;
+    } else if (n == "gm_pc") {
+        c->gm_pc = value ? 1 : 0;
     } else if (n == "gm_ksplit") {
         if (value != 0 && value != 1 && value != 2 && value != 4 && value != 8)
             return c->fail(LE_ERR_ARG, "gm_ksplit must be 0, 1, 2, 4 or 8");
@@ -522,9 +525,12 @@ int le_gemm(le_ctx *c, int ty, const void *w, const float *x, int m, float *y, i
         if (c->gm_tile) {
             TM = c->gm_tile / 10;
             TN = c->gm_tile % 10;
+        } else if (c->gm_pc && TM == 2) {
+            TN = 1; /* the producer/consumer kernel of 64 x 256 tiles does not fit its registers */
         } else if ((long long)((rows + 255) / 256) * ((m + 32 * TM - 1) / (32 * TM)) < c->cus) {
             TN = 1; /* more, smaller row tiles when the grid would not fill the chip */
         }
+        const bool pc = c->gm_pc && !(TM == 2 && TN == 2);
         const int BM = 32 * TM, BN = 128 * TN, nsb = cols / 256;
         const long long nt = (rows + BN - 1) / BN, mt = (m + BM - 1) / BM;
         const long long grid = (nt + 7) / 8 * 8 * mt;
@@ -554,9 +560,9 @@ int le_gemm(le_ctx *c, int ty, const void *w, const float *x, int m, float *y, i
         const size_t lds = 2 * ((size_t)BN * 128 + (size_t)BM * 544) + (size_t)BM * 64;
         if (grid > 0x7FFFFFFFLL) return c->fail(LE_ERR_SHAPE, "GEMM grid too large");
         char name[48];
-        snprintf(name, sizeof name, "le_gm_12_m%d_n%d", TM, TN);
+        snprintf(name, sizeof name, "le_gm_12_m%d_n%d%s", TM, TN, pc ? "_pc" : "");
         void *args[] = {&a, &ws};
-        return c->launch(name, dim3((unsigned)grid, (unsigned)ks), 256, lds, (hipStream_t)stream, args);
+        return c->launch(name, dim3((unsigned)grid, (unsigned)ks), pc ? 512 : 256, lds, (hipStream_t)stream, args);
     }
     return mv_launch(c, ty, nullptr, w, x, 0, cols, y, 0, rows, rows, cols, m, 1, (hipStream_t)stream);
 }
