@@ -316,15 +316,11 @@ __device__ __forceinline__ void gm_q4k_body(const GmArgs &a, const u8 *ws) {
                                 d1[i][k] = __builtin_amdgcn_mfma_f32_32x32x16_f16(al[i], half ? bhi[k] : blo[k], d1[i][k], 0, 0, 0);
                     }
                 }
-#if !defined(GM_DIAG_NOSTAGE)
                 /* the next step's staging and the loads two steps ahead run under this step's MFMAs */
                 if (!PC && gl == 0) {
                     if (s + 1 < nstep) stage(s + 1);
-#if !defined(GM_DIAG_NOISSUE)
                     if (s + 2 < nstep) issue(s + 2);
-#endif
                 }
-#endif
             }
             GM_T(tc);
             GM_ADD(1, tb, tc);
