@@ -1110,15 +1110,16 @@ __device__ __forceinline__ void ms_iq_body(const MvArgs &a) {
 #if defined(LE_PART_MV)
 LE_MV_ALL(LE_PART_MV)
 #if LE_PART_MV == 12
-LE_MQ12(4, 1) LE_MQ12(4, 2) LE_MQ12(4, 4) LE_MQ12(8, 1) LE_MQ12(8, 2) LE_MQ12(2, 4)
+LE_MQ12(4, 1) LE_MQ12(4, 2) LE_MQ12(4, 4) LE_MQ12(8, 1) LE_MQ12(8, 2) LE_MQ12(8, 4) LE_MQ12(2, 1) LE_MQ12(2, 2) LE_MQ12(2, 4)
 LE_MS12(1, 1) LE_MS12(1, 2) LE_MS12(1, 4) LE_MS12(1, 8) LE_MS12(2, 1) LE_MS12(2, 2) LE_MS12(2, 4) LE_MS12(2, 8) LE_MS12(4, 1) LE_MS12(4, 2) LE_MS12(4, 4)
 #endif
 #if LE_PART_MV == 14
-LE_MS14(1, 1) LE_MS14(1, 2) LE_MS14(1, 4) LE_MS14(1, 8) LE_MS14(2, 1) LE_MS14(2, 2) LE_MS14(2, 4) LE_MS14(4, 1) LE_MS14(4, 2)
+LE_MS14(1, 1) LE_MS14(1, 2) LE_MS14(1, 4) LE_MS14(1, 8) LE_MS14(2, 1) LE_MS14(2, 2) LE_MS14(2, 4) LE_MS14(2, 8) LE_MS14(4, 1) LE_MS14(4, 2)
 #endif
 #if LE_PART_MV == 16 || LE_PART_MV == 18
 LE_MSIQ(LE_PART_MV, 1, 1) LE_MSIQ(LE_PART_MV, 1, 2) LE_MSIQ(LE_PART_MV, 1, 4) LE_MSIQ(LE_PART_MV, 2, 1) LE_MSIQ(LE_PART_MV, 2, 2)
 LE_MSIQ(LE_PART_MV, 2, 4) LE_MSIQ(LE_PART_MV, 4, 1) LE_MSIQ(LE_PART_MV, 4, 2) LE_MSIQ(LE_PART_MV, 4, 4)
+LE_MSIQ(LE_PART_MV, 1, 8) LE_MSIQ(LE_PART_MV, 2, 8)
 #endif
 #endif
 

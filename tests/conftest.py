@@ -19,3 +19,14 @@ def engine():
         pytest.skip("no GPU")
     import lastengine_amd as le
     return le.Engine()
+
+
+@pytest.fixture
+def fresh_engine():
+    """A context of its own, for tests that change launch options (the session engine keeps the
+    defaults)."""
+    import torch
+    if not torch.cuda.is_available():
+        pytest.skip("no GPU")
+    import lastengine_amd as le
+    return le.Engine()

@@ -101,9 +101,10 @@ def test_moe_staged_shapes(engine, hidden, ff, td, n_tok):
     run(engine, le.Q4_K, td, 32, 4, hidden, ff, n_tok, seed=hidden + ff + n_tok)
 
 
-def test_moe_staged_matches_vector_path(engine):
+def test_moe_staged_matches_vector_path(fresh_engine):
     """The staged MFMA kernels and the vector-ALU kernels agree on the same call."""
     import torch
+    engine = fresh_engine
     n_exp, k, hidden, ff, n_tok = 64, 8, 2048, 768, 4
     g, _ = weights(le.Q4_K, n_exp * ff, hidden, 501)
     u, _ = weights(le.Q4_K, n_exp * ff, hidden, 502)

@@ -241,3 +241,44 @@ def test_error_codes(engine):
     with pytest.raises(le.LeError) as e:
         engine.mv(le.Q4_K, w, x, y, 0, 1024)
     assert e.value.code == -3
+
+
+def test_options_validated(fresh_engine):
+    """Every documented launch-policy knob is accepted with a valid value; bad names and values
+    are refused with LE_ERR_ARG and leave the context usable."""
+    good = {"mv_block": 512, "mv_blocks_per_cu": 1, "mv_shape": 0, "mq": 1, "ms": 1, "mq_waves": 4, "mq_steps": 2,
+            "mq_blocks_per_cu": 2, "ms_p": 2, "ms_p6": 2, "ms_piq": 2, "mq6": 1, "mqiq": 1, "gm_min_m": 4,
+            "gm_tile": 0, "gm_ksplit": 0, "gm_pc": 1, "moe_mfma": 1, "moe_fused": 1, "moe_fused_min_tok": 3,
+            "moe_fast": 1}
+    engine = fresh_engine
+    for k, v in good.items():
+        engine.set_option(k, v)
+    for k, v in [("no_such_option", 1), ("gm_tile", 33), ("gm_ksplit", 3), ("ms_p6", 4), ("ms_piq", 3)]:
+        with pytest.raises(le.LeError) as e:
+            engine.set_option(k, v)
+        assert e.value.code == -1, (k, v)
+    # still usable
+    import torch
+    q, _ = weights(le.Q4_K, 64, 512, seed=3)
+    x = acts(512, 4)
+    y = torch.empty(64, dtype=torch.float32, device="cuda")
+    engine.mv(le.Q4_K, dev(q), dev(x), y, 64, 512)
+    sync()
+    check_close(y.cpu().numpy(), oracle.matvec(le.Q4_K, q, 64, 512, x), absmag(le.Q4_K, q, 64, 512, x)[0])
+
+
+@pytest.mark.parametrize("name", ["Q4_K", "Q6_K", "IQ2_XXS", "IQ3_XXS"])
+@pytest.mark.parametrize("opts", [{"mq_waves": 8}, {"mq_waves": 2}, {"ms": 0}, {"mq": 0}])
+def test_matvec_launch_options(fresh_engine, name, opts):
+    """Every staged-kernel shape the options can select exists and gives the same answer."""
+    import torch
+    engine = fresh_engine
+    ty, rows, cols = le.TYPES[name], 300, 4096
+    for k, v in opts.items():
+        engine.set_option(k, v)
+    q, _ = weights(ty, rows, cols, seed=77 + ty)
+    x = acts(cols, 78)
+    y = torch.empty(rows, dtype=torch.float32, device="cuda")
+    engine.mv(ty, dev(q), dev(x), y, rows, cols)
+    sync()
+    check_close(y.cpu().numpy(), oracle.matvec(ty, q, rows, cols, x), absmag(ty, q, rows, cols, x)[0])
