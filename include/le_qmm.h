@@ -73,6 +73,7 @@ const char *le_last_error(const le_ctx *ctx);
  *   decode matvec, vector path:  "mv_block" threads per block (512, 1024), "mv_blocks_per_cu" grid
  *     cap, "mv_shape" rows x super-blocks in flight per lane (0 auto, 1: 1x2, 2: 2x1, 3: 2x2, 4: 4x1)
  *   decode matvec, matrix cores: "mq" (0/1), "ms" staged variant (0/1), "mq_waves" (2, 4, 8),
+ *     "mq_waves_auto" (0/1: twice the waves when the row tiles do not fill the chip),
  *     "mq_steps", "mq_blocks_per_cu", super-blocks per row and step "ms_p" (Q4_K), "ms_p6" (Q6_K),
  *     "ms_piq" (IQ2_XXS, IQ3_XXS), and "mq6" / "mqiq" (0/1) for the Q6_K / IQ staged kernels
  *   GEMM: "gm_min_m" smallest M on the matrix cores, "gm_tile" (0 auto, 11, 12, 21, 22),

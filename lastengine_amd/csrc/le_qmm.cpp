@@ -64,6 +64,7 @@ struct le_ctx {
     int mv_blocks_per_cu = 1; /* grid cap = CUs * this */
     int mv_shape = 0;        /* (rows, steps) per lane: 0 auto, 1 (1,2), 2 (2,1), 3 (2,2), 4 (4,1) */
     int mq = 1;              /* decode matvec on MFMA where available */
+    int mq_waves_auto = 1;   /* double mq_waves for grids smaller than the chip */
     int mq_waves = 4, mq_steps = 2, mq_blocks_per_cu = 2;
     int ms = 1, ms_p = 2;    /* staged MFMA variant and its super-blocks per row and step */
     int mq6 = 1, ms_p6 = 2;  /* Q6_K decode matvec on the staged MFMA kernels, super-blocks per step */
@@ -156,8 +157,10 @@ int pick_g(int nsb) {
 /* MFMA decode matvec (Q4_K, Q6_K): one block of mq_waves waves per 16-row tile at a time. */
 int mq_launch(le_ctx *c, int ty, const void *const *ptrs, const void *w, const float *x, long long x_slot, float *y,
               long long y_slot, int rows, int cols, int slots, hipStream_t st) {
-    const int nsb = cols / 256, NW = c->mq_waves, U = c->mq_steps;
     const long long ntile = (rows + 15) / 16;
+    const int nsb = cols / 256, U = c->mq_steps;
+    /* when the row tiles alone leave CUs idle, split K over twice the waves (shorter chains) */
+    const int NW = c->mq_waves_auto && ntile * slots <= c->cus && c->mq_waves < 8 ? 2 * c->mq_waves : c->mq_waves;
     long long gx = ntile, cap = (long long)c->cus * c->mq_blocks_per_cu;
     if (gx > cap) {
         const long long it = (gx + cap - 1) / cap;
@@ -338,6 +341,8 @@ int le_set_option(le_ctx *c, const char *name, int value) {
     } else if (n == "mv_blocks_per_cu") {
         if (value < 1 || value > 64) return c->fail(LE_ERR_ARG, "mv_blocks_per_cu must be 1..64");
         c->mv_blocks_per_cu = value;
+    } else if (n == "mq_waves_auto") {
+        c->mq_waves_auto = value ? 1 : 0;
     } else if (n == "mq") {
         c->mq = value ? 1 : 0;
     } else if (n == "mqiq") {

@@ -247,7 +247,7 @@ def test_options_validated(fresh_engine):
     """Every documented launch-policy knob is accepted with a valid value; bad names and values
     are refused with LE_ERR_ARG and leave the context usable."""
     good = {"mv_block": 512, "mv_blocks_per_cu": 1, "mv_shape": 0, "mq": 1, "ms": 1, "mq_waves": 4, "mq_steps": 2,
-            "mq_blocks_per_cu": 2, "ms_p": 2, "ms_p6": 2, "ms_piq": 2, "mq6": 1, "mqiq": 1, "gm_min_m": 4,
+            "mq_blocks_per_cu": 2, "mq_waves_auto": 1, "ms_p": 2, "ms_p6": 2, "ms_piq": 2, "mq6": 1, "mqiq": 1, "gm_min_m": 4,
             "gm_tile": 0, "gm_ksplit": 0, "gm_pc": 1, "moe_mfma": 1, "moe_fused": 1, "moe_fused_min_tok": 3,
             "moe_fast": 1}
     engine = fresh_engine
