@@ -69,7 +69,7 @@ void le_destroy(le_ctx *ctx);
 const char *le_last_error(const le_ctx *ctx);
 /* Launch-policy knobs (the counterpart of the reference's LE_MMQ* / LE_TMAX env switches,
  * src/gpu/dense.rs:182-192). Defaults are the measured best on MI355X; results do not depend on
- * them beyond fp32 summation order. Unknown names or values give LE_ERR_ARG.
+ * them beyond fp32 summation order, except "gm_split". Unknown names or values give LE_ERR_ARG.
  *   decode matvec, vector path:  "mv_block" threads per block (512, 1024), "mv_blocks_per_cu" grid
  *     cap, "mv_shape" rows x super-blocks in flight per lane (0 auto, 1: 1x2, 2: 2x1, 3: 2x2, 4: 4x1)
  *   decode matvec, matrix cores: "mq" (0/1), "ms" staged variant (0/1), "mq_waves" (2, 4, 8),
@@ -77,7 +77,9 @@ const char *le_last_error(const le_ctx *ctx);
  *     "mq_steps", "mq_blocks_per_cu", super-blocks per row and step "ms_p" (Q4_K), "ms_p6" (Q6_K),
  *     "ms_piq" (IQ2_XXS, IQ3_XXS), and "mq6" / "mqiq" (0/1) for the Q6_K / IQ staged kernels
  *   GEMM: "gm_min_m" smallest M on the matrix cores, "gm_tile" (0 auto, 11, 12, 21, 22),
- *     "gm_ksplit" K slices (0 auto, 1, 2, 4, 8), "gm_pc" producer/consumer waves (0/1)
+ *     "gm_ksplit" K slices (0 auto, 1, 2, 4, 8), "gm_pc" producer/consumer waves (0/1),
+ *     "gm_split" activation precision on the matrix cores: 0 (default) rounds each value to fp16
+ *     (relative error 2^-11 per value), 1 carries a second fp16 half (about 2^-22 per value)
  *   MoE: "moe_mfma" staged kernels (0/1), "moe_fused" single launch (0/1), "moe_fused_min_tok",
  *     "moe_fast" decode-shaped vector kernels (0/1) */
 int le_set_option(le_ctx *ctx, const char *name, int value);

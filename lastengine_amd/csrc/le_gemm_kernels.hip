@@ -42,6 +42,7 @@ struct GmArgs {
     int rows, cols, m;
     int ksplit; /* K slices (blockIdx.y); with more than one, the slices add into y, which the
                    pre-pass clears */
+    int split;  /* 1: activations as fp16 high and low halves; 0: the high half only */
 };
 
 
@@ -118,7 +119,7 @@ extern "C" __global__ void __launch_bounds__(256) le_gm_xprep(GmArgs a, u8 *ws) 
     gm_split2(v.y, v.w, h1, l1);
     _Float16 *Xh = (_Float16 *)ws, *Xl = Xh + (size_t)a.m * K;
     *(LE_GLOBAL uint2 *)(Xh + e) = make_uint2(h0, h1);
-    *(LE_GLOBAL uint2 *)(Xl + e) = make_uint2(l0, l1);
+    if (a.split) *(LE_GLOBAL uint2 *)(Xl + e) = make_uint2(l0, l1);
     const float sum = group_sum<8>((v.x + v.y) + (v.z + v.w));
     const int si = __builtin_bit_cast(int, sum);
     /* the lane reads run on the whole wave, outside the single-lane store below (a reduction
@@ -150,7 +151,7 @@ struct GmLds {
 /* PC = producer/consumer blocks of 8 waves: waves 0-3 only compute (MFMAs, epilogues), waves
  * 4-7 only load and stage the next step, so the staging work overlaps the MFMAs on other waves
  * instead of alternating with them; otherwise 4 waves do both. */
-template <int TM, int TN, bool PC>
+template <int TM, int TN, bool PC, bool SPLIT = true>
 __device__ __forceinline__ void gm_q4k_body(const GmArgs &a, const u8 *ws) {
     using L = GmLds<TM, TN>;
     constexpr int BM = L::BM, BN = L::BN;
@@ -195,6 +196,7 @@ __device__ __forceinline__ void gm_q4k_body(const GmArgs &a, const u8 *ws) {
 #pragma unroll
         for (int i = 0; i < NXC; i++) {
             const int c = st + 256 * i, t = min(mb + (c >> 5), M - 1);
+            if (!SPLIT && ((c >> 4) & 1)) continue; /* one fp16 plane: the low halves are not read */
             const _Float16 *src = ((c >> 4) & 1 ? Xl : Xh) + (size_t)t * K + 256 * sb + 128 * h + 8 * (c & 15);
             xa[i] = ldg16c((const u8 *)src);
         }
@@ -238,6 +240,7 @@ __device__ __forceinline__ void gm_q4k_body(const GmArgs &a, const u8 *ws) {
 #pragma unroll
         for (int i = 0; i < NXC; i++) {
             const int c = st + 256 * i;
+            if (!SPLIT && ((c >> 4) & 1)) continue;
             *(uint4 *)(B + ((c >> 4) & 1 ? L::AL_OFF : L::AH_OFF) + ((c >> 5) * GM_AS + 8 * (c & 15)) * 2) = xa[i];
         }
         if (h == 0 && st < 2 * BM) Sx[((sb & 1) * BM + (st >> 1)) * 2 + (st & 1)] = xs;
@@ -299,7 +302,7 @@ __device__ __forceinline__ void gm_q4k_body(const GmArgs &a, const u8 *ws) {
 #pragma unroll
                         for (int i = 0; i < TM; i++) {
                             ah[i] = __builtin_bit_cast(le_v8h, *(const uint4 *)(Ah + (32 * i + r32) * GM_AS + ko));
-                            al[i] = __builtin_bit_cast(le_v8h, *(const uint4 *)(Al + (32 * i + r32) * GM_AS + ko));
+                            if constexpr (SPLIT) al[i] = __builtin_bit_cast(le_v8h, *(const uint4 *)(Al + (32 * i + r32) * GM_AS + ko));
                         }
                         /* the super-block's first MFMA starts from zero: no clearing pass */
                         const bool first = h == 0 && gl == 0 && c == 0 && half == 0;
@@ -309,11 +312,13 @@ __device__ __forceinline__ void gm_q4k_body(const GmArgs &a, const u8 *ws) {
                             for (int k = 0; k < TN; k++)
                                 d1[i][k] = __builtin_amdgcn_mfma_f32_32x32x16_f16(ah[i], half ? bhi[k] : blo[k],
                                                                                   first ? (v16f){} : d1[i][k], 0, 0, 0);
+                        if constexpr (SPLIT) {
 #pragma unroll
-                        for (int i = 0; i < TM; i++)
+                            for (int i = 0; i < TM; i++)
 #pragma unroll
-                            for (int k = 0; k < TN; k++)
-                                d1[i][k] = __builtin_amdgcn_mfma_f32_32x32x16_f16(al[i], half ? bhi[k] : blo[k], d1[i][k], 0, 0, 0);
+                                for (int k = 0; k < TN; k++)
+                                    d1[i][k] = __builtin_amdgcn_mfma_f32_32x32x16_f16(al[i], half ? bhi[k] : blo[k], d1[i][k], 0, 0, 0);
+                        }
                     }
                 }
                 /* the next step's staging and the loads two steps ahead run under this step's MFMAs */
@@ -386,9 +391,16 @@ __device__ __forceinline__ void gm_q4k_body(const GmArgs &a, const u8 *ws) {
 #define LE_GM(TM, TN)                                                                                      \
     extern "C" __global__ void __launch_bounds__(256) le_gm_12_m##TM##_n##TN(GmArgs a, const u8 *ws) {    \
         gm_q4k_body<TM, TN, false>(a, ws);                                                                 \
-    }                                                                                                      \
-    extern "C" __global__ void __launch_bounds__(512) le_gm_12_m##TM##_n##TN##_pc(GmArgs a, const u8 *ws) { \
-        gm_q4k_body<TM, TN, true>(a, ws);                                                                  \
+    }
+/* producer/consumer forms, with both activation halves (_pc) or the high half only (_pc1); the
+ * 64 x 256 tile has none, as it does not fit the registers */
+#define LE_GM_PC(TM, TN)                                                                                     \
+    extern "C" __global__ void __launch_bounds__(512) le_gm_12_m##TM##_n##TN##_pc(GmArgs a, const u8 *ws) {  \
+        gm_q4k_body<TM, TN, true>(a, ws);                                                                    \
+    }                                                                                                        \
+    extern "C" __global__ void __launch_bounds__(512) le_gm_12_m##TM##_n##TN##_pc1(GmArgs a, const u8 *ws) { \
+        gm_q4k_body<TM, TN, true, false>(a, ws);                                                             \
     }
 
 LE_GM(1, 1) LE_GM(1, 2) LE_GM(2, 1) LE_GM(2, 2)
+LE_GM_PC(1, 1) LE_GM_PC(1, 2) LE_GM_PC(2, 1)

@@ -78,6 +78,7 @@ struct le_ctx {
     int gm_tile = 0;         /* MFMA GEMM tile: 0 auto, else 10*TM + TN (TM, TN in 1..2) */
     int gm_ksplit = 0;       /* MFMA GEMM K slices: 0 auto, else 1, 2, 4, 8 */
     int gm_pc = 1;           /* MFMA GEMM with producer/consumer waves */
+    int gm_split = 0;        /* 1: activations as two fp16 halves (22 bits); 0: one fp16 value (11 bits) */
     std::vector<hipModule_t> mods;
     std::map<std::string, hipFunction_t> fns;
     std::string err;
@@ -355,6 +356,9 @@ int le_set_option(le_ctx *c, const char *name, int value) {
     } else if (n == "ms_p6") {
         if (value != 1 && value != 2) return c->fail(LE_ERR_ARG, "ms_p6 must be 1 or 2");
         c->ms_p6 = value;
+    } else if (n == "gm_split") {
+        if (value != 0 && value != 1) return c->fail(LE_ERR_ARG, "gm_split must be 0 or 1");
+        c->gm_split = value;
     } else if (n == "gm_pc") {
         c->gm_pc = value ? 1 : 0;
     } else if (n == "gm_ksplit") {
@@ -550,8 +554,8 @@ int le_gemm(le_ctx *c, int ty, const void *w, const float *x, int m, float *y, i
             const void *w;
             const float *x;
             float *y;
-            int rows, cols, m, ksplit;
-        } a{w, x, y, rows, cols, m, ks};
+            int rows, cols, m, ksplit, split;
+        } a{w, x, y, rows, cols, m, ks, pc ? c->gm_split : 1}; /* only the producer/consumer kernel has a one-half form */
         /* pass 1: activation halves and sub-block sums into the workspace, one wave per
          * (token, super-block); clears y when K is split */
         void *pargs[] = {&a, &ws};
@@ -565,7 +569,7 @@ int le_gemm(le_ctx *c, int ty, const void *w, const float *x, int m, float *y, i
         const size_t lds = 2 * ((size_t)BN * 128 + (size_t)BM * 544) + (size_t)BM * 64;
         if (grid > 0x7FFFFFFFLL) return c->fail(LE_ERR_SHAPE, "GEMM grid too large");
         char name[48];
-        snprintf(name, sizeof name, "le_gm_12_m%d_n%d%s", TM, TN, pc ? "_pc" : "");
+        snprintf(name, sizeof name, "le_gm_12_m%d_n%d%s", TM, TN, pc ? (a.split ? "_pc" : "_pc1") : "");
         void *args[] = {&a, &ws};
         return c->launch(name, dim3((unsigned)grid, (unsigned)ks), pc ? 512 : 256, lds, (hipStream_t)stream, args);
     }

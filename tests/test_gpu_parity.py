@@ -243,17 +243,40 @@ def test_error_codes(engine):
     assert e.value.code == -3
 
 
+@pytest.mark.parametrize("m", [16, 128])
+def test_gemm_activation_split(fresh_engine, m):
+    """gm_split=1 carries each activation as two fp16 halves: the result then agrees with the fp64
+    oracle to about 2^-22 of sum|w*x| (fp32 accumulation), well inside the single-half bound of
+    2^-11 that the default meets."""
+    import torch
+    engine = fresh_engine
+    ty, rows, cols = le.Q4_K, 512, 2048
+    q, _ = weights(ty, rows, cols, seed=23)
+    xs = np.stack([acts(cols, 5000 + t) for t in range(m)])
+    want = oracle.matmat(ty, q, rows, cols, xs)
+    mag = absmag(ty, q, rows, cols, xs)
+    errs = {}
+    for split in (0, 1):
+        engine.set_option("gm_split", split)
+        y = torch.empty(m, rows, dtype=torch.float32, device="cuda")
+        engine.gemm(ty, dev(q), dev(xs), m, y, rows, cols)
+        sync()
+        errs[split] = float(np.max(np.abs(y.cpu().numpy() - want) / mag))
+    assert errs[0] <= 2.0 ** -11, errs
+    assert errs[1] <= 1e-5, errs
+
+
 def test_options_validated(fresh_engine):
     """Every documented launch-policy knob is accepted with a valid value; bad names and values
     are refused with LE_ERR_ARG and leave the context usable."""
     good = {"mv_block": 512, "mv_blocks_per_cu": 1, "mv_shape": 0, "mq": 1, "ms": 1, "mq_waves": 4, "mq_steps": 2,
             "mq_blocks_per_cu": 2, "mq_waves_auto": 1, "ms_p": 2, "ms_p6": 2, "ms_piq": 2, "mq6": 1, "mqiq": 1, "gm_min_m": 4,
-            "gm_tile": 0, "gm_ksplit": 0, "gm_pc": 1, "moe_mfma": 1, "moe_fused": 1, "moe_fused_min_tok": 3,
+            "gm_tile": 0, "gm_ksplit": 0, "gm_pc": 1, "gm_split": 0, "moe_mfma": 1, "moe_fused": 1, "moe_fused_min_tok": 3,
             "moe_fast": 1}
     engine = fresh_engine
     for k, v in good.items():
         engine.set_option(k, v)
-    for k, v in [("no_such_option", 1), ("gm_tile", 33), ("gm_ksplit", 3), ("ms_p6", 4), ("ms_piq", 3)]:
+    for k, v in [("no_such_option", 1), ("gm_tile", 33), ("gm_ksplit", 3), ("gm_split", 2), ("ms_p6", 4), ("ms_piq", 3)]:
         with pytest.raises(le.LeError) as e:
             engine.set_option(k, v)
         assert e.value.code == -1, (k, v)
