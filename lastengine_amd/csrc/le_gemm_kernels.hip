@@ -98,13 +98,15 @@ __device__ __forceinline__ void gm_q4k_frag(uint2 w, uint4 k, le_v8h &lo, le_v8h
 
 #define GM_WS 72  /* LDS bytes per row of a half super-block's quants: 64 + 8 */
 #define GM_AS 136 /* fp16 per activation row of a half super-block: 128 + 8 */
+#define GM_PD 2 /* producer register sets (steps of loads in flight + 1), one-half form */
 
 /* Activation pre-pass: X fp32 [M][K] -> workspace planes Xh, Xl fp16 [M][K] (x = xh + xl, order
  * 0,2,1,3 within each four) and per (token, super-block) a 32-byte record of the eight sub-block
  * sums S_j as fp16 high halves then low halves. One wave per (token, super-block). */
 extern "C" __global__ void __launch_bounds__(256) le_gm_xprep(GmArgs a, u8 *ws) {
     const int K = a.cols, nsb = K >> 8;
-    if (a.ksplit > 1) { /* the K slices of the main pass add into y */
+    if (a.ksplit > 1) { /* the K slices of the main pass add into y; the host sizes the grid to
+                           cover y in a few trips */
         const size_t ny = (size_t)a.m * a.rows;
         for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < ny; i += (size_t)gridDim.x * blockDim.x) a.y[i] = 0.f;
     }
@@ -138,13 +140,14 @@ extern "C" __global__ void __launch_bounds__(256) le_gm_xprep(GmArgs a, u8 *ws) 
     }
 }
 
-template <int TM, int TN>
+template <int TM, int TN, bool SPLIT>
 struct GmLds {
     static constexpr int BM = 32 * TM, BN = 128 * TN;
     /* one pipeline buffer: the half super-block's quants, fragment constants of its two groups,
-     * offsets m_j, (d, dmin), activation halves */
+     * offsets m_j, (d, dmin), activation high halves, low halves (SPLIT only) */
     static constexpr int W_OFF = 0, K_OFF = BN * GM_WS, M_OFF = K_OFF + BN * 32, D_OFF = M_OFF + BN * 16,
-                         AH_OFF = D_OFF + BN * 8, AL_OFF = AH_OFF + BM * GM_AS * 2, BUF = AL_OFF + BM * GM_AS * 2;
+                         AH_OFF = D_OFF + BN * 8, AL_OFF = AH_OFF + BM * GM_AS * 2,
+                         BUF = AL_OFF + (SPLIT ? BM * GM_AS * 2 : 0);
     static constexpr int S_OFF = 2 * BUF, BYTES = S_OFF + 2 * BM * 32; /* + sum records [2][BM][32 B] */
 };
 
@@ -153,9 +156,9 @@ struct GmLds {
  * instead of alternating with them; otherwise 4 waves do both. */
 template <int TM, int TN, bool PC, bool SPLIT = true>
 __device__ __forceinline__ void gm_q4k_body(const GmArgs &a, const u8 *ws) {
-    using L = GmLds<TM, TN>;
+    using L = GmLds<TM, TN, SPLIT>;
     constexpr int BM = L::BM, BN = L::BN;
-    constexpr int NQC = BN * 4 / 256, NHC = BN / 256 > 0 ? BN / 256 : 1, NXC = BM * 32 / 256;
+    constexpr int NQC = BN * 4 / 256, NHC = BN / 256 > 0 ? BN / 256 : 1, NXC = BM * (SPLIT ? 32 : 16) / 256;
     typedef float v16f __attribute__((ext_vector_type(16)));
     extern __shared__ uint4 smem[];
     u8 *lds = (u8 *)smem;
@@ -180,36 +183,43 @@ __device__ __forceinline__ void gm_q4k_body(const GmArgs &a, const u8 *ws) {
     /* staging of step s (super-block s/2, half s&1), all copies of 16 bytes:
      *   header of row tid (+256 i), decoded by this thread;
      *   quant chunk c = tid + 256 i: row c/4, 16-byte column c%4 of the half's 64 bytes;
-     *   activation chunk c = tid + 256 i: token c/32, plane (c/16)&1, 8-value column c%16;
-     *   sum record chunk tid < 2*BM: token tid/2, half tid&1 (once per super-block) */
-    uint4 wh[NHC] = {}, wq[NQC] = {}, xa[NXC] = {}, xs = make_uint4(0u, 0u, 0u, 0u);
-    auto issue = [&](int s) {
-        const int sb = s >> 1, h = s & 1;
+     *   activation chunk c = tid + 256 i: token c/32, plane (c/16)&1, 8-value column c%16
+     *   (two halves), or token c/16, column c%16 (high half only);
+     *   sum record chunk tid < 2*BM: token tid/2, half tid&1 (staged once per super-block) */
+    struct Set {
+        uint4 wh[NHC], wq[NQC], xa[NXC], xs;
+    };
+    /* every load is unconditional and wave-uniform in count, so the compiler's wait before
+     * staging step s+1 counts only that step's loads and the later steps stay in flight; a step
+     * past the slice (prefetch tail) re-reads the last one */
+    auto issue = [&](int s_, Set &R) {
+        const int s = min(s_, nstep - 1), sb = s >> 1, h = s & 1;
         const u8 *w0 = a.w + (size_t)sb * 144;
 #pragma unroll
-        for (int i = 0; i < NHC; i++) wh[i] = ldg16(w0 + (size_t)min(nb + st + 256 * i, a.rows - 1) * rb);
+        for (int i = 0; i < NHC; i++) R.wh[i] = ldg16(w0 + (size_t)min(nb + st + 256 * i, a.rows - 1) * rb);
 #pragma unroll
         for (int i = 0; i < NQC; i++) {
             const int c = st + 256 * i, row = c >> 2;
-            wq[i] = ldg16(w0 + (size_t)min(nb + row, a.rows - 1) * rb + 16 + 64 * h + 16 * (c & 3));
+            R.wq[i] = ldg16(w0 + (size_t)min(nb + row, a.rows - 1) * rb + 16 + 64 * h + 16 * (c & 3));
         }
 #pragma unroll
         for (int i = 0; i < NXC; i++) {
-            const int c = st + 256 * i, t = min(mb + (c >> 5), M - 1);
-            if (!SPLIT && ((c >> 4) & 1)) continue; /* one fp16 plane: the low halves are not read */
-            const _Float16 *src = ((c >> 4) & 1 ? Xl : Xh) + (size_t)t * K + 256 * sb + 128 * h + 8 * (c & 15);
-            xa[i] = ldg16c((const u8 *)src);
+            const int c = st + 256 * i;
+            /* SPLIT: token c/32, plane (c/16)&1; otherwise token c/16 of the high plane */
+            const int t = min(mb + (SPLIT ? c >> 5 : c >> 4), M - 1);
+            const _Float16 *src = (SPLIT && ((c >> 4) & 1) ? Xl : Xh) + (size_t)t * K + 256 * sb + 128 * h + 8 * (c & 15);
+            R.xa[i] = ldg16c((const u8 *)src);
         }
-        if (h == 0 && st < 2 * BM) xs = ldg16c((const u8 *)(Xs + 2 * ((size_t)min(mb + (st >> 1), M - 1) * nsb + sb) + (st & 1)));
+        R.xs = ldg16c((const u8 *)(Xs + 2 * ((size_t)min(mb + (st >> 1), M - 1) * nsb + sb) + (st & 1)));
     };
-    auto stage = [&](int s) {
+    auto stage = [&](int s, const Set &R) {
         const int sb = s >> 1, h = s & 1;
         u8 *B = lds + (s & 1) * L::BUF;
 #pragma unroll
         for (int i = 0; i < NHC; i++) {
             const int row = st + 256 * i;
             if (row >= BN) break;
-            const u32 sy = wh[i].y, sz = wh[i].z, sw = wh[i].w;
+            const u32 sy = R.wh[i].y, sz = R.wh[i].z, sw = R.wh[i].w;
             const u32 scw = h ? ((sw & 0x0F0F0F0Fu) | ((sy >> 2) & 0x30303030u)) : (sy & 0x3F3F3F3Fu);
             uint4 *kc = (uint4 *)(B + L::K_OFF) + 2 * row;
 #pragma unroll
@@ -228,22 +238,24 @@ __device__ __forceinline__ void gm_q4k_body(const GmArgs &a, const u8 *ws) {
                 mw[q] = as_u32(v);
             }
             ((uint4 *)(B + L::M_OFF))[row] = make_uint4(mw[0], mw[1], mw[2], mw[3]);
-            ((float2 *)(B + L::D_OFF))[row] = make_float2(h2f(wh[i].x & 0xFFFFu), h2f(wh[i].x >> 16));
+            ((float2 *)(B + L::D_OFF))[row] = make_float2(h2f(R.wh[i].x & 0xFFFFu), h2f(R.wh[i].x >> 16));
         }
 #pragma unroll
         for (int i = 0; i < NQC; i++) {
             const int c = st + 256 * i;
             uint2 *d = (uint2 *)(B + L::W_OFF + (c >> 2) * GM_WS + 16 * (c & 3));
-            d[0] = make_uint2(wq[i].x, wq[i].y);
-            d[1] = make_uint2(wq[i].z, wq[i].w);
+            d[0] = make_uint2(R.wq[i].x, R.wq[i].y);
+            d[1] = make_uint2(R.wq[i].z, R.wq[i].w);
         }
 #pragma unroll
         for (int i = 0; i < NXC; i++) {
             const int c = st + 256 * i;
-            if (!SPLIT && ((c >> 4) & 1)) continue;
-            *(uint4 *)(B + ((c >> 4) & 1 ? L::AL_OFF : L::AH_OFF) + ((c >> 5) * GM_AS + 8 * (c & 15)) * 2) = xa[i];
+            if constexpr (SPLIT)
+                *(uint4 *)(B + ((c >> 4) & 1 ? L::AL_OFF : L::AH_OFF) + ((c >> 5) * GM_AS + 8 * (c & 15)) * 2) = R.xa[i];
+            else
+                *(uint4 *)(B + L::AH_OFF + ((c >> 4) * GM_AS + 8 * (c & 15)) * 2) = R.xa[i];
         }
-        if (h == 0 && st < 2 * BM) Sx[((sb & 1) * BM + (st >> 1)) * 2 + (st & 1)] = xs;
+        if (h == 0 && st < 2 * BM) Sx[((sb & 1) * BM + (st >> 1)) * 2 + (st & 1)] = R.xs;
     };
 
     v16f acc[TM][TN], d1[TM][TN];
@@ -261,10 +273,40 @@ __device__ __forceinline__ void gm_q4k_body(const GmArgs &a, const u8 *ws) {
     unsigned long long tr[8] = {};
 #endif
     GM_T(t_start);
-    if (!PC || producer) {
-        issue(2 * sb0);
-        stage(2 * sb0);
-        issue(2 * sb0 + 1);
+    if (producer) {
+        constexpr int PD = SPLIT ? 2 : GM_PD; /* the two-half form has no registers to spare */
+        /* a ring of PD register sets: while the consumers work on step s, the loads of steps
+         * s+2 .. s+PD are in flight; the loop is unrolled by PD so the sets are registers */
+        Set R[PD];
+        const int s0 = 2 * sb0;
+        issue(s0, R[0]);
+        stage(s0, R[0]);
+#pragma unroll
+        for (int u = 1; u < PD; u++) issue(s0 + u, R[u]);
+        /* whole groups of PD steps without early exits (an exit merging into the loop would
+         * make the compiler wait for every load), then the remaining steps */
+        int s = s0;
+        for (; s + PD <= nstep; s += PD) {
+#pragma unroll
+            for (int u = 0; u < PD; u++) {
+                gm_barrier(); /* step s+u is staged; the consumers are done with step s+u-1's buffer */
+                if (s + u + 1 < nstep) stage(s + u + 1, R[(u + 1) % PD]);
+                issue(s + u + PD, R[u]);
+            }
+        }
+#pragma unroll
+        for (int u = 0; u < PD - 1; u++) {
+            if (s + u >= nstep) break;
+            gm_barrier();
+            if (s + u + 1 < nstep) stage(s + u + 1, R[(u + 1) % PD]);
+        }
+        return;
+    }
+    Set R0;
+    if (!PC) {
+        issue(2 * sb0, R0);
+        stage(2 * sb0, R0);
+        issue(2 * sb0 + 1, R0);
     }
     for (int sb = sb0; sb < sb1; sb++) {
 #pragma unroll
@@ -274,11 +316,6 @@ __device__ __forceinline__ void gm_q4k_body(const GmArgs &a, const u8 *ws) {
             gm_barrier(); /* step s is staged; every wave is done with step s-1's buffer */
             GM_T(tb);
             GM_ADD(0, ta, tb);
-            if (producer) { /* the next step's staging and the loads two steps ahead */
-                if (s + 1 < nstep) stage(s + 1);
-                if (s + 2 < nstep) issue(s + 2);
-                continue;
-            }
             const u8 *B = lds + h * L::BUF; /* s & 1 == h */
             const _Float16 *Ah = (const _Float16 *)(B + L::AH_OFF), *Al = (const _Float16 *)(B + L::AL_OFF);
 #pragma unroll
@@ -323,14 +360,13 @@ __device__ __forceinline__ void gm_q4k_body(const GmArgs &a, const u8 *ws) {
                 }
                 /* the next step's staging and the loads two steps ahead run under this step's MFMAs */
                 if (!PC && gl == 0) {
-                    if (s + 1 < nstep) stage(s + 1);
-                    if (s + 2 < nstep) issue(s + 2);
+                    if (s + 1 < nstep) stage(s + 1, R0);
+                    if (s + 2 < nstep) issue(s + 2, R0);
                 }
             }
             GM_T(tc);
             GM_ADD(1, tb, tc);
         }
-        if (producer) continue;
         GM_T(td0);
         /* super-block epilogue: Y += d * D1 - dmin * D2, D2 = sum_j m_j S_j by one more MFMA per
          * tile (K slice 0: high halves of S_0..7, slice 1: low halves, both against m); all D2
@@ -362,13 +398,7 @@ __device__ __forceinline__ void gm_q4k_body(const GmArgs &a, const u8 *ws) {
         GM_T(td);
         GM_ADD(2, td0, td);
     }
-#if defined(LE_TRACE)
     GM_T(t_end);
-    tr[5] = t_end - t_start;
-    if (tid == 0)
-        for (int i = 0; i < 8; i++) le_gm_trace[blockIdx.x * 8 + i] = tr[i];
-#endif
-    if (producer) return;
     /* D lane l element e: token 8*(e/4) + 4*(l/32) + e%4 of the tile, weight row l%32 */
 #pragma unroll
     for (int i = 0; i < TM; i++)
@@ -386,6 +416,15 @@ __device__ __forceinline__ void gm_q4k_body(const GmArgs &a, const u8 *ws) {
                 }
             }
         }
+#if defined(LE_TRACE)
+    GM_T(t_st);
+    tr[3] = t_st - t_end;
+    tr[5] = t_st - t_start;
+    tr[6] = t_start;
+    tr[7] = t_st;
+    if (tid == 0)
+        for (int i = 0; i < 8; i++) le_gm_trace[((size_t)blockIdx.y * gridDim.x + blockIdx.x) * 8 + i] = tr[i];
+#endif
 }
 
 #define LE_GM(TM, TN)                                                                                      \

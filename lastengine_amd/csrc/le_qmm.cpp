@@ -73,7 +73,7 @@ struct le_ctx {
     int moe_mfma = 1;        /* decode-shaped MoE on the staged MFMA kernels where the types allow */
     int moe_fused = 1;       /* ... in one launch with a device-wide barrier where the grid fits */
     int moe_fused_min_tok = 3; /* ... from this many tokens on (below, two launches are faster) */
-    std::map<std::string, int> occ; /* resident blocks per CU of the barrier kernels */
+    std::map<std::string, int> occ; /* resident blocks per CU, by kernel name and LDS bytes */
     int gm_min_m = 4;        /* le_gemm uses the MFMA kernels from this many tokens on */
     int gm_tile = 0;         /* MFMA GEMM tile: 0 auto, else 10*TM + TN (TM, TN in 1..2) */
     int gm_ksplit = 0;       /* MFMA GEMM K slices: 0 auto, else 1, 2, 4, 8 */
@@ -110,6 +110,20 @@ struct le_ctx {
             }
         }
         return nullptr;
+    }
+    /* resident blocks per CU of kernel `name` at this block size and dynamic LDS (0 if unknown) */
+    int blocks_per_cu(const std::string &name, int block, size_t lds) {
+        const std::string key = name + "/" + std::to_string(block) + "/" + std::to_string(lds);
+        auto it = occ.find(key);
+        if (it != occ.end()) return it->second;
+        hipFunction_t f = fn(name);
+        int per_cu = 0;
+        if (!f || hipModuleOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, f, block, lds) != hipSuccess) {
+            (void)hipGetLastError();
+            per_cu = 0;
+        }
+        occ[key] = per_cu;
+        return per_cu;
     }
     int launch(const std::string &name, dim3 grid, int block, size_t lds, hipStream_t st, void **args) {
         hipFunction_t f = fn(name);
@@ -466,18 +480,7 @@ int le_moe_layer(le_ctx *c, int ty_gate, int ty_up, int ty_down, const void *gat
         const size_t lds = lds1 > lds2 ? lds1 : lds2;
         snprintf(name, sizeof name, "le_moe_fus_12_%d_p%d", ty_down, pd);
         hipFunction_t f = c->fn(name);
-        int per_cu = 0;
-        if (f) {
-            auto it = c->occ.find(name);
-            if (it != c->occ.end()) {
-                per_cu = it->second;
-            } else if (hipModuleOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, f, 512, lds) == hipSuccess) {
-                c->occ[name] = per_cu;
-            } else {
-                (void)hipGetLastError();
-                per_cu = 0;
-            }
-        }
+        const int per_cu = f ? c->blocks_per_cu(name, 512, lds) : 0;
         const long long resident = (long long)c->cus * per_cu, ntile = hidden / 16;
         const long long items = (long long)(ff / 32) * groups;
         if (f && resident >= ntile && ntile <= 1024) { /* 1024: the kernel's arrival flags */
@@ -528,26 +531,32 @@ int le_gemm(le_ctx *c, int ty, const void *w, const float *x, int m, float *y, i
         if (ws_bytes < le_gemm_workspace_size(ty, m, cols))
             return c->fail(LE_ERR_WORKSPACE, "workspace needs %zu bytes", le_gemm_workspace_size(ty, m, cols));
         if (!al16(x) || !al16(ws)) return c->fail(LE_ERR_ALIGN, "x and ws must be 16-byte aligned");
-        /* tiles: 32*TM tokens x 128*TN rows; K split into slices when the tiles alone would not
-         * fill the chip */
-        int TM = m > 32 ? 2 : 1, TN = 2;
+        /* tiles: 32*TM tokens x 128*TN rows: 32 x 256 up to 64 tokens, 64 x 128 above (the
+         * producer/consumer kernel of 64 x 256 tiles does not fit its registers) */
+        int TM = m > 64 ? 2 : 1, TN = m > 64 && c->gm_pc ? 1 : 2;
         if (c->gm_tile) {
             TM = c->gm_tile / 10;
             TN = c->gm_tile % 10;
-        } else if (c->gm_pc && TM == 2) {
-            TN = 1; /* the producer/consumer kernel of 64 x 256 tiles does not fit its registers */
-        } else if ((long long)((rows + 255) / 256) * ((m + 32 * TM - 1) / (32 * TM)) < c->cus) {
-            TN = 1; /* more, smaller row tiles when the grid would not fill the chip */
         }
         const bool pc = c->gm_pc && !(TM == 2 && TN == 2);
+        const int split = pc ? c->gm_split : 1; /* only the producer/consumer kernel has a one-half form */
         const int BM = 32 * TM, BN = 128 * TN, nsb = cols / 256;
         const long long nt = (rows + BN - 1) / BN, mt = (m + BM - 1) / BM;
         const long long grid = (nt + 7) / 8 * 8 * mt;
+        /* two pipeline buffers of BN*(72+32+16+8) + BM*136*2 bytes per activation half, plus
+         * [2][BM] 32-byte sum records */
+        const size_t lds = 2 * ((size_t)BN * 128 + (size_t)BM * 272 * (split ? 2 : 1)) + (size_t)BM * 64;
+        char name[48];
+        snprintf(name, sizeof name, "le_gm_12_m%d_n%d%s", TM, TN, pc ? (split ? "_pc" : "_pc1") : "");
+        const int nthr = pc ? 512 : 256;
+        /* K slices: the most that keep the grid within one block per CU (measured best on
+         * 14336 x 4096 for M = 4..512; more blocks, even resident ones, cost more in clears, atomics
+         * and shared CUs than the slices gain) */
         int ks = 1;
         if (c->gm_ksplit > 0) {
             ks = c->gm_ksplit;
         } else {
-            while (ks < 8 && nt * mt * ks < c->cus && nsb % (2 * ks) == 0) ks *= 2;
+            while (ks < 8 && nt * mt * 2 * ks <= c->cus && nsb % (2 * ks) == 0) ks *= 2;
         }
         if (nsb % ks) return c->fail(LE_ERR_SHAPE, "gm_ksplit=%d does not divide the %d super-blocks", ks, nsb);
         struct {
@@ -555,23 +564,24 @@ int le_gemm(le_ctx *c, int ty, const void *w, const float *x, int m, float *y, i
             const float *x;
             float *y;
             int rows, cols, m, ksplit, split;
-        } a{w, x, y, rows, cols, m, ks, pc ? c->gm_split : 1}; /* only the producer/consumer kernel has a one-half form */
+        } a{w, x, y, rows, cols, m, ks, split};
         /* pass 1: activation halves and sub-block sums into the workspace, one wave per
          * (token, super-block); clears y when K is split */
         void *pargs[] = {&a, &ws};
         const long long waves = (long long)m * (cols / 256);
         if (waves > 0x7FFFFFFFLL) return c->fail(LE_ERR_SHAPE, "GEMM activation size too large");
-        int rc = c->launch("le_gm_xprep", dim3((unsigned)((waves + 3) / 4)), 256, 0, (hipStream_t)stream, pargs);
+        long long pblocks = (waves + 3) / 4;
+        if (ks > 1) {
+            const long long yb = ((long long)m * rows + 1023) / 1024;
+            if (yb > pblocks) pblocks = yb < 8192 ? yb : 8192;
+        }
+        int rc = c->launch("le_gm_xprep", dim3((unsigned)pblocks), 256, 0, (hipStream_t)stream, pargs);
         if (rc) return rc;
         /* pass 2: the row tiles are padded to a multiple of 8 so that the token tiles of one row
          * tile share blockIdx % 8 (one XCD); blockIdx.y is the K slice */
-        /* two pipeline buffers of BN*(72+32+16+8) + BM*2*136*2 bytes, plus [2][BM] 32-byte sum records */
-        const size_t lds = 2 * ((size_t)BN * 128 + (size_t)BM * 544) + (size_t)BM * 64;
         if (grid > 0x7FFFFFFFLL) return c->fail(LE_ERR_SHAPE, "GEMM grid too large");
-        char name[48];
-        snprintf(name, sizeof name, "le_gm_12_m%d_n%d%s", TM, TN, pc ? (a.split ? "_pc" : "_pc1") : "");
         void *args[] = {&a, &ws};
-        return c->launch(name, dim3((unsigned)grid, (unsigned)ks), pc ? 512 : 256, lds, (hipStream_t)stream, args);
+        return c->launch(name, dim3((unsigned)grid, (unsigned)ks), nthr, lds, (hipStream_t)stream, args);
     }
     return mv_launch(c, ty, nullptr, w, x, 0, cols, y, 0, rows, rows, cols, m, 1, (hipStream_t)stream);
 }
