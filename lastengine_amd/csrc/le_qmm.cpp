@@ -67,6 +67,7 @@ struct le_ctx {
     int mq_waves_auto = 1;   /* double mq_waves for grids smaller than the chip */
     int mq_waves = 4, mq_steps = 2, mq_blocks_per_cu = 2;
     int ms = 1, ms_p = 2;    /* staged MFMA variant and its super-blocks per row and step */
+    int ms_t = 1;            /* Q4_K with 2..8 tokens per pass on the staged MFMA kernel */
     int mq6 = 1, ms_p6 = 2;  /* Q6_K decode matvec on the staged MFMA kernels, super-blocks per step */
     int mqiq = 1, ms_piq = 2; /* IQ2_XXS / IQ3_XXS likewise */
     int moe_fast = 1;        /* decode-shaped MoE kernels */
@@ -74,7 +75,8 @@ struct le_ctx {
     int moe_fused = 1;       /* ... in one launch with a device-wide barrier where the grid fits */
     int moe_fused_min_tok = 3; /* ... from this many tokens on (below, two launches are faster) */
     std::map<std::string, int> occ; /* resident blocks per CU, by kernel name and LDS bytes */
-    int gm_min_m = 4;        /* le_gemm uses the MFMA kernels from this many tokens on */
+    int gm_min_m = 5;        /* le_gemm uses the MFMA GEMM from this many tokens on (below: the
+                                staged matvec with 2..4 tokens per pass, faster there) */
     int gm_tile = 0;         /* MFMA GEMM tile: 0 auto, else 10*TM + TN (TM, TN in 1..2) */
     int gm_ksplit = 0;       /* MFMA GEMM K slices: 0 auto, else 1, 2, 4, 8 */
     int gm_pc = 1;           /* MFMA GEMM with producer/consumer waves */
@@ -213,6 +215,55 @@ int mq_launch(le_ctx *c, int ty, const void *const *ptrs, const void *w, const f
     return c->launch(name, dim3((unsigned)gx, (unsigned)slots), NW * 64, lds, st, args);
 }
 
+/* Q4_K for 2..8 tokens (per pass) on the staged MFMA kernel: grid (row-tile workers, slots,
+ * token groups of T). Returns 1 when no instantiated shape fits (the caller falls back). */
+int ms_t_launch(le_ctx *c, const void *const *ptrs, const void *w, const float *x, long long x_slot, long long x_tok,
+                float *y, long long y_slot, long long y_tok, int rows, int cols, int ntok, int slots, hipStream_t st) {
+    const long long ntile = (rows + 15) / 16;
+    const int nsb = cols / 256;
+    const int T = ntok <= 2 ? 2 : ntok <= 4 ? 4 : 8;
+    const long long groups = (ntok + T - 1) / T;
+    const bool wide = c->mq_waves_auto && ntile * slots * groups <= c->cus;
+    /* (P, NW) shapes that are instantiated, in order of preference */
+    static const int kWide[4][2] = {{1, 8}, {1, 4}, {2, 4}, {2, 2}}, kStd[3][2] = {{1, 4}, {2, 4}, {2, 2}};
+    const int(*cand)[2] = wide ? kWide : kStd;
+    const int ncand = wide ? 4 : 3;
+    for (int i = 0; i < ncand; i++) {
+        const int P = cand[i][0], NW = cand[i][1];
+        if (P > c->ms_p || nsb % (NW * P)) continue;
+        const int ni = (16 * (9 * P + 1) + 63) / 64;
+        const size_t lds = (size_t)NW * ((size_t)T * (nsb / NW) * 608 + (size_t)ni * 1024) + (size_t)NW * T * 128;
+        if (lds > c->lds_limit) continue;
+        char name[64];
+        snprintf(name, sizeof name, "le_ms_12_p%d_w%d_t%d", P, NW, T);
+        /* every block quantizes its tokens once, so the grid is what stays resident (blocks then
+         * loop over row tiles) */
+        const int per_cu = c->blocks_per_cu(name, NW * 64, lds);
+        long long gx = ntile, cap = (long long)c->cus * (per_cu > 0 ? per_cu : 1);
+        const long long per_slot = (cap + slots * groups - 1) / (slots * groups);
+        if (gx > per_slot) {
+            const long long it = (gx + per_slot - 1) / per_slot;
+            gx = (gx + it - 1) / it;
+        }
+        MvArgs a{};
+        a.ptrs = ptrs;
+        a.w0 = w;
+        a.w_slot_bytes = (unsigned long long)rows * nsb * sb_bytes(LE_TYPE_Q4_K);
+        a.x = x;
+        a.x_slot = x_slot;
+        a.x_tok = x_tok;
+        a.y = y;
+        a.y_slot = y_slot;
+        a.y_tok = y_tok;
+        a.rows = rows;
+        a.cols = cols;
+        a.ntok = ntok;
+        void *args[] = {&a};
+        return c->launch(name, dim3((unsigned)gx, (unsigned)slots, (unsigned)groups), NW * 64, lds, st, args);
+    }
+    return 1;
+}
+
 /* Matvec/matmul launcher: T tokens per pass, grid (workers, slots, ceil(ntok/T)). */
 int mv_launch(le_ctx *c, int ty, const void *const *ptrs, const void *w, const float *x, long long x_slot,
               long long x_tok, float *y, long long y_slot, long long y_tok, int rows, int cols, int ntok, int slots,
@@ -227,6 +278,10 @@ int mv_launch(le_ctx *c, int ty, const void *const *ptrs, const void *w, const f
     if ((ty == LE_TYPE_Q4_K || (ty == LE_TYPE_Q6_K && c->mq6) || (iq && c->mqiq)) && ntok == 1 && c->mq &&
         (size_t)nsb * 608 + 1024 <= c->lds_limit) {
         const int rc = mq_launch(c, ty, ptrs, w, x, x_slot, y, y_slot, rows, cols, slots, st);
+        if (rc != 1) return rc;
+    }
+    if (ty == LE_TYPE_Q4_K && ntok >= 2 && c->mq && c->ms && c->ms_t) {
+        const int rc = ms_t_launch(c, ptrs, w, x, x_slot, x_tok, y, y_slot, y_tok, rows, cols, ntok, slots, st);
         if (rc != 1) return rc;
     }
     const int xb = xtok_bytes(cols), tb = table_bytes(ty);
@@ -395,6 +450,8 @@ int le_set_option(le_ctx *c, const char *name, int value) {
         c->moe_fast = value ? 1 : 0;
     } else if (n == "ms") {
         c->ms = value ? 1 : 0;
+    } else if (n == "ms_t") {
+        c->ms_t = value ? 1 : 0;
     } else if (n == "ms_p") {
         if (value != 1 && value != 2 && value != 4) return c->fail(LE_ERR_ARG, "ms_p must be 1, 2 or 4");
         c->ms_p = value;

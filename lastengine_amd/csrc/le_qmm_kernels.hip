@@ -840,6 +840,155 @@ __device__ __forceinline__ void ms_q4k_body(const MvArgs &a) {
     LE_TRACE_FLUSH;
 }
 
+/* Q4_K for T tokens on one staged super-block: the B fragments and scales of the row are decoded
+ * once and used by every token; token t's image starts at rec + t * ts (super-block sb of nsbw). */
+template <int T>
+__device__ __forceinline__ void ms_sb_q4k_t(const uint4 *sbp, const uint4 *rec, int ts, int sb, int nsbw, const MsLane &L,
+                                            float (&y)[T]) {
+    const int sq = L.sq;
+    const uint4 hd = sbp[0], l0 = sbp[1 + sq], l1 = sbp[5 + sq];
+    le_v4i B[4];
+#pragma unroll
+    for (int b = 0; b < 4; b++) {
+        const uint4 w = b < 2 ? l0 : l1;
+        const int sh = (b & 1) * 4;
+        B[b] = (le_v4i){(int)((w.x >> sh) & 0x0F0F0F0Fu), (int)((w.y >> sh) & 0x0F0F0F0Fu), (int)((w.z >> sh) & 0x0F0F0F0Fu),
+                        (int)((w.w >> sh) & 0x0F0F0F0Fu)};
+    }
+    le_v4i D[T];
+#pragma unroll
+    for (int b = 0; b < 4; b++) {
+#pragma unroll
+        for (int t = 0; t < T; t++) {
+            /* every lane reads (the address is in range for all), non-live lanes then take zero:
+             * no branch, so the reads of all tokens can be in flight together */
+            const uint4 v = rec[t * ts + sb * 32 + (b * 4 + sq) * 2 + L.p];
+            const bool lv = L.live[b];
+            const le_v4i A = {lv ? (int)v.x : 0, lv ? (int)v.y : 0, lv ? (int)v.z : 0, lv ? (int)v.w : 0};
+            D[t] = __builtin_amdgcn_mfma_i32_16x16x64_i8(A, B[b], b ? D[t] : (le_v4i){0, 0, 0, 0}, 0, 0, 0);
+        }
+    }
+    const u32 sy = hd.y, sz = hd.z, sw = hd.w;
+    const u32 tsc = (sq & 1) ? ((sw & 0x0F0F0F0Fu) | ((sy >> 2) & 0x30303030u)) : (sy & 0x3F3F3F3Fu);
+    const u32 tm = (sq & 1) ? (((sw >> 4) & 0x0F0F0F0Fu) | ((sz >> 2) & 0x30303030u)) : (sz & 0x3F3F3F3Fu);
+    const float c0 = (float)(tsc & 255u), c1 = (float)((tsc >> 8) & 255u), c2 = (float)((tsc >> 16) & 255u), c3 = (float)(tsc >> 24);
+    const u32 mm = tm >> (16 * L.pe);
+    const float m0 = (float)(mm & 255u), m1 = (float)((mm >> 8) & 255u);
+    const float d = h2f(hd.x & 0xFFFFu), dmin = h2f(hd.x >> 16);
+#pragma unroll
+    for (int t = 0; t < T; t++) {
+        const float *dxp = (const float *)(rec + t * ts + nsbw * 32);
+        const float4 dq = *(const float4 *)(dxp + sb * 16 + L.pe * 8 + L.jb);
+        const float2 f2 = *(const float2 *)(dxp + nsbw * 16 + sb * 8 + L.jb + 2 * L.pe);
+        const float tt = c0 * dq.x * (float)D[t][0] + c1 * dq.y * (float)D[t][1] + c2 * dq.z * (float)D[t][2] + c3 * dq.w * (float)D[t][3];
+        y[t] += d * tt - dmin * (m0 * f2.x + m1 * f2.y);
+    }
+}
+
+/* The staged Q4_K matvec for T tokens at once (tokens T*blockIdx.z .. +T-1, clamped to ntok - 1,
+ * of which only real ones are stored): the weight stream is the single-token kernel's, each wave
+ * keeps T activation images, and every decoded weight fragment feeds T MFMA chains. */
+template <int P, int NW, int T>
+__device__ __forceinline__ void ms_q4k_t_body(const MvArgs &a) {
+    extern __shared__ uint4 smem[];
+    constexpr int CPR = 9 * P + 1, NCH = 16 * CPR, NI = (NCH + 63) / 64;
+    const int K = a.cols, nsb = K >> 8;
+    const int slot = blockIdx.y, tok0 = T * blockIdx.z;
+    const u8 *W = a.ptrs ? a.ptrs[slot] : a.w0 + (size_t)slot * a.w_slot_bytes;
+    const size_t rb = (size_t)nsb * 144;
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int n = lane & 15;
+    /* wave-private LDS: T activation images of this wave's super-blocks, then the staging buffer */
+    const int nsbw = nsb / NW, ts = nsbw * 38;
+    uint4 *rec = smem + wave * (T * ts + NI * 64);
+    uint4 *wb = rec + T * ts;
+    float *red = (float *)(smem + NW * (T * ts + NI * 64)); /* [2][NW][T][16] */
+    const int ntile = (a.rows + 15) >> 4;
+
+    int ri[NI], cb[NI];
+#pragma unroll
+    for (int i = 0; i < NI; i++) {
+        const int c = min(64 * i + lane, NCH - 1);
+        const int col = c % CPR;
+        ri[i] = c / CPR;
+        cb[i] = (col == 9 * P ? 0 : col) * 16;
+    }
+    uint4 R[NI];
+    auto issue = [&](int tile, int s0) {
+#pragma unroll
+        for (int i = 0; i < NI; i++) {
+            const int row = min(tile * 16 + ri[i], a.rows - 1);
+            R[i] = ldg16(W + (size_t)row * rb + (size_t)s0 * 144 + cb[i]);
+        }
+    };
+    const int sfirst = wave * P, sstep = NW * P;
+    const bool active = sfirst < nsb;
+    issue(min((int)blockIdx.x, ntile - 1), active ? sfirst : 0);
+    /* the T tokens' images: element el = (token el / nsegw, local segment el % nsegw); the two
+     * segments of a sub-block sit in partner lanes */
+    const int nsegw = nsbw * 16, nel = T * nsegw;
+    constexpr int QB = 4; /* element rounds whose loads are in flight together */
+    for (int base = 0; base < nel; base += 64 * QB) {
+        float4 xv[QB][4];
+#pragma unroll
+        for (int u = 0; u < QB; u++) {
+            const int el = min(base + 64 * u + lane, nel - 1);
+            const int t = el / nsegw, e = el - t * nsegw, ls = e >> 4;
+            const float *xs = a.x + a.x_slot * slot + a.x_tok * min(tok0 + t, a.ntok - 1);
+            mq_load_seg(xs, ((ls / P) * sstep + sfirst + ls % P) * 16 + (e & 15), xv[u]);
+        }
+#pragma unroll
+        for (int u = 0; u < QB; u++) {
+            if (base + 64 * u >= nel) break; /* wave-uniform */
+            const int el = base + 64 * u + lane, elc = min(el, nel - 1);
+            const int t = elc / nsegw, e = elc - t * nsegw;
+            uint4 *rt = rec + t * ts;
+            float *dxp = (float *)(rt + nsbw * 32);
+            mq_quant_seg(e, el < nel, xv[u], rt, dxp, dxp + nsbw * 16);
+        }
+    }
+
+    const MsLane L = ms_lane<0>(lane);
+    int par = 0;
+    for (int tile = blockIdx.x; tile < ntile; tile += gridDim.x) {
+        float y[T];
+#pragma unroll
+        for (int t = 0; t < T; t++) y[t] = 0.f;
+        if (active) {
+            for (int s0 = sfirst, lb = 0; s0 < nsb; s0 += sstep, lb += P) {
+                int nt = tile, ns = s0 + sstep;
+                if (ns >= nsb) { ns = sfirst; nt += gridDim.x; }
+#pragma unroll
+                for (int i = 0; i < NI; i++) wb[64 * i + lane] = R[i];
+                if (nt < ntile) issue(nt, ns);
+#pragma unroll
+                for (int q = 0; q < P; q++) ms_sb_q4k_t<T>(wb + n * CPR + 9 * q, rec, ts, lb + q, nsbw, L, y);
+            }
+        }
+        float *rp = red + par * (NW * T * 16);
+#pragma unroll
+        for (int t = 0; t < T; t++) {
+            float v = y[t];
+            v += __builtin_bit_cast(float, __builtin_amdgcn_ds_swizzle(__builtin_bit_cast(int, v), 0x401F));
+            v += __shfl_xor(v, 32);
+            if (lane < 16) rp[(wave * T + t) * 16 + lane] = v;
+        }
+        __builtin_amdgcn_s_waitcnt(0xC07F);
+        __builtin_amdgcn_s_barrier();
+        if (wave == 0) {
+#pragma unroll
+            for (int o = lane; o < T * 16; o += 64) {
+                const int t = o >> 4, r = tile * 16 + (o & 15);
+                float acc = 0.f;
+#pragma unroll
+                for (int w = 0; w < NW; w++) acc += rp[(w * T + t) * 16 + (o & 15)];
+                if (r < a.rows && tok0 + t < a.ntok) a.y[a.y_slot * slot + a.y_tok * (tok0 + t) + r] = acc;
+            }
+        }
+        par ^= 1;
+    }
+}
+
 template <int P, int NW>
 __device__ __forceinline__ void ms_q6k_body(const MvArgs &a) {
     extern __shared__ uint4 smem[];
@@ -1102,6 +1251,9 @@ __device__ __forceinline__ void ms_iq_body(const MvArgs &a) {
 #define LE_MS12(P, NW)                                                                                     \
     extern "C" __global__ void __launch_bounds__(NW * 64) le_ms_12_p##P##_w##NW(MvArgs a) { ms_q4k_body<P, NW>(a); }
 
+#define LE_MS12T(P, NW, T)                                                                                 \
+    extern "C" __global__ void __launch_bounds__(NW * 64) le_ms_12_p##P##_w##NW##_t##T(MvArgs a) { ms_q4k_t_body<P, NW, T>(a); }
+
 #define LE_MQ12(NW, U)                                                                                     \
     extern "C" __global__ void __launch_bounds__(NW * 64) le_mq_12_w##NW##_u##U(MvArgs a) { mq_q4k_body<NW, U>(a); }
 
@@ -1112,6 +1264,8 @@ LE_MV_ALL(LE_PART_MV)
 #if LE_PART_MV == 12
 LE_MQ12(4, 1) LE_MQ12(4, 2) LE_MQ12(4, 4) LE_MQ12(8, 1) LE_MQ12(8, 2) LE_MQ12(8, 4) LE_MQ12(2, 1) LE_MQ12(2, 2) LE_MQ12(2, 4)
 LE_MS12(1, 1) LE_MS12(1, 2) LE_MS12(1, 4) LE_MS12(1, 8) LE_MS12(2, 1) LE_MS12(2, 2) LE_MS12(2, 4) LE_MS12(2, 8) LE_MS12(4, 1) LE_MS12(4, 2) LE_MS12(4, 4)
+LE_MS12T(1, 4, 2) LE_MS12T(1, 4, 4) LE_MS12T(1, 4, 8) LE_MS12T(1, 8, 2) LE_MS12T(1, 8, 4) LE_MS12T(1, 8, 8)
+LE_MS12T(2, 4, 2) LE_MS12T(2, 4, 4) LE_MS12T(2, 4, 8) LE_MS12T(2, 2, 2) LE_MS12T(2, 2, 4) LE_MS12T(2, 2, 8)
 #endif
 #if LE_PART_MV == 14
 LE_MS14(1, 1) LE_MS14(1, 2) LE_MS14(1, 4) LE_MS14(1, 8) LE_MS14(2, 1) LE_MS14(2, 2) LE_MS14(2, 4) LE_MS14(2, 8) LE_MS14(4, 1) LE_MS14(4, 2)
@@ -2064,6 +2218,7 @@ __device__ __forceinline__ void moe_dnm_body(const MoeArgs &a) {
             R0[i] = R1[i];
         }
         if (z + 2 * NW < R.U) issue(z + 2 * NW, R1);
+        if (z == wave) LE_TRACE_POINT(6);
 #pragma unroll 1
         for (int i = 0; i < nmem; i++) {
             const uint4 *rec;
@@ -2089,6 +2244,7 @@ __device__ __forceinline__ void moe_dnm_body(const MoeArgs &a) {
             y += __shfl_xor(y, 32);
             if (lane < 16) red[wave][mtok[wave][i]][lane] += mw[wave][i] * y;
         }
+        if (z == wave) LE_TRACE_POINT(7);
     }
     LE_TRACE_POINT(2);
     __syncthreads();

@@ -243,6 +243,24 @@ def test_error_codes(engine):
     assert e.value.code == -3
 
 
+@pytest.mark.parametrize("m", [2, 3, 5, 8, 11])
+@pytest.mark.parametrize("rows,cols", [(300, 4096), (64, 2048), (1000, 1024)])
+def test_gemm_few_tokens_staged(fresh_engine, m, rows, cols):
+    """Below gm_min_m tokens Q4_K runs on the staged MFMA matvec with T = 2, 4 or 8 tokens per
+    pass: partial token groups (3, 5, 11), a second group (11 > 8) and ragged row tiles."""
+    import torch
+    engine = fresh_engine
+    engine.set_option("gm_min_m", 64)
+    ty = le.Q4_K
+    q, _ = weights(ty, rows, cols, seed=31 + m)
+    xs = np.stack([acts(cols, 6000 + 17 * m + t) for t in range(m)])
+    y = torch.full((m, rows), float("nan"), dtype=torch.float32, device="cuda")
+    engine.gemm(ty, dev(q), dev(xs), m, y, rows, cols)
+    sync()
+    want = oracle.matmat(ty, q, rows, cols, xs)
+    check_close(y.cpu().numpy(), want, absmag(ty, q, rows, cols, xs))
+
+
 @pytest.mark.parametrize("m", [16, 128])
 def test_gemm_activation_split(fresh_engine, m):
     """gm_split=1 carries each activation as two fp16 halves: the result then agrees with the fp64
@@ -270,7 +288,7 @@ def test_options_validated(fresh_engine):
     """Every documented launch-policy knob is accepted with a valid value; bad names and values
     are refused with LE_ERR_ARG and leave the context usable."""
     good = {"mv_block": 512, "mv_blocks_per_cu": 1, "mv_shape": 0, "mq": 1, "ms": 1, "mq_waves": 4, "mq_steps": 2,
-            "mq_blocks_per_cu": 2, "mq_waves_auto": 1, "ms_p": 2, "ms_p6": 2, "ms_piq": 2, "mq6": 1, "mqiq": 1, "gm_min_m": 4,
+            "mq_blocks_per_cu": 2, "mq_waves_auto": 1, "ms_p": 2, "ms_p6": 2, "ms_piq": 2, "mq6": 1, "mqiq": 1, "ms_t": 1, "gm_min_m": 5,
             "gm_tile": 0, "gm_ksplit": 0, "gm_pc": 1, "gm_split": 0, "moe_mfma": 1, "moe_fused": 1, "moe_fused_min_tok": 3,
             "moe_fast": 1}
     engine = fresh_engine
