@@ -232,7 +232,7 @@ int ms_t_launch(le_ctx *c, const void *const *ptrs, const void *w, const float *
         const int P = cand[i][0], NW = cand[i][1];
         if (P > c->ms_p || nsb % (NW * P)) continue;
         const int ni = (16 * (9 * P + 1) + 63) / 64;
-        const size_t lds = (size_t)NW * ((size_t)T * (nsb / NW) * 608 + (size_t)ni * 1024) + (size_t)NW * T * 128;
+        const size_t lds = (size_t)NW * ((size_t)T * (nsb / NW) * 624 + (size_t)ni * 1024) + (size_t)NW * T * 128;
         if (lds > c->lds_limit) continue;
         char name[64];
         snprintf(name, sizeof name, "le_ms_12_p%d_w%d_t%d", P, NW, T);

@@ -840,48 +840,89 @@ __device__ __forceinline__ void ms_q4k_body(const MvArgs &a) {
     LE_TRACE_FLUSH;
 }
 
-/* Q4_K for T tokens on one staged super-block: the B fragments and scales of the row are decoded
- * once and used by every token; token t's image starts at rec + t * ts (super-block sb of nsbw). */
+/* Q4_K for T tokens on one staged super-block. Token t's image slice of super-block sb is the
+ * 33-slot record img[(sb T + t) 33 ..]: slots 0-31 as in the single-token image, slot 32 zero; the
+ * scales are token-major per super-block (dxv[(sb T + t) 16 + j], fsv[(sb T + t) 8 + j]). Every
+ * token's operand is then one immediate offset (528 B per token) from a shared address, the live
+ * lanes of a read stay in adjacent slots (no bank conflicts), and a lane whose A row is not live
+ * in MFMA b reads the zero slot (cs[b], fixed per lane). B fragments and row scales are decoded
+ * once for all tokens. */
 template <int T>
-__device__ __forceinline__ void ms_sb_q4k_t(const uint4 *sbp, const uint4 *rec, int ts, int sb, int nsbw, const MsLane &L,
-                                            float (&y)[T]) {
+__device__ __forceinline__ void ms_sb_q4k_t(const uint4 *sbp, const uint4 *img, const float *dxv, const float *fsv, int sb,
+                                            const int (&cs)[4], const MsLane &L, float (&y)[T]) {
     const int sq = L.sq;
     const uint4 hd = sbp[0], l0 = sbp[1 + sq], l1 = sbp[5 + sq];
-    le_v4i B[4];
+    le_v4i D[T];
 #pragma unroll
     for (int b = 0; b < 4; b++) {
         const uint4 w = b < 2 ? l0 : l1;
         const int sh = (b & 1) * 4;
-        B[b] = (le_v4i){(int)((w.x >> sh) & 0x0F0F0F0Fu), (int)((w.y >> sh) & 0x0F0F0F0Fu), (int)((w.z >> sh) & 0x0F0F0F0Fu),
-                        (int)((w.w >> sh) & 0x0F0F0F0Fu)};
-    }
-    le_v4i D[T];
-#pragma unroll
-    for (int b = 0; b < 4; b++) {
+        const le_v4i B = {(int)((w.x >> sh) & 0x0F0F0F0Fu), (int)((w.y >> sh) & 0x0F0F0F0Fu), (int)((w.z >> sh) & 0x0F0F0F0Fu),
+                          (int)((w.w >> sh) & 0x0F0F0F0Fu)};
+        const uint4 *ap = img + sb * T * 33 + cs[b];
 #pragma unroll
         for (int t = 0; t < T; t++) {
-            /* every lane reads (the address is in range for all), non-live lanes then take zero:
-             * no branch, so the reads of all tokens can be in flight together */
-            const uint4 v = rec[t * ts + sb * 32 + (b * 4 + sq) * 2 + L.p];
-            const bool lv = L.live[b];
-            const le_v4i A = {lv ? (int)v.x : 0, lv ? (int)v.y : 0, lv ? (int)v.z : 0, lv ? (int)v.w : 0};
-            D[t] = __builtin_amdgcn_mfma_i32_16x16x64_i8(A, B[b], b ? D[t] : (le_v4i){0, 0, 0, 0}, 0, 0, 0);
+            const uint4 v = ap[33 * t];
+            D[t] = __builtin_amdgcn_mfma_i32_16x16x64_i8((le_v4i){(int)v.x, (int)v.y, (int)v.z, (int)v.w}, B,
+                                                         b ? D[t] : (le_v4i){0, 0, 0, 0}, 0, 0, 0);
         }
     }
     const u32 sy = hd.y, sz = hd.z, sw = hd.w;
     const u32 tsc = (sq & 1) ? ((sw & 0x0F0F0F0Fu) | ((sy >> 2) & 0x30303030u)) : (sy & 0x3F3F3F3Fu);
     const u32 tm = (sq & 1) ? (((sw >> 4) & 0x0F0F0F0Fu) | ((sz >> 2) & 0x30303030u)) : (sz & 0x3F3F3F3Fu);
-    const float c0 = (float)(tsc & 255u), c1 = (float)((tsc >> 8) & 255u), c2 = (float)((tsc >> 16) & 255u), c3 = (float)(tsc >> 24);
-    const u32 mm = tm >> (16 * L.pe);
-    const float m0 = (float)(mm & 255u), m1 = (float)((mm >> 8) & 255u);
     const float d = h2f(hd.x & 0xFFFFu), dmin = h2f(hd.x >> 16);
+    /* d * sc_j and dmin * m_j folded once for all tokens */
+    const float c0 = d * (float)(tsc & 255u), c1 = d * (float)((tsc >> 8) & 255u), c2 = d * (float)((tsc >> 16) & 255u),
+                c3 = d * (float)(tsc >> 24);
+    const u32 mm = tm >> (16 * L.pe);
+    const float m0 = dmin * (float)(mm & 255u), m1 = dmin * (float)((mm >> 8) & 255u);
+    const float *dq0 = dxv + sb * T * 16 + L.pe * 8 + L.jb, *f0 = fsv + sb * T * 8 + L.jb + 2 * L.pe;
 #pragma unroll
     for (int t = 0; t < T; t++) {
-        const float *dxp = (const float *)(rec + t * ts + nsbw * 32);
-        const float4 dq = *(const float4 *)(dxp + sb * 16 + L.pe * 8 + L.jb);
-        const float2 f2 = *(const float2 *)(dxp + nsbw * 16 + sb * 8 + L.jb + 2 * L.pe);
-        const float tt = c0 * dq.x * (float)D[t][0] + c1 * dq.y * (float)D[t][1] + c2 * dq.z * (float)D[t][2] + c3 * dq.w * (float)D[t][3];
-        y[t] += d * tt - dmin * (m0 * f2.x + m1 * f2.y);
+        const float4 dq = *(const float4 *)(dq0 + 16 * t);
+        const float2 f2 = *(const float2 *)(f0 + 8 * t);
+        float acc = y[t] - m0 * f2.x;
+        acc = __builtin_fmaf(-m1, f2.y, acc);
+        acc = __builtin_fmaf(c0 * dq.x, (float)D[t][0], acc);
+        acc = __builtin_fmaf(c1 * dq.y, (float)D[t][1], acc);
+        acc = __builtin_fmaf(c2 * dq.z, (float)D[t][2], acc);
+        y[t] = __builtin_fmaf(c3 * dq.w, (float)D[t][3], acc);
+    }
+}
+
+/* The activation split of mq_quant_seg (16 values of one sub-block half, partner lane e^1 holds
+ * the other half) stored in the token-interleaved layout of ms_sb_q4k_t (Q4_K slice map). */
+template <int T>
+__device__ __forceinline__ void mq_quant_seg_t(int e, int t, bool store, const float4 (&v4)[4], uint4 *img, float *dxv,
+                                               float *fsv) {
+    float am = fmaxf(amax8(v4[0], v4[1]), amax8(v4[2], v4[3]));
+    am = fmaxf(am, __shfl_xor(am, 1));
+    const float inv = am > 0.f ? LE_XSPLIT / am : 0.f;
+    const float d = am / LE_XSPLIT;
+    u32 hw[4] = {0, 0, 0, 0}, lw[4] = {0, 0, 0, 0};
+    int sum = 0;
+#pragma unroll
+    for (int i = 0; i < 16; i++) {
+        const float xv = i % 4 == 0 ? v4[i / 4].x : i % 4 == 1 ? v4[i / 4].y : i % 4 == 2 ? v4[i / 4].z : v4[i / 4].w;
+        const int v = (int)rintf(xv * inv);
+        const int h = (v + 64) >> 7;
+        const int lo = v - (h << 7);
+        hw[i >> 2] |= ((u32)h & 255u) << (8 * (i & 3));
+        lw[i >> 2] |= ((u32)lo & 255u) << (8 * (i & 3));
+        sum += v;
+    }
+    sum += __shfl_xor(sum, 1);
+    if (!store) return;
+    const int sb = e >> 4, j = (e & 15) >> 1, c = e & 1;
+    const int b = 2 * (j >> 2) + (j & 1), s = 2 * ((j & 3) >> 1) + c;
+    const int r = (sb * 16 + b * 4 + s) * 2;
+    uint4 *rt = img + (sb * T + t) * 33;
+    rt[r - sb * 32] = make_uint4(hw[0], hw[1], hw[2], hw[3]);
+    rt[r - sb * 32 + 1] = make_uint4(lw[0], lw[1], lw[2], lw[3]);
+    if (c == 0) {
+        dxv[(sb * T + t) * 16 + j] = d * 128.0f;
+        dxv[(sb * T + t) * 16 + 8 + j] = d;
+        fsv[(sb * T + t) * 8 + j] = d * (float)sum;
     }
 }
 
@@ -898,11 +939,14 @@ __device__ __forceinline__ void ms_q4k_t_body(const MvArgs &a) {
     const size_t rb = (size_t)nsb * 144;
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int n = lane & 15;
-    /* wave-private LDS: T activation images of this wave's super-blocks, then the staging buffer */
-    const int nsbw = nsb / NW, ts = nsbw * 38;
-    uint4 *rec = smem + wave * (T * ts + NI * 64);
-    uint4 *wb = rec + T * ts;
-    float *red = (float *)(smem + NW * (T * ts + NI * 64)); /* [2][NW][T][16] */
+    /* wave-private LDS: the T token-interleaved images of this wave's super-blocks, T zero slots,
+     * the scales and sums, then the staging buffer */
+    const int nsbw = nsb / NW, wsz = nsbw * 39 * T;
+    uint4 *img = smem + wave * (wsz + NI * 64);
+    float *dxv = (float *)(img + nsbw * T * 33), *fsv = dxv + nsbw * T * 16;
+    uint4 *wb = img + wsz;
+    float *red = (float *)(smem + NW * (wsz + NI * 64)); /* [2][NW][T][16] */
+    for (int i = lane; i < nsbw * T; i += 64) img[33 * i + 32] = make_uint4(0u, 0u, 0u, 0u);
     const int ntile = (a.rows + 15) >> 4;
 
     int ri[NI], cb[NI];
@@ -942,13 +986,14 @@ __device__ __forceinline__ void ms_q4k_t_body(const MvArgs &a) {
             if (base + 64 * u >= nel) break; /* wave-uniform */
             const int el = base + 64 * u + lane, elc = min(el, nel - 1);
             const int t = elc / nsegw, e = elc - t * nsegw;
-            uint4 *rt = rec + t * ts;
-            float *dxp = (float *)(rt + nsbw * 32);
-            mq_quant_seg(e, el < nel, xv[u], rt, dxp, dxp + nsbw * 16);
+            mq_quant_seg_t<T>(e, t, el < nel, xv[u], img, dxv, fsv);
         }
     }
 
     const MsLane L = ms_lane<0>(lane);
+    int cs[4]; /* the lane's slot in a record for MFMA b: its image slice, or the zero slot */
+#pragma unroll
+    for (int b = 0; b < 4; b++) cs[b] = L.live[b] ? (b * 4 + L.sq) * 2 + L.p : 32;
     int par = 0;
     for (int tile = blockIdx.x; tile < ntile; tile += gridDim.x) {
         float y[T];
@@ -962,7 +1007,7 @@ __device__ __forceinline__ void ms_q4k_t_body(const MvArgs &a) {
                 for (int i = 0; i < NI; i++) wb[64 * i + lane] = R[i];
                 if (nt < ntile) issue(nt, ns);
 #pragma unroll
-                for (int q = 0; q < P; q++) ms_sb_q4k_t<T>(wb + n * CPR + 9 * q, rec, ts, lb + q, nsbw, L, y);
+                for (int q = 0; q < P; q++) ms_sb_q4k_t<T>(wb + n * CPR + 9 * q, img, dxv, fsv, lb + q, cs, L, y);
             }
         }
         float *rp = red + par * (NW * T * 16);
