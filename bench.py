@@ -276,9 +276,10 @@ def main():
         sec["config1_q4k_4096x4096"] = {"us": round(r["us"], 3), "GB/s": round(r["gbs"], 1),
                                         "frac_hbm": round(r["gbs"] / HBM_PEAK_GBS, 4)}
         log("config1", sec["config1_q4k_4096x4096"])
+        # the reference's dense decode layer: q, k, v, o, gate and up as one matrix of
+        # concatenated rows (src/gpu/dense.rs:13,67-73,309), down
         layer = [("wq", le.Q4_K, 4096, 4096), ("wk", le.Q4_K, 1024, 4096), ("wv", le.Q4_K, 1024, 4096),
-                 ("wo", le.Q4_K, 4096, 4096), ("gate", le.Q4_K, 14336, 4096), ("up", le.Q4_K, 14336, 4096),
-                 ("down", le.Q6_K, 4096, 14336)]
+                 ("wo", le.Q4_K, 4096, 4096), ("gate_up", le.Q4_K, 28672, 4096), ("down", le.Q6_K, 4096, 14336)]
         sec["config2_llama3_8b_layer"] = bench_layer(eng, layer, max(40, steps2 // 8), 8)
         log("config2 layer", sec["config2_llama3_8b_layer"])
         sec["config2_q8_0_head_32000x4096"] = bench_layer(eng, [("head", le.Q8_0, 32000, 4096)], max(40, steps2 // 8), 8)

@@ -104,8 +104,8 @@ def test_matvec_slots_ptr_table(engine):
         check_close(got[s], oracle.matvec(ty, qs[s], rows, cols, xs[0]), absmag(ty, qs[s], rows, cols, xs[0])[0])
 
 
-# configs 1, 2 and 5 at their full sizes
-FULL = [("Q4_K", 4096, 4096), ("Q4_K", 14336, 4096), ("Q4_K", 1024, 4096), ("Q6_K", 4096, 14336),
+# configs 1, 2 (including the concatenated gate+up matrix) and 5 at their full sizes
+FULL = [("Q4_K", 4096, 4096), ("Q4_K", 14336, 4096), ("Q4_K", 28672, 4096), ("Q4_K", 1024, 4096), ("Q6_K", 4096, 14336),
         ("Q8_0", 32000, 4096), ("IQ2_XXS", 14336, 4096), ("IQ3_XXS", 4096, 14336)]
 
 
