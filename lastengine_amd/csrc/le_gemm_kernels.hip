@@ -289,9 +289,16 @@ __device__ __forceinline__ void gm_q4k_body(const GmArgs &a, const u8 *ws) {
         for (; s + PD <= nstep; s += PD) {
 #pragma unroll
             for (int u = 0; u < PD; u++) {
+                GM_T(pa);
                 gm_barrier(); /* step s+u is staged; the consumers are done with step s+u-1's buffer */
+                GM_T(pb);
                 if (s + u + 1 < nstep) stage(s + u + 1, R[(u + 1) % PD]);
+                GM_T(pc);
                 issue(s + u + PD, R[u]);
+                GM_T(pd);
+                GM_ADD(0, pa, pb);
+                GM_ADD(1, pb, pc);
+                GM_ADD(2, pc, pd);
             }
         }
 #pragma unroll
@@ -300,6 +307,12 @@ __device__ __forceinline__ void gm_q4k_body(const GmArgs &a, const u8 *ws) {
             gm_barrier();
             if (s + u + 1 < nstep) stage(s + u + 1, R[(u + 1) % PD]);
         }
+#if defined(LE_TRACE)
+        GM_T(pe);
+        tr[5] = pe - t_start;
+        if (tid == 256)
+            for (int i = 0; i < 8; i++) le_gm_trace[(1 << 15) + ((size_t)blockIdx.y * gridDim.x + blockIdx.x) * 8 + i] = tr[i];
+#endif
         return;
     }
     Set R0;
@@ -426,6 +439,166 @@ __device__ __forceinline__ void gm_q4k_body(const GmArgs &a, const u8 *ws) {
         for (int i = 0; i < 8; i++) le_gm_trace[((size_t)blockIdx.y * gridDim.x + blockIdx.x) * 8 + i] = tr[i];
 #endif
 }
+
+/* ===================== few tokens (M <= 8): the matvec's weight stream on f16 MFMAs =====================
+ * The staged matvec layout (16-row tiles, each wave streaming P super-blocks per row as
+ * consecutive 16-byte chunks, one item ahead in registers, into wave-private LDS), with the
+ * tokens as the rows of v_mfma_f32_16x16x32_f16: one MFMA per sub-block covers every token, its
+ * K slice is the sub-block's 32 values, and B holds the exact fp16 codes sc_j * q (gm_q4k_frag),
+ * so the sub-block scales need no per-token work. D2 = sum_j m_j S_j(t) is one more MFMA of the
+ * sum records (high halves in K 0-7, low halves in K 8-15) against the mins. The activations
+ * come from the pre-pass (le_gm_xprep, one fp16 plane) and each wave copies its super-blocks of
+ * all T tokens into LDS once. MFMA rows past T repeat token rows (finite, never stored). */
+struct MhArgs {
+    const u8 *w;
+    const u8 *ws;
+    float *y;
+    int rows, cols, m;
+};
+
+template <int P, int NW, int T>
+__device__ __forceinline__ void mh_q4k_body(const MhArgs &a) {
+    typedef float v4f __attribute__((ext_vector_type(4)));
+    extern __shared__ uint4 smem[];
+    constexpr int CPR = 9 * P + 1, NCH = 16 * CPR, NI = (NCH + 63) / 64;
+    const int K = a.cols, nsb = K >> 8, M = a.m;
+    const int tok0 = T * blockIdx.z;
+    const size_t rb = (size_t)nsb * 144;
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int n = lane & 15, kq = lane >> 4;
+    const int nsbw = nsb / NW;
+    /* wave-private LDS: the image [local sb][sub-block j][token][4 x 16 B], the sum records
+     * [local sb][token][2 x 16 B], then the weight staging */
+    const int wsz = nsbw * 8 * T * 4 + nsbw * T * 2;
+    uint4 *img = smem + wave * (wsz + NI * 64);
+    uint4 *srec = img + nsbw * 8 * T * 4;
+    uint4 *wb = img + wsz;
+    float *red = (float *)(smem + NW * (wsz + NI * 64)); /* [NW][16 tokens][16 rows] */
+    const int ntile = (a.rows + 15) >> 4;
+    const int sfirst = wave * P, sstep = NW * P;
+    const bool active = sfirst < nsb;
+    auto gsb = [&](int l) { return (l / P) * sstep + sfirst + l % P; }; /* local -> global super-block */
+
+    int ri[NI], cb[NI];
+#pragma unroll
+    for (int i = 0; i < NI; i++) {
+        const int c = min(64 * i + lane, NCH - 1);
+        const int col = c % CPR;
+        ri[i] = c / CPR;
+        cb[i] = (col == 9 * P ? 0 : col) * 16;
+    }
+    uint4 R[NI];
+    auto issue = [&](int tile, int s0) {
+#pragma unroll
+        for (int i = 0; i < NI; i++) {
+            const int row = min(tile * 16 + ri[i], a.rows - 1);
+            R[i] = ldg16(a.w + (size_t)row * rb + (size_t)s0 * 144 + cb[i]);
+        }
+    };
+    issue(min((int)blockIdx.x, ntile - 1), active ? sfirst : 0);
+    /* the wave's activations: chunk c = (local sb, token, 16-byte column of the 512) */
+    if (active) {
+        const _Float16 *Xh = (const _Float16 *)a.ws;
+        const uint4 *Xs = (const uint4 *)(a.ws + (size_t)M * K * 4);
+        const int nch = nsbw * T * 32;
+        for (int c0 = 0; c0 < nch; c0 += 64 * 8) {
+            uint4 v[8];
+#pragma unroll
+            for (int u = 0; u < 8; u++) {
+                const int c = min(c0 + 64 * u + lane, nch - 1), l = c / (T * 32), t = (c / 32) % T, col = c & 31;
+                v[u] = ldg16c((const u8 *)(Xh + (size_t)min(tok0 + t, M - 1) * K + 256 * gsb(l) + 8 * col));
+            }
+#pragma unroll
+            for (int u = 0; u < 8; u++) {
+                const int c = c0 + 64 * u + lane;
+                if (c < nch) {
+                    const int l = c / (T * 32), t = (c / 32) % T, col = c & 31;
+                    img[((l * 8 + (col >> 2)) * T + t) * 4 + (col & 3)] = v[u];
+                }
+            }
+        }
+        for (int c = lane; c < nsbw * T * 2; c += 64) {
+            const int l = c / (T * 2), t = (c >> 1) % T;
+            srec[c] = ldg16c((const u8 *)(Xs + 2 * ((size_t)min(tok0 + t, M - 1) * nsb + gsb(l)) + (c & 1)));
+        }
+    }
+    const int ta = n % T; /* this lane's A row (token); rows past T repeat earlier tokens */
+    int par = 0;
+    for (int tile = blockIdx.x; tile < ntile; tile += gridDim.x) {
+        v4f y = {0.f, 0.f, 0.f, 0.f};
+        if (active) {
+            for (int s0 = sfirst, lb = 0; s0 < nsb; s0 += sstep, lb += P) {
+                int nt = tile, ns = s0 + sstep;
+                if (ns >= nsb) { ns = sfirst; nt += gridDim.x; }
+#pragma unroll
+                for (int i = 0; i < NI; i++) wb[64 * i + lane] = R[i];
+                if (nt < ntile) issue(nt, ns);
+#pragma unroll
+                for (int q = 0; q < P; q++) {
+                    const int l = lb + q;
+                    const uint4 *sbp = wb + n * CPR + 9 * q;
+                    const uint4 hd = sbp[0];
+                    const u32 sy = hd.y, sz = hd.z, sw = hd.w;
+                    const u32 scw[2] = {sy & 0x3F3F3F3Fu, (sw & 0x0F0F0F0Fu) | ((sy >> 2) & 0x30303030u)};
+                    const u32 mw[2] = {sz & 0x3F3F3F3Fu, ((sw >> 4) & 0x0F0F0F0Fu) | ((sz >> 2) & 0x30303030u)};
+                    v4f d1 = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+                    for (int g = 0; g < 4; g++) {
+                        const uint2 w = *(const uint2 *)((const u8 *)(sbp + 1) + 32 * g + 8 * kq);
+                        const u32 sc2 = scw[g >> 1] >> (16 * (g & 1));
+                        const float sl = (float)(sc2 & 255u), sh = (float)((sc2 >> 8) & 255u);
+                        const le_h2 v0 = {(_Float16)sl, (_Float16)sl}, v1 = {(_Float16)(-1024.f * sl), (_Float16)(-1024.f * sl)};
+                        const le_h2 v2 = {(_Float16)(0.0625f * sh), (_Float16)(0.0625f * sh)}, v3 = {(_Float16)(-64.f * sh), (_Float16)(-64.f * sh)};
+                        le_v8h blo, bhi;
+                        gm_q4k_frag(w, make_uint4(as_u32(v0), as_u32(v1), as_u32(v2), as_u32(v3)), blo, bhi);
+                        const le_v8h alo = __builtin_bit_cast(le_v8h, img[((l * 8 + 2 * g) * T + ta) * 4 + kq]);
+                        const le_v8h ahi = __builtin_bit_cast(le_v8h, img[((l * 8 + 2 * g + 1) * T + ta) * 4 + kq]);
+                        d1 = __builtin_amdgcn_mfma_f32_16x16x32_f16(alo, blo, d1, 0, 0, 0);
+                        d1 = __builtin_amdgcn_mfma_f32_16x16x32_f16(ahi, bhi, d1, 0, 0, 0);
+                    }
+                    /* D2: K 0-7 = high halves of S_0..7 against m_0..7, K 8-15 = low halves; the
+                     * other K slices multiply zero mins */
+                    u32 mb[4];
+#pragma unroll
+                    for (int qq = 0; qq < 4; qq++) {
+                        const u32 mm = mw[qq >> 1] >> (16 * (qq & 1));
+                        const le_h2 v = {(_Float16)(float)(mm & 255u), (_Float16)(float)((mm >> 8) & 255u)};
+                        mb[qq] = kq < 2 ? as_u32(v) : 0u;
+                    }
+                    const le_v8h b2 = __builtin_bit_cast(le_v8h, make_uint4(mb[0], mb[1], mb[2], mb[3]));
+                    const le_v8h a2 = __builtin_bit_cast(le_v8h, srec[(l * T + ta) * 2 + (kq & 1)]);
+                    const v4f d2 = __builtin_amdgcn_mfma_f32_16x16x32_f16(a2, b2, (v4f){0.f, 0.f, 0.f, 0.f}, 0, 0, 0);
+                    const float dd = h2f(hd.x & 0xFFFFu), dm = h2f(hd.x >> 16);
+#pragma unroll
+                    for (int e = 0; e < 4; e++) y[e] = __builtin_fmaf(dd, d1[e], __builtin_fmaf(-dm, d2[e], y[e]));
+                }
+            }
+        }
+        /* D lane l element e: token 4*kq + e, row n; the waves' K shares add in a fixed order */
+        float *rp = red + par * (NW * 256);
+#pragma unroll
+        for (int e = 0; e < 4; e++) rp[wave * 256 + (4 * kq + e) * 16 + n] = y[e];
+        __builtin_amdgcn_s_waitcnt(0xC07F);
+        __builtin_amdgcn_s_barrier();
+        if (wave == 0) {
+#pragma unroll
+            for (int o = lane; o < T * 16; o += 64) {
+                const int t = o >> 4, r = tile * 16 + (o & 15);
+                float acc = 0.f;
+#pragma unroll
+                for (int w = 0; w < NW; w++) acc += rp[w * 256 + o];
+                if (r < a.rows && tok0 + t < M) a.y[(size_t)(tok0 + t) * a.rows + r] = acc;
+            }
+        }
+        par ^= 1;
+    }
+}
+
+#define LE_MH(P, NW, T)                                                                                    \
+    extern "C" __global__ void __launch_bounds__(NW * 64) le_mh_12_p##P##_w##NW##_t##T(MhArgs a) {        \
+        mh_q4k_body<P, NW, T>(a);                                                                          \
+    }
+LE_MH(1, 4, 4) LE_MH(1, 4, 8) LE_MH(2, 4, 4) LE_MH(2, 4, 8) LE_MH(1, 8, 4) LE_MH(1, 8, 8) LE_MH(2, 2, 4) LE_MH(2, 2, 8)
 
 #define LE_GM(TM, TN)                                                                                      \
     extern "C" __global__ void __launch_bounds__(256) le_gm_12_m##TM##_n##TN(GmArgs a, const u8 *ws) {    \

@@ -68,6 +68,8 @@ struct le_ctx {
     int mq_waves = 4, mq_steps = 2, mq_blocks_per_cu = 2;
     int ms = 1, ms_p = 2;    /* staged MFMA variant and its super-blocks per row and step */
     int ms_t = 1;            /* Q4_K with 2..8 tokens per pass on the staged MFMA kernel */
+    int gm_mh = 1;           /* le_gemm, Q4_K, 3..8 tokens: the staged f16 MFMA kernel */
+    int gm_mh_shape = 0;     /* ... its (P, NW) as 10 * P + NW: 0 auto, 14, 18, 24, 22 */
     int mq6 = 1, ms_p6 = 2;  /* Q6_K decode matvec on the staged MFMA kernels, super-blocks per step */
     int mqiq = 1, ms_piq = 2; /* IQ2_XXS / IQ3_XXS likewise */
     int moe_fast = 1;        /* decode-shaped MoE kernels */
@@ -450,6 +452,12 @@ int le_set_option(le_ctx *c, const char *name, int value) {
         c->moe_fast = value ? 1 : 0;
     } else if (n == "ms") {
         c->ms = value ? 1 : 0;
+    } else if (n == "gm_mh_shape") {
+        if (value != 0 && value != 14 && value != 18 && value != 24 && value != 22)
+            return c->fail(LE_ERR_ARG, "gm_mh_shape must be 0, 14, 18, 24 or 22");
+        c->gm_mh_shape = value;
+    } else if (n == "gm_mh") {
+        c->gm_mh = value ? 1 : 0;
     } else if (n == "ms_t") {
         c->ms_t = value ? 1 : 0;
     } else if (n == "ms_p") {
@@ -574,6 +582,54 @@ int le_moe_layer(le_ctx *c, int ty_gate, int ty_up, int ty_down, const void *gat
     return c->launch(name, dim3((unsigned)(hidden / 8)), fast_dn ? 512 : 256, fast_dn ? 49152 : 0, (hipStream_t)stream, args);
 }
 
+/* Q4_K with 3..8 tokens: the pre-pass (one fp16 plane and the sum records) and the staged f16
+ * MFMA kernel, T = 4 or 8 tokens per weight pass. Returns 1 when no instantiated shape fits. */
+static int mh_launch(le_ctx *c, const void *w, const float *x, int m, float *y, int rows, int cols, void *ws,
+                     hipStream_t st) {
+    const long long ntile = (rows + 15) / 16;
+    const int nsb = cols / 256, T = m <= 4 ? 4 : 8;
+    /* (P, NW) in order of preference, measured on 14336 x 4096 (T=4: 15.0 us with (2,4); T=8:
+     * 16.4 us with (1,8)) */
+    static const int k4[4][2] = {{2, 4}, {1, 4}, {1, 8}, {2, 2}}, k8[4][2] = {{1, 8}, {2, 4}, {1, 4}, {2, 2}};
+    const int(*cand)[2] = T == 4 ? k4 : k8;
+    const int ncand = 4;
+    for (int i = 0; i < ncand; i++) {
+        const int P = c->gm_mh_shape ? c->gm_mh_shape / 10 : cand[i][0], NW = c->gm_mh_shape ? c->gm_mh_shape % 10 : cand[i][1];
+        if (P > c->ms_p || nsb % (NW * P)) continue;
+        const int ni = (16 * (9 * P + 1) + 63) / 64;
+        const size_t lds = (size_t)NW * ((size_t)(nsb / NW) * T * 544 + (size_t)ni * 1024) + (size_t)NW * 2048;
+        if (lds > c->lds_limit) continue;
+        char name[48];
+        snprintf(name, sizeof name, "le_mh_12_p%d_w%d_t%d", P, NW, T);
+        /* every block builds its activation image once: the grid is what stays resident */
+        const int per_cu = c->blocks_per_cu(name, NW * 64, lds);
+        long long gx = ntile, cap = (long long)c->cus * (per_cu > 0 ? per_cu : 1);
+        if (gx > cap) {
+            const long long it = (gx + cap - 1) / cap;
+            gx = (gx + it - 1) / it;
+        }
+        struct {
+            const void *w;
+            const float *x;
+            float *y;
+            int rows, cols, m, ksplit, split;
+        } pa{w, x, y, rows, cols, m, 1, 0};
+        void *pargs[] = {&pa, &ws};
+        const long long waves = (long long)m * nsb;
+        int rc = c->launch("le_gm_xprep", dim3((unsigned)((waves + 3) / 4)), 256, 0, st, pargs);
+        if (rc) return rc;
+        struct {
+            const void *w;
+            const void *ws;
+            float *y;
+            int rows, cols, m;
+        } a{w, ws, y, rows, cols, m};
+        void *args[] = {&a};
+        return c->launch(name, dim3((unsigned)gx, 1, 1), NW * 64, lds, st, args);
+    }
+    return 1;
+}
+
 size_t le_gemm_workspace_size(int ty, int m, int cols) {
     if (ty != LE_TYPE_Q4_K || m <= 0 || cols <= 0 || cols % 256) return 0;
     /* activation halves (2 x fp16 per value) and one 32-byte sum record per (token, super-block) */
@@ -583,11 +639,17 @@ size_t le_gemm_workspace_size(int ty, int m, int cols) {
 int le_gemm(le_ctx *c, int ty, const void *w, const float *x, int m, float *y, int rows, int cols, void *ws,
             size_t ws_bytes, le_stream_t stream) {
     if (!c) return LE_ERR_ARG;
-    if (ty == LE_TYPE_Q4_K && m >= c->gm_min_m && m > 0 && rows > 0 && cols > 0 && cols % 256 == 0 && w && x && y) {
+    /* 3..8 tokens: the staged f16 kernel (2 tokens: the int8 multi-token matvec is faster) */
+    const bool few = ty == LE_TYPE_Q4_K && c->gm_mh && m >= 3 && m <= 8;
+    if (ty == LE_TYPE_Q4_K && (m >= c->gm_min_m || few) && m > 0 && rows > 0 && cols > 0 && cols % 256 == 0 && w && x && y) {
         if (!ws) return c->fail(LE_ERR_ARG, "null workspace");
         if (ws_bytes < le_gemm_workspace_size(ty, m, cols))
             return c->fail(LE_ERR_WORKSPACE, "workspace needs %zu bytes", le_gemm_workspace_size(ty, m, cols));
         if (!al16(x) || !al16(ws)) return c->fail(LE_ERR_ALIGN, "x and ws must be 16-byte aligned");
+        if (few) {
+            const int rc = mh_launch(c, w, x, m, y, rows, cols, ws, (hipStream_t)stream);
+            if (rc != 1) return rc;
+        }
         /* tiles: 32*TM tokens x 128*TN rows: 32 x 256 up to 64 tokens, 64 x 128 above (the
          * producer/consumer kernel of 64 x 256 tiles does not fit its registers) */
         int TM = m > 64 ? 2 : 1, TN = m > 64 && c->gm_pc ? 1 : 2;
