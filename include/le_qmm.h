@@ -79,6 +79,7 @@ const char *le_last_error(const le_ctx *ctx);
  *     "ms_t" (0/1): Q4_K with 2..8 tokens per pass on the staged kernel (one weight stream, 8 tokens
  *     per MFMA pass), used by le_gemm below "gm_min_m" tokens
  *   GEMM: "gm_mh" (0/1) Q4_K with 3..8 tokens on the staged f16 MFMA kernel (tokens as MFMA rows),
+ *     "gm_mh_max" its largest M (8, or 16: one block per CU, where K <= 4096 fits its LDS),
  *     "gm_mh_shape" its (super-blocks per step, waves) as 10 P + NW (0 auto, 14, 18, 24, 22),
  *     "gm_min_m" smallest M on the MFMA GEMM, "gm_tile" (0 auto, 11, 12, 21, 22),
  *     "gm_ksplit" K slices (0 auto, 1, 2, 4, 8), "gm_pc" producer/consumer waves (0/1),

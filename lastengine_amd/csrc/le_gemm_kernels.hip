@@ -7,18 +7,19 @@
  *     w_k = d_r * c_k  -  dmin_r * m_{j(k)}
  * with small integer codes c_k (Q4_K: sc_j * q_k <= 945; the sub-block of value k is j(k)) and
  * integer offsets m_j. Integers below 2048 are exact in fp16, so the weight operand is the fp16
- * code c_k, built in LDS from the raw GGUF bytes. The activations are split x = xh + xl into two
- * fp16 halves (xh = fp16(x), xl = fp16(x - xh), 22 significant bits). v_mfma_f32_16x16x32_f16
- * multiplies both halves by the codes with fp32 accumulation, so per super-block
- *     D1[t, r] = sum_k c_k (xh_k + xl_k)          D2[t, r] = sum_j m_j S_j(t)
- * (S_j = fp32 sum of x over sub-block j, also split into fp16 halves for a second MFMA) and
+ * code c_k, built in registers from the raw GGUF bytes. The activations enter as xh = fp16(x)
+ * (relative error 2^-11), or, under the split option, as two fp16 halves x = xh + xl (xl =
+ * fp16(x - xh), 22 significant bits). The MFMAs multiply them by the codes with fp32
+ * accumulation, so per super-block
+ *     D1[t, r] = sum_k c_k (xh_k [+ xl_k])        D2[t, r] = sum_j m_j S_j(t)
+ * (S_j = fp32 sum of x over sub-block j, split into fp16 halves for one more MFMA) and
  *     Y[t, r] += d_r * D1 - dmin_r * D2
- * in fp32. The only roundings are the activation split (|x - xh - xl| <= 2^-22 |x|) and fp32
- * accumulation; activations must stay inside the fp16 range (|x| < 65504).
+ * in fp32. Activations must stay inside the fp16 range (|x| < 65504).
  *
- * Tiling. A block of four waves computes 32*TM tokens x 128*TN rows; every wave owns 32*TN
- * rows for all the block's tokens, as TM x TN tiles of v_mfma_f32_32x32x16_f16 (this shape runs
- * near the f16 peak with one wave per SIMD). K advances one super-block per step. Staging is
+ * GEMM tiling (M >= 9). A block of four MFMA waves (plus four staging waves in the
+ * producer/consumer form) computes 32*TM tokens x 128*TN rows; every MFMA wave owns 32*TN rows
+ * for all the block's tokens, as TM x TN tiles of v_mfma_f32_32x32x16_f16 (this shape runs near
+ * the f16 peak with one wave per SIMD). K advances half a super-block per step. Staging is
  * coalesced: consecutive lanes load consecutive 16-byte chunks of a weight row's super-block and
  * consecutive float4s of a token's 256 activations, into registers one step ahead, then into LDS.
  * The weights stay raw in LDS (row stride 152 bytes: the 32-row fragment reads are free of bank
@@ -28,6 +29,9 @@
  * on one XCD and share its L2. Within every aligned group of four K positions both operands are
  * stored in the order 0, 2, 1, 3 (what the nibble unpacking produces); the dot product does not
  * depend on the order.
+ *
+ * Few tokens (M = 3..8, le_mh_*): the staged matvec's weight stream with the tokens as the rows
+ * of v_mfma_f32_16x16x32_f16 (described at mh_q4k_body).
  */
 #include "le_qmm_device.h"
 
@@ -599,6 +603,7 @@ __device__ __forceinline__ void mh_q4k_body(const MhArgs &a) {
         mh_q4k_body<P, NW, T>(a);                                                                          \
     }
 LE_MH(1, 4, 4) LE_MH(1, 4, 8) LE_MH(2, 4, 4) LE_MH(2, 4, 8) LE_MH(1, 8, 4) LE_MH(1, 8, 8) LE_MH(2, 2, 4) LE_MH(2, 2, 8)
+LE_MH(1, 4, 16) LE_MH(2, 4, 16) LE_MH(1, 8, 16) LE_MH(2, 2, 16)
 
 #define LE_GM(TM, TN)                                                                                      \
     extern "C" __global__ void __launch_bounds__(256) le_gm_12_m##TM##_n##TN(GmArgs a, const u8 *ws) {    \

@@ -69,6 +69,7 @@ struct le_ctx {
     int ms = 1, ms_p = 2;    /* staged MFMA variant and its super-blocks per row and step */
     int ms_t = 1;            /* Q4_K with 2..8 tokens per pass on the staged MFMA kernel */
     int gm_mh = 1;           /* le_gemm, Q4_K, 3..8 tokens: the staged f16 MFMA kernel */
+    int gm_mh_max = 8;       /* ... up to this many tokens (8 or 16) */
     int gm_mh_shape = 0;     /* ... its (P, NW) as 10 * P + NW: 0 auto, 14, 18, 24, 22 */
     int mq6 = 1, ms_p6 = 2;  /* Q6_K decode matvec on the staged MFMA kernels, super-blocks per step */
     int mqiq = 1, ms_piq = 2; /* IQ2_XXS / IQ3_XXS likewise */
@@ -456,6 +457,9 @@ int le_set_option(le_ctx *c, const char *name, int value) {
         if (value != 0 && value != 14 && value != 18 && value != 24 && value != 22)
             return c->fail(LE_ERR_ARG, "gm_mh_shape must be 0, 14, 18, 24 or 22");
         c->gm_mh_shape = value;
+    } else if (n == "gm_mh_max") {
+        if (value != 8 && value != 16) return c->fail(LE_ERR_ARG, "gm_mh_max must be 8 or 16");
+        c->gm_mh_max = value;
     } else if (n == "gm_mh") {
         c->gm_mh = value ? 1 : 0;
     } else if (n == "ms_t") {
@@ -587,11 +591,12 @@ int le_moe_layer(le_ctx *c, int ty_gate, int ty_up, int ty_down, const void *gat
 static int mh_launch(le_ctx *c, const void *w, const float *x, int m, float *y, int rows, int cols, void *ws,
                      hipStream_t st) {
     const long long ntile = (rows + 15) / 16;
-    const int nsb = cols / 256, T = m <= 4 ? 4 : 8;
+    const int nsb = cols / 256, T = m <= 4 ? 4 : m <= 8 ? 8 : 16;
     /* (P, NW) in order of preference, measured on 14336 x 4096 (T=4: 15.0 us with (2,4); T=8:
      * 16.4 us with (1,8)) */
     static const int k4[4][2] = {{2, 4}, {1, 4}, {1, 8}, {2, 2}}, k8[4][2] = {{1, 8}, {2, 4}, {1, 4}, {2, 2}};
-    const int(*cand)[2] = T == 4 ? k4 : k8;
+    static const int k16[4][2] = {{1, 4}, {1, 8}, {2, 4}, {2, 2}};
+    const int(*cand)[2] = T == 4 ? k4 : T == 8 ? k8 : k16;
     const int ncand = 4;
     for (int i = 0; i < ncand; i++) {
         const int P = c->gm_mh_shape ? c->gm_mh_shape / 10 : cand[i][0], NW = c->gm_mh_shape ? c->gm_mh_shape % 10 : cand[i][1];
@@ -640,7 +645,7 @@ int le_gemm(le_ctx *c, int ty, const void *w, const float *x, int m, float *y, i
             size_t ws_bytes, le_stream_t stream) {
     if (!c) return LE_ERR_ARG;
     /* 3..8 tokens: the staged f16 kernel (2 tokens: the int8 multi-token matvec is faster) */
-    const bool few = ty == LE_TYPE_Q4_K && c->gm_mh && m >= 3 && m <= 8;
+    const bool few = ty == LE_TYPE_Q4_K && c->gm_mh && m >= 3 && m <= c->gm_mh_max;
     if (ty == LE_TYPE_Q4_K && (m >= c->gm_min_m || few) && m > 0 && rows > 0 && cols > 0 && cols % 256 == 0 && w && x && y) {
         if (!ws) return c->fail(LE_ERR_ARG, "null workspace");
         if (ws_bytes < le_gemm_workspace_size(ty, m, cols))
