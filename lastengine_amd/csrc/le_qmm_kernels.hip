@@ -2308,12 +2308,13 @@ __device__ __forceinline__ void moe_dnm_body(const MoeArgs &a) {
 /* ===================== MoE in one launch: gate/up, a device-wide barrier, down =====================
  * A persistent grid (the host launches no more blocks than fit on the device at once) of 8-wave
  * blocks. Every block routes. Phase 1: blocks take the (32-row unit, expert group) items of the
- * gate/up projection round-robin, as in le_moe_gum (hidden 2048). Before that, block b issues the
- * weight loads of its first down group for row tile b (they depend on the routing only), so they
- * arrive while phase 1 runs. A barrier over all blocks (arrival counter + generation word in device
- * memory, self-resetting, bounded wait) separates the phases. Phase 2: block b computes row tile
- * b of the down projection as in le_moe_dnm. If a wait ever exceeds its bound the block writes
- * NaN to its outputs rather than waiting on. */
+ * gate/up projection round-robin, as in le_moe_gum (hidden 2048). Before that, each block issues
+ * the weight loads of its first down group (they depend on the routing only), so they arrive
+ * while phase 1 runs. A barrier over all blocks (per-block arrival flags and a generation word in
+ * device memory, bounded wait) separates the phases. Phase 2: row tile b mod ntile of the down
+ * projection as in le_moe_dnm; when the grid has at least two blocks per tile, blocks b and
+ * b + ntile split the tile's expert groups and add into the output (zeroed in phase 1). If a wait
+ * ever exceeds its bound the block writes NaN to its outputs rather than waiting on. */
 #define LE_MOE_MAXGRID 1024
 __device__ unsigned int le_moe_bar_flag[LE_MOE_MAXGRID]; /* per block: the epoch it last arrived in */
 __device__ unsigned int le_moe_bar_gen;                  /* completed barriers */
@@ -2399,6 +2400,10 @@ __device__ __forceinline__ void moe_fus_body(const MoeArgs &a) {
     LE_TRACE_POINT(1);
     const int ngu = (a.ff >> 5) * R.U, ntile = a.hidden >> 4;
     const int b = blockIdx.x, G = gridDim.x;
+    /* phase 2: row tile tb of the down projection, by H blocks that split its expert groups
+     * (groups z = hh mod H); with H = 2 both add into the output that phase 1 zeroed, so every
+     * element is 0 + a + b in either order: the same bits */
+    const int H = G >= 2 * ntile ? 2 : 1, tb = b % ntile, hh = b / ntile;
     if (b == 0)
         for (int i = threadIdx.x; i < a.n_tok * a.k; i += blockDim.x) {
             if (a.idx_out) a.idx_out[i] = R.topi[i];
@@ -2410,7 +2415,7 @@ __device__ __forceinline__ void moe_fus_body(const MoeArgs &a) {
 #pragma unroll
     for (int i = 0; i < DNI; i++) {
         const int c = min(64 * i + lane, DNCH - 1), col = c % DCPR, cc = col == DCPS * PD ? 0 : col;
-        roff[i] = (16 * b + c / DCPR) * (int)drb + (TD == LE_TYPE_Q6_K ? (cc / 14) * 210 + (cc % 14) * 16 : cc * 16);
+        roff[i] = (16 * tb + c / DCPR) * (int)drb + (TD == LE_TYPE_Q6_K ? (cc / 14) * 210 + (cc % 14) * 16 : cc * 16);
     }
     uint4 R0[DNI];
     auto dissue = [&](int zz, uint4 (&r)[DNI]) {
@@ -2418,7 +2423,7 @@ __device__ __forceinline__ void moe_fus_body(const MoeArgs &a) {
 #pragma unroll
         for (int i = 0; i < DNI; i++) r[i] = TD == LE_TYPE_Q6_K ? ldg16u(W + roff[i]) : ldg16(W + roff[i]);
     };
-    if (b < ntile && wave < R.U) dissue(wave, R0);
+    if (b < H * ntile && hh + H * wave < R.U) dissue(hh + H * wave, R0);
     /* ---- phase 1: gate/up items ---- */
     if (b < ngu) {
 #pragma unroll
@@ -2501,12 +2506,15 @@ __device__ __forceinline__ void moe_fus_body(const MoeArgs &a) {
             mq_quant_seg<MAPD, true>(2 * ux + c, ok, v4, rec, dxp, fsv); /* read by other blocks after the barrier */
         }
     }
+    if (H == 2 && b < ntile) /* device-coherent, ordered before the other half's adds by the barrier */
+        for (int i = threadIdx.x; i < a.n_tok * 16; i += blockDim.x)
+            st_f<true>(a.out + (size_t)(i >> 4) * a.hidden + 16 * b + (i & 15), 0.f);
     /* ---- every down image written ---- */
     LE_TRACE_POINT(2);
     const bool ok = moe_grid_barrier(G);
     LE_TRACE_POINT(3);
-    if (b >= ntile) return;
-    /* ---- phase 2: row tile b of the down projection ---- */
+    if (b >= H * ntile) return;
+    /* ---- phase 2: row tile tb of the down projection, expert groups hh mod H ---- */
     uint4 *imgs = smem;                        /* LE_MOE_DN_IMGS images */
     uint4 *dwb = smem + LE_MOE_DN_IMGS * IMGC + wave * DNI * 64;
     for (int i = threadIdx.x; i < NW * LE_MOE_FAST_TOK * 16; i += blockDim.x) (&red[0][0][0])[i] = 0.f;
@@ -2532,7 +2540,7 @@ __device__ __forceinline__ void moe_fus_body(const MoeArgs &a) {
     uint4 *wimg = imgs + wave * SLOTS * IMGC;
     float *redd = &red[0][0][0]; /* [NW][8][16] */
 #pragma unroll 1
-    for (int z = wave; z < R.U; z += NW) {
+    for (int z = hh + H * wave; z < R.U; z += H * NW) {
         const int e = R.grp_e[z];
         const int nmem = __popcll(R.mask[e]);
         if (lane < nmem) {
@@ -2545,7 +2553,7 @@ __device__ __forceinline__ void moe_fus_body(const MoeArgs &a) {
         }
 #pragma unroll
         for (int i = 0; i < DNI; i++) dwb[64 * i + lane] = R0[i];
-        if (z + NW < R.U) dissue(z + NW, R0);
+        if (z + H * NW < R.U) dissue(z + H * NW, R0);
 #pragma unroll 1
         for (int i = 0; i < nmem; i++) {
             const uint4 *rec;
@@ -2578,7 +2586,11 @@ __device__ __forceinline__ void moe_fus_body(const MoeArgs &a) {
         float acc = 0.f;
 #pragma unroll
         for (int w = 0; w < NW; w++) acc += redd[(w * LE_MOE_FAST_TOK + t) * 16 + r];
-        a.out[(size_t)t * a.hidden + 16 * b + r] = ok ? acc : __builtin_nanf("");
+        float *o = a.out + (size_t)t * a.hidden + 16 * tb + r;
+        if (H == 2)
+            __hip_atomic_fetch_add(o, ok ? acc : __builtin_nanf(""), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        else
+            *o = ok ? acc : __builtin_nanf("");
     }
     LE_TRACE_POINT(4);
     LE_TRACE_FLUSH;
