@@ -2323,7 +2323,8 @@ __device__ unsigned int le_moe_bar_gen;                  /* completed barriers *
  * arrival contends with another; block 0 polls all flags in parallel and then publishes the new
  * generation. Callers store what other blocks read after the barrier with device-coherent stores
  * (mq_quant_seg<.., true>). Every wait is bounded; false means a wait gave up. */
-__device__ __forceinline__ bool moe_grid_barrier(unsigned int nblocks) {
+template <class F>
+__device__ __forceinline__ bool moe_grid_barrier(unsigned int nblocks, F &&after_arrival) {
     __shared__ unsigned int gen_s;
     __shared__ int ok_s;
     __builtin_amdgcn_s_waitcnt(0x0F70); /* vmcnt(0): this thread's coherent stores have completed */
@@ -2338,6 +2339,7 @@ __device__ __forceinline__ bool moe_grid_barrier(unsigned int nblocks) {
     }
     __syncthreads();
     const unsigned int epoch = gen_s + 1u;
+    after_arrival(); /* work that must not delay the arrival (its loads are not waited for above) */
     if (blockIdx.x == 0) {
         for (unsigned int i = threadIdx.x; i < nblocks; i += blockDim.x) {
             unsigned int spins = 0;
@@ -2409,7 +2411,6 @@ __device__ __forceinline__ void moe_fus_body(const MoeArgs &a) {
             if (a.idx_out) a.idx_out[i] = R.topi[i];
             if (a.w_out) a.w_out[i] = R.topw[i];
         }
-    /* the first down group of this block's tile, in flight through phase 1 */
     const size_t drb = (size_t)PD * DSBB;
     int roff[DNI];
 #pragma unroll
@@ -2423,7 +2424,6 @@ __device__ __forceinline__ void moe_fus_body(const MoeArgs &a) {
 #pragma unroll
         for (int i = 0; i < DNI; i++) r[i] = TD == LE_TYPE_Q6_K ? ldg16u(W + roff[i]) : ldg16(W + roff[i]);
     };
-    if (b < H * ntile && hh + H * wave < R.U) dissue(hh + H * wave, R0);
     /* ---- phase 1: gate/up items ---- */
     if (b < ngu) {
 #pragma unroll
@@ -2441,19 +2441,28 @@ __device__ __forceinline__ void moe_fus_body(const MoeArgs &a) {
     le_v4i A[4];
 #pragma unroll
     for (int q = 0; q < 4; q++) A[q] = (le_v4i){0, 0, 0, 0};
-#pragma unroll 1
-    for (int it = b; it < ngu; it += G) {
-        const int ux = it % (a.ff >> 5), z = it / (a.ff >> 5);
-        const int e = R.grp_e[z];
-        const int nmem = __popcll(R.mask[e]);
+    /* the weights of item it (4 tiles: gate rows 32ux.., +16, up rows 32ux.., +16) into Rg; the
+     * next item's loads are issued as soon as the current one is in LDS, so they arrive during its
+     * MFMAs, SwiGLU and quantization (a load past the last item re-reads it: unconditional loads
+     * keep the compiler's waits exact) */
+    uint4 Rg[NI];
+    auto gissue = [&](int it) {
+        it = min(it, ngu - 1);
+        const int ux = it % (a.ff >> 5), e = R.grp_e[it / (a.ff >> 5)];
         const u8 *Wg = a.gate + (size_t)e * a.ff * rb, *Wu = a.up + (size_t)e * a.ff * rb;
-        uint4 Rg[NI];
 #pragma unroll
         for (int i = 0; i < NI; i++) {
             const int c = min(64 * i + lane, NCH - 1), ti = c / (16 * CPR), rem = c % (16 * CPR), col = rem % CPR;
             Rg[i] = ldg16((ti < 2 ? Wg : Wu) + (size_t)(32 * ux + 16 * (ti & 1) + rem / CPR) * rb + (size_t)wave * P * 144 +
                           (col == 9 * P ? 0 : col) * 16);
         }
+    };
+    if (b < ngu) gissue(b);
+#pragma unroll 1
+    for (int it = b; it < ngu; it += G) {
+        const int ux = it % (a.ff >> 5), z = it / (a.ff >> 5);
+        const int e = R.grp_e[z];
+        const int nmem = __popcll(R.mask[e]);
         if (threadIdx.x < nmem) {
             int t, pair;
             float w;
@@ -2464,6 +2473,7 @@ __device__ __forceinline__ void moe_fus_body(const MoeArgs &a) {
         __syncthreads(); /* the previous item's readers of wb / act are done; images and members ready */
 #pragma unroll
         for (int i = 0; i < NI; i++) wb[64 * i + lane] = Rg[i];
+        gissue(it + G);
 #pragma unroll 1
         for (int i = 0; i < nmem; i++) {
             const uint4 *rec = img + mtok[0][i] * (LE_MOE_IMG(K) / 16);
@@ -2511,7 +2521,11 @@ __device__ __forceinline__ void moe_fus_body(const MoeArgs &a) {
             st_f<true>(a.out + (size_t)(i >> 4) * a.hidden + 16 * b + (i & 15), 0.f);
     /* ---- every down image written ---- */
     LE_TRACE_POINT(2);
-    const bool ok = moe_grid_barrier(G);
+    /* the first down group of this block's tile is issued after the arrival, so its loads are in
+     * flight through the wait */
+    const bool ok = moe_grid_barrier(G, [&]() {
+        if (b < H * ntile && hh + H * wave < R.U) dissue(hh + H * wave, R0);
+    });
     LE_TRACE_POINT(3);
     if (b >= H * ntile) return;
     /* ---- phase 2: row tile tb of the down projection, expert groups hh mod H ---- */
