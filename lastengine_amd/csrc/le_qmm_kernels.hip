@@ -588,6 +588,16 @@ __device__ __forceinline__ void mq_q4k_body(const MvArgs &a) {
     }
 }
 
+/* Block barrier that waits for this wave's LDS traffic only: global loads in flight (weight
+ * prefetch) stay in flight, unlike __syncthreads, which is a workgroup fence and waits for all
+ * of them. For data exchanged through LDS. */
+__device__ __forceinline__ void le_lds_barrier() {
+    __asm__ volatile("" ::: "memory");
+    __builtin_amdgcn_s_waitcnt(0xC07F); /* lgkmcnt(0) */
+    __builtin_amdgcn_s_barrier();
+    __asm__ volatile("" ::: "memory");
+}
+
 /* Per-super-block MFMA step of the staged kernels, shared by the decode matvec and the MoE
  * kernels. Lane (row n = lane&15, slice sq = lane>>4); A[b] holds the activation image slice of
  * MFMA b for the lane's A row m = lane&15 (plane m>>3, sub-block m&7) where that row is live, and
@@ -2460,6 +2470,9 @@ __device__ __forceinline__ void moe_fus_body(const MoeArgs &a) {
     if (b < ngu) gissue(b);
 #pragma unroll 1
     for (int it = b; it < ngu; it += G) {
+#if defined(LE_TRACE)
+        const unsigned long long q0 = __builtin_amdgcn_s_memrealtime();
+#endif
         const int ux = it % (a.ff >> 5), z = it / (a.ff >> 5);
         const int e = R.grp_e[z];
         const int nmem = __popcll(R.mask[e]);
@@ -2470,7 +2483,11 @@ __device__ __forceinline__ void moe_fus_body(const MoeArgs &a) {
             mtok[0][threadIdx.x] = t;
             mpair[0][threadIdx.x] = pair;
         }
-        __syncthreads(); /* the previous item's readers of wb / act are done; images and members ready */
+        le_lds_barrier(); /* the previous item's readers of wb / act are done; images and members ready */
+#if defined(LE_TRACE)
+        const unsigned long long q1 = __builtin_amdgcn_s_memrealtime();
+        le_tr_[5] += q1 - q0;
+#endif
 #pragma unroll
         for (int i = 0; i < NI; i++) wb[64 * i + lane] = Rg[i];
         gissue(it + G);
@@ -2490,7 +2507,11 @@ __device__ __forceinline__ void moe_fus_body(const MoeArgs &a) {
                 if (lane < 16) red[wave][i][16 * ti + lane] = v;
             }
         }
-        __syncthreads();
+#if defined(LE_TRACE)
+        const unsigned long long q2 = __builtin_amdgcn_s_memrealtime();
+        le_tr_[6] += q2 - q1;
+#endif
+        le_lds_barrier();
         if (threadIdx.x < 32 * LE_MOE_FAST_TOK) {
             const int i = threadIdx.x >> 5, r = threadIdx.x & 31;
             if (i < nmem) {
@@ -2503,7 +2524,11 @@ __device__ __forceinline__ void moe_fus_body(const MoeArgs &a) {
                 act[i][r] = g / (1.0f + __expf(-g)) * u;
             }
         }
-        __syncthreads();
+        le_lds_barrier();
+#if defined(LE_TRACE)
+        const unsigned long long q3 = __builtin_amdgcn_s_memrealtime();
+        le_tr_[7] += q3 - q2;
+#endif
         if (wave == 0 && lane < 2 * LE_MOE_FAST_TOK) {
             const int i = lane >> 1, c = lane & 1;
             const bool ok = i < nmem;
@@ -2515,6 +2540,10 @@ __device__ __forceinline__ void moe_fus_body(const MoeArgs &a) {
             float *dxp = (float *)(rec + PD * 32), *fsv = dxp + PD * 16;
             mq_quant_seg<MAPD, true>(2 * ux + c, ok, v4, rec, dxp, fsv); /* read by other blocks after the barrier */
         }
+#if defined(LE_TRACE)
+        le_tr_[14] += __builtin_amdgcn_s_memrealtime() - q3;
+        le_tr_[15] += 1;
+#endif
     }
     if (H == 2 && b < ntile) /* device-coherent, ordered before the other half's adds by the barrier */
         for (int i = threadIdx.x; i < a.n_tok * 16; i += blockDim.x)
