@@ -1480,30 +1480,50 @@ __device__ __forceinline__ unsigned long long moe_key(float v, int e) {
     return ((unsigned long long)b << 32) | (u32)(0xFFFFFFFFu - (u32)e);
 }
 
+/* Lane geometry of moe_route_par: C lanes share one (token, expert); lane c of the group compares
+ * against key pairs c, c + C, ... (adjacent lanes read adjacent 16 bytes); C shrinks as tokens
+ * grow so that one pass covers as many tokens as the block has threads for. */
+struct MoeRouteGeom {
+    int tpt, C, tpp, npass;
+};
+__device__ __forceinline__ MoeRouteGeom moe_route_geom(const MoeArgs &a) {
+    MoeRouteGeom g;
+    g.tpt = a.n_exp <= 128 ? 128 : 256;
+    g.C = 8;
+    while (g.C > 1 && g.C * g.tpt * a.n_tok > (int)blockDim.x) g.C >>= 1;
+    g.tpp = blockDim.x / (g.tpt * g.C); /* tokens per pass */
+    g.npass = (a.n_tok + g.tpp - 1) / g.tpp;
+    return g;
+}
+/* This thread's logits of the first MOE_LPASS passes, loaded before anything else the kernel
+ * loads (loads complete in order, so routing then waits for these alone). */
+#define MOE_LPASS 4
+struct MoeLogits {
+    float v[MOE_LPASS];
+};
+__device__ __forceinline__ MoeLogits moe_route_load(const MoeArgs &a) {
+    const MoeRouteGeom g = moe_route_geom(a);
+    MoeLogits L;
+    const int t1 = threadIdx.x / (g.tpt * g.C), e = (threadIdx.x / g.C) % g.tpt;
+#pragma unroll
+    for (int p = 0; p < MOE_LPASS; p++) {
+        const int t = p * g.tpp + t1;
+        L.v[p] = t < a.n_tok && e < a.n_exp ? a.logits[(size_t)t * a.n_exp + e] : 0.f;
+    }
+    return L;
+}
+
 __device__ __forceinline__ void moe_route_par(const MoeArgs &a, MoeRoute &R, unsigned long long *lv /* [n_tok][n_exp] LDS */,
-                                              float *sx /* [n_tok][k] */ LE_TRACE_PARAM) {
-    /* C lanes share one (token, expert): lane c of the group compares against key pairs
-     * c, c + C, ... (adjacent lanes read adjacent 16 bytes); C shrinks as tokens grow so that one
-     * pass covers as many tokens as the block has threads for. */
-    const int tpt = a.n_exp <= 128 ? 128 : 256;
-    int C = 8;
-    while (C > 1 && C * tpt * a.n_tok > (int)blockDim.x) C >>= 1;
-    const int tpp = blockDim.x / (tpt * C); /* tokens per pass */
-    /* n_tok <= 64 on every caller, so a token's bit fits the 64-bit expert mask; the first pass's
+                                              float *sx /* [n_tok][k] */, const MoeLogits &L LE_TRACE_PARAM) {
+    const MoeRouteGeom g = moe_route_geom(a);
+    const int tpt = g.tpt, C = g.C, tpp = g.tpp;
+    /* n_tok <= 64 on every caller, so a token's bit fits the 64-bit expert mask; the first
      * barrier orders this clear before the atomics below */
     for (int e = threadIdx.x; e < a.n_exp; e += blockDim.x) R.mask[e] = 0ull;
     const int c = threadIdx.x % C;
-    for (int t0 = 0; t0 < a.n_tok; t0 += tpp) {
-        const int t = t0 + threadIdx.x / (tpt * C), e = (threadIdx.x / C) % tpt;
-        const bool ok = t < a.n_tok && e < a.n_exp;
-        const float v = ok ? a.logits[(size_t)t * a.n_exp + e] : 0.f;
-        const unsigned long long key = moe_key(v, e);
-        if (ok && c == 0) lv[t * a.n_exp + e] = key;
-        LE_TRACE_POINT(8);
-        __syncthreads();
-        LE_TRACE_POINT(9);
+    auto rank_of = [&](int t, int e, float v, unsigned long long key) {
         int rank = 0;
-        if (ok) {
+        if (t < a.n_tok && e < a.n_exp) {
             const ulonglong2 *row = (const ulonglong2 *)(lv + t * a.n_exp);
             const int npair = a.n_exp >> 1;
             /* eight reads issued before any compare, so LDS latency is paid once per batch */
@@ -1517,14 +1537,43 @@ __device__ __forceinline__ void moe_route_par(const MoeArgs &a, MoeRoute &R, uns
             }
         }
         for (int o = 1; o < C; o <<= 1) rank += __shfl_xor(rank, o); /* groups are lane-aligned */
-        if (ok && c == 0 && rank < a.k) {
+        if (t < a.n_tok && e < a.n_exp && c == 0 && rank < a.k) {
             R.topi[t * a.k + rank] = e;
             sx[t * a.k + rank] = v;
             atomicOr(&R.mask[e], 1ull << t);
         }
+    };
+    const int t1 = threadIdx.x / (tpt * C), e1 = (threadIdx.x / C) % tpt;
+    if (g.npass <= MOE_LPASS) {
+        /* every pass's keys in LDS, one barrier, every pass ranked, one barrier */
+#pragma unroll
+        for (int p = 0; p < MOE_LPASS; p++) {
+            const int t = p * tpp + t1;
+            if (p < g.npass && t < a.n_tok && e1 < a.n_exp && c == 0) lv[t * a.n_exp + e1] = moe_key(L.v[p], e1);
+        }
+        LE_TRACE_POINT(8);
+        __syncthreads();
+        LE_TRACE_POINT(9);
+#pragma unroll
+        for (int p = 0; p < MOE_LPASS; p++) {
+            if (p >= g.npass) break;
+            const int t = p * tpp + t1;
+            rank_of(t, e1, L.v[p], moe_key(L.v[p], e1));
+        }
         LE_TRACE_POINT(10);
         __syncthreads();
         LE_TRACE_POINT(11);
+    } else {
+        for (int t0 = 0; t0 < a.n_tok; t0 += tpp) {
+            const int t = t0 + t1;
+            const bool ok = t < a.n_tok && e1 < a.n_exp;
+            const float v = ok ? a.logits[(size_t)t * a.n_exp + e1] : 0.f;
+            const unsigned long long key = moe_key(v, e1);
+            if (ok && c == 0) lv[t * a.n_exp + e1] = key;
+            __syncthreads();
+            rank_of(t, e1, v, key);
+            __syncthreads();
+        }
     }
     LE_TRACE_POINT(12);
     LE_TRACE_POINT(13);
@@ -1802,6 +1851,7 @@ __device__ void moe_gu_fast(const MoeArgs &a) {
     /* 1. every token's activations (n_tok * ng <= XR * 1024 groups), clamped and unpredicated */
     LE_TRACE_DECL;
     LE_TRACE_POINT(0);
+    const MoeLogits lgt = moe_route_load(a); /* first, so routing waits for these loads alone */
 #if defined(LE_TRACE)
     le_tr_[6] = __builtin_amdgcn_s_memtime();
 #endif
@@ -1815,7 +1865,7 @@ __device__ void moe_gu_fast(const MoeArgs &a) {
         hb[r] = *(const LE_GLOBAL float4 *)(src + 4);
     }
     load_tables<TG>(tab);
-    moe_route_par(a, R, lv, sx LE_TRACE_ARG);
+    moe_route_par(a, R, lv, sx, lgt LE_TRACE_ARG);
     LE_TRACE_POINT(1);
     const int z = blockIdx.y;
     if (z >= R.U) return;
@@ -1962,9 +2012,10 @@ __device__ void moe_down_fast(const MoeArgs &a) {
     __shared__ float sx[LE_MOE_FAST_TOK * LE_MOE_MAXK];
     __shared__ u32 tab[F::TABLES ? 256 + 512 : 1];
     extern __shared__ uint4 smem[];
+    const MoeLogits lgt = moe_route_load(a);
     load_tables<TD>(tab);
     LE_TRACE_DECL;
-    moe_route_par(a, R, lv, sx LE_TRACE_ARG);
+    moe_route_par(a, R, lv, sx, lgt LE_TRACE_ARG);
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int K = a.ff, nsb = K >> 8, ng = K >> 3;
     const int img_bytes = le_xtok_bytes(K);
@@ -2083,6 +2134,7 @@ __device__ __forceinline__ void moe_gum_body(const MoeArgs &a) {
     uint4 *wb = stg + wave * NI * 64;
     LE_TRACE_DECL;
     LE_TRACE_POINT(0);
+    const MoeLogits lgt = moe_route_load(a); /* first, so routing waits for these loads alone */
     /* 1. every token's activations, 16 values per (thread, r), clamped and unpredicated */
     const int nseg = a.n_tok * SEGT;
     float4 hv[XR][4];
@@ -2091,7 +2143,7 @@ __device__ __forceinline__ void moe_gum_body(const MoeArgs &a) {
         const int e = min((int)threadIdx.x + NT * r, nseg - 1);
         mq_load_seg(a.h + (size_t)(e / SEGT) * K, e % SEGT, hv[r]);
     }
-    moe_route_par(a, R, (unsigned long long *)stg, sx LE_TRACE_ARG);
+    moe_route_par(a, R, (unsigned long long *)stg, sx, lgt LE_TRACE_ARG);
     LE_TRACE_POINT(1);
     const int z = blockIdx.y;
     if (z >= R.U) return; /* uniform over the block */
@@ -2400,6 +2452,7 @@ __device__ __forceinline__ void moe_fus_body(const MoeArgs &a) {
     uint4 *wb = stg + wave * NI * 64;
     LE_TRACE_DECL;
     LE_TRACE_POINT(0);
+    const MoeLogits lgt = moe_route_load(a); /* first, so routing waits for these loads alone */
     /* every token's activations */
     const int nseg = a.n_tok * SEGT;
     float4 hv[XR][4];
@@ -2408,7 +2461,7 @@ __device__ __forceinline__ void moe_fus_body(const MoeArgs &a) {
         const int e = min((int)threadIdx.x + NT * r, nseg - 1);
         mq_load_seg(a.h + (size_t)(e / SEGT) * K, e % SEGT, hv[r]);
     }
-    moe_route_par(a, R, (unsigned long long *)stg, sx LE_TRACE_ARG);
+    moe_route_par(a, R, (unsigned long long *)stg, sx, lgt LE_TRACE_ARG);
     LE_TRACE_POINT(1);
     const int ngu = (a.ff >> 5) * R.U, ntile = a.hidden >> 4;
     const int b = blockIdx.x, G = gridDim.x;
