@@ -450,12 +450,13 @@ __device__ __forceinline__ void gm_q4k_body(const GmArgs &a, const u8 *ws) {
  * tokens as the rows of v_mfma_f32_16x16x32_f16: one MFMA per sub-block covers every token, its
  * K slice is the sub-block's 32 values, and B holds the exact fp16 codes sc_j * q (gm_q4k_frag),
  * so the sub-block scales need no per-token work. D2 = sum_j m_j S_j(t) is one more MFMA of the
- * sum records (high halves in K 0-7, low halves in K 8-15) against the mins. The activations
- * come from the pre-pass (le_gm_xprep, one fp16 plane) and each wave copies its super-blocks of
- * all T tokens into LDS once. MFMA rows past T repeat token rows (finite, never stored). */
+ * sum records (high halves in K 0-7, low halves in K 8-15) against the mins. Each wave builds
+ * the fp16 activations (rounded as the GEMM pre-pass rounds them) and sub-block sums of its
+ * super-blocks of all T tokens in LDS once per block. MFMA rows past T repeat token rows
+ * (finite, never stored). */
 struct MhArgs {
     const u8 *w;
-    const u8 *ws;
+    const float *x;
     float *y;
     int rows, cols, m;
 };
@@ -500,30 +501,39 @@ __device__ __forceinline__ void mh_q4k_body(const MhArgs &a) {
         }
     };
     issue(min((int)blockIdx.x, ntile - 1), active ? sfirst : 0);
-    /* the wave's activations: chunk c = (local sb, token, 16-byte column of the 512) */
+    /* the wave's activations, built here: chunk c = (local sb, token, 8-value column of the
+     * 256) -> 16 bytes of fp16 in the order 0,2,1,3 within each four (the order of the B
+     * fragments); the four lanes of a 32-value sub-block add their sums, which go into the
+     * token's record as fp16 high and low halves */
     if (active) {
-        const _Float16 *Xh = (const _Float16 *)a.ws;
-        const uint4 *Xs = (const uint4 *)(a.ws + (size_t)M * K * 4);
         const int nch = nsbw * T * 32;
-        for (int c0 = 0; c0 < nch; c0 += 64 * 8) {
-            uint4 v[8];
+        for (int c0 = 0; c0 < nch; c0 += 64 * 4) {
+            float4 v[4][2];
 #pragma unroll
-            for (int u = 0; u < 8; u++) {
+            for (int u = 0; u < 4; u++) {
                 const int c = min(c0 + 64 * u + lane, nch - 1), l = c / (T * 32), t = (c / 32) % T, col = c & 31;
-                v[u] = ldg16c((const u8 *)(Xh + (size_t)min(tok0 + t, M - 1) * K + 256 * gsb(l) + 8 * col));
+                const float *src = a.x + (size_t)min(tok0 + t, M - 1) * K + 256 * gsb(l) + 8 * col;
+                v[u][0] = *(const LE_GLOBAL float4 *)src;
+                v[u][1] = *(const LE_GLOBAL float4 *)(src + 4);
             }
 #pragma unroll
-            for (int u = 0; u < 8; u++) {
-                const int c = c0 + 64 * u + lane;
-                if (c < nch) {
-                    const int l = c / (T * 32), t = (c / 32) % T, col = c & 31;
-                    img[((l * 8 + (col >> 2)) * T + t) * 4 + (col & 3)] = v[u];
+            for (int u = 0; u < 4; u++) {
+                if (c0 + 64 * u >= nch) break; /* wave-uniform: nch is a multiple of 64 */
+                const int c = c0 + 64 * u + lane, l = c / (T * 32), t = (c / 32) % T, col = c & 31;
+                const float4 p = v[u][0], q = v[u][1];
+                const le_h2 h0 = {(_Float16)p.x, (_Float16)p.z}, h1 = {(_Float16)p.y, (_Float16)p.w};
+                const le_h2 h2 = {(_Float16)q.x, (_Float16)q.z}, h3 = {(_Float16)q.y, (_Float16)q.w};
+                img[((l * 8 + (col >> 2)) * T + t) * 4 + (col & 3)] = make_uint4(as_u32(h0), as_u32(h1), as_u32(h2), as_u32(h3));
+                float sm = ((p.x + p.y) + (p.z + p.w)) + ((q.x + q.y) + (q.z + q.w));
+                sm += __shfl_xor(sm, 1);
+                sm += __shfl_xor(sm, 2);
+                if ((col & 3) == 0) {
+                    const _Float16 hi = (_Float16)sm, lo = (_Float16)(sm - (float)hi);
+                    _Float16 *rec = (_Float16 *)(srec + (l * T + t) * 2);
+                    rec[col >> 2] = hi;
+                    rec[8 + (col >> 2)] = lo;
                 }
             }
-        }
-        for (int c = lane; c < nsbw * T * 2; c += 64) {
-            const int l = c / (T * 2), t = (c >> 1) % T;
-            srec[c] = ldg16c((const u8 *)(Xs + 2 * ((size_t)min(tok0 + t, M - 1) * nsb + gsb(l)) + (c & 1)));
         }
     }
     const int ta = n % T; /* this lane's A row (token); rows past T repeat earlier tokens */

@@ -586,10 +586,9 @@ int le_moe_layer(le_ctx *c, int ty_gate, int ty_up, int ty_down, const void *gat
     return c->launch(name, dim3((unsigned)(hidden / 8)), fast_dn ? 512 : 256, fast_dn ? 49152 : 0, (hipStream_t)stream, args);
 }
 
-/* Q4_K with 3..8 tokens: the pre-pass (one fp16 plane and the sum records) and the staged f16
- * MFMA kernel, T = 4 or 8 tokens per weight pass. Returns 1 when no instantiated shape fits. */
-static int mh_launch(le_ctx *c, const void *w, const float *x, int m, float *y, int rows, int cols, void *ws,
-                     hipStream_t st) {
+/* Q4_K with 3..8 (or 16) tokens: the staged f16 MFMA kernel, T = 4, 8 or 16 tokens per weight
+ * pass (it builds its fp16 activations itself). Returns 1 when no instantiated shape fits. */
+static int mh_launch(le_ctx *c, const void *w, const float *x, int m, float *y, int rows, int cols, hipStream_t st) {
     const long long ntile = (rows + 15) / 16;
     const int nsb = cols / 256, T = m <= 4 ? 4 : m <= 8 ? 8 : 16;
     /* (P, NW) in order of preference, measured on 14336 x 4096 (T=4: 15.0 us with (2,4); T=8:
@@ -617,18 +616,8 @@ static int mh_launch(le_ctx *c, const void *w, const float *x, int m, float *y, 
             const void *w;
             const float *x;
             float *y;
-            int rows, cols, m, ksplit, split;
-        } pa{w, x, y, rows, cols, m, 1, 0};
-        void *pargs[] = {&pa, &ws};
-        const long long waves = (long long)m * nsb;
-        int rc = c->launch("le_gm_xprep", dim3((unsigned)((waves + 3) / 4)), 256, 0, st, pargs);
-        if (rc) return rc;
-        struct {
-            const void *w;
-            const void *ws;
-            float *y;
             int rows, cols, m;
-        } a{w, ws, y, rows, cols, m};
+        } a{w, x, y, rows, cols, m};
         void *args[] = {&a};
         return c->launch(name, dim3((unsigned)gx, 1, 1), NW * 64, lds, st, args);
     }
@@ -652,7 +641,7 @@ int le_gemm(le_ctx *c, int ty, const void *w, const float *x, int m, float *y, i
             return c->fail(LE_ERR_WORKSPACE, "workspace needs %zu bytes", le_gemm_workspace_size(ty, m, cols));
         if (!al16(x) || !al16(ws)) return c->fail(LE_ERR_ALIGN, "x and ws must be 16-byte aligned");
         if (few) {
-            const int rc = mh_launch(c, w, x, m, y, rows, cols, ws, (hipStream_t)stream);
+            const int rc = mh_launch(c, w, x, m, y, rows, cols, (hipStream_t)stream);
             if (rc != 1) return rc;
         }
         /* tiles: 32*TM tokens x 128*TN rows: 32 x 256 up to 64 tokens, 64 x 128 above (the
