@@ -1501,9 +1501,23 @@ __device__ __forceinline__ MoeRouteGeom moe_route_geom(const MoeArgs &a) {
 struct MoeLogits {
     float v[MOE_LPASS];
 };
+/* 2..(waves) tokens, at most 256 experts: one wave selects each token's top-k (k rounds of a
+ * wave-wide max; lane l holds experts l*per .. l*per+per-1) instead of ranking every key */
+__device__ __forceinline__ bool moe_route_by_wave(const MoeArgs &a) {
+    return a.n_tok >= 2 && a.n_tok <= (int)(blockDim.x >> 6) && a.n_exp <= 256;
+}
 __device__ __forceinline__ MoeLogits moe_route_load(const MoeArgs &a) {
-    const MoeRouteGeom g = moe_route_geom(a);
     MoeLogits L;
+    if (moe_route_by_wave(a)) {
+        const int lane = threadIdx.x & 63, t = threadIdx.x >> 6, per = (a.n_exp + 63) >> 6;
+#pragma unroll
+        for (int j = 0; j < MOE_LPASS; j++) {
+            const int e = lane * per + j;
+            L.v[j] = t < a.n_tok && j < per && e < a.n_exp ? a.logits[(size_t)t * a.n_exp + e] : 0.f;
+        }
+        return L;
+    }
+    const MoeRouteGeom g = moe_route_geom(a);
     const int t1 = threadIdx.x / (g.tpt * g.C), e = (threadIdx.x / g.C) % g.tpt;
 #pragma unroll
     for (int p = 0; p < MOE_LPASS; p++) {
@@ -1544,7 +1558,41 @@ __device__ __forceinline__ void moe_route_par(const MoeArgs &a, MoeRoute &R, uns
         }
     };
     const int t1 = threadIdx.x / (tpt * C), e1 = (threadIdx.x / C) % tpt;
-    if (g.npass <= MOE_LPASS) {
+    if (moe_route_by_wave(a)) {
+        __syncthreads(); /* the mask clear above, before the atomics */
+        const int lane = threadIdx.x & 63, t = threadIdx.x >> 6, per = (a.n_exp + 63) >> 6;
+        if (t < a.n_tok) {
+            bool taken[MOE_LPASS];
+#pragma unroll
+            for (int j = 0; j < MOE_LPASS; j++) taken[j] = !(j < per && lane * per + j < a.n_exp);
+            for (int r = 0; r < a.k; r++) {
+                /* the lane's best untaken key (strict >: the lower expert of equal logits), then
+                 * the wave's largest; among tied lanes the lowest holds the lowest expert */
+                float bv = -INFINITY;
+                int bj = -1;
+#pragma unroll
+                for (int j = 0; j < MOE_LPASS; j++)
+                    if (!taken[j] && (bj < 0 || L.v[j] > bv)) { bv = L.v[j]; bj = j; }
+                const float mx = wave_max(bj >= 0 ? bv : -INFINITY);
+                const unsigned long long cand = __ballot(bj >= 0 && bv == mx);
+                const int wl = __ffsll((long long)cand) - 1;
+                if (lane == wl) {
+#pragma unroll
+                    for (int j = 0; j < MOE_LPASS; j++)
+                        if (j == bj) taken[j] = true;
+                    const int e = lane * per + bj;
+                    R.topi[t * a.k + r] = e;
+                    sx[t * a.k + r] = bv;
+                    atomicOr(&R.mask[e], 1ull << t);
+                }
+            }
+        }
+        LE_TRACE_POINT(8);
+        LE_TRACE_POINT(9);
+        LE_TRACE_POINT(10);
+        __syncthreads();
+        LE_TRACE_POINT(11);
+    } else if (g.npass <= MOE_LPASS) {
         /* every pass's keys in LDS, one barrier, every pass ranked, one barrier */
 #pragma unroll
         for (int p = 0; p < MOE_LPASS; p++) {

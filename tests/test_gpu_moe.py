@@ -78,6 +78,20 @@ def test_moe_tied_logits_lower_index_first(engine):
     run(engine, le.Q4_K, le.Q6_K, n_exp, k, 256, 256, n_tok, seed=5, lg=lg)
 
 
+def test_moe_tied_logits_staged(engine):
+    """Ties on the single-launch path (hidden 2048, 128 experts, 4 tokens: one wave selects each
+    token's top-k): equal logits go to the lower expert index, and -0 ties with +0."""
+    n_tok, n_exp, k = 4, 128, 8
+    lg = acts(n_tok * n_exp, 91).reshape(n_tok, n_exp).astype(np.float32)
+    lg[0, [5, 64, 65, 127]] = 3.0            # tied at the top, across lanes and within a lane
+    lg[1, :] = 0.5                           # every expert tied
+    lg[2, :] = -1.0
+    lg[2, [7, 100]] = 0.0
+    lg[2, [3, 90]] = -0.0                    # -0 ties with +0: experts 3, 7, 90, 100 in index order
+    lg[3, ::2] = 2.0                         # 64 tied, more than k
+    run(engine, le.Q4_K, le.Q6_K, n_exp, k, 2048, 256, n_tok, seed=9, lg=lg)
+
+
 def test_moe_errors(engine):
     import torch
     z = torch.zeros(1 << 20, dtype=torch.uint8, device="cuda")
