@@ -1502,7 +1502,8 @@ struct MoeLogits {
     float v[MOE_LPASS];
 };
 /* 2..(waves) tokens, at most 256 experts: one wave selects each token's top-k (k rounds of a
- * wave-wide max; lane l holds experts l*per .. l*per+per-1) instead of ranking every key */
+ * wave-wide max; lane l holds experts l*per .. l*per+per-1) instead of ranking every key. One
+ * token keeps the ranking, spread over eight lanes per expert (measured faster there). */
 __device__ __forceinline__ bool moe_route_by_wave(const MoeArgs &a) {
     return a.n_tok >= 2 && a.n_tok <= (int)(blockDim.x >> 6) && a.n_exp <= 256;
 }
