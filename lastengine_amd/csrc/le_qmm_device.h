@@ -35,10 +35,13 @@ typedef uint32_t u32;
 #endif
 #define LE_XSPLIT 16256.0f /* 127 * 128: |v| <= 16256 so xh = (v+64)>>7 in [-127,127], xl in [-64,63] */
 
-typedef uint2 __attribute__((aligned(2))) le_uint2_a2;
-typedef uint4 __attribute__((aligned(2))) le_uint4_a2;
 typedef u32 __attribute__((aligned(2))) le_u32_a2;
 typedef u32 le_v4u __attribute__((ext_vector_type(4)));
+typedef u32 le_v2u __attribute__((ext_vector_type(2)));
+/* 2-byte aligned native vectors: a load of the HIP struct types uint4 / uint2 at this alignment is
+ * split into scalar loads through a generic pointer, which the backend re-merges as a flat load */
+typedef le_v4u __attribute__((aligned(2))) le_v4u_a2;
+typedef le_v2u __attribute__((aligned(2))) le_v2u_a2;
 
 /* Global loads (never flat: flat loads also count against the LDS wait counter). */
 __device__ __forceinline__ uint4 ldg16(const u8 *p) { /* 16-byte aligned, streamed once */
@@ -49,8 +52,14 @@ __device__ __forceinline__ uint4 ldg16c(const u8 *p) { /* 16-byte aligned, cache
     const le_v4u v = *(const LE_GLOBAL le_v4u *)p;
     return make_uint4(v.x, v.y, v.z, v.w);
 }
-__device__ __forceinline__ uint4 ldg16u(const u8 *p) { return *(const LE_GLOBAL le_uint4_a2 *)p; }
-__device__ __forceinline__ uint2 ldg8u(const u8 *p) { return *(const LE_GLOBAL le_uint2_a2 *)p; }
+__device__ __forceinline__ uint4 ldg16u(const u8 *p) { /* 2-byte aligned */
+    const le_v4u v = *(const LE_GLOBAL le_v4u_a2 *)p;
+    return make_uint4(v.x, v.y, v.z, v.w);
+}
+__device__ __forceinline__ uint2 ldg8u(const u8 *p) {
+    const le_v2u v = *(const LE_GLOBAL le_v2u_a2 *)p;
+    return make_uint2(v.x, v.y);
+}
 __device__ __forceinline__ u32 ldg4u(const u8 *p) { return *(const LE_GLOBAL le_u32_a2 *)p; }
 __device__ __forceinline__ u32 ldg2(const u8 *p) { return *(const LE_GLOBAL uint16_t *)p; }
 
