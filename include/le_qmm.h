@@ -78,13 +78,14 @@ const char *le_last_error(const le_ctx *ctx);
  *     "ms_piq" (IQ2_XXS, IQ3_XXS), and "mq6" / "mqiq" (0/1) for the Q6_K / IQ staged kernels;
  *     "ms_t" (0/1): Q4_K with 2..8 tokens per pass on the staged kernel (one weight stream, 8 tokens
  *     per MFMA pass), used by le_gemm below "gm_min_m" tokens
- *   GEMM: "gm_mh" (0/1) Q4_K with 3..8 tokens on the staged f16 MFMA kernel (tokens as MFMA rows),
- *     "gm_mh_max" its largest M (8, or 16: one block per CU, where K <= 4096 fits its LDS),
+ *   GEMM: "gm_mh" (0/1) Q4_K with 3..16 tokens on the staged f16 MFMA kernel (tokens as MFMA rows),
+ *     "gm_mh_max" its largest M (16, the default, where K <= 4096 fits its LDS; or 8),
  *     "gm_mh_shape" its (super-blocks per step, waves) as 10 P + NW (0 auto, 14, 18, 24, 22),
  *     "gm_min_m" smallest M on the MFMA GEMM, "gm_tile" (0 auto, 11, 12, 21, 22),
  *     "gm_ksplit" K slices (0 auto, 1, 2, 4, 8), "gm_pc" producer/consumer waves (0/1),
  *     "gm_split" activation precision on the matrix cores: 0 (default) rounds each value to fp16
- *     (relative error 2^-11 per value), 1 carries a second fp16 half (about 2^-22 per value)
+ *     (relative error 2^-11 per value), 1 carries a second fp16 half (about 2^-22 per value) and
+ *     so also sends 3..16 tokens to the GEMM
  *   MoE: "moe_mfma" staged kernels (0/1), "moe_fused" single launch (0/1), "moe_fused_min_tok",
  *     "moe_fast" decode-shaped vector kernels (0/1) */
 int le_set_option(le_ctx *ctx, const char *name, int value);
@@ -108,9 +109,10 @@ int le_matvec(le_ctx *ctx, int ty, const void *const *ptrs, const void *w, const
  * Y[t * rows + r] = W[r,:] . X[t * cols ...] for t < m. ws: device workspace of
  * le_gemm_workspace_size(ty, m, cols) bytes (may be 0 bytes / NULL when that size is 0), the
  * counterpart of the reference's pre-quantized activation buffers (xqb/xdb/xsb, src/gpu.rs:210).
- * Q4_K runs on the matrix cores: m >= 9 on the fp16 MFMA GEMM, 3..8 tokens on the staged f16
- * MFMA kernel (both take the activations rounded to fp16, so |x| < 65504), 2 tokens on the
- * staged int8 matvec with several tokens per weight pass (options "gm_mh", "gm_min_m"). */
+ * Q4_K runs on the matrix cores: 3..16 tokens on the staged f16 MFMA kernel (up to 8 where K >
+ * 4096), more on the fp16 MFMA GEMM (both take the activations rounded to fp16, so
+ * |x| < 65504), 2 tokens on the staged int8 matvec with several tokens per weight pass (options
+ * "gm_mh", "gm_mh_max", "gm_min_m"). */
 size_t le_gemm_workspace_size(int ty, int m, int cols);
 int le_gemm(le_ctx *ctx, int ty, const void *w, const float *x, int m, float *y, int rows, int cols, void *ws,
             size_t ws_bytes, le_stream_t stream);

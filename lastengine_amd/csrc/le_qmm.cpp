@@ -69,7 +69,7 @@ struct le_ctx {
     int ms = 1, ms_p = 2;    /* staged MFMA variant and its super-blocks per row and step */
     int ms_t = 1;            /* Q4_K with 2..8 tokens per pass on the staged MFMA kernel */
     int gm_mh = 1;           /* le_gemm, Q4_K, 3..8 tokens: the staged f16 MFMA kernel */
-    int gm_mh_max = 8;       /* ... up to this many tokens (8 or 16) */
+    int gm_mh_max = 16;      /* ... up to this many tokens (8 or 16; 16 only where K fits its LDS) */
     int gm_mh_shape = 0;     /* ... its (P, NW) as 10 * P + NW: 0 auto, 14, 18, 24, 22 */
     int mq6 = 1, ms_p6 = 2;  /* Q6_K decode matvec on the staged MFMA kernels, super-blocks per step */
     int mqiq = 1, ms_piq = 2; /* IQ2_XXS / IQ3_XXS likewise */
@@ -633,8 +633,10 @@ size_t le_gemm_workspace_size(int ty, int m, int cols) {
 int le_gemm(le_ctx *c, int ty, const void *w, const float *x, int m, float *y, int rows, int cols, void *ws,
             size_t ws_bytes, le_stream_t stream) {
     if (!c) return LE_ERR_ARG;
-    /* 3..8 tokens: the staged f16 kernel (2 tokens: the int8 multi-token matvec is faster) */
-    const bool few = ty == LE_TYPE_Q4_K && c->gm_mh && m >= 3 && m <= c->gm_mh_max;
+    /* 3..16 tokens: the staged f16 kernel (2 tokens: the int8 multi-token matvec is faster);
+     * shapes whose activations do not fit its LDS, and gm_split=1 (two fp16 halves, which only
+     * the GEMM carries), go to the GEMM */
+    const bool few = ty == LE_TYPE_Q4_K && c->gm_mh && !c->gm_split && m >= 3 && m <= c->gm_mh_max;
     if (ty == LE_TYPE_Q4_K && (m >= c->gm_min_m || few) && m > 0 && rows > 0 && cols > 0 && cols % 256 == 0 && w && x && y) {
         if (!ws) return c->fail(LE_ERR_ARG, "null workspace");
         if (ws_bytes < le_gemm_workspace_size(ty, m, cols))

@@ -248,15 +248,14 @@ def test_error_codes(engine):
 @pytest.mark.parametrize("rows,cols", [(300, 4096), (64, 2048), (1000, 1024), (4100, 512)])
 def test_gemm_few_tokens_staged(fresh_engine, path, m, rows, cols):
     """Few tokens on the staged kernels: the f16 MFMA kernel for 3..8 tokens (tokens as MFMA
-    rows, T = 4 or 8; up to 16 with gm_mh_max=16) and the int8 multi-token matvec (T = 2, 4 or 8 per pass, option gm_mh=0),
+    rows, T = 4 or 8, and 16 under the default gm_mh_max=16) and the int8 multi-token matvec (T = 2, 4 or 8 per pass, option gm_mh=0),
     with partial token groups (3, 5, 11), a second group (11 > 8 on the int8 kernel) and ragged
     row tiles."""
     import torch
     engine = fresh_engine
     engine.set_option("gm_min_m", 64)
     engine.set_option("gm_mh", 0 if path == "int8" else 1)
-    if path == "f16x16":
-        engine.set_option("gm_mh_max", 16)
+    engine.set_option("gm_mh_max", 16 if path == "f16x16" else 8)
     ty = le.Q4_K
     q, _ = weights(ty, rows, cols, seed=31 + m)
     xs = np.stack([acts(cols, 6000 + 17 * m + t) for t in range(m)])
@@ -294,7 +293,7 @@ def test_options_validated(fresh_engine):
     """Every documented launch-policy knob is accepted with a valid value; bad names and values
     are refused with LE_ERR_ARG and leave the context usable."""
     good = {"mv_block": 512, "mv_blocks_per_cu": 1, "mv_shape": 0, "mq": 1, "ms": 1, "mq_waves": 4, "mq_steps": 2,
-            "mq_blocks_per_cu": 2, "mq_waves_auto": 1, "ms_p": 2, "ms_p6": 2, "ms_piq": 2, "mq6": 1, "mqiq": 1, "ms_t": 1, "gm_mh": 1, "gm_mh_shape": 0, "gm_mh_max": 8, "gm_min_m": 5,
+            "mq_blocks_per_cu": 2, "mq_waves_auto": 1, "ms_p": 2, "ms_p6": 2, "ms_piq": 2, "mq6": 1, "mqiq": 1, "ms_t": 1, "gm_mh": 1, "gm_mh_shape": 0, "gm_mh_max": 16, "gm_min_m": 5,
             "gm_tile": 0, "gm_ksplit": 0, "gm_pc": 1, "gm_split": 0, "moe_mfma": 1, "moe_fused": 1, "moe_fused_min_tok": 3,
             "moe_fast": 1}
     engine = fresh_engine
