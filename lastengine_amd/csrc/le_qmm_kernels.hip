@@ -2077,7 +2077,6 @@ __device__ void moe_down_fast(const MoeArgs &a) {
     }
     for (int i = threadIdx.x; i < NW * LE_MOE_FAST_TOK * 8; i += blockDim.x) (&red[0][0][0])[i] = 0.f;
     __syncthreads();
-    const u8 *img0 = in_lds ? (const u8 *)smem : a.ws;
     const size_t rbd = (size_t)nsb * F::SB;
     const int li = lane & 7, rr = lane >> 3, row = 8 * blockIdx.x + rr;
     Raw ra[SM], rb2[SM];
@@ -2086,7 +2085,10 @@ __device__ void moe_down_fast(const MoeArgs &a) {
 #pragma unroll
         for (int s = 0; s < SM; s++) r[s] = F::load(Wd + (size_t)min(s, nsb - 1) * F::SB, li);
     };
-    auto consume = [&](int z, Raw (&r)[SM]) {
+    /* img0 is either LDS or the workspace; each call site passes one of them, so the image reads
+     * compile to LDS or global loads (a pointer that could be either becomes a flat load, which
+     * also waits on the LDS counter) */
+    auto consume = [&](int z, Raw (&r)[SM], const u8 *img0) {
         const int e = R.grp_e[z];
         const int nmem = __popcll(R.mask[e]);
         int tt[8];
@@ -2128,17 +2130,23 @@ __device__ void moe_down_fast(const MoeArgs &a) {
             }
         }
     };
-    int z = wave;
-    if (z < R.U) issue(z, ra);
-    while (z < R.U) {
-        if (z + NW < R.U) issue(z + NW, rb2);
-        consume(z, ra);
-        z += NW;
-        if (z >= R.U) break;
-        if (z + NW < R.U) issue(z + NW, ra);
-        consume(z, rb2);
-        z += NW;
-    }
+    auto groups = [&](const u8 *img0) {
+        int z = wave;
+        if (z < R.U) issue(z, ra);
+        while (z < R.U) {
+            if (z + NW < R.U) issue(z + NW, rb2);
+            consume(z, ra, img0);
+            z += NW;
+            if (z >= R.U) break;
+            if (z + NW < R.U) issue(z + NW, ra);
+            consume(z, rb2, img0);
+            z += NW;
+        }
+    };
+    if (in_lds)
+        groups((const u8 *)smem);
+    else
+        groups(a.ws);
     __syncthreads();
     for (int i = threadIdx.x; i < a.n_tok * 8; i += blockDim.x) {
         const int t = i >> 3, r = i & 7;

@@ -65,6 +65,13 @@ def test_moe_config4(engine, n_tok):
     run(engine, le.Q4_K, le.Q6_K, 128, 8, 2048, 768, n_tok, seed=100 + n_tok)
 
 
+@pytest.mark.parametrize("tg,td,n_tok,k", [(le.Q8_0, le.Q8_0, 2, 4), (le.Q8_0, le.Q8_0, 8, 4), (le.IQ2_XXS, le.IQ3_XXS, 8, 4)])
+def test_moe_vector_down_images(engine, tg, td, n_tok, k):
+    """The vector-ALU down kernel reads the pair images from LDS when they fit (2 tokens) and from
+    the workspace when they do not (8 tokens x 4 experts at ff 768: 73 KB)."""
+    run(engine, tg, td, 16, k, 512, 768, n_tok, seed=300 + n_tok + tg)
+
+
 def test_moe_many_tokens_shared_experts(engine):
     """More tokens than fit one member pass (8), so expert groups loop over member chunks."""
     run(engine, le.Q4_K, le.Q6_K, 4, 2, 256, 256, 20, seed=77)
