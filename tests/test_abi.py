@@ -37,6 +37,33 @@ def test_code_objects_built():
         assert os.path.getsize(os.path.join(qmm.LIB_DIR, "le_qmm_%s.hsaco" % part)) > 1000
 
 
+ROCM = os.environ.get("ROCM_PATH", "/opt/rocm")
+
+
+def test_code_objects_use_no_flat_memory_ops(tmp_path):
+    """Every kernel addresses global memory and LDS through typed instructions: a flat load or
+    store also counts against the LDS wait counter, so each LDS wait in a kernel would wait for
+    the weight loads in flight as well (checked on the disassembly of the built code objects)."""
+    import subprocess
+    bundler = os.path.join(ROCM, "llvm", "bin", "clang-offload-bundler")
+    objdump = os.path.join(ROCM, "llvm", "bin", "llvm-objdump")
+    if not (os.path.exists(bundler) and os.path.exists(objdump)):
+        pytest.skip("ROCm LLVM tools not installed")
+    lib = os.path.join(REPO, "lastengine_amd", "lib")
+    found = {}
+    for name in sorted(os.listdir(lib)):
+        if not name.endswith(".hsaco"):
+            continue
+        elf = str(tmp_path / (name + ".elf"))
+        subprocess.run([bundler, "--type=o", "--targets=hipv4-amdgcn-amd-amdhsa--gfx950",
+                        "--input=" + os.path.join(lib, name), "--output=" + elf, "--unbundle"], check=True)
+        asm = subprocess.run([objdump, "-d", elf], check=True, capture_output=True, text=True).stdout
+        n = len(re.findall(r"\bflat_(load|store|atomic)", asm))
+        if n:
+            found[name] = n
+    assert not found, found
+
+
 @pytest.mark.parametrize("ty,cols,want", [(8, 4096, 4352), (12, 4096, 2304), (14, 14336, 11760),
                                           (16, 4096, 1056), (18, 14336, 5488), (12, 2048, 1152),
                                           (14, 768, 630)])
