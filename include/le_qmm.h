@@ -117,6 +117,18 @@ size_t le_gemm_workspace_size(int ty, int m, int cols);
 int le_gemm(le_ctx *ctx, int ty, const void *w, const float *x, int m, float *y, int rows, int cols, void *ws,
             size_t ws_bytes, le_stream_t stream);
 
+/* ---- le_gemm without a workspace argument (no counterpart in the reference) ----
+ * For callers that cannot allocate device memory: code under HIP graph capture, tight serving
+ * loops, harnesses that forbid hipMalloc. Same result as le_gemm (same kernels), with the
+ * workspace taken from a device array the library holds per GPU for the life of the process
+ * (LE_GEMM_SCRATCH_BYTES). Allocates nothing. Returns LE_ERR_WORKSPACE when
+ * le_gemm_workspace_size(ty, m, cols) exceeds LE_GEMM_SCRATCH_BYTES (about m * cols <= 8M
+ * values). Every call on one GPU shares that array: calls that overlap on one GPU (two streams or
+ * two host threads) race and must be serialized by the caller. */
+#define LE_GEMM_SCRATCH_BYTES (32u << 20)
+int le_gemm_noalloc(le_ctx *ctx, int ty, const void *w, const float *x, int m, float *y, int rows, int cols,
+                    le_stream_t stream);
+
 /* ---- MoE expert layer, routed part (replaces the decode chain router_topk -> host read-back ->
  *      build_ptrs -> matvec gate/up -> swiglu -> quant_x -> matvec down -> moe_combine,
  *      src/gpu.rs:560-597, and the prefill expert grouping of src/gpu/prefill.rs:153-215; CPU twin

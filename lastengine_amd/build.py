@@ -26,6 +26,8 @@ PARTS["gm"] = []
 SOURCES = {"gm": "le_gemm_kernels.hip"}  # parts not listed here compile le_qmm_kernels.hip
 
 HOST_SOURCES = ["le_qmm.cpp", "le_quant.cpp"]
+# Host sources that declare device memory (hipcc, host and device passes), linked into the library.
+HIP_HOST_SOURCES = ["le_noalloc.hip"]
 
 
 def _run(cmd):
@@ -41,11 +43,21 @@ def code_object_cmd(part):
         os.path.join(CSRC, SOURCES.get(part, "le_qmm_kernels.hip")), "-o", os.path.join(LIB, "le_qmm_%s.hsaco" % part)]
 
 
+def hip_host_obj(src):
+    return os.path.join(LIB, os.path.splitext(src)[0] + ".o")
+
+
+def hip_host_cmd(src):
+    return [HIPCC, "-c", "-fPIC", "-I" + os.path.join(REPO, "include")] + DEVICE_FLAGS + [
+        os.path.join(CSRC, src), "-o", hip_host_obj(src)]
+
+
 def host_lib_cmd():
-    # Host-only C++: the HIP runtime API is used through its C headers, no device pass.
+    # Host C++: the HIP runtime API is used through its C headers; the hipcc-built objects carry
+    # the device arrays the host code addresses.
     return ["g++", "-O2", "-std=c++17", "-fPIC", "-shared", "-Wall", "-D__HIP_PLATFORM_AMD__",
             "-I" + ROCM + "/include", "-I" + CSRC, "-I" + os.path.join(REPO, "include")] + [
-        os.path.join(CSRC, s) for s in HOST_SOURCES] + [
+        os.path.join(CSRC, s) for s in HOST_SOURCES] + [hip_host_obj(s) for s in HIP_HOST_SOURCES] + [
         "-o", os.path.join(LIB, "lible_qmm.so"), "-L" + ROCM + "/lib", "-Wl,-rpath," + ROCM + "/lib",
         "-lamdhip64", "-lpthread", "-ldl"]
 
@@ -56,13 +68,16 @@ def oracle_cmd():
 
 def build(jobs=8, with_oracle=True, parts=None):
     os.makedirs(LIB, exist_ok=True)
-    cmds = [code_object_cmd(p) for p in (parts or PARTS)] + [host_lib_cmd()]
+    cmds = [code_object_cmd(p) for p in (parts or PARTS)] + [hip_host_cmd(s) for s in HIP_HOST_SOURCES]
     if with_oracle:
         cmds.append(oracle_cmd())
     with ThreadPoolExecutor(max_workers=jobs) as ex:
         for out in ex.map(_run, cmds):
             if out:
                 print(out)
+    out = _run(host_lib_cmd())  # links the hipcc objects built above
+    if out:
+        print(out)
 
 
 if __name__ == "__main__":

@@ -55,6 +55,9 @@ int table_bytes(int ty) {
 
 }  // namespace
 
+/* le_noalloc.hip: device address of the per-GPU GEMM scratch array */
+int le_scratch_attach(int device);
+
 struct le_ctx {
     int device = 0;
     int cus = 256;
@@ -393,6 +396,11 @@ int le_init(const char *lib_dir, le_ctx **out) {
         }
         c->mods.push_back(m);
     }
+    if (le_scratch_attach(dev) != LE_OK) {
+        for (hipModule_t mm : c->mods) (void)hipModuleUnload(mm);
+        delete c;
+        return LE_ERR_HIP;
+    }
     *out = c;
     return LE_OK;
 }
@@ -702,3 +710,7 @@ int le_gemm(le_ctx *c, int ty, const void *w, const float *x, int m, float *y, i
 }
 
 }  // extern "C"
+
+/* Context accessors for le_noalloc.hip. */
+int le_ctx_device(const le_ctx *c) { return c ? c->device : -1; }
+int le_ctx_fail(le_ctx *c, int code, const char *msg) { return c ? c->fail(code, "%s", msg) : code; }

@@ -61,6 +61,7 @@ def lib():
         "le_matvec": (I, [P, I, P, P, P, LL, P, I, I, I, P]),
         "le_gemm_workspace_size": (S, [I, I, I]),
         "le_gemm": (I, [P, I, P, P, I, P, I, I, P, S, P]),
+        "le_gemm_noalloc": (I, [P, I, P, P, I, P, I, I, P]),
         "le_moe_workspace_size": (S, [I, I, I]),
         "le_moe_layer": (I, [P, I, I, I, P, P, P, I, I, I, I, P, P, I, P, P, P, P, S, P]),
         "le_fill_normal": (None, [P, S, ctypes.c_uint64, ctypes.c_uint64, D, D, I]),
@@ -203,3 +204,9 @@ class Engine:
             ws_bytes = ws.numel() if hasattr(ws, "numel") else 0
         self._check(self._L.le_gemm(self._ctx, ty, _ptr(w), _ptr(x), m, _ptr(out), rows, cols, _ptr(ws), ws_bytes,
                                     _stream(stream)))
+
+    def gemm_noalloc(self, ty, w, x, m, out, rows, cols, stream=None):
+        """le_gemm with the library's per-GPU scratch array as workspace: allocates nothing
+        (for graph capture and serving loops). Calls overlapping on one GPU race."""
+        self._check(self._L.le_gemm_noalloc(self._ctx, ty, _ptr(w), _ptr(x), m, _ptr(out), rows, cols,
+                                            _stream(stream)))
