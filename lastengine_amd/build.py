@@ -23,7 +23,8 @@ PARTS = {"deq": ["-DLE_PART_DEQ"], "moe": ["-DLE_PART_MOE"]}
 for _ty in (8, 12, 14, 16, 18):
     PARTS["mv%d" % _ty] = ["-DLE_PART_MV=%d" % _ty]
 PARTS["gm"] = []
-SOURCES = {"gm": "le_gemm_kernels.hip"}  # parts not listed here compile le_qmm_kernels.hip
+PARTS["gq"] = []
+SOURCES = {"gm": "le_gemm_kernels.hip", "gq": "le_gq_kernels.hip"}  # parts not listed here compile le_qmm_kernels.hip
 
 HOST_SOURCES = ["le_qmm.cpp", "le_quant.cpp"]
 # Host sources that declare device memory (hipcc, host and device passes), linked into the library.

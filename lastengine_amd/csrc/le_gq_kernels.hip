@@ -1,0 +1,603 @@
+/* Quantized GEMM on the matrix cores for every supported type (gfx950):
+ *     Y[t, r] = W[r, :] . X[t, :],  t < M tokens, r < N rows, K = cols.
+ *
+ * Replaces the int8 MMA kernels mmq*_<ty> / mmq128r_<ty> behind DenseGpu::bmm and prefill::dense
+ * (src/cuda/kernels.cu:965-1235, src/gpu/dense.rs:181-199, src/gpu/prefill.rs:44-60); CPU twin
+ * cpu_ref::matmat (src/cpu_ref.rs:266-276).
+ *
+ * Operands. v_mfma_f32_32x32x16_f16 with the tokens as A (32 x 16) and the weight rows as B
+ * (16 x 32), fp32 accumulation. Lane l of a fragment holds token / row l % 32 and the eight K
+ * positions 8 (l / 32) .. +8 of the 16-value K chunk, stored in the order P8 = 0,2,1,3,4,6,5,7
+ * (what the byte-pair fp16 conversion below produces; the dot product does not depend on the
+ * order as long as A and B agree).
+ *
+ * Activations (pre-pass le_gq_xprep_*). Token t is scaled by 2^-e_t, e_t chosen so that
+ * max|x_t| 2^-e_t lies in [64, 128) (exact: a power of two), and rounded to fp16 (relative error
+ * 2^-11; values below 2^-24 of the token's maximum flush towards zero). The result is written in
+ * fragment order, [32-token tile][K/16 chunk][8-lane half][token][8 halves], so a block copies
+ * each step's activations as contiguous 8 KB runs and every A fragment is one conflict-free
+ * 16-byte LDS read per lane. Q4_K also gets per-super-block sub-block sums S_j (per 32 values,
+ * as fp16 high + low halves) for its offset term. The final store multiplies by
+ * 2^e_t, so the result does not depend on the activations' magnitude.
+ *
+ * Weights. Raw GGUF rows (src/gpu.rs:79-83), read in half super-blocks (128 values) per pipeline
+ * step: each row's bytes for the step are copied as 16-byte chunks (coalesced: consecutive lanes
+ * take consecutive chunks of a row) into a 16-byte-aligned LDS slot of F::SLOT bytes, then each
+ * lane builds its B fragments from them:
+ *   Q4_K   code sc_j * q (<= 945, exact), offset term D2 = sum_j m_j S_j (one more MFMA per
+ *          super-block), epilogue  acc += d * D1 - dmin * D2                 (src/quant.rs:72-82)
+ *   Q6_K   code (q6 - 32) * sc_u / 64 (exact where (q6 - 32) sc_u has at most 11 significant
+ *          bits, else rounded once to fp16), epilogue acc += 64 d * D1           (:96-112)
+ *   IQ2_XXS code (2s+1) * grid * sign (<= 1333, exact), epilogue acc += d/8 * D1   (:142-154)
+ *   IQ3_XXS code (2s+1) * grid * sign (<= 1922, exact), epilogue acc += d/4 * D1   (:127-141)
+ *   Q8_0   per-32 scale d_b inside the code: fp16(q * (64 d_b)) (one rounding, 2^-11 relative),
+ *          no epilogue, final * 2^-6 (fp16 range: |d_b| < 8, i.e. |w| < 1016)       (:68-71)
+ * Integer byte -> fp16 conversion: a byte u placed under the fp16 exponent of 1024 (v_perm_b32)
+ * is the half 1024 + u exactly; one packed fma (u+1024)*c - 1024*c gives u*c rounded once.
+ *
+ * Tiling. A block of WM x WN waves computes BM = 32 TM WM tokens x BN = 32 TN WN rows; a wave
+ * owns TM x TN 32x32 tiles. Steps are double-buffered in LDS; every thread holds two further
+ * steps of loads in registers (issued two steps before they are written to LDS), so the loads of
+ * steps s+2 and s+3 are in flight while step s computes. Blocks that share weight rows (same row
+ * tile, other token tiles or K slices) get the same blockIdx % 8 and therefore the same XCD and
+ * L2. K may be split over blockIdx.y; slices then add into Y with fp32 atomics (the pre-pass
+ * clears Y).
+ */
+#include "le_qmm_device.h"
+#include "le_iq_tables.h"
+
+typedef _Float16 le_h2 __attribute__((ext_vector_type(2)));
+typedef _Float16 le_v8h __attribute__((ext_vector_type(8)));
+typedef float le_v16f __attribute__((ext_vector_type(16)));
+
+__device__ const u32 le_gq_iq2_grid[512] = LE_IQ2XXS_GRID_WORDS;
+__device__ const u32 le_gq_iq3_grid[256] = LE_IQ3XXS_GRID_WORDS;
+
+struct GqArgs {
+    const u8 *w;
+    const float *x;
+    float *y;
+    int rows, cols, m;
+    int mp;     /* tokens rounded up to the largest token tile (the pre-pass pads with zeros) */
+    int ksplit; /* K slices (blockIdx.y), > 1: atomic adds into y, cleared by the pre-pass */
+};
+
+/* Workspace layout: A planes (mp * K halves), S records (mp/32 * nsb * SREC bytes), token scales
+ * (mp floats). */
+__host__ __device__ inline size_t gq_s_off(int mp, int K) { return (size_t)mp * K * 2; }
+__host__ __device__ inline size_t gq_t_off(int mp, int K, int srec) { return gq_s_off(mp, K) + (size_t)(mp / 32) * (K / 256) * srec; }
+
+__device__ __forceinline__ le_h2 as_h2(u32 v) { return __builtin_bit_cast(le_h2, v); }
+__device__ __forceinline__ u32 as_u32(le_h2 v) { return __builtin_bit_cast(u32, v); }
+__device__ __forceinline__ le_v8h as_v8h(uint4 v) { return __builtin_bit_cast(le_v8h, v); }
+
+/* bytes 0 and 2 (lo) or 1 and 3 (hi) of w, each under the fp16 exponent of 1024 */
+__device__ __forceinline__ u32 h1024_02(u32 w) { return __builtin_amdgcn_perm(0x64646464u, w, 0x04020400u); }
+__device__ __forceinline__ u32 h1024_13(u32 w) { return __builtin_amdgcn_perm(0x64646464u, w, 0x04030401u); }
+/* byte i of w duplicated into both halves under the exponent of 1024 */
+__device__ __forceinline__ u32 h1024_dup(u32 w, int i) {
+    const u32 sel = 0x04000400u | (u32)(i * 0x00010001);
+    return __builtin_amdgcn_perm(0x64646464u, w, sel);
+}
+__device__ __forceinline__ u32 pk_fma(u32 a, u32 b, u32 c) {
+    return as_u32(__builtin_elementwise_fma(as_h2(a), as_h2(b), as_h2(c)));
+}
+__device__ __forceinline__ u32 pk_add(u32 a, u32 b) { return as_u32(as_h2(a) + as_h2(b)); }
+__device__ __forceinline__ u32 pk_mul(u32 a, u32 b) { return as_u32(as_h2(a) * as_h2(b)); }
+__device__ __forceinline__ u32 h2dup(float f) {
+    const _Float16 h = (_Float16)f;
+    return as_u32((le_h2){h, h});
+}
+
+__device__ __forceinline__ void gq_barrier() {
+    __asm__ volatile("" ::: "memory");
+    __builtin_amdgcn_s_waitcnt(0xC07F); /* LDS only: the loads of later steps stay in flight */
+    __builtin_amdgcn_s_barrier();
+    __asm__ volatile("" ::: "memory");
+}
+
+template <int TM, int TN>
+__device__ __forceinline__ void gq_mma(le_v16f (&d)[TM][TN], const le_v8h (&A)[TM], const le_v8h (&B)[TN], bool zero) {
+#pragma unroll
+    for (int i = 0; i < TM; i++)
+#pragma unroll
+        for (int k = 0; k < TN; k++) d[i][k] = __builtin_amdgcn_mfma_f32_32x32x16_f16(A[i], B[k], zero ? (le_v16f){} : d[i][k], 0, 0, 0);
+}
+
+/* ============================ per-type formats ============================
+ * SBB: bytes per super-block; NCH 16-byte chunks per row and step, chunk k of half h read from
+ * byte goff(k, h) of the super-block into byte loff(k) of the row's slot; SREC: bytes of sum
+ * records per (32-token tile, super-block); EPI: 1 if the per-super-block epilogue is used. */
+template <int TY>
+struct GqF;
+
+template <>
+struct GqF<LE_TYPE_Q4_K> { /* slot: [0,16) header, [16,80) this half's 64 quant bytes */
+    static constexpr int SBB = 144, NCH = 5, SLOT = 80, SREC = 1024, EPI = 1, TAB = 0;
+    static constexpr bool ALIGNED = true;
+    __device__ static int goff(int k, int h) { return k == 0 ? 0 : 16 + 64 * h + 16 * (k - 1); }
+    __device__ static int loff(int k) { return 16 * k; }
+};
+template <>
+struct GqF<LE_TYPE_Q6_K> { /* slot: [0,64) ql half, [64,96) qh half, [96,112) sc[16], [112,128) bytes 194..209 (d at 126) */
+    static constexpr int SBB = 210, NCH = 8, SLOT = 128, SREC = 0, EPI = 1, TAB = 0;
+    static constexpr bool ALIGNED = false;
+    __device__ static int goff(int k, int h) {
+        return k < 4 ? 64 * h + 16 * k : k < 6 ? 128 + 32 * h + 16 * (k - 4) : k == 6 ? 192 : 194;
+    }
+    __device__ static int loff(int k) { return 16 * k; }
+};
+template <>
+struct GqF<LE_TYPE_Q8_0> { /* slot: [32b, 32b+32) quants of block b of the half, [128 + 16b] chunk starting at d_b */
+    static constexpr int SBB = 272, NCH = 12, SLOT = 192, SREC = 0, EPI = 0, TAB = 0;
+    static constexpr bool ALIGNED = false;
+    __device__ static int goff(int k, int h) {
+        return k < 8 ? 136 * h + 34 * (k >> 1) + 2 + 16 * (k & 1) : 136 * h + 34 * (k - 8);
+    }
+    __device__ static int loff(int k) { return 16 * k; }
+};
+template <>
+struct GqF<LE_TYPE_IQ2_XXS> { /* slot: [0,32) the half's four 8-byte block records, [32,48) bytes 0..15 (d at 32) */
+    static constexpr int SBB = 66, NCH = 3, SLOT = 48, SREC = 0, EPI = 1, TAB = 4096 + 2048;
+    static constexpr bool ALIGNED = false;
+    __device__ static int goff(int k, int h) { return k < 2 ? 2 + 32 * h + 16 * k : 0; }
+    __device__ static int loff(int k) { return 16 * k; }
+};
+template <>
+struct GqF<LE_TYPE_IQ3_XXS> { /* slot: [0,32) the half's grid indices, [32,48) its four aux words, [48,64) bytes 0..15 (d at 48) */
+    static constexpr int SBB = 98, NCH = 4, SLOT = 64, SREC = 0, EPI = 1, TAB = 2048 + 2048;
+    static constexpr bool ALIGNED = false;
+    __device__ static int goff(int k, int h) { return k < 2 ? 2 + 32 * h + 16 * k : k == 2 ? 66 + 16 * h : 0; }
+    __device__ static int loff(int k) { return 16 * k; }
+};
+
+/* IQ tables in LDS, in fragment order: grid entries as fp16 magnitudes (IQ2_XXS: 8 per entry, P8
+ * order; IQ3_XXS: 4 per entry, order 0,2,1,3), then for each 7-bit sign index the 8 half masks of
+ * ksign (src/quant.rs:57), 0x8000 where the value is negative, P8 order. */
+template <int TY>
+__device__ __forceinline__ void gq_tables(u8 *tab) {
+    if constexpr (TY == LE_TYPE_IQ2_XXS || TY == LE_TYPE_IQ3_XXS) {
+        constexpr int NG = 256, GB = TY == LE_TYPE_IQ2_XXS ? 16 : 8;
+        for (int i = threadIdx.x; i < NG; i += blockDim.x) {
+            if constexpr (TY == LE_TYPE_IQ2_XXS) {
+                const u32 w0 = le_gq_iq2_grid[2 * i], w1 = le_gq_iq2_grid[2 * i + 1];
+                *(uint4 *)(tab + GB * i) = make_uint4(pk_add(h1024_02(w0), 0xE400E400u), pk_add(h1024_13(w0), 0xE400E400u),
+                                                      pk_add(h1024_02(w1), 0xE400E400u), pk_add(h1024_13(w1), 0xE400E400u));
+            } else {
+                const u32 w0 = le_gq_iq3_grid[i];
+                *(uint2 *)(tab + GB * i) = make_uint2(pk_add(h1024_02(w0), 0xE400E400u), pk_add(h1024_13(w0), 0xE400E400u));
+            }
+        }
+        u8 *sg = tab + NG * GB;
+        for (int i = threadIdx.x; i < 128; i += blockDim.x) {
+            const u32 ks = (u32)i | ((__builtin_popcount((u32)i) & 1u) << 7);
+            u32 m[4];
+#pragma unroll
+            for (int p = 0; p < 4; p++) { /* halves 2p, 2p+1 hold values P8(2p), P8(2p+1) */
+                const int v0 = (p & 2) * 2 + (p & 1), v1 = v0 + 2;
+                m[p] = (((ks >> v0) & 1u) << 15) | (((ks >> v1) & 1u) << 31);
+            }
+            *(uint4 *)(sg + 16 * i) = make_uint4(m[0], m[1], m[2], m[3]);
+        }
+    }
+}
+
+/* ============================ activation pre-pass ============================ */
+/* One block of 256 threads per (padded) token. SK: 0 no sums, 1 per-32 sums (Q4_K), 2 per-16
+ * sums (Q6_K). */
+template <int SK>
+__device__ __forceinline__ void gq_xprep_body(const GqArgs &a, u8 *ws) {
+    __shared__ float red[4];
+    const int K = a.cols, nsb = K >> 8, t = blockIdx.x, tid = threadIdx.x, lane = tid & 63;
+    if (a.ksplit > 1) { /* the slices add into y */
+        const size_t ny = (size_t)a.m * a.rows;
+        for (size_t i = (size_t)blockIdx.x * blockDim.x + tid; i < ny; i += (size_t)gridDim.x * blockDim.x) a.y[i] = 0.f;
+    }
+    const bool live = t < a.m;
+    const LE_GLOBAL float *xr = (const LE_GLOBAL float *)(a.x + (size_t)(live ? t : 0) * K);
+    float am = 0.f;
+    if (live)
+        for (int i = tid; i < K / 4; i += 256) {
+            const float4 v = ((const LE_GLOBAL float4 *)xr)[i];
+            am = fmaxf(am, fmaxf(fmaxf(fabsf(v.x), fabsf(v.y)), fmaxf(fabsf(v.z), fabsf(v.w))));
+        }
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) am = fmaxf(am, __shfl_xor(am, o));
+    if (lane == 0) red[tid >> 6] = am;
+    __syncthreads();
+    am = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
+    int ex = 0;
+    if (am > 0.f && am <= 3.0e38f) {
+        (void)frexpf(am, &ex); /* am = f 2^ex, f in [0.5, 1) */
+        ex = max(ex - 7, -100);
+    }
+    const float sc = live ? ldexpf(1.f, -ex) : 0.f;
+    _Float16 *A = (_Float16 *)ws;
+    const int tile = t >> 5, tl = t & 31;
+    constexpr int SREC = SK == 1 ? 1024 : 2048;
+    u8 *S = ws + gq_s_off(a.mp, K);
+    for (int g = tid; g < K / 8; g += 256) { /* group g = 8 values 8g..8g+7 = chunk g/2, half g&1 */
+        float v[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+        if (live) {
+            const float4 p = ((const LE_GLOBAL float4 *)xr)[2 * g], q = ((const LE_GLOBAL float4 *)xr)[2 * g + 1];
+            v[0] = p.x * sc; v[1] = p.y * sc; v[2] = p.z * sc; v[3] = p.w * sc;
+            v[4] = q.x * sc; v[5] = q.y * sc; v[6] = q.z * sc; v[7] = q.w * sc;
+        }
+        const le_h2 h0 = {(_Float16)v[0], (_Float16)v[2]}, h1 = {(_Float16)v[1], (_Float16)v[3]};
+        const le_h2 h2 = {(_Float16)v[4], (_Float16)v[6]}, h3 = {(_Float16)v[5], (_Float16)v[7]};
+        const size_t off = ((((size_t)tile * (K / 16) + (g >> 1)) * 2 + (g & 1)) * 32 + tl) * 8;
+        *(LE_GLOBAL uint4 *)(A + off) = make_uint4(as_u32(h0), as_u32(h1), as_u32(h2), as_u32(h3));
+        if constexpr (SK != 0) {
+            /* g runs over consecutive lanes, so the groups of one sum are neighbouring lanes */
+            float s = ((v[0] + v[1]) + (v[2] + v[3])) + ((v[4] + v[5]) + (v[6] + v[7]));
+            s += __shfl_xor(s, 1);
+            if constexpr (SK == 1) s += __shfl_xor(s, 2);
+            const int span = SK == 1 ? 4 : 2;
+            if ((g & (span - 1)) == 0) {
+                const int sb = g >> 5, j = (g & 31) / span; /* sum index within the super-block */
+                const _Float16 hi = (_Float16)s, lo = (_Float16)(s - (float)hi);
+                _Float16 *rec = (_Float16 *)(S + ((size_t)tile * nsb + sb) * SREC);
+                /* position P8(j % 8) (P8 is its own inverse), the order of the B2 operand */
+                const int pj = (j & 4) | ((j & 1) << 1) | ((j >> 1) & 1);
+                if constexpr (SK == 1) { /* [hs][token][8]: hs 0 high halves, hs 1 low halves */
+                    rec[tl * 8 + pj] = hi;
+                    rec[256 + tl * 8 + pj] = lo;
+                } else { /* [f][hs][token][8]: f 0 high, f 1 low; hs = j / 8 */
+                    rec[((j >> 3) * 32 + tl) * 8 + pj] = hi;
+                    rec[512 + ((j >> 3) * 32 + tl) * 8 + pj] = lo;
+                }
+            }
+        }
+    }
+    if (tid == 0) {
+        constexpr int srec = SK == 0 ? 0 : SREC;
+        ((float *)(ws + gq_t_off(a.mp, K, srec)))[t] = live ? ldexpf(1.f, ex) : 0.f;
+    }
+}
+
+/* ============================ main kernel ============================ */
+template <int TY, int WM, int WN, int TM, int TN>
+__device__ __forceinline__ void gq_body(const GqArgs &a, const u8 *ws) {
+    using F = GqF<TY>;
+    constexpr int BM = 32 * TM * WM, BN = 32 * TN * WN, NT = 64 * WM * WN;
+    constexpr int WB = BN * F::SLOT, AB = BM * 256, BUF = WB + AB;
+    constexpr int SBYTES = F::SREC ? (BM / 32) * F::SREC : 0; /* per super-block */
+    constexpr int NWC = (BN * F::NCH + NT - 1) / NT, NAC = AB / 16 / NT, NSC = (SBYTES / 16 + NT - 1) / NT;
+    static_assert(AB / 16 % NT == 0, "activation chunks must divide over the threads");
+    extern __shared__ uint4 smem[];
+    u8 *lds = (u8 *)smem;
+    u8 *Sl = lds + 2 * BUF;            /* [2][SBYTES] sum records, by super-block parity */
+    u8 *tab = Sl + 2 * SBYTES;          /* IQ tables */
+
+    const int K = a.cols, nsb = K >> 8, M = a.m;
+    const int NTR = (a.rows + BN - 1) / BN, MT = (M + BM - 1) / BM;
+    const int id = blockIdx.x, j = id >> 3;
+    const int mt = j % MT, nt = (j / MT) * 8 + (id & 7);
+    if (nt >= NTR) return; /* uniform over the block */
+    const int nb = nt * BN, mb = mt * BM;
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int wm = wave / WN, wn = wave % WN;
+    const size_t rb = (size_t)nsb * F::SBB;
+    const int sb0 = blockIdx.y * (nsb / a.ksplit), sb1 = sb0 + nsb / a.ksplit;
+    const int nstep = 2 * sb1;
+    const u8 *Ag = ws;
+    const u8 *Sg = ws + gq_s_off(a.mp, K);
+    const float *tsc = (const float *)(ws + gq_t_off(a.mp, K, F::SREC));
+
+    if constexpr (F::TAB > 0) gq_tables<TY>(tab);
+
+    struct Set {
+        uint4 w[NWC], x[NAC], s[NSC > 0 ? NSC : 1];
+    };
+    /* every load is unconditional (addresses clamped) so the waits before staging count exactly
+     * the loads of the step being staged; steps past the slice re-read the last one */
+    auto issue = [&](int s_, Set &R) {
+        const int s = min(s_, nstep - 1), sb = s >> 1, h = s & 1;
+        const u8 *w0 = a.w + (size_t)sb * F::SBB;
+#pragma unroll
+        for (int i = 0; i < NWC; i++) {
+            const int c = min(tid + NT * i, BN * F::NCH - 1), row = c / F::NCH, k = c - row * F::NCH;
+            const u8 *p = w0 + (size_t)min(nb + row, a.rows - 1) * rb + F::goff(k, h);
+            R.w[i] = F::ALIGNED ? ldg16(p) : ldg16u(p);
+        }
+#pragma unroll
+        for (int i = 0; i < NAC; i++) {
+            const int c = tid + NT * i, tl = c >> 9, off = c & 511; /* 512 chunks = 8 KB per 32-token tile */
+            R.x[i] = ldg16c(Ag + (((size_t)(mb / 32 + tl) * (K / 16) + sb * 16 + 8 * h) * 1024 + 16 * off));
+        }
+        if constexpr (SBYTES > 0) {
+#pragma unroll
+            for (int i = 0; i < NSC; i++) {
+                const int c = min(tid + NT * i, SBYTES / 16 - 1), tl = c / (F::SREC / 16), off = c % (F::SREC / 16);
+                R.s[i] = ldg16c(Sg + (((size_t)(mb / 32 + tl) * nsb + sb) * F::SREC + 16 * off));
+            }
+        }
+    };
+    auto stage = [&](int s, const Set &R) {
+        const int sb = s >> 1, h = s & 1;
+        u8 *B = lds + h * BUF;
+#pragma unroll
+        for (int i = 0; i < NWC; i++) {
+            const int c = tid + NT * i;
+            if (NWC * NT > BN * F::NCH && c >= BN * F::NCH) break;
+            const int row = c / F::NCH, k = c - row * F::NCH;
+            *(uint4 *)(B + row * F::SLOT + F::loff(k)) = R.w[i];
+        }
+#pragma unroll
+        for (int i = 0; i < NAC; i++) ((uint4 *)(B + WB))[tid + NT * i] = R.x[i];
+        if constexpr (SBYTES > 0) {
+            if (h == 0) {
+#pragma unroll
+                for (int i = 0; i < NSC; i++) {
+                    const int c = tid + NT * i;
+                    if (NSC * NT > SBYTES / 16 && c >= SBYTES / 16) break;
+                    ((uint4 *)(Sl + (sb & 1) * SBYTES))[c] = R.s[i];
+                }
+            }
+        }
+    };
+
+    le_v16f acc[TM][TN], d1[TM][TN];
+#pragma unroll
+    for (int i = 0; i < TM; i++)
+#pragma unroll
+        for (int k = 0; k < TN; k++) acc[i][k] = d1[i][k] = (le_v16f){};
+
+    const int n = lane & 31, hs = lane >> 5;
+    Set RA, RB; /* RA holds odd (h = 1) steps, RB even ones */
+    const int s0 = 2 * sb0;
+    issue(s0, RB);
+    stage(s0, RB);
+    issue(s0 + 1, RA);
+    issue(s0 + 2, RB);
+
+    for (int sb = sb0; sb < sb1; sb++) {
+#pragma unroll
+        for (int h = 0; h < 2; h++) {
+            const int s = 2 * sb + h;
+            gq_barrier(); /* step s is staged; every wave is done with step s-1's buffer */
+            const u8 *Wb = lds + h * BUF, *Ab = Wb + WB + (wm * TM) * 8192;
+            const u8 *rs[TN];
+#pragma unroll
+            for (int k = 0; k < TN; k++) rs[k] = Wb + (wn * TN * 32 + 32 * k + n) * F::SLOT;
+            /* A fragment of tile i, chunk c */
+            auto afrag = [&](int c, le_v8h (&A)[TM]) {
+#pragma unroll
+                for (int i = 0; i < TM; i++) A[i] = as_v8h(*(const uint4 *)(Ab + i * 8192 + c * 1024 + lane * 16));
+            };
+            /* stage the next step and issue the loads two steps ahead once this step's first
+             * fragments are under way */
+            auto pipe = [&]() {
+                if (s + 1 < nstep) stage(s + 1, h ? RB : RA);
+                issue(s + 3, h ? RB : RA);
+            };
+            if constexpr (TY == LE_TYPE_Q4_K) {
+                uint4 hd[TN];
+                u32 scw[TN];
+#pragma unroll
+                for (int k = 0; k < TN; k++) {
+                    hd[k] = *(const uint4 *)rs[k];
+                    scw[k] = h ? ((hd[k].w & 0x0F0F0F0Fu) | ((hd[k].y >> 2) & 0x30303030u)) : (hd[k].y & 0x3F3F3F3Fu);
+                }
+#pragma unroll
+                for (int g = 0; g < 2; g++) {
+                    uint4 kc[TN]; /* (sc_lo, -1024 sc_lo, sc_hi / 16, -64 sc_hi) as duplicated halves */
+#pragma unroll
+                    for (int k = 0; k < TN; k++) {
+                        const u32 slo = pk_add(h1024_dup(scw[k], 2 * g), 0xE400E400u);
+                        const u32 shi = pk_add(h1024_dup(scw[k], 2 * g + 1), 0xE400E400u);
+                        kc[k] = make_uint4(slo, pk_mul(slo, 0xE400E400u), pk_mul(shi, 0x2C002C00u), pk_mul(shi, 0xD400D400u));
+                    }
+#pragma unroll
+                    for (int c1 = 0; c1 < 2; c1++) {
+                        const int c = 4 * g + c1;
+                        le_v8h blo[TN], bhi[TN];
+#pragma unroll
+                        for (int k = 0; k < TN; k++) {
+                            const uint2 q = *(const uint2 *)(rs[k] + 16 + 32 * g + 16 * c1 + 8 * hs);
+                            const u32 ws_[2] = {q.x, q.y};
+                            u32 l[4], hh[4];
+#pragma unroll
+                            for (int e = 0; e < 2; e++) {
+                                const u32 x = ws_[e], x8 = x >> 8;
+                                l[2 * e] = pk_fma((x & 0x000F000Fu) | 0x64006400u, kc[k].x, kc[k].y);
+                                l[2 * e + 1] = pk_fma((x8 & 0x000F000Fu) | 0x64006400u, kc[k].x, kc[k].y);
+                                hh[2 * e] = pk_fma((x & 0x00F000F0u) | 0x64006400u, kc[k].z, kc[k].w);
+                                hh[2 * e + 1] = pk_fma((x8 & 0x00F000F0u) | 0x64006400u, kc[k].z, kc[k].w);
+                            }
+                            blo[k] = as_v8h(make_uint4(l[0], l[1], l[2], l[3]));
+                            bhi[k] = as_v8h(make_uint4(hh[0], hh[1], hh[2], hh[3]));
+                        }
+                        le_v8h A[TM];
+                        afrag(c, A);
+                        gq_mma(d1, A, blo, h == 0 && c == 0);
+                        afrag(c + 2, A);
+                        gq_mma(d1, A, bhi, false);
+                        if (g == 0 && c1 == 0) pipe();
+                    }
+                }
+            } else if constexpr (TY == LE_TYPE_Q6_K) {
+                /* chunk c of half h uses sc[8h + c], as sc / 64 duplicated (exact) */
+                u32 sp[TN][8];
+#pragma unroll
+                for (int k = 0; k < TN; k++) {
+                    const uint2 sv = *(const uint2 *)(rs[k] + 96 + 8 * h);
+                    const u32 sw[2] = {sv.x ^ 0x80808080u, sv.y ^ 0x80808080u};
+#pragma unroll
+                    for (int c = 0; c < 8; c++)
+                        sp[k][c] = pk_mul(pk_add(h1024_dup(sw[c >> 2], c & 3), 0xE480E480u), 0x24002400u); /* (byte - 1152) / 64 */
+                }
+#pragma unroll
+                for (int c1 = 0; c1 < 2; c1++) {
+                    const int l0 = 16 * c1 + 8 * hs;
+                    uint2 qa[TN], qb[TN], qh[TN];
+#pragma unroll
+                    for (int k = 0; k < TN; k++) {
+                        qa[k] = *(const uint2 *)(rs[k] + l0);
+                        qb[k] = *(const uint2 *)(rs[k] + 32 + l0);
+                        qh[k] = *(const uint2 *)(rs[k] + 64 + l0);
+                    }
+#pragma unroll
+                    for (int q = 0; q < 4; q++) {
+                        const int c = 2 * q + c1;
+                        le_v8h B[TN];
+#pragma unroll
+                        for (int k = 0; k < TN; k++) {
+                            const uint2 src = q & 1 ? qb[k] : qa[k];
+                            const u32 sx = src.x >> (4 * (q >> 1)), sy = src.y >> (4 * (q >> 1));
+                            const u32 hx = q < 2 ? (qh[k].x << (4 - 2 * q)) : (qh[k].x >> (2 * q - 4));
+                            const u32 hy = q < 2 ? (qh[k].y << (4 - 2 * q)) : (qh[k].y >> (2 * q - 4));
+                            const u32 vx = (sx & 0x0F0F0F0Fu) | (hx & 0x30303030u);
+                            const u32 vy = (sy & 0x0F0F0F0Fu) | (hy & 0x30303030u);
+                            /* (1024 + q6) - 1056 = q6 - 32 exactly, then one rounding by sc / 64 */
+                            const u32 sc = sp[k][c];
+                            B[k] = as_v8h(make_uint4(pk_mul(pk_add(h1024_02(vx), 0xE420E420u), sc), pk_mul(pk_add(h1024_13(vx), 0xE420E420u), sc),
+                                                     pk_mul(pk_add(h1024_02(vy), 0xE420E420u), sc), pk_mul(pk_add(h1024_13(vy), 0xE420E420u), sc)));
+                        }
+                        le_v8h A[TM];
+                        afrag(c, A);
+                        gq_mma(d1, A, B, h == 0 && c == 0);
+                        if (c1 == 0 && q == 0) pipe();
+                    }
+                }
+            } else if constexpr (TY == LE_TYPE_Q8_0) {
+#pragma unroll
+                for (int b = 0; b < 4; b++) {
+                    u32 r[TN]; /* (64 d_b) duplicated: exact in fp16 for |d_b| < 1024 */
+#pragma unroll
+                    for (int k = 0; k < TN; k++) {
+                        const u32 dv = *(const u32 *)(rs[k] + 128 + 16 * b) & 0xFFFFu;
+                        r[k] = pk_mul(dv | (dv << 16), 0x54005400u);
+                    }
+#pragma unroll
+                    for (int c1 = 0; c1 < 2; c1++) {
+                        const int c = 2 * b + c1;
+                        le_v8h B[TN];
+#pragma unroll
+                        for (int k = 0; k < TN; k++) {
+                            const uint2 q = *(const uint2 *)(rs[k] + 32 * b + 16 * c1 + 8 * hs);
+                            const u32 x = q.x ^ 0x80808080u, y = q.y ^ 0x80808080u;
+                            B[k] = as_v8h(make_uint4(pk_mul(pk_add(h1024_02(x), 0xE480E480u), r[k]), pk_mul(pk_add(h1024_13(x), 0xE480E480u), r[k]),
+                                                     pk_mul(pk_add(h1024_02(y), 0xE480E480u), r[k]), pk_mul(pk_add(h1024_13(y), 0xE480E480u), r[k])));
+                        }
+                        le_v8h A[TM];
+                        afrag(c, A);
+                        gq_mma(acc, A, B, false);
+                        if (c == 0) pipe();
+                    }
+                }
+            } else { /* IQ2_XXS, IQ3_XXS */
+                constexpr int GB = TY == LE_TYPE_IQ2_XXS ? 16 : 8;
+                const u8 *sgt = tab + 256 * GB;
+#pragma unroll
+                for (int b = 0; b < 4; b++) {
+                    uint2 rec[TN];
+                    u32 aux[TN], f[TN];
+#pragma unroll
+                    for (int k = 0; k < TN; k++) {
+                        if constexpr (TY == LE_TYPE_IQ2_XXS) {
+                            rec[k] = *(const uint2 *)(rs[k] + 8 * b);
+                            aux[k] = rec[k].y;
+                        } else {
+                            rec[k] = *(const uint2 *)(rs[k] + 8 * b);
+                            aux[k] = *(const u32 *)(rs[k] + 32 + 4 * b);
+                        }
+                        f[k] = pk_add(h1024_dup(2u * (aux[k] >> 28) + 1u, 0), 0xE400E400u); /* (2s+1) */
+                    }
+#pragma unroll
+                    for (int c1 = 0; c1 < 2; c1++) {
+                        const int c = 2 * b + c1, l = 2 * c1 + hs;
+                        le_v8h B[TN];
+#pragma unroll
+                        for (int k = 0; k < TN; k++) {
+                            const uint4 m = *(const uint4 *)(sgt + 16 * ((aux[k] >> (7 * l)) & 127u));
+                            uint4 g;
+                            if constexpr (TY == LE_TYPE_IQ2_XXS) {
+                                g = *(const uint4 *)(tab + GB * ((rec[k].x >> (8 * l)) & 255u));
+                            } else {
+                                const u32 iw = l < 2 ? rec[k].x : rec[k].y, sh = 16 * (l & 1);
+                                const uint2 g0 = *(const uint2 *)(tab + GB * ((iw >> sh) & 255u));
+                                const uint2 g1 = *(const uint2 *)(tab + GB * ((iw >> (sh + 8)) & 255u));
+                                g = make_uint4(g0.x, g0.y, g1.x, g1.y);
+                            }
+                            B[k] = as_v8h(make_uint4(pk_mul(g.x, f[k]) ^ m.x, pk_mul(g.y, f[k]) ^ m.y, pk_mul(g.z, f[k]) ^ m.z,
+                                                     pk_mul(g.w, f[k]) ^ m.w));
+                        }
+                        le_v8h A[TM];
+                        afrag(c, A);
+                        gq_mma(d1, A, B, h == 0 && c == 0);
+                        if (c == 0) pipe();
+                    }
+                }
+            }
+        }
+        /* super-block epilogue (the h = 1 buffer holds this super-block's second half) */
+        if constexpr (F::EPI) {
+            const u8 *Wb = lds + BUF;
+            const u8 *Sb = Sl + (sb & 1) * SBYTES + (wm * TM) * F::SREC;
+#pragma unroll
+            for (int k = 0; k < TN; k++) {
+                const u8 *r = Wb + (wn * TN * 32 + 32 * k + n) * F::SLOT;
+                if constexpr (TY == LE_TYPE_Q4_K) {
+                    const uint4 hd = *(const uint4 *)r;
+                    const u32 m0 = hd.z & 0x3F3F3F3Fu, m1 = ((hd.w >> 4) & 0x0F0F0F0Fu) | ((hd.z >> 2) & 0x30303030u);
+                    const le_v8h b2 = as_v8h(make_uint4(pk_add(h1024_02(m0), 0xE400E400u), pk_add(h1024_13(m0), 0xE400E400u),
+                                                        pk_add(h1024_02(m1), 0xE400E400u), pk_add(h1024_13(m1), 0xE400E400u)));
+                    const float dd = h2f(hd.x & 0xFFFFu), dm = h2f(hd.x >> 16);
+#pragma unroll
+                    for (int i = 0; i < TM; i++) {
+                        const le_v8h a2 = as_v8h(*(const uint4 *)(Sb + i * 1024 + lane * 16));
+                        const le_v16f d2 = __builtin_amdgcn_mfma_f32_32x32x16_f16(a2, b2, (le_v16f){}, 0, 0, 0);
+#pragma unroll
+                        for (int e = 0; e < 16; e++) acc[i][k][e] = __builtin_fmaf(dd, d1[i][k][e], __builtin_fmaf(-dm, d2[e], acc[i][k][e]));
+                    }
+                } else if constexpr (TY == LE_TYPE_Q6_K) {
+                    const float d64 = 64.f * h2f(*(const uint16_t *)(r + 126));
+#pragma unroll
+                    for (int i = 0; i < TM; i++)
+#pragma unroll
+                        for (int e = 0; e < 16; e++) acc[i][k][e] = __builtin_fmaf(d64, d1[i][k][e], acc[i][k][e]);
+                } else {
+                    const float dd = h2f(*(const uint16_t *)(r + (TY == LE_TYPE_IQ2_XXS ? 32 : 48))) *
+                                     (TY == LE_TYPE_IQ2_XXS ? 0.125f : 0.25f);
+#pragma unroll
+                    for (int i = 0; i < TM; i++)
+#pragma unroll
+                        for (int e = 0; e < 16; e++) acc[i][k][e] = __builtin_fmaf(dd, d1[i][k][e], acc[i][k][e]);
+                }
+            }
+        }
+    }
+    /* D lane l element e: token 8 (e / 4) + 4 (l / 32) + e % 4 of the tile, row l % 32 */
+    const float post = TY == LE_TYPE_Q8_0 ? 0.015625f : 1.f;
+#pragma unroll
+    for (int i = 0; i < TM; i++) {
+        const int t0 = mb + (wm * TM + i) * 32 + 4 * hs;
+#pragma unroll
+        for (int k = 0; k < TN; k++) {
+            const int r = nb + (wn * TN + k) * 32 + n;
+#pragma unroll
+            for (int e = 0; e < 16; e++) {
+                const int t = t0 + 8 * (e >> 2) + (e & 3);
+                if (t < M && r < a.rows) {
+                    const float v = acc[i][k][e] * (tsc[t] * post);
+                    if (a.ksplit > 1)
+                        unsafeAtomicAdd(a.y + (size_t)t * a.rows + r, v);
+                    else
+                        a.y[(size_t)t * a.rows + r] = v;
+                }
+            }
+        }
+    }
+}
+
+#define LE_GQX(TY, SK) \
+    extern "C" __global__ void __launch_bounds__(256) le_gq_xprep_##TY(GqArgs a, u8 *ws) { gq_xprep_body<SK>(a, ws); }
+LE_GQX(8, 0) LE_GQX(12, 1) LE_GQX(14, 0) LE_GQX(16, 0) LE_GQX(18, 0)
+
+#define LE_GQ_(TY, WM, WN, TM, TN)                                                                                     \
+    extern "C" __global__ void __launch_bounds__(WM * WN * 64) le_gq_##TY##_w##WM##WN##_t##TM##TN(GqArgs a, const u8 *ws) { \
+        gq_body<TY, WM, WN, TM, TN>(a, ws);                                                                            \
+    }
+#define LE_GQ(TY) LE_GQ_(TY, 1, 4, 1, 2) LE_GQ_(TY, 1, 4, 2, 2) LE_GQ_(TY, 2, 4, 2, 2) LE_GQ_(TY, 2, 2, 2, 2)
+LE_GQ(8) LE_GQ(12) LE_GQ(14) LE_GQ(16) LE_GQ(18)

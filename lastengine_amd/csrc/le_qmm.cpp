@@ -21,7 +21,8 @@
 
 namespace {
 
-const char *kParts[] = {"le_qmm_deq", "le_qmm_moe", "le_qmm_mv8", "le_qmm_mv12", "le_qmm_mv14", "le_qmm_mv16", "le_qmm_mv18", "le_qmm_gm"};
+const char *kParts[] = {"le_qmm_deq", "le_qmm_moe", "le_qmm_mv8", "le_qmm_mv12", "le_qmm_mv14", "le_qmm_mv16", "le_qmm_mv18", "le_qmm_gm",
+                        "le_qmm_gq"};
 
 /* Kernel argument block of le_mv_* (mirrors MvArgs in le_qmm_kernels.hip). */
 struct MvArgs {
@@ -87,6 +88,10 @@ struct le_ctx {
     int gm_ksplit = 0;       /* MFMA GEMM K slices: 0 auto, else 1, 2, 4, 8 */
     int gm_pc = 1;           /* MFMA GEMM with producer/consumer waves */
     int gm_split = 0;        /* 1: activations as two fp16 halves (22 bits); 0: one fp16 value (11 bits) */
+    int gq = 1;              /* Q4_K GEMM on the generic kernels (le_gq_*) instead of le_gm_12_* */
+    int gq_min_m = 9;        /* other types: smallest M on the matrix-core GEMM (below: vector kernels) */
+    int gq_cfg = 0;          /* generic GEMM block shape: 0 auto, 1 (32x256), 2 (64x256), 3 (128x256), 4 (128x128) */
+    int gq_ksplit = 0;       /* generic GEMM K slices: 0 auto, else 1, 2, 4, 8 */
     std::vector<hipModule_t> mods;
     std::map<std::string, hipFunction_t> fns;
     std::string err;
@@ -439,6 +444,18 @@ int le_set_option(le_ctx *c, const char *name, int value) {
     } else if (n == "gm_split") {
         if (value != 0 && value != 1) return c->fail(LE_ERR_ARG, "gm_split must be 0 or 1");
         c->gm_split = value;
+    } else if (n == "gq") {
+        c->gq = value ? 1 : 0;
+    } else if (n == "gq_min_m") {
+        if (value < 1) return c->fail(LE_ERR_ARG, "gq_min_m must be >= 1");
+        c->gq_min_m = value;
+    } else if (n == "gq_cfg") {
+        if (value < 0 || value > 4) return c->fail(LE_ERR_ARG, "gq_cfg must be 0..4");
+        c->gq_cfg = value;
+    } else if (n == "gq_ksplit") {
+        if (value != 0 && value != 1 && value != 2 && value != 4 && value != 8)
+            return c->fail(LE_ERR_ARG, "gq_ksplit must be 0, 1, 2, 4 or 8");
+        c->gq_ksplit = value;
     } else if (n == "gm_pc") {
         c->gm_pc = value ? 1 : 0;
     } else if (n == "gm_ksplit") {
@@ -632,20 +649,89 @@ static int mh_launch(le_ctx *c, const void *w, const float *x, int m, float *y, 
     return 1;
 }
 
+/* Generic matrix-core GEMM (le_gq_*): workspace = fp16 activation fragments for the tokens rounded
+ * up to 128, per-super-block sum records (Q4_K: 1 KB per 32 tokens), token scales. */
+static int gq_srec(int ty) { return ty == LE_TYPE_Q4_K ? 1024 : 0; }
+static size_t gq_ws_bytes(int ty, int m, int cols) {
+    const size_t mp = ((size_t)m + 127) / 128 * 128;
+    return mp * cols * 2 + mp / 32 * (cols / 256) * gq_srec(ty) + mp * 4;
+}
+static int gq_slot(int ty) {
+    switch (ty) {
+    case LE_TYPE_Q4_K: return 80;
+    case LE_TYPE_Q6_K: return 128;
+    case LE_TYPE_Q8_0: return 192;
+    case LE_TYPE_IQ2_XXS: return 48;
+    case LE_TYPE_IQ3_XXS: return 64;
+    }
+    return 0;
+}
+static int gq_tab(int ty) { return ty == LE_TYPE_IQ2_XXS ? 6144 : ty == LE_TYPE_IQ3_XXS ? 4096 : 0; }
+
+static int gq_launch(le_ctx *c, int ty, const void *w, const float *x, int m, float *y, int rows, int cols, void *ws,
+                     hipStream_t st) {
+    /* block shapes: (WM, WN, TM, TN) -> BM = 32 TM WM tokens, BN = 32 TN WN rows */
+    static const int cfgs[4][4] = {{1, 4, 1, 2}, {1, 4, 2, 2}, {2, 4, 2, 2}, {2, 2, 2, 2}};
+    int ci = c->gq_cfg ? c->gq_cfg - 1 : m <= 32 ? 0 : m <= 64 ? 1 : 2;
+    const int nsb = cols / 256, srec = gq_srec(ty);
+    auto lds_of = [&](int i) {
+        const int BM = 32 * cfgs[i][0] * cfgs[i][2], BN = 32 * cfgs[i][1] * cfgs[i][3];
+        return (size_t)2 * (BN * gq_slot(ty) + BM * 256) + (size_t)2 * (BM / 32) * srec + gq_tab(ty);
+    };
+    if (lds_of(ci) > c->lds_limit && ci == 2) ci = 3;
+    const size_t lds = lds_of(ci);
+    if (lds > c->lds_limit) return c->fail(LE_ERR_SHAPE, "GEMM tile does not fit the LDS");
+    const int WM = cfgs[ci][0], WN = cfgs[ci][1], TM = cfgs[ci][2], TN = cfgs[ci][3];
+    const int BM = 32 * TM * WM, BN = 32 * TN * WN, nthr = 64 * WM * WN;
+    char name[48];
+    snprintf(name, sizeof name, "le_gq_%d_w%d%d_t%d%d", ty, WM, WN, TM, TN);
+    const long long ntr = (rows + BN - 1) / BN, mt = (m + BM - 1) / BM;
+    const long long grid = (ntr + 7) / 8 * 8 * mt;
+    if (grid > 0x7FFFFFFFLL) return c->fail(LE_ERR_SHAPE, "GEMM grid too large");
+    int ks = 1;
+    if (c->gq_ksplit > 0) {
+        ks = c->gq_ksplit;
+    } else {
+        /* K slices while the grid stays within the resident blocks (one wave of blocks) */
+        const int per_cu = c->blocks_per_cu(name, nthr, lds);
+        const long long cap = (long long)c->cus * (per_cu > 0 ? per_cu : 1);
+        while (ks < 8 && ntr * mt * 2 * ks <= cap && nsb % (2 * ks) == 0) ks *= 2;
+    }
+    if (nsb % ks) return c->fail(LE_ERR_SHAPE, "gq_ksplit=%d does not divide the %d super-blocks", ks, nsb);
+    const int mp = (m + 127) / 128 * 128;
+    struct {
+        const void *w;
+        const float *x;
+        float *y;
+        int rows, cols, m, mp, ksplit;
+    } a{w, x, y, rows, cols, m, mp, ks};
+    void *args[] = {&a, &ws};
+    char pname[32];
+    snprintf(pname, sizeof pname, "le_gq_xprep_%d", ty);
+    int rc = c->launch(pname, dim3((unsigned)mp), 256, 0, st, args);
+    if (rc) return rc;
+    return c->launch(name, dim3((unsigned)grid, (unsigned)ks), nthr, lds, st, args);
+}
+
 size_t le_gemm_workspace_size(int ty, int m, int cols) {
-    if (ty != LE_TYPE_Q4_K || m <= 0 || cols <= 0 || cols % 256) return 0;
-    /* activation halves (2 x fp16 per value) and one 32-byte sum record per (token, super-block) */
-    return (size_t)m * cols * 4 + (size_t)m * (cols / 256) * 32;
+    if (!supported(ty) || m <= 0 || cols <= 0 || cols % 256) return 0;
+    const size_t g = gq_ws_bytes(ty, m, cols);
+    if (ty != LE_TYPE_Q4_K) return g;
+    /* the Q4_K GEMM of the split-activation option: two fp16 planes and 32-byte sum records */
+    const size_t o = (size_t)m * cols * 4 + (size_t)m * (cols / 256) * 32;
+    return g > o ? g : o;
 }
 
 int le_gemm(le_ctx *c, int ty, const void *w, const float *x, int m, float *y, int rows, int cols, void *ws,
             size_t ws_bytes, le_stream_t stream) {
     if (!c) return LE_ERR_ARG;
-    /* 3..16 tokens: the staged f16 kernel (2 tokens: the int8 multi-token matvec is faster);
+    if (!supported(ty)) return c->fail(LE_ERR_TYPE, "no kernel for type %d", ty);
+    /* Q4_K, 3..16 tokens: the staged f16 kernel (2 tokens: the int8 multi-token matvec is faster);
      * shapes whose activations do not fit its LDS, and gm_split=1 (two fp16 halves, which only
-     * the GEMM carries), go to the GEMM */
+     * the le_gm GEMM carries), go to a GEMM */
     const bool few = ty == LE_TYPE_Q4_K && c->gm_mh && !c->gm_split && m >= 3 && m <= c->gm_mh_max;
-    if (ty == LE_TYPE_Q4_K && (m >= c->gm_min_m || few) && m > 0 && rows > 0 && cols > 0 && cols % 256 == 0 && w && x && y) {
+    const bool gemm = ty == LE_TYPE_Q4_K ? (m >= c->gm_min_m || few) : m >= c->gq_min_m;
+    if (gemm && m > 0 && rows > 0 && cols > 0 && cols % 256 == 0 && w && x && y) {
         if (!ws) return c->fail(LE_ERR_ARG, "null workspace");
         if (ws_bytes < le_gemm_workspace_size(ty, m, cols))
             return c->fail(LE_ERR_WORKSPACE, "workspace needs %zu bytes", le_gemm_workspace_size(ty, m, cols));
@@ -654,6 +740,8 @@ int le_gemm(le_ctx *c, int ty, const void *w, const float *x, int m, float *y, i
             const int rc = mh_launch(c, w, x, m, y, rows, cols, (hipStream_t)stream);
             if (rc != 1) return rc;
         }
+        if (ty != LE_TYPE_Q4_K || (c->gq && !c->gm_split))
+            return gq_launch(c, ty, w, x, m, y, rows, cols, ws, (hipStream_t)stream);
         /* tiles: 32*TM tokens x 128*TN rows: 32 x 256 up to 64 tokens, 64 x 128 above (the
          * producer/consumer kernel of 64 x 256 tiles does not fit its registers) */
         int TM = m > 64 ? 2 : 1, TN = m > 64 && c->gm_pc ? 1 : 2;

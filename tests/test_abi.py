@@ -125,9 +125,20 @@ def test_init_without_gpu_fails_cleanly():
 
 def test_gemm_workspace_size():
     L = qmm.lib()
-    # fp16 halves of every activation (4 bytes per value) + one 32-byte sum record per super-block
-    assert L.le_gemm_workspace_size(12, 512, 4096) == 512 * 4096 * 4 + 512 * 16 * 32
-    assert L.le_gemm_workspace_size(12, 1, 256) == 1024 + 32
-    assert L.le_gemm_workspace_size(14, 64, 4096) == 0  # no workspace for the other types
+
+    def gq(ty, m, k):  # fp16 activation fragments for m rounded up to 128, sum records, token scales
+        mp = -(-m // 128) * 128
+        srec = {12: 1024}.get(ty, 0)
+        return mp * k * 2 + mp // 32 * (k // 256) * srec + mp * 4
+
+    def gm(m, k):  # Q4_K split-activation GEMM: two fp16 planes + a 32-byte record per super-block
+        return m * k * 4 + m * (k // 256) * 32
+
+    assert L.le_gemm_workspace_size(12, 512, 4096) == max(gq(12, 512, 4096), gm(512, 4096))
+    assert L.le_gemm_workspace_size(12, 1, 256) == max(gq(12, 1, 256), gm(1, 256))
+    for ty in (8, 14, 16, 18):
+        assert L.le_gemm_workspace_size(ty, 64, 4096) == gq(ty, 64, 4096)
+    assert L.le_gemm_workspace_size(14, 64, 4096) == 128 * 4096 * 2 + 128 * 4
     assert L.le_gemm_workspace_size(12, 0, 4096) == 0
     assert L.le_gemm_workspace_size(12, 16, 100) == 0
+    assert L.le_gemm_workspace_size(99, 16, 256) == 0

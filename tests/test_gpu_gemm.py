@@ -1,0 +1,115 @@
+"""GPU parity of the matrix-core GEMM (le_gemm from the token count where it takes over) for every
+type, against the oracle's cpu_ref::matmat restatement (src/cpu_ref.rs:266-276).
+
+Bar (tests/util.py): max|got-want| / max|want| <= 1e-3 and |got-want| <= 1e-3 * sum|w*x| per
+output. Weights enter the matrix cores as exact integer codes (Q4_K, IQ2_XXS, IQ3_XXS; Q6_K where
+the code has at most 11 significant bits) or rounded once to fp16 (Q6_K otherwise, Q8_0), and
+activations as fp16 after a per-token power-of-two scale (relative error 2^-11)."""
+import numpy as np
+import pytest
+
+import lastengine_amd as le
+import oracle
+from tests.util import weights, acts, check_close, random_blocks
+
+pytestmark = pytest.mark.gpu
+
+NAMES = list(le.TYPES)
+# Full-size weights of the configs: Q4_K / IQ2_XXS gate-up, Q6_K / IQ3_XXS down, Q8_0 head
+FULL = {"Q4_K": (14336, 4096), "Q6_K": (4096, 14336), "Q8_0": (32000, 4096), "IQ2_XXS": (14336, 4096),
+        "IQ3_XXS": (4096, 14336)}
+
+
+def dev(a):
+    import torch
+    return torch.from_numpy(np.ascontiguousarray(a)).cuda()
+
+
+def run_gemm(engine, ty, q, xs, rows, cols):
+    import torch
+    m = xs.shape[0]
+    y = torch.full((m, rows), float("nan"), dtype=torch.float32, device="cuda")
+    engine.gemm(ty, dev(q), dev(xs), m, y, rows, cols)
+    torch.cuda.synchronize()
+    return y.cpu().numpy()
+
+
+def absmag(ty, q, rows, cols, xs):
+    w = oracle.dequant_rows(ty, q, rows, cols).astype(np.float32)
+    return (np.abs(xs).astype(np.float32) @ np.abs(w).T).astype(np.float64)
+
+
+@pytest.mark.parametrize("name", NAMES)
+@pytest.mark.parametrize("m", [17, 64, 512])
+def test_gemm_full_shapes(engine, name, m):
+    ty = le.TYPES[name]
+    rows, cols = FULL[name]
+    print("gemm full", name, rows, cols, m, flush=True)
+    q, _ = weights(ty, rows, cols, seed=40 + ty)
+    xs = np.stack([acts(cols, 7000 + t) for t in range(m)])
+    got = run_gemm(engine, ty, q, xs, rows, cols)
+    want = oracle.matmat(ty, q, rows, cols, xs)
+    check_close(got, want, absmag(ty, q, rows, cols, xs))
+
+
+@pytest.mark.parametrize("name", NAMES)
+@pytest.mark.parametrize("cfg", [1, 2, 3, 4])
+@pytest.mark.parametrize("rows,cols,m,ks", [(300, 512, 17, 0), (513, 768, 65, 1), (96, 4096, 40, 4), (1000, 1024, 130, 2)])
+def test_gemm_tiles_and_slices(fresh_engine, name, cfg, rows, cols, m, ks):
+    """Every block shape (32/64/128 tokens x 128/256 rows) with ragged row and token tiles and
+    explicit K slices (fp32 atomic adds into the cleared output)."""
+    engine = fresh_engine
+    engine.set_option("gq_cfg", cfg)
+    engine.set_option("gq_ksplit", ks)
+    engine.set_option("gq_min_m", 1)
+    engine.set_option("gm_min_m", 1)
+    engine.set_option("gm_mh", 0)
+    ty = le.TYPES[name]
+    if (cols // 256) % max(ks, 1):
+        pytest.skip("K slices must divide the super-blocks")
+    print("gemm tiles", name, cfg, rows, cols, m, ks, flush=True)
+    q, _ = weights(ty, rows, cols, seed=rows + m + ty)
+    xs = np.stack([acts(cols, 8000 + t) for t in range(m)])
+    got = run_gemm(engine, ty, q, xs, rows, cols)
+    want = oracle.matmat(ty, q, rows, cols, xs)
+    check_close(got, want, absmag(ty, q, rows, cols, xs))
+
+
+@pytest.mark.parametrize("name", NAMES)
+@pytest.mark.parametrize("m", [1, 8, 24, 96])
+def test_gemm_random_blocks(engine, name, m):
+    """Arbitrary block bytes with bounded finite scales: every 6-bit scale/min code, negative Q6_K
+    sub-block scales, every IQ grid index and sign pattern, on the vector and matrix-core paths."""
+    ty = le.TYPES[name]
+    rows, cols = 384, 2048
+    print("gemm random blocks", name, m, flush=True)
+    q = random_blocks(ty, rows, cols, seed=11 * ty + m)
+    xs = np.stack([acts(cols, 9000 + t) for t in range(m)])
+    got = run_gemm(engine, ty, q, xs, rows, cols)
+    want = oracle.matmat(ty, q, rows, cols, xs)
+    check_close(got, want, absmag(ty, q, rows, cols, xs))
+
+
+@pytest.mark.parametrize("name", NAMES)
+def test_gemm_activation_magnitudes(engine, name):
+    """Tokens of very different magnitude in one call (1e-6 .. 1e6, a zero token, one token with a
+    single non-zero value): each token is scaled by its own power of two before fp16, so none
+    overflows and none loses relative precision."""
+    ty = le.TYPES[name]
+    rows, cols, m = 256, 1024, 40
+    q, _ = weights(ty, rows, cols, seed=5 + ty)
+    xs = np.stack([acts(cols, 9500 + t) for t in range(m)])
+    scales = np.float32(10.0) ** np.linspace(-6, 6, m).astype(np.float32)
+    xs = (xs * scales[:, None]).astype(np.float32)
+    xs[3] = 0.0
+    xs[7] = 0.0
+    xs[7, 100] = 3.0e4
+    got = run_gemm(engine, ty, q, xs, rows, cols)
+    want = oracle.matmat(ty, q, rows, cols, xs)
+    mag = absmag(ty, q, rows, cols, xs)
+    assert np.all(got[3] == 0.0)
+    # per token: the bar relative to that token's own outputs
+    for t in range(m):
+        if t == 3:
+            continue
+        check_close(got[t:t + 1], want[t:t + 1], mag[t:t + 1])

@@ -34,6 +34,7 @@ def _pair(eng, ty, rows, cols, m, seed):
 def test_noalloc_matches_gemm_two_calls(fresh_engine, name):
     ty = le.TYPES[name]
     fresh_engine.set_option("gm_ksplit", 1)  # one K slice: no atomics, reproducible bits
+    fresh_engine.set_option("gq_ksplit", 1)
     for (rows, cols, m, seed) in [(2048, 4096, 64, 11), (1024, 2048, 20, 12)]:
         print("noalloc case", name, rows, cols, m, flush=True)
         q, x, y_ws, y_na = _pair(fresh_engine, ty, rows, cols, m, seed)

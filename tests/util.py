@@ -32,3 +32,22 @@ def check_close(got, want, absmag):
     worst = float(np.max(err / bound))
     assert worst <= 1.0, "per-output error %.3f x of 1e-3*sum|wx|" % worst
     return norm_err, worst
+
+
+# Byte offsets of the f16 scale fields in each block: (block bytes, [field offsets]).
+SCALE_FIELDS = {8: (34, [0]), 12: (144, [0, 2]), 14: (210, [208]), 16: (66, [0]), 18: (98, [0])}
+
+
+def random_blocks(ty, rows, cols, seed, dmax=0.01):
+    """Arbitrary GGUF block bytes (every scale/min code, grid index, sign pattern and, for Q6_K,
+    negative sub-block scales) with the f16 super-block scale fields replaced by finite values
+    drawn uniformly from [-dmax, dmax], as real GGUF tensors have."""
+    rng = np.random.default_rng(seed)
+    q = rng.integers(0, 256, size=(rows, le.row_bytes(ty, cols)), dtype=np.uint8)
+    bb, offs = SCALE_FIELDS[ty]
+    nblk = q.shape[1] // bb
+    blk = q.reshape(rows, nblk, bb)
+    for o in offs:
+        d = rng.uniform(-dmax, dmax, size=(rows, nblk)).astype(np.float16)
+        blk[:, :, o:o + 2] = d.view(np.uint8).reshape(rows, nblk, 2)
+    return q
