@@ -78,14 +78,18 @@ const char *le_last_error(const le_ctx *ctx);
  *     "ms_piq" (IQ2_XXS, IQ3_XXS), and "mq6" / "mqiq" (0/1) for the Q6_K / IQ staged kernels;
  *     "ms_t" (0/1): Q4_K with 2..8 tokens per pass on the staged kernel (one weight stream, 8 tokens
  *     per MFMA pass), used by le_gemm below "gm_min_m" tokens
- *   GEMM: "gm_mh" (0/1) Q4_K with 3..16 tokens on the staged f16 MFMA kernel (tokens as MFMA rows),
+ *   GEMM: "gq" (0/1) Q4_K on the generic matrix-core GEMM (default) or the older le_gm kernels,
+ *     "gq_min_m" smallest M of the other types on the matrix-core GEMM (below: vector kernels that
+ *     read the weights once per 8 tokens), "gq_cfg" its block shape (0 auto; 1..6: 32x256, 64x256,
+ *     128x256, 128x128 tokens x rows on 4 waves, 64x256 and 128x256 on 8 waves), "gq_ksplit" its K
+ *     slices (0 auto, 1, 2, 4, 8);
+ *     "gm_mh" (0/1) Q4_K with 3..16 tokens on the staged f16 MFMA kernel (tokens as MFMA rows),
  *     "gm_mh_max" its largest M (16, the default, where K <= 4096 fits its LDS; or 8),
  *     "gm_mh_shape" its (super-blocks per step, waves) as 10 P + NW (0 auto, 14, 18, 24, 22),
- *     "gm_min_m" smallest M on the MFMA GEMM, "gm_tile" (0 auto, 11, 12, 21, 22),
- *     "gm_ksplit" K slices (0 auto, 1, 2, 4, 8), "gm_pc" producer/consumer waves (0/1),
- *     "gm_split" activation precision on the matrix cores: 0 (default) rounds each value to fp16
- *     (relative error 2^-11 per value), 1 carries a second fp16 half (about 2^-22 per value) and
- *     so also sends 3..16 tokens to the GEMM
+ *     "gm_min_m" smallest Q4_K M on a GEMM, "gm_tile" (0 auto, 11, 12, 21, 22), "gm_ksplit" K
+ *     slices (0 auto, 1, 2, 4, 8), "gm_pc" producer/consumer waves (0/1) of the le_gm kernels,
+ *     "gm_split" 1: Q4_K activations as two fp16 halves (about 2^-22 per value) on the le_gm
+ *     kernels, which then also take 3..16 tokens
  *   MoE: "moe_mfma" staged kernels (0/1), "moe_fused" single launch (0/1), "moe_fused_min_tok",
  *     "moe_fast" decode-shaped vector kernels (0/1) */
 int le_set_option(le_ctx *ctx, const char *name, int value);
@@ -103,16 +107,19 @@ int le_dequant_rows(le_ctx *ctx, int ty, const void *w, float *out, int rows, in
 int le_matvec(le_ctx *ctx, int ty, const void *const *ptrs, const void *w, const float *x, long long xstride,
               float *y, int rows, int cols, int slots, le_stream_t stream);
 
-/* ---- small-M GEMM for speculative verify / prefill (replaces mmq*_<ty> + DenseGpu::bmm,
- *      src/cuda/kernels.cu:965-1223, src/gpu/dense.rs:181-199; CPU twin cpu_ref::matmat,
+/* ---- small-M GEMM for speculative verify / prefill (replaces mmq*_<ty> / mmq128r_<ty> + DenseGpu::bmm,
+ *      src/cuda/kernels.cu:965-1235, src/gpu/dense.rs:181-199; CPU twin cpu_ref::matmat,
  *      src/cpu_ref.rs:266-276) ----
  * Y[t * rows + r] = W[r,:] . X[t * cols ...] for t < m. ws: device workspace of
  * le_gemm_workspace_size(ty, m, cols) bytes (may be 0 bytes / NULL when that size is 0), the
  * counterpart of the reference's pre-quantized activation buffers (xqb/xdb/xsb, src/gpu.rs:210).
- * Q4_K runs on the matrix cores: 3..16 tokens on the staged f16 MFMA kernel (up to 8 where K >
- * 4096), more on the fp16 MFMA GEMM (both take the activations rounded to fp16, so
- * |x| < 65504), 2 tokens on the staged int8 matvec with several tokens per weight pass (options
- * "gm_mh", "gm_mh_max", "gm_min_m"). */
+ * Every type runs on the matrix cores from 17 tokens (Q4_K: 3..16 tokens on a staged f16 MFMA
+ * kernel, 2 on the staged int8 matvec; other types: from "gq_min_m" = 9 tokens, vector kernels
+ * below). On the matrix cores each token is scaled by its own power of two and rounded to fp16
+ * (relative error 2^-11 per value at any magnitude up to 2^127); Q8_0 weights enter as
+ * fp16(q * 64 d) (so |d| < 8), the other types as exact integer codes (Q6_K: rounded to fp16
+ * where (q - 32) * sc has more than 11 significant bits). The 3..16-token Q4_K kernel rounds
+ * unscaled activations to fp16 (|x| < 65504, 32-value sums < 65504). */
 size_t le_gemm_workspace_size(int ty, int m, int cols);
 int le_gemm(le_ctx *ctx, int ty, const void *w, const float *x, int m, float *y, int rows, int cols, void *ws,
             size_t ws_bytes, le_stream_t stream);

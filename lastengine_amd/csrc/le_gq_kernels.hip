@@ -79,6 +79,13 @@ __device__ __forceinline__ u32 h1024_dup(u32 w, int i) {
     const u32 sel = 0x04000400u | (u32)(i * 0x00010001);
     return __builtin_amdgcn_perm(0x64646464u, w, sel);
 }
+/* (x & m) | c in one instruction: the compiler otherwise emits an and and an or, because a VOP3
+ * instruction cannot carry the two literal constants; m and c stay in registers */
+__device__ __forceinline__ u32 and_or(u32 x, u32 m, u32 c) {
+    u32 r;
+    __asm__("v_and_or_b32 %0, %1, %2, %3" : "=v"(r) : "v"(x), "v"(m), "v"(c));
+    return r;
+}
 __device__ __forceinline__ u32 pk_fma(u32 a, u32 b, u32 c) {
     return as_u32(__builtin_elementwise_fma(as_h2(a), as_h2(b), as_h2(c)));
 }
@@ -346,10 +353,14 @@ __device__ __forceinline__ void gq_body(const GqArgs &a, const u8 *ws) {
     const int n = lane & 31, hs = lane >> 5;
     Set RA, RB; /* RA holds odd (h = 1) steps, RB even ones */
     const int s0 = 2 * sb0;
+    /* the loads must reach the memory pipeline in step order (RA's before RB's, as in the loop),
+     * or the wait at the loop head would have to cover both sets: no reordering across issues */
     issue(s0, RB);
     stage(s0, RB);
     issue(s0 + 1, RA);
+    __builtin_amdgcn_sched_barrier(0);
     issue(s0 + 2, RB);
+    __builtin_amdgcn_sched_barrier(0);
 
     for (int sb = sb0; sb < sb1; sb++) {
 #pragma unroll
@@ -368,10 +379,16 @@ __device__ __forceinline__ void gq_body(const GqArgs &a, const u8 *ws) {
             /* stage the next step and issue the loads two steps ahead once this step's first
              * fragments are under way */
             auto pipe = [&]() {
-                if (s + 1 < nstep) stage(s + 1, h ? RB : RA);
+                /* unconditional (a branch here would make the compiler wait for every load in
+                 * flight): past the slice's end this stages a re-read into the buffer that is
+                 * no longer read */
+                stage(s + 1, h ? RB : RA);
+                __builtin_amdgcn_sched_barrier(0);
                 issue(s + 3, h ? RB : RA);
+                __builtin_amdgcn_sched_barrier(0);
             };
             if constexpr (TY == LE_TYPE_Q4_K) {
+                const u32 mlo = 0x000F000Fu, mhi = 0x00F000F0u, c1024 = 0x64006400u;
                 uint4 hd[TN];
                 u32 scw[TN];
 #pragma unroll
@@ -400,10 +417,10 @@ __device__ __forceinline__ void gq_body(const GqArgs &a, const u8 *ws) {
 #pragma unroll
                             for (int e = 0; e < 2; e++) {
                                 const u32 x = ws_[e], x8 = x >> 8;
-                                l[2 * e] = pk_fma((x & 0x000F000Fu) | 0x64006400u, kc[k].x, kc[k].y);
-                                l[2 * e + 1] = pk_fma((x8 & 0x000F000Fu) | 0x64006400u, kc[k].x, kc[k].y);
-                                hh[2 * e] = pk_fma((x & 0x00F000F0u) | 0x64006400u, kc[k].z, kc[k].w);
-                                hh[2 * e + 1] = pk_fma((x8 & 0x00F000F0u) | 0x64006400u, kc[k].z, kc[k].w);
+                                l[2 * e] = pk_fma(and_or(x, mlo, c1024), kc[k].x, kc[k].y);
+                                l[2 * e + 1] = pk_fma(and_or(x8, mlo, c1024), kc[k].x, kc[k].y);
+                                hh[2 * e] = pk_fma(and_or(x, mhi, c1024), kc[k].z, kc[k].w);
+                                hh[2 * e + 1] = pk_fma(and_or(x8, mhi, c1024), kc[k].z, kc[k].w);
                             }
                             blo[k] = as_v8h(make_uint4(l[0], l[1], l[2], l[3]));
                             bhi[k] = as_v8h(make_uint4(hh[0], hh[1], hh[2], hh[3]));
@@ -447,8 +464,8 @@ __device__ __forceinline__ void gq_body(const GqArgs &a, const u8 *ws) {
                             const u32 sx = src.x >> (4 * (q >> 1)), sy = src.y >> (4 * (q >> 1));
                             const u32 hx = q < 2 ? (qh[k].x << (4 - 2 * q)) : (qh[k].x >> (2 * q - 4));
                             const u32 hy = q < 2 ? (qh[k].y << (4 - 2 * q)) : (qh[k].y >> (2 * q - 4));
-                            const u32 vx = (sx & 0x0F0F0F0Fu) | (hx & 0x30303030u);
-                            const u32 vy = (sy & 0x0F0F0F0Fu) | (hy & 0x30303030u);
+                            const u32 vx = and_or(sx, 0x0F0F0F0Fu, hx & 0x30303030u);
+                            const u32 vy = and_or(sy, 0x0F0F0F0Fu, hy & 0x30303030u);
                             /* (1024 + q6) - 1056 = q6 - 32 exactly, then one rounding by sc / 64 */
                             const u32 sc = sp[k][c];
                             B[k] = as_v8h(make_uint4(pk_mul(pk_add(h1024_02(vx), 0xE420E420u), sc), pk_mul(pk_add(h1024_13(vx), 0xE420E420u), sc),
@@ -568,8 +585,14 @@ __device__ __forceinline__ void gq_body(const GqArgs &a, const u8 *ws) {
             }
         }
     }
-    /* D lane l element e: token 8 (e / 4) + 4 (l / 32) + e % 4 of the tile, row l % 32 */
+    /* D lane l element e: token 8 (e / 4) + 4 (l / 32) + e % 4 of the tile, row l % 32; the
+     * token scales of the padded tile are all loaded first (one memory round trip) */
     const float post = TY == LE_TYPE_Q8_0 ? 0.015625f : 1.f;
+    float ts[TM][16];
+#pragma unroll
+    for (int i = 0; i < TM; i++)
+#pragma unroll
+        for (int e = 0; e < 16; e++) ts[i][e] = tsc[mb + (wm * TM + i) * 32 + 4 * hs + 8 * (e >> 2) + (e & 3)] * post;
 #pragma unroll
     for (int i = 0; i < TM; i++) {
         const int t0 = mb + (wm * TM + i) * 32 + 4 * hs;
@@ -580,7 +603,7 @@ __device__ __forceinline__ void gq_body(const GqArgs &a, const u8 *ws) {
             for (int e = 0; e < 16; e++) {
                 const int t = t0 + 8 * (e >> 2) + (e & 3);
                 if (t < M && r < a.rows) {
-                    const float v = acc[i][k][e] * (tsc[t] * post);
+                    const float v = acc[i][k][e] * ts[i][e];
                     if (a.ksplit > 1)
                         unsafeAtomicAdd(a.y + (size_t)t * a.rows + r, v);
                     else
@@ -599,5 +622,6 @@ LE_GQX(8, 0) LE_GQX(12, 1) LE_GQX(14, 0) LE_GQX(16, 0) LE_GQX(18, 0)
     extern "C" __global__ void __launch_bounds__(WM * WN * 64) le_gq_##TY##_w##WM##WN##_t##TM##TN(GqArgs a, const u8 *ws) { \
         gq_body<TY, WM, WN, TM, TN>(a, ws);                                                                            \
     }
-#define LE_GQ(TY) LE_GQ_(TY, 1, 4, 1, 2) LE_GQ_(TY, 1, 4, 2, 2) LE_GQ_(TY, 2, 4, 2, 2) LE_GQ_(TY, 2, 2, 2, 2)
+#define LE_GQ(TY) LE_GQ_(TY, 1, 4, 1, 2) LE_GQ_(TY, 1, 4, 2, 2) LE_GQ_(TY, 1, 4, 4, 2) LE_GQ_(TY, 2, 2, 2, 2) \
+    LE_GQ_(TY, 1, 8, 2, 1) LE_GQ_(TY, 1, 8, 4, 1)
 LE_GQ(8) LE_GQ(12) LE_GQ(14) LE_GQ(16) LE_GQ(18)

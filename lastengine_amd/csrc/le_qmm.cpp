@@ -90,7 +90,8 @@ struct le_ctx {
     int gm_split = 0;        /* 1: activations as two fp16 halves (22 bits); 0: one fp16 value (11 bits) */
     int gq = 1;              /* Q4_K GEMM on the generic kernels (le_gq_*) instead of le_gm_12_* */
     int gq_min_m = 9;        /* other types: smallest M on the matrix-core GEMM (below: vector kernels) */
-    int gq_cfg = 0;          /* generic GEMM block shape: 0 auto, 1 (32x256), 2 (64x256), 3 (128x256), 4 (128x128) */
+    int gq_cfg = 0;          /* generic GEMM block shape (tokens x rows, waves): 0 auto, 1 (32x256, 4), 2 (64x256, 4),
+                                3 (128x256, 4), 4 (128x128, 4), 5 (64x256, 8), 6 (128x256, 8) */
     int gq_ksplit = 0;       /* generic GEMM K slices: 0 auto, else 1, 2, 4, 8 */
     std::vector<hipModule_t> mods;
     std::map<std::string, hipFunction_t> fns;
@@ -450,7 +451,7 @@ int le_set_option(le_ctx *c, const char *name, int value) {
         if (value < 1) return c->fail(LE_ERR_ARG, "gq_min_m must be >= 1");
         c->gq_min_m = value;
     } else if (n == "gq_cfg") {
-        if (value < 0 || value > 4) return c->fail(LE_ERR_ARG, "gq_cfg must be 0..4");
+        if (value < 0 || value > 6) return c->fail(LE_ERR_ARG, "gq_cfg must be 0..6");
         c->gq_cfg = value;
     } else if (n == "gq_ksplit") {
         if (value != 0 && value != 1 && value != 2 && value != 4 && value != 8)
@@ -671,14 +672,16 @@ static int gq_tab(int ty) { return ty == LE_TYPE_IQ2_XXS ? 6144 : ty == LE_TYPE_
 static int gq_launch(le_ctx *c, int ty, const void *w, const float *x, int m, float *y, int rows, int cols, void *ws,
                      hipStream_t st) {
     /* block shapes: (WM, WN, TM, TN) -> BM = 32 TM WM tokens, BN = 32 TN WN rows */
-    static const int cfgs[4][4] = {{1, 4, 1, 2}, {1, 4, 2, 2}, {2, 4, 2, 2}, {2, 2, 2, 2}};
-    int ci = c->gq_cfg ? c->gq_cfg - 1 : m <= 32 ? 0 : m <= 64 ? 1 : 2;
+    static const int cfgs[6][4] = {{1, 4, 1, 2}, {1, 4, 2, 2}, {1, 4, 4, 2}, {2, 2, 2, 2}, {1, 8, 2, 1}, {1, 8, 4, 1}};
+    /* measured on the config shapes: 8 waves (two per SIMD, so one wave's weight decoding runs
+     * under the other's MFMAs), 64 x 256 tiles up to 64 tokens, 128 x 256 above */
+    int ci = c->gq_cfg ? c->gq_cfg - 1 : m <= 64 ? 4 : 5;
     const int nsb = cols / 256, srec = gq_srec(ty);
     auto lds_of = [&](int i) {
         const int BM = 32 * cfgs[i][0] * cfgs[i][2], BN = 32 * cfgs[i][1] * cfgs[i][3];
         return (size_t)2 * (BN * gq_slot(ty) + BM * 256) + (size_t)2 * (BM / 32) * srec + gq_tab(ty);
     };
-    if (lds_of(ci) > c->lds_limit && ci == 2) ci = 3;
+    if (lds_of(ci) > c->lds_limit && (ci == 2 || ci == 5)) ci = 3;
     const size_t lds = lds_of(ci);
     if (lds > c->lds_limit) return c->fail(LE_ERR_SHAPE, "GEMM tile does not fit the LDS");
     const int WM = cfgs[ci][0], WN = cfgs[ci][1], TM = cfgs[ci][2], TN = cfgs[ci][3];
