@@ -5,11 +5,15 @@ decode"): one step = one batch-1 Q4_K matvec over a 14336x4096 weight (33,030,14
 activations, weights resident in HBM. Copies of the weight are rotated so the streamed footprint
 exceeds 512 MB and the 256 MB Infinity Cache cannot serve repeats. The steps are recorded once into
 a HIP graph (one launch per weight copy) and the graph is replayed; HIP events on that stream
-bracket the timed replays. `value` = algorithmic bytes (weights + x + y) per step / time per step.
+bracket every timed replay, at least 200 launches are timed whatever --steps says, and the
+median per-launch time over the replays is reported. `value` = algorithmic bytes (weights + x + y)
+per step / median time per step.
 
 Secondary measurements (same JSON object, "secondary"): the MoE expert layer (config 4) in
 us/token at 1 and 8 tokens, the Llama-3-8B layer matvecs and Q8_0 head (config 2), the IQ2_XXS /
-IQ3_XXS matvecs (config 5), Q4_K 4096x4096 (config 1) and the small-M GEMM (config 3).
+IQ3_XXS matvecs (config 5), Q4_K 4096x4096 (config 1), the small-M GEMM (config 3) and the
+prefill-shaped GEMMs of the other types, and the streaming-read ceiling of this part at 33 MB and
+9.4 MB (a bare read of that many bytes, the practical bound of the matvecs).
 The CPU baseline times the oracle (a C restatement of the reference's cpu_ref::matvec) on a
 bounded sample of the headline workload on the host's cores.
 
@@ -46,9 +50,13 @@ def quantized(ty, rows, cols, seed):
     return le.quantize_rows(ty, le.fill_normal(rows * cols, seed, std=0.02).reshape(rows, cols))
 
 
-def graph_time(record, n_launch, steps, warmup):
-    """Capture record() (n_launch steps) into a HIP graph, replay it, and time `steps` steps with
-    HIP events on the replay stream. Returns ms per step."""
+MIN_TIMED_LAUNCHES = 200
+
+
+def graph_time(record, n_launch, steps, warmup, min_launches=MIN_TIMED_LAUNCHES):
+    """Capture record() (n_launch steps) into a HIP graph, replay it, and time each replay with HIP
+    events on the replay stream. At least max(steps, min_launches) steps are timed; returns the
+    median per-step time over the replays in ms (plus mean/min/max and counts in .stats)."""
     import torch
     s = torch.cuda.Stream()
     with torch.cuda.stream(s):
@@ -57,17 +65,22 @@ def graph_time(record, n_launch, steps, warmup):
     g = torch.cuda.CUDAGraph()
     with torch.cuda.graph(g):
         record()
-    reps = max(1, -(-steps // n_launch))
     for _ in range(max(1, -(-warmup // n_launch))):
         g.replay()
     torch.cuda.synchronize()
-    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    e0.record()
-    for _ in range(reps):
+    reps = max(3, -(-max(steps, min_launches) // n_launch))
+    evs = [torch.cuda.Event(enable_timing=True) for _ in range(reps + 1)]
+    evs[0].record()
+    for r in range(reps):
         g.replay()
-    e1.record()
+        evs[r + 1].record()
     torch.cuda.synchronize()
-    return e0.elapsed_time(e1) / (reps * n_launch)
+    per = sorted(evs[r].elapsed_time(evs[r + 1]) / n_launch for r in range(reps))
+    med = per[len(per) // 2] if len(per) % 2 else 0.5 * (per[len(per) // 2 - 1] + per[len(per) // 2])
+    graph_time.stats = {"replays": reps, "launches_per_replay": n_launch, "timed_launches": reps * n_launch,
+                        "median_us": round(med * 1e3, 3), "mean_us": round(sum(per) / reps * 1e3, 3),
+                        "min_us": round(per[0] * 1e3, 3), "max_us": round(per[-1] * 1e3, 3)}
+    return med
 
 
 def bench_matvec(eng, ty, rows, cols, steps, warmup, seed=1):
@@ -83,7 +96,8 @@ def bench_matvec(eng, ty, rows, cols, steps, warmup, seed=1):
             eng.mv(ty, b, x, y, rows, cols)
     ms = graph_time(record, len(bufs), steps, warmup)
     alg = host.nbytes + 4 * cols + 4 * rows
-    return {"us": ms * 1e3, "ms": ms, "bytes": alg, "gbs": alg / (ms * 1e-3) / 1e9, "copies": len(bufs)}, host
+    return {"us": ms * 1e3, "ms": ms, "bytes": alg, "gbs": alg / (ms * 1e-3) / 1e9, "copies": len(bufs),
+            "timing": dict(graph_time.stats)}, host
 
 
 def bench_layer(eng, mats, steps, warmup):
@@ -101,7 +115,7 @@ def bench_layer(eng, mats, steps, warmup):
         for k in range(ncopy):
             for i, (_, ty, r, c) in enumerate(mats):
                 eng.mv(ty, devs[i][k], xs[c], ys[i], r, c)
-    ms = graph_time(record, ncopy, steps, warmup)
+    ms = graph_time(record, ncopy, steps, warmup, min_launches=40)
     alg = total + sum(4 * (r + c) for (_, _, r, c) in mats)
     return {"us": round(ms * 1e3, 3), "GB/s": round(alg / (ms * 1e-3) / 1e9, 1),
             "frac_hbm": round(alg / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4), "weight_bytes": total}
@@ -119,7 +133,7 @@ def bench_gemm(eng, ty, rows, cols, mtok, steps, warmup, seed=3):
     def record():
         for b in bufs:
             eng.gemm(ty, b, x, mtok, y, rows, cols, ws=ws)
-    ms = graph_time(record, len(bufs), steps, warmup)
+    ms = graph_time(record, len(bufs), steps, warmup, min_launches=20)
     alg = host.nbytes + 4 * mtok * (cols + rows)
     return {"us": round(ms * 1e3, 2), "GB/s": round(alg / (ms * 1e-3) / 1e9, 1),
             "TFLOP/s": round(2.0 * mtok * rows * cols / (ms * 1e-3) / 1e12, 2)}
@@ -158,7 +172,7 @@ def bench_moe(eng, n_tok, steps, warmup, n_exp=128, k=8, hidden=2048, ff=768, co
         for i in range(n_launch):
             gs, us_, ds = sets[i % copies]
             eng.moe(tg, tg, td, gs, us_, ds, n_exp, k, hidden, ff, dlg[i % variants], h, n_tok, out, ws=ws)
-    ms = graph_time(record, n_launch, steps, warmup)
+    ms = graph_time(record, n_launch, steps, warmup, min_launches=64)
     uniq = float(np.mean([unique_experts(l, k) for l in lgs]))
     wbytes = uniq * per_expert
     res = {"n_tok": n_tok, "us_per_layer": round(ms * 1e3, 3), "us_per_token": round(ms * 1e3 / n_tok, 3),
@@ -170,11 +184,31 @@ def bench_moe(eng, n_tok, steps, warmup, n_exp=128, k=8, hidden=2048, ff=768, co
     return res
 
 
+def host_cpu():
+    """(CPU model, logical cores the OS reports)."""
+    model = "unknown"
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    model = line.split(":", 1)[1].strip()
+                    break
+    except OSError:
+        pass
+    return model, os.cpu_count() or 1
+
+
+# Host threads for the CPU baseline: the CPU share of one GPU on the benchmark boxes (16), or fewer
+# where the host has fewer cores.
+CPU_THREADS = 16
+
+
 def cpu_baseline(ty, host_q, rows, cols, budget_s=10.0):
     """Oracle matvec (C restatement of cpu_ref::matvec) on the host cores, bounded sample."""
     import lastengine_amd as le
     import oracle
-    threads = max(1, min(16, os.cpu_count() or 1))
+    model, nproc = host_cpu()
+    threads = max(1, min(CPU_THREADS, nproc))
     x = le.fill_normal(cols, 2)
     oracle.matvec(ty, host_q, rows, cols, x, nthreads=threads)  # warm
     reps, t0 = 0, time.perf_counter()
@@ -187,8 +221,36 @@ def cpu_baseline(ty, host_q, rows, cols, budget_s=10.0):
     per = el / reps
     gbs = (host_q.nbytes + 4 * cols + 4 * rows) / per / 1e9
     return {"value": round(gbs, 3), "unit": "GB/s", "cores": threads, "kind": "port",
-            "sample": "%d full %dx%d Q4_K matvecs by the oracle on %d host threads, %.1f ms each" % (
-                reps, rows, cols, threads, per * 1e3)}
+            "host_nproc": nproc, "host_cpu": model,
+            "sample": "%d full %dx%d Q4_K matvecs by the oracle (rows split over %d threads: the CPU share of one "
+                      "GPU on the box, of %d logical cores), %.1f ms each" % (reps, rows, cols, threads, nproc, per * 1e3)}
+
+
+def bench_stream_read(eng, size, steps, warmup):
+    """Practical HBM read ceiling at `size` bytes: le_stream_read over rotated buffers (the best of
+    the probe's load forms measured for that size), same graph timing as the matvecs."""
+    import torch
+    n = max(1, -(-ROTATE_BYTES // size))
+    bufs = [torch.ones(size // 4, dtype=torch.int32, device="cuda") for _ in range(n)]
+    sink = torch.empty(eng.stream_read_sink_bytes() // 4 * 16, dtype=torch.int32, device="cuda")
+    best = None
+    for opts in ({"rd_u": 4, "rd_blocks_per_cu": 1, "rd_block": 512}, {"rd_u": 1, "rd_blocks_per_cu": 2, "rd_block": 512}):
+        for k, v in opts.items():
+            eng.set_option(k, v)
+
+        def record():
+            for b in bufs:
+                eng.stream_read(b, size, sink)
+        ms = graph_time(record, len(bufs), steps, warmup)
+        if best is None or ms < best[0]:
+            best = (ms, opts)
+    for k, v in {"rd_u": 4, "rd_blocks_per_cu": 1, "rd_block": 512}.items():
+        eng.set_option(k, v)
+    del bufs
+    torch.cuda.empty_cache()
+    gbs = size / (best[0] * 1e-3) / 1e9
+    return {"bytes": size, "us": round(best[0] * 1e3, 3), "GB/s": round(gbs, 1), "frac_hbm": round(gbs / HBM_PEAK_GBS, 4),
+            "load_form": best[1]}
 
 
 def probe(eng, ty, rows, cols, launches=100, copy_bytes=256 << 20):
@@ -249,6 +311,7 @@ def main():
         "steps": args.steps,
         "warmup": args.warmup,
         "ms_per_step": round(head["ms"], 6),
+        "timing": dict(head["timing"], note="value and ms_per_step are the median over the timed graph replays"),
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
@@ -262,8 +325,9 @@ def main():
                      "traffic": None},
     }
     tr = os.path.join(REPO, "profiles", "traffic_le_ms_12_14336x4096.json")
-    if os.path.exists(tr):
+    if os.path.exists(tr):  # from the committed rocprofv3 FETCH_SIZE / WRITE_SIZE passes of this workload
         out["roofline"]["traffic"] = json.load(open(tr)).get("hbm_bytes_per_launch")
+        out["roofline"]["traffic_source"] = "profiles/traffic_le_ms_12_14336x4096.md"
 
     if not args.no_secondary:
         sec = {}
@@ -300,7 +364,24 @@ def main():
             sec["config3_gemm_q4k_14336x4096_m%d" % mt] = g
             log("gemm m=%d" % mt, g)
             torch.cuda.empty_cache()
+        # prefill-shaped GEMMs of the other types (config 2 down / head, config 5 shapes)
+        for tname, ty, r_, c_, mts in [("q6k_down_4096x14336", le.Q6_K, 4096, 14336, (17, 64, 512)),
+                                      ("q8_0_head_32000x4096", le.Q8_0, 32000, 4096, (64, 512)),
+                                      ("iq2xxs_14336x4096", le.IQ2_XXS, 14336, 4096, (64, 512)),
+                                      ("iq3xxs_4096x14336", le.IQ3_XXS, 4096, 14336, (64, 512))]:
+            for mt in mts:
+                g = bench_gemm(eng, ty, r_, c_, mt, max(20, steps2 // (1 + mt // 8)), 4)
+                sec["gemm_%s_m%d" % (tname, mt)] = g
+                log("gemm %s m=%d" % (tname, mt), g)
+                torch.cuda.empty_cache()
+        for size in (33030144, 9437184):
+            sec["stream_read_ceiling_%dB" % size] = bench_stream_read(eng, size, steps2, 20)
+            log("stream read", size, sec["stream_read_ceiling_%dB" % size])
         out["secondary"] = sec
+        ceil = sec.get("stream_read_ceiling_33030144B")
+        if ceil:
+            out["roofline"]["read_ceiling_GBs"] = ceil["GB/s"]
+            out["roofline"]["frac_of_read_ceiling"] = round(head["gbs"] / ceil["GB/s"], 4)
 
     if not args.no_cpu:
         out["cpu_baseline"] = cpu_baseline(le.Q4_K, host, rows, cols)

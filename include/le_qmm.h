@@ -124,6 +124,14 @@ size_t le_gemm_workspace_size(int ty, int m, int cols);
 int le_gemm(le_ctx *ctx, int ty, const void *w, const float *x, int m, float *y, int rows, int cols, void *ws,
             size_t ws_bytes, le_stream_t stream);
 
+/* ---- streaming-read probe (no counterpart in the reference; a measurement helper) ----
+ * Reads `bytes` (a multiple of 16) of device memory at buf the way the matvec kernels read weights
+ * (16-byte loads, consecutive lanes on consecutive chunks) and writes a checksum word per block to
+ * sink (le_stream_read_sink_bytes(ctx) bytes). Its time is the practical HBM read ceiling for that
+ * size; options "rd_nt", "rd_u", "rd_blocks_per_cu", "rd_block" choose the load form. */
+int le_stream_read(le_ctx *ctx, const void *buf, size_t bytes, void *sink, le_stream_t stream);
+int le_stream_read_sink_bytes(le_ctx *ctx);
+
 /* ---- le_gemm without a workspace argument (no counterpart in the reference) ----
  * For callers that cannot allocate device memory: code under HIP graph capture, tight serving
  * loops, harnesses that forbid hipMalloc. Same result as le_gemm (same kernels), with the

@@ -71,6 +71,7 @@ struct le_ctx {
     int mq_waves_auto = 1;   /* double mq_waves for grids smaller than the chip */
     int mq_waves = 4, mq_steps = 2, mq_blocks_per_cu = 2;
     int ms = 1, ms_p = 2;    /* staged MFMA variant and its super-blocks per row and step */
+    int rd_nt = 1, rd_u = 4, rd_blocks_per_cu = 1, rd_block = 512; /* le_stream_read probe shape */
     int ms_t = 1;            /* Q4_K with 2..8 tokens per pass on the staged MFMA kernel */
     int gm_mh = 1;           /* le_gemm, Q4_K, 3..8 tokens: the staged f16 MFMA kernel */
     int gm_mh_max = 16;      /* ... up to this many tokens (8 or 16; 16 only where K fits its LDS) */
@@ -445,6 +446,17 @@ int le_set_option(le_ctx *c, const char *name, int value) {
     } else if (n == "gm_split") {
         if (value != 0 && value != 1) return c->fail(LE_ERR_ARG, "gm_split must be 0 or 1");
         c->gm_split = value;
+    } else if (n == "rd_nt") {
+        c->rd_nt = value ? 1 : 0;
+    } else if (n == "rd_u") {
+        if (value != 1 && value != 2 && value != 4 && value != 8) return c->fail(LE_ERR_ARG, "rd_u must be 1, 2, 4 or 8");
+        c->rd_u = value;
+    } else if (n == "rd_blocks_per_cu") {
+        if (value < 1 || value > 16) return c->fail(LE_ERR_ARG, "rd_blocks_per_cu must be 1..16");
+        c->rd_blocks_per_cu = value;
+    } else if (n == "rd_block") {
+        if (value != 256 && value != 512) return c->fail(LE_ERR_ARG, "rd_block must be 256 or 512");
+        c->rd_block = value;
     } else if (n == "gq") {
         c->gq = value ? 1 : 0;
     } else if (n == "gq_min_m") {
@@ -799,6 +811,20 @@ int le_gemm(le_ctx *c, int ty, const void *w, const float *x, int m, float *y, i
     }
     return mv_launch(c, ty, nullptr, w, x, 0, cols, y, 0, rows, rows, cols, m, 1, (hipStream_t)stream);
 }
+
+int le_stream_read(le_ctx *c, const void *buf, size_t bytes, void *sink, le_stream_t stream) {
+    if (!c) return LE_ERR_ARG;
+    if (!buf || !sink || bytes < 16 || bytes % 16) return c->fail(LE_ERR_ARG, "buf, sink and a size that is a multiple of 16 bytes");
+    if (!al16(buf)) return c->fail(LE_ERR_ALIGN, "buf must be 16-byte aligned");
+    const unsigned blocks = (unsigned)c->cus * c->rd_blocks_per_cu;
+    unsigned long long n16 = bytes / 16;
+    void *args[] = {(void *)&buf, &n16, &sink};
+    char name[32];
+    snprintf(name, sizeof name, "le_read_nt%d_u%d", c->rd_nt, c->rd_u);
+    return c->launch(name, dim3(blocks), c->rd_block, 0, (hipStream_t)stream, args);
+}
+
+int le_stream_read_sink_bytes(le_ctx *c) { return c ? c->cus * 16 * 4 : 0; }
 
 }  // extern "C"
 

@@ -182,6 +182,33 @@ LE_DEQ(LE_TYPE_Q4_K, le_dequant_12)
 LE_DEQ(LE_TYPE_Q6_K, le_dequant_14)
 LE_DEQ(LE_TYPE_IQ2_XXS, le_dequant_16)
 LE_DEQ(LE_TYPE_IQ3_XXS, le_dequant_18)
+
+/* Streaming-read probe: the practical HBM read ceiling of this part at a given size, measured the
+ * way the matvec reads its weights (16-byte loads, consecutive lanes on consecutive chunks). Each
+ * thread keeps U loads in flight per trip of a grid-stride loop and folds every word into a
+ * checksum, so no load can be dropped; one word per block is written. NT: nontemporal loads. */
+template <bool NT, int U>
+__device__ __forceinline__ void read_probe(const u8 *__restrict__ buf, unsigned long long n16, u32 *sink) {
+    const unsigned long long stride = (unsigned long long)gridDim.x * blockDim.x;
+    u32 acc = 0;
+    for (unsigned long long i = (unsigned long long)blockIdx.x * blockDim.x + threadIdx.x; i < n16; i += stride * U) {
+        uint4 v[U];
+#pragma unroll
+        for (int u = 0; u < U; u++) {
+            const unsigned long long j = min(i + stride * u, n16 - 1);
+            v[u] = NT ? ldg16(buf + 16 * j) : ldg16c(buf + 16 * j);
+        }
+#pragma unroll
+        for (int u = 0; u < U; u++) acc += (v[u].x ^ v[u].y) + (v[u].z ^ v[u].w);
+    }
+    acc += __shfl_xor(acc, 1);
+    if (threadIdx.x == 0) sink[blockIdx.x] = acc;
+}
+#define LE_RD(NT, U) \
+    extern "C" __global__ void __launch_bounds__(512) le_read_nt##NT##_u##U(const u8 *buf, unsigned long long n16, u32 *sink) { \
+        read_probe<NT, U>(buf, n16, sink);                                                              \
+    }
+LE_RD(0, 1) LE_RD(0, 2) LE_RD(0, 4) LE_RD(0, 8) LE_RD(1, 1) LE_RD(1, 2) LE_RD(1, 4) LE_RD(1, 8)
 #endif
 
 /* ===================================================================================== */

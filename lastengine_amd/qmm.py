@@ -62,6 +62,8 @@ def lib():
         "le_gemm_workspace_size": (S, [I, I, I]),
         "le_gemm": (I, [P, I, P, P, I, P, I, I, P, S, P]),
         "le_gemm_noalloc": (I, [P, I, P, P, I, P, I, I, P]),
+        "le_stream_read": (I, [P, P, S, P, P]),
+        "le_stream_read_sink_bytes": (I, [P]),
         "le_moe_workspace_size": (S, [I, I, I]),
         "le_moe_layer": (I, [P, I, I, I, P, P, P, I, I, I, I, P, P, I, P, P, P, P, S, P]),
         "le_fill_normal": (None, [P, S, ctypes.c_uint64, ctypes.c_uint64, D, D, I]),
@@ -210,3 +212,10 @@ class Engine:
         (for graph capture and serving loops). Calls overlapping on one GPU race."""
         self._check(self._L.le_gemm_noalloc(self._ctx, ty, _ptr(w), _ptr(x), m, _ptr(out), rows, cols,
                                             _stream(stream)))
+
+    def stream_read(self, buf, nbytes, sink, stream=None):
+        """Streaming-read probe over nbytes of buf (the practical HBM read ceiling at that size)."""
+        self._check(self._L.le_stream_read(self._ctx, _ptr(buf), int(nbytes), _ptr(sink), _stream(stream)))
+
+    def stream_read_sink_bytes(self):
+        return int(self._L.le_stream_read_sink_bytes(self._ctx))
