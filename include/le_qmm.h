@@ -47,7 +47,8 @@ enum le_status {
     LE_ERR_ALIGN = -4,  /* activation/output pointer or stride not 16-byte aligned */
     LE_ERR_HIP = -5,    /* a HIP runtime call failed (reference: .expect("launch"), src/gpu.rs:221) */
     LE_ERR_MODULE = -6, /* code object missing / unloadable, or device is not gfx950 */
-    LE_ERR_WORKSPACE = -7 /* workspace too small */
+    LE_ERR_WORKSPACE = -7, /* workspace too small */
+    LE_ERR_TIMEOUT = -8    /* a bounded device-side wait gave up (le_moe_check) */
 };
 
 /* ---- geometry (src/quant.rs:24-35) ---- */
@@ -154,12 +155,24 @@ int le_gemm_noalloc(le_ctx *ctx, int ty, const void *w, const float *x, int m, f
  * (ty_down), slab e at e * rows * row_bytes. Routing and grouping by expert run on the device
  * (no host synchronisation); each routed expert's weights are read once per call. idx_out/w_out
  * (n_tok*k, optional) receive the selection. ws: device workspace of le_moe_workspace_size bytes.
- * Limits: n_tok <= 64, k <= 16, n_exp <= 256, hidden and ff multiples of 256. */
+ * Limits: n_tok <= 64, k <= 16, n_exp <= 256, hidden and ff multiples of 256.
+ * For 3..8 tokens at hidden 2048 the layer runs as one launch with a device-wide barrier between
+ * gate/up and down. That launch sizes its grid to the blocks that fit on the device at once and
+ * assumes nothing else occupies it: a concurrent kernel on another stream can make its bounded
+ * waits (about a second, option "moe_spin_limit") give up, and the launch then writes NaN to out
+ * and sets a status word in ws that le_moe_check reports. The barrier state lives in ws, so calls
+ * with different workspaces are independent; calls that share a workspace must not overlap.
+ * Zero-fill ws once when it is allocated (it is then fully rewritten by every call). */
 size_t le_moe_workspace_size(int n_tok, int k, int ff);
 int le_moe_layer(le_ctx *ctx, int ty_gate, int ty_up, int ty_down, const void *gate, const void *up,
                  const void *down, int n_exp, int k, int hidden, int ff, const float *logits, const float *h,
                  int n_tok, float *out, int *idx_out, float *w_out, void *ws, size_t ws_bytes,
                  le_stream_t stream);
+/* Status of the MoE layer calls made with workspace ws (no counterpart in the reference, which
+ * has no device-side waits): synchronizes `stream`, returns LE_ERR_TIMEOUT (and clears the status)
+ * if a one-launch layer on ws gave up at its barrier since the last check, else LE_OK. Not for use
+ * under graph capture. */
+int le_moe_check(le_ctx *ctx, const void *ws, le_stream_t stream);
 
 #ifdef __cplusplus
 }

@@ -11,6 +11,7 @@
 
 #include <cstdarg>
 #include <cstdio>
+#include <atomic>
 #include <cstring>
 #include <map>
 #include <string>
@@ -47,7 +48,15 @@ struct MoeArgs {
     int *idx_out;
     float *w_out;
     int n_tok, n_exp, k, hidden, ff;
+    unsigned int spin_limit;
+    unsigned long long epoch;
+    void *bar;
 };
+/* Barrier area at the start of an MoE workspace (status word, generation word, one 8-byte arrival
+ * flag per block of the one-launch kernel, LE_MOE_MAXGRID = 1024 blocks). */
+constexpr size_t kMoeBarBytes = 128 + 8 * 1024;
+/* Epochs of the one-launch MoE barrier: unique per launch within the process. */
+std::atomic<unsigned long long> g_moe_epoch{0};
 int table_bytes(int ty) {
     if (ty == LE_TYPE_IQ2_XXS) return 4 * (256 + 512);
     if (ty == LE_TYPE_IQ3_XXS) return 4 * (256 + 256);
@@ -82,6 +91,7 @@ struct le_ctx {
     int moe_mfma = 1;        /* decode-shaped MoE on the staged MFMA kernels where the types allow */
     int moe_fused = 1;       /* ... in one launch with a device-wide barrier where the grid fits */
     int moe_fused_min_tok = 3; /* ... from this many tokens on (below, two launches are faster) */
+    unsigned int moe_spin_limit = 1u << 20; /* polls before a barrier wait gives up (about a second); 0 fails it */
     std::map<std::string, int> occ; /* resident blocks per CU, by kernel name and LDS bytes */
     int gm_min_m = 5;        /* le_gemm uses the MFMA GEMM from this many tokens on (below: the
                                 staged matvec with 2..4 tokens per pass, faster there) */
@@ -366,6 +376,7 @@ const char *le_status_str(int s) {
     case LE_ERR_HIP: return "HIP runtime error";
     case LE_ERR_MODULE: return "code object missing or device unsupported";
     case LE_ERR_WORKSPACE: return "workspace too small";
+    case LE_ERR_TIMEOUT: return "a bounded device-side wait gave up";
     }
     return "unknown status";
 }
@@ -483,6 +494,9 @@ int le_set_option(le_ctx *c, const char *name, int value) {
         c->gm_min_m = value;
     } else if (n == "moe_fused_min_tok") {
         c->moe_fused_min_tok = value;
+    } else if (n == "moe_spin_limit") {
+        if (value < 0) return c->fail(LE_ERR_ARG, "moe_spin_limit must be >= 0");
+        c->moe_spin_limit = (unsigned int)value;
     } else if (n == "moe_fused") {
         c->moe_fused = value ? 1 : 0;
     } else if (n == "moe_mfma") {
@@ -551,7 +565,23 @@ size_t le_moe_workspace_size(int n_tok, int k, int ff) {
     if (n_tok <= 0 || k <= 0 || ff <= 0) return 0;
     /* per (token, slot) the down projection's activation image, then (staged path) a routing record */
     const size_t img = (size_t)xtok_bytes(ff) > (size_t)(ff / 256) * 608 ? (size_t)xtok_bytes(ff) : (size_t)(ff / 256) * 608;
-    return (size_t)n_tok * (size_t)k * img + 16 + 256 * 4 + 256 * 8 + 1024 * 4 + 1024 * 4;
+    return kMoeBarBytes + (size_t)n_tok * (size_t)k * img + 16 + 256 * 4 + 256 * 8 + 1024 * 4 + 1024 * 4;
+}
+
+int le_moe_check(le_ctx *c, const void *ws, le_stream_t stream) {
+    if (!c) return LE_ERR_ARG;
+    if (!ws) return c->fail(LE_ERR_ARG, "null workspace");
+    int rc = c->hip(hipStreamSynchronize((hipStream_t)stream), "le_moe_check: stream synchronize");
+    if (rc) return rc;
+    unsigned int st = 0;
+    rc = c->hip(hipMemcpy(&st, ws, sizeof st, hipMemcpyDeviceToHost), "le_moe_check: status read");
+    if (rc) return rc;
+    if (st != 0x5EAD0001u) return LE_OK; /* the value the one-launch kernel stores after a give-up */
+    const unsigned int zero = 0;
+    rc = c->hip(hipMemcpy((void *)ws, &zero, sizeof zero, hipMemcpyHostToDevice), "le_moe_check: status clear");
+    if (rc) return rc;
+    return c->fail(LE_ERR_TIMEOUT, "a one-launch MoE layer on this workspace gave up at its device-wide barrier "
+                                   "(its outputs are NaN): the grid was not resident at once");
 }
 
 int le_moe_layer(le_ctx *c, int ty_gate, int ty_up, int ty_down, const void *gate, const void *up, const void *down,
@@ -572,7 +602,8 @@ int le_moe_layer(le_ctx *c, int ty_gate, int ty_up, int ty_down, const void *gat
     if (!al16(h) || !al16(ws)) return c->fail(LE_ERR_ALIGN, "h and ws must be 16-byte aligned");
     const size_t lds = (size_t)8 * xtok_bytes(hidden);
     if (lds + 16384 > c->lds_limit) return c->fail(LE_ERR_SHAPE, "hidden=%d exceeds the LDS budget", hidden);
-    MoeArgs a{gate, up, down, logits, h, out, ws, idx_out, w_out, n_tok, n_exp, k, hidden, ff};
+    MoeArgs a{gate, up, down, logits, h, out, (char *)ws + kMoeBarBytes, idx_out, w_out, n_tok, n_exp, k, hidden, ff,
+              c->moe_spin_limit, ++g_moe_epoch, ws};
     void *args[] = {&a};
     char name[64];
     const int nsb = hidden / 256, g8 = nsb % 8 == 0;

@@ -1382,11 +1382,20 @@ struct MoeArgs {
     const u8 *gate, *up, *down;
     const float *logits, *h;
     float *out;
-    u8 *ws;
+    u8 *ws; /* the caller's workspace after its barrier area (images, then the routing record) */
     int *idx_out;
     float *w_out;
     int n_tok, n_exp, k, hidden, ff;
+    unsigned int spin_limit;  /* bounded waits of the one-launch barrier; 0 makes it fail */
+    unsigned long long epoch; /* unique per launch (process-wide counter on the host) */
+    u8 *bar;                  /* the caller's workspace start: barrier area (LE_MOE_BAR_BYTES) */
 };
+/* Barrier area at the start of the workspace: a status word (sticky, nonzero after a wait gave
+ * up; read and cleared by le_moe_check), the generation word, then one arrival flag per block. */
+#define LE_MOE_BAR_STATUS 0
+#define LE_MOE_BAR_FAILED 0x5EAD0001u /* status word value after a give-up (any other value: none) */
+#define LE_MOE_BAR_GEN 64
+#define LE_MOE_BAR_FLAGS 128
 #define LE_MOE_MAXTOK 64
 #define LE_MOE_MAXK 16
 #define LE_MOE_MAXEXP 256
@@ -2456,58 +2465,72 @@ __device__ __forceinline__ void moe_dnm_body(const MoeArgs &a) {
  * blocks. Every block routes. Phase 1: blocks take the (32-row unit, expert group) items of the
  * gate/up projection round-robin, as in le_moe_gum (hidden 2048). Before that, each block issues
  * the weight loads of its first down group (they depend on the routing only), so they arrive
- * while phase 1 runs. A barrier over all blocks (per-block arrival flags and a generation word in
- * device memory, bounded wait) separates the phases. Phase 2: row tile b mod ntile of the down
- * projection as in le_moe_dnm; when the grid has at least two blocks per tile, blocks b and
- * b + ntile split the tile's expert groups and add into the output (zeroed in phase 1). If a wait
- * ever exceeds its bound the block writes NaN to its outputs rather than waiting on. */
+ * while phase 1 runs. A barrier over all blocks separates the phases. Phase 2: row tile b mod
+ * ntile of the down projection as in le_moe_dnm; when the grid has at least two blocks per tile,
+ * blocks b and b + ntile split the tile's expert groups and add into the output (zeroed in
+ * phase 1).
+ *
+ * Barrier. Its state lives in the caller's workspace (so launches with different workspaces never
+ * share it): per block an arrival flag, one generation word and a status word. Each launch
+ * carries an epoch that no earlier launch used, so a flag or generation left by an earlier launch
+ * (or a late block of a launch that gave up) never matches. Block 0 polls every flag and then
+ * publishes either the epoch or, if a wait gave up, the epoch with the top bit set; every other
+ * block waits for one of the two. Every wait is bounded (spin_limit polls); a block whose wait
+ * gave up, or that sees the failure generation, sets the status word (to LE_MOE_BAR_FAILED, a
+ * value an uninitialised workspace holds with probability 2^-32) and writes NaN to all of
+ * its outputs, so a failed launch is visible in the output and through le_moe_check. Launches
+ * that share one workspace must not overlap (two streams), and the grid assumes it is resident
+ * by itself: a concurrent kernel that occupies CUs can make the waits give up. */
 #define LE_MOE_MAXGRID 1024
-__device__ unsigned int le_moe_bar_flag[LE_MOE_MAXGRID]; /* per block: the epoch it last arrived in */
-__device__ unsigned int le_moe_bar_gen;                  /* completed barriers */
 
-/* Arrival is a plain store of this barrier's epoch (gen + 1) to the block's own flag, so no
- * arrival contends with another; block 0 polls all flags in parallel and then publishes the new
- * generation. Callers store what other blocks read after the barrier with device-coherent stores
- * (mq_quant_seg<.., true>). Every wait is bounded; false means a wait gave up. */
+/* Arrival is a plain store of the epoch to the block's own flag, so no arrival contends with
+ * another; block 0 polls all flags in parallel. Callers store what other blocks read after the
+ * barrier with device-coherent stores (mq_quant_seg<.., true>). Returns false when a wait gave up
+ * or block 0 published a failure. */
 template <class F>
-__device__ __forceinline__ bool moe_grid_barrier(unsigned int nblocks, F &&after_arrival) {
-    __shared__ unsigned int gen_s;
+__device__ __forceinline__ bool moe_grid_barrier(const MoeArgs &a, unsigned int nblocks, F &&after_arrival) {
     __shared__ int ok_s;
+    unsigned int *status = (unsigned int *)(a.bar + LE_MOE_BAR_STATUS);
+    unsigned long long *gen = (unsigned long long *)(a.bar + LE_MOE_BAR_GEN);
+    unsigned long long *flag = (unsigned long long *)(a.bar + LE_MOE_BAR_FLAGS);
+    const unsigned long long ep = a.epoch, fail = a.epoch | (1ull << 63);
     __builtin_amdgcn_s_waitcnt(0x0F70); /* vmcnt(0): this thread's coherent stores have completed */
     __syncthreads();
     if (threadIdx.x == 0) {
-        const unsigned int gen = __hip_atomic_load(&le_moe_bar_gen, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        gen_s = gen;
-        ok_s = 1;
+        ok_s = a.spin_limit > 0; /* a zero limit is the host's way to make the barrier fail */
         /* the data other blocks read was stored device-coherently and has completed (the block
          * barrier above waits for it), so the arrival needs no L2 writeback */
-        __hip_atomic_store(&le_moe_bar_flag[blockIdx.x], gen + 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        __hip_atomic_store(&flag[blockIdx.x], ep, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     }
     __syncthreads();
-    const unsigned int epoch = gen_s + 1u;
     after_arrival(); /* work that must not delay the arrival (its loads are not waited for above) */
     if (blockIdx.x == 0) {
         for (unsigned int i = threadIdx.x; i < nblocks; i += blockDim.x) {
             unsigned int spins = 0;
             /* relaxed polls (an acquire per poll would invalidate L2 every time); one acquire after */
-            while (__hip_atomic_load(&le_moe_bar_flag[i], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) != epoch) {
-                __builtin_amdgcn_s_sleep(1);
-                if (++spins > (1u << 20)) { /* about a second of polling: give up instead of hanging */
+            while (__hip_atomic_load(&flag[i], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) != ep) {
+                if (spins++ >= a.spin_limit) { /* give up instead of hanging */
                     ok_s = 0;
                     break;
                 }
+                __builtin_amdgcn_s_sleep(1);
             }
         }
         __syncthreads();
-        if (threadIdx.x == 0) __hip_atomic_store(&le_moe_bar_gen, epoch, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        if (threadIdx.x == 0) {
+            if (!ok_s) __hip_atomic_store(status, LE_MOE_BAR_FAILED, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            __hip_atomic_store(gen, ok_s ? ep : fail, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        }
     } else if (threadIdx.x == 0) {
         unsigned int spins = 0;
-        while (__hip_atomic_load(&le_moe_bar_gen, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) != epoch) {
+        unsigned long long g;
+        while ((g = __hip_atomic_load(gen, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT)) != ep && g != fail) {
+            if (spins++ >= a.spin_limit) break;
             __builtin_amdgcn_s_sleep(1);
-            if (++spins > (1u << 20)) {
-                ok_s = 0;
-                break;
-            }
+        }
+        if (g != ep) {
+            ok_s = 0;
+            __hip_atomic_store(status, LE_MOE_BAR_FAILED, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         }
     }
     __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
@@ -2689,7 +2712,7 @@ __device__ __forceinline__ void moe_fus_body(const MoeArgs &a) {
     LE_TRACE_POINT(2);
     /* the first down group of this block's tile is issued after the arrival, so its loads are in
      * flight through the wait */
-    const bool ok = moe_grid_barrier(G, [&]() {
+    const bool ok = moe_grid_barrier(a, G, [&]() {
         if (b < H * ntile && hh + H * wave < R.U) dissue(hh + H * wave, R0);
     });
     LE_TRACE_POINT(3);

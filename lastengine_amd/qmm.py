@@ -23,7 +23,8 @@ TYPES = {"Q8_0": Q8_0, "Q4_K": Q4_K, "Q6_K": Q6_K, "IQ2_XXS": IQ2_XXS, "IQ3_XXS"
 
 _STATUS = {0: "ok", -1: "invalid argument", -2: "unsupported quant type", -3: "unsupported shape",
            -4: "misaligned pointer or stride", -5: "HIP runtime error",
-           -6: "code object missing or device unsupported", -7: "workspace too small"}
+           -6: "code object missing or device unsupported", -7: "workspace too small",
+           -8: "a bounded device-side wait gave up"}
 
 
 class LeError(RuntimeError):
@@ -66,6 +67,7 @@ def lib():
         "le_stream_read_sink_bytes": (I, [P]),
         "le_moe_workspace_size": (S, [I, I, I]),
         "le_moe_layer": (I, [P, I, I, I, P, P, P, I, I, I, I, P, P, I, P, P, P, P, S, P]),
+        "le_moe_check": (I, [P, P, P]),
         "le_fill_normal": (None, [P, S, ctypes.c_uint64, ctypes.c_uint64, D, D, I]),
         "le_quantize_rows": (I, [I, P, P, S, S, I]),
         "le_f32_to_f16": (ctypes.c_uint16, [F]),
@@ -185,12 +187,17 @@ class Engine:
         """Routed MoE layer (cpu_ref::moe, src/cpu_ref.rs:242-259) for n_tok tokens."""
         if ws is None:
             import torch
-            ws = torch.empty(max(16, self.moe_workspace_size(n_tok, k, ff)), dtype=torch.uint8, device="cuda")
+            ws = torch.zeros(max(16, self.moe_workspace_size(n_tok, k, ff)), dtype=torch.uint8, device="cuda")
         if ws_bytes is None:
             ws_bytes = ws.numel() if hasattr(ws, "numel") else 0
         self._check(self._L.le_moe_layer(self._ctx, ty_gate, ty_up, ty_down, _ptr(gate), _ptr(up), _ptr(down), n_exp,
                                          k, hidden, ff, _ptr(logits), _ptr(h), n_tok, _ptr(out), _ptr(idx_out),
                                          _ptr(w_out), _ptr(ws), ws_bytes, _stream(stream)))
+
+    def moe_check(self, ws, stream=None):
+        """Raise LeError(-8) if a one-launch MoE layer on workspace ws gave up at its device-wide
+        barrier since the last check (synchronizes the stream)."""
+        self._check(self._L.le_moe_check(self._ctx, _ptr(ws), _stream(stream)))
 
     def gemm_workspace_size(self, ty, m, cols):
         return int(self._L.le_gemm_workspace_size(ty, m, cols))

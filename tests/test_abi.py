@@ -142,3 +142,10 @@ def test_gemm_workspace_size():
     assert L.le_gemm_workspace_size(12, 0, 4096) == 0
     assert L.le_gemm_workspace_size(12, 16, 100) == 0
     assert L.le_gemm_workspace_size(99, 16, 256) == 0
+
+
+def test_moe_check_rejects_null_context():
+    """le_moe_check validates its arguments on the host before touching the device."""
+    L = qmm.lib()
+    assert L.le_moe_check(None, None, None) == -1
+    assert L.le_status_str(-8) == b"a bounded device-side wait gave up"

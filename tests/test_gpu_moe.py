@@ -171,3 +171,14 @@ def test_moe_one_launch_repeated(engine):
             first = got
         else:
             assert np.array_equal(got.view(np.uint32), first.view(np.uint32))
+
+
+def test_moe_limits(engine):
+    """The documented limits at their bounds: 64 tokens, top-16."""
+    run(engine, le.Q4_K, le.Q6_K, 32, 16, 256, 256, 64, seed=700)
+
+
+@pytest.mark.parametrize("n_tok", [16, 64])
+def test_moe_config4_more_tokens(engine, n_tok):
+    """Config 4 beyond the decode-shaped kernels (the vector member-chunk path)."""
+    run(engine, le.Q4_K, le.Q6_K, 128, 8, 2048, 768, n_tok, seed=720 + n_tok)
