@@ -92,6 +92,7 @@ struct le_ctx {
     int moe_fused = 1;       /* ... in one launch with a device-wide barrier where the grid fits */
     int moe_fused_min_tok = 3; /* ... from this many tokens on (below, two launches are faster) */
     unsigned int moe_spin_limit = 1u << 20; /* polls before a barrier wait gives up (about a second); 0 fails it */
+    int moe_dn_split = 0;    /* down launch blocks per row tile: 0 auto, 1, 2 */
     std::map<std::string, int> occ; /* resident blocks per CU, by kernel name and LDS bytes */
     int gm_min_m = 5;        /* le_gemm uses the MFMA GEMM from this many tokens on (below: the
                                 staged matvec with 2..4 tokens per pass, faster there) */
@@ -497,6 +498,9 @@ int le_set_option(le_ctx *c, const char *name, int value) {
     } else if (n == "moe_spin_limit") {
         if (value < 0) return c->fail(LE_ERR_ARG, "moe_spin_limit must be >= 0");
         c->moe_spin_limit = (unsigned int)value;
+    } else if (n == "moe_dn_split") {
+        if (value < 0 || value > 2) return c->fail(LE_ERR_ARG, "moe_dn_split must be 0, 1 or 2");
+        c->moe_dn_split = value;
     } else if (n == "moe_fused") {
         c->moe_fused = value ? 1 : 0;
     } else if (n == "moe_mfma") {
@@ -641,7 +645,10 @@ int le_moe_layer(le_ctx *c, int ty_gate, int ty_up, int ty_down, const void *gat
             int rc = c->launch(name, dim3((unsigned)(ff / 32), (unsigned)groups), 64 * gw, lds_g, (hipStream_t)stream, args);
             if (rc) return rc;
             snprintf(name, sizeof name, "le_moe_dnm_%d_w8_p%d", ty_down, dp);
-            return c->launch(name, dim3((unsigned)(hidden / 16)), 512, lds_d, (hipStream_t)stream, args);
+            /* two blocks per row tile when the tiles alone leave CUs idle (each adds its half of the
+             * expert groups into the output the gate/up launch zeroed) */
+            const int hsplit = c->moe_dn_split == 2 || (c->moe_dn_split == 0 && hidden / 16 * 2 <= c->cus) ? 2 : 1;
+            return c->launch(name, dim3((unsigned)(hsplit * hidden / 16)), 512, lds_d, (hipStream_t)stream, args);
         }
     }
     /* decode-shaped fast paths: few tokens, short rows */

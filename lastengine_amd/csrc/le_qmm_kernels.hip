@@ -1541,7 +1541,7 @@ struct MoeLogits {
  * wave-wide max; lane l holds experts l*per .. l*per+per-1) instead of ranking every key. One
  * token keeps the ranking, spread over eight lanes per expert (measured faster there). */
 __device__ __forceinline__ bool moe_route_by_wave(const MoeArgs &a) {
-    return a.n_tok >= 2 && a.n_tok <= (int)(blockDim.x >> 6) && a.n_exp <= 256;
+    return a.n_tok >= 1 && a.n_tok <= (int)(blockDim.x >> 6) && a.n_exp <= 256;
 }
 __device__ __forceinline__ MoeLogits moe_route_load(const MoeArgs &a) {
     MoeLogits L;
@@ -1599,32 +1599,65 @@ __device__ __forceinline__ void moe_route_par(const MoeArgs &a, MoeRoute &R, uns
         __syncthreads(); /* the mask clear above, before the atomics */
         const int lane = threadIdx.x & 63, t = threadIdx.x >> 6, per = (a.n_exp + 63) >> 6;
         if (t < a.n_tok) {
-            bool taken[MOE_LPASS];
+            /* k rounds of a wave-wide max with no branch: round r's winner (the lowest lane among
+             * equal values, whose lowest untaken index is the lowest expert: expert = lane * per
+             * + j) ends up in lane r's registers, and all k are written to LDS at the end */
+            float vv[MOE_LPASS];
 #pragma unroll
-            for (int j = 0; j < MOE_LPASS; j++) taken[j] = !(j < per && lane * per + j < a.n_exp);
+            for (int j = 0; j < MOE_LPASS; j++) vv[j] = j < per && lane * per + j < a.n_exp ? L.v[j] : -INFINITY;
+            int my_e = 0;
+            float my_v = 0.f;
             for (int r = 0; r < a.k; r++) {
-                /* the lane's best untaken key (strict >: the lower expert of equal logits), then
-                 * the wave's largest; among tied lanes the lowest holds the lowest expert */
-                float bv = -INFINITY;
-                int bj = -1;
+                float bv = vv[0];
+                int bj = 0;
 #pragma unroll
-                for (int j = 0; j < MOE_LPASS; j++)
-                    if (!taken[j] && (bj < 0 || L.v[j] > bv)) { bv = L.v[j]; bj = j; }
-                const float mx = wave_max(bj >= 0 ? bv : -INFINITY);
-                const unsigned long long cand = __ballot(bj >= 0 && bv == mx);
-                const int wl = __ffsll((long long)cand) - 1;
-                if (lane == wl) {
-#pragma unroll
-                    for (int j = 0; j < MOE_LPASS; j++)
-                        if (j == bj) taken[j] = true;
-                    const int e = lane * per + bj;
-                    R.topi[t * a.k + r] = e;
-                    sx[t * a.k + r] = bv;
-                    atomicOr(&R.mask[e], 1ull << t);
+                for (int j = 1; j < MOE_LPASS; j++) {
+                    const bool gt = vv[j] > bv; /* strict: the lower index of equal values stays */
+                    bv = gt ? vv[j] : bv;
+                    bj = gt ? j : bj;
                 }
+                const float mx = wave_max(bv);
+                const int wl = __ffsll((long long)__ballot(bv == mx)) - 1;
+                const int wj = __builtin_amdgcn_readlane(bj, wl);
+#pragma unroll
+                for (int j = 0; j < MOE_LPASS; j++) vv[j] = lane == wl && j == wj ? -INFINITY : vv[j];
+                my_e = lane == r ? wl * per + wj : my_e;
+                my_v = lane == r ? mx : my_v;
+            }
+            if (lane < a.k) {
+                R.topi[t * a.k + lane] = my_e;
+                sx[t * a.k + lane] = my_v;
+                atomicOr(&R.mask[my_e], 1ull << t);
             }
         }
         LE_TRACE_POINT(8);
+        if (a.n_tok == 1) {
+            /* one token: wave 0 holds the k selections; it writes the renormalised weights and
+             * the groups (the k experts in ascending order) itself, with no further LDS pass */
+            if (threadIdx.x < 64) {
+                __builtin_amdgcn_wave_barrier();
+                __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+                __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+                const bool sel = lane < a.k;
+                const float v = sel ? sx[lane] : -INFINITY, top = sx[0];
+                const int e = sel ? R.topi[lane] : 0x7FFFFFFF;
+                /* sum of the k exponentials in selection order (as the general path adds them) */
+                const float ex = sel ? expf(v - top) : 0.f;
+                float tot = 0.f;
+                for (int r = 0; r < a.k; r++) tot += __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, ex), r));
+                int rank = 0;
+                for (int r = 0; r < a.k; r++) rank += __builtin_amdgcn_readlane(e, r) < e;
+                if (sel) {
+                    R.topw[lane] = ex / tot;
+                    R.grp_e[rank] = e;
+                }
+                if (lane == 0) R.U = a.k;
+            }
+            LE_TRACE_POINT(9);
+            __syncthreads();
+            LE_TRACE_POINT(1);
+            return;
+        }
         LE_TRACE_POINT(9);
         LE_TRACE_POINT(10);
         __syncthreads();
@@ -1728,13 +1761,14 @@ __device__ __forceinline__ void moe_rec_read(const MoeArgs &a, MoeRoute &R, cons
     const unsigned long long *rm = (const unsigned long long *)(rec + 16 + 256 * 4);
     const int *rt = (const int *)(rec + 16 + 256 * 12);
     const float *rw = (const float *)(rec + 16 + 256 * 12 + 1024 * 4);
-    const int U = *(const LE_GLOBAL int *)ri;
-    /* every thread issues its loads before any store */
+    /* every load issued at once (the record's arrays have fixed sizes: no load depends on U) */
     const int z = threadIdx.x;
-    const int ge = z < U ? *(const LE_GLOBAL int *)(ri + 4 + z) : 0;
-    const unsigned long long gm = z < U ? *(const LE_GLOBAL unsigned long long *)(rm + z) : 0ull;
-    const int ti = z < nsel ? *(const LE_GLOBAL int *)(rt + z) : 0;
-    const float tw = z < nsel ? *(const LE_GLOBAL float *)(rw + z) : 0.f;
+    const int U = *(const LE_GLOBAL int *)ri;
+    const int zc = min(z, 255), sc = min(z, 1023);
+    const int ge = *(const LE_GLOBAL int *)(ri + 4 + zc);
+    const unsigned long long gm = *(const LE_GLOBAL unsigned long long *)(rm + zc);
+    const int ti = *(const LE_GLOBAL int *)(rt + sc);
+    const float tw = *(const LE_GLOBAL float *)(rw + sc);
     if (z == 0) R.U = U;
     if (z < U) {
         R.grp_e[z] = ge;
@@ -2248,6 +2282,8 @@ __device__ __forceinline__ void moe_gum_body(const MoeArgs &a) {
             if (a.w_out) a.w_out[i] = R.topw[i];
         }
         moe_rec_write(a, R, a.ws + (size_t)a.n_tok * a.k * LE_MOE_IMG(a.ff));
+        /* the down launch may split a row tile over two blocks that add into the output */
+        for (int i = threadIdx.x; i < a.n_tok * a.hidden; i += blockDim.x) a.out[i] = 0.f;
     }
     /* 2. the four tiles of this wave's super-blocks (gate rows 32ux.., +16, up rows 32ux.., +16),
      * packed: chunk c = (tile, row, column) of 4 x 16 x CPR, all in flight at once */
@@ -2359,13 +2395,28 @@ __device__ __forceinline__ void moe_dnm_body(const MoeArgs &a) {
     LE_TRACE_DECL;
     LE_TRACE_POINT(0);
     for (int i = threadIdx.x; i < NW * LE_MOE_FAST_TOK * 16; i += blockDim.x) (&red[0][0][0])[i] = 0.f;
+    const int npair = a.n_tok * a.k;
+    const bool all_in = npair <= LE_MOE_DN_IMGS;
+    /* every pair's down image (written by the gate/up launch; needs no routing), issued before
+     * the routing record is read so the two round trips overlap */
+    uint4 iv[2][4];
+    static_assert(LE_MOE_DN_IMGS * IMGC <= 8 * 64 * NW, "the image preload covers every image chunk");
+    const int nci = npair * IMGC;
+    if (all_in) {
+#pragma unroll
+        for (int u = 0; u < 2; u++)
+#pragma unroll
+            for (int q = 0; q < 4; q++) iv[u][q] = ldg16c(a.ws + 16 * (size_t)min((int)threadIdx.x + 64 * NW * (4 * u + q), nci - 1));
+    }
     /* the routing of the gate/up launch (n_tok * k <= 64 <= blockDim.x, groups <= 64) */
     moe_rec_read(a, R, a.ws + (size_t)a.n_tok * a.k * IMG);
     LE_TRACE_POINT(1);
-    const int npair = a.n_tok * a.k;
-    const bool all_in = npair <= LE_MOE_DN_IMGS;
     const size_t rb = (size_t)P * SBB;
-    const int row0 = 16 * blockIdx.x;
+    /* H blocks per 16-row tile (grid = H * hidden / 16): block hh of a tile takes the expert groups
+     * z = hh (mod H) and, with H = 2, adds into the output the gate/up launch zeroed (every
+     * element is 0 + a + b in either order: the same bits) */
+    const int ntile = a.hidden >> 4, H = gridDim.x / ntile, hh = blockIdx.x / ntile;
+    const int row0 = 16 * (blockIdx.x % ntile);
     int roff[NI];
 #pragma unroll
     for (int i = 0; i < NI; i++) {
@@ -2379,19 +2430,16 @@ __device__ __forceinline__ void moe_dnm_body(const MoeArgs &a) {
 #pragma unroll
         for (int i = 0; i < NI; i++) r[i] = TD == LE_TYPE_Q6_K ? ldg16u(W + roff[i]) : ldg16(W + roff[i]);
     };
-    if (wave < R.U) issue(wave, R0);
-    if (wave + NW < R.U) issue(wave + NW, R1);
-    if (all_in) { /* every pair's down image */
-        const int nc = npair * IMGC;
-#pragma unroll 1
-        for (int c0 = threadIdx.x; c0 < nc; c0 += 4 * 64 * NW) {
-            uint4 v[4];
+    if (hh + H * wave < R.U) issue(hh + H * wave, R0);
+    if (hh + H * (wave + NW) < R.U) issue(hh + H * (wave + NW), R1);
+    if (all_in) { /* the images loaded above (LE_MOE_DN_IMGS * IMGC <= 8 * 64 * NW chunks) */
 #pragma unroll
-            for (int q = 0; q < 4; q++) v[q] = ldg16c(a.ws + 16 * (size_t)min(c0 + 64 * NW * q, nc - 1));
+        for (int u = 0; u < 2; u++)
 #pragma unroll
-            for (int q = 0; q < 4; q++)
-                if (c0 + 64 * NW * q < nc) imgs[c0 + 64 * NW * q] = v[q];
-        }
+            for (int q = 0; q < 4; q++) {
+                const int c = (int)threadIdx.x + 64 * NW * (4 * u + q);
+                if (c < nci) imgs[c] = iv[u][q];
+            }
     }
     __syncthreads(); /* the images, and the routing keys are no longer read before staging reuses them */
     LE_TRACE_POINT(5);
@@ -2401,7 +2449,7 @@ __device__ __forceinline__ void moe_dnm_body(const MoeArgs &a) {
     for (int b = 0; b < 4; b++) A[b] = (le_v4i){0, 0, 0, 0};
     uint4 *wimg = imgs + wave * SLOTS * IMGC;
 #pragma unroll 1
-    for (int z = wave; z < R.U; z += NW) {
+    for (int z = hh + H * wave; z < R.U; z += H * NW) {
         const int e = R.grp_e[z];
         const int nmem = __popcll(R.mask[e]);
         if (lane < nmem) {
@@ -2417,8 +2465,8 @@ __device__ __forceinline__ void moe_dnm_body(const MoeArgs &a) {
             wb[64 * i + lane] = R0[i];
             R0[i] = R1[i];
         }
-        if (z + 2 * NW < R.U) issue(z + 2 * NW, R1);
-        if (z == wave) LE_TRACE_POINT(6);
+        if (z + 2 * H * NW < R.U) issue(z + 2 * H * NW, R1);
+        if (z == hh + H * wave) LE_TRACE_POINT(6);
 #pragma unroll 1
         for (int i = 0; i < nmem; i++) {
             const uint4 *rec;
@@ -2444,7 +2492,7 @@ __device__ __forceinline__ void moe_dnm_body(const MoeArgs &a) {
             y += __shfl_xor(y, 32);
             if (lane < 16) red[wave][mtok[wave][i]][lane] += mw[wave][i] * y;
         }
-        if (z == wave) LE_TRACE_POINT(7);
+        if (z == hh + H * wave) LE_TRACE_POINT(7);
     }
     LE_TRACE_POINT(2);
     __syncthreads();
@@ -2454,7 +2502,10 @@ __device__ __forceinline__ void moe_dnm_body(const MoeArgs &a) {
         float acc = 0.f;
 #pragma unroll
         for (int w = 0; w < NW; w++) acc += red[w][t][r];
-        a.out[(size_t)t * a.hidden + row0 + r] = acc;
+        if (H == 2)
+            atomicAdd(a.out + (size_t)t * a.hidden + row0 + r, acc);
+        else
+            a.out[(size_t)t * a.hidden + row0 + r] = acc;
     }
     LE_TRACE_POINT(4);
     LE_TRACE_FLUSH;
@@ -2802,6 +2853,7 @@ __device__ __forceinline__ void moe_fus_body(const MoeArgs &a) {
 #define LE_MOE_FUS(TD, PD)                                                                                  \
     extern "C" __global__ void __launch_bounds__(512) le_moe_fus_12_##TD##_p##PD(MoeArgs a) { moe_fus_body<TD, PD>(a); }
 LE_MOE_FUS(14, 1) LE_MOE_FUS(14, 2) LE_MOE_FUS(14, 3) LE_MOE_FUS(12, 1) LE_MOE_FUS(12, 2) LE_MOE_FUS(12, 3)
+
 
 #define LE_MOE_GUM(TD, NW, P)                                                                               \
     extern "C" __global__ void __launch_bounds__(64 * NW) le_moe_gum_12_##TD##_w##NW##_p##P(MoeArgs a) {  \
