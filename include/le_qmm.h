@@ -133,6 +133,22 @@ int le_gemm(le_ctx *ctx, int ty, const void *w, const float *x, int m, float *y,
 int le_stream_read(le_ctx *ctx, const void *buf, size_t bytes, void *sink, le_stream_t stream);
 int le_stream_read_sink_bytes(le_ctx *ctx);
 
+/* ---- grouped matmul (replaces mm_<ty> / mm_impl, src/cuda/kernels.cu:679-719, launched by
+ *      prefill::mm, src/gpu/prefill.rs:44-56, over the host pair grouping of prefill.rs:153-214) ----
+ * For each slot s < nslot and each pair i in off[s] .. off[s+1] - 1:
+ *     y[out_idx[i] * rows + r] = W_s[r,:] . x[in_idx[i] * cols ...]   for r < rows,
+ * with W_s = ptrs[s] (device array of nslot weight pointers, like build_ptrs' tables) or, when
+ * ptrs is NULL, w + s * rows * row_bytes (expert slab s of a 3D tensor). off (nslot + 1 ints),
+ * in_idx and out_idx (npair ints) are device arrays; npair = off[nslot] - off[0] is the caller's
+ * bound on the pairs (the reference's host-side grouping knows it). Runs on the matrix cores for
+ * every type, each slot's weights streamed once per tile of 64 or 128 of its pairs, with the
+ * same activation numerics as le_gemm. Output rows of different pairs must differ. ws: device
+ * workspace of le_mm_grouped_workspace_size(ty, nslot, npair, cols) bytes. */
+size_t le_mm_grouped_workspace_size(int ty, int nslot, int npair, int cols);
+int le_mm_grouped(le_ctx *ctx, int ty, const void *const *ptrs, const void *w, const int *off, const int *in_idx,
+                  const int *out_idx, int nslot, int npair, const float *x, float *y, int rows, int cols, void *ws,
+                  size_t ws_bytes, le_stream_t stream);
+
 /* ---- le_gemm without a workspace argument (no counterpart in the reference) ----
  * For callers that cannot allocate device memory: code under HIP graph capture, tight serving
  * loops, harnesses that forbid hipMalloc. Same result as le_gemm (same kernels), with the
@@ -168,6 +184,14 @@ int le_moe_layer(le_ctx *ctx, int ty_gate, int ty_up, int ty_down, const void *g
                  const void *down, int n_exp, int k, int hidden, int ff, const float *logits, const float *h,
                  int n_tok, float *out, int *idx_out, float *w_out, void *ws, size_t ws_bytes,
                  le_stream_t stream);
+/* le_moe_layer with per-expert weight pointer tables (device arrays of n_exp pointers, one slab
+ * of ff x hidden / hidden x ff rows each) instead of contiguous 3D tensors: the layout of an
+ * expert-cache arena, whose per-expert table the reference turns into per-slot pointers with
+ * build_ptrs (src/cuda/kernels.cu:458-468, src/gpu.rs:587-596). Same semantics and workspace. */
+int le_moe_layer_ptrs(le_ctx *ctx, int ty_gate, int ty_up, int ty_down, const void *const *gate_ptrs,
+                      const void *const *up_ptrs, const void *const *down_ptrs, int n_exp, int k, int hidden, int ff,
+                      const float *logits, const float *h, int n_tok, float *out, int *idx_out, float *w_out,
+                      void *ws, size_t ws_bytes, le_stream_t stream);
 /* Status of the MoE layer calls made with workspace ws (no counterpart in the reference, which
  * has no device-side waits): synchronizes `stream`, returns LE_ERR_TIMEOUT (and clears the status)
  * if a one-launch layer on ws gave up at its barrier since the last check, else LE_OK. Not for use

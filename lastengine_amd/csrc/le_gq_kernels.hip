@@ -60,12 +60,21 @@ struct GqArgs {
     int rows, cols, m;
     int mp;     /* tokens rounded up to the largest token tile (the pre-pass pads with zeros) */
     int ksplit; /* K slices (blockIdx.y), > 1: atomic adds into y, cleared by the pre-pass */
+    /* grouped form (le_mm_grouped): slot s multiplies weight ptrs[s] (or w + s * w_slot_bytes)
+     * with the activation rows in_idx[i] of its pairs i in off[s] .. off[s+1], writing output rows
+     * out_idx[i]; the plan kernel lists (slot, first pair) token tiles of bm pairs in the workspace */
+    const u8 *const *ptrs;
+    unsigned long long w_slot_bytes;
+    const int *off, *in_idx, *out_idx;
+    int nslot, maxt, bm, pad;
 };
 
 /* Workspace layout: A planes (mp * K halves), S records (mp/32 * nsb * SREC bytes), token scales
  * (mp floats). */
 __host__ __device__ inline size_t gq_s_off(int mp, int K) { return (size_t)mp * K * 2; }
 __host__ __device__ inline size_t gq_t_off(int mp, int K, int srec) { return gq_s_off(mp, K) + (size_t)(mp / 32) * (K / 256) * srec; }
+/* grouped form: the tile list after the token scales: int count, pad to 16 B, int slot[maxt], int first[maxt] */
+__host__ __device__ inline size_t gq_l_off(int mp, int K, int srec) { return gq_t_off(mp, K, srec) + (size_t)mp * 4; }
 
 __device__ __forceinline__ le_h2 as_h2(u32 v) { return __builtin_bit_cast(le_h2, v); }
 __device__ __forceinline__ u32 as_u32(le_h2 v) { return __builtin_bit_cast(u32, v); }
@@ -192,16 +201,30 @@ __device__ __forceinline__ void gq_tables(u8 *tab) {
 /* ============================ activation pre-pass ============================ */
 /* One block of 256 threads per (padded) token. SK: 0 no sums, 1 per-32 sums (Q4_K), 2 per-16
  * sums (Q6_K). */
-template <int SK>
+template <int SK, bool GR = false>
 __device__ __forceinline__ void gq_xprep_body(const GqArgs &a, u8 *ws) {
     __shared__ float red[4];
     const int K = a.cols, nsb = K >> 8, t = blockIdx.x, tid = threadIdx.x, lane = tid & 63;
-    if (a.ksplit > 1) { /* the slices add into y */
+    if (!GR && a.ksplit > 1) { /* the slices add into y */
         const size_t ny = (size_t)a.m * a.rows;
         for (size_t i = (size_t)blockIdx.x * blockDim.x + tid; i < ny; i += (size_t)gridDim.x * blockDim.x) a.y[i] = 0.f;
     }
-    const bool live = t < a.m;
-    const LE_GLOBAL float *xr = (const LE_GLOBAL float *)(a.x + (size_t)(live ? t : 0) * K);
+    bool live = t < a.m;
+    size_t src = t;
+    if constexpr (GR) { /* position t = tile * bm + j: pair first[tile] + j of the tile's slot, if any */
+        constexpr int srec_ = SK == 1 ? 1024 : 0;
+        const int *lst = (const int *)(ws + gq_l_off(a.mp, K, srec_));
+        const int tile = t / a.bm, j = t - tile * a.bm;
+        live = false;
+        if (tile < lst[0]) {
+            const int sl = lst[4 + tile], p = lst[4 + a.maxt + tile] + j;
+            if (p < a.off[sl + 1]) {
+                live = true;
+                src = (size_t)a.in_idx[p];
+            }
+        }
+    }
+    const LE_GLOBAL float *xr = (const LE_GLOBAL float *)(a.x + (live ? src : 0) * K);
     float am = 0.f;
     if (live)
         for (int i = tid; i < K / 4; i += 256) {
@@ -263,7 +286,7 @@ __device__ __forceinline__ void gq_xprep_body(const GqArgs &a, u8 *ws) {
 }
 
 /* ============================ main kernel ============================ */
-template <int TY, int WM, int WN, int TM, int TN>
+template <int TY, int WM, int WN, int TM, int TN, bool GR = false>
 __device__ __forceinline__ void gq_body(const GqArgs &a, const u8 *ws) {
     using F = GqF<TY>;
     constexpr int BM = 32 * TM * WM, BN = 32 * TN * WN, NT = 64 * WM * WN;
@@ -276,12 +299,23 @@ __device__ __forceinline__ void gq_body(const GqArgs &a, const u8 *ws) {
     u8 *Sl = lds + 2 * BUF;            /* [2][SBYTES] sum records, by super-block parity */
     u8 *tab = Sl + 2 * SBYTES;          /* IQ tables */
 
-    const int K = a.cols, nsb = K >> 8, M = a.m;
-    const int NTR = (a.rows + BN - 1) / BN, MT = (M + BM - 1) / BM;
+    const int K = a.cols, nsb = K >> 8;
+    const int NTR = (a.rows + BN - 1) / BN, MT = GR ? a.maxt : (a.m + BM - 1) / BM;
     const int id = blockIdx.x, j = id >> 3;
     const int mt = j % MT, nt = (j / MT) * 8 + (id & 7);
     if (nt >= NTR) return; /* uniform over the block */
     const int nb = nt * BN, mb = mt * BM;
+    /* tokens of this tile: M = all tokens (plain), or the tile's pairs (grouped: rows of its slot) */
+    int M = a.m, pair0 = 0;
+    const u8 *Wsrc = a.w;
+    if constexpr (GR) {
+        const int *lst = (const int *)(ws + gq_l_off(a.mp, K, F::SREC));
+        if (mt >= lst[0]) return; /* uniform: past the planned tiles */
+        const int sl = lst[4 + mt];
+        pair0 = lst[4 + a.maxt + mt];
+        M = mb + min(BM, a.off[sl + 1] - pair0); /* token t of the tile is valid while t < M */
+        Wsrc = a.ptrs ? a.ptrs[sl] : a.w + (size_t)sl * a.w_slot_bytes;
+    }
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int wm = wave / WN, wn = wave % WN;
     const size_t rb = (size_t)nsb * F::SBB;
@@ -300,7 +334,7 @@ __device__ __forceinline__ void gq_body(const GqArgs &a, const u8 *ws) {
      * the loads of the step being staged; steps past the slice re-read the last one */
     auto issue = [&](int s_, Set &R) {
         const int s = min(s_, nstep - 1), sb = s >> 1, h = s & 1;
-        const u8 *w0 = a.w + (size_t)sb * F::SBB;
+        const u8 *w0 = Wsrc + (size_t)sb * F::SBB;
 #pragma unroll
         for (int i = 0; i < NWC; i++) {
             const int c = min(tid + NT * i, BN * F::NCH - 1), row = c / F::NCH, k = c - row * F::NCH;
@@ -593,6 +627,17 @@ __device__ __forceinline__ void gq_body(const GqArgs &a, const u8 *ws) {
     for (int i = 0; i < TM; i++)
 #pragma unroll
         for (int e = 0; e < 16; e++) ts[i][e] = tsc[mb + (wm * TM + i) * 32 + 4 * hs + 8 * (e >> 2) + (e & 3)] * post;
+    int orow[TM][16]; /* output row of each of the lane's tokens */
+#pragma unroll
+    for (int i = 0; i < TM; i++)
+#pragma unroll
+        for (int e = 0; e < 16; e++) {
+            const int t = mb + (wm * TM + i) * 32 + 4 * hs + 8 * (e >> 2) + (e & 3);
+            if constexpr (GR)
+                orow[i][e] = t < M ? a.out_idx[pair0 + t - mb] : 0;
+            else
+                orow[i][e] = t;
+        }
 #pragma unroll
     for (int i = 0; i < TM; i++) {
         const int t0 = mb + (wm * TM + i) * 32 + 4 * hs;
@@ -604,10 +649,10 @@ __device__ __forceinline__ void gq_body(const GqArgs &a, const u8 *ws) {
                 const int t = t0 + 8 * (e >> 2) + (e & 3);
                 if (t < M && r < a.rows) {
                     const float v = acc[i][k][e] * ts[i][e];
-                    if (a.ksplit > 1)
+                    if (!GR && a.ksplit > 1)
                         unsafeAtomicAdd(a.y + (size_t)t * a.rows + r, v);
                     else
-                        a.y[(size_t)t * a.rows + r] = v;
+                        a.y[(size_t)orow[i][e] * a.rows + r] = v;
                 }
             }
         }
@@ -615,13 +660,49 @@ __device__ __forceinline__ void gq_body(const GqArgs &a, const u8 *ws) {
 }
 
 #define LE_GQX(TY, SK) \
-    extern "C" __global__ void __launch_bounds__(256) le_gq_xprep_##TY(GqArgs a, u8 *ws) { gq_xprep_body<SK>(a, ws); }
+    extern "C" __global__ void __launch_bounds__(256) le_gq_xprep_##TY(GqArgs a, u8 *ws) { gq_xprep_body<SK>(a, ws); } \
+    extern "C" __global__ void __launch_bounds__(256) le_gq_xprepg_##TY(GqArgs a, u8 *ws) { gq_xprep_body<SK, true>(a, ws); }
 LE_GQX(8, 0) LE_GQX(12, 1) LE_GQX(14, 0) LE_GQX(16, 0) LE_GQX(18, 0)
+
+/* Plan of the grouped form: slot s has off[s+1] - off[s] pairs, split into tiles of bm; the
+ * tiles are listed slot by slot (count, then slot and first pair of each) in the workspace. One
+ * block of 1024 threads; slots are taken 1024 at a time with a running base. */
+extern "C" __global__ void __launch_bounds__(1024) le_gq_plan(GqArgs a, u8 *ws, int srec) {
+    __shared__ int scan[1024];
+    int *lst = (int *)(ws + gq_l_off(a.mp, a.cols, srec));
+    int base = 0;
+    for (int s0 = 0; s0 < a.nslot; s0 += 1024) {
+        const int s = s0 + (int)threadIdx.x;
+        const int n = s < a.nslot ? (max(a.off[s + 1] - a.off[s], 0) + a.bm - 1) / a.bm : 0;
+        scan[threadIdx.x] = n;
+        __syncthreads();
+        for (int o = 1; o < 1024; o <<= 1) { /* inclusive Hillis-Steele scan */
+            const int v = threadIdx.x >= (unsigned)o ? scan[threadIdx.x - o] : 0;
+            __syncthreads();
+            scan[threadIdx.x] += v;
+            __syncthreads();
+        }
+        const int first = base + scan[threadIdx.x] - n;
+        for (int q = 0; q < n; q++) {
+            if (first + q < a.maxt) {
+                lst[4 + first + q] = s;
+                lst[4 + a.maxt + first + q] = a.off[s] + q * a.bm;
+            }
+        }
+        base += scan[1023];
+        __syncthreads();
+    }
+    if (threadIdx.x == 0) lst[0] = min(base, a.maxt);
+}
 
 #define LE_GQ_(TY, WM, WN, TM, TN)                                                                                     \
     extern "C" __global__ void __launch_bounds__(WM * WN * 64) le_gq_##TY##_w##WM##WN##_t##TM##TN(GqArgs a, const u8 *ws) { \
         gq_body<TY, WM, WN, TM, TN>(a, ws);                                                                            \
     }
+#define LE_GQG_(TY, WM, WN, TM, TN)                                                                                     \
+    extern "C" __global__ void __launch_bounds__(WM * WN * 64) le_gqg_##TY##_w##WM##WN##_t##TM##TN(GqArgs a, const u8 *ws) { \
+        gq_body<TY, WM, WN, TM, TN, true>(a, ws);                                                                        \
+    }
 #define LE_GQ(TY) LE_GQ_(TY, 1, 4, 1, 2) LE_GQ_(TY, 1, 4, 2, 2) LE_GQ_(TY, 1, 4, 4, 2) LE_GQ_(TY, 2, 2, 2, 2) \
-    LE_GQ_(TY, 1, 8, 2, 1) LE_GQ_(TY, 1, 8, 4, 1)
+    LE_GQ_(TY, 1, 8, 2, 1) LE_GQ_(TY, 1, 8, 4, 1) LE_GQG_(TY, 1, 8, 2, 1) LE_GQG_(TY, 1, 8, 4, 1) LE_GQG_(TY, 2, 2, 2, 2)
 LE_GQ(8) LE_GQ(12) LE_GQ(14) LE_GQ(16) LE_GQ(18)

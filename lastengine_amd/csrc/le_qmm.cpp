@@ -51,6 +51,7 @@ struct MoeArgs {
     unsigned int spin_limit;
     unsigned long long epoch;
     void *bar;
+    const void *const *gptr, *const *uptr, *const *dptr;
 };
 /* Barrier area at the start of an MoE workspace (status word, generation word, one 8-byte arrival
  * flag per block of the one-launch kernel, LE_MOE_MAXGRID = 1024 blocks). */
@@ -588,11 +589,14 @@ int le_moe_check(le_ctx *c, const void *ws, le_stream_t stream) {
                                    "(its outputs are NaN): the grid was not resident at once");
 }
 
-int le_moe_layer(le_ctx *c, int ty_gate, int ty_up, int ty_down, const void *gate, const void *up, const void *down,
-                 int n_exp, int k, int hidden, int ff, const float *logits, const float *h, int n_tok, float *out,
-                 int *idx_out, float *w_out, void *ws, size_t ws_bytes, le_stream_t stream) {
-    if (!c) return LE_ERR_ARG;
-    if (!gate || !up || !down || !logits || !h || !out || !ws) return c->fail(LE_ERR_ARG, "null pointer");
+/* The MoE layer over expert slabs (gate/up/down) or per-expert pointer tables (gptr/uptr/dptr). */
+static int moe_layer_impl(le_ctx *c, int ty_gate, int ty_up, int ty_down, const void *gate, const void *up, const void *down,
+                          const void *const *gptr, const void *const *uptr, const void *const *dptr, int n_exp, int k,
+                          int hidden, int ff, const float *logits, const float *h, int n_tok, float *out, int *idx_out,
+                          float *w_out, void *ws, size_t ws_bytes, hipStream_t stream) {
+    const bool tables = gptr || uptr || dptr;
+    if (tables ? !(gptr && uptr && dptr) : !(gate && up && down)) return c->fail(LE_ERR_ARG, "null weight pointer or table");
+    if (!logits || !h || !out || !ws) return c->fail(LE_ERR_ARG, "null pointer");
     if (ty_gate != ty_up) return c->fail(LE_ERR_TYPE, "gate and up must share a type");
     if (!supported(ty_gate) || !supported(ty_down)) return c->fail(LE_ERR_TYPE, "no kernel for types %d/%d", ty_gate, ty_down);
     static const int combos[][2] = {{12, 14}, {12, 12}, {14, 14}, {8, 8}, {16, 18}, {16, 16}, {18, 18}};
@@ -607,7 +611,7 @@ int le_moe_layer(le_ctx *c, int ty_gate, int ty_up, int ty_down, const void *gat
     const size_t lds = (size_t)8 * xtok_bytes(hidden);
     if (lds + 16384 > c->lds_limit) return c->fail(LE_ERR_SHAPE, "hidden=%d exceeds the LDS budget", hidden);
     MoeArgs a{gate, up, down, logits, h, out, (char *)ws + kMoeBarBytes, idx_out, w_out, n_tok, n_exp, k, hidden, ff,
-              c->moe_spin_limit, ++g_moe_epoch, ws};
+              c->moe_spin_limit, ++g_moe_epoch, ws, gptr, uptr, dptr};
     void *args[] = {&a};
     char name[64];
     const int nsb = hidden / 256, g8 = nsb % 8 == 0;
@@ -660,6 +664,24 @@ int le_moe_layer(le_ctx *c, int ty_gate, int ty_up, int ty_down, const void *gat
     if (rc) return rc;
     snprintf(name, sizeof name, fast_dn ? "le_moe_downf_%d" : "le_moe_down_%d", ty_down);
     return c->launch(name, dim3((unsigned)(hidden / 8)), fast_dn ? 512 : 256, fast_dn ? 49152 : 0, (hipStream_t)stream, args);
+}
+
+int le_moe_layer(le_ctx *c, int ty_gate, int ty_up, int ty_down, const void *gate, const void *up, const void *down,
+                 int n_exp, int k, int hidden, int ff, const float *logits, const float *h, int n_tok, float *out,
+                 int *idx_out, float *w_out, void *ws, size_t ws_bytes, le_stream_t stream) {
+    if (!c) return LE_ERR_ARG;
+    return moe_layer_impl(c, ty_gate, ty_up, ty_down, gate, up, down, nullptr, nullptr, nullptr, n_exp, k, hidden, ff,
+                          logits, h, n_tok, out, idx_out, w_out, ws, ws_bytes, (hipStream_t)stream);
+}
+
+int le_moe_layer_ptrs(le_ctx *c, int ty_gate, int ty_up, int ty_down, const void *const *gate_ptrs,
+                      const void *const *up_ptrs, const void *const *down_ptrs, int n_exp, int k, int hidden, int ff,
+                      const float *logits, const float *h, int n_tok, float *out, int *idx_out, float *w_out, void *ws,
+                      size_t ws_bytes, le_stream_t stream) {
+    if (!c) return LE_ERR_ARG;
+    if (!gate_ptrs || !up_ptrs || !down_ptrs) return c->fail(LE_ERR_ARG, "null pointer table");
+    return moe_layer_impl(c, ty_gate, ty_up, ty_down, nullptr, nullptr, nullptr, gate_ptrs, up_ptrs, down_ptrs, n_exp, k,
+                          hidden, ff, logits, h, n_tok, out, idx_out, w_out, ws, ws_bytes, (hipStream_t)stream);
 }
 
 /* Q4_K with 3..8 (or 16) tokens: the staged f16 MFMA kernel, T = 4, 8 or 16 tokens per weight
@@ -757,13 +779,80 @@ static int gq_launch(le_ctx *c, int ty, const void *w, const float *x, int m, fl
         const float *x;
         float *y;
         int rows, cols, m, mp, ksplit;
-    } a{w, x, y, rows, cols, m, mp, ks};
+        const void *const *ptrs;
+        unsigned long long w_slot_bytes;
+        const int *off, *in_idx, *out_idx;
+        int nslot, maxt, bm, pad;
+    } a{w, x, y, rows, cols, m, mp, ks, nullptr, 0, nullptr, nullptr, nullptr, 0, 0, 0, 0};
     void *args[] = {&a, &ws};
     char pname[32];
     snprintf(pname, sizeof pname, "le_gq_xprep_%d", ty);
     int rc = c->launch(pname, dim3((unsigned)mp), 256, 0, st, args);
     if (rc) return rc;
     return c->launch(name, dim3((unsigned)grid, (unsigned)ks), nthr, lds, st, args);
+}
+
+/* Grouped form (le_mm_grouped): token tiles of bm pairs (64 or 128, from the pairs per slot),
+ * at most nslot + npair / bm of them. */
+static int mmg_cfg(int nslot, int npair) { return (long long)npair <= 64LL * nslot ? 4 : 5; }
+static int mmg_bm(int nslot, int npair) { return mmg_cfg(nslot, npair) == 4 ? 64 : 128; }
+static int mmg_maxt(int nslot, int npair) { const int bm = mmg_bm(nslot, npair); return nslot + (npair + bm - 1) / bm; }
+
+size_t le_mm_grouped_workspace_size(int ty, int nslot, int npair, int cols) {
+    if (!supported(ty) || nslot <= 0 || npair < 0 || cols <= 0 || cols % 256) return 0;
+    const size_t maxt = (size_t)mmg_maxt(nslot, npair), mp = maxt * mmg_bm(nslot, npair);
+    return mp * cols * 2 + mp / 32 * (cols / 256) * gq_srec(ty) + mp * 4 + 16 + 8 * maxt;
+}
+
+int le_mm_grouped(le_ctx *c, int ty, const void *const *ptrs, const void *w, const int *off, const int *in_idx,
+                  const int *out_idx, int nslot, int npair, const float *x, float *y, int rows, int cols, void *ws,
+                  size_t ws_bytes, le_stream_t stream) {
+    if (!c) return LE_ERR_ARG;
+    if (!supported(ty)) return c->fail(LE_ERR_TYPE, "no kernel for type %d", ty);
+    if ((!ptrs && !w) || !off || !in_idx || !out_idx || !x || !y || !ws) return c->fail(LE_ERR_ARG, "null pointer");
+    if (nslot <= 0 || npair < 0 || rows <= 0 || cols <= 0) return c->fail(LE_ERR_SHAPE, "empty shape");
+    if (cols % 256) return c->fail(LE_ERR_SHAPE, "cols=%d is not a multiple of 256", cols);
+    if (!al16(x) || !al16(ws)) return c->fail(LE_ERR_ALIGN, "x and ws must be 16-byte aligned");
+    const size_t need = le_mm_grouped_workspace_size(ty, nslot, npair, cols);
+    if (ws_bytes < need) return c->fail(LE_ERR_WORKSPACE, "workspace needs %zu bytes", need);
+    if (npair == 0) return LE_OK;
+    static const int cfgs[6][4] = {{1, 4, 1, 2}, {1, 4, 2, 2}, {1, 4, 4, 2}, {2, 2, 2, 2}, {1, 8, 2, 1}, {1, 8, 4, 1}};
+    int ci = mmg_cfg(nslot, npair);
+    const int srec = gq_srec(ty), nsb = cols / 256;
+    auto lds_of = [&](int i) {
+        const int BM = 32 * cfgs[i][0] * cfgs[i][2], BN = 32 * cfgs[i][1] * cfgs[i][3];
+        return (size_t)2 * (BN * gq_slot(ty) + BM * 256) + (size_t)2 * (BM / 32) * srec + gq_tab(ty);
+    };
+    if (lds_of(ci) > c->lds_limit) ci = 3; /* 128 x 128 on 4 waves */
+    const int WM = cfgs[ci][0], WN = cfgs[ci][1], TM = cfgs[ci][2], TN = cfgs[ci][3];
+    const int BM = 32 * TM * WM, BN = 32 * TN * WN, nthr = 64 * WM * WN;
+    if (BM != mmg_bm(nslot, npair) && !(ci == 3 && mmg_bm(nslot, npair) == 128))
+        return c->fail(LE_ERR_SHAPE, "grouped GEMM tile does not fit the LDS");
+    const int maxt = mmg_maxt(nslot, npair), mp = maxt * BM;
+    const long long ntr = (rows + BN - 1) / BN, grid = (ntr + 7) / 8 * 8 * (long long)maxt;
+    if (grid > 0x7FFFFFFFLL || (long long)mp * cols > (1LL << 40)) return c->fail(LE_ERR_SHAPE, "grouped GEMM too large");
+    struct {
+        const void *w;
+        const float *x;
+        float *y;
+        int rows, cols, m, mp, ksplit;
+        const void *const *ptrs;
+        unsigned long long w_slot_bytes;
+        const int *off, *in_idx, *out_idx;
+        int nslot, maxt, bm, pad;
+    } a{w, x, y, rows, cols, mp, mp, 1, ptrs, (unsigned long long)rows * le_row_bytes(ty, cols), off, in_idx, out_idx,
+        nslot, maxt, BM, 0};
+    int srec_arg = srec;
+    void *pargs[] = {&a, &ws, &srec_arg};
+    int rc = c->launch("le_gq_plan", dim3(1), 1024, 0, (hipStream_t)stream, pargs);
+    if (rc) return rc;
+    void *args[] = {&a, &ws};
+    char name[48];
+    snprintf(name, sizeof name, "le_gq_xprepg_%d", ty);
+    rc = c->launch(name, dim3((unsigned)mp), 256, 0, (hipStream_t)stream, args);
+    if (rc) return rc;
+    snprintf(name, sizeof name, "le_gqg_%d_w%d%d_t%d%d", ty, WM, WN, TM, TN);
+    return c->launch(name, dim3((unsigned)grid), nthr, lds_of(ci), (hipStream_t)stream, args);
 }
 
 size_t le_gemm_workspace_size(int ty, int m, int cols) {

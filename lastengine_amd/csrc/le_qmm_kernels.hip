@@ -1389,7 +1389,14 @@ struct MoeArgs {
     unsigned int spin_limit;  /* bounded waits of the one-launch barrier; 0 makes it fail */
     unsigned long long epoch; /* unique per launch (process-wide counter on the host) */
     u8 *bar;                  /* the caller's workspace start: barrier area (LE_MOE_BAR_BYTES) */
+    /* per-expert weight pointers (an expert-cache arena), or null: expert e's slab at
+     * e * rows * row_bytes of gate / up / down */
+    const u8 *const *gptr, *const *uptr, *const *dptr;
 };
+/* Expert e's weights: its pointer-table entry, or its slab in the 3D tensor. */
+__device__ __forceinline__ const u8 *moe_w(const u8 *slab, const u8 *const *ptrs, int e, size_t expert_bytes) {
+    return ptrs ? ptrs[e] : slab + (size_t)e * expert_bytes;
+}
 /* Barrier area at the start of the workspace: a status word (sticky, nonzero after a wait gave
  * up; read and cleared by le_moe_check), the generation word, then one arrival flag per block. */
 #define LE_MOE_BAR_STATUS 0
@@ -1805,7 +1812,7 @@ __device__ void moe_gu_body(const MoeArgs &a) {
     }
     const int K = a.hidden, nsb = K >> 8, ng = K >> 3;
     const size_t rbg = (size_t)nsb * F::SB;
-    const u8 *Wg = a.gate + (size_t)e * a.ff * rbg, *Wu = a.up + (size_t)e * a.ff * rbg;
+    const u8 *Wg = moe_w(a.gate, a.gptr, e, (size_t)a.ff * rbg), *Wu = moe_w(a.up, a.uptr, e, (size_t)a.ff * rbg);
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     constexpr int RPW = 8 / G;
     const int li = lane & 7, g = (lane >> 3) % G, rsub = lane / (8 * G);
@@ -1902,7 +1909,7 @@ __device__ void moe_down_body(const MoeArgs &a) {
     for (int z = wave; z < R.U; z += 4) {
         const int e = R.grp_e[z];
         const int nmem = __popcll(R.mask[e]);
-        const u8 *Wd = a.down + (size_t)e * a.hidden * rbd + (size_t)row * rbd;
+        const u8 *Wd = moe_w(a.down, a.dptr, e, (size_t)a.hidden * rbd) + (size_t)row * rbd;
         for (int m0 = 0; m0 < nmem; m0 += 8) {
             const int nt = min(8, nmem - m0);
             XTok xt[8];
@@ -1998,7 +2005,7 @@ __device__ void moe_gu_fast(const MoeArgs &a) {
     }
     /* 2. weight loads of this wave's rows: wave-step ws = wave + NW*j covers rows ws*RPW .. */
     const size_t rbg = (size_t)nsb * F::SB;
-    const u8 *Wg = a.gate + (size_t)e * a.ff * rbg, *Wu = a.up + (size_t)e * a.ff * rbg;
+    const u8 *Wg = moe_w(a.gate, a.gptr, e, (size_t)a.ff * rbg), *Wu = moe_w(a.up, a.uptr, e, (size_t)a.ff * rbg);
     const int li = lane & 7, g = (lane >> 3) % G, rsub = lane / (8 * G);
     const int S = nsb / G; /* <= 2 on this path */
     const int ux = blockIdx.x;
@@ -2151,7 +2158,7 @@ __device__ void moe_down_fast(const MoeArgs &a) {
     const int li = lane & 7, rr = lane >> 3, row = 8 * blockIdx.x + rr;
     Raw ra[SM], rb2[SM];
     auto issue = [&](int z, Raw (&r)[SM]) {
-        const u8 *Wd = a.down + (size_t)R.grp_e[z] * a.hidden * rbd + (size_t)row * rbd;
+        const u8 *Wd = moe_w(a.down, a.dptr, R.grp_e[z], (size_t)a.hidden * rbd) + (size_t)row * rbd;
 #pragma unroll
         for (int s = 0; s < SM; s++) r[s] = F::load(Wd + (size_t)min(s, nsb - 1) * F::SB, li);
     };
@@ -2288,7 +2295,7 @@ __device__ __forceinline__ void moe_gum_body(const MoeArgs &a) {
     /* 2. the four tiles of this wave's super-blocks (gate rows 32ux.., +16, up rows 32ux.., +16),
      * packed: chunk c = (tile, row, column) of 4 x 16 x CPR, all in flight at once */
     const size_t rb = (size_t)NSB * 144;
-    const u8 *Wg = a.gate + (size_t)e * a.ff * rb, *Wu = a.up + (size_t)e * a.ff * rb;
+    const u8 *Wg = moe_w(a.gate, a.gptr, e, (size_t)a.ff * rb), *Wu = moe_w(a.up, a.uptr, e, (size_t)a.ff * rb);
     const int ux = blockIdx.x;
     uint4 Rg[NI];
 #pragma unroll
@@ -2426,7 +2433,7 @@ __device__ __forceinline__ void moe_dnm_body(const MoeArgs &a) {
     /* weights of two groups in flight: R0 is the next group to compute, R1 the one after */
     uint4 R0[NI], R1[NI];
     auto issue = [&](int zz, uint4 (&r)[NI]) {
-        const u8 *W = a.down + (size_t)R.grp_e[zz] * a.hidden * rb;
+        const u8 *W = moe_w(a.down, a.dptr, R.grp_e[zz], (size_t)a.hidden * rb);
 #pragma unroll
         for (int i = 0; i < NI; i++) r[i] = TD == LE_TYPE_Q6_K ? ldg16u(W + roff[i]) : ldg16(W + roff[i]);
     };
@@ -2641,7 +2648,7 @@ __device__ __forceinline__ void moe_fus_body(const MoeArgs &a) {
     }
     uint4 R0[DNI];
     auto dissue = [&](int zz, uint4 (&r)[DNI]) {
-        const u8 *W = a.down + (size_t)R.grp_e[zz] * a.hidden * drb;
+        const u8 *W = moe_w(a.down, a.dptr, R.grp_e[zz], (size_t)a.hidden * drb);
 #pragma unroll
         for (int i = 0; i < DNI; i++) r[i] = TD == LE_TYPE_Q6_K ? ldg16u(W + roff[i]) : ldg16(W + roff[i]);
     };
@@ -2670,7 +2677,7 @@ __device__ __forceinline__ void moe_fus_body(const MoeArgs &a) {
     auto gissue = [&](int it) {
         it = min(it, ngu - 1);
         const int ux = it % (a.ff >> 5), e = R.grp_e[it / (a.ff >> 5)];
-        const u8 *Wg = a.gate + (size_t)e * a.ff * rb, *Wu = a.up + (size_t)e * a.ff * rb;
+        const u8 *Wg = moe_w(a.gate, a.gptr, e, (size_t)a.ff * rb), *Wu = moe_w(a.up, a.uptr, e, (size_t)a.ff * rb);
 #pragma unroll
         for (int i = 0; i < NI; i++) {
             const int c = min(64 * i + lane, NCH - 1), ti = c / (16 * CPR), rem = c % (16 * CPR), col = rem % CPR;

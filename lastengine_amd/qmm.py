@@ -68,6 +68,9 @@ def lib():
         "le_moe_workspace_size": (S, [I, I, I]),
         "le_moe_layer": (I, [P, I, I, I, P, P, P, I, I, I, I, P, P, I, P, P, P, P, S, P]),
         "le_moe_check": (I, [P, P, P]),
+        "le_moe_layer_ptrs": (I, [P, I, I, I, P, P, P, I, I, I, I, P, P, I, P, P, P, P, S, P]),
+        "le_mm_grouped_workspace_size": (S, [I, I, I, I]),
+        "le_mm_grouped": (I, [P, I, P, P, P, P, P, I, I, P, P, I, I, P, S, P]),
         "le_fill_normal": (None, [P, S, ctypes.c_uint64, ctypes.c_uint64, D, D, I]),
         "le_quantize_rows": (I, [I, P, P, S, S, I]),
         "le_f32_to_f16": (ctypes.c_uint16, [F]),
@@ -193,6 +196,35 @@ class Engine:
         self._check(self._L.le_moe_layer(self._ctx, ty_gate, ty_up, ty_down, _ptr(gate), _ptr(up), _ptr(down), n_exp,
                                          k, hidden, ff, _ptr(logits), _ptr(h), n_tok, _ptr(out), _ptr(idx_out),
                                          _ptr(w_out), _ptr(ws), ws_bytes, _stream(stream)))
+
+    def moe_ptrs(self, ty_gate, ty_up, ty_down, gate_ptrs, up_ptrs, down_ptrs, n_exp, k, hidden, ff, logits, h, n_tok,
+                 out, idx_out=None, w_out=None, ws=None, ws_bytes=None, stream=None):
+        """The MoE layer over per-expert pointer tables (device arrays of n_exp weight pointers)."""
+        if ws is None:
+            import torch
+            ws = torch.zeros(max(16, self.moe_workspace_size(n_tok, k, ff)), dtype=torch.uint8, device="cuda")
+        if ws_bytes is None:
+            ws_bytes = ws.numel() if hasattr(ws, "numel") else 0
+        self._check(self._L.le_moe_layer_ptrs(self._ctx, ty_gate, ty_up, ty_down, _ptr(gate_ptrs), _ptr(up_ptrs),
+                                              _ptr(down_ptrs), n_exp, k, hidden, ff, _ptr(logits), _ptr(h), n_tok,
+                                              _ptr(out), _ptr(idx_out), _ptr(w_out), _ptr(ws), ws_bytes, _stream(stream)))
+
+    def mm_grouped_workspace_size(self, ty, nslot, npair, cols):
+        return int(self._L.le_mm_grouped_workspace_size(ty, nslot, npair, cols))
+
+    def mm_grouped(self, ty, off, in_idx, out_idx, nslot, npair, x, y, rows, cols, ptrs=None, w=None, ws=None,
+                   ws_bytes=None, stream=None):
+        """prefill::mm / mm_impl (src/cuda/kernels.cu:679-719): y[out_idx[i]] = W_s . x[in_idx[i]] for the
+        pairs i of slot s (off[s] .. off[s+1])."""
+        if ws is None:
+            import torch
+            ws = torch.empty(max(16, self.mm_grouped_workspace_size(ty, nslot, npair, cols)), dtype=torch.uint8,
+                             device="cuda")
+        if ws_bytes is None:
+            ws_bytes = ws.numel() if hasattr(ws, "numel") else 0
+        self._check(self._L.le_mm_grouped(self._ctx, ty, _ptr(ptrs), _ptr(w), _ptr(off), _ptr(in_idx), _ptr(out_idx),
+                                          nslot, npair, _ptr(x), _ptr(y), rows, cols, _ptr(ws), ws_bytes,
+                                          _stream(stream)))
 
     def moe_check(self, ws, stream=None):
         """Raise LeError(-8) if a one-launch MoE layer on workspace ws gave up at its device-wide
