@@ -171,7 +171,13 @@ int le_gemm_noalloc(le_ctx *ctx, int ty, const void *w, const float *x, int m, f
  * (ty_down), slab e at e * rows * row_bytes. Routing and grouping by expert run on the device
  * (no host synchronisation); each routed expert's weights are read once per call. idx_out/w_out
  * (n_tok*k, optional) receive the selection. ws: device workspace of le_moe_workspace_size bytes.
- * Limits: n_tok <= 64, k <= 16, n_exp <= 256, hidden and ff multiples of 256.
+ * Limits: n_tok <= 65536, k <= 16, n_exp <= 256, hidden and ff multiples of 256.
+ * Prefill-sized calls (more than 64 tokens; from 17 tokens when ws holds
+ * le_moe_prefill_workspace_size bytes) route every token, group the (token, expert) pairs by
+ * expert on the device (token order within an expert) and run the three projections as grouped
+ * matrix-core matmuls (le_mm_grouped), so each expert's weights are streamed once per tile of up
+ * to 128 of its pairs; ws must then hold le_moe_prefill_workspace_size bytes. Decode-sized calls
+ * need le_moe_workspace_size bytes.
  * For 3..8 tokens at hidden 2048 the layer runs as one launch with a device-wide barrier between
  * gate/up and down. That launch sizes its grid to the blocks that fit on the device at once and
  * assumes nothing else occupies it: a concurrent kernel on another stream can make its bounded
@@ -180,6 +186,7 @@ int le_gemm_noalloc(le_ctx *ctx, int ty, const void *w, const float *x, int m, f
  * with different workspaces are independent; calls that share a workspace must not overlap.
  * Zero-fill ws once when it is allocated (it is then fully rewritten by every call). */
 size_t le_moe_workspace_size(int n_tok, int k, int ff);
+size_t le_moe_prefill_workspace_size(int n_tok, int k, int n_exp, int hidden, int ff);
 int le_moe_layer(le_ctx *ctx, int ty_gate, int ty_up, int ty_down, const void *gate, const void *up,
                  const void *down, int n_exp, int k, int hidden, int ff, const float *logits, const float *h,
                  int n_tok, float *out, int *idx_out, float *w_out, void *ws, size_t ws_bytes,

@@ -126,7 +126,11 @@ extern "C" __global__ void __launch_bounds__(256) le_gm_xprep(GmArgs a, u8 *ws) 
     _Float16 *Xh = (_Float16 *)ws, *Xl = Xh + (size_t)a.m * K;
     *(LE_GLOBAL uint2 *)(Xh + e) = make_uint2(h0, h1);
     if (a.split) *(LE_GLOBAL uint2 *)(Xl + e) = make_uint2(l0, l1);
-    const float sum = group_sum<8>((v.x + v.y) + (v.z + v.w));
+    /* without the low plane the MFMA sees only the high halves: sum those, so the mins term
+     * cancels their rounding in the scale term */
+    const le_h2 a0 = __builtin_bit_cast(le_h2, h0), a1 = __builtin_bit_cast(le_h2, h1);
+    const float sum = group_sum<8>(a.split ? (v.x + v.y) + (v.z + v.w)
+                                           : ((float)a0.x + (float)a1.x) + ((float)a0.y + (float)a1.y));
     const int si = __builtin_bit_cast(int, sum);
     /* the lane reads run on the whole wave, outside the single-lane store below (a reduction
      * moved under that branch would see inactive lanes) */
@@ -524,7 +528,10 @@ __device__ __forceinline__ void mh_q4k_body(const MhArgs &a) {
                 const le_h2 h0 = {(_Float16)p.x, (_Float16)p.z}, h1 = {(_Float16)p.y, (_Float16)p.w};
                 const le_h2 h2 = {(_Float16)q.x, (_Float16)q.z}, h3 = {(_Float16)q.y, (_Float16)q.w};
                 img[((l * 8 + (col >> 2)) * T + t) * 4 + (col & 3)] = make_uint4(as_u32(h0), as_u32(h1), as_u32(h2), as_u32(h3));
-                float sm = ((p.x + p.y) + (p.z + p.w)) + ((q.x + q.y) + (q.z + q.w));
+                /* sums of the fp16-rounded values, so the mins term cancels the rounding the
+                 * scale term sees (the error then scales with sum |w x|) */
+                float sm = (((float)h0.x + (float)h1.x) + ((float)h0.y + (float)h1.y)) +
+                           (((float)h2.x + (float)h3.x) + ((float)h2.y + (float)h3.y));
                 sm += __shfl_xor(sm, 1);
                 sm += __shfl_xor(sm, 2);
                 if ((col & 3) == 0) {

@@ -259,7 +259,13 @@ __device__ __forceinline__ void gq_xprep_body(const GqArgs &a, u8 *ws) {
         *(LE_GLOBAL uint4 *)(A + off) = make_uint4(as_u32(h0), as_u32(h1), as_u32(h2), as_u32(h3));
         if constexpr (SK != 0) {
             /* g runs over consecutive lanes, so the groups of one sum are neighbouring lanes */
-            float s = ((v[0] + v[1]) + (v[2] + v[3])) + ((v[4] + v[5]) + (v[6] + v[7]));
+            /* sums of the fp16-rounded values the MFMA sees, so that the mins term cancels the
+             * scale term's share of the rounding exactly: the result is then sum w * x~ with
+             * error relative to sum |w x|, not to sum |sc q x| */
+            float r[8];
+#pragma unroll
+            for (int i = 0; i < 8; i++) r[i] = (float)(_Float16)v[i];
+            float s = ((r[0] + r[1]) + (r[2] + r[3])) + ((r[4] + r[5]) + (r[6] + r[7]));
             s += __shfl_xor(s, 1);
             if constexpr (SK == 1) s += __shfl_xor(s, 2);
             const int span = SK == 1 ? 4 : 2;

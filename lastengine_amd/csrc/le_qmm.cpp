@@ -56,6 +56,7 @@ struct MoeArgs {
 /* Barrier area at the start of an MoE workspace (status word, generation word, one 8-byte arrival
  * flag per block of the one-launch kernel, LE_MOE_MAXGRID = 1024 blocks). */
 constexpr size_t kMoeBarBytes = 128 + 8 * 1024;
+#define LE_MOE_MAX_TOK 65536
 /* Epochs of the one-launch MoE barrier: unique per launch within the process. */
 std::atomic<unsigned long long> g_moe_epoch{0};
 int table_bytes(int ty) {
@@ -93,6 +94,8 @@ struct le_ctx {
     int moe_fused = 1;       /* ... in one launch with a device-wide barrier where the grid fits */
     int moe_fused_min_tok = 3; /* ... from this many tokens on (below, two launches are faster) */
     unsigned int moe_spin_limit = 1u << 20; /* polls before a barrier wait gives up (about a second); 0 fails it */
+    int moe_prefill = 1;        /* grouped matrix-core form for larger token counts (forced above 64) */
+    int moe_prefill_min_tok = 17; /* ... from this many tokens, when the workspace is sized for it */
     int moe_dn_split = 0;    /* down launch blocks per row tile: 0 auto, 1, 2 */
     std::map<std::string, int> occ; /* resident blocks per CU, by kernel name and LDS bytes */
     int gm_min_m = 5;        /* le_gemm uses the MFMA GEMM from this many tokens on (below: the
@@ -499,6 +502,11 @@ int le_set_option(le_ctx *c, const char *name, int value) {
     } else if (n == "moe_spin_limit") {
         if (value < 0) return c->fail(LE_ERR_ARG, "moe_spin_limit must be >= 0");
         c->moe_spin_limit = (unsigned int)value;
+    } else if (n == "moe_prefill") {
+        c->moe_prefill = value ? 1 : 0;
+    } else if (n == "moe_prefill_min_tok") {
+        if (value < 1) return c->fail(LE_ERR_ARG, "moe_prefill_min_tok must be >= 1");
+        c->moe_prefill_min_tok = value;
     } else if (n == "moe_dn_split") {
         if (value < 0 || value > 2) return c->fail(LE_ERR_ARG, "moe_dn_split must be 0, 1 or 2");
         c->moe_dn_split = value;
@@ -589,6 +597,79 @@ int le_moe_check(le_ctx *c, const void *ws, le_stream_t stream) {
                                    "(its outputs are NaN): the grid was not resident at once");
 }
 
+/* Prefill form of the MoE layer (routing, grouping by expert, grouped matmuls): workspace layout. */
+struct MoePreLayout {
+    size_t topi, topw, off, in_idx, out_idx, g, u, d, gemm, total;
+};
+static MoePreLayout moe_pre_layout(int n_tok, int k, int n_exp, int hidden, int ff) {
+    auto al = [](size_t x) { return (x + 255) / 256 * 256; };
+    const size_t np = (size_t)n_tok * k;
+    MoePreLayout L{};
+    size_t o = 0;
+    L.topi = o; o += al(np * 4);
+    L.topw = o; o += al(np * 4);
+    L.off = o; o += al(((size_t)n_exp + 1) * 4);
+    L.in_idx = o; o += al(np * 4);
+    L.out_idx = o; o += al(np * 4);
+    L.g = o; o += al(np * ff * 4);
+    L.u = o; o += al(np * ff * 4);
+    L.d = o; o += al(np * hidden * 4);
+    L.gemm = o;
+    /* the grouped matmuls' workspace for the larger of the two K (Q4_K's, which has sum records) */
+    const size_t g1 = le_mm_grouped_workspace_size(LE_TYPE_Q4_K, n_exp, (int)np, hidden);
+    const size_t g2 = le_mm_grouped_workspace_size(LE_TYPE_Q4_K, n_exp, (int)np, ff);
+    o += al(g1 > g2 ? g1 : g2);
+    L.total = o;
+    return L;
+}
+
+/* Kernel argument block of the prefill routing / grouping kernels (mirrors MoePre). */
+struct MoePreArgs {
+    const float *logits;
+    int *topi;
+    float *topw;
+    int *off, *in_idx, *out_idx, *idx_out;
+    float *w_out;
+    int n_tok, n_exp, k, pad;
+};
+
+static int moe_prefill(le_ctx *c, int ty_gate, int ty_down, const void *gate, const void *up, const void *down,
+                       const void *const *gptr, const void *const *uptr, const void *const *dptr, int n_exp, int k,
+                       int hidden, int ff, const float *logits, const float *h, int n_tok, float *out, int *idx_out,
+                       float *w_out, void *ws, hipStream_t st) {
+    const MoePreLayout L = moe_pre_layout(n_tok, k, n_exp, hidden, ff);
+    char *b = (char *)ws;
+    const int np = n_tok * k;
+    int *topi = (int *)(b + L.topi), *off = (int *)(b + L.off), *in_idx = (int *)(b + L.in_idx), *out_idx = (int *)(b + L.out_idx);
+    float *topw = (float *)(b + L.topw), *G = (float *)(b + L.g), *U = (float *)(b + L.u), *D = (float *)(b + L.d);
+    void *gws = b + L.gemm;
+    const size_t gws_bytes = L.total - L.gemm;
+    MoePreArgs a{logits, topi, topw, off, in_idx, out_idx, idx_out, w_out, n_tok, n_exp, k, 0};
+    void *args[] = {&a};
+    int rc = c->launch("le_moe_route_tok", dim3((unsigned)((n_tok + 7) / 8)), 512, 0, st, args);
+    if (!rc) rc = c->launch("le_moe_group", dim3((unsigned)n_exp), 256, 0, st, args);
+    if (!rc) rc = le_mm_grouped(c, ty_gate, gptr, gate, off, in_idx, out_idx, n_exp, np, h, G, ff, hidden, gws, gws_bytes, st);
+    if (!rc) rc = le_mm_grouped(c, ty_gate, uptr, up, off, in_idx, out_idx, n_exp, np, h, U, ff, hidden, gws, gws_bytes, st);
+    if (rc) return rc;
+    long long n = (long long)np * ff;
+    unsigned blocks = (unsigned)((n + 255) / 256 < 8192 ? (n + 255) / 256 : 8192);
+    void *sargs[] = {&G, &U, &n};
+    rc = c->launch("le_moe_swiglu", dim3(blocks), 256, 0, st, sargs);
+    /* down: the activation rows are the pairs themselves, in the same grouped order */
+    if (!rc) rc = le_mm_grouped(c, ty_down, dptr, down, off, out_idx, out_idx, n_exp, np, G, D, hidden, ff, gws, gws_bytes, st);
+    if (rc) return rc;
+    long long no = (long long)n_tok * hidden;
+    blocks = (unsigned)((no + 255) / 256 < 8192 ? (no + 255) / 256 : 8192);
+    const float *Dc = D, *Wc = topw;
+    void *cargs[] = {&Dc, &Wc, &out, &n_tok, &k, &hidden};
+    return c->launch("le_moe_combine", dim3(blocks), 256, 0, st, cargs);
+}
+
+size_t le_moe_prefill_workspace_size(int n_tok, int k, int n_exp, int hidden, int ff) {
+    if (n_tok <= 0 || k <= 0 || n_exp <= 0 || hidden <= 0 || ff <= 0 || hidden % 256 || ff % 256) return 0;
+    return moe_pre_layout(n_tok, k, n_exp, hidden, ff).total;
+}
+
 /* The MoE layer over expert slabs (gate/up/down) or per-expert pointer tables (gptr/uptr/dptr). */
 static int moe_layer_impl(le_ctx *c, int ty_gate, int ty_up, int ty_down, const void *gate, const void *up, const void *down,
                           const void *const *gptr, const void *const *uptr, const void *const *dptr, int n_exp, int k,
@@ -603,9 +684,21 @@ static int moe_layer_impl(le_ctx *c, int ty_gate, int ty_up, int ty_down, const 
     bool have = false;
     for (auto &cb : combos) have |= cb[0] == ty_gate && cb[1] == ty_down;
     if (!have) return c->fail(LE_ERR_TYPE, "no MoE kernel for gate/up type %d with down type %d", ty_gate, ty_down);
-    if (n_tok <= 0 || n_tok > 64 || k <= 0 || k > 16 || n_exp <= 0 || n_exp > 256 || k > n_exp)
-        return c->fail(LE_ERR_SHAPE, "MoE limits: n_tok <= 64, k <= 16, k <= n_exp <= 256");
+    if (n_tok <= 0 || n_tok > LE_MOE_MAX_TOK || k <= 0 || k > 16 || n_exp <= 0 || n_exp > 256 || k > n_exp)
+        return c->fail(LE_ERR_SHAPE, "MoE limits: n_tok <= %d, k <= 16, k <= n_exp <= 256", LE_MOE_MAX_TOK);
     if (hidden <= 0 || ff <= 0 || hidden % 256 || ff % 256) return c->fail(LE_ERR_SHAPE, "hidden and ff must be multiples of 256");
+    /* prefill-sized token counts: routing, grouping by expert and grouped matrix-core matmuls (each
+     * expert's weights streamed once per tile of its pairs); up to 64 tokens the decode kernels
+     * take the call when the workspace is sized for them only */
+    if (n_tok > 64 || (c->moe_prefill && n_tok >= c->moe_prefill_min_tok &&
+                       ws_bytes >= le_moe_prefill_workspace_size(n_tok, k, n_exp, hidden, ff))) {
+        if (ws_bytes < le_moe_prefill_workspace_size(n_tok, k, n_exp, hidden, ff))
+            return c->fail(LE_ERR_WORKSPACE, "workspace needs %zu bytes (le_moe_prefill_workspace_size)",
+                           le_moe_prefill_workspace_size(n_tok, k, n_exp, hidden, ff));
+        if (!al16(h) || !al16(ws)) return c->fail(LE_ERR_ALIGN, "h and ws must be 16-byte aligned");
+        return moe_prefill(c, ty_gate, ty_down, gate, up, down, gptr, uptr, dptr, n_exp, k, hidden, ff, logits, h, n_tok, out,
+                           idx_out, w_out, ws, stream);
+    }
     if (ws_bytes < le_moe_workspace_size(n_tok, k, ff)) return c->fail(LE_ERR_WORKSPACE, "workspace needs %zu bytes", le_moe_workspace_size(n_tok, k, ff));
     if (!al16(h) || !al16(ws)) return c->fail(LE_ERR_ALIGN, "h and ws must be 16-byte aligned");
     const size_t lds = (size_t)8 * xtok_bytes(hidden);

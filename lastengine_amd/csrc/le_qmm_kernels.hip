@@ -2883,4 +2883,120 @@ LE_MOE_DNM(14, 8, 1) LE_MOE_DNM(14, 8, 2) LE_MOE_DNM(14, 8, 3) LE_MOE_DNM(12, 8,
     extern "C" __global__ void __launch_bounds__(512) le_moe_downf_##TD(MoeArgs a) { moe_down_fast<TD>(a); }
 LE_MOE(12, 14) LE_MOE(12, 12) LE_MOE(14, 14) LE_MOE(8, 8) LE_MOE(16, 18) LE_MOE(16, 16) LE_MOE(18, 18)
 LE_MOE_DOWN(8) LE_MOE_DOWN(12) LE_MOE_DOWN(14) LE_MOE_DOWN(16) LE_MOE_DOWN(18)
+/* ===================== MoE prefill: routing and grouping for the grouped matmul =====================
+ * For prefill-sized token counts (the reference's TMAX = 2048 per chunk, src/gpu/prefill.rs:6) the
+ * layer runs as: le_moe_route_tok (top-k and weights per token) -> le_moe_group (pairs grouped by
+ * expert, each expert's pairs in token order: the host grouping of src/gpu/prefill.rs:153-214 on
+ * the device) -> grouped matmul gate and up -> le_moe_swiglu -> grouped matmul down ->
+ * le_moe_combine (weighted sum in selection order, src/cpu_ref.rs:242-259). */
+struct MoePre {
+    const float *logits;
+    int *topi;     /* [n_tok * k] */
+    float *topw;   /* [n_tok * k] */
+    int *off;      /* [n_exp + 1] */
+    int *in_idx;   /* [n_tok * k]: the token of each grouped pair */
+    int *out_idx;  /* [n_tok * k]: the pair (t * k + s) of each grouped pair */
+    int *idx_out;  /* optional copies of the selection */
+    float *w_out;
+    int n_tok, n_exp, k, pad;
+};
+
+/* One wave per token: k rounds of a wave-wide max (ties keep the lower expert), weights
+ * exp(v - top) / sum in selection order, as the decode kernels compute them. */
+extern "C" __global__ void __launch_bounds__(512) le_moe_route_tok(MoePre a) {
+    const int lane = threadIdx.x & 63, t = blockIdx.x * 8 + (threadIdx.x >> 6);
+    if (t >= a.n_tok) return; /* uniform over the wave */
+    const int per = (a.n_exp + 63) >> 6;
+    float vv[MOE_LPASS];
+#pragma unroll
+    for (int j = 0; j < MOE_LPASS; j++) {
+        const int e = lane * per + j;
+        vv[j] = j < per && e < a.n_exp ? a.logits[(size_t)t * a.n_exp + e] : -INFINITY;
+    }
+    int my_e = 0;
+    float my_v = 0.f;
+    for (int r = 0; r < a.k; r++) {
+        float bv = vv[0];
+        int bj = 0;
+#pragma unroll
+        for (int j = 1; j < MOE_LPASS; j++) {
+            const bool gt = vv[j] > bv;
+            bv = gt ? vv[j] : bv;
+            bj = gt ? j : bj;
+        }
+        const float mx = wave_max(bv);
+        const int wl = __ffsll((long long)__ballot(bv == mx)) - 1;
+        const int wj = __builtin_amdgcn_readlane(bj, wl);
+#pragma unroll
+        for (int j = 0; j < MOE_LPASS; j++) vv[j] = lane == wl && j == wj ? -INFINITY : vv[j];
+        my_e = lane == r ? wl * per + wj : my_e;
+        my_v = lane == r ? mx : my_v;
+    }
+    const float top = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, my_v), 0));
+    const float ex = lane < a.k ? expf(my_v - top) : 0.f;
+    float tot = 0.f;
+    for (int r = 0; r < a.k; r++) tot += __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, ex), r));
+    if (lane < a.k) {
+        const int i = t * a.k + lane;
+        a.topi[i] = my_e;
+        a.topw[i] = ex / tot;
+        if (a.idx_out) a.idx_out[i] = my_e;
+        if (a.w_out) a.w_out[i] = ex / tot;
+    }
+}
+
+/* One block per expert e, two passes over the selection: the number of pairs routed to lower
+ * experts (its offset), then its own pairs in pair (= token) order, so the grouping is
+ * deterministic. The block for the last expert also writes off[n_exp]. */
+extern "C" __global__ void __launch_bounds__(256) le_moe_group(MoePre a) {
+    __shared__ int wsum[4];
+    const int e = blockIdx.x, lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int npair = a.n_tok * a.k;
+    int low = 0;
+    for (int p = threadIdx.x; p < npair; p += 256) low += a.topi[p] < e;
+    for (int o = 32; o > 0; o >>= 1) low += __shfl_xor(low, o);
+    if (lane == 0) wsum[wave] = low;
+    __syncthreads();
+    const int off = wsum[0] + wsum[1] + wsum[2] + wsum[3];
+    if (threadIdx.x == 0) a.off[e] = off;
+    int base = off;
+    __shared__ int wcnt[4];
+    for (int p0 = 0; p0 < npair; p0 += 256) {
+        const int p = p0 + (int)threadIdx.x;
+        const int x = p < npair ? a.topi[p] : -1;
+        const unsigned long long mine = __ballot(x == e);
+        if (lane == 0) wcnt[wave] = __popcll(mine);
+        __syncthreads();
+        int before = 0;
+        for (int w = 0; w < wave; w++) before += wcnt[w];
+        if (x == e) {
+            const int r = base + before + __popcll(mine & ((1ull << lane) - 1ull));
+            a.in_idx[r] = p / a.k;
+            a.out_idx[r] = p;
+        }
+        base += wcnt[0] + wcnt[1] + wcnt[2] + wcnt[3];
+        __syncthreads();
+    }
+    if (e == a.n_exp - 1 && threadIdx.x == 0) a.off[a.n_exp] = base;
+}
+
+/* act[p][c] = silu(g) * u over the grouped pairs' gate / up rows (in place into g). */
+extern "C" __global__ void __launch_bounds__(256) le_moe_swiglu(float *g, const float *u, long long n) {
+    for (long long i = (long long)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (long long)gridDim.x * blockDim.x) {
+        const float x = g[i];
+        g[i] = x / (1.0f + __expf(-x)) * u[i];
+    }
+}
+
+/* out[t][c] = sum over s < k of w[t k + s] * d[t k + s][c], added in selection order. */
+extern "C" __global__ void __launch_bounds__(256) le_moe_combine(const float *d, const float *w, float *out, int n_tok, int k,
+                                                                 int hidden) {
+    const long long n = (long long)n_tok * hidden;
+    for (long long i = (long long)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (long long)gridDim.x * blockDim.x) {
+        const int t = (int)(i / hidden), c = (int)(i - (long long)t * hidden);
+        float acc = 0.f;
+        for (int s = 0; s < k; s++) acc += w[t * k + s] * d[((size_t)t * k + s) * hidden + c];
+        out[i] = acc;
+    }
+}
 #endif /* LE_PART_MOE */

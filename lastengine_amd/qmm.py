@@ -68,6 +68,7 @@ def lib():
         "le_moe_workspace_size": (S, [I, I, I]),
         "le_moe_layer": (I, [P, I, I, I, P, P, P, I, I, I, I, P, P, I, P, P, P, P, S, P]),
         "le_moe_check": (I, [P, P, P]),
+        "le_moe_prefill_workspace_size": (S, [I, I, I, I, I]),
         "le_moe_layer_ptrs": (I, [P, I, I, I, P, P, P, I, I, I, I, P, P, I, P, P, P, P, S, P]),
         "le_mm_grouped_workspace_size": (S, [I, I, I, I]),
         "le_mm_grouped": (I, [P, I, P, P, P, P, P, I, I, P, P, I, I, P, S, P]),
@@ -185,12 +186,18 @@ class Engine:
     def moe_workspace_size(self, n_tok, k, ff):
         return int(self._L.le_moe_workspace_size(n_tok, k, ff))
 
+    def moe_prefill_workspace_size(self, n_tok, k, n_exp, hidden, ff):
+        return int(self._L.le_moe_prefill_workspace_size(n_tok, k, n_exp, hidden, ff))
+
     def moe(self, ty_gate, ty_up, ty_down, gate, up, down, n_exp, k, hidden, ff, logits, h, n_tok, out,
             idx_out=None, w_out=None, ws=None, ws_bytes=None, stream=None):
         """Routed MoE layer (cpu_ref::moe, src/cpu_ref.rs:242-259) for n_tok tokens."""
         if ws is None:
             import torch
-            ws = torch.zeros(max(16, self.moe_workspace_size(n_tok, k, ff)), dtype=torch.uint8, device="cuda")
+            n = self.moe_workspace_size(n_tok, k, ff)
+            if n_tok > 16:
+                n = max(n, self.moe_prefill_workspace_size(n_tok, k, n_exp, hidden, ff))
+            ws = torch.zeros(max(16, n), dtype=torch.uint8, device="cuda")
         if ws_bytes is None:
             ws_bytes = ws.numel() if hasattr(ws, "numel") else 0
         self._check(self._L.le_moe_layer(self._ctx, ty_gate, ty_up, ty_down, _ptr(gate), _ptr(up), _ptr(down), n_exp,
@@ -202,7 +209,10 @@ class Engine:
         """The MoE layer over per-expert pointer tables (device arrays of n_exp weight pointers)."""
         if ws is None:
             import torch
-            ws = torch.zeros(max(16, self.moe_workspace_size(n_tok, k, ff)), dtype=torch.uint8, device="cuda")
+            n = self.moe_workspace_size(n_tok, k, ff)
+            if n_tok > 16:
+                n = max(n, self.moe_prefill_workspace_size(n_tok, k, n_exp, hidden, ff))
+            ws = torch.zeros(max(16, n), dtype=torch.uint8, device="cuda")
         if ws_bytes is None:
             ws_bytes = ws.numel() if hasattr(ws, "numel") else 0
         self._check(self._L.le_moe_layer_ptrs(self._ctx, ty_gate, ty_up, ty_down, _ptr(gate_ptrs), _ptr(up_ptrs),

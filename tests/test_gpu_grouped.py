@@ -68,7 +68,7 @@ def test_mm_grouped(engine, name, counts, tables):
         check_close(got[out_idx[lo:hi]], want, mag)
 
 
-@pytest.mark.parametrize("n_tok", [1, 4, 8, 20])
+@pytest.mark.parametrize("n_tok", [1, 4, 8, 20, 100])
 def test_moe_pointer_tables(engine, n_tok):
     """le_moe_layer_ptrs gives the same bits as le_moe_layer on the same experts (here placed in a
     shuffled arena): only the weight addressing differs."""

@@ -4,7 +4,7 @@ import pytest
 
 import lastengine_amd as le
 import oracle
-from tests.util import weights, acts, check_close
+from tests.util import weights, acts, check_close, random_blocks
 
 pytestmark = pytest.mark.gpu
 
@@ -15,33 +15,41 @@ def dev(a):
 
 
 def reference(tg, td, g, u, d, n_exp, k, hidden, ff, h, lg):
-    """Oracle output plus the condition number sum_s w_s * sum_c |down[r,c] * a_c| per output."""
+    """Oracle output plus the condition number sum_s w_s * sum_c |down[r,c] * a_c| per output
+    (computed per expert over all the pairs routed to it, from the dequantized weights)."""
     out, idx, w = oracle.moe(tg, tg, td, g, u, d, n_exp, k, hidden, ff, h, lg)
     rbg, rbd = le.row_bytes(tg, hidden), le.row_bytes(td, ff)
     mag = np.zeros_like(out, dtype=np.float64)
-    for t in range(h.shape[0]):
-        for s in range(k):
-            e = idx[t, s]
-            gg = oracle.matvec(tg, g.reshape(-1)[e * ff * rbg:(e + 1) * ff * rbg], ff, hidden, h[t])
-            uu = oracle.matvec(tg, u.reshape(-1)[e * ff * rbg:(e + 1) * ff * rbg], ff, hidden, h[t])
-            a = gg / (1 + np.exp(-gg.astype(np.float64))) * uu
-            dw = oracle.dequant_rows(td, d.reshape(-1)[e * hidden * rbd:(e + 1) * hidden * rbd], hidden, ff)
-            mag[t] += w[t, s] * (np.abs(dw).astype(np.float64) @ np.abs(a))
+    gf, uf, df = g.reshape(-1), u.reshape(-1), d.reshape(-1)
+    for e in np.unique(idx):
+        ts, ss = np.nonzero(idx == e)
+        gw = oracle.dequant_rows(tg, gf[e * ff * rbg:(e + 1) * ff * rbg], ff, hidden).astype(np.float64)
+        uw = oracle.dequant_rows(tg, uf[e * ff * rbg:(e + 1) * ff * rbg], ff, hidden).astype(np.float64)
+        dw = oracle.dequant_rows(td, df[e * hidden * rbd:(e + 1) * hidden * rbd], hidden, ff).astype(np.float64)
+        hh = h[ts].astype(np.float64)
+        gg, uu = hh @ gw.T, hh @ uw.T
+        a = gg / (1 + np.exp(-gg)) * uu
+        mag[ts] += w[ts, ss][:, None] * (np.abs(a) @ np.abs(dw).T)
     return out, idx, w, mag
 
 
-def run(engine, tg, td, n_exp, k, hidden, ff, n_tok, seed, lg=None):
+def run(engine, tg, td, n_exp, k, hidden, ff, n_tok, seed, lg=None, rand=False, ws=None):
     import torch
-    g, _ = weights(tg, n_exp * ff, hidden, seed)
-    u, _ = weights(tg, n_exp * ff, hidden, seed + 1)
-    d, _ = weights(td, n_exp * hidden, ff, seed + 2)
+    if rand:
+        g = random_blocks(tg, n_exp * ff, hidden, seed)
+        u = random_blocks(tg, n_exp * ff, hidden, seed + 1)
+        d = random_blocks(td, n_exp * hidden, ff, seed + 2)
+    else:
+        g, _ = weights(tg, n_exp * ff, hidden, seed)
+        u, _ = weights(tg, n_exp * ff, hidden, seed + 1)
+        d, _ = weights(td, n_exp * hidden, ff, seed + 2)
     h = acts(n_tok * hidden, seed + 3).reshape(n_tok, hidden)
     if lg is None:
         lg = acts(n_tok * n_exp, seed + 4).reshape(n_tok, n_exp)
     out = torch.empty(n_tok, hidden, dtype=torch.float32, device="cuda")
     idx = torch.empty(n_tok, k, dtype=torch.int32, device="cuda")
     w = torch.empty(n_tok, k, dtype=torch.float32, device="cuda")
-    engine.moe(tg, tg, td, dev(g), dev(u), dev(d), n_exp, k, hidden, ff, dev(lg), dev(h), n_tok, out, idx, w)
+    engine.moe(tg, tg, td, dev(g), dev(u), dev(d), n_exp, k, hidden, ff, dev(lg), dev(h), n_tok, out, idx, w, ws=ws)
     torch.cuda.synchronize()
     want, widx, ww, mag = reference(tg, td, g, u, d, n_exp, k, hidden, ff, h, lg)
     assert np.array_equal(idx.cpu().numpy(), widx)
@@ -107,7 +115,7 @@ def test_moe_errors(engine):
         engine.moe(le.Q4_K, le.Q8_0, le.Q6_K, z, z, z, 8, 2, 256, 256, f, f, 1, f)
     assert e.value.code == -2
     with pytest.raises(le.LeError) as e:
-        engine.moe(le.Q4_K, le.Q4_K, le.Q6_K, z, z, z, 8, 2, 256, 256, f, f, 65, f)
+        engine.moe(le.Q4_K, le.Q4_K, le.Q6_K, z, z, z, 8, 2, 256, 256, f, f, 65537, f)
     assert e.value.code == -3
     with pytest.raises(le.LeError) as e:
         engine.moe(le.Q4_K, le.Q4_K, le.Q6_K, z, z, z, 8, 2, 256, 256, f, f, 1, f, ws=z, ws_bytes=16)
@@ -182,3 +190,71 @@ def test_moe_limits(engine):
 def test_moe_config4_more_tokens(engine, n_tok):
     """Config 4 beyond the decode-shaped kernels (the vector member-chunk path)."""
     run(engine, le.Q4_K, le.Q6_K, 128, 8, 2048, 768, n_tok, seed=720 + n_tok)
+
+
+@pytest.mark.parametrize("n_tok", [64, 256])
+def test_moe_prefill_config4(engine, n_tok):
+    """Config 4 on the grouped matrix-core form: route, group the pairs by expert, grouped gate /
+    up / down matmuls, SwiGLU and the weighted combine."""
+    run(engine, le.Q4_K, le.Q6_K, 128, 8, 2048, 768, n_tok, seed=800 + n_tok)
+
+
+@pytest.mark.parametrize("tg,td", [(le.Q8_0, le.Q8_0), (le.IQ2_XXS, le.IQ3_XXS), (le.Q4_K, le.Q4_K), (le.Q6_K, le.Q6_K)])
+def test_moe_prefill_types(engine, tg, td):
+    run(engine, tg, td, 16, 4, 512, 512, 100, seed=820 + tg)
+
+
+def test_moe_prefill_random_blocks(engine):
+    """Arbitrary block bytes (bounded super-block scales) through the grouped form."""
+    run(engine, le.Q4_K, le.Q6_K, 32, 4, 1024, 512, 130, seed=840, rand=True)
+
+
+@pytest.mark.parametrize("tg,td", [(le.Q4_K, le.Q6_K), (le.IQ2_XXS, le.IQ3_XXS), (le.Q8_0, le.Q8_0)])
+def test_moe_decode_random_blocks(engine, tg, td):
+    """Arbitrary block bytes through the decode kernels (1 and 6 tokens)."""
+    run(engine, tg, td, 32, 4, 1024, 512, 1, seed=860 + tg, rand=True)
+    run(engine, tg, td, 32, 4, 1024, 512, 6, seed=870 + tg, rand=True)
+
+
+def test_moe_prefill_uneven_experts(engine):
+    """Most pairs on two experts, most experts empty; a token count that is not a tile multiple."""
+    n_tok, n_exp, k = 300, 64, 2
+    lg = acts(n_tok * n_exp, 880).reshape(n_tok, n_exp).astype(np.float32) * 0.01
+    lg[:, 5] += 4.0
+    lg[: n_tok // 2, 40] += 3.0
+    lg[n_tok // 2:, 63] += 3.0
+    run(engine, le.Q4_K, le.Q6_K, n_exp, k, 512, 256, n_tok, seed=881, lg=lg)
+
+
+@pytest.mark.parametrize("n_tok", [17, 64])
+def test_moe_prefill_matches_decode(fresh_engine, n_tok):
+    """The grouped form and the decode kernels agree (both against the oracle) where both apply."""
+    import torch
+    engine = fresh_engine
+    n_exp, k, hidden, ff = 64, 8, 2048, 768
+    g, _ = weights(le.Q4_K, n_exp * ff, hidden, 901)
+    u, _ = weights(le.Q4_K, n_exp * ff, hidden, 902)
+    d, _ = weights(le.Q6_K, n_exp * hidden, ff, 903)
+    h = acts(n_tok * hidden, 904).reshape(n_tok, hidden)
+    lg = acts(n_tok * n_exp, 905).reshape(n_tok, n_exp)
+    want, _, _, mag = reference(le.Q4_K, le.Q6_K, g, u, d, n_exp, k, hidden, ff, h, lg)
+    for pre in (1, 0):
+        engine.set_option("moe_prefill", pre)
+        out = torch.empty(n_tok, hidden, dtype=torch.float32, device="cuda")
+        engine.moe(le.Q4_K, le.Q4_K, le.Q6_K, dev(g), dev(u), dev(d), n_exp, k, hidden, ff, dev(lg), dev(h), n_tok, out)
+        torch.cuda.synchronize()
+        check_close(out.cpu().numpy(), want, mag)
+    engine.set_option("moe_prefill", 1)
+
+
+def test_moe_prefill_workspace(engine):
+    """Above 64 tokens the call needs the prefill workspace; a decode-sized one is refused."""
+    import torch
+    n_exp, k, hidden, ff, n_tok = 16, 2, 256, 256, 80
+    need = engine.moe_prefill_workspace_size(n_tok, k, n_exp, hidden, ff)
+    assert need > engine.moe_workspace_size(n_tok, k, ff)
+    z = torch.zeros(1 << 20, dtype=torch.uint8, device="cuda")
+    f = torch.zeros(n_tok * max(hidden, n_exp), dtype=torch.float32, device="cuda")
+    with pytest.raises(le.LeError) as e:
+        engine.moe(le.Q4_K, le.Q4_K, le.Q6_K, z, z, z, n_exp, k, hidden, ff, f, f, n_tok, f, ws=z, ws_bytes=need - 1)
+    assert e.value.code == -7
