@@ -67,6 +67,27 @@ __device__ __forceinline__ float h2f(u32 bits16) {
     return (float)__builtin_bit_cast(_Float16, (uint16_t)bits16);
 }
 
+/* src/quant.rs:37-49, in integer arithmetic (also reproduces NaN payloads bit for bit). */
+__device__ inline float f16_exact(u32 h) {
+    const u32 s = (h >> 15) & 1u, e = (h >> 10) & 0x1fu, m = h & 0x3ffu;
+    u32 bits;
+    if (e == 0) {
+        if (m == 0) {
+            bits = s << 31;
+        } else {
+            const int lz = __builtin_clz(m) - 21; /* shifts until bit 10 is set */
+            bits = (s << 31) | ((u32)(113 - lz) << 23) | (((m << lz) & 0x3ffu) << 13);
+        }
+    } else if (e == 31) {
+        bits = (s << 31) | (0xffu << 23) | (m << 13);
+    } else {
+        bits = (s << 31) | ((e + 112) << 23) | (m << 13);
+    }
+    return __builtin_bit_cast(float, bits);
+}
+
+__device__ __forceinline__ u32 ksign_dev(u32 i) { return (i & 0x7fu) | ((__builtin_popcount(i & 0x7fu) & 1u) << 7); }
+
 __device__ __forceinline__ int dot4(u32 a, u32 b, int c) {
     return __builtin_amdgcn_sdot4((int)a, (int)b, c, false);
 }

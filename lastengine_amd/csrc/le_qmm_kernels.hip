@@ -48,27 +48,6 @@ __device__ const u32 le_iq3xxs_grid[256] = LE_IQ3XXS_GRID_WORDS;
 /* src/quant.rs operation by operation with FP contraction disabled.                         */
 /* ===================================================================================== */
 
-/* src/quant.rs:37-49, in integer arithmetic (also reproduces NaN payloads bit for bit). */
-__device__ float f16_exact(u32 h) {
-    const u32 s = (h >> 15) & 1u, e = (h >> 10) & 0x1fu, m = h & 0x3ffu;
-    u32 bits;
-    if (e == 0) {
-        if (m == 0) {
-            bits = s << 31;
-        } else {
-            const int lz = __builtin_clz(m) - 21; /* shifts until bit 10 is set */
-            bits = (s << 31) | ((u32)(113 - lz) << 23) | (((m << lz) & 0x3ffu) << 13);
-        }
-    } else if (e == 31) {
-        bits = (s << 31) | (0xffu << 23) | (m << 13);
-    } else {
-        bits = (s << 31) | ((e + 112) << 23) | (m << 13);
-    }
-    return __builtin_bit_cast(float, bits);
-}
-
-__device__ __forceinline__ u32 ksign_dev(u32 i) { return (i & 0x7fu) | ((__builtin_popcount(i & 0x7fu) & 1u) << 7); }
-
 template <int TY>
 __device__ void dequant_unit(const u8 *row, int unit, float *o);
 

@@ -32,6 +32,8 @@ def lib():
         "or_matvec": (I, [I, P, S, S, P, P, I]),
         "or_route": (None, [P, I, I, P, P]),
         "or_moe": (I, [I, I, I, P, P, P, I, I, S, S, P, P, I, P, P, P, I]),
+        "or_quant_x": (None, [P, P, P, P, S]),
+        "or_matvec_q8": (I, [I, P, S, S, P, P, P, P]),
     }
     for name, (res, args) in sig.items():
         fn = getattr(L, name)
@@ -109,3 +111,27 @@ def moe(ty_g, ty_u, ty_d, gate, up, down, n_exp, k, hidden, ff, h, logits, nthre
     if not ok:
         raise ValueError("bad moe arguments")
     return out, idx, w
+
+
+def quant_x(x):
+    """quant_x (src/cuda/kernels.cu:15-25) over a length-32n vector -> (xq int8, xd f32, xs i32)."""
+    x = np.ascontiguousarray(x, dtype=np.float32).reshape(-1)
+    assert x.size % 32 == 0
+    n = x.size // 32
+    xq = np.empty(x.size, dtype=np.int8)
+    xd = np.empty(n, dtype=np.float32)
+    xs = np.empty(n, dtype=np.int32)
+    lib().or_quant_x(x.ctypes.data, xq.ctypes.data, xd.ctypes.data, xs.ctypes.data, n)
+    return xq, xd, xs
+
+
+def matvec_q8(ty, w, rows, cols, xq, xd, xs):
+    """matvec_<ty> on int8 activations (src/cuda/kernels.cu:36-110,371-392) -> (rows,)."""
+    w = np.ascontiguousarray(w, dtype=np.uint8)
+    xq = np.ascontiguousarray(xq, dtype=np.int8)
+    xd = np.ascontiguousarray(xd, dtype=np.float32)
+    xs = np.ascontiguousarray(xs, dtype=np.int32)
+    y = np.empty(rows, dtype=np.float32)
+    if not lib().or_matvec_q8(ty, w.ctypes.data, rows, cols, xq.ctypes.data, xd.ctypes.data, xs.ctypes.data, y.ctypes.data):
+        raise ValueError("unsupported type %d or shape" % ty)
+    return y

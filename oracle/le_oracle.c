@@ -9,8 +9,12 @@
  *   - block_info/row_bytes  src/quant.rs:24-35
  *   - scale_min_k4          src/quant.rs:52-55
  *   - ksign                 src/quant.rs:57
- *   - dequant_row           src/quant.rs:59-170 (Q8_0 :68-71, Q4_K :72-82, Q6_K :96-112,
- *                           IQ3_XXS :127-141, IQ2_XXS :142-154)
+ *   - dequant_row           src/quant.rs:59-170 (Q4_0 :64-67, Q8_0 :68-71, Q4_K :72-82,
+ *                           Q5_K :83-95, Q6_K :96-112, Q3_K :113-126, IQ3_XXS :127-141,
+ *                           IQ2_XXS :142-154, IQ2_S :155-167)
+ *   - quant_x               src/cuda/kernels.cu:15-25 (int8 activations per 32 values)
+ *   - matvec_<ty> on int8 activations: udot<ty> per 32-value unit, src/cuda/kernels.cu:36-110,
+ *                           summed per row in mv_impl's lane order, :371-392
  *   - Model::matvec         src/cpu_ref.rs:109-118 (per-row dequant, sequential f32 sum)
  *   - Model::matmat         src/cpu_ref.rs:266-276
  *   - Model::moe routed part src/cpu_ref.rs:242-259 (softmax, stable sort, top-k, renormalise,
@@ -33,7 +37,8 @@
 
 #include "le_oracle_tables.h"
 
-enum { OR_Q8_0 = 8, OR_Q4_K = 12, OR_Q6_K = 14, OR_IQ2_XXS = 16, OR_IQ3_XXS = 18 };
+enum { OR_Q4_0 = 2, OR_Q8_0 = 8, OR_Q3_K = 11, OR_Q4_K = 12, OR_Q5_K = 13, OR_Q6_K = 14, OR_IQ2_XXS = 16,
+       OR_IQ3_XXS = 18, OR_IQ2_S = 22 };
 
 /* src/quant.rs:37-49 */
 float or_f16_to_f32(uint16_t h) {
@@ -61,8 +66,12 @@ static float hf(const uint8_t *b, size_t o) { return or_f16_to_f32((uint16_t)(b[
 /* src/quant.rs:24-31: values per block, bytes per block. Returns 0 for unsupported types. */
 int or_block_info(int ty, int *values, int *bytes) {
     switch (ty) {
+    case OR_Q4_0: *values = 32; *bytes = 18; return 1;
     case OR_Q8_0: *values = 32; *bytes = 34; return 1;
+    case OR_Q3_K: *values = 256; *bytes = 110; return 1;
     case OR_Q4_K: *values = 256; *bytes = 144; return 1;
+    case OR_Q5_K: *values = 256; *bytes = 176; return 1;
+    case OR_IQ2_S: *values = 256; *bytes = 82; return 1;
     case OR_Q6_K: *values = 256; *bytes = 210; return 1;
     case OR_IQ2_XXS: *values = 256; *bytes = 66; return 1;
     case OR_IQ3_XXS: *values = 256; *bytes = 98; return 1;
@@ -106,6 +115,66 @@ int or_dequant_row(int ty, const uint8_t *src, float *o, size_t n) {
             const uint8_t *b = src + blk * 34;
             float d = hf(b, 0);
             for (int j = 0; j < 32; j++) o[blk * 32 + j] = d * (float)(int8_t)b[2 + j];
+        }
+        return 1;
+    case OR_Q4_0: /* :64-67 */
+        for (size_t blk = 0; blk < n / 32; blk++) {
+            const uint8_t *b = src + blk * 18;
+            float d = hf(b, 0);
+            for (int j = 0; j < 16; j++) {
+                o[blk * 32 + j] = d * ((float)(b[2 + j] & 15) - 8.0f);
+                o[blk * 32 + j + 16] = d * ((float)(b[2 + j] >> 4) - 8.0f);
+            }
+        }
+        return 1;
+    case OR_Q5_K: /* :83-95 */
+        for (size_t blk = 0; blk < n / 256; blk++) {
+            const uint8_t *b = src + blk * 176, *sc = b + 4, *qh = b + 16, *qs = b + 48;
+            float d = hf(b, 0), dmin = hf(b, 2), *ob = o + blk * 256;
+            for (int g = 0; g < 4; g++) {
+                uint8_t s1, m1, s2, m2;
+                scale_min_k4(2 * g, sc, &s1, &m1);
+                scale_min_k4(2 * g + 1, sc, &s2, &m2);
+                for (int l = 0; l < 32; l++) {
+                    float lo = (float)(qs[g * 32 + l] & 15) + (((qh[l] >> (2 * g)) & 1) ? 16.0f : 0.0f);
+                    float hi = (float)(qs[g * 32 + l] >> 4) + (((qh[l] >> (2 * g + 1)) & 1) ? 16.0f : 0.0f);
+                    ob[g * 64 + l] = d * (float)s1 * lo - dmin * (float)m1;
+                    ob[g * 64 + 32 + l] = d * (float)s2 * hi - dmin * (float)m2;
+                }
+            }
+        }
+        return 1;
+    case OR_Q3_K: /* :113-126 */
+        for (size_t blk = 0; blk < n / 256; blk++) {
+            const uint8_t *b = src + blk * 110, *hm = b, *qs = b + 32, *sc = b + 96;
+            float d = hf(b, 108);
+            int scales[16];
+            for (int i = 0; i < 16; i++) {
+                int lo = i < 8 ? (sc[i] & 15) : (sc[i - 8] >> 4);
+                int hi = (sc[8 + i % 4] >> (2 * (i / 4))) & 3;
+                scales[i] = (lo | (hi << 4)) - 32;
+            }
+            for (int e = 0; e < 256; e++) {
+                int c = e / 128, sh = (e % 128) / 32, l = e % 32;
+                int q = ((qs[32 * c + l] >> (2 * sh)) & 3) - (((hm[l] >> (e / 32)) & 1) == 0 ? 4 : 0);
+                o[blk * 256 + e] = d * (float)scales[e / 16] * (float)q;
+            }
+        }
+        return 1;
+    case OR_IQ2_S: /* :155-167 */
+        for (size_t blk = 0; blk < n / 256; blk++) {
+            const uint8_t *b = src + blk * 82, *qs = b + 2, *signs = b + 34, *qh = b + 66, *sc = b + 74;
+            float d = hf(b, 0);
+            for (int ib = 0; ib < 8; ib++) {
+                float db[2] = {d * (0.5f + (float)(sc[ib] & 15)) * 0.25f, d * (0.5f + (float)(sc[ib] >> 4)) * 0.25f};
+                for (int l = 0; l < 4; l++) {
+                    int gi = qs[ib * 4 + l] | (((int)qh[ib] << (8 - 2 * l)) & 0x300);
+                    const uint8_t *g = OR_IQ2S_GRID[gi];
+                    uint8_t sgn = signs[ib * 4 + l];
+                    for (int j = 0; j < 8; j++)
+                        o[blk * 256 + ib * 32 + l * 8 + j] = db[l / 2] * (float)g[j] * ((sgn >> j) & 1 ? -1.0f : 1.0f);
+                }
+            }
         }
         return 1;
     case OR_Q4_K: /* :72-82 */
@@ -309,5 +378,163 @@ int or_moe(int ty_g, int ty_u, int ty_d, const uint8_t *gate, const uint8_t *up,
             for (int s = 0; s < k; s++) { idx_out[t * k + s] = idx[s]; w_out[t * k + s] = w[s]; }
     }
     free(gg); free(uu); free(a); free(r); free(idx); free(w);
+    return 1;
+}
+
+/* ---- int8 activation mode (reference GPU path) ---- */
+
+/* quant_x (src/cuda/kernels.cu:15-25): per 32 values d = amax / 127, q = round-half-even(x / d)
+ * computed as x * (1 / d), xs = sum q. One unit per 32 values. */
+void or_quant_x(const float *x, int8_t *xq, float *xd, int32_t *xs, size_t n_units) {
+    for (size_t u = 0; u < n_units; u++) {
+        float a = 0.0f;
+        for (int l = 0; l < 32; l++) a = fmaxf(a, fabsf(x[u * 32 + l]));
+        float d = a / 127.0f, id = d > 0.0f ? 1.0f / d : 0.0f;
+        int s = 0;
+        for (int l = 0; l < 32; l++) {
+            int q = (int)nearbyintf(x[u * 32 + l] * id);
+            xq[u * 32 + l] = (int8_t)q;
+            s += q;
+        }
+        xd[u] = d;
+        xs[u] = s;
+    }
+}
+
+static int dot8(const int8_t *a, const int *w) { /* w: 8 values as ints */
+    int s = 0;
+    for (int i = 0; i < 8; i++) s += a[i] * w[i];
+    return s;
+}
+
+/* Integer weight values of 32-value unit j of block b (the q the dequant multiplies), in the
+ * order the activations of that unit are laid out. */
+static void unit_q(int ty, const uint8_t *b, int j, int *q) {
+    switch (ty) {
+    case OR_Q4_0:
+        for (int l = 0; l < 16; l++) { q[l] = b[2 + l] & 15; q[l + 16] = b[2 + l] >> 4; }
+        break;
+    case OR_Q8_0:
+        for (int l = 0; l < 32; l++) q[l] = (int8_t)b[2 + l];
+        break;
+    case OR_Q4_K:
+        for (int l = 0; l < 32; l++) q[l] = (j & 1) ? (b[16 + (j >> 1) * 32 + l] >> 4) : (b[16 + (j >> 1) * 32 + l] & 15);
+        break;
+    case OR_Q5_K:
+        for (int l = 0; l < 32; l++) {
+            int v = (j & 1) ? (b[48 + (j >> 1) * 32 + l] >> 4) : (b[48 + (j >> 1) * 32 + l] & 15);
+            q[l] = v | (((b[16 + l] >> j) & 1) << 4);
+        }
+        break;
+    case OR_Q3_K:
+        for (int l = 0; l < 32; l++)
+            q[l] = ((b[32 + (j >> 2) * 32 + l] >> (2 * (j & 3))) & 3) - (((b[l] >> j) & 1) ? 0 : 4);
+        break;
+    case OR_Q6_K: {
+        int half = j >> 2, s = j & 3;
+        const uint8_t *ql = b + half * 64 + (s & 1) * 32, *qh = b + 128 + half * 32;
+        for (int l = 0; l < 32; l++) q[l] = (((ql[l] >> ((s >> 1) * 4)) & 15) | (((qh[l] >> (2 * s)) & 3) << 4)) - 32;
+        break;
+    }
+    case OR_IQ2_XXS: {
+        const uint8_t *g8 = b + 2 + j * 8;
+        uint32_t aux = rd32(g8 + 4);
+        for (int l = 0; l < 4; l++) {
+            uint8_t sg = or_ksign((int)((aux >> (7 * l)) & 127));
+            for (int t = 0; t < 8; t++) q[l * 8 + t] = ((sg >> t) & 1) ? -(int)OR_IQ2XXS_GRID[g8[l]][t] : OR_IQ2XXS_GRID[g8[l]][t];
+        }
+        break;
+    }
+    case OR_IQ3_XXS: {
+        const uint8_t *qs = b + 2 + j * 8;
+        uint32_t aux = rd32(b + 66 + j * 4);
+        for (int l = 0; l < 4; l++) {
+            uint8_t sg = or_ksign((int)((aux >> (7 * l)) & 127));
+            for (int t = 0; t < 8; t++) {
+                int g = OR_IQ3XXS_GRID[qs[2 * l + t / 4]][t & 3];
+                q[l * 8 + t] = ((sg >> t) & 1) ? -g : g;
+            }
+        }
+        break;
+    }
+    case OR_IQ2_S: {
+        const uint8_t *qs = b + 2 + j * 4, *sn = b + 34 + j * 4;
+        int qh = b[66 + j];
+        for (int l = 0; l < 4; l++) {
+            int gi = qs[l] | ((qh << (8 - 2 * l)) & 0x300);
+            for (int t = 0; t < 8; t++) q[l * 8 + t] = ((sn[l] >> t) & 1) ? -(int)OR_IQ2S_GRID[gi][t] : OR_IQ2S_GRID[gi][t];
+        }
+        break;
+    }
+    }
+}
+
+/* udot<ty> (src/cuda/kernels.cu:36-110): unit j of block b against int8 activations xq[32], scale
+ * dx, sum sx; the integer dot is exact and the float expression keeps the reference's order. */
+static float unit_dot(int ty, const uint8_t *b, int j, const int8_t *xq, float dx, int sx) {
+    int q[32];
+    unit_q(ty, b, j, q);
+    int a0 = dot8(xq, q) + dot8(xq + 8, q + 8), a1 = dot8(xq + 16, q + 16) + dot8(xq + 24, q + 24);
+    int a = a0 + a1;
+    switch (ty) {
+    case OR_Q4_0: return hf(b, 0) * dx * (float)(a - 8 * sx);
+    case OR_Q8_0: return hf(b, 0) * dx * (float)a;
+    case OR_Q4_K:
+    case OR_Q5_K: {
+        uint8_t sc, m;
+        scale_min_k4(j, b + 4, &sc, &m);
+        return dx * (hf(b, 0) * (float)sc * (float)a - hf(b, 2) * (float)m * (float)sx);
+    }
+    case OR_Q3_K: {
+        const uint8_t *sc = b + 96;
+        float r = 0.0f;
+        for (int h = 0; h < 2; h++) {
+            int i = 2 * j + h;
+            int lo = i < 8 ? (sc[i] & 15) : (sc[i - 8] >> 4), hi = (sc[8 + (i & 3)] >> (2 * (i >> 2))) & 3;
+            r += (float)(((lo | (hi << 4)) - 32) * (h ? a1 : a0));
+        }
+        return hf(b, 108) * dx * r;
+    }
+    case OR_Q6_K: {
+        const int8_t *sc = (const int8_t *)(b + 192) + (j >> 2) * 8 + (j & 3) * 2;
+        return hf(b, 208) * dx * (float)(sc[0] * a0 + sc[1] * a1);
+    }
+    case OR_IQ2_XXS: return hf(b, 0) * (0.5f + (float)(rd32(b + 2 + j * 8 + 4) >> 28)) * 0.25f * dx * (float)a;
+    case OR_IQ3_XXS: return hf(b, 0) * (0.5f + (float)(rd32(b + 66 + j * 4) >> 28)) * 0.5f * dx * (float)a;
+    case OR_IQ2_S: {
+        int sc = b[74 + j];
+        return hf(b, 0) * 0.25f * dx * ((0.5f + (float)(sc & 15)) * (float)a0 + (0.5f + (float)(sc >> 4)) * (float)a1);
+    }
+    }
+    return 0.0f;
+}
+
+/* matvec_<ty> on int8 activations (src/cuda/kernels.cu:371-392): per row, lane li of lpr lanes
+ * sums units li, li + lpr, ... in order; the lanes are then combined by the xor butterfly
+ * o = lpr/2 .. 1 (lane 0's value is stored). lpr = min(32, units) as in the reference when that
+ * is a power of two; otherwise (units = 24, i.e. 768 columns) the largest power of two below it,
+ * since the reference's butterfly would then mix lanes of two rows. cols % 256 == 0. */
+int or_matvec_q8(int ty, const uint8_t *w, size_t rows, size_t cols, const int8_t *xq, const float *xd, const int32_t *xs,
+                 float *y) {
+    int v, bb;
+    if (!or_block_info(ty, &v, &bb) || cols % 256) return 0;
+    size_t rb = or_row_bytes(ty, cols);
+    int units = (int)(cols / 32), lpr = units >= 32 ? 32 : units >= 16 ? 16 : 8, ub = v / 32;
+    float acc[32];
+    for (size_t r = 0; r < rows; r++) {
+        const uint8_t *row = w + r * rb;
+        for (int li = 0; li < lpr; li++) {
+            float a = 0.0f;
+            for (int u = li; u < units; u += lpr)
+                a += unit_dot(ty, row + (size_t)(u / ub) * bb, u % ub, xq + (size_t)u * 32, xd[u], xs[u]);
+            acc[li] = a;
+        }
+        for (int o = lpr >> 1; o; o >>= 1) {
+            float nx[32];
+            for (int li = 0; li < lpr; li++) nx[li] = acc[li] + acc[li ^ o];
+            memcpy(acc, nx, sizeof(float) * (size_t)lpr);
+        }
+        y[r] = acc[0];
+    }
     return 1;
 }

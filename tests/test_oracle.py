@@ -52,6 +52,28 @@ def _grids():
     return g2, g3
 
 
+def _grid_s():
+    from oracle import HERE
+    import os, re
+    txt = open(os.path.join(HERE, "le_oracle_tables.h")).read()
+    blocks = re.findall(r"\{([0-9,]+)\}", txt)
+    return np.array([[int(v) for v in b.split(",")] for b in blocks[512:]], dtype=np.int32)
+
+
+def test_iq2s_grid_invariants():
+    """IQ2_S grid (src/quant_iq2_grids.rs:260-1284): 1024 distinct points with magnitudes in
+    {8, 25, 43}, an even number of odd multiples of 8 per point, listed in strictly increasing order
+    of the base-3 number whose digit j is the magnitude index of byte j (so a byte transposition or
+    a dropped/duplicated row fails)."""
+    gs = _grid_s()
+    assert gs.shape == (1024, 8)
+    assert set(np.unique(gs)) == {8, 25, 43}
+    m = {8: 0, 25: 1, 43: 2}
+    keys = [sum(m[int(v)] * 3 ** j for j, v in enumerate(r)) for r in gs]
+    assert all(a < b for a, b in zip(keys, keys[1:]))
+    assert set(((gs // 8) % 2).sum(1) % 2) == {0}
+
+
 def test_grid_invariants():
     g2, g3 = _grids()
     assert g2.shape == (256, 8) and g3.shape == (256, 4)
@@ -67,10 +89,13 @@ def test_product_tables_match_oracle_tables():
     g2, g3 = _grids()
     txt = open(os.path.join(os.path.dirname(oracle.HERE), "lastengine_amd", "csrc", "le_iq_tables.h")).read()
     w2 = [int(v, 16) for v in re.findall(r"0x([0-9a-f]{8})u", txt.split("LE_IQ3XXS_GRID_WORDS")[0])]
-    w3 = [int(v, 16) for v in re.findall(r"0x([0-9a-f]{8})u", txt.split("LE_IQ3XXS_GRID_WORDS")[1])]
+    w3 = [int(v, 16) for v in re.findall(r"0x([0-9a-f]{8})u",
+                                         txt.split("LE_IQ3XXS_GRID_WORDS")[1].split("LE_IQ2S_GRID_WORDS")[0])]
+    ws = [int(v, 16) for v in re.findall(r"0x([0-9a-f]{8})u", txt.split("LE_IQ2S_GRID_WORDS")[1])]
     b2 = np.array(w2, dtype=np.uint32).view(np.uint8).reshape(256, 8)
     b3 = np.array(w3, dtype=np.uint32).view(np.uint8).reshape(256, 4)
-    assert np.array_equal(b2, g2) and np.array_equal(b3, g3)
+    bs = np.array(ws, dtype=np.uint32).view(np.uint8).reshape(1024, 8)
+    assert np.array_equal(b2, g2) and np.array_equal(b3, g3) and np.array_equal(bs, _grid_s())
 
 
 # ---------------------------------------------------------------- closed forms
