@@ -253,25 +253,62 @@ def bench_stream_read(eng, size, steps, warmup):
             "load_form": best[1]}
 
 
-def probe(eng, ty, rows, cols, launches=100, copy_bytes=256 << 20):
-    """Workload for rocprofv3 --pmc passes: `launches` eager headline matvecs over rotated weight
-    copies, then 10 copies of a `copy_bytes` buffer (torch's elementwise copy kernel) whose
-    FETCH_SIZE / WRITE_SIZE per dispatch calibrate the counters against known traffic."""
+PROBES = {
+    # name: (kind, type, rows, cols, tokens)
+    "headline": ("mv", "Q4_K", 14336, 4096, 1),
+    "config1": ("mv", "Q4_K", 4096, 4096, 1),
+    "q6k_down": ("mv", "Q6_K", 4096, 14336, 1),
+    "q8_0_head": ("mv", "Q8_0", 32000, 4096, 1),
+    "iq2xxs": ("mv", "IQ2_XXS", 14336, 4096, 1),
+    "iq3xxs": ("mv", "IQ3_XXS", 4096, 14336, 1),
+    "gemm_m64": ("gemm", "Q4_K", 14336, 4096, 64),
+    "gemm_m512": ("gemm", "Q4_K", 14336, 4096, 512),
+    "gemm_q6k_m512": ("gemm", "Q6_K", 4096, 14336, 512),
+    "moe_ntok1": ("moe", None, 0, 0, 1),
+    "moe_ntok8": ("moe", None, 0, 0, 8),
+}
+
+
+def probe(eng, name, launches=100, copy_bytes=256 << 20):
+    """Workload for rocprofv3 --pmc passes: `launches` eager launches of one workload of PROBES over
+    rotated weight copies, then 10 copies of a `copy_bytes` buffer (torch's elementwise copy kernel)
+    whose FETCH_SIZE / WRITE_SIZE per dispatch calibrate the counters against known traffic."""
     import torch
     import lastengine_amd as le
-    host = quantized(ty, rows, cols, 1)
-    bufs = device_copies(host)
-    x = torch.from_numpy(le.fill_normal(cols, 2)).cuda()
-    y = torch.empty(rows, dtype=torch.float32, device="cuda")
-    for i in range(launches):
-        eng.mv(ty, bufs[i % len(bufs)], x, y, rows, cols)
+    kind, tname, rows, cols, mtok = PROBES[name]
+    wbytes = 0
+    if kind == "moe":
+        n_exp, k, hidden, ff = 128, 8, 2048, 768
+        g = quantized(le.Q4_K, n_exp * ff, hidden, 201)
+        u = quantized(le.Q4_K, n_exp * ff, hidden, 202)
+        d = quantized(le.Q6_K, n_exp * hidden, ff, 203)
+        dg, du, dd = (torch.from_numpy(a).cuda() for a in (g, u, d))
+        lgs = [torch.from_numpy(le.fill_normal(mtok * n_exp, 300 + i)).cuda() for i in range(8)]
+        h = torch.from_numpy(le.fill_normal(mtok * hidden, 299)).cuda()
+        out = torch.empty(mtok * hidden, dtype=torch.float32, device="cuda")
+        ws = torch.zeros(eng.moe_workspace_size(mtok, k, ff), dtype=torch.uint8, device="cuda")
+        for i in range(launches):
+            eng.moe(le.Q4_K, le.Q4_K, le.Q6_K, dg, du, dd, n_exp, k, hidden, ff, lgs[i % 8], h, mtok, out, ws=ws)
+    else:
+        ty = le.TYPES[tname]
+        host = quantized(ty, rows, cols, 1)
+        wbytes = int(host.nbytes)
+        bufs = device_copies(host)
+        x = torch.from_numpy(le.fill_normal(mtok * cols, 2)).cuda()
+        y = torch.empty(mtok * rows, dtype=torch.float32, device="cuda")
+        if kind == "gemm":
+            ws = torch.empty(max(16, eng.gemm_workspace_size(ty, mtok, cols)), dtype=torch.uint8, device="cuda")
+        for i in range(launches):
+            if kind == "mv":
+                eng.mv(ty, bufs[i % len(bufs)], x, y, rows, cols)
+            else:
+                eng.gemm(ty, bufs[i % len(bufs)], x, mtok, y, rows, cols, ws=ws)
     src = torch.ones(copy_bytes // 4, dtype=torch.float32, device="cuda")
     dst = torch.empty_like(src)
     for _ in range(10):
         dst.copy_(src)
     torch.cuda.synchronize()
-    print(json.dumps({"probe": "done", "matvec_launches": launches, "copy_bytes": copy_bytes,
-                      "weight_bytes": int(host.nbytes)}))
+    print(json.dumps({"probe": name, "launches": launches, "copy_bytes": copy_bytes, "weight_bytes": wbytes}))
 
 
 def main():
@@ -281,8 +318,8 @@ def main():
     ap.add_argument("--warmup", type=int, default=200)
     ap.add_argument("--no-secondary", action="store_true")
     ap.add_argument("--no-cpu", action="store_true")
-    ap.add_argument("--probe", action="store_true",
-                    help="counter-pass workload: eager headline launches plus a 256 MiB copy kernel")
+    ap.add_argument("--probe", nargs="?", const="headline", choices=sorted(PROBES),
+                    help="counter-pass workload: eager launches of one workload plus a 256 MiB copy kernel")
     args = ap.parse_args()
     if args.gpus != 1:
         print("bench.py measures one GPU: this build has no multi-GPU path (each box has one GPU); "
@@ -298,7 +335,7 @@ def main():
 
     rows, cols = 14336, 4096
     if args.probe:
-        probe(eng, le.Q4_K, rows, cols)
+        probe(eng, args.probe)
         return
     head, host = bench_matvec(eng, le.Q4_K, rows, cols, args.steps, args.warmup)
     log("headline Q4_K %dx%d: %.3f us, %.1f GB/s" % (rows, cols, head["us"], head["gbs"]))

@@ -911,7 +911,7 @@ int le_mm_grouped(le_ctx *c, int ty, const void *const *ptrs, const void *w, con
     if (npair == 0) return LE_OK;
     static const int cfgs[6][4] = {{1, 4, 1, 2}, {1, 4, 2, 2}, {1, 4, 4, 2}, {2, 2, 2, 2}, {1, 8, 2, 1}, {1, 8, 4, 1}};
     int ci = mmg_cfg(nslot, npair);
-    const int srec = gq_srec(ty), nsb = cols / 256;
+    const int srec = gq_srec(ty);
     auto lds_of = [&](int i) {
         const int BM = 32 * cfgs[i][0] * cfgs[i][2], BN = 32 * cfgs[i][1] * cfgs[i][3];
         return (size_t)2 * (BN * gq_slot(ty) + BM * 256) + (size_t)2 * (BM / 32) * srec + gq_tab(ty);
