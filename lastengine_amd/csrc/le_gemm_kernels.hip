@@ -50,16 +50,6 @@ struct GmArgs {
 };
 
 
-/* Diagnostic builds (-DLE_TRACE) accumulate per-phase s_memrealtime deltas in registers and write
- * them per block to le_gm_trace[block * 8 + i]; compiled out otherwise. */
-#if defined(LE_TRACE)
-__device__ unsigned long long le_gm_trace[1 << 16];
-#define GM_T(v) unsigned long long v = __builtin_amdgcn_s_memrealtime()
-#define GM_ADD(i, a, b) tr[i] += (b) - (a)
-#else
-#define GM_T(v) do { } while (0)
-#define GM_ADD(i, a, b) do { } while (0)
-#endif
 
 __device__ __forceinline__ void gm_barrier() {
     __asm__ volatile("" ::: "memory");
@@ -277,10 +267,6 @@ __device__ __forceinline__ void gm_q4k_body(const GmArgs &a, const u8 *ws) {
 #pragma unroll
     for (int k = 0; k < TN; k++) brow[k] = 32 * (wave * TN + k) + r32;
 
-#if defined(LE_TRACE)
-    unsigned long long tr[8] = {};
-#endif
-    GM_T(t_start);
     if (producer) {
         constexpr int PD = SPLIT ? 2 : GM_PD; /* the two-half form has no registers to spare */
         /* a ring of PD register sets: while the consumers work on step s, the loads of steps
@@ -297,16 +283,9 @@ __device__ __forceinline__ void gm_q4k_body(const GmArgs &a, const u8 *ws) {
         for (; s + PD <= nstep; s += PD) {
 #pragma unroll
             for (int u = 0; u < PD; u++) {
-                GM_T(pa);
                 gm_barrier(); /* step s+u is staged; the consumers are done with step s+u-1's buffer */
-                GM_T(pb);
                 if (s + u + 1 < nstep) stage(s + u + 1, R[(u + 1) % PD]);
-                GM_T(pc);
                 issue(s + u + PD, R[u]);
-                GM_T(pd);
-                GM_ADD(0, pa, pb);
-                GM_ADD(1, pb, pc);
-                GM_ADD(2, pc, pd);
             }
         }
 #pragma unroll
@@ -315,12 +294,6 @@ __device__ __forceinline__ void gm_q4k_body(const GmArgs &a, const u8 *ws) {
             gm_barrier();
             if (s + u + 1 < nstep) stage(s + u + 1, R[(u + 1) % PD]);
         }
-#if defined(LE_TRACE)
-        GM_T(pe);
-        tr[5] = pe - t_start;
-        if (tid == 256)
-            for (int i = 0; i < 8; i++) le_gm_trace[(1 << 15) + ((size_t)blockIdx.y * gridDim.x + blockIdx.x) * 8 + i] = tr[i];
-#endif
         return;
     }
     Set R0;
@@ -333,10 +306,7 @@ __device__ __forceinline__ void gm_q4k_body(const GmArgs &a, const u8 *ws) {
 #pragma unroll
         for (int h = 0; h < 2; h++) {
             const int s = 2 * sb + h;
-            GM_T(ta);
             gm_barrier(); /* step s is staged; every wave is done with step s-1's buffer */
-            GM_T(tb);
-            GM_ADD(0, ta, tb);
             const u8 *B = lds + h * L::BUF; /* s & 1 == h */
             const _Float16 *Ah = (const _Float16 *)(B + L::AH_OFF), *Al = (const _Float16 *)(B + L::AL_OFF);
 #pragma unroll
@@ -385,10 +355,7 @@ __device__ __forceinline__ void gm_q4k_body(const GmArgs &a, const u8 *ws) {
                     if (s + 2 < nstep) issue(s + 2, R0);
                 }
             }
-            GM_T(tc);
-            GM_ADD(1, tb, tc);
         }
-        GM_T(td0);
         /* super-block epilogue: Y += d * D1 - dmin * D2, D2 = sum_j m_j S_j by one more MFMA per
          * tile (K slice 0: high halves of S_0..7, slice 1: low halves, both against m); all D2
          * MFMAs are issued before their results are read */
@@ -416,10 +383,7 @@ __device__ __forceinline__ void gm_q4k_body(const GmArgs &a, const u8 *ws) {
                     }
             }
         }
-        GM_T(td);
-        GM_ADD(2, td0, td);
     }
-    GM_T(t_end);
     /* D lane l element e: token 8*(e/4) + 4*(l/32) + e%4 of the tile, weight row l%32 */
 #pragma unroll
     for (int i = 0; i < TM; i++)
@@ -437,15 +401,6 @@ __device__ __forceinline__ void gm_q4k_body(const GmArgs &a, const u8 *ws) {
                 }
             }
         }
-#if defined(LE_TRACE)
-    GM_T(t_st);
-    tr[3] = t_st - t_end;
-    tr[5] = t_st - t_start;
-    tr[6] = t_start;
-    tr[7] = t_st;
-    if (tid == 0)
-        for (int i = 0; i < 8; i++) le_gm_trace[((size_t)blockIdx.y * gridDim.x + blockIdx.x) * 8 + i] = tr[i];
-#endif
 }
 
 /* ===================== few tokens (M <= 8): the matvec's weight stream on f16 MFMAs =====================
