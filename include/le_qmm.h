@@ -22,7 +22,10 @@
  *     32-value activation block is held as a 15-bit integer split into two int8 planes with an
  *     fp32 scale (error <= 3.1e-5 of the block maximum per value); weight codes are exact.
  *
- * Supported types (GGML ids, src/quant.rs:13-20): Q8_0=8, Q4_K=12, Q6_K=14, IQ2_XXS=16, IQ3_XXS=18.
+ * Supported types (GGML ids, src/quant.rs:13-20): Q8_0=8, Q4_K=12, Q6_K=14, IQ2_XXS=16, IQ3_XXS=18 on
+ * every entry point; Q4_0=2, Q3_K=11, Q5_K=13 and IQ2_S=22 (src/quant.rs:64-67,83-95,113-126,155-167,
+ * the reference's matvec_2/_11/_13/_22, src/cuda/kernels.cu:391) on le_dequant_rows, le_matvec,
+ * le_matvec_q8 and le_gemm (vector-ALU kernels; LE_ERR_TYPE from the MoE and grouped entries).
  */
 #ifndef LE_QMM_H
 #define LE_QMM_H
@@ -37,7 +40,10 @@ extern "C" {
 typedef struct le_ctx le_ctx;
 typedef void *le_stream_t; /* hipStream_t */
 
-enum le_type { LE_Q8_0 = 8, LE_Q4_K = 12, LE_Q6_K = 14, LE_IQ2_XXS = 16, LE_IQ3_XXS = 18 };
+enum le_type {
+    LE_Q4_0 = 2, LE_Q8_0 = 8, LE_Q3_K = 11, LE_Q4_K = 12, LE_Q5_K = 13, LE_Q6_K = 14, LE_IQ2_XXS = 16, LE_IQ3_XXS = 18,
+    LE_IQ2_S = 22
+};
 
 enum le_status {
     LE_OK = 0,
@@ -108,11 +114,28 @@ int le_dequant_rows(le_ctx *ctx, int ty, const void *w, float *out, int rows, in
 int le_matvec(le_ctx *ctx, int ty, const void *const *ptrs, const void *w, const float *x, long long xstride,
               float *y, int rows, int cols, int slots, le_stream_t stream);
 
+/* ---- int8 activation mode: the reference's own GPU numerics (optional; not the fp32-parity path) ----
+ * le_quant_x replaces quant_x (src/cuda/kernels.cu:15-25) as launched by Gpu::qx (src/gpu.rs:223-226):
+ * for u < n_units, xd[u] = max|x[32u..32u+31]| / 127, xq[32u+l] = x[32u+l] * (1 / xd[u]) rounded to
+ * nearest even (0 when xd[u] = 0), xs[u] = sum of the unit's xq.
+ * le_matvec_q8 replaces matvec_<ty> on those activations (src/cuda/kernels.cu:371-392, udot<ty>
+ * :36-110; Gpu::mv_ptrs src/gpu.rs:228-237): for slot s < slots, y[s * rows + r] = sum over units u
+ * of W_s[r, unit u] . (xd[u'] * xq[32u' ..]) with u' = s * xstride / 32 + u, i.e. the reference's
+ * exact integer dot per 32-value unit times its scales, summed in fp32. xq/xd/xs of slot s start
+ * at s * xstride values (xstride % 32 == 0; 0 shares one vector); xq 8-byte aligned. xs is
+ * accepted for the reference's signature and may be NULL (the kernels form the sums from xq).
+ * Per value the activation error is up to xd / 2 (about 4e-3 relative at K = 4096, as on the
+ * reference's GPU path), so results differ from cpu_ref by more than le_matvec's. */
+int le_quant_x(le_ctx *ctx, const float *x, int8_t *xq, float *xd, int32_t *xs, int n_units, le_stream_t stream);
+int le_matvec_q8(le_ctx *ctx, int ty, const void *const *ptrs, const void *w, const int8_t *xq, const float *xd,
+                 const int32_t *xs, long long xstride, float *y, int rows, int cols, int slots, le_stream_t stream);
+
 /* ---- small-M GEMM for speculative verify / prefill (replaces mmq*_<ty> / mmq128r_<ty> + DenseGpu::bmm,
  *      src/cuda/kernels.cu:965-1235, src/gpu/dense.rs:181-199; CPU twin cpu_ref::matmat,
  *      src/cpu_ref.rs:266-276) ----
  * Y[t * rows + r] = W[r,:] . X[t * cols ...] for t < m. ws: device workspace of
- * le_gemm_workspace_size(ty, m, cols) bytes (may be 0 bytes / NULL when that size is 0), the
+ * le_gemm_workspace_size(ty, m, cols) bytes (may be 0 bytes / NULL when that size is 0, as it is for
+ * Q4_0, Q3_K, Q5_K and IQ2_S, which run on the vector multi-token kernels at every M), the
  * counterpart of the reference's pre-quantized activation buffers (xqb/xdb/xsb, src/gpu.rs:210).
  * Every type runs on the matrix cores from 17 tokens (Q4_K: 3..16 tokens on a staged f16 MFMA
  * kernel, 2 on the staged int8 matvec; other types: from "gq_min_m" = 9 tokens, vector kernels

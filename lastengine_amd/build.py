@@ -20,7 +20,7 @@ HIPCC = os.environ.get("HIPCC", ROCM + "/bin/hipcc")
 DEVICE_FLAGS = ["--offload-arch=gfx950", "-O3", "-std=c++17", "-Xclang", "-target-feature", "-Xclang",
                 "-packed-fp32-ops", "-I" + CSRC]
 PARTS = {"deq": ["-DLE_PART_DEQ"], "moe": ["-DLE_PART_MOE"]}
-for _ty in (8, 12, 14, 16, 18):
+for _ty in (2, 8, 11, 12, 13, 14, 16, 18, 22):
     PARTS["mv%d" % _ty] = ["-DLE_PART_MV=%d" % _ty]
 PARTS["gm"] = []
 PARTS["gq"] = []

@@ -23,7 +23,7 @@
 namespace {
 
 const char *kParts[] = {"le_qmm_deq", "le_qmm_moe", "le_qmm_mv8", "le_qmm_mv12", "le_qmm_mv14", "le_qmm_mv16", "le_qmm_mv18", "le_qmm_gm",
-                        "le_qmm_gq"};
+                        "le_qmm_gq", "le_qmm_mv2", "le_qmm_mv11", "le_qmm_mv13", "le_qmm_mv22"};
 
 /* Kernel argument block of le_mv_* (mirrors MvArgs in le_qmm_kernels.hip). */
 struct MvArgs {
@@ -35,6 +35,8 @@ struct MvArgs {
     float *y;
     long long y_slot, y_tok;
     int rows, cols, ntok, pad;
+    const int8_t *xq8;
+    const float *xd8;
 };
 
 int xtok_bytes(int K) { return (K / 8) * 24; }
@@ -62,6 +64,7 @@ std::atomic<unsigned long long> g_moe_epoch{0};
 int table_bytes(int ty) {
     if (ty == LE_TYPE_IQ2_XXS) return 4 * (256 + 512);
     if (ty == LE_TYPE_IQ3_XXS) return 4 * (256 + 256);
+    if (ty == LE_TYPE_IQ2_S) return 4 * (256 + 2048);
     return 0;
 }
 
@@ -165,9 +168,15 @@ struct le_ctx {
 
 namespace {
 
+/* The five types of every entry point (matrix-core GEMM, MoE, grouped matmul). */
 bool supported(int ty) {
     return ty == LE_TYPE_Q8_0 || ty == LE_TYPE_Q4_K || ty == LE_TYPE_Q6_K || ty == LE_TYPE_IQ2_XXS ||
            ty == LE_TYPE_IQ3_XXS;
+}
+/* ... plus Q4_0, Q3_K, Q5_K and IQ2_S, which dequant, matvec and le_gemm (on the vector-ALU
+ * multi-token kernels) accept. */
+bool supported_mv(int ty) {
+    return supported(ty) || ty == LE_TYPE_Q4_0 || ty == LE_TYPE_Q3_K || ty == LE_TYPE_Q5_K || ty == LE_TYPE_IQ2_S;
 }
 int sb_bytes(int ty) {
     switch (ty) {
@@ -176,6 +185,10 @@ int sb_bytes(int ty) {
     case LE_TYPE_Q6_K: return LE_SB_BYTES_Q6_K;
     case LE_TYPE_IQ2_XXS: return LE_SB_BYTES_IQ2_XXS;
     case LE_TYPE_IQ3_XXS: return LE_SB_BYTES_IQ3_XXS;
+    case LE_TYPE_Q4_0: return LE_SB_BYTES_Q4_0;
+    case LE_TYPE_Q3_K: return LE_SB_BYTES_Q3_K;
+    case LE_TYPE_Q5_K: return LE_SB_BYTES_Q5_K;
+    case LE_TYPE_IQ2_S: return LE_SB_BYTES_IQ2_S;
     }
     return 0;
 }
@@ -295,20 +308,28 @@ int ms_t_launch(le_ctx *c, const void *const *ptrs, const void *w, const float *
 /* Matvec/matmul launcher: T tokens per pass, grid (workers, slots, ceil(ntok/T)). */
 int mv_launch(le_ctx *c, int ty, const void *const *ptrs, const void *w, const float *x, long long x_slot,
               long long x_tok, float *y, long long y_slot, long long y_tok, int rows, int cols, int ntok, int slots,
-              hipStream_t st) {
-    if (!supported(ty)) return c->fail(LE_ERR_TYPE, "no kernel for type %d", ty);
+              hipStream_t st,
+              const int8_t *xq8 = nullptr, const float *xd8 = nullptr) {
+    if (!supported_mv(ty)) return c->fail(LE_ERR_TYPE, "no kernel for type %d", ty);
     if (rows <= 0 || cols <= 0 || ntok <= 0 || slots <= 0) return c->fail(LE_ERR_SHAPE, "empty shape");
     if (cols % 256) return c->fail(LE_ERR_SHAPE, "cols=%d is not a multiple of 256", cols);
-    if (!x || !y || (!ptrs && !w)) return c->fail(LE_ERR_ARG, "null pointer");
-    if (!al16(x) || (x_slot % 4) || (x_tok % 4)) return c->fail(LE_ERR_ALIGN, "activations must be 16-byte aligned");
+    const bool q8 = xq8 != nullptr;
+    if (q8) {
+        if (!xd8 || !y || (!ptrs && !w)) return c->fail(LE_ERR_ARG, "null pointer");
+        if (((uintptr_t)xq8 & 7) || ((uintptr_t)xd8 & 3) || (x_slot % 32) || ntok != 1)
+            return c->fail(LE_ERR_ALIGN, "xq must be 8-byte aligned and xstride a multiple of 32");
+    } else {
+        if (!x || !y || (!ptrs && !w)) return c->fail(LE_ERR_ARG, "null pointer");
+        if (!al16(x) || (x_slot % 4) || (x_tok % 4)) return c->fail(LE_ERR_ALIGN, "activations must be 16-byte aligned");
+    }
     const int nsb = cols / 256, G = pick_g(nsb), S = nsb / G;
     const bool iq = ty == LE_TYPE_IQ2_XXS || ty == LE_TYPE_IQ3_XXS;
-    if ((ty == LE_TYPE_Q4_K || (ty == LE_TYPE_Q6_K && c->mq6) || (iq && c->mqiq)) && ntok == 1 && c->mq &&
+    if (!q8 && (ty == LE_TYPE_Q4_K || (ty == LE_TYPE_Q6_K && c->mq6) || (iq && c->mqiq)) && ntok == 1 && c->mq &&
         (size_t)nsb * 608 + 1024 <= c->lds_limit) {
         const int rc = mq_launch(c, ty, ptrs, w, x, x_slot, y, y_slot, rows, cols, slots, st);
         if (rc != 1) return rc;
     }
-    if (ty == LE_TYPE_Q4_K && ntok >= 2 && c->mq && c->ms && c->ms_t) {
+    if (!q8 && ty == LE_TYPE_Q4_K && ntok >= 2 && c->mq && c->ms && c->ms_t) {
         const int rc = ms_t_launch(c, ptrs, w, x, x_slot, x_tok, y, y_slot, y_tok, rows, cols, ntok, slots, st);
         if (rc != 1) return rc;
     }
@@ -348,7 +369,9 @@ int mv_launch(le_ctx *c, int ty, const void *const *ptrs, const void *w, const f
     a.ntok = ntok;
     void *args[] = {&a};
     char name[96];
-    snprintf(name, sizeof name, "le_mv_%d_g%d_t%d_r%d_c%d_b%d", ty, G, T, RW, CH, block);
+    a.xq8 = xq8;
+    a.xd8 = xd8;
+    snprintf(name, sizeof name, "le_mv_%d_g%d_t%d_r%d_c%d_b%d%s", ty, G, T, RW, CH, block, q8 ? "_q8" : "");
     return c->launch(name, dim3((unsigned)gx, (unsigned)slots, (unsigned)((ntok + T - 1) / T)), block,
                      (size_t)(T * xb + tb), st, args);
 }
@@ -552,7 +575,7 @@ int le_set_option(le_ctx *c, const char *name, int value) {
 
 int le_dequant_rows(le_ctx *c, int ty, const void *w, float *out, int rows, int cols, le_stream_t stream) {
     if (!c) return LE_ERR_ARG;
-    if (!supported(ty)) return c->fail(LE_ERR_TYPE, "no kernel for type %d", ty);
+    if (!supported_mv(ty)) return c->fail(LE_ERR_TYPE, "no kernel for type %d", ty);
     if (!w || !out) return c->fail(LE_ERR_ARG, "null pointer");
     int v = 1, b = 0;
     le_block_geometry(ty, &v, &b);
@@ -572,6 +595,24 @@ int le_matvec(le_ctx *c, int ty, const void *const *ptrs, const void *w, const f
               int rows, int cols, int slots, le_stream_t stream) {
     if (!c) return LE_ERR_ARG;
     return mv_launch(c, ty, ptrs, w, x, xstride, 0, y, (long long)rows, 0, rows, cols, 1, slots, (hipStream_t)stream);
+}
+
+int le_quant_x(le_ctx *c, const float *x, int8_t *xq, float *xd, int32_t *xs, int n_units, le_stream_t stream) {
+    if (!c) return LE_ERR_ARG;
+    if (!x || !xq || !xd || !xs) return c->fail(LE_ERR_ARG, "null pointer");
+    if (n_units <= 0) return c->fail(LE_ERR_SHAPE, "n_units must be positive");
+    const unsigned blocks = (unsigned)((n_units + 7) / 8);
+    void *args[] = {(void *)&x, (void *)&xq, (void *)&xd, (void *)&xs, (void *)&n_units};
+    return c->launch("le_quant_x", dim3(blocks), 256, 0, (hipStream_t)stream, args);
+}
+
+int le_matvec_q8(le_ctx *c, int ty, const void *const *ptrs, const void *w, const int8_t *xq, const float *xd,
+                 const int32_t *xs, long long xstride, float *y, int rows, int cols, int slots, le_stream_t stream) {
+    (void)xs; /* the kernels form the group sums they need from xq */
+    if (!c) return LE_ERR_ARG;
+    if (!xq) return c->fail(LE_ERR_ARG, "null pointer");
+    return mv_launch(c, ty, ptrs, w, nullptr, xstride, 0, y, (long long)rows, 0, rows, cols, 1, slots, (hipStream_t)stream,
+                     xq, xd);
 }
 
 size_t le_moe_workspace_size(int n_tok, int k, int ff) {
@@ -960,12 +1001,12 @@ size_t le_gemm_workspace_size(int ty, int m, int cols) {
 int le_gemm(le_ctx *c, int ty, const void *w, const float *x, int m, float *y, int rows, int cols, void *ws,
             size_t ws_bytes, le_stream_t stream) {
     if (!c) return LE_ERR_ARG;
-    if (!supported(ty)) return c->fail(LE_ERR_TYPE, "no kernel for type %d", ty);
+    if (!supported_mv(ty)) return c->fail(LE_ERR_TYPE, "no kernel for type %d", ty);
     /* Q4_K, 3..16 tokens: the staged f16 kernel (2 tokens: the int8 multi-token matvec is faster);
      * shapes whose activations do not fit its LDS, and gm_split=1 (two fp16 halves, which only
      * the le_gm GEMM carries), go to a GEMM */
     const bool few = ty == LE_TYPE_Q4_K && c->gm_mh && !c->gm_split && m >= 3 && m <= c->gm_mh_max;
-    const bool gemm = ty == LE_TYPE_Q4_K ? (m >= c->gm_min_m || few) : m >= c->gq_min_m;
+    const bool gemm = ty == LE_TYPE_Q4_K ? (m >= c->gm_min_m || few) : supported(ty) && m >= c->gq_min_m;
     if (gemm && m > 0 && rows > 0 && cols > 0 && cols % 256 == 0 && w && x && y) {
         if (!ws) return c->fail(LE_ERR_ARG, "null workspace");
         if (ws_bytes < le_gemm_workspace_size(ty, m, cols))

@@ -426,3 +426,207 @@ struct Fmt<LE_TYPE_IQ3_XXS> {
         d.mu[0] = 0.f;
     }
 };
+
+/* Byte masks of a 4-bit sign nibble: byte i is 0xFF where bit i is set (bit i moved to bit 8i by
+ * shifts that never overlap, then spread over the byte). */
+__device__ __forceinline__ u32 nib_mask(u32 n) { return ((n * 0x00204081u) & 0x01010101u) * 0xFFu; }
+
+/* ---------------- Q4_0 (8 blocks of 18 B = d f16 + 16 nibble bytes per 256 values, src/quant.rs:64-67).
+ * Lane li owns block li: low nibbles are values 0-15, high nibbles 16-31; q - 8 through mu = 8 d. */
+template <>
+struct Fmt<LE_TYPE_Q4_0> {
+    static constexpr int SB = LE_SB_BYTES_Q4_0;
+    static constexpr bool HAS_MU = true;
+    static constexpr bool TABLES = false;
+    static constexpr int NSEG = 1, WPS = 8, XL = XL_ROW;
+    struct Raw {
+        uint4 q;
+        u32 d;
+    };
+    __device__ static __forceinline__ Raw load(const u8 *p, int li) {
+        const u8 *bp = p + 18 * li;
+        Raw r;
+        r.d = ldg2(bp);
+        r.q = ldg16u(bp + 2);
+        return r;
+    }
+    __device__ static __forceinline__ void decode(const Raw &r, int li, int sb, const u32 *, Dec<NSEG, WPS> &d) {
+        const u32 q[4] = {r.q.x, r.q.y, r.q.z, r.q.w};
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            d.w[i] = q[i] & 0x0F0F0F0Fu;
+            d.w[4 + i] = (q[i] >> 4) & 0x0F0F0F0Fu;
+        }
+        d.sig[0] = h2f(r.d);
+        d.mu[0] = 8.0f * d.sig[0];
+    }
+};
+
+/* ---------------- Q5_K: 176 B = d, dmin, 12 B scales/mins (as Q4_K), qh[32], qs[128]
+ * (src/quant.rs:83-95). Lane li as Q4_K (pair g = li>>1, half hh = li&1); the fifth bit of value
+ * 64g + l (l < 32) is bit 2g of qh[l], of value 64g + 32 + l bit 2g+1. */
+template <>
+struct Fmt<LE_TYPE_Q5_K> {
+    static constexpr int SB = LE_SB_BYTES_Q5_K;
+    static constexpr bool HAS_MU = true;
+    static constexpr bool TABLES = false;
+    static constexpr int NSEG = 2, WPS = 4, XL = XL_Q4K;
+    struct Raw {
+        uint4 h, q, qh;
+    };
+    __device__ static __forceinline__ Raw load(const u8 *p, int li) {
+        Raw r;
+        r.h = ldg16c(p);
+        r.qh = ldg16c(p + 16 + 16 * (li & 1));
+        r.q = ldg16(p + 48 + 16 * li);
+        return r;
+    }
+    __device__ static __forceinline__ void decode(const Raw &r, int li, int sb, const u32 *, Dec<NSEG, WPS> &d) {
+        const int g = li >> 1;
+        const u32 q[4] = {r.q.x, r.q.y, r.q.z, r.q.w}, h[4] = {r.qh.x, r.qh.y, r.qh.z, r.qh.w};
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            d.w[i] = (q[i] & 0x0F0F0F0Fu) | (((h[i] >> (2 * g)) & 0x01010101u) << 4);
+            d.w[4 + i] = ((q[i] >> 4) & 0x0F0F0F0Fu) | (((h[i] >> (2 * g + 1)) & 0x01010101u) << 4);
+        }
+        const int sh8 = 8 * (li & 3);
+        const u32 a = r.h.y >> sh8, b = r.h.z >> sh8, c = r.h.w >> sh8;
+        const u32 sc = li < 4 ? (a & 63u) : ((c & 15u) | ((a >> 2) & 0x30u));
+        const u32 mn = li < 4 ? (b & 63u) : (((c >> 4) & 15u) | ((b >> 2) & 0x30u));
+        const float sj = h2f(r.h.x & 0xFFFFu) * (float)sc, mj = h2f(r.h.x >> 16) * (float)mn;
+        d.sig[0] = dpp_f<0xA0>(sj);
+        d.sig[1] = dpp_f<0xF5>(sj);
+        d.mu[0] = dpp_f<0xA0>(mj);
+        d.mu[1] = dpp_f<0xF5>(mj);
+    }
+};
+
+/* ---------------- Q3_K: 110 B = hmask[32], qs[64], 12 B of 6-bit scales, d f16 (src/quant.rs:113-126).
+ * Lane li: half c = li>>2 (128 values), l-range [8t, 8t+8) with t = li&3, four quadrants s (the Q6_K
+ * lane split). Value 128c + 32s + l has the 2-bit code (qs[32c+l] >> 2s) & 3 and high bit
+ * (hmask[l] >> (4c+s)) & 1; the code u = q2 | 4h is used unsigned and the -4 goes into mu = 4 sig.
+ * Scale i (one per 16 values, stored + 32): low nibble from byte i (i < 8) or the high nibble of
+ * byte i-8, top two bits at 2(i>>2) of byte 8 + (i&3). */
+template <>
+struct Fmt<LE_TYPE_Q3_K> {
+    static constexpr int SB = LE_SB_BYTES_Q3_K;
+    static constexpr bool HAS_MU = true;
+    static constexpr bool TABLES = false;
+    static constexpr int NSEG = 4, WPS = 2, XL = XL_Q6K;
+    struct Raw {
+        uint2 hm, qs, sa;
+        u32 sb4, d;
+    };
+    __device__ static __forceinline__ Raw load(const u8 *p, int li) {
+        const int c = li >> 2, t = li & 3;
+        Raw r;
+        r.hm = ldg8u(p + 8 * t);
+        r.qs = ldg8u(p + 32 + 32 * c + 8 * t);
+        r.sa = ldg8u(p + 96);
+        r.sb4 = ldg4u(p + 104);
+        r.d = ldg2(p + 108);
+        return r;
+    }
+    __device__ static __forceinline__ void decode(const Raw &r, int li, int sb, const u32 *, Dec<NSEG, WPS> &d) {
+        const int c = li >> 2, t = li & 3;
+        const u32 hm[2] = {r.hm.x, r.hm.y}, qs[2] = {r.qs.x, r.qs.y};
+#pragma unroll
+        for (int s = 0; s < 4; s++)
+#pragma unroll
+            for (int k = 0; k < 2; k++)
+                d.w[2 * s + k] = ((qs[k] >> (2 * s)) & 0x03030303u) | (((hm[k] >> (4 * c + s)) & 0x01010101u) << 2);
+        const float dd = h2f(r.d);
+#pragma unroll
+        for (int s = 0; s < 4; s++) {
+            const int i = 8 * c + 2 * s + (t >> 1);
+            const int lb = i & 7;
+            const u32 lw = lb < 4 ? r.sa.x : r.sa.y;
+            const u32 lo = ((lw >> (8 * (lb & 3))) >> (c ? 4 : 0)) & 15u;
+            const u32 hi = (r.sb4 >> (8 * (i & 3) + 2 * (i >> 2))) & 3u;
+            d.sig[s] = dd * (float)((int)(lo | (hi << 4)) - 32);
+            d.mu[s] = 4.0f * d.sig[s];
+        }
+    }
+};
+
+/* ---------------- IQ2_S: 82 B = d f16, qs[32], signs[32], qh[8], scales[8] (src/quant.rs:155-167).
+ * Lane li owns 32-value sub-block ib = li: grid index qs[4ib+l] | ((qh[ib] << (8-2l)) & 0x300) of
+ * the 1024-entry grid (LDS), an explicit sign byte per 8 values, the scale nibble of its first (low)
+ * and second (high) 16 values. */
+template <>
+struct Fmt<LE_TYPE_IQ2_S> {
+    static constexpr int SB = LE_SB_BYTES_IQ2_S;
+    static constexpr bool HAS_MU = false;
+    static constexpr bool TABLES = true;
+    static constexpr int GRID_WORDS = 2048;
+    static constexpr int NSEG = 2, WPS = 4, XL = XL_ROW;
+    struct Raw {
+        u32 qs, sn, qh2, sc2, d;
+    };
+    __device__ static __forceinline__ Raw load(const u8 *p, int li) {
+        Raw r;
+        r.d = ldg2(p);
+        r.qs = ldg4u(p + 2 + 4 * li);
+        r.sn = ldg4u(p + 34 + 4 * li);
+        r.qh2 = ldg2(p + 66 + (li & 6));
+        r.sc2 = ldg2(p + 74 + (li & 6));
+        return r;
+    }
+    __device__ static __forceinline__ void decode(const Raw &r, int li, int sb, const u32 *tab, Dec<NSEG, WPS> &d) {
+        const u32 *grid = tab + LE_TAB_GRID;
+        const u32 qh = (r.qh2 >> (8 * (li & 1))) & 255u, sc = (r.sc2 >> (8 * (li & 1))) & 255u;
+#pragma unroll
+        for (int l = 0; l < 4; l++) {
+            const u32 gi = ((r.qs >> (8 * l)) & 255u) | ((qh << (8 - 2 * l)) & 0x300u);
+            const u32 sg = (r.sn >> (8 * l)) & 255u;
+            const uint2 g = *(const uint2 *)(grid + 2 * gi);
+            d.w[2 * l] = apply_sign(g.x, nib_mask(sg & 15u));
+            d.w[2 * l + 1] = apply_sign(g.y, nib_mask(sg >> 4));
+        }
+        const float dd = h2f(r.d);
+        d.sig[0] = dd * (0.5f + (float)(sc & 15u)) * 0.25f;
+        d.sig[1] = dd * (0.5f + (float)(sc >> 4)) * 0.25f;
+        d.mu[0] = d.mu[1] = 0.f;
+    }
+};
+
+/* Activation image from the reference's int8 activations (quant_x output: xq per value, xd per 32
+ * values): the xl plane carries xq, the xh plane is zero, dx = xd, and the group sum is formed from
+ * xq. The vector kernels then compute exactly the reference's integer dot per unit times its
+ * scales (udot<ty>, src/cuda/kernels.cu:36-110). Same two-phase shape as XLoad. */
+__device__ __forceinline__ void le_q8_group(uint2 w, float d, uint4 *xq, float2 *xs, int p) {
+    int s = 0;
+#pragma unroll
+    for (int i = 0; i < 4; i++) s += (int)(int8_t)((w.x >> (8 * i)) & 255u) + (int)(int8_t)((w.y >> (8 * i)) & 255u);
+    xq[p] = make_uint4(0u, 0u, w.x, w.y);
+    xs[p] = make_float2(d, d * (float)s);
+}
+template <int BLOCK, int XR>
+struct XLoadQ8 {
+    uint2 w[XR];
+    float d[XR];
+    __device__ __forceinline__ void load(const int8_t *__restrict__ xq, const float *__restrict__ xd, int K) {
+        const int ng = K >> 3;
+#pragma unroll
+        for (int r = 0; r < XR; r++) {
+            const int p = min((int)threadIdx.x + r * BLOCK, ng - 1);
+            w[r] = *(const LE_GLOBAL uint2 *)(xq + 8 * p);
+            d[r] = *(const LE_GLOBAL float *)(xd + (p >> 2));
+        }
+    }
+    template <int XL>
+    __device__ __forceinline__ void store(int K, uint4 *xq, float2 *xs) {
+        const int ng = K >> 3;
+#pragma unroll
+        for (int r = 0; r < XR; r++) {
+            const int p = threadIdx.x + r * BLOCK;
+            if (p < ng) le_q8_group(w[r], d[r], xq, xs, le_xpos<XL>(p));
+        }
+    }
+};
+template <int XL>
+__device__ __forceinline__ void le_q8_x_lds(const int8_t *__restrict__ xqg, const float *__restrict__ xd, int K, uint4 *xq,
+                                            float2 *xs) {
+    for (int p = threadIdx.x; p < (K >> 3); p += blockDim.x)
+        le_q8_group(*(const LE_GLOBAL uint2 *)(xqg + 8 * p), xd[p >> 2], xq, xs, le_xpos<XL>(p));
+}

@@ -17,31 +17,10 @@
 #include "le_iq_tables.h"
 #include "le_qmm_device.h"
 
-/* Optional per-block timestamps for diagnostic builds (-DLE_TRACE): LE_TRACE_DECL at kernel
- * entry, LE_TRACE_POINT(i) keeps s_memrealtime in registers (no store between barriers, which
- * would make the next barrier wait for it), LE_TRACE_FLUSH writes slot i of block b to
- * le_trace_buf[b * 16 + i]. Compiled out otherwise. */
-#if defined(LE_TRACE)
-__device__ unsigned long long le_trace_buf[1 << 16];
-#define LE_TRACE_DECL unsigned long long le_tr_[16] = {}
-#define LE_TRACE_PARAM , unsigned long long *le_tr_
-#define LE_TRACE_ARG , le_tr_
-#define LE_TRACE_POINT(i) do { le_tr_[i] = __builtin_amdgcn_s_memrealtime(); } while (0)
-#define LE_TRACE_FLUSH                                                                                     \
-    do {                                                                                                   \
-        if (threadIdx.x == 0 && blockIdx.y == 0 && blockIdx.x < (1 << 12))                                 \
-            for (int i_ = 0; i_ < 16; i_++) le_trace_buf[blockIdx.x * 16 + i_] = le_tr_[i_];               \
-    } while (0)
-#else
-#define LE_TRACE_DECL do { } while (0)
-#define LE_TRACE_POINT(i) do { } while (0)
-#define LE_TRACE_FLUSH do { } while (0)
-#define LE_TRACE_PARAM
-#define LE_TRACE_ARG
-#endif
 
 __device__ const u32 le_iq2xxs_grid[512] = LE_IQ2XXS_GRID_WORDS;
 __device__ const u32 le_iq3xxs_grid[256] = LE_IQ3XXS_GRID_WORDS;
+__device__ const u32 le_iq2s_grid[2048] = LE_IQ2S_GRID_WORDS;
 
 /* ===================================================================================== */
 /* Bit-exact dequantization. One thread per 32-value unit; the arithmetic follows           */
@@ -135,6 +114,83 @@ __device__ void dequant_unit<LE_TYPE_IQ3_XXS>(const u8 *row, int unit, float *o)
     }
 }
 
+/* src/quant.rs:64-67: one 18-byte block per unit, q - 8 on 4-bit codes (low nibbles: values 0-15). */
+template <>
+__device__ void dequant_unit<LE_TYPE_Q4_0>(const u8 *row, int unit, float *o) {
+#pragma clang fp contract(off)
+    const u8 *b = row + (size_t)unit * 18;
+    const float d = f16_exact(b[0] | (b[1] << 8));
+    for (int l = 0; l < 16; l++) {
+        o[l] = d * ((float)(b[2 + l] & 15) - 8.0f);
+        o[l + 16] = d * ((float)(b[2 + l] >> 4) - 8.0f);
+    }
+}
+
+/* src/quant.rs:83-95: Q4_K's scales and nibbles plus a fifth bit per value in qh (bit j of qh[l]
+ * for value 32j + l). */
+template <>
+__device__ void dequant_unit<LE_TYPE_Q5_K>(const u8 *row, int unit, float *o) {
+#pragma clang fp contract(off)
+    const u8 *b = row + (size_t)(unit >> 3) * 176;
+    const int j = unit & 7, g = j >> 1;
+    const float d = f16_exact(b[0] | (b[1] << 8)), dmin = f16_exact(b[2] | (b[3] << 8));
+    const u8 *s = b + 4, *qh = b + 16, *qs = b + 48 + g * 32;
+    u32 sc, m;
+    if (j < 4) {
+        sc = s[j] & 63;
+        m = s[j + 4] & 63;
+    } else {
+        sc = (s[j + 4] & 15) | ((s[j - 4] >> 6) << 4);
+        m = (s[j + 4] >> 4) | ((s[j] >> 6) << 4);
+    }
+    for (int l = 0; l < 32; l++) {
+        const u32 q = ((j & 1) ? (qs[l] >> 4) : (qs[l] & 15)) + (((qh[l] >> j) & 1) ? 16u : 0u);
+        o[l] = d * (float)sc * (float)q - dmin * (float)m;
+    }
+}
+
+/* src/quant.rs:113-126: value e = 32j + l takes 2 bits at 2(j&3) of qs[32(j>>2) + l], minus 4 when
+ * bit j of hmask[l] is clear; 16 signed 6-bit scales, one per 16 values. */
+template <>
+__device__ void dequant_unit<LE_TYPE_Q3_K>(const u8 *row, int unit, float *o) {
+#pragma clang fp contract(off)
+    const u8 *b = row + (size_t)(unit >> 3) * 110;
+    const int j = unit & 7;
+    const u8 *hm = b, *qs = b + 32 + (j >> 2) * 32, *sc = b + 96;
+    const float d = f16_exact(b[108] | (b[109] << 8));
+    int scl[2];
+    for (int h = 0; h < 2; h++) {
+        const int i = 2 * j + h;
+        const int lo = i < 8 ? (sc[i] & 15) : (sc[i - 8] >> 4), hi = (sc[8 + (i & 3)] >> (2 * (i >> 2))) & 3;
+        scl[h] = (lo | (hi << 4)) - 32;
+    }
+    for (int l = 0; l < 32; l++) {
+        const int q = (int)((qs[l] >> (2 * (j & 3))) & 3) - (((hm[l] >> j) & 1) ? 0 : 4);
+        o[l] = d * (float)scl[l >> 4] * (float)q;
+    }
+}
+
+/* src/quant.rs:155-167: 10-bit grid index (qs byte, two bits of qh), an explicit sign byte per 8
+ * values, a 4-bit scale per 16 values. */
+template <>
+__device__ void dequant_unit<LE_TYPE_IQ2_S>(const u8 *row, int unit, float *o) {
+#pragma clang fp contract(off)
+    const u8 *b = row + (size_t)(unit >> 3) * 82;
+    const int ib = unit & 7;
+    const u8 *qs = b + 2 + ib * 4, *sn = b + 34 + ib * 4;
+    const u32 qh = b[66 + ib], scb = b[74 + ib];
+    const float d = f16_exact(b[0] | (b[1] << 8));
+    const float db[2] = {d * (0.5f + (float)(scb & 15)) * 0.25f, d * (0.5f + (float)(scb >> 4)) * 0.25f};
+    for (int l = 0; l < 4; l++) {
+        const u32 gi = qs[l] | ((qh << (8 - 2 * l)) & 0x300u);
+        const u32 g0 = le_iq2s_grid[2 * gi], g1 = le_iq2s_grid[2 * gi + 1];
+        for (int jj = 0; jj < 8; jj++) {
+            const u32 gv = ((jj < 4 ? g0 : g1) >> (8 * (jj & 3))) & 255u;
+            o[l * 8 + jj] = db[l >> 1] * (float)gv * (((sn[l] >> jj) & 1) ? -1.0f : 1.0f);
+        }
+    }
+}
+
 /* out[r*cols + c] for rows x cols; unit index over the whole matrix. */
 template <int TY>
 __device__ void dequant_rows(const u8 *__restrict__ w, float *__restrict__ out, int rows, int cols, size_t row_bytes) {
@@ -151,11 +207,38 @@ __device__ void dequant_rows(const u8 *__restrict__ w, float *__restrict__ out, 
 }
 
 #if defined(LE_PART_DEQ)
+/* quant_x (src/cuda/kernels.cu:15-25): per 32 values d = amax / 127, q = x * (1 / d) rounded to
+ * nearest even (d = 0: q = 0), xs = sum q. 32 lanes per unit, two units per wave. */
+extern "C" __global__ void __launch_bounds__(256) le_quant_x(const float *x, int8_t *xq, float *xd, int *xs, int n_units) {
+    const long long u = (long long)blockIdx.x * 8 + (threadIdx.x >> 5);
+    const int l = threadIdx.x & 31;
+    const bool ok = u < n_units;
+    const float v = ok ? x[u * 32 + l] : 0.f;
+    float am = fabsf(v);
+#pragma unroll
+    for (int o = 16; o; o >>= 1) am = fmaxf(am, __shfl_xor(am, o, 32));
+    const float d = am / 127.0f, id = d > 0.f ? 1.0f / d : 0.f;
+    const int q = (int)rintf(v * id);
+    int s = q;
+#pragma unroll
+    for (int o = 16; o; o >>= 1) s += __shfl_xor(s, o, 32);
+    if (ok) {
+        xq[u * 32 + l] = (int8_t)q;
+        if (l == 0) {
+            xd[u] = d;
+            xs[u] = s;
+        }
+    }
+}
 #define LE_DEQ(TY, NAME)                                                                                   \
     extern "C" __global__ void __launch_bounds__(256) NAME(const u8 *w, float *out, int rows, int cols,     \
                                                           unsigned long long row_bytes) {                  \
         dequant_rows<TY>(w, out, rows, cols, (size_t)row_bytes);                                           \
     }
+LE_DEQ(LE_TYPE_Q4_0, le_dequant_2)
+LE_DEQ(LE_TYPE_Q3_K, le_dequant_11)
+LE_DEQ(LE_TYPE_Q5_K, le_dequant_13)
+LE_DEQ(LE_TYPE_IQ2_S, le_dequant_22)
 LE_DEQ(LE_TYPE_Q8_0, le_dequant_8)
 LE_DEQ(LE_TYPE_Q4_K, le_dequant_12)
 LE_DEQ(LE_TYPE_Q6_K, le_dequant_14)
@@ -209,6 +292,9 @@ struct MvArgs {
     float *y;
     long long y_slot, y_tok;
     int rows, cols, ntok, pad;
+    /* int8 activation mode (le_matvec_q8): xq8 + s * x_slot values, xd8 + s * x_slot / 32 scales */
+    const int8_t *xq8;
+    const float *xd8;
 };
 
 template <int TY>
@@ -225,7 +311,7 @@ __device__ __forceinline__ void load_tables(u32 *tab) {
             tab[LE_TAB_SIGN + 2 * i] = m0;
             tab[LE_TAB_SIGN + 2 * i + 1] = m1;
         }
-        const u32 *src = TY == LE_TYPE_IQ2_XXS ? le_iq2xxs_grid : le_iq3xxs_grid;
+        const u32 *src = TY == LE_TYPE_IQ2_XXS ? le_iq2xxs_grid : TY == LE_TYPE_IQ3_XXS ? le_iq3xxs_grid : le_iq2s_grid;
         for (int i = threadIdx.x; i < Fmt<TY>::GRID_WORDS; i += blockDim.x) tab[LE_TAB_GRID + i] = src[i];
     }
 }
@@ -272,7 +358,7 @@ __device__ __forceinline__ void rows_dot(const Dec<NSEG, WPS> (&d)[RW], const XT
  * row) and walks them in steps of CH super-blocks per lane and row. Steps are double-buffered:
  * the loads of step n+1 are in flight while step n is decoded and multiplied, and the first
  * step's loads are issued before the activation prologue so HBM latency overlaps it. */
-template <int TY, int G, int T, int RW, int CH, int BLOCK>
+template <int TY, int G, int T, int RW, int CH, int BLOCK, bool Q8 = false>
 __device__ __forceinline__ void mv_body(const MvArgs &a) {
     using F = Fmt<TY>;
     using D = Dec<F::NSEG, F::WPS>;
@@ -318,7 +404,19 @@ __device__ __forceinline__ void mv_body(const MvArgs &a) {
         xt[t].xs = xs + t * ng;
     }
     constexpr int XR = 16384 / 8 / BLOCK; /* register-staged activations up to K = 16384 */
-    if (T == 1 && ng <= XR * BLOCK) {
+    if constexpr (Q8) {
+        const int8_t *xq8 = a.xq8 + a.x_slot * slot;
+        const float *xd8 = a.xd8 + (a.x_slot >> 5) * slot;
+        if (ng <= XR * BLOCK) {
+            XLoadQ8<BLOCK, XR> xl;
+            xl.load(xq8, xd8, K);
+            if (rbk < nrb) issue(ra, rbk, 0);
+            xl.template store<F::XL>(K, xq, xs);
+        } else {
+            if (rbk < nrb) issue(ra, rbk, 0);
+            le_q8_x_lds<F::XL>(xq8, xd8, K, xq, xs);
+        }
+    } else if (T == 1 && ng <= XR * BLOCK) {
         XLoad<BLOCK, XR> xl;
         xl.load(a.x + a.x_slot * slot + a.x_tok * t0, K);
         if (rbk < nrb) issue(ra, rbk, 0);
@@ -402,7 +500,16 @@ __device__ __forceinline__ void mv_body(const MvArgs &a) {
 #define LE_MV_T1(TY, G) LE_MV_T1B(TY, G, 512) LE_MV_T1B(TY, G, 1024)
 #define LE_MV_TN(TY, G, T) LE_MV(TY, G, T, 2, 2, 256) LE_MV(TY, G, T, 4, 1, 256)
 #define LE_MV_G(TY, G) LE_MV_T1(TY, G) LE_MV_TN(TY, G, 2) LE_MV_TN(TY, G, 4) LE_MV_TN(TY, G, 8)
-#define LE_MV_ALL(TY) LE_MV_G(TY, 1) LE_MV_G(TY, 2) LE_MV_G(TY, 4) LE_MV_G(TY, 8)
+#define LE_MV_ALL(TY) LE_MV_G(TY, 1) LE_MV_G(TY, 2) LE_MV_G(TY, 4) LE_MV_G(TY, 8) LE_MVQ8_ALL(TY)
+/* int8 activation mode: T = 1, the shapes of the decode matvec */
+#define LE_MVQ8(TY, G, RW, CH, BLOCK)                                                                       \
+    extern "C" __global__ void __launch_bounds__(BLOCK) le_mv_##TY##_g##G##_t1_r##RW##_c##CH##_b##BLOCK##_q8( \
+        MvArgs a) {                                                                                           \
+        mv_body<TY, G, 1, RW, CH, BLOCK, true>(a);                                                            \
+    }
+#define LE_MVQ8_B(TY, G, B) LE_MVQ8(TY, G, 1, 2, B) LE_MVQ8(TY, G, 2, 1, B) LE_MVQ8(TY, G, 2, 2, B) LE_MVQ8(TY, G, 4, 1, B)
+#define LE_MVQ8_G(TY, G) LE_MVQ8_B(TY, G, 512) LE_MVQ8_B(TY, G, 1024)
+#define LE_MVQ8_ALL(TY) LE_MVQ8_G(TY, 1) LE_MVQ8_G(TY, 2) LE_MVQ8_G(TY, 4) LE_MVQ8_G(TY, 8)
 
 /* ===================================================================================== */
 /* MFMA matvec (decode, one token).                                                          */
@@ -792,8 +899,6 @@ __device__ __forceinline__ void ms_q4k_body(const MvArgs &a) {
             R[i] = ldg16(W + (size_t)row * rb + (size_t)s0 * 144 + cb[i]);
         }
     };
-    LE_TRACE_DECL;
-    LE_TRACE_POINT(0);
     const int sfirst = wave * P, sstep = NW * P;
     const bool active = sfirst < nsb;
     /* activations of the first segment round go out first (clamped, unpredicated), then the
@@ -812,7 +917,6 @@ __device__ __forceinline__ void ms_q4k_body(const MvArgs &a) {
         mq_load_seg(xs, gseg(el), xv);
         mq_quant_seg(el, true, xv, rec, dxp, fsv);
     }
-    LE_TRACE_POINT(1);
 
     const MsLane L = ms_lane<0>(lane);
     le_v4i A[4];
@@ -852,8 +956,6 @@ __device__ __forceinline__ void ms_q4k_body(const MvArgs &a) {
         }
         par ^= 1;
     }
-    LE_TRACE_POINT(2);
-    LE_TRACE_FLUSH;
 }
 
 /* Q4_K for T tokens on one staged super-block. Token t's image slice of super-block sb is the
@@ -1551,7 +1653,7 @@ __device__ __forceinline__ MoeLogits moe_route_load(const MoeArgs &a) {
 }
 
 __device__ __forceinline__ void moe_route_par(const MoeArgs &a, MoeRoute &R, unsigned long long *lv /* [n_tok][n_exp] LDS */,
-                                              float *sx /* [n_tok][k] */, const MoeLogits &L LE_TRACE_PARAM) {
+                                              float *sx /* [n_tok][k] */, const MoeLogits &L) {
     const MoeRouteGeom g = moe_route_geom(a);
     const int tpt = g.tpt, C = g.C, tpp = g.tpp;
     /* n_tok <= 64 on every caller, so a token's bit fits the 64-bit expert mask; the first
@@ -1616,7 +1718,6 @@ __device__ __forceinline__ void moe_route_par(const MoeArgs &a, MoeRoute &R, uns
                 atomicOr(&R.mask[my_e], 1ull << t);
             }
         }
-        LE_TRACE_POINT(8);
         if (a.n_tok == 1) {
             /* one token: wave 0 holds the k selections; it writes the renormalised weights and
              * the groups (the k experts in ascending order) itself, with no further LDS pass */
@@ -1639,15 +1740,10 @@ __device__ __forceinline__ void moe_route_par(const MoeArgs &a, MoeRoute &R, uns
                 }
                 if (lane == 0) R.U = a.k;
             }
-            LE_TRACE_POINT(9);
             __syncthreads();
-            LE_TRACE_POINT(1);
             return;
         }
-        LE_TRACE_POINT(9);
-        LE_TRACE_POINT(10);
         __syncthreads();
-        LE_TRACE_POINT(11);
     } else if (g.npass <= MOE_LPASS) {
         /* every pass's keys in LDS, one barrier, every pass ranked, one barrier */
 #pragma unroll
@@ -1655,18 +1751,14 @@ __device__ __forceinline__ void moe_route_par(const MoeArgs &a, MoeRoute &R, uns
             const int t = p * tpp + t1;
             if (p < g.npass && t < a.n_tok && e1 < a.n_exp && c == 0) lv[t * a.n_exp + e1] = moe_key(L.v[p], e1);
         }
-        LE_TRACE_POINT(8);
         __syncthreads();
-        LE_TRACE_POINT(9);
 #pragma unroll
         for (int p = 0; p < MOE_LPASS; p++) {
             if (p >= g.npass) break;
             const int t = p * tpp + t1;
             rank_of(t, e1, L.v[p], moe_key(L.v[p], e1));
         }
-        LE_TRACE_POINT(10);
         __syncthreads();
-        LE_TRACE_POINT(11);
     } else {
         for (int t0 = 0; t0 < a.n_tok; t0 += tpp) {
             const int t = t0 + t1;
@@ -1679,8 +1771,6 @@ __device__ __forceinline__ void moe_route_par(const MoeArgs &a, MoeRoute &R, uns
             __syncthreads();
         }
     }
-    LE_TRACE_POINT(12);
-    LE_TRACE_POINT(13);
     const int lane = threadIdx.x & 63, nsel = a.n_tok * a.k;
     if (threadIdx.x < 64) {
         /* wave 0: list the experts with members in ascending order */
@@ -1954,12 +2044,7 @@ __device__ void moe_gu_fast(const MoeArgs &a) {
     const int K = a.hidden, nsb = K >> 8, ng = K >> 3;
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     /* 1. every token's activations (n_tok * ng <= XR * 1024 groups), clamped and unpredicated */
-    LE_TRACE_DECL;
-    LE_TRACE_POINT(0);
     const MoeLogits lgt = moe_route_load(a); /* first, so routing waits for these loads alone */
-#if defined(LE_TRACE)
-    le_tr_[6] = __builtin_amdgcn_s_memtime();
-#endif
     float4 ha[XR], hb[XR];
     const int ngt = a.n_tok * ng;
 #pragma unroll
@@ -1970,8 +2055,7 @@ __device__ void moe_gu_fast(const MoeArgs &a) {
         hb[r] = *(const LE_GLOBAL float4 *)(src + 4);
     }
     load_tables<TG>(tab);
-    moe_route_par(a, R, lv, sx, lgt LE_TRACE_ARG);
-    LE_TRACE_POINT(1);
+    moe_route_par(a, R, lv, sx, lgt);
     const int z = blockIdx.y;
     if (z >= R.U) return;
     const int e = R.grp_e[z];
@@ -2024,7 +2108,6 @@ __device__ void moe_gu_fast(const MoeArgs &a) {
         if (i < nmem) moe_member(a, R, e, i, tokm[i], pairm[i], wm[i]);
     }
     __syncthreads();
-    LE_TRACE_POINT(2);
     /* 4. gate and up rows for every member; the wave's JS rows go through one dot so their
      * chains interleave */
     float ag[JS][8], au[JS][8];
@@ -2075,7 +2158,6 @@ __device__ void moe_gu_fast(const MoeArgs &a) {
         }
     }
     __syncthreads();
-    LE_TRACE_POINT(4);
     /* 5. the unit's SwiGLU values, quantized into each member's down image */
     if (threadIdx.x < 32) {
         const int i = threadIdx.x >> 2, gw = threadIdx.x & 3;
@@ -2095,11 +2177,6 @@ __device__ void moe_gu_fast(const MoeArgs &a) {
             le_quant_group(va, vb, am, img, (float2 *)(img + (a.ff >> 3)), le_xpos<Fmt<TD>::XL>(4 * ux + gw));
         }
     }
-    LE_TRACE_POINT(3);
-#if defined(LE_TRACE)
-    le_tr_[5] = __builtin_amdgcn_s_memtime();
-#endif
-    LE_TRACE_FLUSH;
 }
 
 /* Launch 2 fast path: 8 output rows per block, 8 waves take the groups round-robin (one group in
@@ -2119,8 +2196,7 @@ __device__ void moe_down_fast(const MoeArgs &a) {
     extern __shared__ uint4 smem[];
     const MoeLogits lgt = moe_route_load(a);
     load_tables<TD>(tab);
-    LE_TRACE_DECL;
-    moe_route_par(a, R, lv, sx, lgt LE_TRACE_ARG);
+    moe_route_par(a, R, lv, sx, lgt);
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int K = a.ff, nsb = K >> 8, ng = K >> 3;
     const int img_bytes = le_xtok_bytes(K);
@@ -2245,8 +2321,6 @@ __device__ __forceinline__ void moe_gum_body(const MoeArgs &a) {
     uint4 *img = smem;                                          /* [n_tok][image] */
     uint4 *stg = smem + LE_MOE_FAST_TOK * LE_MOE_IMG(K) / 16;  /* [NW][NI*64] staging; routing keys first */
     uint4 *wb = stg + wave * NI * 64;
-    LE_TRACE_DECL;
-    LE_TRACE_POINT(0);
     const MoeLogits lgt = moe_route_load(a); /* first, so routing waits for these loads alone */
     /* 1. every token's activations, 16 values per (thread, r), clamped and unpredicated */
     const int nseg = a.n_tok * SEGT;
@@ -2256,8 +2330,7 @@ __device__ __forceinline__ void moe_gum_body(const MoeArgs &a) {
         const int e = min((int)threadIdx.x + NT * r, nseg - 1);
         mq_load_seg(a.h + (size_t)(e / SEGT) * K, e % SEGT, hv[r]);
     }
-    moe_route_par(a, R, (unsigned long long *)stg, sx, lgt LE_TRACE_ARG);
-    LE_TRACE_POINT(1);
+    moe_route_par(a, R, (unsigned long long *)stg, sx, lgt);
     const int z = blockIdx.y;
     if (z >= R.U) return; /* uniform over the block */
     const int e = R.grp_e[z];
@@ -2303,7 +2376,6 @@ __device__ __forceinline__ void moe_gum_body(const MoeArgs &a) {
 #pragma unroll
     for (int i = 0; i < NI; i++) wb[64 * i + lane] = Rg[i];
     __syncthreads();
-    LE_TRACE_POINT(2);
     /* 4. per member (a runtime loop: the code stays small), four tiles x this wave's super-blocks */
     const MsLane L = ms_lane<0>(lane);
     le_v4i A[4];
@@ -2329,7 +2401,6 @@ __device__ __forceinline__ void moe_gum_body(const MoeArgs &a) {
         }
     }
     __syncthreads();
-    LE_TRACE_POINT(3);
     /* 5. SwiGLU of the unit's 32 values = sub-block ux of the down input: thread (member i, row r)
      * adds the waves for gate and up; then lanes 2i, 2i+1 of wave 0 quantize member i's two
      * 16-value segments into its down image */
@@ -2358,8 +2429,6 @@ __device__ __forceinline__ void moe_gum_body(const MoeArgs &a) {
         float *dxp = (float *)(rec + nsbd * 32), *fsv = dxp + nsbd * 16;
         mq_quant_seg<MAPD>(2 * ux + c, ok, v4, rec, dxp, fsv);
     }
-    LE_TRACE_POINT(4);
-    LE_TRACE_FLUSH;
 }
 
 #define LE_MOE_DN_IMGS 16 /* pair images the down kernel keeps in LDS */
@@ -2378,8 +2447,6 @@ __device__ __forceinline__ void moe_dnm_body(const MoeArgs &a) {
     uint4 *imgs = smem;                          /* LE_MOE_DN_IMGS images */
     uint4 *stg = smem + LE_MOE_DN_IMGS * IMGC;   /* [NW][NI*64] staging; routing keys first */
     uint4 *wb = stg + wave * NI * 64;
-    LE_TRACE_DECL;
-    LE_TRACE_POINT(0);
     for (int i = threadIdx.x; i < NW * LE_MOE_FAST_TOK * 16; i += blockDim.x) (&red[0][0][0])[i] = 0.f;
     const int npair = a.n_tok * a.k;
     const bool all_in = npair <= LE_MOE_DN_IMGS;
@@ -2396,7 +2463,6 @@ __device__ __forceinline__ void moe_dnm_body(const MoeArgs &a) {
     }
     /* the routing of the gate/up launch (n_tok * k <= 64 <= blockDim.x, groups <= 64) */
     moe_rec_read(a, R, a.ws + (size_t)a.n_tok * a.k * IMG);
-    LE_TRACE_POINT(1);
     const size_t rb = (size_t)P * SBB;
     /* H blocks per 16-row tile (grid = H * hidden / 16): block hh of a tile takes the expert groups
      * z = hh (mod H) and, with H = 2, adds into the output the gate/up launch zeroed (every
@@ -2428,7 +2494,6 @@ __device__ __forceinline__ void moe_dnm_body(const MoeArgs &a) {
             }
     }
     __syncthreads(); /* the images, and the routing keys are no longer read before staging reuses them */
-    LE_TRACE_POINT(5);
     const MsLane L = ms_lane<MAPD>(lane);
     le_v4i A[4];
 #pragma unroll
@@ -2452,7 +2517,6 @@ __device__ __forceinline__ void moe_dnm_body(const MoeArgs &a) {
             R0[i] = R1[i];
         }
         if (z + 2 * H * NW < R.U) issue(z + 2 * H * NW, R1);
-        if (z == hh + H * wave) LE_TRACE_POINT(6);
 #pragma unroll 1
         for (int i = 0; i < nmem; i++) {
             const uint4 *rec;
@@ -2478,11 +2542,8 @@ __device__ __forceinline__ void moe_dnm_body(const MoeArgs &a) {
             y += __shfl_xor(y, 32);
             if (lane < 16) red[wave][mtok[wave][i]][lane] += mw[wave][i] * y;
         }
-        if (z == hh + H * wave) LE_TRACE_POINT(7);
     }
-    LE_TRACE_POINT(2);
     __syncthreads();
-    LE_TRACE_POINT(3);
     for (int i = threadIdx.x; i < a.n_tok * 16; i += blockDim.x) {
         const int t = i >> 4, r = i & 15;
         float acc = 0.f;
@@ -2493,8 +2554,6 @@ __device__ __forceinline__ void moe_dnm_body(const MoeArgs &a) {
         else
             a.out[(size_t)t * a.hidden + row0 + r] = acc;
     }
-    LE_TRACE_POINT(4);
-    LE_TRACE_FLUSH;
 }
 
 /* ===================== MoE in one launch: gate/up, a device-wide barrier, down =====================
@@ -2594,8 +2653,6 @@ __device__ __forceinline__ void moe_fus_body(const MoeArgs &a) {
     uint4 *img = smem;                                         /* phase 1: [n_tok][image] */
     uint4 *stg = smem + LE_MOE_FAST_TOK * LE_MOE_IMG(K) / 16; /* phase 1: [NW][NI*64] staging; routing keys first */
     uint4 *wb = stg + wave * NI * 64;
-    LE_TRACE_DECL;
-    LE_TRACE_POINT(0);
     const MoeLogits lgt = moe_route_load(a); /* first, so routing waits for these loads alone */
     /* every token's activations */
     const int nseg = a.n_tok * SEGT;
@@ -2605,8 +2662,7 @@ __device__ __forceinline__ void moe_fus_body(const MoeArgs &a) {
         const int e = min((int)threadIdx.x + NT * r, nseg - 1);
         mq_load_seg(a.h + (size_t)(e / SEGT) * K, e % SEGT, hv[r]);
     }
-    moe_route_par(a, R, (unsigned long long *)stg, sx, lgt LE_TRACE_ARG);
-    LE_TRACE_POINT(1);
+    moe_route_par(a, R, (unsigned long long *)stg, sx, lgt);
     const int ngu = (a.ff >> 5) * R.U, ntile = a.hidden >> 4;
     const int b = blockIdx.x, G = gridDim.x;
     /* phase 2: row tile tb of the down projection, by H blocks that split its expert groups
@@ -2667,9 +2723,6 @@ __device__ __forceinline__ void moe_fus_body(const MoeArgs &a) {
     if (b < ngu) gissue(b);
 #pragma unroll 1
     for (int it = b; it < ngu; it += G) {
-#if defined(LE_TRACE)
-        const unsigned long long q0 = __builtin_amdgcn_s_memrealtime();
-#endif
         const int ux = it % (a.ff >> 5), z = it / (a.ff >> 5);
         const int e = R.grp_e[z];
         const int nmem = __popcll(R.mask[e]);
@@ -2681,10 +2734,6 @@ __device__ __forceinline__ void moe_fus_body(const MoeArgs &a) {
             mpair[0][threadIdx.x] = pair;
         }
         le_lds_barrier(); /* the previous item's readers of wb / act are done; images and members ready */
-#if defined(LE_TRACE)
-        const unsigned long long q1 = __builtin_amdgcn_s_memrealtime();
-        le_tr_[5] += q1 - q0;
-#endif
 #pragma unroll
         for (int i = 0; i < NI; i++) wb[64 * i + lane] = Rg[i];
         gissue(it + G);
@@ -2704,10 +2753,6 @@ __device__ __forceinline__ void moe_fus_body(const MoeArgs &a) {
                 if (lane < 16) red[wave][i][16 * ti + lane] = v;
             }
         }
-#if defined(LE_TRACE)
-        const unsigned long long q2 = __builtin_amdgcn_s_memrealtime();
-        le_tr_[6] += q2 - q1;
-#endif
         le_lds_barrier();
         if (threadIdx.x < 32 * LE_MOE_FAST_TOK) {
             const int i = threadIdx.x >> 5, r = threadIdx.x & 31;
@@ -2722,10 +2767,6 @@ __device__ __forceinline__ void moe_fus_body(const MoeArgs &a) {
             }
         }
         le_lds_barrier();
-#if defined(LE_TRACE)
-        const unsigned long long q3 = __builtin_amdgcn_s_memrealtime();
-        le_tr_[7] += q3 - q2;
-#endif
         if (wave == 0 && lane < 2 * LE_MOE_FAST_TOK) {
             const int i = lane >> 1, c = lane & 1;
             const bool ok = i < nmem;
@@ -2737,22 +2778,16 @@ __device__ __forceinline__ void moe_fus_body(const MoeArgs &a) {
             float *dxp = (float *)(rec + PD * 32), *fsv = dxp + PD * 16;
             mq_quant_seg<MAPD, true>(2 * ux + c, ok, v4, rec, dxp, fsv); /* read by other blocks after the barrier */
         }
-#if defined(LE_TRACE)
-        le_tr_[14] += __builtin_amdgcn_s_memrealtime() - q3;
-        le_tr_[15] += 1;
-#endif
     }
     if (H == 2 && b < ntile) /* device-coherent, ordered before the other half's adds by the barrier */
         for (int i = threadIdx.x; i < a.n_tok * 16; i += blockDim.x)
             st_f<true>(a.out + (size_t)(i >> 4) * a.hidden + 16 * b + (i & 15), 0.f);
     /* ---- every down image written ---- */
-    LE_TRACE_POINT(2);
     /* the first down group of this block's tile is issued after the arrival, so its loads are in
      * flight through the wait */
     const bool ok = moe_grid_barrier(a, G, [&]() {
         if (b < H * ntile && hh + H * wave < R.U) dissue(hh + H * wave, R0);
     });
-    LE_TRACE_POINT(3);
     if (b >= H * ntile) return;
     /* ---- phase 2: row tile tb of the down projection, expert groups hh mod H ---- */
     uint4 *imgs = smem;                        /* LE_MOE_DN_IMGS images */
@@ -2832,8 +2867,6 @@ __device__ __forceinline__ void moe_fus_body(const MoeArgs &a) {
         else
             *o = ok ? acc : __builtin_nanf("");
     }
-    LE_TRACE_POINT(4);
-    LE_TRACE_FLUSH;
 }
 
 #define LE_MOE_FUS(TD, PD)                                                                                  \

@@ -18,8 +18,11 @@ import numpy as np
 HERE = os.path.dirname(os.path.abspath(__file__))
 LIB_DIR = os.path.join(HERE, "lib")
 
-Q8_0, Q4_K, Q6_K, IQ2_XXS, IQ3_XXS = 8, 12, 14, 16, 18
+Q4_0, Q8_0, Q3_K, Q4_K, Q5_K, Q6_K, IQ2_XXS, IQ3_XXS, IQ2_S = 2, 8, 11, 12, 13, 14, 16, 18, 22
+# the five types of every entry point (and of this build's quantizer)
 TYPES = {"Q8_0": Q8_0, "Q4_K": Q4_K, "Q6_K": Q6_K, "IQ2_XXS": IQ2_XXS, "IQ3_XXS": IQ3_XXS}
+# types that le_dequant_rows, le_matvec, le_matvec_q8 and le_gemm also accept
+MV_TYPES = dict(TYPES, Q4_0=Q4_0, Q3_K=Q3_K, Q5_K=Q5_K, IQ2_S=IQ2_S)
 
 _STATUS = {0: "ok", -1: "invalid argument", -2: "unsupported quant type", -3: "unsupported shape",
            -4: "misaligned pointer or stride", -5: "HIP runtime error",
@@ -60,6 +63,8 @@ def lib():
         "le_set_option": (I, [P, ctypes.c_char_p, I]),
         "le_dequant_rows": (I, [P, I, P, P, I, I, P]),
         "le_matvec": (I, [P, I, P, P, P, LL, P, I, I, I, P]),
+        "le_quant_x": (I, [P, P, P, P, P, I, P]),
+        "le_matvec_q8": (I, [P, I, P, P, P, P, P, LL, P, I, I, I, P]),
         "le_gemm_workspace_size": (S, [I, I, I]),
         "le_gemm": (I, [P, I, P, P, I, P, I, I, P, S, P]),
         "le_gemm_noalloc": (I, [P, I, P, P, I, P, I, I, P]),
@@ -178,6 +183,15 @@ class Engine:
         """Gpu::mv_ptrs (src/gpu.rs:228): out[s*rows + r] = W_s[r] . x[s*xstride:]."""
         self._check(self._L.le_matvec(self._ctx, ty, _ptr(ptrs), _ptr(w), _ptr(x), int(xstride), _ptr(out), rows,
                                       cols, slots, _stream(stream)))
+
+    def quant_x(self, x, xq, xd, xs, n_units, stream=None):
+        """Gpu::qx / quant_x (src/gpu.rs:223, src/cuda/kernels.cu:15-25): int8 activations per 32 values."""
+        self._check(self._L.le_quant_x(self._ctx, _ptr(x), _ptr(xq), _ptr(xd), _ptr(xs), int(n_units), _stream(stream)))
+
+    def mv_q8(self, ty, ptrs, xq, xd, xs, out, rows, cols, xstride, slots, w=None, stream=None):
+        """matvec_<ty> on quantized activations (src/cuda/kernels.cu:371-392) through le_matvec_q8."""
+        self._check(self._L.le_matvec_q8(self._ctx, ty, _ptr(ptrs), _ptr(w), _ptr(xq), _ptr(xd), _ptr(xs), int(xstride),
+                                         _ptr(out), rows, cols, slots, _stream(stream)))
 
     def mv(self, ty, w, x, out, rows, cols, stream=None):
         """Gpu::mv (src/gpu.rs:238): one matrix, one activation."""

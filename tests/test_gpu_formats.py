@@ -1,0 +1,164 @@
+"""GPU parity of the wider formats (Q4_0, Q3_K, Q5_K, IQ2_S) and of the int8 activation mode.
+
+Inputs are arbitrary GGUF block bytes with the f16 super-block scales replaced by bounded finite
+values (every scale code, grid index and sign pattern occurs), so the kernels see what real GGUF
+tensors hold. Bars: dequant bit-exact; le_matvec / le_gemm within the 1e-3 parity bar against the
+oracle's cpu_ref::matvec / matmat; quant_x bit-exact against the oracle's quant_x; le_matvec_q8
+within 1e-5 * sum|w * xa| of the oracle's udot-based matvec (the integer dots are exact on both
+sides, only the fp32 summation order differs)."""
+import numpy as np
+import pytest
+
+import lastengine_amd as le
+import oracle
+from tests.util import acts, check_close, random_blocks
+
+pytestmark = pytest.mark.gpu
+
+NEW = ["Q4_0", "Q3_K", "Q5_K", "IQ2_S"]
+ALL = list(le.MV_TYPES)
+
+
+def dev(a):
+    import torch
+    return torch.from_numpy(np.ascontiguousarray(a)).cuda()
+
+
+def sync():
+    import torch
+    torch.cuda.synchronize()
+
+
+@pytest.mark.parametrize("name", NEW)
+@pytest.mark.parametrize("rows,cols", [(8, 1024), (37, 768), (3, 4096)])
+def test_new_dequant_bit_exact(engine, name, rows, cols):
+    import torch
+    ty = le.MV_TYPES[name]
+    q = random_blocks(ty, rows, cols, seed=rows * 7 + cols + ty)
+    out = torch.empty(rows, cols, dtype=torch.float32, device="cuda")
+    engine.dequant_rows(ty, dev(q), out, rows, cols)
+    sync()
+    want = oracle.dequant_rows(ty, q, rows, cols)
+    assert np.array_equal(out.cpu().numpy().view(np.uint32), want.view(np.uint32))
+
+
+@pytest.mark.parametrize("name", NEW)
+def test_new_dequant_raw_bytes(engine, name):
+    """Unbounded bytes (subnormal, Inf and NaN scales): non-NaN values bit-identical, NaN where NaN."""
+    import torch
+    ty = le.MV_TYPES[name]
+    rows, cols = 16, 1024
+    q = np.random.default_rng(ty + 1).integers(0, 256, size=(rows, le.row_bytes(ty, cols)), dtype=np.uint8)
+    out = torch.empty(rows, cols, dtype=torch.float32, device="cuda")
+    engine.dequant_rows(ty, dev(q), out, rows, cols)
+    sync()
+    want = oracle.dequant_rows(ty, q, rows, cols)
+    got = out.cpu().numpy()
+    nan = np.isnan(want)
+    assert np.array_equal(np.isnan(got), nan)
+    assert np.array_equal(got[~nan].view(np.uint32), want[~nan].view(np.uint32))
+
+
+def _absmag(ty, q, rows, cols, xs):
+    w = oracle.dequant_rows(ty, q, rows, cols).astype(np.float64)
+    return np.abs(np.atleast_2d(xs).astype(np.float64)) @ np.abs(w).T
+
+
+@pytest.mark.parametrize("name", NEW)
+@pytest.mark.parametrize("rows,cols", [(64, 256), (333, 4096), (77, 768), (40, 14336), (1, 512)])
+def test_new_matvec_parity(engine, name, rows, cols):
+    import torch
+    ty = le.MV_TYPES[name]
+    q = random_blocks(ty, rows, cols, seed=ty * 31 + rows)
+    x = acts(cols, 5 + rows)
+    y = torch.full((rows,), float("nan"), device="cuda")
+    engine.mv(ty, dev(q), dev(x), y, rows, cols)
+    sync()
+    want = oracle.matvec(ty, q, rows, cols, x)
+    check_close(y.cpu().numpy(), want, _absmag(ty, q, rows, cols, x)[0])
+
+
+@pytest.mark.parametrize("name", NEW)
+@pytest.mark.parametrize("m", [2, 5, 17])
+def test_new_gemm_parity(engine, name, m):
+    import torch
+    ty = le.MV_TYPES[name]
+    rows, cols = 96, 2048
+    q = random_blocks(ty, rows, cols, seed=ty + m)
+    xs = np.stack([acts(cols, 50 + t) for t in range(m)])
+    assert engine.gemm_workspace_size(ty, m, cols) == 0
+    y = torch.full((m * rows,), float("nan"), device="cuda")
+    engine.gemm(ty, dev(q), dev(xs), m, y, rows, cols)
+    sync()
+    want = oracle.matmat(ty, q, rows, cols, xs)
+    check_close(y.cpu().numpy().reshape(m, rows), want, _absmag(ty, q, rows, cols, xs))
+
+
+def test_new_types_rejected_by_moe(engine):
+    import torch
+    with pytest.raises(le.LeError) as e:
+        engine.moe(le.Q5_K, le.Q5_K, le.Q6_K, dev(np.zeros(16, np.uint8)), dev(np.zeros(16, np.uint8)),
+                   dev(np.zeros(16, np.uint8)), 4, 2, 256, 256, dev(np.zeros(4, np.float32)),
+                   dev(np.zeros(256, np.float32)), 1, torch.empty(256, device="cuda"), ws=torch.empty(1 << 20, dtype=torch.uint8, device="cuda"))
+    assert e.value.code == -2
+
+
+# ------------------------------------------------------------------ int8 activation mode
+
+@pytest.mark.parametrize("n", [32, 4096, 14336])
+def test_quant_x_bit_exact(engine, n):
+    import torch
+    x = acts(n, n)
+    x[:32] = 0.0            # an all-zero unit
+    x[32:64] *= 1e-30
+    xq = torch.empty(n, dtype=torch.int8, device="cuda")
+    xd = torch.empty(n // 32, dtype=torch.float32, device="cuda")
+    xs = torch.empty(n // 32, dtype=torch.int32, device="cuda")
+    engine.quant_x(dev(x), xq, xd, xs, n // 32)
+    sync()
+    wq, wd, ws = oracle.quant_x(x)
+    assert np.array_equal(xq.cpu().numpy(), wq)
+    assert np.array_equal(xd.cpu().numpy().view(np.uint32), wd.view(np.uint32))
+    assert np.array_equal(xs.cpu().numpy(), ws)
+
+
+@pytest.mark.parametrize("name", ALL)
+@pytest.mark.parametrize("rows,cols", [(100, 4096), (40, 14336), (77, 768)])
+def test_matvec_q8_parity(engine, name, rows, cols):
+    import torch
+    ty = le.MV_TYPES[name]
+    q = random_blocks(ty, rows, cols, seed=ty * 3 + cols)
+    x = acts(cols, 9 + rows)
+    xq, xd, xs = oracle.quant_x(x)
+    y = torch.full((rows,), float("nan"), device="cuda")
+    engine.mv_q8(ty, None, dev(xq), dev(xd), dev(xs), y, rows, cols, 0, 1, w=dev(q))
+    sync()
+    want = oracle.matvec_q8(ty, q, rows, cols, xq, xd, xs)
+    wd = oracle.dequant_rows(ty, q, rows, cols).astype(np.float64)
+    xa = np.repeat(xd.astype(np.float64), 32) * xq.astype(np.float64)
+    mag = np.abs(wd) @ np.abs(xa)
+    got = y.cpu().numpy()
+    assert np.all(np.isfinite(got))
+    assert np.all(np.abs(got - want) <= 1e-5 * mag + 1e-30), float(np.max(np.abs(got - want) / mag))
+
+
+def test_matvec_q8_slots_and_pointer_table(engine):
+    """Two slots through a device pointer table with per-slot activations (xstride = cols), the
+    reference's fused gate+up launch shape with distinct inputs."""
+    import torch
+    ty, rows, cols = le.Q4_K, 48, 2048
+    qs = [random_blocks(ty, rows, cols, seed=100 + s) for s in range(2)]
+    xs_ = [acts(cols, 200 + s) for s in range(2)]
+    quant = [oracle.quant_x(x) for x in xs_]
+    dws = [dev(q) for q in qs]
+    ptrs = dev(np.array([w.data_ptr() for w in dws], dtype=np.uint64))
+    xq = dev(np.concatenate([t[0] for t in quant]))
+    xd = dev(np.concatenate([t[1] for t in quant]))
+    xsum = dev(np.concatenate([t[2] for t in quant]))
+    y = torch.full((2 * rows,), float("nan"), device="cuda")
+    engine.mv_q8(ty, ptrs, xq, xd, xsum, y, rows, cols, cols, 2)
+    sync()
+    got = y.cpu().numpy().reshape(2, rows)
+    for s in range(2):
+        want = oracle.matvec_q8(ty, qs[s], rows, cols, *quant[s])
+        np.testing.assert_allclose(got[s], want, rtol=1e-4, atol=1e-6 * np.abs(want).max())

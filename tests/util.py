@@ -35,7 +35,8 @@ def check_close(got, want, absmag):
 
 
 # Byte offsets of the f16 scale fields in each block: (block bytes, [field offsets]).
-SCALE_FIELDS = {8: (34, [0]), 12: (144, [0, 2]), 14: (210, [208]), 16: (66, [0]), 18: (98, [0])}
+SCALE_FIELDS = {8: (34, [0]), 12: (144, [0, 2]), 14: (210, [208]), 16: (66, [0]), 18: (98, [0]),
+                2: (18, [0]), 11: (110, [108]), 13: (176, [0, 2]), 22: (82, [0])}
 
 
 def random_blocks(ty, rows, cols, seed, dmax=0.01):
