@@ -47,7 +47,27 @@ def device_copies(host, min_bytes=ROTATE_BYTES):
 
 def quantized(ty, rows, cols, seed):
     import lastengine_amd as le
+    if ty not in le.TYPES.values():
+        return synthetic_blocks(ty, rows, cols, seed)
     return le.quantize_rows(ty, le.fill_normal(rows * cols, seed, std=0.02).reshape(rows, cols))
+
+
+# f16 super-block scale fields per type (block bytes, offsets): Q4_0, Q3_K, Q5_K, IQ2_S
+_SCALE_FIELDS = {2: (18, [0]), 11: (110, [108]), 13: (176, [0, 2]), 22: (82, [0])}
+
+
+def synthetic_blocks(ty, rows, cols, seed):
+    """Seeded block bytes for the types this build has no quantizer for (Q4_0, Q3_K, Q5_K, IQ2_S):
+    uniform random codes with the f16 scale fields set to finite values in [-0.01, 0.01]."""
+    import lastengine_amd as le
+    rng = np.random.default_rng(seed)
+    q = rng.integers(0, 256, size=(rows, le.row_bytes(ty, cols)), dtype=np.uint8)
+    bb, offs = _SCALE_FIELDS[ty]
+    blk = q.reshape(rows, -1, bb)
+    for o in offs:
+        blk[:, :, o:o + 2] = rng.uniform(-0.01, 0.01, size=blk.shape[:2]).astype(np.float16).view(np.uint8).reshape(
+            blk.shape[0], blk.shape[1], 2)
+    return q
 
 
 MIN_TIMED_LAUNCHES = 200
@@ -98,6 +118,35 @@ def bench_matvec(eng, ty, rows, cols, steps, warmup, seed=1):
     alg = host.nbytes + 4 * cols + 4 * rows
     return {"us": ms * 1e3, "ms": ms, "bytes": alg, "gbs": alg / (ms * 1e-3) / 1e9, "copies": len(bufs),
             "timing": dict(graph_time.stats)}, host
+
+
+def bench_matvec_q8(eng, ty, rows, cols, steps, warmup, seed=1):
+    """int8 activation mode: le_matvec_q8 on activations quantize_x'd once (the reference's
+    matvec_<ty> launch), and le_quant_x alone."""
+    import torch
+    import lastengine_amd as le
+    host = quantized(ty, rows, cols, seed)
+    bufs = device_copies(host)
+    x = torch.from_numpy(le.fill_normal(cols, seed + 1)).cuda()
+    xq = torch.empty(cols, dtype=torch.int8, device="cuda")
+    xd = torch.empty(cols // 32, dtype=torch.float32, device="cuda")
+    xs = torch.empty(cols // 32, dtype=torch.int32, device="cuda")
+    y = torch.empty(rows, dtype=torch.float32, device="cuda")
+    eng.quant_x(x, xq, xd, xs, cols // 32)
+
+    def record():
+        for b in bufs:
+            eng.mv_q8(ty, None, xq, xd, xs, y, rows, cols, 0, 1, w=b)
+    ms = graph_time(record, len(bufs), steps, warmup)
+
+    def record_qx():
+        for _ in range(20):
+            eng.quant_x(x, xq, xd, xs, cols // 32)
+    msq = graph_time(record_qx, 20, steps, warmup)
+    alg = host.nbytes + cols + 8 * (cols // 32) + 4 * rows
+    gbs = alg / (ms * 1e-3) / 1e9
+    return {"us": round(ms * 1e3, 3), "GB/s": round(gbs, 1), "frac_hbm": round(gbs / HBM_PEAK_GBS, 4),
+            "quant_x_us": round(msq * 1e3, 3)}
 
 
 def bench_layer(eng, mats, steps, warmup):
@@ -391,6 +440,16 @@ def main():
             r, _ = bench_matvec(eng, ty, r_, c_, steps2, args.warmup // 4)
             sec[name] = {"us": round(r["us"], 3), "GB/s": round(r["gbs"], 1), "frac_hbm": round(r["gbs"] / HBM_PEAK_GBS, 4)}
             log(name, sec[name])
+            torch.cuda.empty_cache()
+        for name, ty in [("q4_0", le.Q4_0), ("q3_k", le.Q3_K), ("q5_k", le.Q5_K), ("iq2_s", le.IQ2_S)]:
+            r, _ = bench_matvec(eng, ty, 14336, 4096, steps2, args.warmup // 4)
+            sec["%s_14336x4096" % name] = {"us": round(r["us"], 3), "GB/s": round(r["gbs"], 1),
+                                          "frac_hbm": round(r["gbs"] / HBM_PEAK_GBS, 4)}
+            log(name, sec["%s_14336x4096" % name])
+            torch.cuda.empty_cache()
+        for name, ty, r_, c_ in [("q4k_14336x4096", le.Q4_K, 14336, 4096), ("q6k_4096x14336", le.Q6_K, 4096, 14336)]:
+            sec["int8_mode_" + name] = bench_matvec_q8(eng, ty, r_, c_, steps2, args.warmup // 4)
+            log("int8 mode", name, sec["int8_mode_" + name])
             torch.cuda.empty_cache()
         sec["config5_iq_gate_up_down"] = bench_layer(
             eng, [("gate", le.IQ2_XXS, 14336, 4096), ("up", le.IQ2_XXS, 14336, 4096), ("down", le.IQ3_XXS, 4096, 14336)],

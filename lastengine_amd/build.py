@@ -26,7 +26,7 @@ PARTS["gm"] = []
 PARTS["gq"] = []
 SOURCES = {"gm": "le_gemm_kernels.hip", "gq": "le_gq_kernels.hip"}  # parts not listed here compile le_qmm_kernels.hip
 
-HOST_SOURCES = ["le_qmm.cpp", "le_quant.cpp"]
+HOST_SOURCES = ["le_qmm.cpp", "le_quant.cpp", "le_gguf.cpp"]
 # Host sources that declare device memory (hipcc, host and device passes), linked into the library.
 HIP_HOST_SOURCES = ["le_noalloc.hip"]
 

@@ -12,7 +12,7 @@ import lastengine_amd as le
 from lastengine_amd import qmm
 from tests.conftest import REPO
 
-HEADERS = [os.path.join(REPO, "include", h) for h in ("le_qmm.h", "le_quant.h")]
+HEADERS = [os.path.join(REPO, "include", h) for h in ("le_qmm.h", "le_quant.h", "le_gguf.h")]
 
 
 def declared_functions():
@@ -33,7 +33,7 @@ def test_library_exports_every_declared_symbol():
 
 
 def test_code_objects_built():
-    for part in ("deq", "moe", "gm", "mv8", "mv12", "mv14", "mv16", "mv18"):
+    for part in ("deq", "moe", "gm", "gq", "mv2", "mv8", "mv11", "mv12", "mv13", "mv14", "mv16", "mv18", "mv22"):
         assert os.path.getsize(os.path.join(qmm.LIB_DIR, "le_qmm_%s.hsaco" % part)) > 1000
 
 
