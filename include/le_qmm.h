@@ -127,6 +127,12 @@ int le_matvec(le_ctx *ctx, int ty, const void *const *ptrs, const void *w, const
  * Per value the activation error is up to xd / 2 (about 4e-3 relative at K = 4096, as on the
  * reference's GPU path), so results differ from cpu_ref by more than le_matvec's. */
 int le_quant_x(le_ctx *ctx, const float *x, int8_t *xq, float *xd, int32_t *xs, int n_units, le_stream_t stream);
+/* rms_quant (src/cuda/dense.cu:33-56, launched by DenseGpu::rms_q, src/gpu/dense.rs:143): RMSNorm
+ * and int8 quantization of the result in one launch. o[i] = x[i] * r * w[i] with
+ * r = 1 / sqrt(sum(x^2) / n + eps) (cpu_ref::rms, src/cpu_ref.rs:32-36; the sum is reduced in a
+ * different order, so r agrees to a few ulp), and xq/xd/xs = le_quant_x(o) exactly. n % 32 == 0. */
+int le_rms_quant(le_ctx *ctx, const float *x, const float *w, float *o, int8_t *xq, float *xd, int32_t *xs, int n, float eps,
+                 le_stream_t stream);
 int le_matvec_q8(le_ctx *ctx, int ty, const void *const *ptrs, const void *w, const int8_t *xq, const float *xd,
                  const int32_t *xs, long long xstride, float *y, int rows, int cols, int slots, le_stream_t stream);
 

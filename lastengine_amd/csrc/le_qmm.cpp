@@ -606,6 +606,17 @@ int le_quant_x(le_ctx *c, const float *x, int8_t *xq, float *xd, int32_t *xs, in
     return c->launch("le_quant_x", dim3(blocks), 256, 0, (hipStream_t)stream, args);
 }
 
+int le_rms_quant(le_ctx *c, const float *x, const float *w, float *o, int8_t *xq, float *xd, int32_t *xs, int n, float eps,
+                 le_stream_t stream) {
+    if (!c) return LE_ERR_ARG;
+    if (!x || !w || !o || !xq || !xd || !xs) return c->fail(LE_ERR_ARG, "null pointer");
+    if (n <= 0 || n % 32) return c->fail(LE_ERR_SHAPE, "n=%d is not a positive multiple of 32", n);
+    int blocks = (n / 32 + 7) / 8;
+    if (blocks > 64) blocks = 64;
+    void *args[] = {(void *)&x, (void *)&w, (void *)&o, (void *)&xq, (void *)&xd, (void *)&xs, (void *)&n, (void *)&eps};
+    return c->launch("le_rms_quant", dim3((unsigned)blocks), 256, 0, (hipStream_t)stream, args);
+}
+
 int le_matvec_q8(le_ctx *c, int ty, const void *const *ptrs, const void *w, const int8_t *xq, const float *xd,
                  const int32_t *xs, long long xstride, float *y, int rows, int cols, int slots, le_stream_t stream) {
     (void)xs; /* the kernels form the group sums they need from xq */

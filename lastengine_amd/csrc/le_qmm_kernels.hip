@@ -230,6 +230,40 @@ extern "C" __global__ void __launch_bounds__(256) le_quant_x(const float *x, int
         }
     }
 }
+/* rms_quant (src/cuda/dense.cu:33-56): o = x * r * w with r = 1 / sqrt(sum(x^2) / n + eps) (the
+ * RMSNorm of cpu_ref::rms, src/cpu_ref.rs:32-36), and o quantized as le_quant_x does, in one
+ * launch. Every block forms the sum of squares over all n values (block-wide, from L2), then
+ * quantizes its own 32-value units (32 lanes per unit, grid-stride). */
+extern "C" __global__ void __launch_bounds__(256) le_rms_quant(const float *x, const float *w, float *o, int8_t *xq, float *xd,
+                                                               int *xs, int n, float eps) {
+    __shared__ float part[4];
+    float s = 0.f;
+    for (int i = threadIdx.x; i < n; i += 256) s += x[i] * x[i];
+#pragma unroll
+    for (int off = 32; off; off >>= 1) s += __shfl_xor(s, off);
+    if ((threadIdx.x & 63) == 0) part[threadIdx.x >> 6] = s;
+    __syncthreads();
+    const float ss = (part[0] + part[1]) + (part[2] + part[3]);
+    const float r = 1.0f / sqrtf(ss / (float)n + eps);
+    const int l = threadIdx.x & 31, nu = n >> 5;
+    for (int u = blockIdx.x * 8 + (threadIdx.x >> 5); u < nu; u += gridDim.x * 8) {
+        const float v = x[u * 32 + l] * r * w[u * 32 + l];
+        o[u * 32 + l] = v;
+        float am = fabsf(v);
+#pragma unroll
+        for (int off = 16; off; off >>= 1) am = fmaxf(am, __shfl_xor(am, off, 32));
+        const float d = am / 127.0f, id = d > 0.f ? 1.0f / d : 0.f;
+        const int q = (int)rintf(v * id);
+        int sm = q;
+#pragma unroll
+        for (int off = 16; off; off >>= 1) sm += __shfl_xor(sm, off, 32);
+        xq[u * 32 + l] = (int8_t)q;
+        if (l == 0) {
+            xd[u] = d;
+            xs[u] = sm;
+        }
+    }
+}
 #define LE_DEQ(TY, NAME)                                                                                   \
     extern "C" __global__ void __launch_bounds__(256) NAME(const u8 *w, float *out, int rows, int cols,     \
                                                           unsigned long long row_bytes) {                  \

@@ -64,6 +64,7 @@ def lib():
         "le_dequant_rows": (I, [P, I, P, P, I, I, P]),
         "le_matvec": (I, [P, I, P, P, P, LL, P, I, I, I, P]),
         "le_quant_x": (I, [P, P, P, P, P, I, P]),
+        "le_rms_quant": (I, [P, P, P, P, P, P, P, I, F, P]),
         "le_matvec_q8": (I, [P, I, P, P, P, P, P, LL, P, I, I, I, P]),
         "le_gemm_workspace_size": (S, [I, I, I]),
         "le_gemm": (I, [P, I, P, P, I, P, I, I, P, S, P]),
@@ -187,6 +188,11 @@ class Engine:
     def quant_x(self, x, xq, xd, xs, n_units, stream=None):
         """Gpu::qx / quant_x (src/gpu.rs:223, src/cuda/kernels.cu:15-25): int8 activations per 32 values."""
         self._check(self._L.le_quant_x(self._ctx, _ptr(x), _ptr(xq), _ptr(xd), _ptr(xs), int(n_units), _stream(stream)))
+
+    def rms_quant(self, x, w, o, xq, xd, xs, n, eps, stream=None):
+        """rms_quant (src/cuda/dense.cu:33-56): RMSNorm into o and its int8 quantization."""
+        self._check(self._L.le_rms_quant(self._ctx, _ptr(x), _ptr(w), _ptr(o), _ptr(xq), _ptr(xd), _ptr(xs), int(n),
+                                         float(eps), _stream(stream)))
 
     def mv_q8(self, ty, ptrs, xq, xd, xs, out, rows, cols, xstride, slots, w=None, stream=None):
         """matvec_<ty> on quantized activations (src/cuda/kernels.cu:371-392) through le_matvec_q8."""

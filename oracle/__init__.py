@@ -34,6 +34,7 @@ def lib():
         "or_moe": (I, [I, I, I, P, P, P, I, I, S, S, P, P, I, P, P, P, I]),
         "or_quant_x": (None, [P, P, P, P, S]),
         "or_matvec_q8": (I, [I, P, S, S, P, P, P, P]),
+        "or_rms": (None, [P, P, P, S, F]),
     }
     for name, (res, args) in sig.items():
         fn = getattr(L, name)
@@ -135,3 +136,12 @@ def matvec_q8(ty, w, rows, cols, xq, xd, xs):
     if not lib().or_matvec_q8(ty, w.ctypes.data, rows, cols, xq.ctypes.data, xd.ctypes.data, xs.ctypes.data, y.ctypes.data):
         raise ValueError("unsupported type %d or shape" % ty)
     return y
+
+
+def rms(x, w, eps):
+    """cpu_ref::rms (src/cpu_ref.rs:32-36): x * (1 / sqrt(mean(x^2) + eps)) * w."""
+    x = np.ascontiguousarray(x, dtype=np.float32).reshape(-1)
+    w = np.ascontiguousarray(w, dtype=np.float32).reshape(-1)
+    o = np.empty_like(x)
+    lib().or_rms(x.ctypes.data, w.ctypes.data, o.ctypes.data, x.size, float(eps))
+    return o

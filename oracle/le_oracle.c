@@ -13,6 +13,7 @@
  *                           Q5_K :83-95, Q6_K :96-112, Q3_K :113-126, IQ3_XXS :127-141,
  *                           IQ2_XXS :142-154, IQ2_S :155-167)
  *   - quant_x               src/cuda/kernels.cu:15-25 (int8 activations per 32 values)
+ *   - rms                   src/cpu_ref.rs:32-36 (RMSNorm)
  *   - matvec_<ty> on int8 activations: udot<ty> per 32-value unit, src/cuda/kernels.cu:36-110,
  *                           summed per row in mv_impl's lane order, :371-392
  *   - Model::matvec         src/cpu_ref.rs:109-118 (per-row dequant, sequential f32 sum)
@@ -537,4 +538,14 @@ int or_matvec_q8(int ty, const uint8_t *w, size_t rows, size_t cols, const int8_
         y[r] = acc[0];
     }
     return 1;
+}
+
+/* cpu_ref::rms (src/cpu_ref.rs:32-36): ss = sequential f32 sum of x*x, divided by n; r = 1 / sqrt(ss + eps);
+ * o = x * r * w. */
+void or_rms(const float *x, const float *w, float *o, size_t n, float eps) {
+    float ss = 0.0f;
+    for (size_t i = 0; i < n; i++) ss += x[i] * x[i];
+    ss = ss / (float)n;
+    const float r = 1.0f / sqrtf(ss + eps);
+    for (size_t i = 0; i < n; i++) o[i] = x[i] * r * w[i];
 }

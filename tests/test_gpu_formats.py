@@ -162,3 +162,25 @@ def test_matvec_q8_slots_and_pointer_table(engine):
     for s in range(2):
         want = oracle.matvec_q8(ty, qs[s], rows, cols, *quant[s])
         np.testing.assert_allclose(got[s], want, rtol=1e-4, atol=1e-6 * np.abs(want).max())
+
+
+@pytest.mark.parametrize("n", [32, 4096, 14336])
+def test_rms_quant(engine, n):
+    """le_rms_quant: o within a few ulp of cpu_ref::rms (the sum of squares is reduced in another
+    order), and xq/xd/xs bit-identical to quant_x of that o."""
+    import torch
+    x = acts(n, 3 * n)
+    w = acts(n, 3 * n + 1)
+    o = torch.empty(n, dtype=torch.float32, device="cuda")
+    xq = torch.empty(n, dtype=torch.int8, device="cuda")
+    xd = torch.empty(n // 32, dtype=torch.float32, device="cuda")
+    xs = torch.empty(n // 32, dtype=torch.int32, device="cuda")
+    engine.rms_quant(dev(x), dev(w), o, xq, xd, xs, n, 1e-6)
+    sync()
+    og = o.cpu().numpy()
+    want = oracle.rms(x, w, 1e-6)
+    np.testing.assert_allclose(og, want, rtol=4e-6, atol=1e-7 * np.abs(want).max())
+    wq, wd, ws = oracle.quant_x(og)
+    assert np.array_equal(xq.cpu().numpy(), wq)
+    assert np.array_equal(xd.cpu().numpy().view(np.uint32), wd.view(np.uint32))
+    assert np.array_equal(xs.cpu().numpy(), ws)

@@ -183,3 +183,19 @@ def test_matvec_q8_vs_float64(ty, cols):
     # and the int8 mode tracks the fp32 oracle within the activation quantization error
     yf = oracle.matvec(ty, w, rows, cols, x)
     assert np.all(np.abs(y - yf) <= 0.02 * (np.abs(wd) @ np.abs(x.astype(np.float64))) + 1e-30)
+
+
+def test_rms_pins():
+    """or_rms against numpy: the strictly sequential float32 sum of squares (bit-identical), and
+    the float64 RMSNorm within a few ulp; constant input has the closed form w * c / sqrt(c^2 + eps)."""
+    rng = np.random.default_rng(11)
+    x = rng.normal(size=4096).astype(np.float32)
+    w = rng.normal(size=4096).astype(np.float32)
+    o = oracle.rms(x, w, 1e-6)
+    ss = np.add.accumulate(x * x, dtype=np.float32)[-1] / np.float32(4096)
+    r = np.float32(1.0) / np.sqrt(ss + np.float32(1e-6))
+    assert np.array_equal(o, (x * r) * w)
+    ref = x.astype(np.float64) / np.sqrt((x.astype(np.float64) ** 2).mean() + 1e-6) * w
+    assert np.allclose(o, ref, rtol=1e-5, atol=1e-6)
+    c = np.full(64, 3.0, dtype=np.float32)
+    np.testing.assert_allclose(oracle.rms(c, np.ones(64, np.float32), 0.0), np.ones(64), rtol=1e-6)
