@@ -233,6 +233,34 @@ def bench_moe(eng, n_tok, steps, warmup, n_exp=128, k=8, hidden=2048, ff=768, co
     return res
 
 
+def bench_moe_prefill(eng, n_tok, steps, warmup, n_exp=128, k=8, hidden=2048, ff=768, copies=2):
+    """Config 4's expert layer at prefill sizes (grouped matrix-core form): us per layer, tokens/s
+    and TFLOP/s over the routed gate/up/down products; `copies` expert sets rotated."""
+    import torch
+    import lastengine_amd as le
+    g = quantized(le.Q4_K, n_exp * ff, hidden, 201)
+    u = quantized(le.Q4_K, n_exp * ff, hidden, 202)
+    d = quantized(le.Q6_K, n_exp * hidden, ff, 203)
+    sets = [tuple(torch.from_numpy(a).cuda() for a in (g, u, d))]
+    sets += [tuple(t.clone() for t in sets[0]) for _ in range(copies - 1)]
+    del g, u, d
+    lg = torch.from_numpy(le.fill_normal(n_tok * n_exp, 400).reshape(n_tok, n_exp)).cuda()
+    h = torch.from_numpy(le.fill_normal(n_tok * hidden, 401)).cuda()
+    out = torch.empty(n_tok * hidden, dtype=torch.float32, device="cuda")
+    nws = max(eng.moe_workspace_size(n_tok, k, ff), eng.moe_prefill_workspace_size(n_tok, k, n_exp, hidden, ff))
+    ws = torch.zeros(nws, dtype=torch.uint8, device="cuda")
+
+    def record():
+        for gs, us_, ds in sets:
+            eng.moe(le.Q4_K, le.Q4_K, le.Q6_K, gs, us_, ds, n_exp, k, hidden, ff, lg, h, n_tok, out, ws=ws)
+    ms = graph_time(record, copies, steps, warmup, min_launches=8)
+    flops = 2.0 * n_tok * k * 3 * hidden * ff
+    del sets
+    torch.cuda.empty_cache()
+    return {"n_tok": n_tok, "us_per_layer": round(ms * 1e3, 2), "tok_per_s": round(n_tok / (ms * 1e-3), 0),
+            "TFLOP/s": round(flops / (ms * 1e-3) / 1e12, 2)}
+
+
 def host_cpu():
     """(CPU model, logical cores the OS reports)."""
     model = "unknown"
@@ -422,6 +450,10 @@ def main():
             r = bench_moe(eng, nt, max(64, steps2 // 4), 32)
             sec["moe_config4_ntok%d" % nt] = r
             log("moe", r)
+        for nt in (64, 512, 2048):
+            r = bench_moe_prefill(eng, nt, 16, 4)
+            sec["moe_config4_prefill_ntok%d" % nt] = r
+            log("moe prefill", r)
         r, _ = bench_matvec(eng, le.Q4_K, 4096, 4096, steps2, args.warmup // 4)
         sec["config1_q4k_4096x4096"] = {"us": round(r["us"], 3), "GB/s": round(r["gbs"], 1),
                                         "frac_hbm": round(r["gbs"] / HBM_PEAK_GBS, 4)}

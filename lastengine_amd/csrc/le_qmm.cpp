@@ -340,7 +340,15 @@ int mv_launch(le_ctx *c, int ty, const void *const *ptrs, const void *w, const f
         if ((size_t)(t * xb + tb) <= c->lds_limit) { T = t; break; }
     if ((size_t)(xb + tb) > c->lds_limit) return c->fail(LE_ERR_SHAPE, "cols=%d exceeds the LDS activation budget", cols);
     static const int kRW[5] = {0, 1, 2, 2, 4}, kCH[5] = {0, 2, 1, 2, 1};
-    int shape = c->mv_shape ? c->mv_shape : (S == 1 ? 4 : 3);
+    /* default (rows, steps) per lane: measured best at 14336 x 4096 (T = 1) for each type; the
+     * formats with three 16-byte loads per super-block and lane (Q5_K, Q3_K, IQ2_S) lose occupancy
+     * at 2 x 2 */
+    int shape = c->mv_shape;
+    if (!shape) {
+        if (ty == LE_TYPE_Q5_K || ty == LE_TYPE_Q3_K || ty == LE_TYPE_IQ2_S) shape = 2;
+        else if (ty == LE_TYPE_Q4_0) shape = 4;
+        else shape = S == 1 ? 4 : 3;
+    }
     if (T > 1 && shape < 3) shape = 3;
     const int RW = kRW[shape], CH = kCH[shape];
     const int block = T == 1 ? c->mv_block : 256;

@@ -122,6 +122,22 @@ def test_matvec_config_sizes(engine, name, rows, cols):
     check_close(y.cpu().numpy(), want, absmag(ty, q, rows, cols, x)[0])
 
 
+@pytest.mark.parametrize("name,rows,cols", FULL)
+def test_matvec_config_sizes_random_blocks(engine, name, rows, cols):
+    """The config shapes on arbitrary block bytes with bounded finite scales (every scale/min code,
+    negative Q6_K scales, every IQ grid index and sign pattern) through the staged kernels."""
+    import torch
+    from tests.util import random_blocks
+    ty = le.TYPES[name]
+    q = random_blocks(ty, rows, cols, seed=rows + cols + ty)
+    x = acts(cols, seed=cols + 1)
+    y = torch.empty(rows, dtype=torch.float32, device="cuda")
+    engine.mv(ty, dev(q), dev(x), y, rows, cols)
+    sync()
+    want = oracle.matvec(ty, q, rows, cols, x)
+    check_close(y.cpu().numpy(), want, absmag(ty, q, rows, cols, x)[0])
+
+
 # ------------------------------------------------------------------ small-M GEMM
 
 @pytest.mark.parametrize("name", NAMES)
@@ -196,9 +212,9 @@ def test_gemm_workspace_errors(engine):
 
 
 def test_gemm_config3_m512(engine):
-    """Config 3's largest M on a 2048-row slice of the 14336x4096 weight (rows are independent)."""
+    """Config 3's largest M at its full 14336x4096 shape (the benchmarked launch geometry)."""
     import torch
-    ty, rows, cols, m = le.Q4_K, 2048, 4096, 512
+    ty, rows, cols, m = le.Q4_K, 14336, 4096, 512
     q, _ = weights(ty, rows, cols, seed=3)
     xs = np.stack([acts(cols, 5000 + t) for t in range(m)])
     y = torch.empty(m, rows, dtype=torch.float32, device="cuda")
