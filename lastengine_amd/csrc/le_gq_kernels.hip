@@ -135,8 +135,9 @@ struct GqF<LE_TYPE_Q4_K> { /* slot: [0,16) header, [16,80) this half's 64 quant 
     __device__ static int loff(int k) { return 16 * k; }
 };
 template <>
-struct GqF<LE_TYPE_Q6_K> { /* slot: [0,64) ql half, [64,96) qh half, [96,112) sc[16], [112,128) bytes 194..209 (d at 126) */
-    static constexpr int SBB = 210, NCH = 8, SLOT = 128, SREC = 0, EPI = 1, TAB = 0;
+struct GqF<LE_TYPE_Q6_K> { /* slot: [0,64) ql half, [64,96) qh half, [96,112) sc[16], [112,128) bytes 194..209 (d at 126);
+                             * 144-byte stride: at 128 the 32 rows of a fragment read fell into two bank groups */
+    static constexpr int SBB = 210, NCH = 8, SLOT = 144, SREC = 0, EPI = 1, TAB = 0;
     static constexpr bool ALIGNED = false;
     __device__ static int goff(int k, int h) {
         return k < 4 ? 64 * h + 16 * k : k < 6 ? 128 + 32 * h + 16 * (k - 4) : k == 6 ? 192 : 194;
@@ -160,8 +161,9 @@ struct GqF<LE_TYPE_IQ2_XXS> { /* slot: [0,32) the half's four 8-byte block recor
     __device__ static int loff(int k) { return 16 * k; }
 };
 template <>
-struct GqF<LE_TYPE_IQ3_XXS> { /* slot: [0,32) the half's grid indices, [32,48) its four aux words, [48,64) bytes 0..15 (d at 48) */
-    static constexpr int SBB = 98, NCH = 4, SLOT = 64, SREC = 0, EPI = 1, TAB = 2048 + 2048;
+struct GqF<LE_TYPE_IQ3_XXS> { /* slot: [0,32) the half's grid indices, [32,48) its four aux words, [48,64) bytes 0..15 (d at 48);
+                                * 80-byte stride, as Q6_K's */
+    static constexpr int SBB = 98, NCH = 4, SLOT = 80, SREC = 0, EPI = 1, TAB = 2048 + 2048;
     static constexpr bool ALIGNED = false;
     __device__ static int goff(int k, int h) { return k < 2 ? 2 + 32 * h + 16 * k : k == 2 ? 66 + 16 * h : 0; }
     __device__ static int loff(int k) { return 16 * k; }

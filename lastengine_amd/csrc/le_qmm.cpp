@@ -885,10 +885,10 @@ static size_t gq_ws_bytes(int ty, int m, int cols) {
 static int gq_slot(int ty) {
     switch (ty) {
     case LE_TYPE_Q4_K: return 80;
-    case LE_TYPE_Q6_K: return 128;
+    case LE_TYPE_Q6_K: return 144;
     case LE_TYPE_Q8_0: return 192;
     case LE_TYPE_IQ2_XXS: return 48;
-    case LE_TYPE_IQ3_XXS: return 64;
+    case LE_TYPE_IQ3_XXS: return 80;
     }
     return 0;
 }
