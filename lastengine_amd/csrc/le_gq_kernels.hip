@@ -227,12 +227,32 @@ __device__ __forceinline__ void gq_xprep_body(const GqArgs &a, u8 *ws) {
         }
     }
     const LE_GLOBAL float *xr = (const LE_GLOBAL float *)(a.x + (live ? src : 0) * K);
+    /* up to K = 16384 every thread keeps its groups' values in registers between the max and the
+     * conversion: one read of the token, all of a thread's loads in flight at once */
+    constexpr int XG = 8;
+    const int ng = K / 8;
+    const bool inreg = ng <= 256 * XG;
+    float4 P[XG], Q[XG];
     float am = 0.f;
-    if (live)
+    if (inreg) {
+#pragma unroll
+        for (int i = 0; i < XG; i++) {
+            const int g = tid + 256 * i;
+            if (live && g < ng) {
+                P[i] = ((const LE_GLOBAL float4 *)xr)[2 * g];
+                Q[i] = ((const LE_GLOBAL float4 *)xr)[2 * g + 1];
+            } else {
+                P[i] = Q[i] = make_float4(0.f, 0.f, 0.f, 0.f);
+            }
+        }
+#pragma unroll
+        for (int i = 0; i < XG; i++) am = fmaxf(am, amax8(P[i], Q[i]));
+    } else if (live) {
         for (int i = tid; i < K / 4; i += 256) {
             const float4 v = ((const LE_GLOBAL float4 *)xr)[i];
             am = fmaxf(am, fmaxf(fmaxf(fabsf(v.x), fabsf(v.y)), fmaxf(fabsf(v.z), fabsf(v.w))));
         }
+    }
 #pragma unroll
     for (int o = 32; o > 0; o >>= 1) am = fmaxf(am, __shfl_xor(am, o));
     if (lane == 0) red[tid >> 6] = am;
@@ -248,13 +268,10 @@ __device__ __forceinline__ void gq_xprep_body(const GqArgs &a, u8 *ws) {
     const int tile = t >> 5, tl = t & 31;
     constexpr int SREC = SK == 1 ? 1024 : 2048;
     u8 *S = ws + gq_s_off(a.mp, K);
-    for (int g = tid; g < K / 8; g += 256) { /* group g = 8 values 8g..8g+7 = chunk g/2, half g&1 */
-        float v[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
-        if (live) {
-            const float4 p = ((const LE_GLOBAL float4 *)xr)[2 * g], q = ((const LE_GLOBAL float4 *)xr)[2 * g + 1];
-            v[0] = p.x * sc; v[1] = p.y * sc; v[2] = p.z * sc; v[3] = p.w * sc;
-            v[4] = q.x * sc; v[5] = q.y * sc; v[6] = q.z * sc; v[7] = q.w * sc;
-        }
+    /* group g = 8 values 8g..8g+7 = chunk g/2, half g&1. ng % 32 == 0 (K % 256 == 0), so the 2 or
+     * 4 lanes of one sum below are all inside or all outside ng */
+    auto convert = [&](int g, float4 p, float4 q) {
+        float v[8] = {p.x * sc, p.y * sc, p.z * sc, p.w * sc, q.x * sc, q.y * sc, q.z * sc, q.w * sc};
         const le_h2 h0 = {(_Float16)v[0], (_Float16)v[2]}, h1 = {(_Float16)v[1], (_Float16)v[3]};
         const le_h2 h2 = {(_Float16)v[4], (_Float16)v[6]}, h3 = {(_Float16)v[5], (_Float16)v[7]};
         const size_t off = ((((size_t)tile * (K / 16) + (g >> 1)) * 2 + (g & 1)) * 32 + tl) * 8;
@@ -285,6 +302,22 @@ __device__ __forceinline__ void gq_xprep_body(const GqArgs &a, u8 *ws) {
                     rec[512 + ((j >> 3) * 32 + tl) * 8 + pj] = lo;
                 }
             }
+        }
+    };
+    if (inreg) {
+#pragma unroll
+        for (int i = 0; i < XG; i++) {
+            const int g = tid + 256 * i;
+            if (g < ng) convert(g, P[i], Q[i]);
+        }
+    } else {
+        for (int g = tid; g < ng; g += 256) {
+            float4 p = make_float4(0.f, 0.f, 0.f, 0.f), q = p;
+            if (live) {
+                p = ((const LE_GLOBAL float4 *)xr)[2 * g];
+                q = ((const LE_GLOBAL float4 *)xr)[2 * g + 1];
+            }
+            convert(g, p, q);
         }
     }
     if (tid == 0) {
