@@ -162,8 +162,11 @@ def bench_layer(eng, mats, steps, warmup):
 
     def record():
         for k in range(ncopy):
-            for i, (_, ty, r, c) in enumerate(mats):
-                eng.mv(ty, devs[i][k], xs[c], ys[i], r, c)
+            for i, (name, ty, r, c) in enumerate(mats):
+                if name == "down_swiglu":  # SwiGLU of the previous (gate | up) output fused into the down matvec
+                    eng.mv_swiglu(ty, devs[i][k], ys[i - 1], ys[i], r, c)
+                else:
+                    eng.mv(ty, devs[i][k], xs[c], ys[i], r, c)
     ms = graph_time(record, ncopy, steps, warmup, min_launches=40)
     alg = total + sum(4 * (r + c) for (_, _, r, c) in mats)
     return {"us": round(ms * 1e3, 3), "GB/s": round(alg / (ms * 1e-3) / 1e9, 1),
@@ -459,9 +462,10 @@ def main():
                                         "frac_hbm": round(r["gbs"] / HBM_PEAK_GBS, 4)}
         log("config1", sec["config1_q4k_4096x4096"])
         # the reference's dense decode layer: q, k, v, o, gate and up as one matrix of
-        # concatenated rows (src/gpu/dense.rs:13,67-73,309), down
+        # concatenated rows (src/gpu/dense.rs:13,67-73,309), then down on silu(gate) * up formed
+        # inside the down matvec (swiglu_gu + quant_x + matvec_14 in the reference, :310-312)
         layer = [("wq", le.Q4_K, 4096, 4096), ("wk", le.Q4_K, 1024, 4096), ("wv", le.Q4_K, 1024, 4096),
-                 ("wo", le.Q4_K, 4096, 4096), ("gate_up", le.Q4_K, 28672, 4096), ("down", le.Q6_K, 4096, 14336)]
+                 ("wo", le.Q4_K, 4096, 4096), ("gate_up", le.Q4_K, 28672, 4096), ("down_swiglu", le.Q6_K, 4096, 14336)]
         sec["config2_llama3_8b_layer"] = bench_layer(eng, layer, max(40, steps2 // 8), 8)
         log("config2 layer", sec["config2_llama3_8b_layer"])
         sec["config2_q8_0_head_32000x4096"] = bench_layer(eng, [("head", le.Q8_0, 32000, 4096)], max(40, steps2 // 8), 8)

@@ -114,6 +114,17 @@ int le_dequant_rows(le_ctx *ctx, int ty, const void *w, float *out, int rows, in
 int le_matvec(le_ctx *ctx, int ty, const void *const *ptrs, const void *w, const float *x, long long xstride,
               float *y, int rows, int cols, int slots, le_stream_t stream);
 
+/* ---- SwiGLU fused into the down projection (replaces swiglu_gu + quant_x + matvec_<ty>,
+ *      src/cuda/kernels.cu:430-435, DenseGpu's FFN tail src/gpu/dense.rs:309-312, and swiglu + the
+ *      down mv_ptrs of the MoE block src/gpu.rs:594-597) ----
+ * le_matvec with the activation of slot s formed inside the kernel from a gate | up vector:
+ * a[c] = silu(gu[c]) * gu[cols + c] for c < cols, gu = gu_base + s * xstride (xstride 0 shares one
+ * vector, else >= 2 * cols), silu(g) = g / (1 + exp(-g)). gu is exactly the output of the
+ * concatenated gate+up matvec (rows 0..cols-1 gate, cols..2 cols-1 up), so the FFN's middle
+ * vector is never written. Same types, limits and numerics as le_matvec. */
+int le_matvec_swiglu(le_ctx *ctx, int ty, const void *const *ptrs, const void *w, const float *gu, long long xstride,
+                     float *y, int rows, int cols, int slots, le_stream_t stream);
+
 /* ---- int8 activation mode: the reference's own GPU numerics (optional; not the fp32-parity path) ----
  * le_quant_x replaces quant_x (src/cuda/kernels.cu:15-25) as launched by Gpu::qx (src/gpu.rs:223-226):
  * for u < n_units, xd[u] = max|x[32u..32u+31]| / 127, xq[32u+l] = x[32u+l] * (1 / xd[u]) rounded to

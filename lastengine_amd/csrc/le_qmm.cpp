@@ -34,7 +34,7 @@ struct MvArgs {
     long long x_slot, x_tok;
     float *y;
     long long y_slot, y_tok;
-    int rows, cols, ntok, pad;
+    int rows, cols, ntok, swiglu;
     const int8_t *xq8;
     const float *xd8;
 };
@@ -214,7 +214,7 @@ int pick_g(int nsb) {
 
 /* MFMA decode matvec (Q4_K, Q6_K): one block of mq_waves waves per 16-row tile at a time. */
 int mq_launch(le_ctx *c, int ty, const void *const *ptrs, const void *w, const float *x, long long x_slot, float *y,
-              long long y_slot, int rows, int cols, int slots, hipStream_t st) {
+              long long y_slot, int rows, int cols, int slots, hipStream_t st, int swiglu = 0) {
     const long long ntile = (rows + 15) / 16;
     const int nsb = cols / 256, U = c->mq_steps;
     /* when the row tiles alone leave CUs idle, split K over twice the waves (shorter chains) */
@@ -235,6 +235,7 @@ int mq_launch(le_ctx *c, int ty, const void *const *ptrs, const void *w, const f
     a.rows = rows;
     a.cols = cols;
     a.ntok = 1;
+    a.swiglu = swiglu;
     void *args[] = {&a};
     char name[64];
     size_t lds = (size_t)nsb * 608 + (size_t)NW * 64;
@@ -251,7 +252,9 @@ int mq_launch(le_ctx *c, int ty, const void *const *ptrs, const void *w, const f
             return c->launch(name, dim3((unsigned)gx, (unsigned)slots), NWs * 64, lds, st, args);
         lds = (size_t)nsb * 608 + (size_t)NW * 64;
     }
-    if (ty != LE_TYPE_Q4_K) return 1; /* no unstaged MFMA variant: the caller falls back */
+    /* no unstaged MFMA variant for the other types, nor one that forms silu(gate) * up: the caller
+     * falls back to the vector kernels */
+    if (ty != LE_TYPE_Q4_K || swiglu) return 1;
     snprintf(name, sizeof name, "le_mq_12_w%d_u%d", NW, U);
     return c->launch(name, dim3((unsigned)gx, (unsigned)slots), NW * 64, lds, st, args);
 }
@@ -309,7 +312,7 @@ int ms_t_launch(le_ctx *c, const void *const *ptrs, const void *w, const float *
 int mv_launch(le_ctx *c, int ty, const void *const *ptrs, const void *w, const float *x, long long x_slot,
               long long x_tok, float *y, long long y_slot, long long y_tok, int rows, int cols, int ntok, int slots,
               hipStream_t st,
-              const int8_t *xq8 = nullptr, const float *xd8 = nullptr) {
+              const int8_t *xq8 = nullptr, const float *xd8 = nullptr, int swiglu = 0) {
     if (!supported_mv(ty)) return c->fail(LE_ERR_TYPE, "no kernel for type %d", ty);
     if (rows <= 0 || cols <= 0 || ntok <= 0 || slots <= 0) return c->fail(LE_ERR_SHAPE, "empty shape");
     if (cols % 256) return c->fail(LE_ERR_SHAPE, "cols=%d is not a multiple of 256", cols);
@@ -326,7 +329,7 @@ int mv_launch(le_ctx *c, int ty, const void *const *ptrs, const void *w, const f
     const bool iq = ty == LE_TYPE_IQ2_XXS || ty == LE_TYPE_IQ3_XXS;
     if (!q8 && (ty == LE_TYPE_Q4_K || (ty == LE_TYPE_Q6_K && c->mq6) || (iq && c->mqiq)) && ntok == 1 && c->mq &&
         (size_t)nsb * 608 + 1024 <= c->lds_limit) {
-        const int rc = mq_launch(c, ty, ptrs, w, x, x_slot, y, y_slot, rows, cols, slots, st);
+        const int rc = mq_launch(c, ty, ptrs, w, x, x_slot, y, y_slot, rows, cols, slots, st, swiglu);
         if (rc != 1) return rc;
     }
     if (!q8 && ty == LE_TYPE_Q4_K && ntok >= 2 && c->mq && c->ms && c->ms_t) {
@@ -379,6 +382,7 @@ int mv_launch(le_ctx *c, int ty, const void *const *ptrs, const void *w, const f
     char name[96];
     a.xq8 = xq8;
     a.xd8 = xd8;
+    a.swiglu = swiglu;
     snprintf(name, sizeof name, "le_mv_%d_g%d_t%d_r%d_c%d_b%d%s", ty, G, T, RW, CH, block, q8 ? "_q8" : "");
     return c->launch(name, dim3((unsigned)gx, (unsigned)slots, (unsigned)((ntok + T - 1) / T)), block,
                      (size_t)(T * xb + tb), st, args);
@@ -603,6 +607,15 @@ int le_matvec(le_ctx *c, int ty, const void *const *ptrs, const void *w, const f
               int rows, int cols, int slots, le_stream_t stream) {
     if (!c) return LE_ERR_ARG;
     return mv_launch(c, ty, ptrs, w, x, xstride, 0, y, (long long)rows, 0, rows, cols, 1, slots, (hipStream_t)stream);
+}
+
+int le_matvec_swiglu(le_ctx *c, int ty, const void *const *ptrs, const void *w, const float *gu, long long xstride,
+                     float *y, int rows, int cols, int slots, le_stream_t stream) {
+    if (!c) return LE_ERR_ARG;
+    if (slots > 1 && xstride != 0 && xstride < 2LL * cols)
+        return c->fail(LE_ERR_SHAPE, "xstride must be 0 or at least 2 * cols (gate and up of one slot)");
+    return mv_launch(c, ty, ptrs, w, gu, xstride, 0, y, (long long)rows, 0, rows, cols, 1, slots, (hipStream_t)stream,
+                     nullptr, nullptr, 1);
 }
 
 int le_quant_x(le_ctx *c, const float *x, int8_t *xq, float *xd, int32_t *xs, int n_units, le_stream_t stream) {

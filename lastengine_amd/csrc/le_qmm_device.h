@@ -150,8 +150,16 @@ __device__ __forceinline__ float amax8(float4 a, float4 b) {
 
 /* Quantize one token's K activations (K % 32 == 0) into the LDS image. Called by all threads of
  * the block; 4 consecutive threads share a 32-value unit. */
+/* silu(g) * u per component (the reference's swiglu, src/cuda/kernels.cu:7,428) */
+__device__ __forceinline__ float4 le_silu_mul4(float4 g, float4 u) {
+    return make_float4(g.x / (1.0f + __expf(-g.x)) * u.x, g.y / (1.0f + __expf(-g.y)) * u.y, g.z / (1.0f + __expf(-g.z)) * u.z,
+                       g.w / (1.0f + __expf(-g.w)) * u.w);
+}
+
+/* up != nullptr: the activation is silu(x) * up (le_matvec_swiglu). */
 template <int XL>
-__device__ __forceinline__ void le_quant_x_lds(const float *__restrict__ x, int K, uint4 *xq, float2 *xs) {
+__device__ __forceinline__ void le_quant_x_lds(const float *__restrict__ x, int K, uint4 *xq, float2 *xs,
+                                               const float *__restrict__ up = nullptr) {
     const int ng = K >> 3;
     const LE_GLOBAL float *xg = (const LE_GLOBAL float *)x;
     for (int p = threadIdx.x; p < ((ng + 3) & ~3); p += blockDim.x) {
@@ -160,6 +168,10 @@ __device__ __forceinline__ void le_quant_x_lds(const float *__restrict__ x, int 
         if (ok) {
             a = *(const LE_GLOBAL float4 *)(xg + 8 * p);
             b = *(const LE_GLOBAL float4 *)(xg + 8 * p + 4);
+            if (up) {
+                a = le_silu_mul4(a, *(const LE_GLOBAL float4 *)(up + 8 * p));
+                b = le_silu_mul4(b, *(const LE_GLOBAL float4 *)(up + 8 * p + 4));
+            }
         }
         float am = amax8(a, b);
         am = fmaxf(am, __shfl_xor(am, 1));
@@ -175,7 +187,8 @@ __device__ __forceinline__ void le_quant_x_lds(const float *__restrict__ x, int 
 template <int BLOCK, int XR>
 struct XLoad {
     float4 a[XR], b[XR];
-    __device__ __forceinline__ void load(const float *__restrict__ x, int K) {
+    /* up != nullptr: the activation is silu(x) * up, formed at load (le_matvec_swiglu) */
+    __device__ __forceinline__ void load(const float *__restrict__ x, int K, const float *__restrict__ up = nullptr) {
         const int ng = K >> 3;
         const LE_GLOBAL float *xg = (const LE_GLOBAL float *)x;
 #pragma unroll
@@ -183,6 +196,23 @@ struct XLoad {
             const int p = min((int)threadIdx.x + r * BLOCK, ng - 1);
             a[r] = *(const LE_GLOBAL float4 *)(xg + 8 * p);
             b[r] = *(const LE_GLOBAL float4 *)(xg + 8 * p + 4);
+        }
+        /* issued either way (without up: a cached re-read of x), so the wait counts of the
+         * kernel do not depend on the mode */
+        const LE_GLOBAL float *ug = (const LE_GLOBAL float *)(up ? up : x);
+        float4 ua[XR], ub[XR];
+#pragma unroll
+        for (int r = 0; r < XR; r++) {
+            const int p = min((int)threadIdx.x + r * BLOCK, ng - 1);
+            ua[r] = *(const LE_GLOBAL float4 *)(ug + 8 * p);
+            ub[r] = *(const LE_GLOBAL float4 *)(ug + 8 * p + 4);
+        }
+        if (up) {
+#pragma unroll
+            for (int r = 0; r < XR; r++) {
+                a[r] = le_silu_mul4(a[r], ua[r]);
+                b[r] = le_silu_mul4(b[r], ub[r]);
+            }
         }
     }
     template <int XL>

@@ -325,7 +325,8 @@ struct MvArgs {
     long long x_slot, x_tok;
     float *y;
     long long y_slot, y_tok;
-    int rows, cols, ntok, pad;
+    int rows, cols, ntok;
+    int swiglu; /* 1: the activation is silu(x[0, cols)) * x[cols, 2 cols) (le_matvec_swiglu) */
     /* int8 activation mode (le_matvec_q8): xq8 + s * x_slot values, xd8 + s * x_slot / 32 scales */
     const int8_t *xq8;
     const float *xd8;
@@ -452,13 +453,16 @@ __device__ __forceinline__ void mv_body(const MvArgs &a) {
         }
     } else if (T == 1 && ng <= XR * BLOCK) {
         XLoad<BLOCK, XR> xl;
-        xl.load(a.x + a.x_slot * slot + a.x_tok * t0, K);
+        const float *x0 = a.x + a.x_slot * slot + a.x_tok * t0;
+        xl.load(x0, K, a.swiglu ? x0 + K : nullptr);
         if (rbk < nrb) issue(ra, rbk, 0);
         xl.template store<F::XL>(K, xq, xs);
     } else {
         if (rbk < nrb) issue(ra, rbk, 0);
-        for (int t = 0; t < nt; t++)
-            le_quant_x_lds<F::XL>(a.x + a.x_slot * slot + a.x_tok * (t0 + t), K, xq + t * ng, xs + t * ng);
+        for (int t = 0; t < nt; t++) {
+            const float *xt_ = a.x + a.x_slot * slot + a.x_tok * (t0 + t);
+            le_quant_x_lds<F::XL>(xt_, K, xq + t * ng, xs + t * ng, a.swiglu ? xt_ + K : nullptr);
+        }
     }
     u32 *tab = (u32 *)((float2 *)(smem + T * ng) + T * ng);
     load_tables<TY>(tab);
@@ -573,6 +577,19 @@ __device__ __forceinline__ void mq_load_seg(const float *__restrict__ x, int e, 
     const LE_GLOBAL float4 *xg = (const LE_GLOBAL float4 *)x;
 #pragma unroll
     for (int i = 0; i < 4; i++) v4[i] = xg[4 * e + i];
+}
+/* A decode kernel's activation segment: x itself, or with `swiglu` silu(gate) * up from a
+ * gate | up vector (gate at x[0, K), up at x[K, 2K)); the flag is uniform over the launch. The
+ * second load is issued either way (without swiglu it re-reads the segment from cache), so the
+ * kernels' wait counts do not depend on the flag. */
+__device__ __forceinline__ void mq_load_seg_a(const float *__restrict__ x, int e, int K, bool swiglu, float4 (&v4)[4]) {
+    float4 u[4];
+    mq_load_seg(x, e, v4);
+    mq_load_seg(x + (swiglu ? K : 0), e, u);
+    if (swiglu) {
+#pragma unroll
+        for (int i = 0; i < 4; i++) v4[i] = le_silu_mul4(v4[i], u[i]);
+    }
 }
 /* MAP 0 (Q4_K): slice s of MFMA b is sub-block j(b,s) = 4*(b>>1) + 2*(s>>1) + (b&1), positions
  * 16*(s&1)..; MAP 1 (Q6_K): MFMA b = (half b>>1, 16-value index b&1), slice s = quarter, so
@@ -944,11 +961,11 @@ __device__ __forceinline__ void ms_q4k_body(const MvArgs &a) {
         return ((ls / P) * sstep + sfirst + ls % P) * 16 + (el & 15);
     };
     float4 xv[4];
-    mq_load_seg(xs, gseg(min(lane, nsegw - 1)), xv);
+    mq_load_seg_a(xs, gseg(min(lane, nsegw - 1)), a.cols, a.swiglu, xv);
     issue(min((int)blockIdx.x, ntile - 1), active ? sfirst : 0); /* unpredicated: exact wait counts */
     mq_quant_seg(lane, lane < nsegw, xv, rec, dxp, fsv);
     for (int el = lane + 64; el < nsegw; el += 64) {
-        mq_load_seg(xs, gseg(el), xv);
+        mq_load_seg_a(xs, gseg(el), a.cols, a.swiglu, xv);
         mq_quant_seg(el, true, xv, rec, dxp, fsv);
     }
 
@@ -1231,11 +1248,11 @@ __device__ __forceinline__ void ms_q6k_body(const MvArgs &a) {
         return ((ls / P) * sstep + sfirst + ls % P) * 16 + (el & 15);
     };
     float4 xv[4];
-    mq_load_seg(xs, gseg(min(lane, nsegw - 1)), xv);
+    mq_load_seg_a(xs, gseg(min(lane, nsegw - 1)), a.cols, a.swiglu, xv);
     issue(min((int)blockIdx.x, ntile - 1), active ? sfirst : 0);
     mq_quant_seg<1>(lane, lane < nsegw, xv, rec, dxp, fsv);
     for (int el = lane + 64; el < nsegw; el += 64) {
-        mq_load_seg(xs, gseg(el), xv);
+        mq_load_seg_a(xs, gseg(el), a.cols, a.swiglu, xv);
         mq_quant_seg<1>(el, true, xv, rec, dxp, fsv);
     }
 
@@ -1394,11 +1411,11 @@ __device__ __forceinline__ void ms_iq_body(const MvArgs &a) {
         return ((ls / P) * sstep + sfirst + ls % P) * 16 + (el & 15);
     };
     float4 xv[4];
-    mq_load_seg(xs, gseg(min(lane, nsegw - 1)), xv);
+    mq_load_seg_a(xs, gseg(min(lane, nsegw - 1)), a.cols, a.swiglu, xv);
     issue(min((int)blockIdx.x, ntile - 1), active ? sfirst : 0);
     mq_quant_seg<0>(lane, lane < nsegw, xv, rec, dxp, fsv);
     for (int el = lane + 64; el < nsegw; el += 64) {
-        mq_load_seg(xs, gseg(el), xv);
+        mq_load_seg_a(xs, gseg(el), a.cols, a.swiglu, xv);
         mq_quant_seg<0>(el, true, xv, rec, dxp, fsv);
     }
     __syncthreads(); /* the tables */

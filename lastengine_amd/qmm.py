@@ -64,6 +64,7 @@ def lib():
         "le_dequant_rows": (I, [P, I, P, P, I, I, P]),
         "le_matvec": (I, [P, I, P, P, P, LL, P, I, I, I, P]),
         "le_quant_x": (I, [P, P, P, P, P, I, P]),
+        "le_matvec_swiglu": (I, [P, I, P, P, P, LL, P, I, I, I, P]),
         "le_rms_quant": (I, [P, P, P, P, P, P, P, I, F, P]),
         "le_matvec_q8": (I, [P, I, P, P, P, P, P, LL, P, I, I, I, P]),
         "le_gemm_workspace_size": (S, [I, I, I]),
@@ -184,6 +185,11 @@ class Engine:
         """Gpu::mv_ptrs (src/gpu.rs:228): out[s*rows + r] = W_s[r] . x[s*xstride:]."""
         self._check(self._L.le_matvec(self._ctx, ty, _ptr(ptrs), _ptr(w), _ptr(x), int(xstride), _ptr(out), rows,
                                       cols, slots, _stream(stream)))
+
+    def mv_swiglu(self, ty, w, gu, out, rows, cols, ptrs=None, xstride=0, slots=1, stream=None):
+        """swiglu_gu + down matvec in one launch: out = W . (silu(gu[:cols]) * gu[cols:2 cols])."""
+        self._check(self._L.le_matvec_swiglu(self._ctx, ty, _ptr(ptrs), _ptr(w), _ptr(gu), int(xstride), _ptr(out), rows,
+                                             cols, slots, _stream(stream)))
 
     def quant_x(self, x, xq, xd, xs, n_units, stream=None):
         """Gpu::qx / quant_x (src/gpu.rs:223, src/cuda/kernels.cu:15-25): int8 activations per 32 values."""

@@ -35,6 +35,7 @@ def lib():
         "or_quant_x": (None, [P, P, P, P, S]),
         "or_matvec_q8": (I, [I, P, S, S, P, P, P, P]),
         "or_rms": (None, [P, P, P, S, F]),
+        "or_swiglu": (None, [P, P, P, S]),
     }
     for name, (res, args) in sig.items():
         fn = getattr(L, name)
@@ -144,4 +145,13 @@ def rms(x, w, eps):
     w = np.ascontiguousarray(w, dtype=np.float32).reshape(-1)
     o = np.empty_like(x)
     lib().or_rms(x.ctypes.data, w.ctypes.data, o.ctypes.data, x.size, float(eps))
+    return o
+
+
+def swiglu(g, u):
+    """silu(g) * u as cpu_ref computes it (src/cpu_ref.rs:37,255)."""
+    g = np.ascontiguousarray(g, dtype=np.float32).reshape(-1)
+    u = np.ascontiguousarray(u, dtype=np.float32).reshape(-1)
+    o = np.empty_like(g)
+    lib().or_swiglu(g.ctypes.data, u.ctypes.data, o.ctypes.data, g.size)
     return o

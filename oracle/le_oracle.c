@@ -14,6 +14,7 @@
  *                           IQ2_XXS :142-154, IQ2_S :155-167)
  *   - quant_x               src/cuda/kernels.cu:15-25 (int8 activations per 32 values)
  *   - rms                   src/cpu_ref.rs:32-36 (RMSNorm)
+ *   - swiglu                src/cpu_ref.rs:37 silu, applied as silu(g) * u (:255)
  *   - matvec_<ty> on int8 activations: udot<ty> per 32-value unit, src/cuda/kernels.cu:36-110,
  *                           summed per row in mv_impl's lane order, :371-392
  *   - Model::matvec         src/cpu_ref.rs:109-118 (per-row dequant, sequential f32 sum)
@@ -548,4 +549,9 @@ void or_rms(const float *x, const float *w, float *o, size_t n, float eps) {
     ss = ss / (float)n;
     const float r = 1.0f / sqrtf(ss + eps);
     for (size_t i = 0; i < n; i++) o[i] = x[i] * r * w[i];
+}
+
+/* SwiGLU of cpu_ref (src/cpu_ref.rs:37 silu, applied as silu(g) * u at :255): o = g / (1 + exp(-g)) * u. */
+void or_swiglu(const float *g, const float *u, float *o, size_t n) {
+    for (size_t i = 0; i < n; i++) o[i] = g[i] / (1.0f + expf(-g[i])) * u[i];
 }

@@ -184,3 +184,41 @@ def test_rms_quant(engine, n):
     assert np.array_equal(xq.cpu().numpy(), wq)
     assert np.array_equal(xd.cpu().numpy().view(np.uint32), wd.view(np.uint32))
     assert np.array_equal(xs.cpu().numpy(), ws)
+
+
+SWIGLU_SHAPES = [("Q6_K", 4096, 14336), ("Q4_K", 4096, 14336), ("Q4_K", 333, 1024), ("Q8_0", 200, 4096),
+                 ("IQ2_XXS", 64, 4096), ("IQ3_XXS", 96, 2048), ("Q4_0", 100, 768), ("Q3_K", 64, 2048),
+                 ("Q5_K", 77, 4096), ("IQ2_S", 50, 1024)]
+
+
+@pytest.mark.parametrize("name,rows,cols", SWIGLU_SHAPES)
+def test_matvec_swiglu(engine, name, rows, cols):
+    """le_matvec_swiglu against cpu_ref: down . (silu(gate) * up) from one gate | up vector (the
+    Q6_K 4096x14336 case is config 2's down projection on the staged matrix-core kernel)."""
+    import torch
+    ty = le.MV_TYPES[name]
+    q = random_blocks(ty, rows, cols, seed=ty + rows + cols)
+    gu = acts(2 * cols, 31 + cols)
+    y = torch.full((rows,), float("nan"), device="cuda")
+    engine.mv_swiglu(ty, dev(q), dev(gu), y, rows, cols)
+    sync()
+    a = oracle.swiglu(gu[:cols], gu[cols:])
+    want = oracle.matvec(ty, q, rows, cols, a)
+    check_close(y.cpu().numpy(), want, _absmag(ty, q, rows, cols, a)[0])
+
+
+def test_matvec_swiglu_slots(engine):
+    """Two slots through a pointer table, each with its own gate | up vector (xstride = 2 cols)."""
+    import torch
+    ty, rows, cols = le.Q6_K, 256, 768
+    qs = [random_blocks(ty, rows, cols, seed=900 + s) for s in range(2)]
+    gus = [acts(2 * cols, 910 + s) for s in range(2)]
+    dws = [dev(q) for q in qs]
+    ptrs = dev(np.array([w.data_ptr() for w in dws], dtype=np.uint64))
+    y = torch.full((2 * rows,), float("nan"), device="cuda")
+    engine.mv_swiglu(ty, None, dev(np.concatenate(gus)), y, rows, cols, ptrs=ptrs, xstride=2 * cols, slots=2)
+    sync()
+    got = y.cpu().numpy().reshape(2, rows)
+    for s in range(2):
+        a = oracle.swiglu(gus[s][:cols], gus[s][cols:])
+        check_close(got[s], oracle.matvec(ty, qs[s], rows, cols, a), _absmag(ty, qs[s], rows, cols, a)[0])

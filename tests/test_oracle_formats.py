@@ -199,3 +199,16 @@ def test_rms_pins():
     assert np.allclose(o, ref, rtol=1e-5, atol=1e-6)
     c = np.full(64, 3.0, dtype=np.float32)
     np.testing.assert_allclose(oracle.rms(c, np.ones(64, np.float32), 0.0), np.ones(64), rtol=1e-6)
+
+
+def test_swiglu_pins():
+    """or_swiglu against a float64 silu(g) * u within float32 rounding, and its closed forms
+    (silu(0) = 0, silu(g) -> g for large g, -> 0 for very negative g)."""
+    rng = np.random.default_rng(12)
+    g = (rng.normal(size=4096) * 4).astype(np.float32)
+    u = rng.normal(size=4096).astype(np.float32)
+    o = oracle.swiglu(g, u)
+    ref = g.astype(np.float64) / (1 + np.exp(-g.astype(np.float64))) * u
+    assert np.allclose(o, ref, rtol=2e-6, atol=1e-30)
+    z = oracle.swiglu(np.array([0.0, 60.0, -60.0], np.float32), np.ones(3, np.float32))
+    assert z[0] == 0.0 and z[1] == np.float32(60.0) and abs(z[2]) < 1e-20
