@@ -226,6 +226,10 @@ __device__ __forceinline__ void gq_xprep_body(const GqArgs &a, u8 *ws) {
             }
         }
     }
+    /* grouped form: a tile position without a pair writes nothing. Its activation rows, sums and
+     * scale are never combined with a valid row (an MFMA output row depends on its own A row
+     * only) and its outputs are not stored, so whatever the workspace holds there is harmless. */
+    if (GR && !live) return;
     const LE_GLOBAL float *xr = (const LE_GLOBAL float *)(a.x + (live ? src : 0) * K);
     /* up to K = 16384 every thread keeps its groups' values in registers between the max and the
      * conversion: one read of the token, all of a thread's loads in flight at once */
