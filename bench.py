@@ -180,7 +180,7 @@ def bench_gemm(eng, ty, rows, cols, mtok, steps, warmup, seed=3):
     bufs = device_copies(host)
     x = torch.from_numpy(le.fill_normal(mtok * cols, seed + 1)).cuda()
     y = torch.empty(mtok * rows, dtype=torch.float32, device="cuda")
-    ws = torch.empty(max(16, eng.gemm_workspace_size(ty, mtok, cols)), dtype=torch.uint8, device="cuda")
+    ws = torch.empty(max(16, eng.gemm_workspace_size_rows(ty, mtok, rows, cols)), dtype=torch.uint8, device="cuda")
 
     def record():
         for b in bufs:
@@ -377,7 +377,7 @@ def probe(eng, name, launches=100, copy_bytes=256 << 20):
         x = torch.from_numpy(le.fill_normal(mtok * cols, 2)).cuda()
         y = torch.empty(mtok * rows, dtype=torch.float32, device="cuda")
         if kind == "gemm":
-            ws = torch.empty(max(16, eng.gemm_workspace_size(ty, mtok, cols)), dtype=torch.uint8, device="cuda")
+            ws = torch.empty(max(16, eng.gemm_workspace_size_rows(ty, mtok, rows, cols)), dtype=torch.uint8, device="cuda")
         for i in range(launches):
             if kind == "mv":
                 eng.mv(ty, bufs[i % len(bufs)], x, y, rows, cols)

@@ -162,6 +162,11 @@ int le_matvec_q8(le_ctx *ctx, int ty, const void *const *ptrs, const void *w, co
  * where (q - 32) * sc has more than 11 significant bits). The 3..16-token Q4_K kernel rounds
  * unscaled activations to fp16 (|x| < 65504, 32-value sums < 65504). */
 size_t le_gemm_workspace_size(int ty, int m, int cols);
+/* Workspace with room for the K slices' partial results as well (no counterpart in the reference,
+ * whose GEMM never splits K): shapes with few row and token tiles are split along K to fill the
+ * GPU, and with this much workspace the slices are summed in a second pass in a fixed order
+ * (bit-reproducible), instead of adding into y atomically. At least le_gemm_workspace_size. */
+size_t le_gemm_workspace_size_rows(int ty, int m, int rows, int cols);
 int le_gemm(le_ctx *ctx, int ty, const void *w, const float *x, int m, float *y, int rows, int cols, void *ws,
             size_t ws_bytes, le_stream_t stream);
 

@@ -59,7 +59,8 @@ struct GqArgs {
     float *y;
     int rows, cols, m;
     int mp;     /* tokens rounded up to the largest token tile (the pre-pass pads with zeros) */
-    int ksplit; /* K slices (blockIdx.y), > 1: atomic adds into y, cleared by the pre-pass */
+    int ksplit; /* K slices (blockIdx.y); > 1: partial sums into part (then le_gq_ksum), or, with no
+                 * part buffer, atomic adds into y, cleared by the pre-pass */
     /* grouped form (le_mm_grouped): slot s multiplies weight ptrs[s] (or w + s * w_slot_bytes)
      * with the activation rows in_idx[i] of its pairs i in off[s] .. off[s+1], writing output rows
      * out_idx[i]; the plan kernel lists (slot, first pair) token tiles of bm pairs in the workspace */
@@ -67,6 +68,7 @@ struct GqArgs {
     unsigned long long w_slot_bytes;
     const int *off, *in_idx, *out_idx;
     int nslot, maxt, bm, pad;
+    float *part; /* [ksplit][m][rows] partial results of the K slices, or null */
 };
 
 /* Workspace layout: A planes (mp * K halves), S records (mp/32 * nsb * SREC bytes), token scales
@@ -207,9 +209,13 @@ template <int SK, bool GR = false>
 __device__ __forceinline__ void gq_xprep_body(const GqArgs &a, u8 *ws) {
     __shared__ float red[4];
     const int K = a.cols, nsb = K >> 8, t = blockIdx.x, tid = threadIdx.x, lane = tid & 63;
-    if (!GR && a.ksplit > 1) { /* the slices add into y */
-        const size_t ny = (size_t)a.m * a.rows;
-        for (size_t i = (size_t)blockIdx.x * blockDim.x + tid; i < ny; i += (size_t)gridDim.x * blockDim.x) a.y[i] = 0.f;
+    if (!GR && a.ksplit > 1 && !a.part) { /* the slices add into y */
+        const size_t ny = (size_t)a.m * a.rows, st = (size_t)gridDim.x * blockDim.x;
+        size_t i = (size_t)blockIdx.x * blockDim.x + tid;
+        if ((ny & 3) == 0 && ((size_t)a.y & 15) == 0)
+            for (; i < ny / 4; i += st) ((float4 *)a.y)[i] = make_float4(0.f, 0.f, 0.f, 0.f);
+        else
+            for (; i < ny; i += st) a.y[i] = 0.f;
     }
     bool live = t < a.m;
     size_t src = t;
@@ -376,8 +382,9 @@ __device__ __forceinline__ void gq_body(const GqArgs &a, const u8 *ws) {
         uint4 w[NWC], x[NAC], s[NSC > 0 ? NSC : 1];
     };
     /* every load is unconditional (addresses clamped) so the waits before staging count exactly
-     * the loads of the step being staged; steps past the slice re-read the last one */
-    auto issue = [&](int s_, Set &R) {
+     * the loads of the step being staged; steps past the slice re-read the last one. Even steps
+     * (first halves of super-blocks, always set RB) also bring the super-block's sum records. */
+    auto issue = [&](int s_, Set &R, bool even) {
         const int s = min(s_, nstep - 1), sb = s >> 1, h = s & 1;
         const u8 *w0 = Wsrc + (size_t)sb * F::SBB;
 #pragma unroll
@@ -391,7 +398,7 @@ __device__ __forceinline__ void gq_body(const GqArgs &a, const u8 *ws) {
             const int c = tid + NT * i, tl = c >> 9, off = c & 511; /* 512 chunks = 8 KB per 32-token tile */
             R.x[i] = ldg16c(Ag + (((size_t)(mb / 32 + tl) * (K / 16) + sb * 16 + 8 * h) * 1024 + 16 * off));
         }
-        if constexpr (SBYTES > 0) {
+        if (SBYTES > 0 && even) {
 #pragma unroll
             for (int i = 0; i < NSC; i++) {
                 const int c = min(tid + NT * i, SBYTES / 16 - 1), tl = c / (F::SREC / 16), off = c % (F::SREC / 16);
@@ -399,7 +406,7 @@ __device__ __forceinline__ void gq_body(const GqArgs &a, const u8 *ws) {
             }
         }
     };
-    auto stage = [&](int s, const Set &R) {
+    auto stage = [&](int s, const Set &R, bool even) {
         const int sb = s >> 1, h = s & 1;
         u8 *B = lds + h * BUF;
 #pragma unroll
@@ -412,7 +419,7 @@ __device__ __forceinline__ void gq_body(const GqArgs &a, const u8 *ws) {
 #pragma unroll
         for (int i = 0; i < NAC; i++) ((uint4 *)(B + WB))[tid + NT * i] = R.x[i];
         if constexpr (SBYTES > 0) {
-            if (h == 0) {
+            if (even) {
 #pragma unroll
                 for (int i = 0; i < NSC; i++) {
                     const int c = tid + NT * i;
@@ -434,11 +441,11 @@ __device__ __forceinline__ void gq_body(const GqArgs &a, const u8 *ws) {
     const int s0 = 2 * sb0;
     /* the loads must reach the memory pipeline in step order (RA's before RB's, as in the loop),
      * or the wait at the loop head would have to cover both sets: no reordering across issues */
-    issue(s0, RB);
-    stage(s0, RB);
-    issue(s0 + 1, RA);
+    issue(s0, RB, true);
+    stage(s0, RB, true);
+    issue(s0 + 1, RA, false);
     __builtin_amdgcn_sched_barrier(0);
-    issue(s0 + 2, RB);
+    issue(s0 + 2, RB, true);
     __builtin_amdgcn_sched_barrier(0);
 
     for (int sb = sb0; sb < sb1; sb++) {
@@ -461,9 +468,11 @@ __device__ __forceinline__ void gq_body(const GqArgs &a, const u8 *ws) {
                 /* unconditional (a branch here would make the compiler wait for every load in
                  * flight): past the slice's end this stages a re-read into the buffer that is
                  * no longer read */
-                stage(s + 1, h ? RB : RA);
+                if (h) stage(s + 1, RB, true);
+                else stage(s + 1, RA, false);
                 __builtin_amdgcn_sched_barrier(0);
-                issue(s + 3, h ? RB : RA);
+                if (h) issue(s + 3, RB, true);
+                else issue(s + 3, RA, false);
                 __builtin_amdgcn_sched_barrier(0);
             };
             if constexpr (TY == LE_TYPE_Q4_K) {
@@ -672,33 +681,55 @@ __device__ __forceinline__ void gq_body(const GqArgs &a, const u8 *ws) {
     for (int i = 0; i < TM; i++)
 #pragma unroll
         for (int e = 0; e < 16; e++) ts[i][e] = tsc[mb + (wm * TM + i) * 32 + 4 * hs + 8 * (e >> 2) + (e & 3)] * post;
-    int orow[TM][16]; /* output row of each of the lane's tokens */
+    if (!GR && a.ksplit > 1 && !a.part) { /* K slices without a partial-result buffer: atomic adds */
 #pragma unroll
-    for (int i = 0; i < TM; i++)
+        for (int i = 0; i < TM; i++) {
+            const int t0 = mb + (wm * TM + i) * 32 + 4 * hs;
 #pragma unroll
-        for (int e = 0; e < 16; e++) {
-            const int t = mb + (wm * TM + i) * 32 + 4 * hs + 8 * (e >> 2) + (e & 3);
-            if constexpr (GR)
-                orow[i][e] = t < M ? a.out_idx[pair0 + t - mb] : 0;
-            else
-                orow[i][e] = t;
+            for (int k = 0; k < TN; k++) {
+                const int r = nb + (wn * TN + k) * 32 + n;
+#pragma unroll
+                for (int e = 0; e < 16; e++) {
+                    const int t = t0 + 8 * (e >> 2) + (e & 3);
+                    if (t < M && r < a.rows) unsafeAtomicAdd(a.y + (size_t)t * a.rows + r, acc[i][k][e] * ts[i][e]);
+                }
+            }
         }
+        return;
+    }
+    /* Stores through LDS, one 32-token tile of every wave row at a time: the waves place their
+     * results as [token][row] (row stride BN + 8 floats: the two 4-token halves of a fragment fall
+     * on different banks), then each token's BN outputs leave as 16-byte stores of consecutive
+     * rows (a wave covers 1 KB of one output row) instead of 4-byte stores 32 to a row. */
+    float *dst = (!GR && a.ksplit > 1) ? a.part + (size_t)blockIdx.y * a.m * a.rows : a.y;
+    constexpr int TS = BN + 8, NQ = BN / 4;
+    static_assert((size_t)WM * 32 * TS * 4 <= (size_t)2 * BUF, "output staging must fit the step buffers");
+    float *T = (float *)lds;
+    const bool vec = (a.rows & 3) == 0 && ((size_t)dst & 15) == 0;
 #pragma unroll
     for (int i = 0; i < TM; i++) {
-        const int t0 = mb + (wm * TM + i) * 32 + 4 * hs;
+        __syncthreads(); /* the step buffers (or the previous round) are no longer read */
 #pragma unroll
         for (int k = 0; k < TN; k++) {
-            const int r = nb + (wn * TN + k) * 32 + n;
+            const int rl = (wn * TN + k) * 32 + n;
 #pragma unroll
-            for (int e = 0; e < 16; e++) {
-                const int t = t0 + 8 * (e >> 2) + (e & 3);
-                if (t < M && r < a.rows) {
-                    const float v = acc[i][k][e] * ts[i][e];
-                    if (!GR && a.ksplit > 1)
-                        unsafeAtomicAdd(a.y + (size_t)t * a.rows + r, v);
-                    else
-                        a.y[(size_t)orow[i][e] * a.rows + r] = v;
-                }
+            for (int e = 0; e < 16; e++)
+                T[(wm * 32 + 4 * hs + 8 * (e >> 2) + (e & 3)) * TS + rl] = acc[i][k][e] * ts[i][e];
+        }
+        __syncthreads();
+        for (int c = tid; c < WM * 32 * NQ; c += NT) {
+            const int tl = c / NQ, q = c - tl * NQ;
+            const int t = mb + ((tl >> 5) * TM + i) * 32 + (tl & 31), r = nb + 4 * q;
+            if (t >= M || r >= a.rows) continue;
+            int o = t;
+            if constexpr (GR) o = a.out_idx[pair0 + t - mb];
+            const float4 v = *(const float4 *)(T + tl * TS + 4 * q);
+            float *yp = dst + (size_t)o * a.rows + r;
+            if (vec && r + 3 < a.rows) {
+                *(float4 *)yp = v;
+            } else {
+                const float vv[4] = {v.x, v.y, v.z, v.w};
+                for (int u = 0; u < 4 && r + u < a.rows; u++) yp[u] = vv[u];
             }
         }
     }
@@ -708,6 +739,35 @@ __device__ __forceinline__ void gq_body(const GqArgs &a, const u8 *ws) {
     extern "C" __global__ void __launch_bounds__(256) le_gq_xprep_##TY(GqArgs a, u8 *ws) { gq_xprep_body<SK>(a, ws); } \
     extern "C" __global__ void __launch_bounds__(256) le_gq_xprepg_##TY(GqArgs a, u8 *ws) { gq_xprep_body<SK, true>(a, ws); }
 LE_GQX(8, 0) LE_GQX(12, 1) LE_GQX(14, 0) LE_GQX(16, 0) LE_GQX(18, 0)
+
+/* Sum of the K slices' partial results: y[e] = part[0][e] + part[1][e] + ... in slice order
+ * (deterministic, unlike atomic adds). */
+extern "C" __global__ void __launch_bounds__(256) le_gq_ksum(GqArgs a) {
+    const size_t n = (size_t)a.m * a.rows, st = (size_t)gridDim.x * blockDim.x;
+    size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+    const int ks = a.ksplit;
+    if ((n & 3) == 0 && ((size_t)a.y & 15) == 0) { /* part is 256-byte aligned in the workspace */
+        const size_t n4 = n / 4;
+        const float4 *p = (const float4 *)a.part;
+        for (; i < n4; i += st) {
+            float4 s = p[i];
+            for (int q = 1; q < ks; q++) {
+                const float4 v = p[q * n4 + i];
+                s.x += v.x;
+                s.y += v.y;
+                s.z += v.z;
+                s.w += v.w;
+            }
+            ((float4 *)a.y)[i] = s;
+        }
+    } else {
+        for (; i < n; i += st) {
+            float s = a.part[i];
+            for (int q = 1; q < ks; q++) s += a.part[q * n + i];
+            a.y[i] = s;
+        }
+    }
+}
 
 /* Plan of the grouped form: slot s has off[s+1] - off[s] pairs, split into tiles of bm; the
  * tiles are listed slot by slot (count, then slot and first pair of each) in the workspace. One

@@ -9,8 +9,10 @@
  * receive.
  *
  * Sharing: every call on one GPU uses that GPU's array and leaves the last call's contents in it.
- * The GEMM pre-pass writes every workspace byte the main pass reads, so nothing has to start at
- * zero. Calls that overlap on one GPU (two streams, two host threads) race on the array; callers
+ * The GEMM pre-pass writes every workspace byte the main pass reads, and the main pass every
+ * K-slice partial result the summing pass reads, so nothing has to start at zero. The whole array
+ * is offered as workspace, so shapes whose K slices' partial results fit in it are summed
+ * reproducibly, as le_gemm does with le_gemm_workspace_size_rows bytes. Calls that overlap on one GPU (two streams, two host threads) race on the array; callers
  * serialize them.
  *
  * This file is compiled by hipcc (it declares device memory) and linked into lible_qmm.so.

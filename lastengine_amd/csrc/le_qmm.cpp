@@ -11,6 +11,7 @@
 
 #include <cstdarg>
 #include <cstdio>
+#include <algorithm>
 #include <atomic>
 #include <cstring>
 #include <map>
@@ -895,6 +896,24 @@ static size_t gq_ws_bytes(int ty, int m, int cols) {
     const size_t mp = ((size_t)m + 127) / 128 * 128;
     return mp * cols * 2 + mp / 32 * (cols / 256) * gq_srec(ty) + mp * 4;
 }
+/* K-slice partial results follow at the next 256-byte boundary: [ks][m][rows] floats, ks <= 8. A
+ * launch splits K only while (row tiles) x (token tiles) x 2 fits the resident blocks, at most 512
+ * on gfx950, and its tiles hold at least 256 rows x 128 tokens when that count is smallest, so a
+ * shape with more than 256 such tiles never splits. */
+static size_t gq_part_off(int ty, int m, int cols) { return (gq_ws_bytes(ty, m, cols) + 255) / 256 * 256; }
+static bool gq_may_split(int m, int rows) { return (long long)((rows + 255) / 256) * ((m + 127) / 128) <= 256; }
+/* Kernel arguments of le_gq_* (GqArgs in le_gq_kernels.hip). */
+struct GqHostArgs {
+    const void *w;
+    const float *x;
+    float *y;
+    int rows, cols, m, mp, ksplit;
+    const void *const *ptrs;
+    unsigned long long w_slot_bytes;
+    const int *off, *in_idx, *out_idx;
+    int nslot, maxt, bm, pad;
+    float *part;
+};
 static int gq_slot(int ty) {
     switch (ty) {
     case LE_TYPE_Q4_K: return 80;
@@ -908,7 +927,7 @@ static int gq_slot(int ty) {
 static int gq_tab(int ty) { return ty == LE_TYPE_IQ2_XXS ? 6144 : ty == LE_TYPE_IQ3_XXS ? 4096 : 0; }
 
 static int gq_launch(le_ctx *c, int ty, const void *w, const float *x, int m, float *y, int rows, int cols, void *ws,
-                     hipStream_t st) {
+                     size_t ws_bytes, hipStream_t st) {
     /* block shapes: (WM, WN, TM, TN) -> BM = 32 TM WM tokens, BN = 32 TN WN rows */
     static const int cfgs[6][4] = {{1, 4, 1, 2}, {1, 4, 2, 2}, {1, 4, 4, 2}, {2, 2, 2, 2}, {1, 8, 2, 1}, {1, 8, 4, 1}};
     /* measured on the config shapes: 8 waves (two per SIMD, so one wave's weight decoding runs
@@ -940,22 +959,23 @@ static int gq_launch(le_ctx *c, int ty, const void *w, const float *x, int m, fl
     }
     if (nsb % ks) return c->fail(LE_ERR_SHAPE, "gq_ksplit=%d does not divide the %d super-blocks", ks, nsb);
     const int mp = (m + 127) / 128 * 128;
-    struct {
-        const void *w;
-        const float *x;
-        float *y;
-        int rows, cols, m, mp, ksplit;
-        const void *const *ptrs;
-        unsigned long long w_slot_bytes;
-        const int *off, *in_idx, *out_idx;
-        int nslot, maxt, bm, pad;
-    } a{w, x, y, rows, cols, m, mp, ks, nullptr, 0, nullptr, nullptr, nullptr, 0, 0, 0, 0};
+    /* K slices sum their partial results in a second pass when the workspace holds them (a
+     * deterministic sum; le_gemm_workspace_size_rows), else add into y atomically */
+    float *part = nullptr;
+    const size_t poff = gq_part_off(ty, m, cols);
+    if (ks > 1 && ws_bytes >= poff + (size_t)ks * m * rows * 4) part = (float *)((char *)ws + poff);
+    GqHostArgs a{w, x, y, rows, cols, m, mp, ks, nullptr, 0, nullptr, nullptr, nullptr, 0, 0, 0, 0, part};
     void *args[] = {&a, &ws};
     char pname[32];
     snprintf(pname, sizeof pname, "le_gq_xprep_%d", ty);
     int rc = c->launch(pname, dim3((unsigned)mp), 256, 0, st, args);
     if (rc) return rc;
-    return c->launch(name, dim3((unsigned)grid, (unsigned)ks), nthr, lds, st, args);
+    rc = c->launch(name, dim3((unsigned)grid, (unsigned)ks), nthr, lds, st, args);
+    if (rc || !part) return rc;
+    const size_t n4 = ((size_t)m * rows + 3) / 4;
+    const unsigned sg = (unsigned)std::min<size_t>((n4 + 255) / 256, (size_t)c->cus * 8);
+    void *sargs[] = {&a};
+    return c->launch("le_gq_ksum", dim3(sg), 256, 0, st, sargs);
 }
 
 /* Grouped form (le_mm_grouped): token tiles of bm pairs (64 or 128, from the pairs per slot),
@@ -997,17 +1017,8 @@ int le_mm_grouped(le_ctx *c, int ty, const void *const *ptrs, const void *w, con
     const int maxt = mmg_maxt(nslot, npair), mp = maxt * BM;
     const long long ntr = (rows + BN - 1) / BN, grid = (ntr + 7) / 8 * 8 * (long long)maxt;
     if (grid > 0x7FFFFFFFLL || (long long)mp * cols > (1LL << 40)) return c->fail(LE_ERR_SHAPE, "grouped GEMM too large");
-    struct {
-        const void *w;
-        const float *x;
-        float *y;
-        int rows, cols, m, mp, ksplit;
-        const void *const *ptrs;
-        unsigned long long w_slot_bytes;
-        const int *off, *in_idx, *out_idx;
-        int nslot, maxt, bm, pad;
-    } a{w, x, y, rows, cols, mp, mp, 1, ptrs, (unsigned long long)rows * le_row_bytes(ty, cols), off, in_idx, out_idx,
-        nslot, maxt, BM, 0};
+    GqHostArgs a{w, x, y, rows, cols, mp, mp, 1, ptrs, (unsigned long long)rows * le_row_bytes(ty, cols), off, in_idx,
+                 out_idx, nslot, maxt, BM, 0, nullptr};
     int srec_arg = srec;
     void *pargs[] = {&a, &ws, &srec_arg};
     int rc = c->launch("le_gq_plan", dim3(1), 1024, 0, (hipStream_t)stream, pargs);
@@ -1030,6 +1041,13 @@ size_t le_gemm_workspace_size(int ty, int m, int cols) {
     return g > o ? g : o;
 }
 
+size_t le_gemm_workspace_size_rows(int ty, int m, int rows, int cols) {
+    const size_t base = le_gemm_workspace_size(ty, m, cols);
+    if (!base || rows <= 0 || !gq_may_split(m, rows)) return base;
+    const size_t full = gq_part_off(ty, m, cols) + (size_t)8 * m * rows * 4;
+    return full > base ? full : base;
+}
+
 int le_gemm(le_ctx *c, int ty, const void *w, const float *x, int m, float *y, int rows, int cols, void *ws,
             size_t ws_bytes, le_stream_t stream) {
     if (!c) return LE_ERR_ARG;
@@ -1049,7 +1067,7 @@ int le_gemm(le_ctx *c, int ty, const void *w, const float *x, int m, float *y, i
             if (rc != 1) return rc;
         }
         if (ty != LE_TYPE_Q4_K || (c->gq && !c->gm_split))
-            return gq_launch(c, ty, w, x, m, y, rows, cols, ws, (hipStream_t)stream);
+            return gq_launch(c, ty, w, x, m, y, rows, cols, ws, ws_bytes, (hipStream_t)stream);
         /* tiles: 32*TM tokens x 128*TN rows: 32 x 256 up to 64 tokens, 64 x 128 above (the
          * producer/consumer kernel of 64 x 256 tiles does not fit its registers) */
         int TM = m > 64 ? 2 : 1, TN = m > 64 && c->gm_pc ? 1 : 2;

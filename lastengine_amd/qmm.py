@@ -68,6 +68,7 @@ def lib():
         "le_rms_quant": (I, [P, P, P, P, P, P, P, I, F, P]),
         "le_matvec_q8": (I, [P, I, P, P, P, P, P, LL, P, I, I, I, P]),
         "le_gemm_workspace_size": (S, [I, I, I]),
+        "le_gemm_workspace_size_rows": (S, [I, I, I, I]),
         "le_gemm": (I, [P, I, P, P, I, P, I, I, P, S, P]),
         "le_gemm_noalloc": (I, [P, I, P, P, I, P, I, I, P]),
         "le_stream_read": (I, [P, P, S, P, P]),
@@ -270,10 +271,14 @@ class Engine:
     def gemm_workspace_size(self, ty, m, cols):
         return int(self._L.le_gemm_workspace_size(ty, m, cols))
 
+    def gemm_workspace_size_rows(self, ty, m, rows, cols):
+        """Workspace that also holds the K slices' partial results (reproducible sums)."""
+        return int(self._L.le_gemm_workspace_size_rows(ty, m, rows, cols))
+
     def gemm(self, ty, w, x, m, out, rows, cols, ws=None, ws_bytes=None, stream=None):
         """DenseGpu::bmm (src/gpu/dense.rs:181): out[t*rows + r] = W[r] . x[t] for t < m."""
         if ws is None:
-            n = self.gemm_workspace_size(ty, m, cols)
+            n = self.gemm_workspace_size_rows(ty, m, rows, cols)
             if n:
                 import torch
                 ws = torch.empty(n, dtype=torch.uint8, device="cuda")

@@ -142,6 +142,12 @@ def test_gemm_workspace_size():
     assert L.le_gemm_workspace_size(12, 0, 4096) == 0
     assert L.le_gemm_workspace_size(12, 16, 100) == 0
     assert L.le_gemm_workspace_size(99, 16, 256) == 0
+    # with room for up to 8 K slices' partial results (256-byte aligned) where a shape may split
+    L.le_gemm_workspace_size_rows.restype = ctypes.c_size_t
+    base = L.le_gemm_workspace_size(12, 64, 4096)
+    assert L.le_gemm_workspace_size_rows(12, 64, 14336, 4096) == (base + 255) // 256 * 256 + 8 * 64 * 14336 * 4
+    assert L.le_gemm_workspace_size_rows(14, 512, 200000, 4096) == L.le_gemm_workspace_size(14, 512, 4096)
+    assert L.le_gemm_workspace_size_rows(12, 0, 4096, 4096) == 0
 
 
 def test_moe_check_rejects_null_context():

@@ -113,3 +113,35 @@ def test_gemm_activation_magnitudes(engine, name):
         if t == 3:
             continue
         check_close(got[t:t + 1], want[t:t + 1], mag[t:t + 1])
+
+
+@pytest.mark.parametrize("name", NAMES)
+@pytest.mark.parametrize("rows,cols,m,ks", [(1000, 4096, 64, 4), (257, 2048, 20, 8), (130, 1024, 33, 2)])
+def test_gemm_slice_sums(fresh_engine, name, rows, cols, m, ks):
+    """K slices with the partial-result workspace (le_gemm_workspace_size_rows: summed in a second
+    pass, slice order fixed) and with the minimal one (atomic adds into y): both meet the oracle
+    bar, and the summed form gives the same bits on a second call."""
+    import torch
+    ty = le.TYPES[name]
+    fresh_engine.set_option("gq_ksplit", ks)
+    if name == "Q4_K":
+        fresh_engine.set_option("gm_min_m", 17)
+        fresh_engine.set_option("gm_mh", 0)
+    q, _ = weights(ty, rows, cols, seed=ks + m)
+    xs = acts(m * cols, seed=rows).reshape(m, cols)
+    want = oracle.matmat(ty, q, rows, cols, xs)
+    mag = absmag(ty, q, rows, cols, xs)
+    dq, dx = dev(q), dev(xs)
+    full = fresh_engine.gemm_workspace_size_rows(ty, m, rows, cols)
+    small = fresh_engine.gemm_workspace_size(ty, m, cols)
+    assert full >= small + ks * m * rows * 4
+    outs = []
+    for nbytes in (full, full, small):
+        print("slice sums", name, rows, cols, m, ks, nbytes, flush=True)
+        ws = torch.empty(nbytes, dtype=torch.uint8, device="cuda")
+        y = torch.full((m, rows), float("nan"), dtype=torch.float32, device="cuda")
+        fresh_engine.gemm(ty, dq, dx, m, y, rows, cols, ws=ws)
+        torch.cuda.synchronize()
+        outs.append(y.cpu().numpy())
+        check_close(outs[-1], want, mag)
+    assert np.array_equal(outs[0].view(np.uint32), outs[1].view(np.uint32))
