@@ -384,26 +384,42 @@ __device__ __forceinline__ void gq_body(const GqArgs &a, const u8 *ws) {
     /* every load is unconditional (addresses clamped) so the waits before staging count exactly
      * the loads of the step being staged; steps past the slice re-read the last one. Even steps
      * (first halves of super-blocks, always set RB) also bring the super-block's sum records. */
+    /* per-thread 32-bit load offsets, computed once (the host keeps a slice's weights and the
+     * activation planes below 4 GiB): so each load is a scalar base plus one of these */
+    u32 wo0[NWC], wo1[NWC], xo[NAC], so[NSC > 0 ? NSC : 1];
+#pragma unroll
+    for (int i = 0; i < NWC; i++) {
+        const int c = min(tid + NT * i, BN * F::NCH - 1), row = c / F::NCH, k = c - row * F::NCH;
+        const u32 base = (u32)min(nb + row, a.rows - 1) * (u32)rb;
+        wo0[i] = base + F::goff(k, 0);
+        wo1[i] = base + F::goff(k, 1);
+    }
+#pragma unroll
+    for (int i = 0; i < NAC; i++) {
+        const int c = tid + NT * i, tl = c >> 9, off = c & 511; /* 512 chunks = 8 KB per 32-token tile */
+        xo[i] = (u32)(mb / 32 + tl) * (u32)(K / 16) * 1024u + 16u * off;
+    }
+#pragma unroll
+    for (int i = 0; i < (NSC > 0 ? NSC : 1); i++) {
+        const int c = min(tid + NT * i, SBYTES > 0 ? SBYTES / 16 - 1 : 0), tl = c / (F::SREC > 0 ? F::SREC / 16 : 1);
+        const int off = c - tl * (F::SREC > 0 ? F::SREC / 16 : 1);
+        so[i] = (u32)(mb / 32 + tl) * (u32)nsb * (u32)F::SREC + 16u * off;
+    }
     auto issue = [&](int s_, Set &R, bool even) {
         const int s = min(s_, nstep - 1), sb = s >> 1, h = s & 1;
         const u8 *w0 = Wsrc + (size_t)sb * F::SBB;
 #pragma unroll
         for (int i = 0; i < NWC; i++) {
-            const int c = min(tid + NT * i, BN * F::NCH - 1), row = c / F::NCH, k = c - row * F::NCH;
-            const u8 *p = w0 + (size_t)min(nb + row, a.rows - 1) * rb + F::goff(k, h);
+            const u8 *p = w0 + (h ? wo1[i] : wo0[i]);
             R.w[i] = F::ALIGNED ? ldg16(p) : ldg16u(p);
         }
+        const u8 *x0 = Ag + (size_t)(sb * 16 + 8 * h) * 1024;
 #pragma unroll
-        for (int i = 0; i < NAC; i++) {
-            const int c = tid + NT * i, tl = c >> 9, off = c & 511; /* 512 chunks = 8 KB per 32-token tile */
-            R.x[i] = ldg16c(Ag + (((size_t)(mb / 32 + tl) * (K / 16) + sb * 16 + 8 * h) * 1024 + 16 * off));
-        }
+        for (int i = 0; i < NAC; i++) R.x[i] = ldg16c(x0 + xo[i]);
         if (SBYTES > 0 && even) {
+            const u8 *s0p = Sg + (size_t)sb * F::SREC;
 #pragma unroll
-            for (int i = 0; i < NSC; i++) {
-                const int c = min(tid + NT * i, SBYTES / 16 - 1), tl = c / (F::SREC / 16), off = c % (F::SREC / 16);
-                R.s[i] = ldg16c(Sg + (((size_t)(mb / 32 + tl) * nsb + sb) * F::SREC + 16 * off));
-            }
+            for (int i = 0; i < NSC; i++) R.s[i] = ldg16c(s0p + so[i]);
         }
     };
     auto stage = [&](int s, const Set &R, bool even) {

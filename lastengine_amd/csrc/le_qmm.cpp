@@ -959,6 +959,9 @@ static int gq_launch(le_ctx *c, int ty, const void *w, const float *x, int m, fl
     }
     if (nsb % ks) return c->fail(LE_ERR_SHAPE, "gq_ksplit=%d does not divide the %d super-blocks", ks, nsb);
     const int mp = (m + 127) / 128 * 128;
+    /* the kernels address the weights and the activation planes with 32-bit offsets */
+    if ((unsigned long long)rows * le_row_bytes(ty, cols) >= (1ull << 32) || (unsigned long long)mp * cols * 2 >= (1ull << 32))
+        return c->fail(LE_ERR_SHAPE, "GEMM weights or activation planes of 4 GiB or more");
     /* K slices sum their partial results in a second pass when the workspace holds them (a
      * deterministic sum; le_gemm_workspace_size_rows), else add into y atomically */
     float *part = nullptr;
@@ -1016,7 +1019,9 @@ int le_mm_grouped(le_ctx *c, int ty, const void *const *ptrs, const void *w, con
         return c->fail(LE_ERR_SHAPE, "grouped GEMM tile does not fit the LDS");
     const int maxt = mmg_maxt(nslot, npair), mp = maxt * BM;
     const long long ntr = (rows + BN - 1) / BN, grid = (ntr + 7) / 8 * 8 * (long long)maxt;
-    if (grid > 0x7FFFFFFFLL || (long long)mp * cols > (1LL << 40)) return c->fail(LE_ERR_SHAPE, "grouped GEMM too large");
+    if (grid > 0x7FFFFFFFLL || (unsigned long long)mp * cols * 2 >= (1ull << 32) ||
+        (unsigned long long)rows * le_row_bytes(ty, cols) >= (1ull << 32))
+        return c->fail(LE_ERR_SHAPE, "grouped GEMM too large (32-bit weight or activation offsets)");
     GqHostArgs a{w, x, y, rows, cols, mp, mp, 1, ptrs, (unsigned long long)rows * le_row_bytes(ty, cols), off, in_idx,
                  out_idx, nslot, maxt, BM, 0, nullptr};
     int srec_arg = srec;
