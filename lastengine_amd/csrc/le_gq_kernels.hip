@@ -40,8 +40,10 @@
  * steps of loads in registers (issued two steps before they are written to LDS), so the loads of
  * steps s+2 and s+3 are in flight while step s computes. Blocks that share weight rows (same row
  * tile, other token tiles or K slices) get the same blockIdx % 8 and therefore the same XCD and
- * L2. K may be split over blockIdx.y; slices then add into Y with fp32 atomics (the pre-pass
- * clears Y).
+ * L2. With fewer than 8 row tiles, row tiles vary fastest instead, so the blocks
+ * spread over all XCDs. K may be split over blockIdx.y; the slices' partial results are then
+ * summed by le_gq_ksum (or, without room for them, added into Y atomically after the pre-pass
+ * cleared it).
  */
 #include "le_qmm_device.h"
 #include "le_iq_tables.h"
@@ -352,9 +354,11 @@ __device__ __forceinline__ void gq_body(const GqArgs &a, const u8 *ws) {
 
     const int K = a.cols, nsb = K >> 8;
     const int NTR = (a.rows + BN - 1) / BN, MT = GR ? a.maxt : (a.m + BM - 1) / BM;
+    /* 8 or more row tiles: blocks of one row tile (its token tiles) share blockIdx % 8, the XCD
+     * and its L2; fewer: row tiles vary fastest, so consecutive blocks spread over every XCD */
     const int id = blockIdx.x, j = id >> 3;
-    const int mt = j % MT, nt = (j / MT) * 8 + (id & 7);
-    if (nt >= NTR) return; /* uniform over the block */
+    const int mt = NTR >= 8 ? j % MT : id / NTR, nt = NTR >= 8 ? (j / MT) * 8 + (id & 7) : id % NTR;
+    if (nt >= NTR || mt >= MT) return; /* uniform over the block */
     const int nb = nt * BN, mb = mt * BM;
     /* tokens of this tile: M = all tokens (plain), or the tile's pairs (grouped: rows of its slot) */
     int M = a.m, pair0 = 0;

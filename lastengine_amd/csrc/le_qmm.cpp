@@ -946,7 +946,7 @@ static int gq_launch(le_ctx *c, int ty, const void *w, const float *x, int m, fl
     char name[48];
     snprintf(name, sizeof name, "le_gq_%d_w%d%d_t%d%d", ty, WM, WN, TM, TN);
     const long long ntr = (rows + BN - 1) / BN, mt = (m + BM - 1) / BM;
-    const long long grid = (ntr + 7) / 8 * 8 * mt;
+    const long long grid = (ntr >= 8 ? (ntr + 7) / 8 * 8 : ntr) * mt; /* block order: le_gq_kernels.hip */
     if (grid > 0x7FFFFFFFLL) return c->fail(LE_ERR_SHAPE, "GEMM grid too large");
     int ks = 1;
     if (c->gq_ksplit > 0) {
@@ -1018,7 +1018,7 @@ int le_mm_grouped(le_ctx *c, int ty, const void *const *ptrs, const void *w, con
     if (BM != mmg_bm(nslot, npair) && !(ci == 3 && mmg_bm(nslot, npair) == 128))
         return c->fail(LE_ERR_SHAPE, "grouped GEMM tile does not fit the LDS");
     const int maxt = mmg_maxt(nslot, npair), mp = maxt * BM;
-    const long long ntr = (rows + BN - 1) / BN, grid = (ntr + 7) / 8 * 8 * (long long)maxt;
+    const long long ntr = (rows + BN - 1) / BN, grid = (ntr >= 8 ? (ntr + 7) / 8 * 8 : ntr) * (long long)maxt;
     if (grid > 0x7FFFFFFFLL || (unsigned long long)mp * cols * 2 >= (1ull << 32) ||
         (unsigned long long)rows * le_row_bytes(ty, cols) >= (1ull << 32))
         return c->fail(LE_ERR_SHAPE, "grouped GEMM too large (32-bit weight or activation offsets)");
