@@ -210,7 +210,8 @@ __device__ __forceinline__ void gq_tables(u8 *tab) {
 template <int SK, bool GR = false>
 __device__ __forceinline__ void gq_xprep_body(const GqArgs &a, u8 *ws) {
     __shared__ float red[4];
-    const int K = a.cols, nsb = K >> 8, t = blockIdx.x, tid = threadIdx.x, lane = tid & 63;
+    const int K = a.cols, nsb = K >> 8, tid = threadIdx.x, lane = tid & 63;
+    int t = blockIdx.x; /* padded token (grouped form: the pair's tile position, below) */
     if (!GR && a.ksplit > 1 && !a.part) { /* the slices add into y */
         const size_t ny = (size_t)a.m * a.rows, st = (size_t)gridDim.x * blockDim.x;
         size_t i = (size_t)blockIdx.x * blockDim.x + tid;
@@ -221,15 +222,24 @@ __device__ __forceinline__ void gq_xprep_body(const GqArgs &a, u8 *ws) {
     }
     bool live = t < a.m;
     size_t src = t;
-    if constexpr (GR) { /* position t = tile * bm + j: pair first[tile] + j of the tile's slot, if any */
+    if constexpr (GR) {
+        /* one block per pair p: its slot s (off[s] <= p < off[s+1], by bisection), then its
+         * position tfirst[s] * bm + (p - off[s]) among the planned tiles */
         constexpr int srec_ = SK == 1 ? 1024 : 0;
         const int *lst = (const int *)(ws + gq_l_off(a.mp, K, srec_));
-        const int tile = t / a.bm, j = t - tile * a.bm;
+        const int p = blockIdx.x;
         live = false;
-        if (tile < lst[0]) {
-            const int sl = lst[4 + tile], p = lst[4 + a.maxt + tile] + j;
-            if (p < a.off[sl + 1]) {
+        if (p >= a.off[0] && p < a.off[a.nslot]) {
+            int lo = 0, hi = a.nslot;
+            while (hi - lo > 1) {
+                const int mid = (lo + hi) >> 1;
+                if (a.off[mid] <= p) lo = mid;
+                else hi = mid;
+            }
+            const int j = p - a.off[lo], tile = lst[4 + 2 * a.maxt + lo] + j / a.bm;
+            if (j >= 0 && p < a.off[lo + 1] && tile < lst[0]) {
                 live = true;
+                t = tile * a.bm + j % a.bm;
                 src = (size_t)a.in_idx[p];
             }
         }
@@ -808,6 +818,7 @@ extern "C" __global__ void __launch_bounds__(1024) le_gq_plan(GqArgs a, u8 *ws, 
             __syncthreads();
         }
         const int first = base + scan[threadIdx.x] - n;
+        if (s < a.nslot) lst[4 + 2 * a.maxt + s] = first; /* the slot's first tile */
         for (int q = 0; q < n; q++) {
             if (first + q < a.maxt) {
                 lst[4 + first + q] = s;
