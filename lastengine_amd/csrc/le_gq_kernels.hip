@@ -71,13 +71,20 @@ struct GqArgs {
     const int *off, *in_idx, *out_idx;
     int nslot, maxt, bm, pad;
     float *part; /* [ksplit][m][rows] partial results of the K slices, or null */
+    /* grouped form, dual: a second weight set (ptrs2 or w2, same type and shape) applied to the same
+     * pairs, written to y2 (the MoE gate and up projections in one launch) */
+    const u8 *const *ptrs2;
+    const u8 *w2;
+    float *y2;
+    int dual, pad2;
 };
 
 /* Workspace layout: A planes (mp * K halves), S records (mp/32 * nsb * SREC bytes), token scales
  * (mp floats). */
 __host__ __device__ inline size_t gq_s_off(int mp, int K) { return (size_t)mp * K * 2; }
 __host__ __device__ inline size_t gq_t_off(int mp, int K, int srec) { return gq_s_off(mp, K) + (size_t)(mp / 32) * (K / 256) * srec; }
-/* grouped form: the tile list after the token scales: int count, pad to 16 B, int slot[maxt], int first[maxt] */
+/* grouped form: the tile list after the token scales: int count, pad to 16 B, int slot[maxt], int first[maxt],
+ * then each slot's first tile, int tfirst[nslot] */
 __host__ __device__ inline size_t gq_l_off(int mp, int K, int srec) { return gq_t_off(mp, K, srec) + (size_t)mp * 4; }
 
 __device__ __forceinline__ le_h2 as_h2(u32 v) { return __builtin_bit_cast(le_h2, v); }
@@ -205,7 +212,7 @@ __device__ __forceinline__ void gq_tables(u8 *tab) {
 }
 
 /* ============================ activation pre-pass ============================ */
-/* One block of 256 threads per (padded) token. SK: 0 no sums, 1 per-32 sums (Q4_K), 2 per-16
+/* One block of 256 threads per (padded) token, or per pair in the grouped form. SK: 0 no sums, 1 per-32 sums (Q4_K), 2 per-16
  * sums (Q6_K). */
 template <int SK, bool GR = false>
 __device__ __forceinline__ void gq_xprep_body(const GqArgs &a, u8 *ws) {
@@ -363,13 +370,14 @@ __device__ __forceinline__ void gq_body(const GqArgs &a, const u8 *ws) {
     u8 *tab = Sl + 2 * SBYTES;          /* IQ tables */
 
     const int K = a.cols, nsb = K >> 8;
-    const int NTR = (a.rows + BN - 1) / BN, MT = GR ? a.maxt : (a.m + BM - 1) / BM;
+    const int NTR1 = (a.rows + BN - 1) / BN, NTR = GR && a.dual ? 2 * NTR1 : NTR1, MT = GR ? a.maxt : (a.m + BM - 1) / BM;
     /* 8 or more row tiles: blocks of one row tile (its token tiles) share blockIdx % 8, the XCD
      * and its L2; fewer: row tiles vary fastest, so consecutive blocks spread over every XCD */
     const int id = blockIdx.x, j = id >> 3;
     const int mt = NTR >= 8 ? j % MT : id / NTR, nt = NTR >= 8 ? (j / MT) * 8 + (id & 7) : id % NTR;
     if (nt >= NTR || mt >= MT) return; /* uniform over the block */
-    const int nb = nt * BN, mb = mt * BM;
+    const bool second = nt >= NTR1; /* dual grouped form: a row tile of the second weight set */
+    const int nb = (second ? nt - NTR1 : nt) * BN, mb = mt * BM;
     /* tokens of this tile: M = all tokens (plain), or the tile's pairs (grouped: rows of its slot) */
     int M = a.m, pair0 = 0;
     const u8 *Wsrc = a.w;
@@ -379,7 +387,10 @@ __device__ __forceinline__ void gq_body(const GqArgs &a, const u8 *ws) {
         const int sl = lst[4 + mt];
         pair0 = lst[4 + a.maxt + mt];
         M = mb + min(BM, a.off[sl + 1] - pair0); /* token t of the tile is valid while t < M */
-        Wsrc = a.ptrs ? a.ptrs[sl] : a.w + (size_t)sl * a.w_slot_bytes;
+        if (second)
+            Wsrc = a.ptrs2 ? a.ptrs2[sl] : a.w2 + (size_t)sl * a.w_slot_bytes;
+        else
+            Wsrc = a.ptrs ? a.ptrs[sl] : a.w + (size_t)sl * a.w_slot_bytes;
     }
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int wm = wave / WN, wn = wave % WN;
@@ -731,7 +742,7 @@ __device__ __forceinline__ void gq_body(const GqArgs &a, const u8 *ws) {
      * results as [token][row] (row stride BN + 8 floats: the two 4-token halves of a fragment fall
      * on different banks), then each token's BN outputs leave as 16-byte stores of consecutive
      * rows (a wave covers 1 KB of one output row) instead of 4-byte stores 32 to a row. */
-    float *dst = (!GR && a.ksplit > 1) ? a.part + (size_t)blockIdx.y * a.m * a.rows : a.y;
+    float *dst = (!GR && a.ksplit > 1) ? a.part + (size_t)blockIdx.y * a.m * a.rows : second ? a.y2 : a.y;
     constexpr int TS = BN + 8, NQ = BN / 4;
     static_assert((size_t)WM * 32 * TS * 4 <= (size_t)2 * BUF, "output staging must fit the step buffers");
     float *T = (float *)lds;

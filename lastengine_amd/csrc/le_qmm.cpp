@@ -707,6 +707,10 @@ struct MoePreArgs {
     int n_tok, n_exp, k, pad;
 };
 
+static int mm_grouped(le_ctx *c, int ty, const void *const *ptrs, const void *w, const void *const *ptrs2, const void *w2,
+                      const int *off, const int *in_idx, const int *out_idx, int nslot, int npair, const float *x, float *y,
+                      float *y2, int rows, int cols, void *ws, size_t ws_bytes, hipStream_t stream);
+
 static int moe_prefill(le_ctx *c, int ty_gate, int ty_down, const void *gate, const void *up, const void *down,
                        const void *const *gptr, const void *const *uptr, const void *const *dptr, int n_exp, int k,
                        int hidden, int ff, const float *logits, const float *h, int n_tok, float *out, int *idx_out,
@@ -722,15 +726,15 @@ static int moe_prefill(le_ctx *c, int ty_gate, int ty_down, const void *gate, co
     void *args[] = {&a};
     int rc = c->launch("le_moe_route_tok", dim3((unsigned)((n_tok + 7) / 8)), 512, 0, st, args);
     if (!rc) rc = c->launch("le_moe_group", dim3((unsigned)n_exp), 256, 0, st, args);
-    if (!rc) rc = le_mm_grouped(c, ty_gate, gptr, gate, off, in_idx, out_idx, n_exp, np, h, G, ff, hidden, gws, gws_bytes, st);
-    if (!rc) rc = le_mm_grouped(c, ty_gate, uptr, up, off, in_idx, out_idx, n_exp, np, h, U, ff, hidden, gws, gws_bytes, st);
+    /* gate and up in one grouped launch (one plan and one activation pre-pass for both) */
+    if (!rc) rc = mm_grouped(c, ty_gate, gptr, gate, uptr, up, off, in_idx, out_idx, n_exp, np, h, G, U, ff, hidden, gws, gws_bytes, st);
     if (rc) return rc;
     long long n = (long long)np * ff;
     unsigned blocks = (unsigned)((n + 255) / 256 < 8192 ? (n + 255) / 256 : 8192);
     void *sargs[] = {&G, &U, &n};
     rc = c->launch("le_moe_swiglu", dim3(blocks), 256, 0, st, sargs);
     /* down: the activation rows are the pairs themselves, in the same grouped order */
-    if (!rc) rc = le_mm_grouped(c, ty_down, dptr, down, off, out_idx, out_idx, n_exp, np, G, D, hidden, ff, gws, gws_bytes, st);
+    if (!rc) rc = mm_grouped(c, ty_down, dptr, down, nullptr, nullptr, off, out_idx, out_idx, n_exp, np, G, D, nullptr, hidden, ff, gws, gws_bytes, st);
     if (rc) return rc;
     long long no = (long long)n_tok * hidden;
     blocks = (unsigned)((no + 255) / 256 < 8192 ? (no + 255) / 256 : 8192);
@@ -913,6 +917,10 @@ struct GqHostArgs {
     const int *off, *in_idx, *out_idx;
     int nslot, maxt, bm, pad;
     float *part;
+    const void *const *ptrs2;
+    const void *w2;
+    float *y2;
+    int dual, pad2;
 };
 static int gq_slot(int ty) {
     switch (ty) {
@@ -967,7 +975,7 @@ static int gq_launch(le_ctx *c, int ty, const void *w, const float *x, int m, fl
     float *part = nullptr;
     const size_t poff = gq_part_off(ty, m, cols);
     if (ks > 1 && ws_bytes >= poff + (size_t)ks * m * rows * 4) part = (float *)((char *)ws + poff);
-    GqHostArgs a{w, x, y, rows, cols, m, mp, ks, nullptr, 0, nullptr, nullptr, nullptr, 0, 0, 0, 0, part};
+    GqHostArgs a{w, x, y, rows, cols, m, mp, ks, nullptr, 0, nullptr, nullptr, nullptr, 0, 0, 0, 0, part, nullptr, nullptr, nullptr, 0, 0};
     void *args[] = {&a, &ws};
     char pname[32];
     snprintf(pname, sizeof pname, "le_gq_xprep_%d", ty);
@@ -990,13 +998,16 @@ static int mmg_maxt(int nslot, int npair) { const int bm = mmg_bm(nslot, npair);
 size_t le_mm_grouped_workspace_size(int ty, int nslot, int npair, int cols) {
     if (!supported(ty) || nslot <= 0 || npair < 0 || cols <= 0 || cols % 256) return 0;
     const size_t maxt = (size_t)mmg_maxt(nslot, npair), mp = maxt * mmg_bm(nslot, npair);
-    return mp * cols * 2 + mp / 32 * (cols / 256) * gq_srec(ty) + mp * 4 + 16 + 8 * maxt;
+    return mp * cols * 2 + mp / 32 * (cols / 256) * gq_srec(ty) + mp * 4 + 16 + 8 * maxt + 4 * (size_t)nslot;
 }
 
-int le_mm_grouped(le_ctx *c, int ty, const void *const *ptrs, const void *w, const int *off, const int *in_idx,
-                  const int *out_idx, int nslot, int npair, const float *x, float *y, int rows, int cols, void *ws,
-                  size_t ws_bytes, le_stream_t stream) {
-    if (!c) return LE_ERR_ARG;
+/* Grouped matmul; with a second weight set (ptrs2 or w2, same type and shape) the same pairs are
+ * also multiplied by it into y2, in the same launches (one plan, one pre-pass, one grid). */
+static int mm_grouped(le_ctx *c, int ty, const void *const *ptrs, const void *w, const void *const *ptrs2, const void *w2,
+                      const int *off, const int *in_idx, const int *out_idx, int nslot, int npair, const float *x, float *y,
+                      float *y2, int rows, int cols, void *ws, size_t ws_bytes, hipStream_t stream) {
+    const bool dual = ptrs2 || w2;
+    if (dual && !y2) return c->fail(LE_ERR_ARG, "null second output");
     if (!supported(ty)) return c->fail(LE_ERR_TYPE, "no kernel for type %d", ty);
     if ((!ptrs && !w) || !off || !in_idx || !out_idx || !x || !y || !ws) return c->fail(LE_ERR_ARG, "null pointer");
     if (nslot <= 0 || npair < 0 || rows <= 0 || cols <= 0) return c->fail(LE_ERR_SHAPE, "empty shape");
@@ -1018,12 +1029,12 @@ int le_mm_grouped(le_ctx *c, int ty, const void *const *ptrs, const void *w, con
     if (BM != mmg_bm(nslot, npair) && !(ci == 3 && mmg_bm(nslot, npair) == 128))
         return c->fail(LE_ERR_SHAPE, "grouped GEMM tile does not fit the LDS");
     const int maxt = mmg_maxt(nslot, npair), mp = maxt * BM;
-    const long long ntr = (rows + BN - 1) / BN, grid = (ntr >= 8 ? (ntr + 7) / 8 * 8 : ntr) * (long long)maxt;
+    const long long ntr = (rows + BN - 1) / BN * (dual ? 2 : 1), grid = (ntr >= 8 ? (ntr + 7) / 8 * 8 : ntr) * (long long)maxt;
     if (grid > 0x7FFFFFFFLL || (unsigned long long)mp * cols * 2 >= (1ull << 32) ||
         (unsigned long long)rows * le_row_bytes(ty, cols) >= (1ull << 32))
         return c->fail(LE_ERR_SHAPE, "grouped GEMM too large (32-bit weight or activation offsets)");
     GqHostArgs a{w, x, y, rows, cols, mp, mp, 1, ptrs, (unsigned long long)rows * le_row_bytes(ty, cols), off, in_idx,
-                 out_idx, nslot, maxt, BM, 0, nullptr};
+                 out_idx, nslot, maxt, BM, 0, nullptr, ptrs2, w2, y2, dual ? 1 : 0, 0};
     int srec_arg = srec;
     void *pargs[] = {&a, &ws, &srec_arg};
     int rc = c->launch("le_gq_plan", dim3(1), 1024, 0, (hipStream_t)stream, pargs);
@@ -1031,10 +1042,18 @@ int le_mm_grouped(le_ctx *c, int ty, const void *const *ptrs, const void *w, con
     void *args[] = {&a, &ws};
     char name[48];
     snprintf(name, sizeof name, "le_gq_xprepg_%d", ty);
-    rc = c->launch(name, dim3((unsigned)mp), 256, 0, (hipStream_t)stream, args);
+    rc = c->launch(name, dim3((unsigned)npair), 256, 0, (hipStream_t)stream, args); /* one block per pair */
     if (rc) return rc;
     snprintf(name, sizeof name, "le_gqg_%d_w%d%d_t%d%d", ty, WM, WN, TM, TN);
     return c->launch(name, dim3((unsigned)grid), nthr, lds_of(ci), (hipStream_t)stream, args);
+}
+
+int le_mm_grouped(le_ctx *c, int ty, const void *const *ptrs, const void *w, const int *off, const int *in_idx,
+                  const int *out_idx, int nslot, int npair, const float *x, float *y, int rows, int cols, void *ws,
+                  size_t ws_bytes, le_stream_t stream) {
+    if (!c) return LE_ERR_ARG;
+    return mm_grouped(c, ty, ptrs, w, nullptr, nullptr, off, in_idx, out_idx, nslot, npair, x, y, nullptr, rows, cols, ws,
+                      ws_bytes, (hipStream_t)stream);
 }
 
 size_t le_gemm_workspace_size(int ty, int m, int cols) {
