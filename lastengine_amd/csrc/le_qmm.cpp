@@ -989,10 +989,13 @@ static int gq_launch(le_ctx *c, int ty, const void *w, const float *x, int m, fl
     return c->launch("le_gq_ksum", dim3(sg), 256, 0, st, sargs);
 }
 
-/* Grouped form (le_mm_grouped): token tiles of bm pairs (64 or 128, from the pairs per slot),
+/* Grouped form (le_mm_grouped): token tiles of bm pairs (32 up to 16 pairs per slot on average, 64
+ * up to 64, else 128; 32 at 40 per slot measured slower: slots then span several tiles),
  * at most nslot + npair / bm of them. */
-static int mmg_cfg(int nslot, int npair) { return (long long)npair <= 64LL * nslot ? 4 : 5; }
-static int mmg_bm(int nslot, int npair) { return mmg_cfg(nslot, npair) == 4 ? 64 : 128; }
+static int mmg_cfg(int nslot, int npair) {
+    return (long long)npair <= 16LL * nslot ? 6 : (long long)npair <= 64LL * nslot ? 4 : 5;
+}
+static int mmg_bm(int nslot, int npair) { const int c = mmg_cfg(nslot, npair); return c == 6 ? 32 : c == 4 ? 64 : 128; }
 static int mmg_maxt(int nslot, int npair) { const int bm = mmg_bm(nslot, npair); return nslot + (npair + bm - 1) / bm; }
 
 size_t le_mm_grouped_workspace_size(int ty, int nslot, int npair, int cols) {
@@ -1016,7 +1019,7 @@ static int mm_grouped(le_ctx *c, int ty, const void *const *ptrs, const void *w,
     const size_t need = le_mm_grouped_workspace_size(ty, nslot, npair, cols);
     if (ws_bytes < need) return c->fail(LE_ERR_WORKSPACE, "workspace needs %zu bytes", need);
     if (npair == 0) return LE_OK;
-    static const int cfgs[6][4] = {{1, 4, 1, 2}, {1, 4, 2, 2}, {1, 4, 4, 2}, {2, 2, 2, 2}, {1, 8, 2, 1}, {1, 8, 4, 1}};
+    static const int cfgs[7][4] = {{1, 4, 1, 2}, {1, 4, 2, 2}, {1, 4, 4, 2}, {2, 2, 2, 2}, {1, 8, 2, 1}, {1, 8, 4, 1}, {1, 8, 1, 1}};
     int ci = mmg_cfg(nslot, npair);
     const int srec = gq_srec(ty);
     auto lds_of = [&](int i) {
