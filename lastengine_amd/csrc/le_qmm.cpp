@@ -111,7 +111,7 @@ struct le_ctx {
     int gq = 1;              /* Q4_K GEMM on the generic kernels (le_gq_*) instead of le_gm_12_* */
     int gq_min_m = 9;        /* other types: smallest M on the matrix-core GEMM (below: vector kernels) */
     int gq_cfg = 0;          /* generic GEMM block shape (tokens x rows, waves): 0 auto, 1 (32x256, 4), 2 (64x256, 4),
-                                3 (128x256, 4), 4 (128x128, 4), 5 (64x256, 8), 6 (128x256, 8) */
+                                3 (128x256, 4), 4 (128x128, 4), 5 (64x256, 8), 6 (128x256, 8), 7 (32x256, 8) */
     int gq_ksplit = 0;       /* generic GEMM K slices: 0 auto, else 1, 2, 4, 8 */
     std::vector<hipModule_t> mods;
     std::map<std::string, hipFunction_t> fns;
@@ -515,7 +515,7 @@ int le_set_option(le_ctx *c, const char *name, int value) {
         if (value < 1) return c->fail(LE_ERR_ARG, "gq_min_m must be >= 1");
         c->gq_min_m = value;
     } else if (n == "gq_cfg") {
-        if (value < 0 || value > 6) return c->fail(LE_ERR_ARG, "gq_cfg must be 0..6");
+        if (value < 0 || value > 7) return c->fail(LE_ERR_ARG, "gq_cfg must be 0..7");
         c->gq_cfg = value;
     } else if (n == "gq_ksplit") {
         if (value != 0 && value != 1 && value != 2 && value != 4 && value != 8)
@@ -937,10 +937,12 @@ static int gq_tab(int ty) { return ty == LE_TYPE_IQ2_XXS ? 6144 : ty == LE_TYPE_
 static int gq_launch(le_ctx *c, int ty, const void *w, const float *x, int m, float *y, int rows, int cols, void *ws,
                      size_t ws_bytes, hipStream_t st) {
     /* block shapes: (WM, WN, TM, TN) -> BM = 32 TM WM tokens, BN = 32 TN WN rows */
-    static const int cfgs[6][4] = {{1, 4, 1, 2}, {1, 4, 2, 2}, {1, 4, 4, 2}, {2, 2, 2, 2}, {1, 8, 2, 1}, {1, 8, 4, 1}};
+    static const int cfgs[7][4] = {{1, 4, 1, 2}, {1, 4, 2, 2}, {1, 4, 4, 2}, {2, 2, 2, 2}, {1, 8, 2, 1}, {1, 8, 4, 1}, {1, 8, 1, 1}};
     /* measured on the config shapes: 8 waves (two per SIMD, so one wave's weight decoding runs
      * under the other's MFMAs), 64 x 256 tiles up to 64 tokens, 128 x 256 above */
-    int ci = c->gq_cfg ? c->gq_cfg - 1 : m <= 64 ? 4 : 5;
+    /* 32 x 256 tiles up to 32 tokens for the types other than Q4_K (Q6_K M=17: 39.6 -> 34.1 us,
+     * IQ2_XXS 27.3 -> 25.8; Q4_K measured slower: 34.0 -> 36.1) */
+    int ci = c->gq_cfg ? c->gq_cfg - 1 : m <= 32 && ty != LE_TYPE_Q4_K ? 6 : m <= 64 ? 4 : 5;
     const int nsb = cols / 256, srec = gq_srec(ty);
     auto lds_of = [&](int i) {
         const int BM = 32 * cfgs[i][0] * cfgs[i][2], BN = 32 * cfgs[i][1] * cfgs[i][3];
