@@ -449,8 +449,8 @@ def main():
     if not args.no_secondary:
         sec = {}
         steps2 = max(100, args.steps // 4)
-        for nt in (1, 8):
-            r = bench_moe(eng, nt, max(64, steps2 // 4), 32)
+        for nt in (1, 8, 16):
+            r = bench_moe(eng, nt, max(64, steps2 // 4) if nt <= 8 else 16, 32 if nt <= 8 else 4)
             sec["moe_config4_ntok%d" % nt] = r
             log("moe", r)
         for nt in (64, 512, 2048):

@@ -94,12 +94,14 @@ struct le_ctx {
     int mq6 = 1, ms_p6 = 2;  /* Q6_K decode matvec on the staged MFMA kernels, super-blocks per step */
     int mqiq = 1, ms_piq = 2; /* IQ2_XXS / IQ3_XXS likewise */
     int moe_fast = 1;        /* decode-shaped MoE kernels */
+    int moe_chunk = 1;       /* decode-form MoE above 8 tokens: consecutive calls of at most 8 tokens */
     int moe_mfma = 1;        /* decode-shaped MoE on the staged MFMA kernels where the types allow */
     int moe_fused = 1;       /* ... in one launch with a device-wide barrier where the grid fits */
     int moe_fused_min_tok = 3; /* ... from this many tokens on (below, two launches are faster) */
     unsigned int moe_spin_limit = 1u << 20; /* polls before a barrier wait gives up (about a second); 0 fails it */
     int moe_prefill = 1;        /* grouped matrix-core form for larger token counts (forced above 64) */
-    int moe_prefill_min_tok = 17; /* ... from this many tokens, when the workspace is sized for it */
+    int moe_prefill_min_tok = 24; /* ... from this many tokens, when the workspace is sized for it (config 4: 8-token
+                                     decode calls 201.5 us against 201.7 grouped at 24 tokens, 136 against 159 at 16) */
     int moe_dn_split = 0;    /* down launch blocks per row tile: 0 auto, 1, 2 */
     std::map<std::string, int> occ; /* resident blocks per CU, by kernel name and LDS bytes */
     int gm_min_m = 5;        /* le_gemm uses the MFMA GEMM from this many tokens on (below: the
@@ -550,6 +552,8 @@ int le_set_option(le_ctx *c, const char *name, int value) {
         c->moe_fused = value ? 1 : 0;
     } else if (n == "moe_mfma") {
         c->moe_mfma = value ? 1 : 0;
+    } else if (n == "moe_chunk") {
+        c->moe_chunk = value ? 1 : 0;
     } else if (n == "moe_fast") {
         c->moe_fast = value ? 1 : 0;
     } else if (n == "ms") {
@@ -779,6 +783,20 @@ static int moe_layer_impl(le_ctx *c, int ty_gate, int ty_up, int ty_down, const 
     }
     if (ws_bytes < le_moe_workspace_size(n_tok, k, ff)) return c->fail(LE_ERR_WORKSPACE, "workspace needs %zu bytes", le_moe_workspace_size(n_tok, k, ff));
     if (!al16(h) || !al16(ws)) return c->fail(LE_ERR_ALIGN, "h and ws must be 16-byte aligned");
+    /* 9..64 tokens in the decode form: stream-ordered calls of at most 8 tokens, each on the
+     * decode kernels' fast paths (config 4, 16 tokens: 442 -> 136 us against one call on the
+     * member-chunk kernels; 12 tokens 313 -> 115 us); each call reuses the workspace after the previous one */
+    if (n_tok > 8 && c->moe_chunk) {
+        for (int t0 = 0; t0 < n_tok; t0 += 8) {
+            const int nt = n_tok - t0 < 8 ? n_tok - t0 : 8;
+            const int rc = moe_layer_impl(c, ty_gate, ty_up, ty_down, gate, up, down, gptr, uptr, dptr, n_exp, k, hidden, ff,
+                                          logits + (size_t)t0 * n_exp, h + (size_t)t0 * hidden, nt, out + (size_t)t0 * hidden,
+                                          idx_out ? idx_out + (size_t)t0 * k : nullptr, w_out ? w_out + (size_t)t0 * k : nullptr,
+                                          ws, ws_bytes, stream);
+            if (rc) return rc;
+        }
+        return LE_OK;
+    }
     const size_t lds = (size_t)8 * xtok_bytes(hidden);
     if (lds + 16384 > c->lds_limit) return c->fail(LE_ERR_SHAPE, "hidden=%d exceeds the LDS budget", hidden);
     MoeArgs a{gate, up, down, logits, h, out, (char *)ws + kMoeBarBytes, idx_out, w_out, n_tok, n_exp, k, hidden, ff,
