@@ -113,7 +113,8 @@ struct le_ctx {
     int gq = 1;              /* Q4_K GEMM on the generic kernels (le_gq_*) instead of le_gm_12_* */
     int gq_min_m = 9;        /* other types: smallest M on the matrix-core GEMM (below: vector kernels) */
     int gq_cfg = 0;          /* generic GEMM block shape (tokens x rows, waves): 0 auto, 1 (32x256, 4), 2 (64x256, 4),
-                                3 (128x256, 4), 4 (128x128, 4), 5 (64x256, 8), 6 (128x256, 8), 7 (32x256, 8) */
+                                3 (128x256, 4), 4 (128x128, 4), 5 (64x256, 8), 6 (128x256, 8), 7 (32x256, 8),
+                                8 (64x128, 4), 9 (32x128, 4) */
     int gq_ksplit = 0;       /* generic GEMM K slices: 0 auto, else 1, 2, 4, 8 */
     std::vector<hipModule_t> mods;
     std::map<std::string, hipFunction_t> fns;
@@ -517,7 +518,7 @@ int le_set_option(le_ctx *c, const char *name, int value) {
         if (value < 1) return c->fail(LE_ERR_ARG, "gq_min_m must be >= 1");
         c->gq_min_m = value;
     } else if (n == "gq_cfg") {
-        if (value < 0 || value > 7) return c->fail(LE_ERR_ARG, "gq_cfg must be 0..7");
+        if (value < 0 || value > 9) return c->fail(LE_ERR_ARG, "gq_cfg must be 0..9");
         c->gq_cfg = value;
     } else if (n == "gq_ksplit") {
         if (value != 0 && value != 1 && value != 2 && value != 4 && value != 8)
@@ -955,12 +956,16 @@ static int gq_tab(int ty) { return ty == LE_TYPE_IQ2_XXS ? 6144 : ty == LE_TYPE_
 static int gq_launch(le_ctx *c, int ty, const void *w, const float *x, int m, float *y, int rows, int cols, void *ws,
                      size_t ws_bytes, hipStream_t st) {
     /* block shapes: (WM, WN, TM, TN) -> BM = 32 TM WM tokens, BN = 32 TN WN rows */
-    static const int cfgs[7][4] = {{1, 4, 1, 2}, {1, 4, 2, 2}, {1, 4, 4, 2}, {2, 2, 2, 2}, {1, 8, 2, 1}, {1, 8, 4, 1}, {1, 8, 1, 1}};
-    /* measured on the config shapes: 8 waves (two per SIMD, so one wave's weight decoding runs
-     * under the other's MFMAs), 64 x 256 tiles up to 64 tokens, 128 x 256 above */
-    /* 32 x 256 tiles up to 32 tokens for the types other than Q4_K (Q6_K M=17: 39.6 -> 34.1 us,
-     * IQ2_XXS 27.3 -> 25.8; Q4_K measured slower: 34.0 -> 36.1) */
-    int ci = c->gq_cfg ? c->gq_cfg - 1 : m <= 32 && ty != LE_TYPE_Q4_K ? 6 : m <= 64 ? 4 : 5;
+    static const int cfgs[9][4] = {{1, 4, 1, 2}, {1, 4, 2, 2}, {1, 4, 4, 2}, {2, 2, 2, 2}, {1, 8, 2, 1}, {1, 8, 4, 1}, {1, 8, 1, 1}, {1, 4, 2, 1}, {1, 4, 1, 1}};
+    /* block shape by token count and type, from a sweep of every type at its config shape
+     * (M = 17, 32, 48, 64): up to 32 tokens 32 x 128 tiles on 4 waves (Q4_K M=17 33.4 -> 26.4 us,
+     * Q6_K 39.4 -> 28.5, Q8_0 64.5 -> 55.8, IQ3_XXS 39.0 -> 28.7); 33..64 tokens 32 x 128 for Q4_K
+     * (two token tiles: 37.7 -> 32.6 us at M=64), 64 x 128 on 4 waves for Q6_K and IQ3_XXS,
+     * 64 x 256 on 8 waves for Q8_0 and IQ2_XXS; above, 128 x 256 on 8 waves */
+    int ci = 5;
+    if (m <= 32) ci = 8;
+    else if (m <= 64) ci = ty == LE_TYPE_Q4_K ? 8 : (ty == LE_TYPE_Q6_K || ty == LE_TYPE_IQ3_XXS) ? 7 : 4;
+    if (c->gq_cfg) ci = c->gq_cfg - 1;
     const int nsb = cols / 256, srec = gq_srec(ty);
     auto lds_of = [&](int i) {
         const int BM = 32 * cfgs[i][0] * cfgs[i][2], BN = 32 * cfgs[i][1] * cfgs[i][3];
@@ -980,8 +985,10 @@ static int gq_launch(le_ctx *c, int ty, const void *w, const float *x, int m, fl
     if (c->gq_ksplit > 0) {
         ks = c->gq_ksplit;
     } else {
-        /* K slices while the grid stays within the resident blocks (one wave of blocks) */
-        const int per_cu = c->blocks_per_cu(name, nthr, lds);
+        /* K slices while the grid stays within the resident blocks (one wave of blocks); the
+         * 4-wave tiles stop at one block per CU (measured best: Q4_K 14336x4096 M=17, 32x128
+         * tiles: 26.2 us at 224 blocks, 29.7 at 448) */
+        const int per_cu = nthr == 256 ? 1 : c->blocks_per_cu(name, nthr, lds);
         const long long cap = (long long)c->cus * (per_cu > 0 ? per_cu : 1);
         while (ks < 8 && ntr * mt * 2 * ks <= cap && nsb % (2 * ks) == 0) ks *= 2;
     }
