@@ -961,10 +961,14 @@ static int gq_launch(le_ctx *c, int ty, const void *w, const float *x, int m, fl
      * (M = 17, 32, 48, 64): up to 32 tokens 32 x 128 tiles on 4 waves (Q4_K M=17 33.4 -> 26.4 us,
      * Q6_K 39.4 -> 28.5, Q8_0 64.5 -> 55.8, IQ3_XXS 39.0 -> 28.7); 33..64 tokens 32 x 128 for Q4_K
      * (two token tiles: 37.7 -> 32.6 us at M=64), 64 x 128 on 4 waves for Q6_K and IQ3_XXS,
-     * 64 x 256 on 8 waves for Q8_0 and IQ2_XXS; above, 128 x 256 on 8 waves */
+     * 64 x 256 on 8 waves for Q8_0 and IQ2_XXS; 65..128 tokens 64 x 128 on 4 waves for Q4_K and Q6_K
+     * (Q4_K M=128 52.2 -> 45.6 us, Q6_K 71.4 -> 53.1); above, 128 x 256 on 4 waves for Q6_K
+     * (M=512 140.5 -> 128.5 us) and 128 x 256 on 8 waves otherwise */
     int ci = 5;
     if (m <= 32) ci = 8;
     else if (m <= 64) ci = ty == LE_TYPE_Q4_K ? 8 : (ty == LE_TYPE_Q6_K || ty == LE_TYPE_IQ3_XXS) ? 7 : 4;
+    else if (m <= 128 && (ty == LE_TYPE_Q4_K || ty == LE_TYPE_Q6_K)) ci = 7;
+    else if (ty == LE_TYPE_Q6_K) ci = 2;
     if (c->gq_cfg) ci = c->gq_cfg - 1;
     const int nsb = cols / 256, srec = gq_srec(ty);
     auto lds_of = [&](int i) {
