@@ -160,11 +160,25 @@ def bench_layer(eng, mats, steps, warmup):
     xs = {c: torch.from_numpy(le.fill_normal(c, c)).cuda() for (_, _, _, c) in mats}
     ys = [torch.empty(r, dtype=torch.float32, device="cuda") for (_, _, r, _) in mats]
 
+    # "qkv": q, k and v (same input) as one matvec over a pointer table of 1024-row slots: q's four
+    # row blocks, then k and v, outputs [q | k | v] (Gpu::mv_ptrs, src/gpu.rs:228-237)
+    tabs = {}
+    for i, (name, ty, r, c) in enumerate(mats):
+        if name == "qkv":
+            rb = le.row_bytes(ty, c)
+            assert r % 1024 == 0
+            tabs[i] = []
+            for k in range(ncopy):
+                base = devs[i][k].data_ptr()
+                tabs[i].append(torch.tensor([base + j * 1024 * rb for j in range(r // 1024)], dtype=torch.int64, device="cuda"))
+
     def record():
         for k in range(ncopy):
             for i, (name, ty, r, c) in enumerate(mats):
                 if name == "down_swiglu":  # SwiGLU of the previous (gate | up) output fused into the down matvec
                     eng.mv_swiglu(ty, devs[i][k], ys[i - 1], ys[i], r, c)
+                elif name == "qkv":
+                    eng.mv_ptrs(ty, tabs[i][k], xs[c], ys[i], 1024, c, 0, r // 1024)
                 else:
                     eng.mv(ty, devs[i][k], xs[c], ys[i], r, c)
     ms = graph_time(record, ncopy, steps, warmup, min_launches=40)
@@ -461,11 +475,12 @@ def main():
         sec["config1_q4k_4096x4096"] = {"us": round(r["us"], 3), "GB/s": round(r["gbs"], 1),
                                         "frac_hbm": round(r["gbs"] / HBM_PEAK_GBS, 4)}
         log("config1", sec["config1_q4k_4096x4096"])
-        # the reference's dense decode layer: q, k, v, o, gate and up as one matrix of
-        # concatenated rows (src/gpu/dense.rs:13,67-73,309), then down on silu(gate) * up formed
-        # inside the down matvec (swiglu_gu + quant_x + matvec_14 in the reference, :310-312)
-        layer = [("wq", le.Q4_K, 4096, 4096), ("wk", le.Q4_K, 1024, 4096), ("wv", le.Q4_K, 1024, 4096),
-                 ("wo", le.Q4_K, 4096, 4096), ("gate_up", le.Q4_K, 28672, 4096), ("down_swiglu", le.Q6_K, 4096, 14336)]
+        # the reference's dense decode layer: q, k, v (src/gpu/dense.rs:284), o, gate and up as one
+        # matrix of concatenated rows (:67-73,309), then down on silu(gate) * up formed inside the
+        # down matvec (swiglu_gu + quant_x + matvec_14 in the reference, :310-312)
+        # q, k and v read the same input, so they run as one matvec over a pointer table of 1024-row
+        # slots (q's four row blocks, k, v; weights as separate tensors, as in the GGUF file)
+        layer = [("qkv", le.Q4_K, 6144, 4096), ("wo", le.Q4_K, 4096, 4096), ("gate_up", le.Q4_K, 28672, 4096), ("down_swiglu", le.Q6_K, 4096, 14336)]
         sec["config2_llama3_8b_layer"] = bench_layer(eng, layer, max(40, steps2 // 8), 8)
         log("config2 layer", sec["config2_llama3_8b_layer"])
         sec["config2_q8_0_head_32000x4096"] = bench_layer(eng, [("head", le.Q8_0, 32000, 4096)], max(40, steps2 // 8), 8)
