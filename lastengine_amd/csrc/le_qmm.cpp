@@ -91,7 +91,8 @@ struct le_ctx {
     int gm_mh = 1;           /* le_gemm, Q4_K, 3..8 tokens: the staged f16 MFMA kernel */
     int gm_mh_max = 16;      /* ... up to this many tokens (8 or 16; 16 only where K fits its LDS) */
     int gm_mh_shape = 0;     /* ... its (P, NW) as 10 * P + NW: 0 auto, 14, 18, 24, 22 */
-    int mq6 = 1, ms_p6 = 2;  /* Q6_K decode matvec on the staged MFMA kernels, super-blocks per step */
+    int mq6 = 1, ms_p6 = 1;  /* Q6_K decode matvec on the staged MFMA kernels, super-blocks per step (1: 1024x4096 5.6 -> 5.0 us,
+                                4096x4096 6.3 -> 5.5, 14336x4096 14.8 -> 14.2 against 2) */
     int mqiq = 1, ms_piq = 2; /* IQ2_XXS / IQ3_XXS likewise */
     int moe_fast = 1;        /* decode-shaped MoE kernels */
     int moe_chunk = 1;       /* decode-form MoE above 8 tokens: consecutive calls of at most 8 tokens */
