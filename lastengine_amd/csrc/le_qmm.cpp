@@ -115,7 +115,7 @@ struct le_ctx {
     int gq_min_m = 9;        /* other types: smallest M on the matrix-core GEMM (below: vector kernels) */
     int gq_cfg = 0;          /* generic GEMM block shape (tokens x rows, waves): 0 auto, 1 (32x256, 4), 2 (64x256, 4),
                                 3 (128x256, 4), 4 (128x128, 4), 5 (64x256, 8), 6 (128x256, 8), 7 (32x256, 8),
-                                8 (64x128, 4), 9 (32x128, 4) */
+                                8 (64x128, 4), 9 (32x128, 4), 10 (128x128, 4) */
     int gq_ksplit = 0;       /* generic GEMM K slices: 0 auto, else 1, 2, 4, 8 */
     std::vector<hipModule_t> mods;
     std::map<std::string, hipFunction_t> fns;
@@ -523,7 +523,7 @@ int le_set_option(le_ctx *c, const char *name, int value) {
         if (value < 1) return c->fail(LE_ERR_ARG, "gq_min_m must be >= 1");
         c->gq_min_m = value;
     } else if (n == "gq_cfg") {
-        if (value < 0 || value > 9) return c->fail(LE_ERR_ARG, "gq_cfg must be 0..9");
+        if (value < 0 || value > 10) return c->fail(LE_ERR_ARG, "gq_cfg must be 0..10");
         c->gq_cfg = value;
     } else if (n == "gq_ksplit") {
         if (value != 0 && value != 1 && value != 2 && value != 4 && value != 8)
@@ -961,18 +961,20 @@ static int gq_tab(int ty) { return ty == LE_TYPE_IQ2_XXS ? 6144 : ty == LE_TYPE_
 static int gq_launch(le_ctx *c, int ty, const void *w, const float *x, int m, float *y, int rows, int cols, void *ws,
                      size_t ws_bytes, hipStream_t st) {
     /* block shapes: (WM, WN, TM, TN) -> BM = 32 TM WM tokens, BN = 32 TN WN rows */
-    static const int cfgs[9][4] = {{1, 4, 1, 2}, {1, 4, 2, 2}, {1, 4, 4, 2}, {2, 2, 2, 2}, {1, 8, 2, 1}, {1, 8, 4, 1}, {1, 8, 1, 1}, {1, 4, 2, 1}, {1, 4, 1, 1}};
+    static const int cfgs[10][4] = {{1, 4, 1, 2}, {1, 4, 2, 2}, {1, 4, 4, 2}, {2, 2, 2, 2}, {1, 8, 2, 1}, {1, 8, 4, 1}, {1, 8, 1, 1}, {1, 4, 2, 1}, {1, 4, 1, 1}, {1, 4, 4, 1}};
     /* block shape by token count and type, from a sweep of every type at its config shape
      * (M = 17, 32, 48, 64): up to 32 tokens 32 x 128 tiles on 4 waves (Q4_K M=17 33.4 -> 26.4 us,
      * Q6_K 39.4 -> 28.5, Q8_0 64.5 -> 55.8, IQ3_XXS 39.0 -> 28.7); 33..64 tokens 32 x 128 for Q4_K
      * (two token tiles: 37.7 -> 32.6 us at M=64), 64 x 128 on 4 waves for Q6_K and IQ3_XXS,
-     * 64 x 256 on 8 waves for Q8_0 and IQ2_XXS; 65..128 tokens 64 x 128 on 4 waves for Q4_K and Q6_K
-     * (Q4_K M=128 52.2 -> 45.6 us, Q6_K 71.4 -> 53.1); above, 128 x 256 on 4 waves for Q6_K
+     * 64 x 256 on 8 waves for Q8_0 and IQ2_XXS; 65..128 tokens 64 x 128 on 4 waves for Q4_K (M=128
+     * 52.2 -> 45.6 us) and 128 x 128 on 4 waves for Q6_K and IQ3_XXS (74.0 -> 49.9, 55.6 -> 49.7);
+     * above, 128 x 256 on 4 waves for Q6_K
      * (M=512 140.5 -> 128.5 us) and 128 x 256 on 8 waves otherwise */
     int ci = 5;
     if (m <= 32) ci = 8;
     else if (m <= 64) ci = ty == LE_TYPE_Q4_K ? 8 : (ty == LE_TYPE_Q6_K || ty == LE_TYPE_IQ3_XXS) ? 7 : 4;
-    else if (m <= 128 && (ty == LE_TYPE_Q4_K || ty == LE_TYPE_Q6_K)) ci = 7;
+    else if (m <= 128 && ty == LE_TYPE_Q4_K) ci = 7;
+    else if (m <= 128 && (ty == LE_TYPE_Q6_K || ty == LE_TYPE_IQ3_XXS)) ci = 9;
     else if (ty == LE_TYPE_Q6_K) ci = 2;
     if (c->gq_cfg) ci = c->gq_cfg - 1;
     const int nsb = cols / 256, srec = gq_srec(ty);

@@ -53,7 +53,7 @@ def test_gemm_full_shapes(engine, name, m):
 
 
 @pytest.mark.parametrize("name", NAMES)
-@pytest.mark.parametrize("cfg", [1, 2, 3, 4, 5, 6, 7, 8, 9])
+@pytest.mark.parametrize("cfg", [1, 2, 3, 4, 5, 6, 7, 8, 9, 10])
 @pytest.mark.parametrize("rows,cols,m,ks", [(300, 512, 17, 0), (513, 768, 65, 1), (96, 4096, 40, 4), (1000, 1024, 130, 2)])
 def test_gemm_tiles_and_slices(fresh_engine, name, cfg, rows, cols, m, ks):
     """Every block shape (32/64/128 tokens x 128/256 rows, 4 or 8 waves) with ragged row and token tiles and

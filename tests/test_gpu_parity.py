@@ -315,7 +315,7 @@ def test_options_validated(fresh_engine):
     engine = fresh_engine
     for k, v in good.items():
         engine.set_option(k, v)
-    for k, v in [("no_such_option", 1), ("gm_tile", 33), ("gm_ksplit", 3), ("gm_split", 2), ("gm_mh_shape", 13), ("gm_mh_max", 12), ("ms_p6", 4), ("ms_piq", 3), ("gq_cfg", 10), ("gq_ksplit", 3), ("gq_min_m", 0)]:
+    for k, v in [("no_such_option", 1), ("gm_tile", 33), ("gm_ksplit", 3), ("gm_split", 2), ("gm_mh_shape", 13), ("gm_mh_max", 12), ("ms_p6", 4), ("ms_piq", 3), ("gq_cfg", 11), ("gq_ksplit", 3), ("gq_min_m", 0)]:
         with pytest.raises(le.LeError) as e:
             engine.set_option(k, v)
         assert e.value.code == -1, (k, v)
