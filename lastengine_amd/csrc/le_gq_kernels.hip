@@ -77,6 +77,7 @@ struct GqArgs {
     const u8 *w2;
     float *y2;
     int dual, pad2;
+    const float *up; /* non-null: the activation rows are silu(x) * up (the MoE down input) */
 };
 
 /* Workspace layout: A planes (mp * K halves), S records (mp/32 * nsb * SREC bytes), token scales
@@ -270,6 +271,11 @@ __device__ __forceinline__ void gq_xprep_body(const GqArgs &a, u8 *ws) {
             if (live && g < ng) {
                 P[i] = ((const LE_GLOBAL float4 *)xr)[2 * g];
                 Q[i] = ((const LE_GLOBAL float4 *)xr)[2 * g + 1];
+                if (a.up) {
+                    const LE_GLOBAL float4 *ur = (const LE_GLOBAL float4 *)(a.up + src * K);
+                    P[i] = le_silu_mul4(P[i], ur[2 * g]);
+                    Q[i] = le_silu_mul4(Q[i], ur[2 * g + 1]);
+                }
             } else {
                 P[i] = Q[i] = make_float4(0.f, 0.f, 0.f, 0.f);
             }
@@ -278,7 +284,8 @@ __device__ __forceinline__ void gq_xprep_body(const GqArgs &a, u8 *ws) {
         for (int i = 0; i < XG; i++) am = fmaxf(am, amax8(P[i], Q[i]));
     } else if (live) {
         for (int i = tid; i < K / 4; i += 256) {
-            const float4 v = ((const LE_GLOBAL float4 *)xr)[i];
+            float4 v = ((const LE_GLOBAL float4 *)xr)[i];
+            if (a.up) v = le_silu_mul4(v, ((const LE_GLOBAL float4 *)(a.up + src * K))[i]);
             am = fmaxf(am, fmaxf(fmaxf(fabsf(v.x), fabsf(v.y)), fmaxf(fabsf(v.z), fabsf(v.w))));
         }
     }
@@ -345,6 +352,11 @@ __device__ __forceinline__ void gq_xprep_body(const GqArgs &a, u8 *ws) {
             if (live) {
                 p = ((const LE_GLOBAL float4 *)xr)[2 * g];
                 q = ((const LE_GLOBAL float4 *)xr)[2 * g + 1];
+                if (a.up) {
+                    const LE_GLOBAL float4 *ur = (const LE_GLOBAL float4 *)(a.up + src * K);
+                    p = le_silu_mul4(p, ur[2 * g]);
+                    q = le_silu_mul4(q, ur[2 * g + 1]);
+                }
             }
             convert(g, p, q);
         }

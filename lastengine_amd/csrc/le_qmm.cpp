@@ -719,7 +719,7 @@ struct MoePreArgs {
 
 static int mm_grouped(le_ctx *c, int ty, const void *const *ptrs, const void *w, const void *const *ptrs2, const void *w2,
                       const int *off, const int *in_idx, const int *out_idx, int nslot, int npair, const float *x, float *y,
-                      float *y2, int rows, int cols, void *ws, size_t ws_bytes, hipStream_t stream);
+                      float *y2, int rows, int cols, void *ws, size_t ws_bytes, hipStream_t stream, const float *up = nullptr);
 
 static int moe_prefill(le_ctx *c, int ty_gate, int ty_down, const void *gate, const void *up, const void *down,
                        const void *const *gptr, const void *const *uptr, const void *const *dptr, int n_exp, int k,
@@ -739,15 +739,13 @@ static int moe_prefill(le_ctx *c, int ty_gate, int ty_down, const void *gate, co
     /* gate and up in one grouped launch (one plan and one activation pre-pass for both) */
     if (!rc) rc = mm_grouped(c, ty_gate, gptr, gate, uptr, up, off, in_idx, out_idx, n_exp, np, h, G, U, ff, hidden, gws, gws_bytes, st);
     if (rc) return rc;
-    long long n = (long long)np * ff;
-    unsigned blocks = (unsigned)((n + 255) / 256 < 8192 ? (n + 255) / 256 : 8192);
-    void *sargs[] = {&G, &U, &n};
-    rc = c->launch("le_moe_swiglu", dim3(blocks), 256, 0, st, sargs);
-    /* down: the activation rows are the pairs themselves, in the same grouped order */
-    if (!rc) rc = mm_grouped(c, ty_down, dptr, down, nullptr, nullptr, off, out_idx, out_idx, n_exp, np, G, D, nullptr, hidden, ff, gws, gws_bytes, st);
+    /* down: the activation rows are the pairs themselves, in the same grouped order, each formed
+     * as silu(gate) * up by the down matmul's pre-pass */
+    rc = mm_grouped(c, ty_down, dptr, down, nullptr, nullptr, off, out_idx, out_idx, n_exp, np, G, D, nullptr, hidden, ff, gws,
+                    gws_bytes, st, U);
     if (rc) return rc;
     long long no = (long long)n_tok * hidden;
-    blocks = (unsigned)((no + 255) / 256 < 8192 ? (no + 255) / 256 : 8192);
+    const unsigned blocks = (unsigned)((no + 255) / 256 < 8192 ? (no + 255) / 256 : 8192);
     const float *Dc = D, *Wc = topw;
     void *cargs[] = {&Dc, &Wc, &out, &n_tok, &k, &hidden};
     return c->launch("le_moe_combine", dim3(blocks), 256, 0, st, cargs);
@@ -945,6 +943,7 @@ struct GqHostArgs {
     const void *w2;
     float *y2;
     int dual, pad2;
+    const float *up;
 };
 static int gq_slot(int ty) {
     switch (ty) {
@@ -1013,7 +1012,7 @@ static int gq_launch(le_ctx *c, int ty, const void *w, const float *x, int m, fl
     float *part = nullptr;
     const size_t poff = gq_part_off(ty, m, cols);
     if (ks > 1 && ws_bytes >= poff + (size_t)ks * m * rows * 4) part = (float *)((char *)ws + poff);
-    GqHostArgs a{w, x, y, rows, cols, m, mp, ks, nullptr, 0, nullptr, nullptr, nullptr, 0, 0, 0, 0, part, nullptr, nullptr, nullptr, 0, 0};
+    GqHostArgs a{w, x, y, rows, cols, m, mp, ks, nullptr, 0, nullptr, nullptr, nullptr, 0, 0, 0, 0, part, nullptr, nullptr, nullptr, 0, 0, nullptr};
     void *args[] = {&a, &ws};
     char pname[32];
     snprintf(pname, sizeof pname, "le_gq_xprep_%d", ty);
@@ -1046,7 +1045,7 @@ size_t le_mm_grouped_workspace_size(int ty, int nslot, int npair, int cols) {
  * also multiplied by it into y2, in the same launches (one plan, one pre-pass, one grid). */
 static int mm_grouped(le_ctx *c, int ty, const void *const *ptrs, const void *w, const void *const *ptrs2, const void *w2,
                       const int *off, const int *in_idx, const int *out_idx, int nslot, int npair, const float *x, float *y,
-                      float *y2, int rows, int cols, void *ws, size_t ws_bytes, hipStream_t stream) {
+                      float *y2, int rows, int cols, void *ws, size_t ws_bytes, hipStream_t stream, const float *up) {
     const bool dual = ptrs2 || w2;
     if (dual && !y2) return c->fail(LE_ERR_ARG, "null second output");
     if (!supported(ty)) return c->fail(LE_ERR_TYPE, "no kernel for type %d", ty);
@@ -1075,7 +1074,7 @@ static int mm_grouped(le_ctx *c, int ty, const void *const *ptrs, const void *w,
         (unsigned long long)rows * le_row_bytes(ty, cols) >= (1ull << 32))
         return c->fail(LE_ERR_SHAPE, "grouped GEMM too large (32-bit weight or activation offsets)");
     GqHostArgs a{w, x, y, rows, cols, mp, mp, 1, ptrs, (unsigned long long)rows * le_row_bytes(ty, cols), off, in_idx,
-                 out_idx, nslot, maxt, BM, 0, nullptr, ptrs2, w2, y2, dual ? 1 : 0, 0};
+                 out_idx, nslot, maxt, BM, 0, nullptr, ptrs2, w2, y2, dual ? 1 : 0, 0, up};
     int srec_arg = srec;
     void *pargs[] = {&a, &ws, &srec_arg};
     int rc = c->launch("le_gq_plan", dim3(1), 1024, 0, (hipStream_t)stream, pargs);

@@ -2950,7 +2950,7 @@ LE_MOE_DOWN(8) LE_MOE_DOWN(12) LE_MOE_DOWN(14) LE_MOE_DOWN(16) LE_MOE_DOWN(18)
  * For prefill-sized token counts (the reference's TMAX = 2048 per chunk, src/gpu/prefill.rs:6) the
  * layer runs as: le_moe_route_tok (top-k and weights per token) -> le_moe_group (pairs grouped by
  * expert, each expert's pairs in token order: the host grouping of src/gpu/prefill.rs:153-214 on
- * the device) -> grouped matmul gate and up -> le_moe_swiglu -> grouped matmul down ->
+ * the device) -> grouped matmul gate and up (one launch) -> grouped matmul down on silu(gate) * up ->
  * le_moe_combine (weighted sum in selection order, src/cpu_ref.rs:242-259). */
 struct MoePre {
     const float *logits;
@@ -3024,31 +3024,37 @@ extern "C" __global__ void __launch_bounds__(256) le_moe_group(MoePre a) {
     if (threadIdx.x == 0) a.off[e] = off;
     int base = off;
     __shared__ int wcnt[4];
-    for (int p0 = 0; p0 < npair; p0 += 256) {
-        const int p = p0 + (int)threadIdx.x;
-        const int x = p < npair ? a.topi[p] : -1;
-        const unsigned long long mine = __ballot(x == e);
-        if (lane == 0) wcnt[wave] = __popcll(mine);
+    /* 2048 pairs per round, 8 consecutive ones per thread: thread order is pair order, so an
+     * exclusive scan of the per-thread match counts gives each match its rank */
+    for (int p0 = 0; p0 < npair; p0 += 2048) {
+        const int pt = p0 + 8 * (int)threadIdx.x;
+        unsigned m = 0;
+#pragma unroll
+        for (int j = 0; j < 8; j++) m |= (pt + j < npair && a.topi[pt + j] == e ? 1u : 0u) << j;
+        const int cnt = __popc(m);
+        int incl = cnt;
+#pragma unroll
+        for (int o = 1; o < 64; o <<= 1) {
+            const int t = __shfl_up(incl, o);
+            if (lane >= o) incl += t;
+        }
+        if (lane == 63) wcnt[wave] = incl;
         __syncthreads();
         int before = 0;
         for (int w = 0; w < wave; w++) before += wcnt[w];
-        if (x == e) {
-            const int r = base + before + __popcll(mine & ((1ull << lane) - 1ull));
-            a.in_idx[r] = p / a.k;
-            a.out_idx[r] = p;
+        int r = base + before + incl - cnt;
+#pragma unroll
+        for (int j = 0; j < 8; j++) {
+            if ((m >> j) & 1u) {
+                a.in_idx[r] = (pt + j) / a.k;
+                a.out_idx[r] = pt + j;
+                r++;
+            }
         }
         base += wcnt[0] + wcnt[1] + wcnt[2] + wcnt[3];
         __syncthreads();
     }
     if (e == a.n_exp - 1 && threadIdx.x == 0) a.off[a.n_exp] = base;
-}
-
-/* act[p][c] = silu(g) * u over the grouped pairs' gate / up rows (in place into g). */
-extern "C" __global__ void __launch_bounds__(256) le_moe_swiglu(float *g, const float *u, long long n) {
-    for (long long i = (long long)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (long long)gridDim.x * blockDim.x) {
-        const float x = g[i];
-        g[i] = x / (1.0f + __expf(-x)) * u[i];
-    }
 }
 
 /* out[t][c] = sum over s < k of w[t k + s] * d[t k + s][c], added in selection order. */
