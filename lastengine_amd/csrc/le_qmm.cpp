@@ -91,6 +91,9 @@ struct le_ctx {
     int gm_mh = 1;           /* le_gemm, Q4_K, 3..8 tokens: the staged f16 MFMA kernel */
     int gm_mh_max = 16;      /* ... up to this many tokens (8 or 16; 16 only where K fits its LDS) */
     int gm_mh_shape = 0;     /* ... its (P, NW) as 10 * P + NW: 0 auto, 14, 18, 24, 22 */
+    int mq_q8 = 1;           /* int8 mode on the staged MFMA kernels: Q4_K 14336x4096 13.1 -> 9.9 us, Q6_K 4096x14336
+                                27.7 -> 15.3, IQ3_XXS 16.6 -> 15.7 against the vector kernels (IQ2_XXS stays
+                                there: 10.5 against 11.3) */
     int mq6 = 1, ms_p6 = 1;  /* Q6_K decode matvec on the staged MFMA kernels, super-blocks per step (1: 1024x4096 5.6 -> 5.0 us,
                                 4096x4096 6.3 -> 5.5, 14336x4096 14.8 -> 14.2 against 2) */
     int mqiq = 1, ms_piq = 2; /* IQ2_XXS / IQ3_XXS likewise */
@@ -219,7 +222,8 @@ int pick_g(int nsb) {
 
 /* MFMA decode matvec (Q4_K, Q6_K): one block of mq_waves waves per 16-row tile at a time. */
 int mq_launch(le_ctx *c, int ty, const void *const *ptrs, const void *w, const float *x, long long x_slot, float *y,
-              long long y_slot, int rows, int cols, int slots, hipStream_t st, int swiglu = 0) {
+              long long y_slot, int rows, int cols, int slots, hipStream_t st, int swiglu = 0, const int8_t *xq8 = nullptr,
+              const float *xd8 = nullptr) {
     const long long ntile = (rows + 15) / 16;
     const int nsb = cols / 256, U = c->mq_steps;
     /* when the row tiles alone leave CUs idle, split K over twice the waves (shorter chains) */
@@ -241,6 +245,8 @@ int mq_launch(le_ctx *c, int ty, const void *const *ptrs, const void *w, const f
     a.cols = cols;
     a.ntok = 1;
     a.swiglu = swiglu;
+    a.xq8 = xq8; /* int8 mode: the staged kernels build their image from xq / xd */
+    a.xd8 = xd8;
     void *args[] = {&a};
     char name[64];
     size_t lds = (size_t)nsb * 608 + (size_t)NW * 64;
@@ -263,7 +269,7 @@ int mq_launch(le_ctx *c, int ty, const void *const *ptrs, const void *w, const f
     }
     /* no unstaged MFMA variant for the other types, nor one that forms silu(gate) * up: the caller
      * falls back to the vector kernels */
-    if (ty != LE_TYPE_Q4_K || swiglu) return 1;
+    if (ty != LE_TYPE_Q4_K || swiglu || xq8) return 1;
     snprintf(name, sizeof name, "le_mq_12_w%d_u%d", NW, U);
     return c->launch(name, dim3((unsigned)gx, (unsigned)slots), NW * 64, lds, st, args);
 }
@@ -336,9 +342,9 @@ int mv_launch(le_ctx *c, int ty, const void *const *ptrs, const void *w, const f
     }
     const int nsb = cols / 256, G = pick_g(nsb), S = nsb / G;
     const bool iq = ty == LE_TYPE_IQ2_XXS || ty == LE_TYPE_IQ3_XXS;
-    if (!q8 && (ty == LE_TYPE_Q4_K || (ty == LE_TYPE_Q6_K && c->mq6) || (iq && c->mqiq)) && ntok == 1 && c->mq &&
-        (size_t)nsb * 608 + 1024 <= c->lds_limit) {
-        const int rc = mq_launch(c, ty, ptrs, w, x, x_slot, y, y_slot, rows, cols, slots, st, swiglu);
+    if ((ty == LE_TYPE_Q4_K || (ty == LE_TYPE_Q6_K && c->mq6) || (iq && c->mqiq)) && ntok == 1 && c->mq &&
+        (!q8 || (c->mq_q8 && ty != LE_TYPE_IQ2_XXS)) && (size_t)nsb * 608 + 1024 <= c->lds_limit) {
+        const int rc = mq_launch(c, ty, ptrs, w, x, x_slot, y, y_slot, rows, cols, slots, st, swiglu, xq8, xd8);
         if (rc != 1) return rc;
     }
     if (!q8 && ty == LE_TYPE_Q4_K && ntok >= 2 && c->mq && c->ms && c->ms_t) {
@@ -558,6 +564,8 @@ int le_set_option(le_ctx *c, const char *name, int value) {
         c->moe_fused = value ? 1 : 0;
     } else if (n == "moe_mfma") {
         c->moe_mfma = value ? 1 : 0;
+    } else if (n == "mq_q8") {
+        c->mq_q8 = value ? 1 : 0;
     } else if (n == "moe_chunk") {
         c->moe_chunk = value ? 1 : 0;
     } else if (n == "moe_fast") {

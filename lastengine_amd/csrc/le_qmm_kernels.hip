@@ -647,6 +647,35 @@ __device__ __forceinline__ void mq_quant_seg(int e, bool store, const float4 (&v
         st_f<COH>(fsv + sb * 8 + j, d * (float)sum);
     }
 }
+/* mq_quant_seg for int8 activations (le_matvec_q8): the 16 values of segment e are the caller's
+ * xq (|v| <= 127) with its block scale d = xd, split as v = 128 h + lo exactly. */
+template <int MAP = 0>
+__device__ __forceinline__ void mq_quant_seg_q8(int e, bool store, uint4 q, float d, uint4 *rec, float *dxp, float *fsv) {
+    const u32 qw[4] = {q.x, q.y, q.z, q.w};
+    u32 hw[4] = {0, 0, 0, 0}, lw[4] = {0, 0, 0, 0};
+    int sum = 0;
+#pragma unroll
+    for (int i = 0; i < 16; i++) {
+        const int v = (int)(int8_t)((qw[i >> 2] >> (8 * (i & 3))) & 255u);
+        const int h = (v + 64) >> 7;
+        const int lo = v - (h << 7);
+        hw[i >> 2] |= ((u32)h & 255u) << (8 * (i & 3));
+        lw[i >> 2] |= ((u32)lo & 255u) << (8 * (i & 3));
+        sum += v;
+    }
+    sum += __shfl_xor(sum, 1);
+    if (!store) return;
+    const int sb = e >> 4, j = (e & 15) >> 1, c = e & 1;
+    const int b = MAP ? 2 * (j >> 2) + c : 2 * (j >> 2) + (j & 1), s = MAP ? (j & 3) : 2 * ((j & 3) >> 1) + c;
+    const int r = (sb * 16 + b * 4 + s) * 2;
+    rec[r] = make_uint4(hw[0], hw[1], hw[2], hw[3]);
+    rec[r + 1] = make_uint4(lw[0], lw[1], lw[2], lw[3]);
+    if (c == 0) {
+        dxp[sb * 16 + j] = d * 128.0f;
+        dxp[sb * 16 + 8 + j] = d;
+        fsv[sb * 8 + j] = d * (float)sum;
+    }
+}
 __device__ __forceinline__ void mq_quant_x(const float *__restrict__ x, int K, uint4 *rec, float *dxp, float *fsv) {
     const int nseg = K >> 4; /* even: partners share trips */
     for (int e = threadIdx.x; e < nseg; e += blockDim.x) {
@@ -960,6 +989,15 @@ __device__ __forceinline__ void ms_q4k_body(const MvArgs &a) {
         const int ls = el >> 4;
         return ((ls / P) * sstep + sfirst + ls % P) * 16 + (el & 15);
     };
+    if (a.xq8) { /* int8 mode: the image holds the caller's xq, scale xd per 32 values (exact) */
+        issue(min((int)blockIdx.x, ntile - 1), active ? sfirst : 0); /* unpredicated: exact wait counts */
+        const int8_t *xq8 = a.xq8 + a.x_slot * slot;
+        const float *xd8 = a.xd8 + (a.x_slot >> 5) * slot;
+        for (int el0 = 0; el0 < nsegw; el0 += 64) {
+            const int el = el0 + lane, ge = gseg(min(el, nsegw - 1));
+            mq_quant_seg_q8<0>(el, el < nsegw, ldg16u((const u8 *)(xq8 + 16 * ge)), xd8[ge >> 1], rec, dxp, fsv);
+        }
+    } else {
     float4 xv[4];
     mq_load_seg_a(xs, gseg(min(lane, nsegw - 1)), a.cols, a.swiglu, xv);
     issue(min((int)blockIdx.x, ntile - 1), active ? sfirst : 0); /* unpredicated: exact wait counts */
@@ -967,6 +1005,7 @@ __device__ __forceinline__ void ms_q4k_body(const MvArgs &a) {
     for (int el = lane + 64; el < nsegw; el += 64) {
         mq_load_seg_a(xs, gseg(el), a.cols, a.swiglu, xv);
         mq_quant_seg(el, true, xv, rec, dxp, fsv);
+    }
     }
 
     const MsLane L = ms_lane<0>(lane);
@@ -1247,6 +1286,15 @@ __device__ __forceinline__ void ms_q6k_body(const MvArgs &a) {
         const int ls = el >> 4;
         return ((ls / P) * sstep + sfirst + ls % P) * 16 + (el & 15);
     };
+    if (a.xq8) { /* int8 mode: the image holds the caller's xq, scale xd per 32 values (exact) */
+        issue(min((int)blockIdx.x, ntile - 1), active ? sfirst : 0);
+        const int8_t *xq8 = a.xq8 + a.x_slot * slot;
+        const float *xd8 = a.xd8 + (a.x_slot >> 5) * slot;
+        for (int el0 = 0; el0 < nsegw; el0 += 64) {
+            const int el = el0 + lane, ge = gseg(min(el, nsegw - 1));
+            mq_quant_seg_q8<1>(el, el < nsegw, ldg16u((const u8 *)(xq8 + 16 * ge)), xd8[ge >> 1], rec, dxp, fsv);
+        }
+    } else {
     float4 xv[4];
     mq_load_seg_a(xs, gseg(min(lane, nsegw - 1)), a.cols, a.swiglu, xv);
     issue(min((int)blockIdx.x, ntile - 1), active ? sfirst : 0);
@@ -1254,6 +1302,7 @@ __device__ __forceinline__ void ms_q6k_body(const MvArgs &a) {
     for (int el = lane + 64; el < nsegw; el += 64) {
         mq_load_seg_a(xs, gseg(el), a.cols, a.swiglu, xv);
         mq_quant_seg<1>(el, true, xv, rec, dxp, fsv);
+    }
     }
 
     const MsLane L = ms_lane<1>(lane);
@@ -1410,6 +1459,15 @@ __device__ __forceinline__ void ms_iq_body(const MvArgs &a) {
         const int ls = el >> 4;
         return ((ls / P) * sstep + sfirst + ls % P) * 16 + (el & 15);
     };
+    if (a.xq8) { /* int8 mode: the image holds the caller's xq, scale xd per 32 values (exact) */
+        issue(min((int)blockIdx.x, ntile - 1), active ? sfirst : 0);
+        const int8_t *xq8 = a.xq8 + a.x_slot * slot;
+        const float *xd8 = a.xd8 + (a.x_slot >> 5) * slot;
+        for (int el0 = 0; el0 < nsegw; el0 += 64) {
+            const int el = el0 + lane, ge = gseg(min(el, nsegw - 1));
+            mq_quant_seg_q8<0>(el, el < nsegw, ldg16u((const u8 *)(xq8 + 16 * ge)), xd8[ge >> 1], rec, dxp, fsv);
+        }
+    } else {
     float4 xv[4];
     mq_load_seg_a(xs, gseg(min(lane, nsegw - 1)), a.cols, a.swiglu, xv);
     issue(min((int)blockIdx.x, ntile - 1), active ? sfirst : 0);
@@ -1417,6 +1475,7 @@ __device__ __forceinline__ void ms_iq_body(const MvArgs &a) {
     for (int el = lane + 64; el < nsegw; el += 64) {
         mq_load_seg_a(xs, gseg(el), a.cols, a.swiglu, xv);
         mq_quant_seg<0>(el, true, xv, rec, dxp, fsv);
+    }
     }
     __syncthreads(); /* the tables */
     const MsLane L = ms_lane<0>(lane);

@@ -222,3 +222,25 @@ def test_matvec_swiglu_slots(engine):
     for s in range(2):
         a = oracle.swiglu(gus[s][:cols], gus[s][cols:])
         check_close(got[s], oracle.matvec(ty, qs[s], rows, cols, a), _absmag(ty, qs[s], rows, cols, a)[0])
+
+
+@pytest.mark.parametrize("name", ["Q4_K", "Q6_K", "IQ3_XXS"])
+def test_matvec_q8_vector_path(fresh_engine, name):
+    """The int8 mode runs on the staged matrix-core kernels for these types by default; option
+    mq_q8=0 keeps them on the vector kernels. Both meet the same bar against the oracle."""
+    import torch
+    ty = le.MV_TYPES[name]
+    rows, cols = 96, 4096
+    q = random_blocks(ty, rows, cols, seed=ty + 5)
+    x = acts(cols, 17)
+    xq, xd, xs = oracle.quant_x(x)
+    want = oracle.matvec_q8(ty, q, rows, cols, xq, xd, xs)
+    wd = oracle.dequant_rows(ty, q, rows, cols).astype(np.float64)
+    mag = np.abs(wd) @ np.abs(np.repeat(xd.astype(np.float64), 32) * xq.astype(np.float64))
+    for flag in (1, 0):
+        fresh_engine.set_option("mq_q8", flag)
+        y = torch.full((rows,), float("nan"), device="cuda")
+        fresh_engine.mv_q8(ty, None, dev(xq), dev(xd), dev(xs), y, rows, cols, 0, 1, w=dev(q))
+        sync()
+        got = y.cpu().numpy()
+        assert np.all(np.abs(got - want) <= 1e-5 * mag + 1e-30), (flag, float(np.max(np.abs(got - want) / mag)))
