@@ -159,8 +159,8 @@ int le_matvec_q8(le_ctx *ctx, int ty, const void *const *ptrs, const void *w, co
  * below). On the matrix cores each token is scaled by its own power of two and rounded to fp16
  * (relative error 2^-11 per value at any magnitude up to 2^127); Q8_0 weights enter as
  * fp16(q * 64 d) (so |d| < 8), the other types as exact integer codes (Q6_K: rounded to fp16
- * where (q - 32) * sc has more than 11 significant bits). The 3..16-token Q4_K kernel rounds
- * unscaled activations to fp16 (|x| < 65504, 32-value sums < 65504). */
+ * where (q - 32) * sc has more than 11 significant bits). The 3..16-token Q4_K kernel scales each
+ * token's 256-value super-block by its own power of two instead (the same 2^-11 at any magnitude). */
 size_t le_gemm_workspace_size(int ty, int m, int cols);
 /* Workspace with room for the K slices' partial results as well (no counterpart in the reference,
  * whose GEMM never splits K): shapes with few row and token tiles are split along K to fill the

@@ -410,9 +410,11 @@ __device__ __forceinline__ void gm_q4k_body(const GmArgs &a, const u8 *ws) {
  * K slice is the sub-block's 32 values, and B holds the exact fp16 codes sc_j * q (gm_q4k_frag),
  * so the sub-block scales need no per-token work. D2 = sum_j m_j S_j(t) is one more MFMA of the
  * sum records (high halves in K 0-7, low halves in K 8-15) against the mins. Each wave builds
- * the fp16 activations (rounded as the GEMM pre-pass rounds them) and sub-block sums of its
- * super-blocks of all T tokens in LDS once per block. MFMA rows past T repeat token rows
- * (finite, never stored). */
+ * the fp16 activations and sub-block sums of its super-blocks of all T tokens in LDS once per
+ * block, each (token, super-block) scaled by the power of two 2^s that puts its largest |x| in
+ * [512, 1024) (so every value keeps 11 significant bits down to 2^-14 of that maximum and a
+ * 32-value sum stays below 32768 at any input magnitude); 2^-s multiplies the super-block's
+ * d D1 - dmin D2. MFMA rows past T repeat token rows (finite, never stored). */
 struct MhArgs {
     const u8 *w;
     const float *x;
@@ -432,10 +434,12 @@ __device__ __forceinline__ void mh_q4k_body(const MhArgs &a) {
     const int n = lane & 15, kq = lane >> 4;
     const int nsbw = nsb / NW;
     /* wave-private LDS: the image [local sb][sub-block j][token][4 x 16 B], the sum records
-     * [local sb][token][2 x 16 B], then the weight staging */
-    const int wsz = nsbw * 8 * T * 4 + nsbw * T * 2;
+     * [local sb][token][2 x 16 B], the inverse scales [local sb][MFMA row 0..15] (float), then
+     * the weight staging */
+    const int wsz = nsbw * 8 * T * 4 + nsbw * T * 2 + nsbw * 4;
     uint4 *img = smem + wave * (wsz + NI * 64);
     uint4 *srec = img + nsbw * 8 * T * 4;
+    float *isc = (float *)(srec + nsbw * T * 2);
     uint4 *wb = img + wsz;
     float *red = (float *)(smem + NW * (wsz + NI * 64)); /* [NW][16 tokens][16 rows] */
     const int ntile = (a.rows + 15) >> 4;
@@ -479,7 +483,28 @@ __device__ __forceinline__ void mh_q4k_body(const MhArgs &a) {
             for (int u = 0; u < 4; u++) {
                 if (c0 + 64 * u >= nch) break; /* wave-uniform: nch is a multiple of 64 */
                 const int c = c0 + 64 * u + lane, l = c / (T * 32), t = (c / 32) % T, col = c & 31;
-                const float4 p = v[u][0], q = v[u][1];
+                /* the 32 lanes of each half-wave hold one (token, super-block) */
+                /* the largest magnitude as an integer maximum of the bit patterns without sign
+                 * (the float order for every non-NaN value); over the 32 lanes by DPP within
+                 * each row of 16 and one swizzle (xor 16) across */
+                const float4 v0 = v[u][0], v1 = v[u][1];
+                u32 mx = max(max(max(__float_as_uint(v0.x) & 0x7FFFFFFFu, __float_as_uint(v0.y) & 0x7FFFFFFFu),
+                             max(__float_as_uint(v0.z) & 0x7FFFFFFFu, __float_as_uint(v0.w) & 0x7FFFFFFFu)),
+                         max(max(__float_as_uint(v1.x) & 0x7FFFFFFFu, __float_as_uint(v1.y) & 0x7FFFFFFFu),
+                             max(__float_as_uint(v1.z) & 0x7FFFFFFFu, __float_as_uint(v1.w) & 0x7FFFFFFFu)));
+                mx = max(mx, (u32)__builtin_amdgcn_update_dpp(0, (int)mx, 0xB1, 0xF, 0xF, true));  /* quad_perm [1,0,3,2] */
+                mx = max(mx, (u32)__builtin_amdgcn_update_dpp(0, (int)mx, 0x4E, 0xF, 0xF, true));  /* quad_perm [2,3,0,1] */
+                mx = max(mx, (u32)__builtin_amdgcn_update_dpp(0, (int)mx, 0x141, 0xF, 0xF, true)); /* row_half_mirror */
+                mx = max(mx, (u32)__builtin_amdgcn_update_dpp(0, (int)mx, 0x140, 0xF, 0xF, true)); /* row_mirror */
+                mx = max(mx, (u32)__builtin_amdgcn_ds_swizzle((int)mx, 0x401F));
+                /* biased exponent b of the maximum: x 2^(136 - b) puts it in [512, 1024); the
+                 * factor is kept within 2^-118 .. 2^126 (zero or subnormal maxima, inf / NaN) */
+                const int be = (int)(mx >> 23);
+                const int sx = min(max(136 - be, -118), 126);
+                const float sc = __uint_as_float((u32)(127 + sx) << 23), inv = __uint_as_float((u32)(127 - sx) << 23);
+                if (col < 16 / T) isc[l * 16 + t + T * col] = inv; /* MFMA rows t, t + T, ... */
+                const float4 p = make_float4(v[u][0].x * sc, v[u][0].y * sc, v[u][0].z * sc, v[u][0].w * sc);
+                const float4 q = make_float4(v[u][1].x * sc, v[u][1].y * sc, v[u][1].z * sc, v[u][1].w * sc);
                 const le_h2 h0 = {(_Float16)p.x, (_Float16)p.z}, h1 = {(_Float16)p.y, (_Float16)p.w};
                 const le_h2 h2 = {(_Float16)q.x, (_Float16)q.z}, h3 = {(_Float16)q.y, (_Float16)q.w};
                 img[((l * 8 + (col >> 2)) * T + t) * 4 + (col & 3)] = make_uint4(as_u32(h0), as_u32(h1), as_u32(h2), as_u32(h3));
@@ -487,8 +512,8 @@ __device__ __forceinline__ void mh_q4k_body(const MhArgs &a) {
                  * scale term sees (the error then scales with sum |w x|) */
                 float sm = (((float)h0.x + (float)h1.x) + ((float)h0.y + (float)h1.y)) +
                            (((float)h2.x + (float)h3.x) + ((float)h2.y + (float)h3.y));
-                sm += __shfl_xor(sm, 1);
-                sm += __shfl_xor(sm, 2);
+                sm += dpp_f<0xB1>(sm);
+                sm += dpp_f<0x4E>(sm);
                 if ((col & 3) == 0) {
                     const _Float16 hi = (_Float16)sm, lo = (_Float16)(sm - (float)hi);
                     _Float16 *rec = (_Float16 *)(srec + (l * T + t) * 2);
@@ -545,8 +570,10 @@ __device__ __forceinline__ void mh_q4k_body(const MhArgs &a) {
                     const le_v8h a2 = __builtin_bit_cast(le_v8h, srec[(l * T + ta) * 2 + (kq & 1)]);
                     const v4f d2 = __builtin_amdgcn_mfma_f32_16x16x32_f16(a2, b2, (v4f){0.f, 0.f, 0.f, 0.f}, 0, 0, 0);
                     const float dd = h2f(hd.x & 0xFFFFu), dm = h2f(hd.x >> 16);
+                    const float4 iv = *(const float4 *)(isc + l * 16 + 4 * kq);
+                    const float ivs[4] = {iv.x, iv.y, iv.z, iv.w};
 #pragma unroll
-                    for (int e = 0; e < 4; e++) y[e] = __builtin_fmaf(dd, d1[e], __builtin_fmaf(-dm, d2[e], y[e]));
+                    for (int e = 0; e < 4; e++) y[e] = __builtin_fmaf(ivs[e], __builtin_fmaf(dd, d1[e], -dm * d2[e]), y[e]);
                 }
             }
         }

@@ -91,26 +91,33 @@ def test_gemm_random_blocks(engine, name, m):
 
 
 @pytest.mark.parametrize("name", NAMES)
-def test_gemm_activation_magnitudes(engine, name):
+@pytest.mark.parametrize("m", [5, 12, 40])
+def test_gemm_activation_magnitudes(engine, name, m):
     """Tokens of very different magnitude in one call (1e-6 .. 1e6, a zero token, one token with a
-    single non-zero value): each token is scaled by its own power of two before fp16, so none
-    overflows and none loses relative precision."""
+    single non-zero value): each token (3..16-token Q4_K kernel: each token's super-block) is
+    scaled by its own power of two before fp16, so none overflows and none loses relative
+    precision."""
+    if m < 17 and name != "Q4_K":
+        pytest.skip("below 9 tokens the other types run on the vector kernels (per-block int8 images, "
+                    "no fp16 range); their offset form leaves 2^-15-level residues where sum|wx| is 0")
     ty = le.TYPES[name]
-    rows, cols, m = 256, 1024, 40
+    rows, cols = 256, 1024
+    zt, st = (3, 7) if m > 7 else (1, m - 1)
     q, _ = weights(ty, rows, cols, seed=5 + ty)
     xs = np.stack([acts(cols, 9500 + t) for t in range(m)])
     scales = np.float32(10.0) ** np.linspace(-6, 6, m).astype(np.float32)
     xs = (xs * scales[:, None]).astype(np.float32)
-    xs[3] = 0.0
-    xs[7] = 0.0
-    xs[7, 100] = 3.0e4
+    xs[zt] = 0.0
+    xs[st] = 0.0
+    xs[st, 100] = 3.0e4
+    print("gemm magnitudes", name, m, flush=True)
     got = run_gemm(engine, ty, q, xs, rows, cols)
     want = oracle.matmat(ty, q, rows, cols, xs)
     mag = absmag(ty, q, rows, cols, xs)
-    assert np.all(got[3] == 0.0)
+    assert np.all(got[zt] == 0.0)
     # per token: the bar relative to that token's own outputs
     for t in range(m):
-        if t == 3:
+        if t == zt:
             continue
         check_close(got[t:t + 1], want[t:t + 1], mag[t:t + 1])
 
