@@ -96,7 +96,8 @@ const char *le_last_error(const le_ctx *ctx);
  *     "gm_min_m" smallest Q4_K M on a GEMM, "gm_tile" (0 auto, 11, 12, 21, 22), "gm_ksplit" K
  *     slices (0 auto, 1, 2, 4, 8), "gm_pc" producer/consumer waves (0/1) of the le_gm kernels,
  *     "gm_split" 1: Q4_K activations as two fp16 halves (about 2^-22 per value) on the le_gm
- *     kernels, which then also take 3..16 tokens
+ *     kernels, which then also take 3..16 tokens (the le_gm kernels, selected by "gq" 0 or
+ *     "gm_split" 1, take activations unscaled: |x| and 32-value sums below 65504)
  *   MoE: "moe_mfma" staged kernels (0/1), "moe_fused" single launch (0/1), "moe_fused_min_tok",
  *     "moe_fast" decode-shaped vector kernels (0/1) */
 int le_set_option(le_ctx *ctx, const char *name, int value);
