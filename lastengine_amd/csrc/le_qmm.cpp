@@ -263,7 +263,7 @@ int mq_launch(le_ctx *c, int ty, const void *const *ptrs, const void *w, const f
     if (c->ms && nsb % (NWs * P) == 0) {
         const int cps = ty == LE_TYPE_Q6_K ? 14 : ty == LE_TYPE_IQ2_XXS ? 5 : ty == LE_TYPE_IQ3_XXS ? 7 : ty == LE_TYPE_Q8_0 ? 17 : 9;
         const int cpr = cps * P + 1, ni = (16 * cpr + 63) / 64;
-        snprintf(name, sizeof name, "le_ms_%d_p%d_w%d", ty, P, NWs);
+        snprintf(name, sizeof name, "le_ms_%d_p%d_w%d%s", ty, P, NWs, xq8 ? "_q8" : "");
         lds = (size_t)NWs * ((size_t)(nsb / NWs) * 608 + (size_t)ni * 1024) + (size_t)NWs * 128;
         if (lds <= c->lds_limit)
             return c->launch(name, dim3((unsigned)gx, (unsigned)slots), NWs * 64, lds, st, args);

@@ -940,7 +940,7 @@ __device__ __forceinline__ float ms_sb_q6k(const uint4 *sbp, const le_v4i (&A)[4
  * LDS buffer where one pad chunk per row keeps the 16 rows of a read in distinct banks. MFMA
  * operands then come from LDS. Barriers wait on LDS traffic only, so weight loads in flight are
  * not drained at a barrier. */
-template <int P, int NW>
+template <int P, int NW, bool Q8>
 __device__ __forceinline__ void ms_q4k_body(const MvArgs &a) {
     extern __shared__ uint4 smem[];
     constexpr int CPR = 9 * P + 1, NCH = 16 * CPR, NI = (NCH + 63) / 64;
@@ -989,7 +989,7 @@ __device__ __forceinline__ void ms_q4k_body(const MvArgs &a) {
         const int ls = el >> 4;
         return ((ls / P) * sstep + sfirst + ls % P) * 16 + (el & 15);
     };
-    if (a.xq8) { /* int8 mode: the image holds the caller's xq, scale xd per 32 values (exact) */
+    if constexpr (Q8) { /* int8 mode (the _q8 kernels): the image holds the caller's xq, scale xd per 32 values (exact) */
         issue(min((int)blockIdx.x, ntile - 1), active ? sfirst : 0); /* unpredicated: exact wait counts */
         const int8_t *xq8 = a.xq8 + a.x_slot * slot;
         const float *xd8 = a.xd8 + (a.x_slot >> 5) * slot;
@@ -1242,7 +1242,7 @@ __device__ __forceinline__ void ms_q4k_t_body(const MvArgs &a) {
     }
 }
 
-template <int P, int NW>
+template <int P, int NW, bool Q8>
 __device__ __forceinline__ void ms_q6k_body(const MvArgs &a) {
     extern __shared__ uint4 smem[];
     constexpr int CPS = 14, CPR = CPS * P + 1, NCH = 16 * CPR, NI = (NCH + 63) / 64;
@@ -1286,7 +1286,7 @@ __device__ __forceinline__ void ms_q6k_body(const MvArgs &a) {
         const int ls = el >> 4;
         return ((ls / P) * sstep + sfirst + ls % P) * 16 + (el & 15);
     };
-    if (a.xq8) { /* int8 mode: the image holds the caller's xq, scale xd per 32 values (exact) */
+    if constexpr (Q8) { /* int8 mode (the _q8 kernels): the image holds the caller's xq, scale xd per 32 values (exact) */
         issue(min((int)blockIdx.x, ntile - 1), active ? sfirst : 0);
         const int8_t *xq8 = a.xq8 + a.x_slot * slot;
         const float *xd8 = a.xd8 + (a.x_slot >> 5) * slot;
@@ -1346,7 +1346,8 @@ __device__ __forceinline__ void ms_q6k_body(const MvArgs &a) {
 }
 
 #define LE_MS14(P, NW)                                                                                     \
-    extern "C" __global__ void __launch_bounds__(NW * 64) le_ms_14_p##P##_w##NW(MvArgs a) { ms_q6k_body<P, NW>(a); }
+    extern "C" __global__ void __launch_bounds__(NW * 64) le_ms_14_p##P##_w##NW(MvArgs a) { ms_q6k_body<P, NW, false>(a); } \
+    extern "C" __global__ void __launch_bounds__(NW * 64) le_ms_14_p##P##_w##NW##_q8(MvArgs a) { ms_q6k_body<P, NW, true>(a); }
 
 /* IQ2_XXS / IQ3_XXS on the staged MFMA design, under the Q4_K slice map (slice s of MFMA b is
  * sub-block j = 4*(b>>1) + 2*(s>>1) + (b&1), values 16*(s&1)..+15). A super-block is staged from
@@ -1446,7 +1447,7 @@ __device__ __forceinline__ float ms_sb_iq(const u8 *sb, const le_v4i (&A)[4], co
     return F::d(sb) * F::SCALE * t;
 }
 
-template <int TY, int P, int NW>
+template <int TY, int P, int NW, bool Q8>
 __device__ __forceinline__ void ms_iq_body(const MvArgs &a) {
     using F = MsIq<TY>;
     extern __shared__ uint4 smem[];
@@ -1490,7 +1491,7 @@ __device__ __forceinline__ void ms_iq_body(const MvArgs &a) {
         const int ls = el >> 4;
         return ((ls / P) * sstep + sfirst + ls % P) * 16 + (el & 15);
     };
-    if (a.xq8) { /* int8 mode: the image holds the caller's xq, scale xd per 32 values (exact) */
+    if constexpr (Q8) { /* int8 mode (the _q8 kernels): the image holds the caller's xq, scale xd per 32 values (exact) */
         issue(min((int)blockIdx.x, ntile - 1), active ? sfirst : 0);
         const int8_t *xq8 = a.xq8 + a.x_slot * slot;
         const float *xd8 = a.xd8 + (a.x_slot >> 5) * slot;
@@ -1549,11 +1550,13 @@ __device__ __forceinline__ void ms_iq_body(const MvArgs &a) {
 }
 
 #define LE_MSIQ_(TY, P, NW)                                                                                \
-    extern "C" __global__ void __launch_bounds__(NW * 64) le_ms_##TY##_p##P##_w##NW(MvArgs a) { ms_iq_body<TY, P, NW>(a); }
+    extern "C" __global__ void __launch_bounds__(NW * 64) le_ms_##TY##_p##P##_w##NW(MvArgs a) { ms_iq_body<TY, P, NW, false>(a); } \
+    extern "C" __global__ void __launch_bounds__(NW * 64) le_ms_##TY##_p##P##_w##NW##_q8(MvArgs a) { ms_iq_body<TY, P, NW, true>(a); }
 #define LE_MSIQ(TY, P, NW) LE_MSIQ_(TY, P, NW) /* expands TY before pasting */
 
 #define LE_MS12(P, NW)                                                                                     \
-    extern "C" __global__ void __launch_bounds__(NW * 64) le_ms_12_p##P##_w##NW(MvArgs a) { ms_q4k_body<P, NW>(a); }
+    extern "C" __global__ void __launch_bounds__(NW * 64) le_ms_12_p##P##_w##NW(MvArgs a) { ms_q4k_body<P, NW, false>(a); } \
+    extern "C" __global__ void __launch_bounds__(NW * 64) le_ms_12_p##P##_w##NW##_q8(MvArgs a) { ms_q4k_body<P, NW, true>(a); }
 
 #define LE_MS12T(P, NW, T)                                                                                 \
     extern "C" __global__ void __launch_bounds__(NW * 64) le_ms_12_p##P##_w##NW##_t##T(MvArgs a) { ms_q4k_t_body<P, NW, T>(a); }
