@@ -91,8 +91,10 @@ struct le_ctx {
     int gm_mh = 1;           /* le_gemm, Q4_K, 3..8 tokens: the staged f16 MFMA kernel */
     int gm_mh_max = 16;      /* ... up to this many tokens (8 or 16; 16 only where K fits its LDS) */
     int gm_mh_shape = 0;     /* ... its (P, NW) as 10 * P + NW: 0 auto, 14, 18, 24, 22 */
-    int ms80 = 1, ms_p80 = 1; /* Q8_0 decode matvec on the staged MFMA kernels (32000x4096: 36.8 -> 32.9 us against the
-                                 vector kernel, with one super-block per item; 35.7 with two) */
+    /* Q8_0 and Q4_0 batch-1 matvec on the staged MFMA kernels, with ms_p80 / ms_p40 super-blocks per
+     * item (Q8_0 32000x4096: 29.7 us against the vector kernel's 36.5; Q4_0 14336x4096: 10.7 against
+     * 12.6, 4096x4096: 5.4 against 11.1) */
+    int ms80 = 1, ms_p80 = 1, ms40 = 1, ms_p40 = 2;
     int mq_q8 = 1;           /* int8 mode on the staged MFMA kernels: Q4_K 14336x4096 13.1 -> 9.9 us, Q6_K 4096x14336
                                 27.7 -> 15.3, IQ3_XXS 16.6 -> 15.7 against the vector kernels (IQ2_XXS stays
                                 there: 10.5 against 11.3) */
@@ -253,7 +255,7 @@ int mq_launch(le_ctx *c, int ty, const void *const *ptrs, const void *w, const f
     char name[64];
     size_t lds = (size_t)nsb * 608 + (size_t)NW * 64;
     /* staged variant: P super-blocks per row and item, NWs waves splitting K evenly */
-    int P = ty == LE_TYPE_Q6_K ? c->ms_p6 : ty == LE_TYPE_Q4_K ? c->ms_p : ty == LE_TYPE_Q8_0 ? c->ms_p80 : c->ms_piq, NWs = NW;
+    int P = ty == LE_TYPE_Q6_K ? c->ms_p6 : ty == LE_TYPE_Q4_K ? c->ms_p : ty == LE_TYPE_Q8_0 ? c->ms_p80 : ty == LE_TYPE_Q4_0 ? c->ms_p40 : c->ms_piq, NWs = NW;
     while (P > 1 && nsb % P) P >>= 1;
     /* Q6_K keeps the waves and gives up super-blocks per item when both do not divide K (4096 x
      * 14336, 56 super-blocks: P=1 on 8 waves 14.1 us against P=2 on 4 waves 16.0); the other
@@ -344,7 +346,7 @@ int mv_launch(le_ctx *c, int ty, const void *const *ptrs, const void *w, const f
     }
     const int nsb = cols / 256, G = pick_g(nsb), S = nsb / G;
     const bool iq = ty == LE_TYPE_IQ2_XXS || ty == LE_TYPE_IQ3_XXS;
-    const bool q80 = ty == LE_TYPE_Q8_0 && c->ms80;
+    const bool q80 = (ty == LE_TYPE_Q8_0 && c->ms80) || (ty == LE_TYPE_Q4_0 && c->ms40);
     if ((ty == LE_TYPE_Q4_K || (ty == LE_TYPE_Q6_K && c->mq6) || (iq && c->mqiq) || q80) && ntok == 1 && c->mq &&
         (!q8 || (c->mq_q8 && ty != LE_TYPE_IQ2_XXS)) && (size_t)nsb * 608 + 1024 <= c->lds_limit) {
         const int rc = mq_launch(c, ty, ptrs, w, x, x_slot, y, y_slot, rows, cols, slots, st, swiglu, xq8, xd8);
@@ -567,6 +569,11 @@ int le_set_option(le_ctx *c, const char *name, int value) {
         c->moe_fused = value ? 1 : 0;
     } else if (n == "moe_mfma") {
         c->moe_mfma = value ? 1 : 0;
+    } else if (n == "ms_p40") {
+        if (value != 1 && value != 2 && value != 4) return c->fail(LE_ERR_ARG, "ms_p40 must be 1, 2 or 4");
+        c->ms_p40 = value;
+    } else if (n == "ms40") {
+        c->ms40 = value ? 1 : 0;
     } else if (n == "ms_p80") {
         if (value != 1 && value != 2 && value != 4) return c->fail(LE_ERR_ARG, "ms_p80 must be 1, 2 or 4");
         c->ms_p80 = value;

@@ -1405,14 +1405,14 @@ struct MsIq<LE_TYPE_IQ3_XXS> {
 
 /* 16 bytes at a 2-byte-aligned LDS address: five aligned words, funnel-shifted */
 __device__ __forceinline__ uint4 lds16_a2(const u8 *p) {
-    const u32 *w = (const u32 *)((size_t)p & ~(size_t)3);
+    const u32 *w = (const u32 *)(p - ((size_t)p & 3)); /* pointer arithmetic keeps the LDS address space */
     const u32 sh = (u32)((size_t)p & 3) * 8u;
     const u32 w0 = w[0], w1 = w[1], w2 = w[2], w3 = w[3], w4 = w[4];
     return make_uint4(__builtin_amdgcn_alignbit(w1, w0, sh), __builtin_amdgcn_alignbit(w2, w1, sh),
                       __builtin_amdgcn_alignbit(w3, w2, sh), __builtin_amdgcn_alignbit(w4, w3, sh));
 }
 __device__ __forceinline__ float lds_h2f_a2(const u8 *p) {
-    const u32 w = *(const u32 *)((size_t)p & ~(size_t)3);
+    const u32 w = *(const u32 *)(p - ((size_t)p & 3));
     return h2f((w >> (((size_t)p & 2) * 8)) & 0xFFFFu);
 }
 /* Q8_0 on the same staged design: a "super-block" is 8 consecutive 32-value blocks (272 bytes,
@@ -1429,6 +1429,25 @@ struct MsIq<LE_TYPE_Q8_0> {
         return (le_v4i){(int)q.x, (int)q.y, (int)q.z, (int)q.w};
     }
     static __device__ __forceinline__ float sscale(const u8 *sb, int j) { return lds_h2f_a2(sb + 34 * j); }
+    static __device__ __forceinline__ float d(const u8 *) { return 1.f; }
+};
+/* Q4_0 the same way: eight 18-byte blocks (144 bytes, 9 chunks), codes the nibbles minus 8
+ * (src/quant.rs:64-67: value i < 16 the low nibble of byte i, 16 + i the high one) */
+template <>
+struct MsIq<LE_TYPE_Q4_0> {
+    static constexpr int CPS = 9, SBB = 144;
+    static constexpr float SCALE = 1.f;
+    static __device__ __forceinline__ int goff(int c) { return 16 * c; }
+    static __device__ __forceinline__ le_v4i bfrag(const u8 *sb, int j, int h, const u32 *) {
+        const uint4 q = lds16_a2(sb + 18 * j + 2);
+        const u32 w[4] = {q.x, q.y, q.z, q.w};
+        int o[4];
+#pragma unroll
+        for (int i = 0; i < 4; i++) /* nibble - 8 bytewise: (n + 0x78) ^ 0x80, no carries */
+            o[i] = (int)((((h ? w[i] >> 4 : w[i]) & 0x0F0F0F0Fu) + 0x78787878u) ^ 0x80808080u);
+        return (le_v4i){o[0], o[1], o[2], o[3]};
+    }
+    static __device__ __forceinline__ float sscale(const u8 *sb, int j) { return lds_h2f_a2(sb + 18 * j); }
     static __device__ __forceinline__ float d(const u8 *) { return 1.f; }
 };
 
@@ -1577,7 +1596,7 @@ LE_MS12T(2, 4, 2) LE_MS12T(2, 4, 4) LE_MS12T(2, 4, 8) LE_MS12T(2, 2, 2) LE_MS12T
 #if LE_PART_MV == 14
 LE_MS14(1, 1) LE_MS14(1, 2) LE_MS14(1, 4) LE_MS14(1, 8) LE_MS14(2, 1) LE_MS14(2, 2) LE_MS14(2, 4) LE_MS14(2, 8) LE_MS14(4, 1) LE_MS14(4, 2)
 #endif
-#if LE_PART_MV == 16 || LE_PART_MV == 18 || LE_PART_MV == 8
+#if LE_PART_MV == 16 || LE_PART_MV == 18 || LE_PART_MV == 8 || LE_PART_MV == 2
 LE_MSIQ(LE_PART_MV, 1, 1) LE_MSIQ(LE_PART_MV, 1, 2) LE_MSIQ(LE_PART_MV, 1, 4) LE_MSIQ(LE_PART_MV, 2, 1) LE_MSIQ(LE_PART_MV, 2, 2)
 LE_MSIQ(LE_PART_MV, 2, 4) LE_MSIQ(LE_PART_MV, 4, 1) LE_MSIQ(LE_PART_MV, 4, 2) LE_MSIQ(LE_PART_MV, 4, 4)
 LE_MSIQ(LE_PART_MV, 1, 8) LE_MSIQ(LE_PART_MV, 2, 8)

@@ -244,3 +244,33 @@ def test_matvec_q8_vector_path(fresh_engine, name):
         sync()
         got = y.cpu().numpy()
         assert np.all(np.abs(got - want) <= 1e-5 * mag + 1e-30), (flag, float(np.max(np.abs(got - want) / mag)))
+
+
+@pytest.mark.parametrize("name,opt", [("Q8_0", "ms80"), ("Q4_0", "ms40")])
+@pytest.mark.parametrize("rows,cols", [(333, 4096), (40, 14336), (17, 256), (64, 768)])
+def test_matvec_staged_q8_0_q4_0(fresh_engine, name, opt, rows, cols):
+    """Q8_0 and Q4_0 batch-1 matvec on the staged matrix-core kernels (option 1) and on the vector
+    kernels (option 0): both meet the parity bar against the oracle, with and without the int8
+    activation mode."""
+    import torch
+    ty = le.MV_TYPES[name]
+    q = random_blocks(ty, rows, cols, seed=ty * 13 + rows + cols)
+    x = acts(cols, 3 + rows)
+    want = oracle.matvec(ty, q, rows, cols, x)
+    mag = _absmag(ty, q, rows, cols, x)[0]
+    xq, xd, xs = oracle.quant_x(x)
+    want8 = oracle.matvec_q8(ty, q, rows, cols, xq, xd, xs)
+    wd = oracle.dequant_rows(ty, q, rows, cols).astype(np.float64)
+    mag8 = np.abs(wd) @ np.abs(np.repeat(xd.astype(np.float64), 32) * xq.astype(np.float64))
+    for flag in (1, 0):
+        fresh_engine.set_option(opt, flag)
+        print("staged", name, flag, rows, cols, flush=True)
+        y = torch.full((rows,), float("nan"), device="cuda")
+        fresh_engine.mv(ty, dev(q), dev(x), y, rows, cols)
+        sync()
+        check_close(y.cpu().numpy(), want, mag)
+        y = torch.full((rows,), float("nan"), device="cuda")
+        fresh_engine.mv_q8(ty, None, dev(xq), dev(xd), dev(xs), y, rows, cols, 0, 1, w=dev(q))
+        sync()
+        got = y.cpu().numpy()
+        assert np.all(np.abs(got - want8) <= 1e-5 * mag8 + 1e-30), (flag, float(np.max(np.abs(got - want8) / mag8)))
