@@ -847,6 +847,38 @@ __device__ __forceinline__ float ms_sb_q4k(const uint4 *sbp, const le_v4i (&A)[4
     return h2f(hd.x & 0xFFFFu) * t - h2f(hd.x >> 16) * mt;
 }
 
+/* Q5_K (src/quant.rs:83-95): the Q4_K header chunk, qh in chunks 1-2, the nibbles in chunks 3-10 in
+ * Q4_K's order; the code of sub-block j at position l is its nibble + 16 * bit j of qh[l]. Lane
+ * sq reads qh bytes 16 (sq & 1) .. of its half, MFMA b takes bit mq_j(b, sq). */
+__device__ __forceinline__ float ms_sb_q5k(const uint4 *sbp, const le_v4i (&A)[4], const float *dxp_sb, const float *fsv_sb,
+                                           const MsLane &L) {
+    const int sq = L.sq, j0 = 2 * (sq >> 1);
+    const uint4 hd = sbp[0], qh = sbp[1 + (sq & 1)], l0 = sbp[3 + sq], l1 = sbp[7 + sq];
+    auto hb = [&](u32 h, int j) { return ((h >> j) & 0x01010101u) << 4; };
+    const le_v4i B0 = {(int)((l0.x & 0x0F0F0F0Fu) | hb(qh.x, j0)), (int)((l0.y & 0x0F0F0F0Fu) | hb(qh.y, j0)),
+                       (int)((l0.z & 0x0F0F0F0Fu) | hb(qh.z, j0)), (int)((l0.w & 0x0F0F0F0Fu) | hb(qh.w, j0))};
+    const le_v4i B1 = {(int)(((l0.x >> 4) & 0x0F0F0F0Fu) | hb(qh.x, j0 + 1)), (int)(((l0.y >> 4) & 0x0F0F0F0Fu) | hb(qh.y, j0 + 1)),
+                       (int)(((l0.z >> 4) & 0x0F0F0F0Fu) | hb(qh.z, j0 + 1)), (int)(((l0.w >> 4) & 0x0F0F0F0Fu) | hb(qh.w, j0 + 1))};
+    const le_v4i B2 = {(int)((l1.x & 0x0F0F0F0Fu) | hb(qh.x, j0 + 4)), (int)((l1.y & 0x0F0F0F0Fu) | hb(qh.y, j0 + 4)),
+                       (int)((l1.z & 0x0F0F0F0Fu) | hb(qh.z, j0 + 4)), (int)((l1.w & 0x0F0F0F0Fu) | hb(qh.w, j0 + 4))};
+    const le_v4i B3 = {(int)(((l1.x >> 4) & 0x0F0F0F0Fu) | hb(qh.x, j0 + 5)), (int)(((l1.y >> 4) & 0x0F0F0F0Fu) | hb(qh.y, j0 + 5)),
+                       (int)(((l1.z >> 4) & 0x0F0F0F0Fu) | hb(qh.z, j0 + 5)), (int)(((l1.w >> 4) & 0x0F0F0F0Fu) | hb(qh.w, j0 + 5))};
+    le_v4i D = __builtin_amdgcn_mfma_i32_16x16x64_i8(A[0], B0, (le_v4i){0, 0, 0, 0}, 0, 0, 0);
+    D = __builtin_amdgcn_mfma_i32_16x16x64_i8(A[1], B1, D, 0, 0, 0);
+    D = __builtin_amdgcn_mfma_i32_16x16x64_i8(A[2], B2, D, 0, 0, 0);
+    D = __builtin_amdgcn_mfma_i32_16x16x64_i8(A[3], B3, D, 0, 0, 0);
+    const u32 sy = hd.y, sz = hd.z, sw = hd.w;
+    const u32 tsc = (sq & 1) ? ((sw & 0x0F0F0F0Fu) | ((sy >> 2) & 0x30303030u)) : (sy & 0x3F3F3F3Fu);
+    const u32 tm = (sq & 1) ? (((sw >> 4) & 0x0F0F0F0Fu) | ((sz >> 2) & 0x30303030u)) : (sz & 0x3F3F3F3Fu);
+    const float4 dq = *(const float4 *)(dxp_sb + L.pe * 8 + L.jb);
+    const float t = (float)(tsc & 255u) * dq.x * (float)D[0] + (float)((tsc >> 8) & 255u) * dq.y * (float)D[1] +
+                    (float)((tsc >> 16) & 255u) * dq.z * (float)D[2] + (float)(tsc >> 24) * dq.w * (float)D[3];
+    const float2 f2 = *(const float2 *)(fsv_sb + L.jb + 2 * L.pe);
+    const u32 mm = tm >> (16 * L.pe);
+    const float mt = (float)(mm & 255u) * f2.x + (float)((mm >> 8) & 255u) * f2.y;
+    return h2f(hd.x & 0xFFFFu) * t - h2f(hd.x >> 16) * mt;
+}
+
 /* Q4_K for NT tiles that share the activation (rows sbp + ti * tstride chunks): the MFMAs of the
  * tiles are interleaved, so NT accumulation chains are in flight instead of one. */
 template <int NT>
@@ -940,14 +972,15 @@ __device__ __forceinline__ float ms_sb_q6k(const uint4 *sbp, const le_v4i (&A)[4
  * LDS buffer where one pad chunk per row keeps the 16 rows of a read in distinct banks. MFMA
  * operands then come from LDS. Barriers wait on LDS traffic only, so weight loads in flight are
  * not drained at a barrier. */
-template <int P, int NW, bool Q8>
+template <int P, int NW, bool Q8, int TY = LE_TYPE_Q4_K>
 __device__ __forceinline__ void ms_q4k_body(const MvArgs &a) {
     extern __shared__ uint4 smem[];
-    constexpr int CPR = 9 * P + 1, NCH = 16 * CPR, NI = (NCH + 63) / 64;
+    constexpr int CPS = TY == LE_TYPE_Q5_K ? 11 : 9; /* 16-byte chunks per super-block (Q4_K, Q5_K) */
+    constexpr int CPR = CPS * P + 1, NCH = 16 * CPR, NI = (NCH + 63) / 64;
     const int K = a.cols, nsb = K >> 8;
     const int slot = blockIdx.y;
     const u8 *W = a.ptrs ? a.ptrs[slot] : a.w0 + (size_t)slot * a.w_slot_bytes;
-    const size_t rb = (size_t)nsb * 144;
+    const size_t rb = (size_t)nsb * (16 * CPS);
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int n = lane & 15, sq = lane >> 4;
     /* wave-private LDS: the activation image of this wave's super-blocks (local index ls, global
@@ -968,7 +1001,7 @@ __device__ __forceinline__ void ms_q4k_body(const MvArgs &a) {
         const int c = min(64 * i + lane, NCH - 1);
         const int col = c % CPR;
         ri[i] = c / CPR;
-        cb[i] = (col == 9 * P ? 0 : col) * 16;
+        cb[i] = (col == CPS * P ? 0 : col) * 16;
     }
     /* register staging: the chunks of the next item are loaded while the current one computes */
     uint4 R[NI];
@@ -976,7 +1009,7 @@ __device__ __forceinline__ void ms_q4k_body(const MvArgs &a) {
 #pragma unroll
         for (int i = 0; i < NI; i++) {
             const int row = min(tile * 16 + ri[i], a.rows - 1);
-            R[i] = ldg16(W + (size_t)row * rb + (size_t)s0 * 144 + cb[i]);
+            R[i] = ldg16(W + (size_t)row * rb + (size_t)s0 * (16 * CPS) + cb[i]);
         }
     };
     const int sfirst = wave * P, sstep = NW * P;
@@ -1027,7 +1060,10 @@ __device__ __forceinline__ void ms_q4k_body(const MvArgs &a) {
                 for (int q = 0; q < P; q++) {
                     const int sb = lb + q; /* local super-block of this wave's image */
                     ms_load_a(rec + sb * 32, L, A);
-                    y += ms_sb_q4k(wb + n * CPR + 9 * q, A, dxp + sb * 16, fsv + sb * 8, L);
+                    if constexpr (TY == LE_TYPE_Q5_K)
+                        y += ms_sb_q5k(wb + n * CPR + CPS * q, A, dxp + sb * 16, fsv + sb * 8, L);
+                    else
+                        y += ms_sb_q4k(wb + n * CPR + CPS * q, A, dxp + sb * 16, fsv + sb * 8, L);
                 }
             }
         }
@@ -1592,6 +1628,12 @@ LE_MQ12(4, 1) LE_MQ12(4, 2) LE_MQ12(4, 4) LE_MQ12(8, 1) LE_MQ12(8, 2) LE_MQ12(8,
 LE_MS12(1, 1) LE_MS12(1, 2) LE_MS12(1, 4) LE_MS12(1, 8) LE_MS12(2, 1) LE_MS12(2, 2) LE_MS12(2, 4) LE_MS12(2, 8) LE_MS12(4, 1) LE_MS12(4, 2) LE_MS12(4, 4)
 LE_MS12T(1, 4, 2) LE_MS12T(1, 4, 4) LE_MS12T(1, 4, 8) LE_MS12T(1, 8, 2) LE_MS12T(1, 8, 4) LE_MS12T(1, 8, 8)
 LE_MS12T(2, 4, 2) LE_MS12T(2, 4, 4) LE_MS12T(2, 4, 8) LE_MS12T(2, 2, 2) LE_MS12T(2, 2, 4) LE_MS12T(2, 2, 8)
+#endif
+#if LE_PART_MV == 13
+#define LE_MS13(P, NW)                                                                                     \
+    extern "C" __global__ void __launch_bounds__(NW * 64) le_ms_13_p##P##_w##NW(MvArgs a) { ms_q4k_body<P, NW, false, LE_TYPE_Q5_K>(a); } \
+    extern "C" __global__ void __launch_bounds__(NW * 64) le_ms_13_p##P##_w##NW##_q8(MvArgs a) { ms_q4k_body<P, NW, true, LE_TYPE_Q5_K>(a); }
+LE_MS13(1, 1) LE_MS13(1, 2) LE_MS13(1, 4) LE_MS13(1, 8) LE_MS13(2, 1) LE_MS13(2, 2) LE_MS13(2, 4) LE_MS13(2, 8) LE_MS13(4, 1) LE_MS13(4, 2) LE_MS13(4, 4)
 #endif
 #if LE_PART_MV == 14
 LE_MS14(1, 1) LE_MS14(1, 2) LE_MS14(1, 4) LE_MS14(1, 8) LE_MS14(2, 1) LE_MS14(2, 2) LE_MS14(2, 4) LE_MS14(2, 8) LE_MS14(4, 1) LE_MS14(4, 2)
