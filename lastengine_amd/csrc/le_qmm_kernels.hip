@@ -936,6 +936,10 @@ __device__ __forceinline__ u32 q6_code(u32 ql, u32 qh, int s) {
 
 /* Q6_K: sbp = the row's staged super-block (14 chunks: ql 0-7, qh 8-11, sc 12, d 13). A[b] is the
  * image slice under the Q6_K map (MAP 1). */
+/* Byte offset of staged chunk c of a 210-byte Q6_K super-block: chunks 0-12 at 16 c, chunk 13 at
+ * 194 (bytes 194-209, ending with d) so no load reads past the super-block, nor past the end of
+ * the last row. */
+__device__ __forceinline__ int q6_goff(int c) { return c == 13 ? 194 : 16 * c; }
 __device__ __forceinline__ float ms_sb_q6k(const uint4 *sbp, const le_v4i (&A)[4], const float *dxp_sb, const MsLane &L) {
     const int sq = L.sq;
     le_v4i D0 = {0, 0, 0, 0}, D1 = {0, 0, 0, 0};
@@ -963,7 +967,54 @@ __device__ __forceinline__ float ms_sb_q6k(const uint4 *sbp, const le_v4i (&A)[4
         const int sbb = (int)(signed char)((sw >> (16 * (i & 1) + 8)) & 255u);
         t += dqa[i] * ((float)sa * (float)D0[i] + (float)sbb * (float)D1[i]);
     }
-    return h2f(sbp[13].x & 0xFFFFu) * t;
+    return h2f(sbp[13].w >> 16) * t; /* d: bytes 208-209, the last two of chunk 13 */
+}
+
+/* Q3_K (src/quant.rs:113-126), 110 bytes: hm[32], qs[64], 6-bit scales packed in 12 bytes, d. Value
+ * e = 128 c + 32 s + l has code ((qs[32 c + l] >> 2 s) & 3) - 4 (hm bit 4 c + s of byte l clear)
+ * and scale e / 16 = 8 c + 2 s + l / 16: the Q6_K layout of halves, quarters and 16-value scales,
+ * so the Q6_K kernel's map applies. Staged as 7 chunks, the last one at byte 94 (bytes 94-109:
+ * the scales from its byte 2, d in its last two), so no load reads past the super-block. */
+__device__ __forceinline__ int q3_goff(int c) { return c == 6 ? 94 : 16 * c; }
+__device__ __forceinline__ float ms_sb_q3k(const uint4 *sbp, const le_v4i (&A)[4], const float *dxp_sb, const MsLane &L) {
+    const int sq = L.sq;
+    le_v4i D0 = {0, 0, 0, 0}, D1 = {0, 0, 0, 0};
+#pragma unroll
+    for (int b = 0; b < 4; b++) {
+        const int hn = b >> 1, is = b & 1, hs = 4 * hn + sq, qsft = 2 * sq;
+        const uint4 q = sbp[2 + 2 * hn + is], h = sbp[is];
+        const u32 w[4] = {q.x, q.y, q.z, q.w}, m[4] = {h.x, h.y, h.z, h.w};
+        int o[4];
+#pragma unroll
+        for (int k = 0; k < 4; k++) /* (code | high bit << 2) - 4 bytewise: (v + 0x7C) ^ 0x80, no carries */
+            o[k] = (int)(((((w[k] >> qsft) & 0x03030303u) | (((m[k] >> hs) & 0x01010101u) << 2)) + 0x7C7C7C7Cu) ^ 0x80808080u);
+        const le_v4i B = {o[0], o[1], o[2], o[3]};
+        if (is)
+            D1 = __builtin_amdgcn_mfma_i32_16x16x64_i8(A[b], B, D1, 0, 0, 0);
+        else
+            D0 = __builtin_amdgcn_mfma_i32_16x16x64_i8(A[b], B, D0, 0, 0, 0);
+    }
+    /* lane: sub-blocks jb + i (jb = 4 (sq & 1)), scales 2 (jb + i) + is */
+    const uint4 c6 = sbp[6];
+    const u32 s0 = __builtin_amdgcn_alignbit(c6.y, c6.x, 16), s1 = __builtin_amdgcn_alignbit(c6.z, c6.y, 16),
+              s2 = __builtin_amdgcn_alignbit(c6.w, c6.z, 16);
+    const int hi = sq & 1;
+    const float4 dq = *(const float4 *)(dxp_sb + L.pe * 8 + L.jb);
+    const float dqa[4] = {dq.x, dq.y, dq.z, dq.w};
+    float t = 0.f;
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+        int sc[2];
+#pragma unroll
+        for (int is = 0; is < 2; is++) {
+            const int k = 2 * i + is; /* scale index 8 hi + k: low 4 bits in byte k (nibble hi), high 2 in byte 8 + k % 4 */
+            const u32 lo = ((k < 4 ? s0 : s1) >> (8 * (k & 3) + 4 * hi)) & 15u;
+            const u32 hb = (s2 >> (8 * (k & 3) + 2 * (2 * hi + (i >> 1)))) & 3u;
+            sc[is] = (int)(lo | (hb << 4)) - 32;
+        }
+        t += dqa[i] * ((float)sc[0] * (float)D0[i] + (float)sc[1] * (float)D1[i]);
+    }
+    return h2f(c6.w >> 16) * t;
 }
 
 /* Staged variant: each wave streams its tile's P super-blocks per row as consecutive 16-byte
@@ -1278,14 +1329,15 @@ __device__ __forceinline__ void ms_q4k_t_body(const MvArgs &a) {
     }
 }
 
-template <int P, int NW, bool Q8>
+template <int P, int NW, bool Q8, int TY = LE_TYPE_Q6_K>
 __device__ __forceinline__ void ms_q6k_body(const MvArgs &a) {
     extern __shared__ uint4 smem[];
-    constexpr int CPS = 14, CPR = CPS * P + 1, NCH = 16 * CPR, NI = (NCH + 63) / 64;
+    constexpr bool Q3 = TY == LE_TYPE_Q3_K;
+    constexpr int CPS = Q3 ? 7 : 14, SBB = Q3 ? 110 : 210, CPR = CPS * P + 1, NCH = 16 * CPR, NI = (NCH + 63) / 64;
     const int K = a.cols, nsb = K >> 8;
     const int slot = blockIdx.y;
     const u8 *W = a.ptrs ? a.ptrs[slot] : a.w0 + (size_t)slot * a.w_slot_bytes;
-    const size_t rb = (size_t)nsb * 210;
+    const size_t rb = (size_t)nsb * SBB;
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int n = lane & 15, sq = lane >> 4;
     const int nsbw = nsb / NW;
@@ -1304,14 +1356,14 @@ __device__ __forceinline__ void ms_q6k_body(const MvArgs &a) {
         const int c = min(64 * i + lane, NCH - 1);
         const int col = c % CPR, cc = col == CPS * P ? 0 : col;
         ri[i] = c / CPR;
-        gb[i] = (cc / CPS) * 210 + (cc % CPS) * 16;
+        gb[i] = (cc / CPS) * SBB + (Q3 ? q3_goff(cc % CPS) : q6_goff(cc % CPS));
     }
     uint4 R[NI];
     auto issue = [&](int tile, int s0) {
 #pragma unroll
         for (int i = 0; i < NI; i++) {
             const int row = min(tile * 16 + ri[i], a.rows - 1);
-            R[i] = ldg16u(W + (size_t)row * rb + (size_t)s0 * 210 + gb[i]);
+            R[i] = ldg16u(W + (size_t)row * rb + (size_t)s0 * SBB + gb[i]);
         }
     };
     const int sfirst = wave * P, sstep = NW * P;
@@ -1360,7 +1412,10 @@ __device__ __forceinline__ void ms_q6k_body(const MvArgs &a) {
                 for (int q = 0; q < P; q++) {
                     const int sb = lb + q;
                     ms_load_a(rec + sb * 32, L, A);
-                    y += ms_sb_q6k(wb + n * CPR + CPS * q, A, dxp + sb * 16, L);
+                    if constexpr (Q3)
+                        y += ms_sb_q3k(wb + n * CPR + CPS * q, A, dxp + sb * 16, L);
+                    else
+                        y += ms_sb_q6k(wb + n * CPR + CPS * q, A, dxp + sb * 16, L);
                 }
             }
         }
@@ -1634,6 +1689,12 @@ LE_MS12T(2, 4, 2) LE_MS12T(2, 4, 4) LE_MS12T(2, 4, 8) LE_MS12T(2, 2, 2) LE_MS12T
     extern "C" __global__ void __launch_bounds__(NW * 64) le_ms_13_p##P##_w##NW(MvArgs a) { ms_q4k_body<P, NW, false, LE_TYPE_Q5_K>(a); } \
     extern "C" __global__ void __launch_bounds__(NW * 64) le_ms_13_p##P##_w##NW##_q8(MvArgs a) { ms_q4k_body<P, NW, true, LE_TYPE_Q5_K>(a); }
 LE_MS13(1, 1) LE_MS13(1, 2) LE_MS13(1, 4) LE_MS13(1, 8) LE_MS13(2, 1) LE_MS13(2, 2) LE_MS13(2, 4) LE_MS13(2, 8) LE_MS13(4, 1) LE_MS13(4, 2) LE_MS13(4, 4)
+#endif
+#if LE_PART_MV == 11
+#define LE_MS11(P, NW)                                                                                     \
+    extern "C" __global__ void __launch_bounds__(NW * 64) le_ms_11_p##P##_w##NW(MvArgs a) { ms_q6k_body<P, NW, false, LE_TYPE_Q3_K>(a); } \
+    extern "C" __global__ void __launch_bounds__(NW * 64) le_ms_11_p##P##_w##NW##_q8(MvArgs a) { ms_q6k_body<P, NW, true, LE_TYPE_Q3_K>(a); }
+LE_MS11(1, 1) LE_MS11(1, 2) LE_MS11(1, 4) LE_MS11(1, 8) LE_MS11(2, 1) LE_MS11(2, 2) LE_MS11(2, 4) LE_MS11(2, 8) LE_MS11(4, 1) LE_MS11(4, 2) LE_MS11(4, 4)
 #endif
 #if LE_PART_MV == 14
 LE_MS14(1, 1) LE_MS14(1, 2) LE_MS14(1, 4) LE_MS14(1, 8) LE_MS14(2, 1) LE_MS14(2, 2) LE_MS14(2, 4) LE_MS14(2, 8) LE_MS14(4, 1) LE_MS14(4, 2)
@@ -2678,7 +2739,7 @@ __device__ __forceinline__ void moe_dnm_body(const MoeArgs &a) {
 #pragma unroll
     for (int i = 0; i < NI; i++) {
         const int c = min(64 * i + lane, NCH - 1), col = c % CPR, cc = col == CPS * P ? 0 : col;
-        roff[i] = (row0 + c / CPR) * (int)rb + (TD == LE_TYPE_Q6_K ? (cc / 14) * 210 + (cc % 14) * 16 : cc * 16);
+        roff[i] = (row0 + c / CPR) * (int)rb + (TD == LE_TYPE_Q6_K ? (cc / 14) * 210 + q6_goff(cc % 14) : cc * 16);
     }
     /* weights of two groups in flight: R0 is the next group to compute, R1 the one after */
     uint4 R0[NI], R1[NI];
@@ -2884,7 +2945,7 @@ __device__ __forceinline__ void moe_fus_body(const MoeArgs &a) {
 #pragma unroll
     for (int i = 0; i < DNI; i++) {
         const int c = min(64 * i + lane, DNCH - 1), col = c % DCPR, cc = col == DCPS * PD ? 0 : col;
-        roff[i] = (16 * tb + c / DCPR) * (int)drb + (TD == LE_TYPE_Q6_K ? (cc / 14) * 210 + (cc % 14) * 16 : cc * 16);
+        roff[i] = (16 * tb + c / DCPR) * (int)drb + (TD == LE_TYPE_Q6_K ? (cc / 14) * 210 + q6_goff(cc % 14) : cc * 16);
     }
     uint4 R0[DNI];
     auto dissue = [&](int zz, uint4 (&r)[DNI]) {
