@@ -95,6 +95,7 @@ struct le_ctx {
      * item (Q8_0 32000x4096: 29.7 us against the vector kernel's 36.5; Q4_0 14336x4096: 10.7 against
      * 12.6, 4096x4096: 5.4 against 11.1) */
     int ms80 = 1, ms_p80 = 1, ms40 = 1, ms_p40 = 2;
+    int ms2s = 1, ms_p2s = 1; /* IQ2_S on the Q6_K kernel's map (14336x4096: 13.0 us against the vector kernel's 13.9, 4096x4096: 6.2 against 8.7) */
     int ms3k = 1, ms_p3k = 2; /* Q3_K on the Q6_K kernel's map (14336x4096: 11.7 us against the vector kernel's 15.7, 4096x4096: 5.4 against 9.5) */
     int ms5k = 1, ms_p5k = 1; /* Q5_K the same way (the Q4_K kernel with the fifth bit from qh; 14336x4096: 11.1 us against the vector kernel's 14.5, 4096x4096: 4.9 against 8.5) */
     int mq_q8 = 1;           /* int8 mode on the staged MFMA kernels: Q4_K 14336x4096 13.1 -> 9.9 us, Q6_K 4096x14336
@@ -257,7 +258,7 @@ int mq_launch(le_ctx *c, int ty, const void *const *ptrs, const void *w, const f
     char name[64];
     size_t lds = (size_t)nsb * 608 + (size_t)NW * 64;
     /* staged variant: P super-blocks per row and item, NWs waves splitting K evenly */
-    int P = ty == LE_TYPE_Q6_K ? c->ms_p6 : ty == LE_TYPE_Q4_K ? c->ms_p : ty == LE_TYPE_Q8_0 ? c->ms_p80 : ty == LE_TYPE_Q4_0 ? c->ms_p40 : ty == LE_TYPE_Q5_K ? c->ms_p5k : ty == LE_TYPE_Q3_K ? c->ms_p3k : c->ms_piq, NWs = NW;
+    int P = ty == LE_TYPE_Q6_K ? c->ms_p6 : ty == LE_TYPE_Q4_K ? c->ms_p : ty == LE_TYPE_Q8_0 ? c->ms_p80 : ty == LE_TYPE_Q4_0 ? c->ms_p40 : ty == LE_TYPE_Q5_K ? c->ms_p5k : ty == LE_TYPE_Q3_K ? c->ms_p3k : ty == LE_TYPE_IQ2_S ? c->ms_p2s : c->ms_piq, NWs = NW;
     while (P > 1 && nsb % P) P >>= 1;
     /* Q6_K keeps the waves and gives up super-blocks per item when both do not divide K (4096 x
      * 14336, 56 super-blocks: P=1 on 8 waves 14.1 us against P=2 on 4 waves 16.0); the other
@@ -265,7 +266,7 @@ int mq_launch(le_ctx *c, int ty, const void *const *ptrs, const void *w, const f
     if (ty == LE_TYPE_Q6_K && nsb % (NWs * P) && nsb % NWs == 0) P = 1;
     while (NWs > 1 && nsb % (NWs * P)) NWs >>= 1;
     if (c->ms && nsb % (NWs * P) == 0) {
-        const int cps = ty == LE_TYPE_Q6_K ? 14 : ty == LE_TYPE_IQ2_XXS ? 5 : ty == LE_TYPE_IQ3_XXS ? 7 : ty == LE_TYPE_Q8_0 ? 17 : ty == LE_TYPE_Q5_K ? 11 : ty == LE_TYPE_Q3_K ? 7 : 9;
+        const int cps = ty == LE_TYPE_Q6_K ? 14 : ty == LE_TYPE_IQ2_XXS ? 5 : ty == LE_TYPE_IQ3_XXS ? 7 : ty == LE_TYPE_Q8_0 ? 17 : ty == LE_TYPE_Q5_K ? 11 : ty == LE_TYPE_Q3_K ? 7 : ty == LE_TYPE_IQ2_S ? 6 : 9;
         const int cpr = cps * P + 1, ni = (16 * cpr + 63) / 64;
         snprintf(name, sizeof name, "le_ms_%d_p%d_w%d%s", ty, P, NWs, xq8 ? "_q8" : "");
         lds = (size_t)NWs * ((size_t)(nsb / NWs) * 608 + (size_t)ni * 1024) + (size_t)NWs * 128;
@@ -349,7 +350,7 @@ int mv_launch(le_ctx *c, int ty, const void *const *ptrs, const void *w, const f
     const int nsb = cols / 256, G = pick_g(nsb), S = nsb / G;
     const bool iq = ty == LE_TYPE_IQ2_XXS || ty == LE_TYPE_IQ3_XXS;
     const bool q80 = (ty == LE_TYPE_Q8_0 && c->ms80) || (ty == LE_TYPE_Q4_0 && c->ms40) || (ty == LE_TYPE_Q5_K && c->ms5k) ||
-                     (ty == LE_TYPE_Q3_K && c->ms3k);
+                     (ty == LE_TYPE_Q3_K && c->ms3k) || (ty == LE_TYPE_IQ2_S && c->ms2s);
     if ((ty == LE_TYPE_Q4_K || (ty == LE_TYPE_Q6_K && c->mq6) || (iq && c->mqiq) || q80) && ntok == 1 && c->mq &&
         (!q8 || (c->mq_q8 && ty != LE_TYPE_IQ2_XXS)) && (size_t)nsb * 608 + 1024 <= c->lds_limit) {
         const int rc = mq_launch(c, ty, ptrs, w, x, x_slot, y, y_slot, rows, cols, slots, st, swiglu, xq8, xd8);
@@ -572,6 +573,11 @@ int le_set_option(le_ctx *c, const char *name, int value) {
         c->moe_fused = value ? 1 : 0;
     } else if (n == "moe_mfma") {
         c->moe_mfma = value ? 1 : 0;
+    } else if (n == "ms_p2s") {
+        if (value != 1 && value != 2 && value != 4) return c->fail(LE_ERR_ARG, "ms_p2s must be 1, 2 or 4");
+        c->ms_p2s = value;
+    } else if (n == "ms2s") {
+        c->ms2s = value ? 1 : 0;
     } else if (n == "ms_p3k") {
         if (value != 1 && value != 2 && value != 4) return c->fail(LE_ERR_ARG, "ms_p3k must be 1, 2 or 4");
         c->ms_p3k = value;

@@ -1017,6 +1017,54 @@ __device__ __forceinline__ float ms_sb_q3k(const uint4 *sbp, const le_v4i (&A)[4
     return h2f(c6.w >> 16) * t;
 }
 
+/* IQ2_S (src/quant.rs:155-167), 82 bytes: d, qs[32] (grid index low bits), signs[32], qh[8] (index
+ * high bits), scales[8] (4 bits per 16 values). Sub-block ib is one 32-value block with one scale
+ * per 16 values, so the Q6_K kernel's map (two accumulators per sub-block) applies with sub-block
+ * j = 4 (b >> 1) + sq and values 16 (b & 1) ... Staged as 6 chunks, the last one at byte 66
+ * (bytes 66-81: qh, then the scales), so no load reads past the super-block; slot bytes 0-79 are
+ * the super-block's, 80-87 qh, 88-95 the scales. */
+__device__ __forceinline__ int i2s_goff(int c) { return c == 5 ? 66 : 16 * c; }
+__device__ __forceinline__ float ms_sb_iq2s(const uint4 *sbp, const le_v4i (&A)[4], const float *dxp_sb, const MsLane &L,
+                                            const u32 *tab) {
+    const int sq = L.sq;
+    const u32 *w32 = (const u32 *)sbp, *grid = tab + LE_TAB_GRID;
+    le_v4i D0 = {0, 0, 0, 0}, D1 = {0, 0, 0, 0};
+#pragma unroll
+    for (int b = 0; b < 4; b++) {
+        const int hn = b >> 1, is = b & 1, j = 4 * hn + sq;
+        /* qs bytes 2 + 4j + 2is, +1 and sign bytes 34 + 4j + 2is, +1 (2 mod 4 aligned) */
+        const u32 q16 = is ? (w32[j + 1] & 0xFFFFu) : (w32[j] >> 16);
+        const u32 s16 = is ? (w32[9 + j] & 0xFFFFu) : (w32[8 + j] >> 16);
+        const u32 qh = (w32[20 + (j >> 2)] >> (8 * (j & 3))) & 255u;
+        u32 o[4];
+#pragma unroll
+        for (int l = 0; l < 2; l++) {
+            const int g = 2 * is + l; /* 8-value group of the 32 */
+            const u32 gi = ((q16 >> (8 * l)) & 255u) | ((qh << (8 - 2 * g)) & 0x300u);
+            const u32 sg = (s16 >> (8 * l)) & 255u;
+            const uint2 gv = *(const uint2 *)(grid + 2 * gi);
+            o[2 * l] = apply_sign(gv.x, nib_mask(sg & 15u));
+            o[2 * l + 1] = apply_sign(gv.y, nib_mask(sg >> 4));
+        }
+        const le_v4i B = {(int)o[0], (int)o[1], (int)o[2], (int)o[3]};
+        if (is)
+            D1 = __builtin_amdgcn_mfma_i32_16x16x64_i8(A[b], B, D1, 0, 0, 0);
+        else
+            D0 = __builtin_amdgcn_mfma_i32_16x16x64_i8(A[b], B, D0, 0, 0, 0);
+    }
+    /* lane: sub-blocks jb + i (jb = 4 (sq & 1)), 16-value scales 2 ls + 1 (d / 8 outside) */
+    const u32 scw = w32[22 + (sq & 1)];
+    const float4 dq = *(const float4 *)(dxp_sb + L.pe * 8 + L.jb);
+    const float dqa[4] = {dq.x, dq.y, dq.z, dq.w};
+    float t = 0.f;
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+        const u32 sc = (scw >> (8 * i)) & 255u;
+        t += dqa[i] * ((float)(2 * (sc & 15u) + 1) * (float)D0[i] + (float)(2 * (sc >> 4) + 1) * (float)D1[i]);
+    }
+    return h2f(w32[0] & 0xFFFFu) * 0.125f * t;
+}
+
 /* Staged variant: each wave streams its tile's P super-blocks per row as consecutive 16-byte
  * chunks (consecutive lanes take consecutive chunks of a row, so every load instruction reads
  * long contiguous runs), prefetched into registers one item ahead and written to a wave-private
@@ -1332,8 +1380,8 @@ __device__ __forceinline__ void ms_q4k_t_body(const MvArgs &a) {
 template <int P, int NW, bool Q8, int TY = LE_TYPE_Q6_K>
 __device__ __forceinline__ void ms_q6k_body(const MvArgs &a) {
     extern __shared__ uint4 smem[];
-    constexpr bool Q3 = TY == LE_TYPE_Q3_K;
-    constexpr int CPS = Q3 ? 7 : 14, SBB = Q3 ? 110 : 210, CPR = CPS * P + 1, NCH = 16 * CPR, NI = (NCH + 63) / 64;
+    constexpr bool Q3 = TY == LE_TYPE_Q3_K, S2 = TY == LE_TYPE_IQ2_S;
+    constexpr int CPS = Q3 ? 7 : S2 ? 6 : 14, SBB = Q3 ? 110 : S2 ? 82 : 210, CPR = CPS * P + 1, NCH = 16 * CPR, NI = (NCH + 63) / 64;
     const int K = a.cols, nsb = K >> 8;
     const int slot = blockIdx.y;
     const u8 *W = a.ptrs ? a.ptrs[slot] : a.w0 + (size_t)slot * a.w_slot_bytes;
@@ -1347,6 +1395,11 @@ __device__ __forceinline__ void ms_q6k_body(const MvArgs &a) {
     uint4 *wb = (uint4 *)(fsv + nsbw * 8);
     float *red = (float *)(smem + NW * (nsbw * 38 + NI * 64)); /* [2][NW][16] */
     const int ntile = (a.rows + 15) >> 4;
+    __shared__ u32 tab[S2 ? LE_TAB_GRID + 2048 : 1]; /* IQ2_S: sign masks and the 1024-entry grid */
+    if constexpr (S2) {
+        load_tables<TY>(tab);
+        __syncthreads();
+    }
 
     /* chunk i of this lane: row ri[i] of the tile, global byte gb[i] and LDS chunk index of the
      * row's P-super-block run (the pad chunk re-reads chunk 0) */
@@ -1356,7 +1409,7 @@ __device__ __forceinline__ void ms_q6k_body(const MvArgs &a) {
         const int c = min(64 * i + lane, NCH - 1);
         const int col = c % CPR, cc = col == CPS * P ? 0 : col;
         ri[i] = c / CPR;
-        gb[i] = (cc / CPS) * SBB + (Q3 ? q3_goff(cc % CPS) : q6_goff(cc % CPS));
+        gb[i] = (cc / CPS) * SBB + (Q3 ? q3_goff(cc % CPS) : S2 ? i2s_goff(cc % CPS) : q6_goff(cc % CPS));
     }
     uint4 R[NI];
     auto issue = [&](int tile, int s0) {
@@ -1414,6 +1467,8 @@ __device__ __forceinline__ void ms_q6k_body(const MvArgs &a) {
                     ms_load_a(rec + sb * 32, L, A);
                     if constexpr (Q3)
                         y += ms_sb_q3k(wb + n * CPR + CPS * q, A, dxp + sb * 16, L);
+                    else if constexpr (S2)
+                        y += ms_sb_iq2s(wb + n * CPR + CPS * q, A, dxp + sb * 16, L, tab);
                     else
                         y += ms_sb_q6k(wb + n * CPR + CPS * q, A, dxp + sb * 16, L);
                 }
@@ -1695,6 +1750,12 @@ LE_MS13(1, 1) LE_MS13(1, 2) LE_MS13(1, 4) LE_MS13(1, 8) LE_MS13(2, 1) LE_MS13(2,
     extern "C" __global__ void __launch_bounds__(NW * 64) le_ms_11_p##P##_w##NW(MvArgs a) { ms_q6k_body<P, NW, false, LE_TYPE_Q3_K>(a); } \
     extern "C" __global__ void __launch_bounds__(NW * 64) le_ms_11_p##P##_w##NW##_q8(MvArgs a) { ms_q6k_body<P, NW, true, LE_TYPE_Q3_K>(a); }
 LE_MS11(1, 1) LE_MS11(1, 2) LE_MS11(1, 4) LE_MS11(1, 8) LE_MS11(2, 1) LE_MS11(2, 2) LE_MS11(2, 4) LE_MS11(2, 8) LE_MS11(4, 1) LE_MS11(4, 2) LE_MS11(4, 4)
+#endif
+#if LE_PART_MV == 22
+#define LE_MS22(P, NW)                                                                                     \
+    extern "C" __global__ void __launch_bounds__(NW * 64) le_ms_22_p##P##_w##NW(MvArgs a) { ms_q6k_body<P, NW, false, LE_TYPE_IQ2_S>(a); } \
+    extern "C" __global__ void __launch_bounds__(NW * 64) le_ms_22_p##P##_w##NW##_q8(MvArgs a) { ms_q6k_body<P, NW, true, LE_TYPE_IQ2_S>(a); }
+LE_MS22(1, 1) LE_MS22(1, 2) LE_MS22(1, 4) LE_MS22(1, 8) LE_MS22(2, 1) LE_MS22(2, 2) LE_MS22(2, 4) LE_MS22(2, 8) LE_MS22(4, 1) LE_MS22(4, 2) LE_MS22(4, 4)
 #endif
 #if LE_PART_MV == 14
 LE_MS14(1, 1) LE_MS14(1, 2) LE_MS14(1, 4) LE_MS14(1, 8) LE_MS14(2, 1) LE_MS14(2, 2) LE_MS14(2, 4) LE_MS14(2, 8) LE_MS14(4, 1) LE_MS14(4, 2)

@@ -246,10 +246,10 @@ def test_matvec_q8_vector_path(fresh_engine, name):
         assert np.all(np.abs(got - want) <= 1e-5 * mag + 1e-30), (flag, float(np.max(np.abs(got - want) / mag)))
 
 
-@pytest.mark.parametrize("name,opt", [("Q8_0", "ms80"), ("Q4_0", "ms40"), ("Q5_K", "ms5k"), ("Q3_K", "ms3k")])
+@pytest.mark.parametrize("name,opt", [("Q8_0", "ms80"), ("Q4_0", "ms40"), ("Q5_K", "ms5k"), ("Q3_K", "ms3k"), ("IQ2_S", "ms2s")])
 @pytest.mark.parametrize("rows,cols", [(333, 4096), (40, 14336), (17, 256), (64, 768)])
 def test_matvec_staged_q8_0_q4_0(fresh_engine, name, opt, rows, cols):
-    """Q8_0, Q4_0, Q5_K and Q3_K batch-1 matvec on the staged matrix-core kernels (option 1) and on the vector
+    """Q8_0, Q4_0, Q5_K, Q3_K and IQ2_S batch-1 matvec on the staged matrix-core kernels (option 1) and on the vector
     kernels (option 0): both meet the parity bar against the oracle, with and without the int8
     activation mode."""
     import torch
