@@ -1764,6 +1764,9 @@ LE_MS14(1, 1) LE_MS14(1, 2) LE_MS14(1, 4) LE_MS14(1, 8) LE_MS14(2, 1) LE_MS14(2,
 LE_MSIQ(LE_PART_MV, 1, 1) LE_MSIQ(LE_PART_MV, 1, 2) LE_MSIQ(LE_PART_MV, 1, 4) LE_MSIQ(LE_PART_MV, 2, 1) LE_MSIQ(LE_PART_MV, 2, 2)
 LE_MSIQ(LE_PART_MV, 2, 4) LE_MSIQ(LE_PART_MV, 4, 1) LE_MSIQ(LE_PART_MV, 4, 2) LE_MSIQ(LE_PART_MV, 4, 4)
 LE_MSIQ(LE_PART_MV, 1, 8) LE_MSIQ(LE_PART_MV, 2, 8)
+#if LE_PART_MV == 18 /* down-projection shapes: one row tile per block, K split over 12-16 waves */
+LE_MSIQ(LE_PART_MV, 2, 12) LE_MSIQ(LE_PART_MV, 2, 14) LE_MSIQ(LE_PART_MV, 2, 16)
+#endif
 #endif
 #endif
 
