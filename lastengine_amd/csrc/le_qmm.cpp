@@ -261,10 +261,11 @@ int mq_launch(le_ctx *c, int ty, const void *const *ptrs, const void *w, const f
     /* staged variant: P super-blocks per row and item, NWs waves splitting K evenly */
     int P = ty == LE_TYPE_Q6_K ? c->ms_p6 : ty == LE_TYPE_Q4_K ? c->ms_p : ty == LE_TYPE_Q8_0 ? c->ms_p80 : ty == LE_TYPE_Q4_0 ? c->ms_p40 : ty == LE_TYPE_Q5_K ? c->ms_p5k : ty == LE_TYPE_Q3_K ? c->ms_p3k : ty == LE_TYPE_IQ2_S ? c->ms_p2s : c->ms_piq, NWs = NW;
     while (P > 1 && nsb % P) P >>= 1;
-    /* Q6_K keeps the waves and gives up super-blocks per item when both do not divide K (4096 x
-     * 14336, 56 super-blocks: P=1 on 8 waves 14.1 us against P=2 on 4 waves 16.0); the other
-     * types keep P (IQ3_XXS: 15.4 against 20.0 us) */
-    if (ty == LE_TYPE_Q6_K && nsb % (NWs * P) && nsb % NWs == 0) P = 1;
+    /* keep the waves and give up super-blocks per item when both do not divide K (4096 x 14336, 56
+     * super-blocks, P=1 on 8 waves against P=2 on 4: Q6_K 14.1 against 16.0 us, Q4_K 10.6 / 12.1,
+     * Q4_0 13.6 / 14.0, Q3_K 13.4 / 14.0, IQ2_S 12.7 / 16.1); IQ3_XXS keeps P (15.4 against 20.0
+     * us; its down shapes take the wider split below) */
+    if (ty != LE_TYPE_IQ3_XXS && nsb % (NWs * P) && nsb % NWs == 0) P = 1;
     /* IQ3_XXS with no more row tiles than CUs and K of 48 super-blocks or more (a down projection:
      * one tile per block) splits K over 12-16 waves of two super-blocks each: 4096 x 14336 15.5 ->
      * 12.8 us, 4096 x 12288 11.9 -> 11.0 (2048 x 8192, 32 super-blocks: 8.2 -> 8.8, so not there;
