@@ -1755,7 +1755,7 @@ LE_MS11(1, 1) LE_MS11(1, 2) LE_MS11(1, 4) LE_MS11(1, 8) LE_MS11(2, 1) LE_MS11(2,
 #define LE_MS22(P, NW)                                                                                     \
     extern "C" __global__ void __launch_bounds__(NW * 64) le_ms_22_p##P##_w##NW(MvArgs a) { ms_q6k_body<P, NW, false, LE_TYPE_IQ2_S>(a); } \
     extern "C" __global__ void __launch_bounds__(NW * 64) le_ms_22_p##P##_w##NW##_q8(MvArgs a) { ms_q6k_body<P, NW, true, LE_TYPE_IQ2_S>(a); }
-LE_MS22(1, 1) LE_MS22(1, 2) LE_MS22(1, 4) LE_MS22(1, 8) LE_MS22(2, 1) LE_MS22(2, 2) LE_MS22(2, 4) LE_MS22(2, 8) LE_MS22(4, 1) LE_MS22(4, 2) LE_MS22(4, 4)
+LE_MS22(2, 12) LE_MS22(2, 14) LE_MS22(2, 16) LE_MS22(1, 1) LE_MS22(1, 2) LE_MS22(1, 4) LE_MS22(1, 8) LE_MS22(2, 1) LE_MS22(2, 2) LE_MS22(2, 4) LE_MS22(2, 8) LE_MS22(4, 1) LE_MS22(4, 2) LE_MS22(4, 4)
 #endif
 #if LE_PART_MV == 14
 LE_MS14(1, 1) LE_MS14(1, 2) LE_MS14(1, 4) LE_MS14(1, 8) LE_MS14(2, 1) LE_MS14(2, 2) LE_MS14(2, 4) LE_MS14(2, 8) LE_MS14(4, 1) LE_MS14(4, 2)
@@ -1764,7 +1764,7 @@ LE_MS14(1, 1) LE_MS14(1, 2) LE_MS14(1, 4) LE_MS14(1, 8) LE_MS14(2, 1) LE_MS14(2,
 LE_MSIQ(LE_PART_MV, 1, 1) LE_MSIQ(LE_PART_MV, 1, 2) LE_MSIQ(LE_PART_MV, 1, 4) LE_MSIQ(LE_PART_MV, 2, 1) LE_MSIQ(LE_PART_MV, 2, 2)
 LE_MSIQ(LE_PART_MV, 2, 4) LE_MSIQ(LE_PART_MV, 4, 1) LE_MSIQ(LE_PART_MV, 4, 2) LE_MSIQ(LE_PART_MV, 4, 4)
 LE_MSIQ(LE_PART_MV, 1, 8) LE_MSIQ(LE_PART_MV, 2, 8)
-#if LE_PART_MV == 18 /* down-projection shapes: one row tile per block, K split over 12-16 waves */
+#if LE_PART_MV == 18 || LE_PART_MV == 16 || LE_PART_MV == 2 /* down-projection shapes: one row tile per block, K split over 12-16 waves */
 LE_MSIQ(LE_PART_MV, 2, 12) LE_MSIQ(LE_PART_MV, 2, 14) LE_MSIQ(LE_PART_MV, 2, 16)
 #endif
 #endif
