@@ -85,8 +85,8 @@ const char *le_last_error(const le_ctx *ctx);
  *     "ms_piq" (IQ2_XXS, IQ3_XXS), "ms_p80" (Q8_0), "ms_p40" (Q4_0), "ms_p5k" (Q5_K), "ms_p3k"
  *     (Q3_K), "ms_p2s" (IQ2_S), and "mq6" / "mqiq" / "ms80" / "ms40" / "ms5k" / "ms3k" / "ms2s"
  *     (0/1) for the Q6_K / IQ / Q8_0 / Q4_0 / Q5_K / Q3_K / IQ2_S staged kernels (0: vector kernels);
- *     "ms_wide" (0/1) IQ3_XXS / IQ2_XXS / IQ2_S / Q4_0 down shapes (row tiles <= CUs, K >= 48
- *     super-blocks) on 12-16 waves; "mq_q8" (0/1) int8 mode on
+ *     "ms_wide" (0/1) down shapes (row tiles <= CUs, K >= 48 super-blocks) on 12-16 waves, every
+ *     type but Q6_K and Q8_0; "mq_q8" (0/1) int8 mode on
  *     the staged kernels;
  *     "ms_t" (0/1): Q4_K with 2..8 tokens per pass on the staged kernel (one weight stream, 8 tokens
  *     per MFMA pass), used by le_gemm below "gm_min_m" tokens

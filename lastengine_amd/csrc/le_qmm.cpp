@@ -95,7 +95,7 @@ struct le_ctx {
      * item (Q8_0 32000x4096: 29.7 us against the vector kernel's 36.5; Q4_0 14336x4096: 10.7 against
      * 12.6, 4096x4096: 5.4 against 11.1) */
     int ms80 = 1, ms_p80 = 1, ms40 = 1, ms_p40 = 2;
-    int ms_wide = 1;         /* IQ3_XXS / IQ2_XXS / IQ2_S / Q4_0 down shapes on 12-16 waves (below) */
+    int ms_wide = 1;         /* down shapes on 12-16 waves, every type but Q6_K and Q8_0 (below) */
     int ms2s = 1, ms_p2s = 1; /* IQ2_S on the Q6_K kernel's map (14336x4096: 13.0 us against the vector kernel's 13.9, 4096x4096: 6.2 against 8.7) */
     int ms3k = 1, ms_p3k = 2; /* Q3_K on the Q6_K kernel's map (14336x4096: 11.7 us against the vector kernel's 15.7, 4096x4096: 5.4 against 9.5) */
     int ms5k = 1, ms_p5k = 1; /* Q5_K the same way (the Q4_K kernel with the fifth bit from qh; 14336x4096: 11.1 us against the vector kernel's 14.5, 4096x4096: 4.9 against 8.5) */
@@ -266,12 +266,12 @@ int mq_launch(le_ctx *c, int ty, const void *const *ptrs, const void *w, const f
      * Q4_0 13.6 / 14.0, Q3_K 13.4 / 14.0, IQ2_S 12.7 / 16.1); IQ3_XXS keeps P (15.4 against 20.0
      * us; its down shapes take the wider split below) */
     if (ty != LE_TYPE_IQ3_XXS && nsb % (NWs * P) && nsb % NWs == 0) P = 1;
-    /* IQ3_XXS, IQ2_XXS, IQ2_S and Q4_0 with no more row tiles than CUs and K of 48 super-blocks or
-     * more (a down projection: one tile per block) split K over 12-16 waves of two super-blocks
-     * each: 4096 x 14336 IQ3_XXS 15.5 -> 12.8 us, IQ2_XXS 12.1 -> 10.9, IQ2_S 13.2 -> 12.5, Q4_0
-     * 13.9 -> 10.8; IQ3_XXS 4096 x 12288 11.9 -> 11.0 (2048 x 8192, 32 super-blocks: 8.2 -> 8.8,
-     * so not there; Q6_K 14.3 -> 14.8 and Q8_0 17.0 -> 28.4 lose) */
-    if ((ty == LE_TYPE_IQ3_XXS || ty == LE_TYPE_IQ2_XXS || ty == LE_TYPE_IQ2_S || ty == LE_TYPE_Q4_0) && c->ms_wide && (rows + 15) / 16 * (long long)slots <= c->cus && nsb >= 48 && nsb % 2 == 0)
+    /* with no more row tiles than CUs and K of 48 super-blocks or more (a down projection: one tile
+     * per block), K is split over 12-16 waves of two super-blocks each: 4096 x 14336 IQ3_XXS 15.5
+     * -> 12.8 us, IQ2_XXS 12.1 -> 10.9, IQ2_S 13.2 -> 12.5, Q4_0 13.9 -> 10.8, Q4_K 10.6 -> 9.8,
+     * Q5_K 12.4 -> 11.7, Q3_K 13.6 -> 12.4; IQ3_XXS 4096 x 12288 11.9 -> 11.0 (2048 x 8192, 32
+     * super-blocks: 8.2 -> 8.8, so not there); Q6_K 14.3 -> 14.8 and Q8_0 17.0 -> 28.4 lose */
+    if (ty != LE_TYPE_Q6_K && ty != LE_TYPE_Q8_0 && c->ms_wide && (rows + 15) / 16 * (long long)slots <= c->cus && nsb >= 48 && nsb % 2 == 0)
         for (const int w : {16, 14, 12})
             if ((nsb / 2) % w == 0) { NWs = w; P = 2; break; }
     while (NWs > 1 && nsb % (NWs * P)) NWs >>= 1;

@@ -1735,7 +1735,7 @@ __device__ __forceinline__ void ms_iq_body(const MvArgs &a) {
 LE_MV_ALL(LE_PART_MV)
 #if LE_PART_MV == 12
 LE_MQ12(4, 1) LE_MQ12(4, 2) LE_MQ12(4, 4) LE_MQ12(8, 1) LE_MQ12(8, 2) LE_MQ12(8, 4) LE_MQ12(2, 1) LE_MQ12(2, 2) LE_MQ12(2, 4)
-LE_MS12(1, 1) LE_MS12(1, 2) LE_MS12(1, 4) LE_MS12(1, 8) LE_MS12(2, 1) LE_MS12(2, 2) LE_MS12(2, 4) LE_MS12(2, 8) LE_MS12(4, 1) LE_MS12(4, 2) LE_MS12(4, 4)
+LE_MS12(2, 12) LE_MS12(2, 14) LE_MS12(2, 16) LE_MS12(1, 1) LE_MS12(1, 2) LE_MS12(1, 4) LE_MS12(1, 8) LE_MS12(2, 1) LE_MS12(2, 2) LE_MS12(2, 4) LE_MS12(2, 8) LE_MS12(4, 1) LE_MS12(4, 2) LE_MS12(4, 4)
 LE_MS12T(1, 4, 2) LE_MS12T(1, 4, 4) LE_MS12T(1, 4, 8) LE_MS12T(1, 8, 2) LE_MS12T(1, 8, 4) LE_MS12T(1, 8, 8)
 LE_MS12T(2, 4, 2) LE_MS12T(2, 4, 4) LE_MS12T(2, 4, 8) LE_MS12T(2, 2, 2) LE_MS12T(2, 2, 4) LE_MS12T(2, 2, 8)
 #endif
@@ -1743,13 +1743,13 @@ LE_MS12T(2, 4, 2) LE_MS12T(2, 4, 4) LE_MS12T(2, 4, 8) LE_MS12T(2, 2, 2) LE_MS12T
 #define LE_MS13(P, NW)                                                                                     \
     extern "C" __global__ void __launch_bounds__(NW * 64) le_ms_13_p##P##_w##NW(MvArgs a) { ms_q4k_body<P, NW, false, LE_TYPE_Q5_K>(a); } \
     extern "C" __global__ void __launch_bounds__(NW * 64) le_ms_13_p##P##_w##NW##_q8(MvArgs a) { ms_q4k_body<P, NW, true, LE_TYPE_Q5_K>(a); }
-LE_MS13(1, 1) LE_MS13(1, 2) LE_MS13(1, 4) LE_MS13(1, 8) LE_MS13(2, 1) LE_MS13(2, 2) LE_MS13(2, 4) LE_MS13(2, 8) LE_MS13(4, 1) LE_MS13(4, 2) LE_MS13(4, 4)
+LE_MS13(2, 12) LE_MS13(2, 14) LE_MS13(2, 16) LE_MS13(1, 1) LE_MS13(1, 2) LE_MS13(1, 4) LE_MS13(1, 8) LE_MS13(2, 1) LE_MS13(2, 2) LE_MS13(2, 4) LE_MS13(2, 8) LE_MS13(4, 1) LE_MS13(4, 2) LE_MS13(4, 4)
 #endif
 #if LE_PART_MV == 11
 #define LE_MS11(P, NW)                                                                                     \
     extern "C" __global__ void __launch_bounds__(NW * 64) le_ms_11_p##P##_w##NW(MvArgs a) { ms_q6k_body<P, NW, false, LE_TYPE_Q3_K>(a); } \
     extern "C" __global__ void __launch_bounds__(NW * 64) le_ms_11_p##P##_w##NW##_q8(MvArgs a) { ms_q6k_body<P, NW, true, LE_TYPE_Q3_K>(a); }
-LE_MS11(1, 1) LE_MS11(1, 2) LE_MS11(1, 4) LE_MS11(1, 8) LE_MS11(2, 1) LE_MS11(2, 2) LE_MS11(2, 4) LE_MS11(2, 8) LE_MS11(4, 1) LE_MS11(4, 2) LE_MS11(4, 4)
+LE_MS11(2, 12) LE_MS11(2, 14) LE_MS11(2, 16) LE_MS11(1, 1) LE_MS11(1, 2) LE_MS11(1, 4) LE_MS11(1, 8) LE_MS11(2, 1) LE_MS11(2, 2) LE_MS11(2, 4) LE_MS11(2, 8) LE_MS11(4, 1) LE_MS11(4, 2) LE_MS11(4, 4)
 #endif
 #if LE_PART_MV == 22
 #define LE_MS22(P, NW)                                                                                     \
