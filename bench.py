@@ -515,13 +515,17 @@ def main():
         for tname, ty, r_, c_, mts in [("q6k_down_4096x14336", le.Q6_K, 4096, 14336, (17, 64, 512)),
                                       ("q8_0_head_32000x4096", le.Q8_0, 32000, 4096, (64, 512)),
                                       ("iq2xxs_14336x4096", le.IQ2_XXS, 14336, 4096, (64, 512)),
-                                      ("iq3xxs_4096x14336", le.IQ3_XXS, 4096, 14336, (64, 512))]:
+                                      ("iq3xxs_4096x14336", le.IQ3_XXS, 4096, 14336, (64, 512)),
+                                      ("q4_0_14336x4096", le.Q4_0, 14336, 4096, (64, 512)),
+                                      ("q3_k_14336x4096", le.Q3_K, 14336, 4096, (64, 512)),
+                                      ("q5_k_14336x4096", le.Q5_K, 14336, 4096, (64, 512)),
+                                      ("iq2_s_14336x4096", le.IQ2_S, 14336, 4096, (64, 512))]:
             for mt in mts:
                 g = bench_gemm(eng, ty, r_, c_, mt, max(20, steps2 // (1 + mt // 8)), 4)
                 sec["gemm_%s_m%d" % (tname, mt)] = g
                 log("gemm %s m=%d" % (tname, mt), g)
                 torch.cuda.empty_cache()
-        for size in (33030144, 9437184):
+        for size in (536870912, 33030144, 9437184):
             sec["stream_read_ceiling_%dB" % size] = bench_stream_read(eng, size, steps2, 20)
             log("stream read", size, sec["stream_read_ceiling_%dB" % size])
         out["secondary"] = sec

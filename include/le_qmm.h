@@ -22,10 +22,11 @@
  *     32-value activation block is held as a 15-bit integer split into two int8 planes with an
  *     fp32 scale (error <= 3.1e-5 of the block maximum per value); weight codes are exact.
  *
- * Supported types (GGML ids, src/quant.rs:13-20): Q8_0=8, Q4_K=12, Q6_K=14, IQ2_XXS=16, IQ3_XXS=18 on
- * every entry point; Q4_0=2, Q3_K=11, Q5_K=13 and IQ2_S=22 (src/quant.rs:64-67,83-95,113-126,155-167,
- * the reference's matvec_2/_11/_13/_22, src/cuda/kernels.cu:391) on le_dequant_rows, le_matvec,
- * le_matvec_q8 and le_gemm (vector-ALU kernels; LE_ERR_TYPE from the MoE and grouped entries).
+ * Supported types (GGML ids, src/quant.rs:13-20): Q8_0=8, Q4_K=12, Q6_K=14, IQ2_XXS=16, IQ3_XXS=18,
+ * and Q4_0=2, Q3_K=11, Q5_K=13, IQ2_S=22 (src/quant.rs:64-67,83-95,113-126,155-167; the reference's
+ * matvec_2/_11/_13/_22, mmq128r_2/_11/_13 and mm_22/mmq_22, src/cuda/kernels.cu:391,719,1225-1234),
+ * on every entry point. The MoE layer's decode-shaped kernels take the type pairs listed there;
+ * every other pair runs its grouped form.
  */
 #ifndef LE_QMM_H
 #define LE_QMM_H
@@ -157,16 +158,16 @@ int le_matvec_q8(le_ctx *ctx, int ty, const void *const *ptrs, const void *w, co
  *      src/cuda/kernels.cu:965-1235, src/gpu/dense.rs:181-199; CPU twin cpu_ref::matmat,
  *      src/cpu_ref.rs:266-276) ----
  * Y[t * rows + r] = W[r,:] . X[t * cols ...] for t < m. ws: device workspace of
- * le_gemm_workspace_size(ty, m, cols) bytes (may be 0 bytes / NULL when that size is 0, as it is for
- * Q4_0, Q3_K, Q5_K and IQ2_S, which run on the vector multi-token kernels at every M), the
- * counterpart of the reference's pre-quantized activation buffers (xqb/xdb/xsb, src/gpu.rs:210).
- * Every type runs on the matrix cores from 17 tokens (Q4_K: 3..16 tokens on a staged f16 MFMA
- * kernel, 2 on the staged int8 matvec; other types: from "gq_min_m" = 9 tokens, vector kernels
- * below). On the matrix cores each token is scaled by its own power of two and rounded to fp16
- * (relative error 2^-11 per value at any magnitude up to 2^127); Q8_0 weights enter as
- * fp16(q * 64 d) (so |d| < 8), the other types as exact integer codes (Q6_K: rounded to fp16
- * where (q - 32) * sc has more than 11 significant bits). The 3..16-token Q4_K kernel scales each
- * token's 256-value super-block by its own power of two instead (the same 2^-11 at any magnitude). */
+ * le_gemm_workspace_size(ty, m, cols) bytes, the counterpart of the reference's pre-quantized
+ * activation buffers (xqb/xdb/xsb, src/gpu.rs:210). Every type runs on the matrix cores from 17
+ * tokens (Q4_K: 3..16 tokens on a staged f16 MFMA kernel, 2 on the staged int8 matvec; other types:
+ * from "gq_min_m" = 9 tokens, vector kernels below). On the matrix cores each token is scaled by
+ * its own power of two and rounded to fp16 (relative error 2^-11 per value at any magnitude up to
+ * 2^127); Q8_0 and Q4_0 weights enter as fp16(q * d_b * 2^S), one rounding, with a power of two per
+ * row that keeps every code inside the fp16 range for any finite scales; the other types as exact
+ * integer codes (Q6_K: rounded to fp16 where (q - 32) * sc has more than 11 significant bits). The
+ * 3..16-token Q4_K kernel scales each token's 256-value super-block by its own power of two
+ * instead (the same 2^-11 at any magnitude). */
 size_t le_gemm_workspace_size(int ty, int m, int cols);
 /* Workspace with room for the K slices' partial results as well (no counterpart in the reference,
  * whose GEMM never splits K): shapes with few row and token tiles are split along K to fill the
@@ -221,7 +222,10 @@ int le_gemm_noalloc(le_ctx *ctx, int ty, const void *w, const float *x, int m, f
  * gate/up: n_exp slabs of ff x hidden (types ty_gate, ty_up), down: n_exp slabs of hidden x ff
  * (ty_down), slab e at e * rows * row_bytes. Routing and grouping by expert run on the device
  * (no host synchronisation); each routed expert's weights are read once per call. idx_out/w_out
- * (n_tok*k, optional) receive the selection. ws: device workspace of le_moe_workspace_size bytes.
+ * (n_tok*k, optional) receive the selection. ws: device workspace of le_moe_workspace_size bytes
+ * (type pairs other than (Q4_K, Q6_K), (Q4_K, Q4_K), (Q6_K, Q6_K), (Q8_0, Q8_0), (IQ2_XXS, IQ3_XXS),
+ * (IQ2_XXS, IQ2_XXS), (IQ3_XXS, IQ3_XXS) run the grouped form below at every token count and need
+ * le_moe_prefill_workspace_size bytes).
  * Limits: n_tok <= 65536, k <= 16, n_exp <= 256, hidden and ff multiples of 256.
  * Prefill-sized calls (more than 64 tokens; from 24 tokens when ws holds
  * le_moe_prefill_workspace_size bytes) route every token, group the (token, expert) pairs by

@@ -23,8 +23,9 @@ PARTS = {"deq": ["-DLE_PART_DEQ"], "moe": ["-DLE_PART_MOE"]}
 for _ty in (2, 8, 11, 12, 13, 14, 16, 18, 22):
     PARTS["mv%d" % _ty] = ["-DLE_PART_MV=%d" % _ty]
 PARTS["gm"] = []
-PARTS["gq"] = []
-SOURCES = {"gm": "le_gemm_kernels.hip", "gq": "le_gq_kernels.hip"}  # parts not listed here compile le_qmm_kernels.hip
+PARTS["gq"] = ["-DLE_GQ_SET=1"]
+PARTS["gq2"] = ["-DLE_GQ_SET=2"]
+SOURCES = {"gm": "le_gemm_kernels.hip", "gq": "le_gq_kernels.hip", "gq2": "le_gq_kernels.hip"}  # parts not listed here compile le_qmm_kernels.hip
 
 HOST_SOURCES = ["le_qmm.cpp", "le_quant.cpp", "le_gguf.cpp"]
 # Host sources that declare device memory (hipcc, host and device passes), linked into the library.

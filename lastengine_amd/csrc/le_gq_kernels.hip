@@ -16,8 +16,8 @@
  * 2^-11; values below 2^-24 of the token's maximum flush towards zero). The result is written in
  * fragment order, [32-token tile][K/16 chunk][8-lane half][token][8 halves], so a block copies
  * each step's activations as contiguous 8 KB runs and every A fragment is one conflict-free
- * 16-byte LDS read per lane. Q4_K also gets per-super-block sub-block sums S_j (per 32 values,
- * as fp16 high + low halves) for its offset term. The final store multiplies by
+ * 16-byte LDS read per lane. Q4_K and Q5_K also get per-super-block sub-block sums S_j (per 32
+ * values, as fp16 high + low halves) for their offset term. The final store multiplies by
  * 2^e_t, so the result does not depend on the activations' magnitude.
  *
  * Weights. Raw GGUF rows (src/gpu.rs:79-83), read in half super-blocks (128 values) per pipeline
@@ -30,8 +30,13 @@
  *          bits, else rounded once to fp16), epilogue acc += 64 d * D1           (:96-112)
  *   IQ2_XXS code (2s+1) * grid * sign (<= 1333, exact), epilogue acc += d/8 * D1   (:142-154)
  *   IQ3_XXS code (2s+1) * grid * sign (<= 1922, exact), epilogue acc += d/4 * D1   (:127-141)
- *   Q8_0   per-32 scale d_b inside the code: fp16(q * (64 d_b)) (one rounding, 2^-11 relative),
- *          no epilogue, final * 2^-6 (fp16 range: |d_b| < 8, i.e. |w| < 1016)       (:68-71)
+ *   Q5_K   as Q4_K with the fifth bit from qh, code sc_j * q (<= 1953, exact)     (:83-95)
+ *   Q3_K   code (q3 - 4) * (sc6 - 32) (|.| <= 128, exact), epilogue acc += d * D1 (:113-126)
+ *   IQ2_S  code (2s+1) * grid * sign, 1024-entry grid, explicit sign bytes, epilogue acc += d/8 * D1
+ *                                                                                  (:155-167)
+ *   Q8_0, Q4_0  per-32 scale d_b inside the code: fp16(q * d_b 2^S) (one rounding, 2^-11
+ *          relative), S a per-row power of two that only decreases (the accumulator is rescaled
+ *          when it does) and keeps every code inside the fp16 range, final * 2^-S  (:64-71)
  * Integer byte -> fp16 conversion: a byte u placed under the fp16 exponent of 1024 (v_perm_b32)
  * is the half 1024 + u exactly; one packed fma (u+1024)*c - 1024*c gives u*c rounded once.
  *
@@ -54,6 +59,7 @@ typedef float le_v16f __attribute__((ext_vector_type(16)));
 
 __device__ const u32 le_gq_iq2_grid[512] = LE_IQ2XXS_GRID_WORDS;
 __device__ const u32 le_gq_iq3_grid[256] = LE_IQ3XXS_GRID_WORDS;
+__device__ const u32 le_gq_iq2s_grid[2048] = LE_IQ2S_GRID_WORDS;
 
 struct GqArgs {
     const u8 *w;
@@ -157,8 +163,39 @@ struct GqF<LE_TYPE_Q6_K> { /* slot: [0,64) ql half, [64,96) qh half, [96,112) sc
     __device__ static int loff(int k) { return 16 * k; }
 };
 template <>
+struct GqF<LE_TYPE_Q5_K> { /* slot: [0,16) header, [16,48) qh (all 32 bytes), [48,112) this half's 64 quant bytes */
+    static constexpr int SBB = 176, NCH = 7, SLOT = 112, SREC = 1024, EPI = 1, TAB = 0;
+    static constexpr bool ALIGNED = true;
+    __device__ static int goff(int k, int h) { return k < 3 ? 16 * k : 48 + 64 * h + 16 * (k - 3); }
+    __device__ static int loff(int k) { return 16 * k; }
+};
+template <>
+struct GqF<LE_TYPE_Q3_K> { /* slot: [0,32) the half's 32 quant bytes, [32,64) hmask, [64,80) bytes 94..109 (scales at
+                             * 66..77, d at 78) */
+    static constexpr int SBB = 110, NCH = 5, SLOT = 80, SREC = 0, EPI = 1, TAB = 0;
+    static constexpr bool ALIGNED = false;
+    __device__ static int goff(int k, int h) { return k < 2 ? 32 + 32 * h + 16 * k : k < 4 ? 16 * (k - 2) : 94; }
+    __device__ static int loff(int k) { return 16 * k; }
+};
+template <>
+struct GqF<LE_TYPE_IQ2_S> { /* slot: [0,16) the half's grid index bytes, [16,32) its sign bytes, [32,48) bytes 66..81
+                             * (qh[8], scales[8]), [48,64) bytes 0..15 (d at 48) */
+    static constexpr int SBB = 82, NCH = 4, SLOT = 80, SREC = 0, EPI = 1, TAB = 16384 + 4096;
+    static constexpr bool ALIGNED = false;
+    __device__ static int goff(int k, int h) { return k == 0 ? 2 + 16 * h : k == 1 ? 34 + 16 * h : k == 2 ? 66 : 0; }
+    __device__ static int loff(int k) { return 16 * k; }
+};
+template <>
+struct GqF<LE_TYPE_Q4_0> { /* 8 blocks of 18 bytes form a 144-byte super-block; slot: [16b, 16b+16) quant bytes of block b
+                            * of the half, [64 + 16b] chunk starting at d_b; 144-byte stride */
+    static constexpr int SBB = 144, NCH = 8, SLOT = 144, SREC = 0, EPI = 2, TAB = 0;
+    static constexpr bool ALIGNED = false;
+    __device__ static int goff(int k, int h) { return k < 4 ? 72 * h + 18 * k + 2 : 72 * h + 18 * (k - 4); }
+    __device__ static int loff(int k) { return 16 * k; }
+};
+template <>
 struct GqF<LE_TYPE_Q8_0> { /* slot: [32b, 32b+32) quants of block b of the half, [128 + 16b] chunk starting at d_b */
-    static constexpr int SBB = 272, NCH = 12, SLOT = 192, SREC = 0, EPI = 0, TAB = 0;
+    static constexpr int SBB = 272, NCH = 12, SLOT = 192, SREC = 0, EPI = 2, TAB = 0;
     static constexpr bool ALIGNED = false;
     __device__ static int goff(int k, int h) {
         return k < 8 ? 136 * h + 34 * (k >> 1) + 2 + 16 * (k & 1) : 136 * h + 34 * (k - 8);
@@ -181,16 +218,18 @@ struct GqF<LE_TYPE_IQ3_XXS> { /* slot: [0,32) the half's grid indices, [32,48) i
     __device__ static int loff(int k) { return 16 * k; }
 };
 
-/* IQ tables in LDS, in fragment order: grid entries as fp16 magnitudes (IQ2_XXS: 8 per entry, P8
- * order; IQ3_XXS: 4 per entry, order 0,2,1,3), then for each 7-bit sign index the 8 half masks of
- * ksign (src/quant.rs:57), 0x8000 where the value is negative, P8 order. */
+/* IQ tables in LDS, in fragment order: grid entries as fp16 magnitudes (IQ2_XXS, IQ2_S: 8 per
+ * entry, P8 order; IQ3_XXS: 4 per entry, order 0,2,1,3), then for each 7-bit sign index the 8 half
+ * masks of ksign (src/quant.rs:57), or for IQ2_S for each sign byte its 8 bits (src/quant.rs:155-167),
+ * 0x8000 where the value is negative, P8 order. */
 template <int TY>
 __device__ __forceinline__ void gq_tables(u8 *tab) {
-    if constexpr (TY == LE_TYPE_IQ2_XXS || TY == LE_TYPE_IQ3_XXS) {
-        constexpr int NG = 256, GB = TY == LE_TYPE_IQ2_XXS ? 16 : 8;
+    if constexpr (TY == LE_TYPE_IQ2_XXS || TY == LE_TYPE_IQ3_XXS || TY == LE_TYPE_IQ2_S) {
+        constexpr int NG = TY == LE_TYPE_IQ2_S ? 1024 : 256, GB = TY == LE_TYPE_IQ3_XXS ? 8 : 16;
         for (int i = threadIdx.x; i < NG; i += blockDim.x) {
-            if constexpr (TY == LE_TYPE_IQ2_XXS) {
-                const u32 w0 = le_gq_iq2_grid[2 * i], w1 = le_gq_iq2_grid[2 * i + 1];
+            if constexpr (TY != LE_TYPE_IQ3_XXS) {
+                const u32 *gw = TY == LE_TYPE_IQ2_S ? le_gq_iq2s_grid : le_gq_iq2_grid;
+                const u32 w0 = gw[2 * i], w1 = gw[2 * i + 1];
                 *(uint4 *)(tab + GB * i) = make_uint4(pk_add(h1024_02(w0), 0xE400E400u), pk_add(h1024_13(w0), 0xE400E400u),
                                                       pk_add(h1024_02(w1), 0xE400E400u), pk_add(h1024_13(w1), 0xE400E400u));
             } else {
@@ -198,9 +237,11 @@ __device__ __forceinline__ void gq_tables(u8 *tab) {
                 *(uint2 *)(tab + GB * i) = make_uint2(pk_add(h1024_02(w0), 0xE400E400u), pk_add(h1024_13(w0), 0xE400E400u));
             }
         }
+        /* IQ2_S stores its 8 sign bits explicitly: 256 entries indexed by the sign byte */
+        constexpr int NS = TY == LE_TYPE_IQ2_S ? 256 : 128;
         u8 *sg = tab + NG * GB;
-        for (int i = threadIdx.x; i < 128; i += blockDim.x) {
-            const u32 ks = (u32)i | ((__builtin_popcount((u32)i) & 1u) << 7);
+        for (int i = threadIdx.x; i < NS; i += blockDim.x) {
+            const u32 ks = NS == 256 ? (u32)i : (u32)i | ((__builtin_popcount((u32)i) & 1u) << 7);
             u32 m[4];
 #pragma unroll
             for (int p = 0; p < 4; p++) { /* halves 2p, 2p+1 hold values P8(2p), P8(2p+1) */
@@ -490,6 +531,9 @@ __device__ __forceinline__ void gq_body(const GqArgs &a, const u8 *ws) {
         for (int k = 0; k < TN; k++) acc[i][k] = d1[i][k] = (le_v16f){};
 
     const int n = lane & 31, hs = lane >> 5;
+    int rowS[TN]; /* Q8_0 / Q4_0: the accumulator holds the row's sum times 2^rowS */
+#pragma unroll
+    for (int k = 0; k < TN; k++) rowS[k] = 127;
     Set RA, RB; /* RA holds odd (h = 1) steps, RB even ones */
     const int s0 = 2 * sb0;
     /* the loads must reach the memory pipeline in step order (RA's before RB's, as in the loop),
@@ -618,25 +662,62 @@ __device__ __forceinline__ void gq_body(const GqArgs &a, const u8 *ws) {
                         if (c1 == 0 && q == 0) pipe();
                     }
                 }
-            } else if constexpr (TY == LE_TYPE_Q8_0) {
+            } else if constexpr (TY == LE_TYPE_Q8_0 || TY == LE_TYPE_Q4_0) {
+                /* per-32 scales inside the codes: fp16(q * d_b 2^S) (one rounding), with a power of two
+                 * 2^S per row that keeps every code inside the fp16 range whatever the scales are:
+                 * S only decreases, to the value that puts the step's largest |d_b| 2^S in
+                 * [128, 256) (|q| <= 128) when that is below the current one, and the accumulator
+                 * is then rescaled (a wave-uniform branch, taken at the first step and
+                 * otherwise only when a row's scales grow); the result is multiplied by 2^-S */
+                constexpr int DO = TY == LE_TYPE_Q8_0 ? 128 : 64, QB = TY == LE_TYPE_Q8_0 ? 32 : 16;
+                u32 r[TN][4];
+                bool grow = false;
+                int sn[TN];
 #pragma unroll
-                for (int b = 0; b < 4; b++) {
-                    u32 r[TN]; /* (64 d_b) duplicated: exact in fp16 for |d_b| < 1024 */
+                for (int k = 0; k < TN; k++) {
+                    u32 dv[4], mx = 0;
+#pragma unroll
+                    for (int b = 0; b < 4; b++) {
+                        dv[b] = *(const u32 *)(rs[k] + DO + 16 * b) & 0xFFFFu;
+                        mx = max(mx, dv[b] & 0x7FFFu);
+                    }
+                    const int e = max((int)(mx >> 10), 1); /* biased fp16 exponent of the largest |d_b| */
+                    sn[k] = min(rowS[k], 22 - e);
+                    grow |= sn[k] != rowS[k];
+                    const float up_ = __builtin_bit_cast(float, (u32)(127 + sn[k]) << 23);
+#pragma unroll
+                    for (int b = 0; b < 4; b++) r[k][b] = h2dup(h2f(dv[b]) * up_);
+                }
+                if (__any(grow)) {
 #pragma unroll
                     for (int k = 0; k < TN; k++) {
-                        const u32 dv = *(const u32 *)(rs[k] + 128 + 16 * b) & 0xFFFFu;
-                        r[k] = pk_mul(dv | (dv << 16), 0x54005400u);
+                        const float f = ldexpf(1.f, sn[k] - rowS[k]);
+                        rowS[k] = sn[k];
+#pragma unroll
+                        for (int i = 0; i < TM; i++)
+#pragma unroll
+                            for (int e = 0; e < 16; e++) acc[i][k][e] *= f;
                     }
+                }
+#pragma unroll
+                for (int b = 0; b < 4; b++) {
 #pragma unroll
                     for (int c1 = 0; c1 < 2; c1++) {
                         const int c = 2 * b + c1;
                         le_v8h B[TN];
 #pragma unroll
                         for (int k = 0; k < TN; k++) {
-                            const uint2 q = *(const uint2 *)(rs[k] + 32 * b + 16 * c1 + 8 * hs);
-                            const u32 x = q.x ^ 0x80808080u, y = q.y ^ 0x80808080u;
-                            B[k] = as_v8h(make_uint4(pk_mul(pk_add(h1024_02(x), 0xE480E480u), r[k]), pk_mul(pk_add(h1024_13(x), 0xE480E480u), r[k]),
-                                                     pk_mul(pk_add(h1024_02(y), 0xE480E480u), r[k]), pk_mul(pk_add(h1024_13(y), 0xE480E480u), r[k])));
+                            if constexpr (TY == LE_TYPE_Q8_0) {
+                                const uint2 q = *(const uint2 *)(rs[k] + QB * b + 16 * c1 + 8 * hs);
+                                const u32 x = q.x ^ 0x80808080u, y = q.y ^ 0x80808080u; /* q + 128 */
+                                B[k] = as_v8h(make_uint4(pk_mul(pk_add(h1024_02(x), 0xE480E480u), r[k][b]), pk_mul(pk_add(h1024_13(x), 0xE480E480u), r[k][b]),
+                                                         pk_mul(pk_add(h1024_02(y), 0xE480E480u), r[k][b]), pk_mul(pk_add(h1024_13(y), 0xE480E480u), r[k][b])));
+                            } else { /* value j < 16: low nibble of byte j; j >= 16: high nibble of byte j - 16 */
+                                const uint2 q = *(const uint2 *)(rs[k] + QB * b + 8 * hs);
+                                const u32 x = (q.x >> (4 * c1)) & 0x0F0F0F0Fu, y = (q.y >> (4 * c1)) & 0x0F0F0F0Fu;
+                                B[k] = as_v8h(make_uint4(pk_mul(pk_add(h1024_02(x), 0xE408E408u), r[k][b]), pk_mul(pk_add(h1024_13(x), 0xE408E408u), r[k][b]),
+                                                         pk_mul(pk_add(h1024_02(y), 0xE408E408u), r[k][b]), pk_mul(pk_add(h1024_13(y), 0xE408E408u), r[k][b])));
+                            }
                         }
                         le_v8h A[TM];
                         afrag(c, A);
@@ -644,7 +725,129 @@ __device__ __forceinline__ void gq_body(const GqArgs &a, const u8 *ws) {
                         if (c == 0) pipe();
                     }
                 }
-            } else { /* IQ2_XXS, IQ3_XXS */
+            } else if constexpr (TY == LE_TYPE_Q5_K) {
+                /* the Q4_K decode with the fifth bit of each code from qh: bit 2G (low nibbles of group
+                 * G) and 2G + 1 (high nibbles) of byte l (src/quant.rs:83-95); codes sc * q <= 1953 */
+                u32 scw[TN];
+#pragma unroll
+                for (int k = 0; k < TN; k++) {
+                    const uint4 hd = *(const uint4 *)rs[k];
+                    scw[k] = h ? ((hd.w & 0x0F0F0F0Fu) | ((hd.y >> 2) & 0x30303030u)) : (hd.y & 0x3F3F3F3Fu);
+                }
+#pragma unroll
+                for (int g = 0; g < 2; g++) {
+                    const int G = 2 * h + g;
+                    uint4 kc[TN]; /* (sc_lo, -1024 sc_lo, sc_hi, -1024 sc_hi) as duplicated halves */
+#pragma unroll
+                    for (int k = 0; k < TN; k++) {
+                        const u32 slo = pk_add(h1024_dup(scw[k], 2 * g), 0xE400E400u);
+                        const u32 shi = pk_add(h1024_dup(scw[k], 2 * g + 1), 0xE400E400u);
+                        kc[k] = make_uint4(slo, pk_mul(slo, 0xE400E400u), shi, pk_mul(shi, 0xE400E400u));
+                    }
+#pragma unroll
+                    for (int c1 = 0; c1 < 2; c1++) {
+                        const int c = 4 * g + c1;
+                        le_v8h blo[TN], bhi[TN];
+#pragma unroll
+                        for (int k = 0; k < TN; k++) {
+                            const uint2 q = *(const uint2 *)(rs[k] + 48 + 32 * g + 16 * c1 + 8 * hs);
+                            const uint2 qh = *(const uint2 *)(rs[k] + 16 + 16 * c1 + 8 * hs);
+                            const u32 lx = and_or(q.x, 0x0F0F0F0Fu, ((qh.x >> (2 * G)) << 4) & 0x10101010u);
+                            const u32 ly = and_or(q.y, 0x0F0F0F0Fu, ((qh.y >> (2 * G)) << 4) & 0x10101010u);
+                            const u32 hx = and_or(q.x >> 4, 0x0F0F0F0Fu, ((qh.x >> (2 * G + 1)) << 4) & 0x10101010u);
+                            const u32 hy = and_or(q.y >> 4, 0x0F0F0F0Fu, ((qh.y >> (2 * G + 1)) << 4) & 0x10101010u);
+                            blo[k] = as_v8h(make_uint4(pk_fma(h1024_02(lx), kc[k].x, kc[k].y), pk_fma(h1024_13(lx), kc[k].x, kc[k].y),
+                                                       pk_fma(h1024_02(ly), kc[k].x, kc[k].y), pk_fma(h1024_13(ly), kc[k].x, kc[k].y)));
+                            bhi[k] = as_v8h(make_uint4(pk_fma(h1024_02(hx), kc[k].z, kc[k].w), pk_fma(h1024_13(hx), kc[k].z, kc[k].w),
+                                                       pk_fma(h1024_02(hy), kc[k].z, kc[k].w), pk_fma(h1024_13(hy), kc[k].z, kc[k].w)));
+                        }
+                        le_v8h A[TM];
+                        afrag(c, A);
+                        gq_mma(d1, A, blo, h == 0 && c == 0);
+                        afrag(c + 2, A);
+                        gq_mma(d1, A, bhi, false);
+                        if (g == 0 && c1 == 0) pipe();
+                    }
+                }
+            } else if constexpr (TY == LE_TYPE_Q3_K) {
+                /* value 128h + 32s + l: code ((qs[32h + l] >> 2s) & 3) - (hm[l] bit 4h + s ? 0 : 4), scale
+                 * 8h + c of the sixteen signed 6-bit scales (src/quant.rs:113-126); |code * scale| <= 128, exact */
+                u32 sp[TN][8];
+#pragma unroll
+                for (int k = 0; k < TN; k++) {
+                    const uint4 sw = *(const uint4 *)(rs[k] + 64); /* scale byte i at slot byte 66 + i */
+                    const u32 s0 = __builtin_amdgcn_alignbyte(sw.y, sw.x, 2), s1 = __builtin_amdgcn_alignbyte(sw.z, sw.y, 2);
+                    const u32 s2 = __builtin_amdgcn_alignbyte(sw.w, sw.z, 2);
+                    /* scale i = 8h + c: low 4 bits from byte c (h = 0) or its high nibble (h = 1), bits 4-5
+                     * from byte 8 + c % 4 at bit 2 (2h + c / 4) */
+                    const u32 v0 = ((s0 >> (4 * h)) & 0x0F0F0F0Fu) | (((s2 >> (4 * h)) & 0x03030303u) << 4);
+                    const u32 v1 = ((s1 >> (4 * h)) & 0x0F0F0F0Fu) | (((s2 >> (4 * h + 2)) & 0x03030303u) << 4);
+#pragma unroll
+                    for (int c = 0; c < 8; c++) sp[k][c] = pk_add(h1024_dup(c < 4 ? v0 : v1, c & 3), 0xE420E420u); /* byte - 32 */
+                }
+                uint2 qa[TN][2], hm[TN][2];
+#pragma unroll
+                for (int k = 0; k < TN; k++)
+#pragma unroll
+                    for (int p = 0; p < 2; p++) {
+                        qa[k][p] = *(const uint2 *)(rs[k] + 16 * p + 8 * hs);
+                        hm[k][p] = *(const uint2 *)(rs[k] + 32 + 16 * p + 8 * hs);
+                    }
+#pragma unroll
+                for (int c = 0; c < 8; c++) {
+                    const int sub = c >> 1, p = c & 1;
+                    le_v8h B[TN];
+#pragma unroll
+                    for (int k = 0; k < TN; k++) {
+                        const u32 vx = and_or(qa[k][p].x >> (2 * sub), 0x03030303u, ((hm[k][p].x >> (4 * h + sub)) & 0x01010101u) << 2);
+                        const u32 vy = and_or(qa[k][p].y >> (2 * sub), 0x03030303u, ((hm[k][p].y >> (4 * h + sub)) & 0x01010101u) << 2);
+                        const u32 sc = sp[k][c];
+                        B[k] = as_v8h(make_uint4(pk_mul(pk_add(h1024_02(vx), 0xE404E404u), sc), pk_mul(pk_add(h1024_13(vx), 0xE404E404u), sc),
+                                                 pk_mul(pk_add(h1024_02(vy), 0xE404E404u), sc), pk_mul(pk_add(h1024_13(vy), 0xE404E404u), sc)));
+                    }
+                    le_v8h A[TM];
+                    afrag(c, A);
+                    gq_mma(d1, A, B, h == 0 && c == 0);
+                    if (c == 0) pipe();
+                }
+            } else if constexpr (TY == LE_TYPE_IQ2_S) {
+                /* block 4h + b, 8-value group l: grid index qs[4b + l] | bits 2l, 2l+1 of qh[b] as bits 8-9,
+                 * signs = byte 4b + l, factor 2 s + 1 of the block's nibble l / 2 (src/quant.rs:155-167) */
+                const u8 *sgt = tab + 1024 * 16;
+                u32 qhw[TN], scw[TN];
+#pragma unroll
+                for (int k = 0; k < TN; k++) {
+                    qhw[k] = *(const u32 *)(rs[k] + 32 + 4 * h);
+                    scw[k] = *(const u32 *)(rs[k] + 40 + 4 * h);
+                }
+#pragma unroll
+                for (int b = 0; b < 4; b++) {
+                    u32 qi[TN], sg[TN];
+#pragma unroll
+                    for (int k = 0; k < TN; k++) {
+                        qi[k] = *(const u32 *)(rs[k] + 4 * b);
+                        sg[k] = *(const u32 *)(rs[k] + 16 + 4 * b);
+                    }
+#pragma unroll
+                    for (int c1 = 0; c1 < 2; c1++) {
+                        const int c = 2 * b + c1, l = 2 * c1 + hs;
+                        le_v8h B[TN];
+#pragma unroll
+                        for (int k = 0; k < TN; k++) {
+                            const u32 qhb = (qhw[k] >> (8 * b)) & 0xFFu;
+                            const u32 gi = ((qi[k] >> (8 * l)) & 255u) | ((qhb << (8 - 2 * l)) & 0x300u);
+                            const u32 f = pk_add(h1024_dup(2u * ((scw[k] >> (8 * b + 4 * c1)) & 15u) + 1u, 0), 0xE400E400u);
+                            const uint4 g = *(const uint4 *)(tab + 16 * gi);
+                            const uint4 m = *(const uint4 *)(sgt + 16 * ((sg[k] >> (8 * l)) & 255u));
+                            B[k] = as_v8h(make_uint4(pk_mul(g.x, f) ^ m.x, pk_mul(g.y, f) ^ m.y, pk_mul(g.z, f) ^ m.z, pk_mul(g.w, f) ^ m.w));
+                        }
+                        le_v8h A[TM];
+                        afrag(c, A);
+                        gq_mma(d1, A, B, h == 0 && c == 0);
+                        if (c == 0) pipe();
+                    }
+                }
+            } else if constexpr (TY == LE_TYPE_IQ2_XXS || TY == LE_TYPE_IQ3_XXS) {
                 constexpr int GB = TY == LE_TYPE_IQ2_XXS ? 16 : 8;
                 const u8 *sgt = tab + 256 * GB;
 #pragma unroll
@@ -690,13 +893,13 @@ __device__ __forceinline__ void gq_body(const GqArgs &a, const u8 *ws) {
             }
         }
         /* super-block epilogue (the h = 1 buffer holds this super-block's second half) */
-        if constexpr (F::EPI) {
+        if constexpr (F::EPI == 1) {
             const u8 *Wb = lds + BUF;
             const u8 *Sb = Sl + (sb & 1) * SBYTES + (wm * TM) * F::SREC;
 #pragma unroll
             for (int k = 0; k < TN; k++) {
                 const u8 *r = Wb + (wn * TN * 32 + 32 * k + n) * F::SLOT;
-                if constexpr (TY == LE_TYPE_Q4_K) {
+                if constexpr (TY == LE_TYPE_Q4_K || TY == LE_TYPE_Q5_K) {
                     const uint4 hd = *(const uint4 *)r;
                     const u32 m0 = hd.z & 0x3F3F3F3Fu, m1 = ((hd.w >> 4) & 0x0F0F0F0Fu) | ((hd.z >> 2) & 0x30303030u);
                     const le_v8h b2 = as_v8h(make_uint4(pk_add(h1024_02(m0), 0xE400E400u), pk_add(h1024_13(m0), 0xE400E400u),
@@ -715,9 +918,15 @@ __device__ __forceinline__ void gq_body(const GqArgs &a, const u8 *ws) {
                     for (int i = 0; i < TM; i++)
 #pragma unroll
                         for (int e = 0; e < 16; e++) acc[i][k][e] = __builtin_fmaf(d64, d1[i][k][e], acc[i][k][e]);
+                } else if constexpr (TY == LE_TYPE_Q3_K) {
+                    const float dd = h2f(*(const uint16_t *)(r + 78));
+#pragma unroll
+                    for (int i = 0; i < TM; i++)
+#pragma unroll
+                        for (int e = 0; e < 16; e++) acc[i][k][e] = __builtin_fmaf(dd, d1[i][k][e], acc[i][k][e]);
                 } else {
                     const float dd = h2f(*(const uint16_t *)(r + (TY == LE_TYPE_IQ2_XXS ? 32 : 48))) *
-                                     (TY == LE_TYPE_IQ2_XXS ? 0.125f : 0.25f);
+                                     (TY == LE_TYPE_IQ3_XXS ? 0.25f : 0.125f);
 #pragma unroll
                     for (int i = 0; i < TM; i++)
 #pragma unroll
@@ -728,12 +937,21 @@ __device__ __forceinline__ void gq_body(const GqArgs &a, const u8 *ws) {
     }
     /* D lane l element e: token 8 (e / 4) + 4 (l / 32) + e % 4 of the tile, row l % 32; the
      * token scales of the padded tile are all loaded first (one memory round trip) */
-    const float post = TY == LE_TYPE_Q8_0 ? 0.015625f : 1.f;
+    if constexpr (F::EPI == 2) {
+#pragma unroll
+        for (int k = 0; k < TN; k++) {
+            const float f = ldexpf(1.f, -rowS[k]);
+#pragma unroll
+            for (int i = 0; i < TM; i++)
+#pragma unroll
+                for (int e = 0; e < 16; e++) acc[i][k][e] *= f;
+        }
+    }
     float ts[TM][16];
 #pragma unroll
     for (int i = 0; i < TM; i++)
 #pragma unroll
-        for (int e = 0; e < 16; e++) ts[i][e] = tsc[mb + (wm * TM + i) * 32 + 4 * hs + 8 * (e >> 2) + (e & 3)] * post;
+        for (int e = 0; e < 16; e++) ts[i][e] = tsc[mb + (wm * TM + i) * 32 + 4 * hs + 8 * (e >> 2) + (e & 3)];
     if (!GR && a.ksplit > 1 && !a.part) { /* K slices without a partial-result buffer: atomic adds */
 #pragma unroll
         for (int i = 0; i < TM; i++) {
@@ -791,10 +1009,17 @@ __device__ __forceinline__ void gq_body(const GqArgs &a, const u8 *ws) {
 #define LE_GQX(TY, SK) \
     extern "C" __global__ void __launch_bounds__(256) le_gq_xprep_##TY(GqArgs a, u8 *ws) { gq_xprep_body<SK>(a, ws); } \
     extern "C" __global__ void __launch_bounds__(256) le_gq_xprepg_##TY(GqArgs a, u8 *ws) { gq_xprep_body<SK, true>(a, ws); }
+/* two code objects, compiled in parallel: the five types of the reference's mmq kernels, and the
+ * four formats added beside them (LE_GQ_SET=2) */
+#if LE_GQ_SET == 2
+LE_GQX(2, 0) LE_GQX(11, 0) LE_GQX(13, 1) LE_GQX(22, 0)
+#else
 LE_GQX(8, 0) LE_GQX(12, 1) LE_GQX(14, 0) LE_GQX(16, 0) LE_GQX(18, 0)
+#endif
 
 /* Sum of the K slices' partial results: y[e] = part[0][e] + part[1][e] + ... in slice order
  * (deterministic, unlike atomic adds). */
+#if LE_GQ_SET != 2
 extern "C" __global__ void __launch_bounds__(256) le_gq_ksum(GqArgs a) {
     const size_t n = (size_t)a.m * a.rows, st = (size_t)gridDim.x * blockDim.x;
     size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
@@ -853,6 +1078,7 @@ extern "C" __global__ void __launch_bounds__(1024) le_gq_plan(GqArgs a, u8 *ws, 
     }
     if (threadIdx.x == 0) lst[0] = min(base, a.maxt);
 }
+#endif
 
 #define LE_GQ_(TY, WM, WN, TM, TN)                                                                                     \
     extern "C" __global__ void __launch_bounds__(WM * WN * 64) le_gq_##TY##_w##WM##WN##_t##TM##TN(GqArgs a, const u8 *ws) { \
@@ -864,4 +1090,8 @@ extern "C" __global__ void __launch_bounds__(1024) le_gq_plan(GqArgs a, u8 *ws, 
     }
 #define LE_GQ(TY) LE_GQ_(TY, 1, 4, 1, 2) LE_GQ_(TY, 1, 4, 2, 2) LE_GQ_(TY, 1, 4, 4, 2) LE_GQ_(TY, 2, 2, 2, 2) \
     LE_GQ_(TY, 1, 8, 2, 1) LE_GQ_(TY, 1, 8, 4, 1) LE_GQ_(TY, 1, 8, 1, 1) LE_GQ_(TY, 1, 4, 2, 1) LE_GQ_(TY, 1, 4, 1, 1) LE_GQ_(TY, 1, 4, 4, 1) LE_GQG_(TY, 1, 8, 2, 1) LE_GQG_(TY, 1, 8, 4, 1) LE_GQG_(TY, 2, 2, 2, 2) LE_GQG_(TY, 1, 8, 1, 1)
+#if LE_GQ_SET == 2
+LE_GQ(2) LE_GQ(11) LE_GQ(13) LE_GQ(22)
+#else
 LE_GQ(8) LE_GQ(12) LE_GQ(14) LE_GQ(16) LE_GQ(18)
+#endif

@@ -24,7 +24,7 @@
 namespace {
 
 const char *kParts[] = {"le_qmm_deq", "le_qmm_moe", "le_qmm_mv8", "le_qmm_mv12", "le_qmm_mv14", "le_qmm_mv16", "le_qmm_mv18", "le_qmm_gm",
-                        "le_qmm_gq", "le_qmm_mv2", "le_qmm_mv11", "le_qmm_mv13", "le_qmm_mv22"};
+                        "le_qmm_gq", "le_qmm_gq2", "le_qmm_mv2", "le_qmm_mv11", "le_qmm_mv13", "le_qmm_mv22"};
 
 /* Kernel argument block of le_mv_* (mirrors MvArgs in le_qmm_kernels.hip). */
 struct MvArgs {
@@ -184,13 +184,13 @@ struct le_ctx {
 
 namespace {
 
-/* The five types of every entry point (matrix-core GEMM, MoE, grouped matmul). */
+/* The five types of the decode-shaped MoE kernels. */
 bool supported(int ty) {
     return ty == LE_TYPE_Q8_0 || ty == LE_TYPE_Q4_K || ty == LE_TYPE_Q6_K || ty == LE_TYPE_IQ2_XXS ||
            ty == LE_TYPE_IQ3_XXS;
 }
-/* ... plus Q4_0, Q3_K, Q5_K and IQ2_S, which dequant, matvec and le_gemm (on the vector-ALU
- * multi-token kernels) accept. */
+/* ... plus Q4_0, Q3_K, Q5_K and IQ2_S: the nine types of dequant, matvec, the matrix-core GEMM, the
+ * grouped matmul and the MoE layer (other type pairs than the decode kernels' through its grouped form). */
 bool supported_mv(int ty) {
     return supported(ty) || ty == LE_TYPE_Q4_0 || ty == LE_TYPE_Q3_K || ty == LE_TYPE_Q5_K || ty == LE_TYPE_IQ2_S;
 }
@@ -819,18 +819,19 @@ static int moe_layer_impl(le_ctx *c, int ty_gate, int ty_up, int ty_down, const 
     if (tables ? !(gptr && uptr && dptr) : !(gate && up && down)) return c->fail(LE_ERR_ARG, "null weight pointer or table");
     if (!logits || !h || !out || !ws) return c->fail(LE_ERR_ARG, "null pointer");
     if (ty_gate != ty_up) return c->fail(LE_ERR_TYPE, "gate and up must share a type");
-    if (!supported(ty_gate) || !supported(ty_down)) return c->fail(LE_ERR_TYPE, "no kernel for types %d/%d", ty_gate, ty_down);
+    if (!supported_mv(ty_gate) || !supported_mv(ty_down)) return c->fail(LE_ERR_TYPE, "no kernel for types %d/%d", ty_gate, ty_down);
+    /* type pairs of the decode-shaped kernels; every other pair of the nine types runs the grouped
+     * (prefill) form at any token count */
     static const int combos[][2] = {{12, 14}, {12, 12}, {14, 14}, {8, 8}, {16, 18}, {16, 16}, {18, 18}};
     bool have = false;
     for (auto &cb : combos) have |= cb[0] == ty_gate && cb[1] == ty_down;
-    if (!have) return c->fail(LE_ERR_TYPE, "no MoE kernel for gate/up type %d with down type %d", ty_gate, ty_down);
     if (n_tok <= 0 || n_tok > LE_MOE_MAX_TOK || k <= 0 || k > 16 || n_exp <= 0 || n_exp > 256 || k > n_exp)
         return c->fail(LE_ERR_SHAPE, "MoE limits: n_tok <= %d, k <= 16, k <= n_exp <= 256", LE_MOE_MAX_TOK);
     if (hidden <= 0 || ff <= 0 || hidden % 256 || ff % 256) return c->fail(LE_ERR_SHAPE, "hidden and ff must be multiples of 256");
     /* prefill-sized token counts: routing, grouping by expert and grouped matrix-core matmuls (each
      * expert's weights streamed once per tile of its pairs); up to 64 tokens the decode kernels
      * take the call when the workspace is sized for them only */
-    if (n_tok > 64 || (c->moe_prefill && n_tok >= c->moe_prefill_min_tok &&
+    if (!have || n_tok > 64 || (c->moe_prefill && n_tok >= c->moe_prefill_min_tok &&
                        ws_bytes >= le_moe_prefill_workspace_size(n_tok, k, n_exp, hidden, ff))) {
         if (ws_bytes < le_moe_prefill_workspace_size(n_tok, k, n_exp, hidden, ff))
             return c->fail(LE_ERR_WORKSPACE, "workspace needs %zu bytes (le_moe_prefill_workspace_size)",
@@ -971,7 +972,7 @@ static int mh_launch(le_ctx *c, const void *w, const float *x, int m, float *y, 
 
 /* Generic matrix-core GEMM (le_gq_*): workspace = fp16 activation fragments for the tokens rounded
  * up to 128, per-super-block sum records (Q4_K: 1 KB per 32 tokens), token scales. */
-static int gq_srec(int ty) { return ty == LE_TYPE_Q4_K ? 1024 : 0; }
+static int gq_srec(int ty) { return ty == LE_TYPE_Q4_K || ty == LE_TYPE_Q5_K ? 1024 : 0; }
 static size_t gq_ws_bytes(int ty, int m, int cols) {
     const size_t mp = ((size_t)m + 127) / 128 * 128;
     return mp * cols * 2 + mp / 32 * (cols / 256) * gq_srec(ty) + mp * 4;
@@ -1006,10 +1007,16 @@ static int gq_slot(int ty) {
     case LE_TYPE_Q8_0: return 192;
     case LE_TYPE_IQ2_XXS: return 48;
     case LE_TYPE_IQ3_XXS: return 80;
+    case LE_TYPE_Q4_0: return 144;
+    case LE_TYPE_Q3_K: return 80;
+    case LE_TYPE_Q5_K: return 112;
+    case LE_TYPE_IQ2_S: return 80;
     }
     return 0;
 }
-static int gq_tab(int ty) { return ty == LE_TYPE_IQ2_XXS ? 6144 : ty == LE_TYPE_IQ3_XXS ? 4096 : 0; }
+static int gq_tab(int ty) {
+    return ty == LE_TYPE_IQ2_XXS ? 6144 : ty == LE_TYPE_IQ3_XXS ? 4096 : ty == LE_TYPE_IQ2_S ? 16384 + 4096 : 0;
+}
 
 static int gq_launch(le_ctx *c, int ty, const void *w, const float *x, int m, float *y, int rows, int cols, void *ws,
                      size_t ws_bytes, hipStream_t st) {
@@ -1090,7 +1097,7 @@ static int mmg_bm(int nslot, int npair) { const int c = mmg_cfg(nslot, npair); r
 static int mmg_maxt(int nslot, int npair) { const int bm = mmg_bm(nslot, npair); return nslot + (npair + bm - 1) / bm; }
 
 size_t le_mm_grouped_workspace_size(int ty, int nslot, int npair, int cols) {
-    if (!supported(ty) || nslot <= 0 || npair < 0 || cols <= 0 || cols % 256) return 0;
+    if (!supported_mv(ty) || nslot <= 0 || npair < 0 || cols <= 0 || cols % 256) return 0;
     const size_t maxt = (size_t)mmg_maxt(nslot, npair), mp = maxt * mmg_bm(nslot, npair);
     return mp * cols * 2 + mp / 32 * (cols / 256) * gq_srec(ty) + mp * 4 + 16 + 8 * maxt + 4 * (size_t)nslot;
 }
@@ -1102,7 +1109,7 @@ static int mm_grouped(le_ctx *c, int ty, const void *const *ptrs, const void *w,
                       float *y2, int rows, int cols, void *ws, size_t ws_bytes, hipStream_t stream, const float *up) {
     const bool dual = ptrs2 || w2;
     if (dual && !y2) return c->fail(LE_ERR_ARG, "null second output");
-    if (!supported(ty)) return c->fail(LE_ERR_TYPE, "no kernel for type %d", ty);
+    if (!supported_mv(ty)) return c->fail(LE_ERR_TYPE, "no kernel for type %d", ty);
     if ((!ptrs && !w) || !off || !in_idx || !out_idx || !x || !y || !ws) return c->fail(LE_ERR_ARG, "null pointer");
     if (nslot <= 0 || npair < 0 || rows <= 0 || cols <= 0) return c->fail(LE_ERR_SHAPE, "empty shape");
     if (cols % 256) return c->fail(LE_ERR_SHAPE, "cols=%d is not a multiple of 256", cols);
@@ -1151,7 +1158,7 @@ int le_mm_grouped(le_ctx *c, int ty, const void *const *ptrs, const void *w, con
 }
 
 size_t le_gemm_workspace_size(int ty, int m, int cols) {
-    if (!supported(ty) || m <= 0 || cols <= 0 || cols % 256) return 0;
+    if (!supported_mv(ty) || m <= 0 || cols <= 0 || cols % 256) return 0;
     const size_t g = gq_ws_bytes(ty, m, cols);
     if (ty != LE_TYPE_Q4_K) return g;
     /* the Q4_K GEMM of the split-activation option: two fp16 planes and 32-byte sum records */
@@ -1174,7 +1181,7 @@ int le_gemm(le_ctx *c, int ty, const void *w, const float *x, int m, float *y, i
      * shapes whose activations do not fit its LDS, and gm_split=1 (two fp16 halves, which only
      * the le_gm GEMM carries), go to a GEMM */
     const bool few = ty == LE_TYPE_Q4_K && c->gm_mh && !c->gm_split && m >= 3 && m <= c->gm_mh_max;
-    const bool gemm = ty == LE_TYPE_Q4_K ? (m >= c->gm_min_m || few) : supported(ty) && m >= c->gq_min_m;
+    const bool gemm = ty == LE_TYPE_Q4_K ? (m >= c->gm_min_m || few) : m >= c->gq_min_m;
     if (gemm && m > 0 && rows > 0 && cols > 0 && cols % 256 == 0 && w && x && y) {
         if (!ws) return c->fail(LE_ERR_ARG, "null workspace");
         if (ws_bytes < le_gemm_workspace_size(ty, m, cols))

@@ -23,6 +23,10 @@ Q4_0, Q8_0, Q3_K, Q4_K, Q5_K, Q6_K, IQ2_XXS, IQ3_XXS, IQ2_S = 2, 8, 11, 12, 13, 
 TYPES = {"Q8_0": Q8_0, "Q4_K": Q4_K, "Q6_K": Q6_K, "IQ2_XXS": IQ2_XXS, "IQ3_XXS": IQ3_XXS}
 # types that le_dequant_rows, le_matvec, le_matvec_q8 and le_gemm also accept
 MV_TYPES = dict(TYPES, Q4_0=Q4_0, Q3_K=Q3_K, Q5_K=Q5_K, IQ2_S=IQ2_S)
+# (gate/up, down) type pairs of the decode-shaped MoE kernels; every other pair of MV_TYPES runs the
+# grouped form, whose workspace is le_moe_prefill_workspace_size at any token count
+MOE_DECODE_PAIRS = {(Q4_K, Q6_K), (Q4_K, Q4_K), (Q6_K, Q6_K), (Q8_0, Q8_0), (IQ2_XXS, IQ3_XXS), (IQ2_XXS, IQ2_XXS),
+                    (IQ3_XXS, IQ3_XXS)}
 
 _STATUS = {0: "ok", -1: "invalid argument", -2: "unsupported quant type", -3: "unsupported shape",
            -4: "misaligned pointer or stride", -5: "HIP runtime error",
@@ -222,7 +226,7 @@ class Engine:
         if ws is None:
             import torch
             n = self.moe_workspace_size(n_tok, k, ff)
-            if n_tok > 16:
+            if n_tok > 16 or (ty_gate, ty_down) not in MOE_DECODE_PAIRS:
                 n = max(n, self.moe_prefill_workspace_size(n_tok, k, n_exp, hidden, ff))
             ws = torch.zeros(max(16, n), dtype=torch.uint8, device="cuda")
         if ws_bytes is None:
@@ -237,7 +241,7 @@ class Engine:
         if ws is None:
             import torch
             n = self.moe_workspace_size(n_tok, k, ff)
-            if n_tok > 16:
+            if n_tok > 16 or (ty_gate, ty_down) not in MOE_DECODE_PAIRS:
                 n = max(n, self.moe_prefill_workspace_size(n_tok, k, n_exp, hidden, ff))
             ws = torch.zeros(max(16, n), dtype=torch.uint8, device="cuda")
         if ws_bytes is None:

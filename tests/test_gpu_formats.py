@@ -86,7 +86,7 @@ def test_new_gemm_parity(engine, name, m):
     rows, cols = 96, 2048
     q = random_blocks(ty, rows, cols, seed=ty + m)
     xs = np.stack([acts(cols, 50 + t) for t in range(m)])
-    assert engine.gemm_workspace_size(ty, m, cols) == 0
+    assert engine.gemm_workspace_size(ty, m, cols) > 0  # the matrix-core GEMM's activation fragments
     y = torch.full((m * rows,), float("nan"), device="cuda")
     engine.gemm(ty, dev(q), dev(xs), m, y, rows, cols)
     sync()
@@ -94,10 +94,10 @@ def test_new_gemm_parity(engine, name, m):
     check_close(y.cpu().numpy().reshape(m, rows), want, _absmag(ty, q, rows, cols, xs))
 
 
-def test_new_types_rejected_by_moe(engine):
+def test_unknown_type_rejected_by_moe(engine):
     import torch
     with pytest.raises(le.LeError) as e:
-        engine.moe(le.Q5_K, le.Q5_K, le.Q6_K, dev(np.zeros(16, np.uint8)), dev(np.zeros(16, np.uint8)),
+        engine.moe(7, 7, le.Q6_K, dev(np.zeros(16, np.uint8)), dev(np.zeros(16, np.uint8)),
                    dev(np.zeros(16, np.uint8)), 4, 2, 256, 256, dev(np.zeros(4, np.float32)),
                    dev(np.zeros(256, np.float32)), 1, torch.empty(256, device="cuda"), ws=torch.empty(1 << 20, dtype=torch.uint8, device="cuda"))
     assert e.value.code == -2

@@ -2,22 +2,26 @@
 type, against the oracle's cpu_ref::matmat restatement (src/cpu_ref.rs:266-276).
 
 Bar (tests/util.py): max|got-want| / max|want| <= 1e-3 and |got-want| <= 1e-3 * sum|w*x| per
-output. Weights enter the matrix cores as exact integer codes (Q4_K, IQ2_XXS, IQ3_XXS; Q6_K where
-the code has at most 11 significant bits) or rounded once to fp16 (Q6_K otherwise, Q8_0), and
-activations as fp16 after a per-token power-of-two scale (relative error 2^-11)."""
+output. Weights enter the matrix cores as exact integer codes (Q4_K, Q5_K, Q3_K, IQ2_XXS, IQ3_XXS,
+IQ2_S; Q6_K where the code has at most 11 significant bits) or rounded once to fp16 (Q6_K otherwise,
+Q8_0, Q4_0), and activations as fp16 after a per-token power-of-two scale (relative error 2^-11).
+The types without a quantizer here (Q4_0, Q3_K, Q5_K, IQ2_S) are tested on arbitrary block bytes
+with bounded finite scales."""
 import numpy as np
 import pytest
 
 import lastengine_amd as le
 import oracle
-from tests.util import weights, acts, check_close, random_blocks
+from tests.util import weights, acts, check_close, random_blocks, wbytes
 
 pytestmark = pytest.mark.gpu
 
-NAMES = list(le.TYPES)
-# Full-size weights of the configs: Q4_K / IQ2_XXS gate-up, Q6_K / IQ3_XXS down, Q8_0 head
+NAMES = list(le.MV_TYPES)
+# Full-size weights of the configs: Q4_K / IQ2_XXS gate-up, Q6_K / IQ3_XXS down, Q8_0 head; the other
+# formats at the gate/up shape
 FULL = {"Q4_K": (14336, 4096), "Q6_K": (4096, 14336), "Q8_0": (32000, 4096), "IQ2_XXS": (14336, 4096),
-        "IQ3_XXS": (4096, 14336)}
+        "IQ3_XXS": (4096, 14336), "Q4_0": (14336, 4096), "Q3_K": (14336, 4096), "Q5_K": (14336, 4096),
+        "IQ2_S": (14336, 4096)}
 
 
 def dev(a):
@@ -42,10 +46,10 @@ def absmag(ty, q, rows, cols, xs):
 @pytest.mark.parametrize("name", NAMES)
 @pytest.mark.parametrize("m", [17, 64, 512])
 def test_gemm_full_shapes(engine, name, m):
-    ty = le.TYPES[name]
+    ty = le.MV_TYPES[name]
     rows, cols = FULL[name]
     print("gemm full", name, rows, cols, m, flush=True)
-    q, _ = weights(ty, rows, cols, seed=40 + ty)
+    q = wbytes(ty, rows, cols, seed=40 + ty)
     xs = np.stack([acts(cols, 7000 + t) for t in range(m)])
     got = run_gemm(engine, ty, q, xs, rows, cols)
     want = oracle.matmat(ty, q, rows, cols, xs)
@@ -64,11 +68,11 @@ def test_gemm_tiles_and_slices(fresh_engine, name, cfg, rows, cols, m, ks):
     engine.set_option("gq_min_m", 1)
     engine.set_option("gm_min_m", 1)
     engine.set_option("gm_mh", 0)
-    ty = le.TYPES[name]
+    ty = le.MV_TYPES[name]
     if (cols // 256) % max(ks, 1):
         pytest.skip("K slices must divide the super-blocks")
     print("gemm tiles", name, cfg, rows, cols, m, ks, flush=True)
-    q, _ = weights(ty, rows, cols, seed=rows + m + ty)
+    q = wbytes(ty, rows, cols, seed=rows + m + ty)
     xs = np.stack([acts(cols, 8000 + t) for t in range(m)])
     got = run_gemm(engine, ty, q, xs, rows, cols)
     want = oracle.matmat(ty, q, rows, cols, xs)
@@ -80,7 +84,7 @@ def test_gemm_tiles_and_slices(fresh_engine, name, cfg, rows, cols, m, ks):
 def test_gemm_random_blocks(engine, name, m):
     """Arbitrary block bytes with bounded finite scales: every 6-bit scale/min code, negative Q6_K
     sub-block scales, every IQ grid index and sign pattern, on the vector and matrix-core paths."""
-    ty = le.TYPES[name]
+    ty = le.MV_TYPES[name]
     rows, cols = 384, 2048
     print("gemm random blocks", name, m, flush=True)
     q = random_blocks(ty, rows, cols, seed=11 * ty + m)
@@ -100,10 +104,10 @@ def test_gemm_activation_magnitudes(engine, name, m):
     if m < 9 and name != "Q4_K":
         pytest.skip("below 9 tokens the other types run on the vector kernels (per-block int8 images, "
                     "no fp16 range); their offset form leaves 2^-15-level residues where sum|wx| is 0")
-    ty = le.TYPES[name]
+    ty = le.MV_TYPES[name]
     rows, cols = 256, 1024
     zt, st = (3, 7) if m > 7 else (1, m - 1)
-    q, _ = weights(ty, rows, cols, seed=5 + ty)
+    q = wbytes(ty, rows, cols, seed=5 + ty)
     xs = np.stack([acts(cols, 9500 + t) for t in range(m)])
     scales = np.float32(10.0) ** np.linspace(-6, 6, m).astype(np.float32)
     xs = (xs * scales[:, None]).astype(np.float32)
@@ -129,12 +133,12 @@ def test_gemm_slice_sums(fresh_engine, name, rows, cols, m, ks):
     pass, slice order fixed) and with the minimal one (atomic adds into y): both meet the oracle
     bar, and the summed form gives the same bits on a second call."""
     import torch
-    ty = le.TYPES[name]
+    ty = le.MV_TYPES[name]
     fresh_engine.set_option("gq_ksplit", ks)
     if name == "Q4_K":
         fresh_engine.set_option("gm_min_m", 17)
         fresh_engine.set_option("gm_mh", 0)
-    q, _ = weights(ty, rows, cols, seed=ks + m)
+    q = wbytes(ty, rows, cols, seed=ks + m)
     xs = acts(m * cols, seed=rows).reshape(m, cols)
     want = oracle.matmat(ty, q, rows, cols, xs)
     mag = absmag(ty, q, rows, cols, xs)
@@ -152,3 +156,27 @@ def test_gemm_slice_sums(fresh_engine, name, rows, cols, m, ks):
         outs.append(y.cpu().numpy())
         check_close(outs[-1], want, mag)
     assert np.array_equal(outs[0].view(np.uint32), outs[1].view(np.uint32))
+
+
+@pytest.mark.parametrize("name", ["Q8_0", "Q4_0"])
+@pytest.mark.parametrize("m", [17, 130])
+def test_gemm_per_block_scale_range(engine, name, m):
+    """Q8_0 / Q4_0 carry a scale per 32 values inside their fp16 codes: blocks with |d| from 2^-20
+    to 3e4 in one row (fp16 scales up to the top of its range, and codes that would leave it under
+    a fixed multiplier) and a row of all-zero scales stay within the parity bar."""
+    ty = le.MV_TYPES[name]
+    rows, cols = 200, 2048
+    q = random_blocks(ty, rows, cols, seed=300 + m)
+    bb = 34 if ty == le.Q8_0 else 18
+    blk = q.reshape(rows, -1, bb)
+    rng = np.random.default_rng(m)
+    mag = np.float32(2.0) ** rng.uniform(-20, np.log2(3.0e4), size=blk.shape[:2]).astype(np.float32)
+    d = (mag * rng.choice([-1, 1], size=blk.shape[:2])).astype(np.float16)
+    d[5] = 0
+    blk[:, :, 0:2] = d.view(np.uint8).reshape(rows, -1, 2)
+    xs = np.stack([acts(cols, 9100 + t) for t in range(m)])
+    print("gemm scale range", name, m, flush=True)
+    got = run_gemm(engine, ty, q, xs, rows, cols)
+    want = oracle.matmat(ty, q, rows, cols, xs)
+    assert np.all(got[:, 5] == 0.0)
+    check_close(got, want, absmag(ty, q, rows, cols, xs))

@@ -6,7 +6,7 @@ import pytest
 
 import lastengine_amd as le
 import oracle
-from tests.util import weights, acts, check_close
+from tests.util import weights, acts, check_close, wbytes
 
 pytestmark = pytest.mark.gpu
 
@@ -28,15 +28,15 @@ def grouping(counts, n_src, seed):
     return off, in_idx, out_idx
 
 
-@pytest.mark.parametrize("name", list(le.TYPES))
+@pytest.mark.parametrize("name", list(le.MV_TYPES))
 @pytest.mark.parametrize("counts", [(0, 5, 300, 17, 1, 128, 64, 40), (3, 3, 3)])
 @pytest.mark.parametrize("tables", [False, True])
 def test_mm_grouped(engine, name, counts, tables):
     import torch
-    ty = le.TYPES[name]
+    ty = le.MV_TYPES[name]
     nslot, rows, cols, n_src = len(counts), 320, 1024, 200
     print("mm_grouped", name, counts, tables, flush=True)
-    q, _ = weights(ty, nslot * rows, cols, seed=60 + ty)
+    q = wbytes(ty, nslot * rows, cols, seed=60 + ty)
     xs = np.stack([acts(cols, 7700 + t) for t in range(n_src)])
     off, in_idx, out_idx = grouping(counts, n_src, seed=ty + len(counts))
     npair = int(off[-1])

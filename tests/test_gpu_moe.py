@@ -4,7 +4,7 @@ import pytest
 
 import lastengine_amd as le
 import oracle
-from tests.util import weights, acts, check_close, random_blocks
+from tests.util import weights, acts, check_close, random_blocks, wbytes
 
 pytestmark = pytest.mark.gpu
 
@@ -40,9 +40,9 @@ def run(engine, tg, td, n_exp, k, hidden, ff, n_tok, seed, lg=None, rand=False, 
         u = random_blocks(tg, n_exp * ff, hidden, seed + 1)
         d = random_blocks(td, n_exp * hidden, ff, seed + 2)
     else:
-        g, _ = weights(tg, n_exp * ff, hidden, seed)
-        u, _ = weights(tg, n_exp * ff, hidden, seed + 1)
-        d, _ = weights(td, n_exp * hidden, ff, seed + 2)
+        g = wbytes(tg, n_exp * ff, hidden, seed)
+        u = wbytes(tg, n_exp * ff, hidden, seed + 1)
+        d = wbytes(td, n_exp * hidden, ff, seed + 2)
     h = acts(n_tok * hidden, seed + 3).reshape(n_tok, hidden)
     if lg is None:
         lg = acts(n_tok * n_exp, seed + 4).reshape(n_tok, n_exp)
@@ -65,6 +65,16 @@ def test_moe_small(engine, n_tok):
 @pytest.mark.parametrize("tg,td", [(le.Q8_0, le.Q8_0), (le.IQ2_XXS, le.IQ3_XXS), (le.Q4_K, le.Q4_K)])
 def test_moe_type_combos(engine, tg, td):
     run(engine, tg, td, 8, 2, 512, 256, 2, seed=40 + tg)
+
+
+@pytest.mark.parametrize("tg,td", [(le.Q5_K, le.Q3_K), (le.Q4_0, le.Q4_0), (le.IQ2_S, le.Q5_K), (le.Q3_K, le.Q6_K),
+                                   (le.Q4_K, le.Q5_K), (le.Q6_K, le.Q8_0)])
+@pytest.mark.parametrize("n_tok", [1, 9, 70])
+def test_moe_grouped_type_pairs(engine, tg, td, n_tok):
+    """Type pairs without decode-shaped kernels (every pair of the nine types that the decode
+    kernels do not take) run the grouped form at any token count."""
+    print("moe type pair", tg, td, n_tok, flush=True)
+    run(engine, tg, td, 16, 4, 512, 256, n_tok, seed=500 + tg + td + n_tok)
 
 
 @pytest.mark.parametrize("n_tok", [1, 8])

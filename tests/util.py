@@ -15,6 +15,14 @@ def weights(ty, rows, cols, seed, std=0.02):
     return le.quantize_rows(ty, src), src
 
 
+def wbytes(ty, rows, cols, seed):
+    """Weight bytes for a type: seeded N(0, 0.02) weights through the product quantizer where it has
+    one (the five config types), else arbitrary block bytes with bounded finite scales."""
+    if ty in le.TYPES.values():
+        return weights(ty, rows, cols, seed)[0]
+    return random_blocks(ty, rows, cols, seed)
+
+
 def acts(n, seed):
     return le.fill_normal(n, seed)
 
