@@ -220,6 +220,23 @@ int le_gguf_find(const le_gguf *g, const char *name) {
     return it == g->by_name.end() ? -1 : it->second;
 }
 
+/* Bytes of tensor t (product of its dims over the block geometry), with every product and the
+ * end of its data (data_start + offset + bytes) checked against overflow and the file size.
+ * Returns false when the tensor does not fit the file or its type has no block geometry. */
+static bool tensor_extent(const le_gguf *g, const Tensor &t, uint64_t *bytes) {
+    uint64_t n = 1;
+    for (uint64_t d : t.dims)
+        if (__builtin_mul_overflow(n, d, &n)) return false;
+    int v = 0, b = 0;
+    if (!le_block_geometry((int)t.type, &v, &b) || n % (uint64_t)v) return false;
+    uint64_t nb = 0, start = 0, end = 0;
+    if (__builtin_mul_overflow(n / (uint64_t)v, (uint64_t)b, &nb) || __builtin_add_overflow(g->data_start, t.offset, &start) ||
+        __builtin_add_overflow(start, nb, &end) || end > g->file_size)
+        return false;
+    *bytes = nb;
+    return true;
+}
+
 int le_gguf_tensor_info(const le_gguf *g, int i, const char **name, int *ggml_type, int *n_dims, uint64_t *dims,
                         uint64_t *offset, uint64_t *nbytes) {
     if (!g || i < 0 || i >= (int)g->tensors.size()) return LE_ERR_ARG;
@@ -230,13 +247,14 @@ int le_gguf_tensor_info(const le_gguf *g, int i, const char **name, int *ggml_ty
     if (dims)
         for (size_t d = 0; d < 8; d++) dims[d] = d < t.dims.size() ? t.dims[d] : 1;
     if (offset) *offset = g->data_start + t.offset;
-    if (nbytes) {
-        uint64_t n = 1;
-        for (uint64_t d : t.dims) n *= d;
-        int v = 0, b = 0;
-        *nbytes = le_block_geometry((int)t.type, &v, &b) && n % (uint64_t)v == 0 ? n / (uint64_t)v * (uint64_t)b : 0;
-    }
-    return LE_OK;
+    /* a type without block geometry reports 0 bytes; a tensor whose size overflows or whose data
+     * runs past the end of the file is an error (its name, type and dims are still reported) */
+    int v = 0, b = 0;
+    uint64_t nb = 0;
+    const bool known = le_block_geometry((int)t.type, &v, &b) != 0;
+    const bool fits = tensor_extent(g, t, &nb);
+    if (nbytes) *nbytes = fits ? nb : 0;
+    return !known || fits ? LE_OK : LE_ERR_SHAPE;
 }
 
 /* Expert e's slab of a 3D tensor (dims [cols, rows, n_expert]): cpu_ref::expert_parts,
@@ -250,7 +268,12 @@ int le_gguf_expert_slab(const le_gguf *g, const char *name, int expert, uint64_t
     if (t.dims.empty() || t.dims[0] % (uint64_t)v) return LE_ERR_SHAPE;
     const uint64_t rows = t.dims.size() > 1 ? t.dims[1] : 1, nexp = t.dims.size() > 2 ? t.dims[2] : 1;
     if (expert < 0 || (uint64_t)expert >= nexp) return LE_ERR_ARG;
-    const uint64_t slab = t.dims[0] / (uint64_t)v * (uint64_t)b * rows;
+    uint64_t total = 0, slab = 0;
+    /* the whole tensor inside the file (overflow-checked), so every slab of it is too */
+    if (!tensor_extent(g, t, &total)) return LE_ERR_SHAPE;
+    if (__builtin_mul_overflow(t.dims[0] / (uint64_t)v * (uint64_t)b, rows, &slab) || slab > total ||
+        (uint64_t)expert * slab + slab > total)
+        return LE_ERR_SHAPE;
     if (offset) *offset = g->data_start + t.offset + (uint64_t)expert * slab;
     if (bytes) *bytes = slab;
     return LE_OK;

@@ -52,7 +52,6 @@ struct MoeArgs {
     float *w_out;
     int n_tok, n_exp, k, hidden, ff;
     unsigned int spin_limit;
-    unsigned long long epoch;
     void *bar;
     const void *const *gptr, *const *uptr, *const *dptr;
 };
@@ -60,8 +59,6 @@ struct MoeArgs {
  * flag per block of the one-launch kernel, LE_MOE_MAXGRID = 1024 blocks). */
 constexpr size_t kMoeBarBytes = 128 + 8 * 1024;
 #define LE_MOE_MAX_TOK 65536
-/* Epochs of the one-launch MoE barrier: unique per launch within the process. */
-std::atomic<unsigned long long> g_moe_epoch{0};
 int table_bytes(int ty) {
     if (ty == LE_TYPE_IQ2_XXS) return 4 * (256 + 512);
     if (ty == LE_TYPE_IQ3_XXS) return 4 * (256 + 256);
@@ -275,7 +272,13 @@ int mq_launch(le_ctx *c, int ty, const void *const *ptrs, const void *w, const f
         for (const int w : {16, 14, 12})
             if ((nsb / 2) % w == 0) { NWs = w; P = 2; break; }
     while (NWs > 1 && nsb % (NWs * P)) NWs >>= 1;
-    if (c->ms && nsb % (NWs * P) == 0) {
+    /* only some (P, NWs) pairs are instantiated (e.g. no P = 4 with 8 waves): lower P until the
+     * kernel exists, else fall through to the unstaged or vector kernels */
+    while (c->ms && P > 1 && !c->fn(std::string("le_ms_") + std::to_string(ty) + "_p" + std::to_string(P) + "_w" +
+                                    std::to_string(NWs) + (xq8 ? "_q8" : "")))
+        P >>= 1;
+    if (c->ms && nsb % (NWs * P) == 0 &&
+        c->fn(std::string("le_ms_") + std::to_string(ty) + "_p" + std::to_string(P) + "_w" + std::to_string(NWs) + (xq8 ? "_q8" : ""))) {
         const int cps = ty == LE_TYPE_Q6_K ? 14 : ty == LE_TYPE_IQ2_XXS ? 5 : ty == LE_TYPE_IQ3_XXS ? 7 : ty == LE_TYPE_Q8_0 ? 17 : ty == LE_TYPE_Q5_K ? 11 : ty == LE_TYPE_Q3_K ? 7 : ty == LE_TYPE_IQ2_S ? 6 : 9;
         const int cpr = cps * P + 1, ni = (16 * cpr + 63) / 64;
         snprintf(name, sizeof name, "le_ms_%d_p%d_w%d%s", ty, P, NWs, xq8 ? "_q8" : "");
@@ -859,7 +862,7 @@ static int moe_layer_impl(le_ctx *c, int ty_gate, int ty_up, int ty_down, const 
     const size_t lds = (size_t)8 * xtok_bytes(hidden);
     if (lds + 16384 > c->lds_limit) return c->fail(LE_ERR_SHAPE, "hidden=%d exceeds the LDS budget", hidden);
     MoeArgs a{gate, up, down, logits, h, out, (char *)ws + kMoeBarBytes, idx_out, w_out, n_tok, n_exp, k, hidden, ff,
-              c->moe_spin_limit, ++g_moe_epoch, ws, gptr, uptr, dptr};
+              c->moe_spin_limit, ws, gptr, uptr, dptr};
     void *args[] = {&a};
     char name[64];
     const int nsb = hidden / 256, g8 = nsb % 8 == 0;

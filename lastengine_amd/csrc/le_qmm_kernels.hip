@@ -1798,7 +1798,6 @@ struct MoeArgs {
     float *w_out;
     int n_tok, n_exp, k, hidden, ff;
     unsigned int spin_limit;  /* bounded waits of the one-launch barrier; 0 makes it fail */
-    unsigned long long epoch; /* unique per launch (process-wide counter on the host) */
     u8 *bar;                  /* the caller's workspace start: barrier area (LE_MOE_BAR_BYTES) */
     /* per-expert weight pointers (an expert-cache arena), or null: expert e's slab at
      * e * rows * row_bytes of gate / up / down */
@@ -2898,8 +2897,11 @@ __device__ __forceinline__ void moe_dnm_body(const MoeArgs &a) {
  *
  * Barrier. Its state lives in the caller's workspace (so launches with different workspaces never
  * share it): per block an arrival flag, one generation word and a status word. Each launch
- * carries an epoch that no earlier launch used, so a flag or generation left by an earlier launch
- * (or a late block of a launch that gave up) never matches. Block 0 polls every flag and then
+ * takes its epoch from the device: every block reads the generation word before it arrives, and
+ * nothing changes that word until every block has arrived, so all blocks read the same value g
+ * and use g + 1 (top bit cleared). Launches on one workspace therefore count up one by one,
+ * also when a HIP graph replays the same kernel arguments, and a flag or generation left by an
+ * earlier launch (or a late block of a launch that gave up) never matches. Block 0 polls every flag and then
  * publishes either the epoch or, if a wait gave up, the epoch with the top bit set; every other
  * block waits for one of the two. Every wait is bounded (spin_limit polls); a block whose wait
  * gave up, or that sees the failure generation, sets the status word (to LE_MOE_BAR_FAILED, a
@@ -2919,9 +2921,12 @@ __device__ __forceinline__ bool moe_grid_barrier(const MoeArgs &a, unsigned int 
     unsigned int *status = (unsigned int *)(a.bar + LE_MOE_BAR_STATUS);
     unsigned long long *gen = (unsigned long long *)(a.bar + LE_MOE_BAR_GEN);
     unsigned long long *flag = (unsigned long long *)(a.bar + LE_MOE_BAR_FLAGS);
-    const unsigned long long ep = a.epoch, fail = a.epoch | (1ull << 63);
+    __shared__ unsigned long long ep_s;
+    if (threadIdx.x == 0) /* before this block's arrival: no block can publish a new generation yet */
+        ep_s = (__hip_atomic_load(gen, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) & ~(1ull << 63)) + 1;
     __builtin_amdgcn_s_waitcnt(0x0F70); /* vmcnt(0): this thread's coherent stores have completed */
     __syncthreads();
+    const unsigned long long ep = ep_s & ~(1ull << 63), fail = ep | (1ull << 63);
     if (threadIdx.x == 0) {
         ok_s = a.spin_limit > 0; /* a zero limit is the host's way to make the barrier fail */
         /* the data other blocks read was stored device-coherently and has completed (the block

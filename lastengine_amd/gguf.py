@@ -46,10 +46,11 @@ def _L():
 
 
 class TensorInfo:
-    __slots__ = ("name", "dims", "ggml_type", "offset", "nbytes")
+    __slots__ = ("name", "dims", "ggml_type", "offset", "nbytes", "fits")
 
-    def __init__(self, name, dims, ggml_type, offset, nbytes):
+    def __init__(self, name, dims, ggml_type, offset, nbytes, fits=True):
         self.name, self.dims, self.ggml_type, self.offset, self.nbytes = name, dims, ggml_type, offset, nbytes
+        self.fits = fits
 
     def __repr__(self):
         return "TensorInfo(%r, dims=%r, type=%d, offset=%d, nbytes=%d)" % (
@@ -87,9 +88,11 @@ class Gguf:
         dims, off, nb = (ctypes.c_uint64 * 8)(), ctypes.c_uint64(), ctypes.c_uint64()
         rc = _L().le_gguf_tensor_info(self._g, i, ctypes.byref(name), ctypes.byref(ty), ctypes.byref(nd), dims,
                                       ctypes.byref(off), ctypes.byref(nb))
-        if rc:
+        if rc and rc != -3:
             raise LeError(rc)
-        return TensorInfo(name.value.decode(), [int(dims[d]) for d in range(nd.value)], ty.value, off.value, nb.value)
+        t = TensorInfo(name.value.decode(), [int(dims[d]) for d in range(nd.value)], ty.value, off.value, nb.value)
+        t.fits = rc == 0  # -3: its size overflows or its data runs past the end of the file
+        return t
 
     def find(self, name):
         i = _L().le_gguf_find(self._g, name.encode())
@@ -134,6 +137,8 @@ class Gguf:
         t = self.find(name)
         if t is None:
             raise LeError(-1, "missing tensor %s" % name)
+        if not t.fits:
+            raise LeError(-3, "tensor %s does not fit the file" % name)
         return self.read(t.offset, t.nbytes)
 
     def expert_slab(self, name, expert):

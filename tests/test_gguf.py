@@ -128,3 +128,27 @@ def test_v2_and_default_alignment(tmp_path):
                    alignment=32, version=2)
     g = Gguf(str(p))
     assert g.version == 2 and g.data_start % 32 == 0 and g.tensors[0].offset == offs[0]
+
+
+def test_tensor_extent_checks(tmp_path):
+    """A tensor whose dims product overflows 64 bits, or whose data would run past the end of the
+    file, is reported as an error (LE_ERR_SHAPE) by le_gguf_tensor_info and le_gguf_expert_slab
+    instead of a wrapped size or an out-of-file offset; the other tensors stay readable."""
+    ok = np.arange(34 * 2, dtype=np.uint8)
+    tensors = [("ok", [64], le.Q8_0, ok),
+               ("wrap", [1 << 40, 1 << 40, 1 << 20], le.Q8_0, ok[:34]),   # 2^100 values: the product wraps
+               ("past_end", [32, 1000, 4], le.Q8_0, ok[:34])]             # 136000 bytes claimed, 34 present
+    p = tmp_path / "bad.gguf"
+    W.write(str(p), [("general.architecture", W.STR, "llama")], tensors, alignment=32)
+    g = Gguf(str(p))
+    assert g.find("ok").fits and g.find("ok").nbytes == 68
+    assert np.array_equal(g.tensor_bytes("ok"), ok)
+    for name in ("wrap", "past_end"):
+        t = g.find(name)
+        assert not t.fits and t.nbytes == 0
+        with pytest.raises(le.LeError) as e:
+            g.tensor_bytes(name)
+        assert e.value.code == -3
+        with pytest.raises(le.LeError) as e:
+            g.expert_slab(name, 0)
+        assert e.value.code == -3

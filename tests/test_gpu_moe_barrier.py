@@ -73,3 +73,37 @@ def test_barrier_separate_workspaces(fresh_engine):
             got = call(engine, *args, ws)
             check_close(got, want, mag)
             engine.moe_check(ws)
+
+
+def test_barrier_graph_replays(fresh_engine):
+    """One captured one-launch layer (the only launch on its workspace), replayed with new token
+    activations copied in between: each replay's launch takes a fresh epoch from the workspace,
+    so its barrier waits for this replay's gate/up images (an epoch fixed in the kernel arguments
+    would let the second replay's barrier pass at once and read the previous replay's images)."""
+    import torch
+    engine = fresh_engine
+    n_tok = 4
+    g, u, d, h0, lg = inputs(n_tok, 700)
+    dg, du, dd, dl = dev(g), dev(u), dev(d), dev(lg)
+    dh = dev(h0)
+    ws = torch.zeros(engine.moe_workspace_size(n_tok, K, FF), dtype=torch.uint8, device="cuda")
+    out = torch.empty(n_tok, HIDDEN, dtype=torch.float32, device="cuda")
+    s = torch.cuda.Stream()
+    with torch.cuda.stream(s):
+        engine.moe(TG, TG, TD, dg, du, dd, N_EXP, K, HIDDEN, FF, dl, dh, n_tok, out, ws=ws, stream=s)
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph, stream=s):
+        engine.moe(TG, TG, TD, dg, du, dd, N_EXP, K, HIDDEN, FF, dl, dh, n_tok, out, ws=ws, stream=s)
+    torch.cuda.synchronize()
+    for rep in range(4):
+        h = acts(n_tok * HIDDEN, 710 + rep).reshape(n_tok, HIDDEN)
+        dh.copy_(torch.from_numpy(h))  # eager work between the replays
+        out.fill_(7.0)
+        torch.cuda.synchronize()
+        print("moe barrier: graph replay", rep, flush=True)
+        graph.replay()
+        torch.cuda.synchronize()
+        engine.moe_check(ws)
+        want, _, _, mag = reference(TG, TD, g, u, d, N_EXP, K, HIDDEN, FF, h, lg)
+        check_close(out.cpu().numpy(), want, mag)

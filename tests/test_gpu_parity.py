@@ -344,3 +344,21 @@ def test_matvec_launch_options(fresh_engine, name, opts):
     engine.mv(ty, dev(q), dev(x), y, rows, cols)
     sync()
     check_close(y.cpu().numpy(), oracle.matvec(ty, q, rows, cols, x), absmag(ty, q, rows, cols, x)[0])
+
+
+@pytest.mark.parametrize("name,opt", [("Q4_K", "ms_p"), ("Q8_0", "ms_p80"), ("IQ2_XXS", "ms_piq")])
+@pytest.mark.parametrize("rows,cols", [(64, 8192), (4000, 8192)])
+def test_staged_shape_not_instantiated(fresh_engine, name, opt, rows, cols):
+    """Four super-blocks per item: with few row tiles the waves double to 8, and (P = 4, 8 waves)
+    has no kernel; the launch lowers P to an instantiated shape instead of failing."""
+    import torch
+    ty = le.TYPES[name]
+    fresh_engine.set_option(opt, 4)
+    q, _ = weights(ty, rows, cols, seed=rows + ty)
+    x = acts(cols, 3 + rows)
+    y = torch.full((rows,), float("nan"), device="cuda")
+    print("staged shape fallback", name, opt, rows, cols, flush=True)
+    fresh_engine.mv(ty, dev(q), dev(x), y, rows, cols)
+    sync()
+    want = oracle.matvec(ty, q, rows, cols, x)
+    check_close(y.cpu().numpy(), want, absmag(ty, q, rows, cols, x)[0])
