@@ -63,6 +63,21 @@ __device__ __forceinline__ uint2 ldg8u(const u8 *p) {
 __device__ __forceinline__ u32 ldg4u(const u8 *p) { return *(const LE_GLOBAL le_u32_a2 *)p; }
 __device__ __forceinline__ u32 ldg2(const u8 *p) { return *(const LE_GLOBAL uint16_t *)p; }
 
+/* Sum over lanes l, l ^ 16, l ^ 32 and l ^ 48 (the four 16-lane rows of the wave), in every lane:
+ * xor 16 by a swizzle, xor 32 by the gfx950 permlane32 swap on the VALU (no LDS round trip for
+ * that half): (v_l + v_l^16) + (same)^32, the same bits in every lane as a swizzle/shuffle
+ * butterfly (each step adds the same two values). */
+__device__ __forceinline__ float row4_sum(float v) {
+    const float s = v + __builtin_bit_cast(float, __builtin_amdgcn_ds_swizzle(__builtin_bit_cast(int, v), 0x401F));
+    /* the swap's operands as two distinct values (the compiler would otherwise treat a swap of a
+     * value with itself as a no-op); after it p[0] holds s of lanes 0-31 in both halves, p[1] s of
+     * lanes 32-63 */
+    u32 hi;
+    __asm__("v_mov_b32 %0, %1" : "=v"(hi) : "v"(s));
+    const auto p = __builtin_amdgcn_permlane32_swap(__builtin_bit_cast(u32, s), hi, false, false);
+    return __builtin_bit_cast(float, (u32)p[0]) + __builtin_bit_cast(float, (u32)p[1]);
+}
+
 __device__ __forceinline__ float h2f(u32 bits16) {
     return (float)__builtin_bit_cast(_Float16, (uint16_t)bits16);
 }

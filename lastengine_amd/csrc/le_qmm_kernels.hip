@@ -766,8 +766,7 @@ __device__ __forceinline__ void mq_q4k_body(const MvArgs &a) {
             }
         }
         /* sum the four slices of row n, then the NW waves */
-        y += __builtin_bit_cast(float, __builtin_amdgcn_ds_swizzle(__builtin_bit_cast(int, y), 0x401F));
-        y += __shfl_xor(y, 32);
+        y = row4_sum(y);
         if (lane < 16) red[wave * 16 + lane] = y;
         __syncthreads();
         if (wave == 0 && lane < 16) {
@@ -1166,8 +1165,7 @@ __device__ __forceinline__ void ms_q4k_body(const MvArgs &a) {
                 }
             }
         }
-        y += __builtin_bit_cast(float, __builtin_amdgcn_ds_swizzle(__builtin_bit_cast(int, y), 0x401F));
-        y += __shfl_xor(y, 32);
+        y = row4_sum(y);
         float *rp = red + par * (NW * 16);
         if (lane < 16) rp[wave * 16 + lane] = y;
         __builtin_amdgcn_s_waitcnt(0xC07F);
@@ -1357,8 +1355,7 @@ __device__ __forceinline__ void ms_q4k_t_body(const MvArgs &a) {
 #pragma unroll
         for (int t = 0; t < T; t++) {
             float v = y[t];
-            v += __builtin_bit_cast(float, __builtin_amdgcn_ds_swizzle(__builtin_bit_cast(int, v), 0x401F));
-            v += __shfl_xor(v, 32);
+            v = row4_sum(v);
             if (lane < 16) rp[(wave * T + t) * 16 + lane] = v;
         }
         __builtin_amdgcn_s_waitcnt(0xC07F);
@@ -1474,8 +1471,7 @@ __device__ __forceinline__ void ms_q6k_body(const MvArgs &a) {
                 }
             }
         }
-        y += __builtin_bit_cast(float, __builtin_amdgcn_ds_swizzle(__builtin_bit_cast(int, y), 0x401F));
-        y += __shfl_xor(y, 32);
+        y = row4_sum(y);
         float *rp = red + par * (NW * 16);
         if (lane < 16) rp[wave * 16 + lane] = y;
         __builtin_amdgcn_s_waitcnt(0xC07F);
@@ -1697,8 +1693,7 @@ __device__ __forceinline__ void ms_iq_body(const MvArgs &a) {
                 }
             }
         }
-        y += __builtin_bit_cast(float, __builtin_amdgcn_ds_swizzle(__builtin_bit_cast(int, y), 0x401F));
-        y += __shfl_xor(y, 32);
+        y = row4_sum(y);
         float *rp = red + par * (NW * 16);
         if (lane < 16) rp[wave * 16 + lane] = y;
         __builtin_amdgcn_s_waitcnt(0xC07F);
@@ -1817,6 +1812,15 @@ __device__ __forceinline__ const u8 *moe_w(const u8 *slab, const u8 *const *ptrs
 #define LE_MOE_MAXK 16
 #define LE_MOE_MAXEXP 256
 
+/* Block barrier for data exchanged through LDS only: waits for this wave's LDS (and scalar)
+ * operations, not for its global loads in flight (__syncthreads waits for those too). */
+__device__ __forceinline__ void moe_sync() {
+    __asm__ volatile("" ::: "memory");
+    __builtin_amdgcn_s_waitcnt(0xC07F);
+    __builtin_amdgcn_s_barrier();
+    __asm__ volatile("" ::: "memory");
+}
+
 /* LDS routing state shared by both kernels. */
 struct MoeRoute {
     int topi[LE_MOE_MAXTOK * LE_MOE_MAXK];
@@ -1824,7 +1828,15 @@ struct MoeRoute {
     unsigned long long mask[LE_MOE_MAXEXP];
     int grp_e[LE_MOE_MAXEXP];
     int U;
+#ifdef LE_MOE_TRACE
+    unsigned long long tr[8];
+#endif
 };
+#ifdef LE_MOE_TRACE
+#define MOE_RT(i) if (threadIdx.x == 0) R.tr[i] = __builtin_amdgcn_s_memrealtime()
+#else
+#define MOE_RT(i)
+#endif
 
 /* Wave-wide max / sum: DPP within 16-lane rows, then the four row results through readlane, so the
  * result is uniform (no LDS-routed shuffles on the routing critical path). */
@@ -1845,6 +1857,69 @@ __device__ __forceinline__ float wave_sum(float v) {
     const int b = __builtin_bit_cast(int, v);
     return (__builtin_bit_cast(float, __builtin_amdgcn_readlane(b, 0)) + __builtin_bit_cast(float, __builtin_amdgcn_readlane(b, 16))) +
            (__builtin_bit_cast(float, __builtin_amdgcn_readlane(b, 32)) + __builtin_bit_cast(float, __builtin_amdgcn_readlane(b, 48)));
+}
+
+/* Order-preserving 32-bit key of a float (-0 as +0, so the two tie as the float compare has
+ * them). */
+__device__ __forceinline__ u32 f2key(float v) {
+    const u32 b = __builtin_bit_cast(u32, v == 0.f ? 0.f : v);
+    return (b & 0x80000000u) ? ~b : (b | 0x80000000u);
+}
+/* One token, at most 128 experts, blocks of 8 waves: wave w compares experts 16 w .. 16 w + 15 */
+__device__ __forceinline__ bool moe_route_is_one(const MoeArgs &a) {
+    return a.n_tok == 1 && a.n_exp <= 128 && a.k <= 64 && blockDim.x == 512;
+}
+/* One token, at most 128 experts, every wave of the block: the rank of expert e (the number of
+ * experts before it in the stable descending sort of src/cpu_ref.rs:248) is counted directly.
+ * Wave w takes the logits of experts 16w .. 16w + 15 as scalars and compares each with the two
+ * experts of every lane (e = lane, lane + 64) through 64-bit keys (order-preserving logit bits
+ * above the inverted index, so "larger, or equal and lower index" is one compare); the waves'
+ * counts are added in LDS (rk[128], zero on entry). Then wave 0: rank < k selects, the selection is
+ * written in rank order, the weights are ex / sum(ex) with ex = exp(logit - top logit) summed in
+ * rank order (as the other paths), and the groups are the selected experts in ascending order
+ * (prefix counts of the two selection ballots). R.mask must be zero for every expert. */
+__device__ __forceinline__ unsigned long long moe_key2(float v, int e) {
+    return ((unsigned long long)f2key(v) << 32) | (u32)(0xFFFFFFFFu - (u32)e);
+}
+__device__ __forceinline__ void moe_route_one(const MoeArgs &a, MoeRoute &R, float *sx, int *rk, float lv0, float lv1,
+                                              const float (&lj)[16]) {
+    const int lane = threadIdx.x & 63, w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int e0 = lane, e1 = lane + 64;
+    const unsigned long long my0 = moe_key2(lv0, e0), my1 = moe_key2(lv1, e1);
+    const int j0 = 16 * w;
+    if (j0 < a.n_exp) {
+        int c0 = 0, c1 = 0;
+#pragma unroll
+        for (int i = 0; i < 16; i++) {
+            /* an expert past n_exp gets key 0, below every real key: it is never counted */
+            const unsigned long long kj = j0 + i < a.n_exp ? moe_key2(lj[i], j0 + i) : 0ull;
+            c0 += kj > my0;
+            c1 += kj > my1;
+        }
+        if (e0 < a.n_exp) atomicAdd(&rk[e0], c0);
+        if (e1 < a.n_exp) atomicAdd(&rk[e1], c1);
+    }
+    moe_sync();
+    if (threadIdx.x < 64) {
+        const int r0 = e0 < a.n_exp ? rk[e0] : 0x7FFFFFFF, r1 = e1 < a.n_exp ? rk[e1] : 0x7FFFFFFF;
+        const bool s0 = r0 < a.k, s1 = r1 < a.k;
+        if (s0) { R.topi[r0] = e0; sx[r0] = lv0; R.mask[e0] = 1ull; }
+        if (s1) { R.topi[r1] = e1; sx[r1] = lv1; R.mask[e1] = 1ull; }
+        const unsigned long long b0 = __ballot(s0), b1 = __ballot(s1);
+        const unsigned long long below = (1ull << lane) - 1ull;
+        if (s0) R.grp_e[__popcll(b0 & below)] = e0;
+        if (s1) R.grp_e[__popcll(b0) + __popcll(b1 & below)] = e1;
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+        __builtin_amdgcn_wave_barrier();
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+        const bool sel = lane < a.k;
+        const float v = sel ? sx[lane] : 0.f, top = sx[0];
+        const float ex = sel ? expf(v - top) : 0.f;
+        float tot = 0.f;
+        for (int r = 0; r < a.k; r++) tot += __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, ex), r));
+        if (sel) R.topw[lane] = ex / tot;
+        if (lane == 0) R.U = a.k;
+    }
 }
 
 /* All threads: route every token (one wave per token), then list the groups. Lane l holds
@@ -1896,7 +1971,7 @@ __device__ void moe_route(const MoeArgs &a, MoeRoute &R) {
         if (lane == 0)
             for (int r = 0; r < a.k; r++) R.topw[t * a.k + r] /= tot;
     }
-    __syncthreads();
+    moe_sync();
     /* expert masks from the top-k table (no atomics, no zeroing pass) */
     const int nsel = a.n_tok * a.k;
     for (int e = threadIdx.x; e < a.n_exp; e += blockDim.x) {
@@ -1905,7 +1980,7 @@ __device__ void moe_route(const MoeArgs &a, MoeRoute &R) {
             if (R.topi[i] == e) msk |= 1ull << (i / a.k);
         R.mask[e] = msk;
     }
-    __syncthreads();
+    moe_sync();
     if (wave == 0) {
         int base = 0;
         for (int c = 0; c < a.n_exp; c += 64) {
@@ -1917,7 +1992,7 @@ __device__ void moe_route(const MoeArgs &a, MoeRoute &R) {
         }
         if (lane == 0) R.U = base;
     }
-    __syncthreads();
+    moe_sync();
 }
 
 /* Parallel routing for the decode-shaped kernels (n_exp <= 256): one thread per (token, expert).
@@ -1953,6 +2028,7 @@ __device__ __forceinline__ MoeRouteGeom moe_route_geom(const MoeArgs &a) {
 #define MOE_LPASS 4
 struct MoeLogits {
     float v[MOE_LPASS];
+    float j[16]; /* single-token ranking: this wave's 16 compared logits (scalar loads) */
 };
 /* 2..(waves) tokens, at most 256 experts: one wave selects each token's top-k (k rounds of a
  * wave-wide max; lane l holds experts l*per .. l*per+per-1) instead of ranking every key. One
@@ -1962,6 +2038,17 @@ __device__ __forceinline__ bool moe_route_by_wave(const MoeArgs &a) {
 }
 __device__ __forceinline__ MoeLogits moe_route_load(const MoeArgs &a) {
     MoeLogits L;
+    if (moe_route_is_one(a)) { /* every lane: experts lane and lane + 64 */
+        const int lane = threadIdx.x & 63;
+        L.v[0] = a.logits[min(lane, a.n_exp - 1)];
+        L.v[1] = a.logits[min(lane + 64, a.n_exp - 1)];
+        L.v[2] = L.v[3] = 0.f;
+        const int j0 = 16 * __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+#pragma unroll
+        for (int i = 0; i < 16; i++) /* wave-uniform, read-only for the kernel: scalar loads */
+            L.j[i] = ((const __attribute__((address_space(4))) float *)a.logits)[min(j0 + i, a.n_exp - 1)];
+        return L;
+    }
     if (moe_route_by_wave(a)) {
         const int lane = threadIdx.x & 63, t = threadIdx.x >> 6, per = (a.n_exp + 63) >> 6;
 #pragma unroll
@@ -2012,8 +2099,19 @@ __device__ __forceinline__ void moe_route_par(const MoeArgs &a, MoeRoute &R, uns
         }
     };
     const int t1 = threadIdx.x / (tpt * C), e1 = (threadIdx.x / C) % tpt;
+    if (moe_route_is_one(a)) {
+        int *rk = (int *)lv;
+        for (int e = threadIdx.x; e < 128; e += blockDim.x) rk[e] = 0;
+        moe_sync(); /* the mask and count clears above, before the counts and the selection */
+        MOE_RT(1);
+        moe_route_one(a, R, sx, rk, L.v[0], L.v[1], L.j);
+        MOE_RT(2);
+        moe_sync();
+        return;
+    }
     if (moe_route_by_wave(a)) {
-        __syncthreads(); /* the mask clear above, before the atomics */
+        moe_sync(); /* the mask clear above, before the atomics */
+        MOE_RT(1);
         const int lane = threadIdx.x & 63, t = threadIdx.x >> 6, per = (a.n_exp + 63) >> 6;
         if (t < a.n_tok) {
             /* k rounds of a wave-wide max with no branch: round r's winner (the lowest lane among
@@ -2047,6 +2145,7 @@ __device__ __forceinline__ void moe_route_par(const MoeArgs &a, MoeRoute &R, uns
                 atomicOr(&R.mask[my_e], 1ull << t);
             }
         }
+        MOE_RT(2);
         if (a.n_tok == 1) {
             /* one token: wave 0 holds the k selections; it writes the renormalised weights and
              * the groups (the k experts in ascending order) itself, with no further LDS pass */
@@ -2069,10 +2168,10 @@ __device__ __forceinline__ void moe_route_par(const MoeArgs &a, MoeRoute &R, uns
                 }
                 if (lane == 0) R.U = a.k;
             }
-            __syncthreads();
+                moe_sync();
             return;
         }
-        __syncthreads();
+        moe_sync();
     } else if (g.npass <= MOE_LPASS) {
         /* every pass's keys in LDS, one barrier, every pass ranked, one barrier */
 #pragma unroll
@@ -2080,14 +2179,16 @@ __device__ __forceinline__ void moe_route_par(const MoeArgs &a, MoeRoute &R, uns
             const int t = p * tpp + t1;
             if (p < g.npass && t < a.n_tok && e1 < a.n_exp && c == 0) lv[t * a.n_exp + e1] = moe_key(L.v[p], e1);
         }
-        __syncthreads();
+        moe_sync();
 #pragma unroll
         for (int p = 0; p < MOE_LPASS; p++) {
             if (p >= g.npass) break;
             const int t = p * tpp + t1;
             rank_of(t, e1, L.v[p], moe_key(L.v[p], e1));
         }
-        __syncthreads();
+        MOE_RT(1);
+        moe_sync();
+        MOE_RT(2);
     } else {
         for (int t0 = 0; t0 < a.n_tok; t0 += tpp) {
             const int t = t0 + t1;
@@ -2095,9 +2196,9 @@ __device__ __forceinline__ void moe_route_par(const MoeArgs &a, MoeRoute &R, uns
             const float v = ok ? a.logits[(size_t)t * a.n_exp + e1] : 0.f;
             const unsigned long long key = moe_key(v, e1);
             if (ok && c == 0) lv[t * a.n_exp + e1] = key;
-            __syncthreads();
+            moe_sync();
             rank_of(t, e1, v, key);
-            __syncthreads();
+            moe_sync();
         }
     }
     const int lane = threadIdx.x & 63, nsel = a.n_tok * a.k;
@@ -2126,7 +2227,7 @@ __device__ __forceinline__ void moe_route_par(const MoeArgs &a, MoeRoute &R, uns
             R.topw[i] = mine / tot;
         }
     }
-    __syncthreads();
+    moe_sync();
 }
 
 /* Member i (token order) of group z: its token, pair index and routing weight. */
@@ -2630,6 +2731,19 @@ __device__ void moe_down_fast(const MoeArgs &a) {
  * members' images are copied into the wave's LDS, and each member's dot is weighted and added to
  * its token's rows. The waves' sums are added in a fixed order. */
 #define LE_MOE_IMG(K) ((K) / 256 * 608) /* bytes of one token's MFMA activation image */
+#ifdef LE_MOE_TRACE /* timing builds only: per-block timestamps after the workspace's first MiB */
+#define MOE_T(i) (tr_[i] = __builtin_amdgcn_s_memrealtime())
+#define MOE_T_DECL unsigned long long tr_[8] = {0, 0, 0, 0, 0, 0, 0, 0}
+#define MOE_T_OUT(base)                                                                              \
+    if (threadIdx.x == 0) {                                                                          \
+        unsigned long long *o_ = (unsigned long long *)(a.bar + (1 << 20)) + (base) + 8 * (blockIdx.x + gridDim.x * blockIdx.y); \
+        for (int i_ = 0; i_ < 8; i_++) o_[i_] = tr_[i_];                                             \
+    }
+#else
+#define MOE_T(i)
+#define MOE_T_DECL
+#define MOE_T_OUT(base)
+#endif
 
 /* LDS layout of the staged MoE kernels: the routing keys (needed only until routing is done)
  * share their bytes with the weight staging that follows. */
@@ -2650,6 +2764,8 @@ __device__ __forceinline__ void moe_gum_body(const MoeArgs &a) {
     uint4 *img = smem;                                          /* [n_tok][image] */
     uint4 *stg = smem + LE_MOE_FAST_TOK * LE_MOE_IMG(K) / 16;  /* [NW][NI*64] staging; routing keys first */
     uint4 *wb = stg + wave * NI * 64;
+    MOE_T_DECL;
+    MOE_T(0);
     const MoeLogits lgt = moe_route_load(a); /* first, so routing waits for these loads alone */
     /* 1. every token's activations, 16 values per (thread, r), clamped and unpredicated */
     const int nseg = a.n_tok * SEGT;
@@ -2660,6 +2776,10 @@ __device__ __forceinline__ void moe_gum_body(const MoeArgs &a) {
         mq_load_seg(a.h + (size_t)(e / SEGT) * K, e % SEGT, hv[r]);
     }
     moe_route_par(a, R, (unsigned long long *)stg, sx, lgt);
+    MOE_T(1);
+#ifdef LE_MOE_TRACE
+    tr_[2] = R.tr[1]; tr_[3] = R.tr[2];
+#endif
     const int z = blockIdx.y;
     if (z >= R.U) return; /* uniform over the block */
     const int e = R.grp_e[z];
@@ -2702,9 +2822,12 @@ __device__ __forceinline__ void moe_gum_body(const MoeArgs &a) {
         mtok[threadIdx.x] = t;
         mpair[threadIdx.x] = pair;
     }
+    
 #pragma unroll
     for (int i = 0; i < NI; i++) wb[64 * i + lane] = Rg[i];
-    __syncthreads();
+    
+    moe_sync();
+    
     /* 4. per member (a runtime loop: the code stays small), four tiles x this wave's super-blocks */
     const MsLane L = ms_lane<0>(lane);
     le_v4i A[4];
@@ -2724,12 +2847,12 @@ __device__ __forceinline__ void moe_gum_body(const MoeArgs &a) {
 #pragma unroll
         for (int ti = 0; ti < 4; ti++) {
             float v = y[ti];
-            v += __builtin_bit_cast(float, __builtin_amdgcn_ds_swizzle(__builtin_bit_cast(int, v), 0x401F));
-            v += __shfl_xor(v, 32);
+            v = row4_sum(v);
             if (lane < 16) red[wave][i][16 * ti + lane] = v;
         }
     }
-    __syncthreads();
+    
+    moe_sync();
     /* 5. SwiGLU of the unit's 32 values = sub-block ux of the down input: thread (member i, row r)
      * adds the waves for gate and up; then lanes 2i, 2i+1 of wave 0 quantize member i's two
      * 16-value segments into its down image */
@@ -2745,7 +2868,7 @@ __device__ __forceinline__ void moe_gum_body(const MoeArgs &a) {
             act[i][r] = g / (1.0f + __expf(-g)) * u;
         }
     }
-    __syncthreads();
+    moe_sync();
     if (wave == 0 && lane < 2 * LE_MOE_FAST_TOK) {
         const int i = lane >> 1, c = lane & 1;
         const bool ok = i < nmem;
@@ -2758,6 +2881,8 @@ __device__ __forceinline__ void moe_gum_body(const MoeArgs &a) {
         float *dxp = (float *)(rec + nsbd * 32), *fsv = dxp + nsbd * 16;
         mq_quant_seg<MAPD>(2 * ux + c, ok, v4, rec, dxp, fsv);
     }
+    MOE_T(6);
+    MOE_T_OUT(0);
 }
 
 #define LE_MOE_DN_IMGS 16 /* pair images the down kernel keeps in LDS */
@@ -2776,6 +2901,8 @@ __device__ __forceinline__ void moe_dnm_body(const MoeArgs &a) {
     uint4 *imgs = smem;                          /* LE_MOE_DN_IMGS images */
     uint4 *stg = smem + LE_MOE_DN_IMGS * IMGC;   /* [NW][NI*64] staging; routing keys first */
     uint4 *wb = stg + wave * NI * 64;
+    MOE_T_DECL;
+    MOE_T(0);
     for (int i = threadIdx.x; i < NW * LE_MOE_FAST_TOK * 16; i += blockDim.x) (&red[0][0][0])[i] = 0.f;
     const int npair = a.n_tok * a.k;
     const bool all_in = npair <= LE_MOE_DN_IMGS;
@@ -2792,6 +2919,7 @@ __device__ __forceinline__ void moe_dnm_body(const MoeArgs &a) {
     }
     /* the routing of the gate/up launch (n_tok * k <= 64 <= blockDim.x, groups <= 64) */
     moe_rec_read(a, R, a.ws + (size_t)a.n_tok * a.k * IMG);
+    MOE_T(1);
     const size_t rb = (size_t)P * SBB;
     /* H blocks per 16-row tile (grid = H * hidden / 16): block hh of a tile takes the expert groups
      * z = hh (mod H) and, with H = 2, adds into the output the gate/up launch zeroed (every
@@ -2822,7 +2950,8 @@ __device__ __forceinline__ void moe_dnm_body(const MoeArgs &a) {
                 if (c < nci) imgs[c] = iv[u][q];
             }
     }
-    __syncthreads(); /* the images, and the routing keys are no longer read before staging reuses them */
+    moe_sync(); /* the images, and the routing keys are no longer read before staging reuses them */
+    MOE_T(2);
     const MsLane L = ms_lane<MAPD>(lane);
     le_v4i A[4];
 #pragma unroll
@@ -2867,12 +2996,14 @@ __device__ __forceinline__ void moe_dnm_body(const MoeArgs &a) {
                 else
                     y += ms_sb_q4k(wb + n * CPR + CPS * q, A, dxp + q * 16, fsv + q * 8, L);
             }
-            y += __builtin_bit_cast(float, __builtin_amdgcn_ds_swizzle(__builtin_bit_cast(int, y), 0x401F));
-            y += __shfl_xor(y, 32);
+            y = row4_sum(y);
             if (lane < 16) red[wave][mtok[wave][i]][lane] += mw[wave][i] * y;
         }
+        MOE_T(3);
     }
-    __syncthreads();
+    MOE_T(4);
+    moe_sync();
+    MOE_T(5);
     for (int i = threadIdx.x; i < a.n_tok * 16; i += blockDim.x) {
         const int t = i >> 4, r = i & 15;
         float acc = 0.f;
@@ -2883,6 +3014,8 @@ __device__ __forceinline__ void moe_dnm_body(const MoeArgs &a) {
         else
             a.out[(size_t)t * a.hidden + row0 + r] = acc;
     }
+    MOE_T(6);
+    MOE_T_OUT(4096);
 }
 
 /* ===================== MoE in one launch: gate/up, a device-wide barrier, down =====================
@@ -3083,8 +3216,7 @@ __device__ __forceinline__ void moe_fus_body(const MoeArgs &a) {
 #pragma unroll
             for (int ti = 0; ti < 4; ti++) {
                 float v = y[ti];
-                v += __builtin_bit_cast(float, __builtin_amdgcn_ds_swizzle(__builtin_bit_cast(int, v), 0x401F));
-                v += __shfl_xor(v, 32);
+                v = row4_sum(v);
                 if (lane < 16) red[wave][i][16 * ti + lane] = v;
             }
         }
@@ -3185,8 +3317,7 @@ __device__ __forceinline__ void moe_fus_body(const MoeArgs &a) {
                 else
                     y += ms_sb_q4k(dwb + n * DCPR + DCPS * q, A, dxp + q * 16, fsv + q * 8, L);
             }
-            y += __builtin_bit_cast(float, __builtin_amdgcn_ds_swizzle(__builtin_bit_cast(int, y), 0x401F));
-            y += __shfl_xor(y, 32);
+            y = row4_sum(y);
             if (lane < 16) redd[(wave * LE_MOE_FAST_TOK + mtok[wave][i]) * 16 + lane] += mw[wave][i] * y;
         }
     }
