@@ -420,6 +420,9 @@ struct MhArgs {
     const float *x;
     float *y;
     int rows, cols, m;
+    int groups; /* token groups of T: block b takes group b % groups and every (gridDim.x / groups)-th
+                 * row tile from b / groups, so the groups of a tile stream its weights at the same
+                 * time (the second read is served by the memory-side cache) */
 };
 
 template <int P, int NW, int T>
@@ -428,7 +431,7 @@ __device__ __forceinline__ void mh_q4k_body(const MhArgs &a) {
     extern __shared__ uint4 smem[];
     constexpr int CPR = 9 * P + 1, NCH = 16 * CPR, NI = (NCH + 63) / 64;
     const int K = a.cols, nsb = K >> 8, M = a.m;
-    const int tok0 = T * blockIdx.z;
+    const int G = max(a.groups, 1), tok0 = T * (int)(blockIdx.x % G), bx = blockIdx.x / G, gx = max((int)gridDim.x / G, 1);
     const size_t rb = (size_t)nsb * 144;
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int n = lane & 15, kq = lane >> 4;
@@ -463,7 +466,7 @@ __device__ __forceinline__ void mh_q4k_body(const MhArgs &a) {
             R[i] = ldg16(a.w + (size_t)row * rb + (size_t)s0 * 144 + cb[i]);
         }
     };
-    issue(min((int)blockIdx.x, ntile - 1), active ? sfirst : 0);
+    issue(min(bx, ntile - 1), active ? sfirst : 0);
     /* the wave's activations, built here: chunk c = (local sb, token, 8-value column of the
      * 256) -> 16 bytes of fp16 in the order 0,2,1,3 within each four (the order of the B
      * fragments); the four lanes of a 32-value sub-block add their sums, which go into the
@@ -525,12 +528,12 @@ __device__ __forceinline__ void mh_q4k_body(const MhArgs &a) {
     }
     const int ta = n % T; /* this lane's A row (token); rows past T repeat earlier tokens */
     int par = 0;
-    for (int tile = blockIdx.x; tile < ntile; tile += gridDim.x) {
+    for (int tile = bx; tile < ntile; tile += gx) {
         v4f y = {0.f, 0.f, 0.f, 0.f};
         if (active) {
             for (int s0 = sfirst, lb = 0; s0 < nsb; s0 += sstep, lb += P) {
                 int nt = tile, ns = s0 + sstep;
-                if (ns >= nsb) { ns = sfirst; nt += gridDim.x; }
+                if (ns >= nsb) { ns = sfirst; nt += gx; }
 #pragma unroll
                 for (int i = 0; i < NI; i++) wb[64 * i + lane] = R[i];
                 if (nt < ntile) issue(nt, ns);

@@ -119,6 +119,7 @@ struct le_ctx {
     int gm_ksplit = 0;       /* MFMA GEMM K slices: 0 auto, else 1, 2, 4, 8 */
     int gm_pc = 1;           /* MFMA GEMM with producer/consumer waves */
     int gm_split = 0;        /* 1: activations as two fp16 halves (22 bits); 0: one fp16 value (11 bits) */
+    int gm_mh_t16 = 0;       /* 9..16 tokens: one 16-token group instead of two 8-token groups */
     int gq = 1;              /* Q4_K GEMM on the generic kernels (le_gq_*) instead of le_gm_12_* */
     int gq_min_m = 9;        /* other types: smallest M on the matrix-core GEMM (below: vector kernels) */
     int gq_cfg = 0;          /* generic GEMM block shape (tokens x rows, waves): 0 auto, 1 (32x256, 4), 2 (64x256, 4),
@@ -545,6 +546,8 @@ int le_set_option(le_ctx *c, const char *name, int value) {
     } else if (n == "rd_block") {
         if (value != 256 && value != 512) return c->fail(LE_ERR_ARG, "rd_block must be 256 or 512");
         c->rd_block = value;
+    } else if (n == "gm_mh_t16") {
+        c->gm_mh_t16 = value ? 1 : 0;
     } else if (n == "gq") {
         c->gq = value ? 1 : 0;
     } else if (n == "gq_min_m") {
@@ -939,7 +942,9 @@ int le_moe_layer_ptrs(le_ctx *c, int ty_gate, int ty_up, int ty_down, const void
  * pass (it builds its fp16 activations itself). Returns 1 when no instantiated shape fits. */
 static int mh_launch(le_ctx *c, const void *w, const float *x, int m, float *y, int rows, int cols, hipStream_t st) {
     const long long ntile = (rows + 15) / 16;
-    const int nsb = cols / 256, T = m <= 4 ? 4 : m <= 8 ? 8 : 16;
+    /* above 8 tokens: groups of 8 tokens whose blocks stream the same row tiles side by side
+     * (option gm_mh_t16 = 1: one 16-token group, whose images need 128 KB of LDS at K = 4096) */
+    const int nsb = cols / 256, T = m <= 4 ? 4 : m <= 8 || !c->gm_mh_t16 ? 8 : 16, G = (m + T - 1) / T;
     /* (P, NW) in order of preference, measured on 14336 x 4096 (T=4: 15.0 us with (2,4); T=8:
      * 16.4 us with (1,8)) */
     static const int k4[4][2] = {{2, 4}, {1, 4}, {1, 8}, {2, 2}}, k8[4][2] = {{1, 8}, {2, 4}, {1, 4}, {2, 2}};
@@ -956,7 +961,8 @@ static int mh_launch(le_ctx *c, const void *w, const float *x, int m, float *y, 
         snprintf(name, sizeof name, "le_mh_12_p%d_w%d_t%d", P, NW, T);
         /* every block builds its activation image once: the grid is what stays resident */
         const int per_cu = c->blocks_per_cu(name, NW * 64, lds);
-        long long gx = ntile, cap = (long long)c->cus * (per_cu > 0 ? per_cu : 1);
+        long long gx = ntile, cap = (long long)c->cus * (per_cu > 0 ? per_cu : 1) / G;
+        if (cap < 1) cap = 1;
         if (gx > cap) {
             const long long it = (gx + cap - 1) / cap;
             gx = (gx + it - 1) / it;
@@ -965,10 +971,10 @@ static int mh_launch(le_ctx *c, const void *w, const float *x, int m, float *y, 
             const void *w;
             const float *x;
             float *y;
-            int rows, cols, m;
-        } a{w, x, y, rows, cols, m};
+            int rows, cols, m, groups;
+        } a{w, x, y, rows, cols, m, G};
         void *args[] = {&a};
-        return c->launch(name, dim3((unsigned)gx, 1, 1), NW * 64, lds, st, args);
+        return c->launch(name, dim3((unsigned)(gx * G), 1, 1), NW * 64, lds, st, args);
     }
     return 1;
 }

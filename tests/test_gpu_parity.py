@@ -259,19 +259,21 @@ def test_error_codes(engine):
     assert e.value.code == -3
 
 
-@pytest.mark.parametrize("path", ["f16", "f16x16", "int8"])
-@pytest.mark.parametrize("m", [2, 3, 5, 8, 11])
+@pytest.mark.parametrize("path", ["f16", "f16x16", "f16t16", "int8"])
+@pytest.mark.parametrize("m", [2, 3, 5, 8, 11, 16])
 @pytest.mark.parametrize("rows,cols", [(300, 4096), (64, 2048), (1000, 1024), (4100, 512)])
 def test_gemm_few_tokens_staged(fresh_engine, path, m, rows, cols):
     """Few tokens on the staged kernels: the f16 MFMA kernel for 3..8 tokens (tokens as MFMA
-    rows, T = 4 or 8, and 16 under the default gm_mh_max=16) and the int8 multi-token matvec (T = 2, 4 or 8 per pass, option gm_mh=0),
-    with partial token groups (3, 5, 11), a second group (11 > 8 on the int8 kernel) and ragged
-    row tiles."""
+    rows, T = 4 or 8; 9..16 tokens under the default gm_mh_max=16 as two 8-token groups streaming
+    the same row tiles side by side, or with gm_mh_t16=1 as one 16-token group) and the int8
+    multi-token matvec (T = 2, 4 or 8 per pass, option gm_mh=0), with partial token groups (3, 5,
+    11), a second group (11, 16 > 8) and ragged row tiles."""
     import torch
     engine = fresh_engine
     engine.set_option("gm_min_m", 64)
     engine.set_option("gm_mh", 0 if path == "int8" else 1)
-    engine.set_option("gm_mh_max", 16 if path == "f16x16" else 8)
+    engine.set_option("gm_mh_max", 16 if path in ("f16x16", "f16t16") else 8)
+    engine.set_option("gm_mh_t16", 1 if path == "f16t16" else 0)
     ty = le.Q4_K
     q, _ = weights(ty, rows, cols, seed=31 + m)
     xs = np.stack([acts(cols, 6000 + 17 * m + t) for t in range(m)])
