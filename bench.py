@@ -360,6 +360,15 @@ PROBES = {
     "gemm_q6k_m512": ("gemm", "Q6_K", 4096, 14336, 512),
     "moe_ntok1": ("moe", None, 0, 0, 1),
     "moe_ntok8": ("moe", None, 0, 0, 8),
+    "moe_prefill64": ("moe", None, 0, 0, 64),
+    "gemm_m8": ("gemm", "Q4_K", 14336, 4096, 8),
+    "gemm_m16": ("gemm", "Q4_K", 14336, 4096, 16),
+    "q4_0": ("mv", "Q4_0", 14336, 4096, 1),
+    "q3_k": ("mv", "Q3_K", 14336, 4096, 1),
+    "q5_k": ("mv", "Q5_K", 14336, 4096, 1),
+    "iq2_s": ("mv", "IQ2_S", 14336, 4096, 1),
+    "gemm_q5k_m512": ("gemm", "Q5_K", 14336, 4096, 512),
+    "gemm_iq2s_m512": ("gemm", "IQ2_S", 14336, 4096, 512),
 }
 
 
@@ -380,11 +389,14 @@ def probe(eng, name, launches=100, copy_bytes=256 << 20):
         lgs = [torch.from_numpy(le.fill_normal(mtok * n_exp, 300 + i)).cuda() for i in range(8)]
         h = torch.from_numpy(le.fill_normal(mtok * hidden, 299)).cuda()
         out = torch.empty(mtok * hidden, dtype=torch.float32, device="cuda")
-        ws = torch.zeros(eng.moe_workspace_size(mtok, k, ff), dtype=torch.uint8, device="cuda")
+        nws = eng.moe_workspace_size(mtok, k, ff)
+        if mtok > 8:  # the grouped (prefill) form: le_moe_route_tok, le_moe_group, le_gqg_*
+            nws = max(nws, eng.moe_prefill_workspace_size(mtok, k, n_exp, hidden, ff))
+        ws = torch.zeros(nws, dtype=torch.uint8, device="cuda")
         for i in range(launches):
             eng.moe(le.Q4_K, le.Q4_K, le.Q6_K, dg, du, dd, n_exp, k, hidden, ff, lgs[i % 8], h, mtok, out, ws=ws)
     else:
-        ty = le.TYPES[tname]
+        ty = le.MV_TYPES[tname]
         host = quantized(ty, rows, cols, 1)
         wbytes = int(host.nbytes)
         bufs = device_copies(host)

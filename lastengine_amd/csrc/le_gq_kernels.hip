@@ -489,7 +489,7 @@ __device__ __forceinline__ void gq_body(const GqArgs &a, const u8 *ws) {
 #pragma unroll
         for (int i = 0; i < NWC; i++) {
             const u8 *p = w0 + (h ? wo1[i] : wo0[i]);
-            R.w[i] = F::ALIGNED ? ldg16(p) : ldg16u(p);
+            R.w[i] = F::ALIGNED ? ldg16c(p) : ldg16u(p); /* cached: the next step reads the same lines */
         }
         const u8 *x0 = Ag + (size_t)(sb * 16 + 8 * h) * 1024;
 #pragma unroll
