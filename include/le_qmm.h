@@ -221,18 +221,20 @@ int le_gemm_noalloc(le_ctx *ctx, int ty, const void *w, const float *x, int m, f
  * weights renormalised over the k, out[t*hidden ...] = sum_s w_s * down_e(silu(gate_e h_t) * up_e h_t).
  * gate/up: n_exp slabs of ff x hidden (types ty_gate, ty_up), down: n_exp slabs of hidden x ff
  * (ty_down), slab e at e * rows * row_bytes. Routing and grouping by expert run on the device
- * (no host synchronisation); each routed expert's weights are read once per call. idx_out/w_out
+ * (no host synchronisation); each routed expert's weights are read once per call (for 9..15
+ * tokens once per 8-token chunk; in the grouped form once per tile of its pairs). idx_out/w_out
  * (n_tok*k, optional) receive the selection. ws: device workspace of le_moe_workspace_size bytes
  * (type pairs other than (Q4_K, Q6_K), (Q4_K, Q4_K), (Q6_K, Q6_K), (Q8_0, Q8_0), (IQ2_XXS, IQ3_XXS),
  * (IQ2_XXS, IQ2_XXS), (IQ3_XXS, IQ3_XXS) run the grouped form below at every token count and need
  * le_moe_prefill_workspace_size bytes).
  * Limits: n_tok <= 65536, k <= 16, n_exp <= 256, hidden and ff multiples of 256.
- * Prefill-sized calls (more than 64 tokens; from 24 tokens when ws holds
+ * Prefill-sized calls (more than 64 tokens; from 16 tokens when ws holds
  * le_moe_prefill_workspace_size bytes) route every token, group the (token, expert) pairs by
  * expert on the device (token order within an expert) and run the three projections as grouped
  * matrix-core matmuls (le_mm_grouped), so each expert's weights are streamed once per tile of up
  * to 128 of its pairs; ws must then hold le_moe_prefill_workspace_size bytes. Decode-sized calls
- * need le_moe_workspace_size bytes; above 8 tokens they run as consecutive calls of at most 8 tokens.
+ * need le_moe_workspace_size bytes; 9..15 tokens (or up to 64 without the grouped form's workspace)
+ * run as consecutive calls of at most 8 tokens, each of which streams its own routed experts.
  * For 3..8 tokens at hidden 2048 the layer runs as one launch with a device-wide barrier between
  * gate/up and down. That launch sizes its grid to the blocks that fit on the device at once and
  * assumes nothing else occupies it: a concurrent kernel on another stream can make its bounded
