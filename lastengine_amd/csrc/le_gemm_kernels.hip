@@ -429,7 +429,9 @@ template <int P, int NW, int T>
 __device__ __forceinline__ void mh_q4k_body(const MhArgs &a) {
     typedef float v4f __attribute__((ext_vector_type(4)));
     extern __shared__ uint4 smem[];
-    constexpr int CPR = 9 * P + 1, NCH = 16 * CPR, NI = (NCH + 63) / 64;
+    /* CPR: 16-byte slots per staged row, odd so that the 16 rows of a read fall into distinct
+     * banks; IMS: slots per (token, sub-block) image record, 5 so that the 8 tokens of a read do */
+    constexpr int CPR = (9 * P + 1) | 1, NCH = 16 * CPR, NI = (NCH + 63) / 64, IMS = 5;
     const int K = a.cols, nsb = K >> 8, M = a.m;
     const int G = max(a.groups, 1), tok0 = T * (int)(blockIdx.x % G), bx = blockIdx.x / G, gx = max((int)gridDim.x / G, 1);
     const size_t rb = (size_t)nsb * 144;
@@ -439,9 +441,9 @@ __device__ __forceinline__ void mh_q4k_body(const MhArgs &a) {
     /* wave-private LDS: the image [local sb][sub-block j][token][4 x 16 B], the sum records
      * [local sb][token][2 x 16 B], the inverse scales [local sb][MFMA row 0..15] (float), then
      * the weight staging */
-    const int wsz = nsbw * 8 * T * 4 + nsbw * T * 2 + nsbw * 4;
+    const int wsz = nsbw * 8 * T * IMS + nsbw * T * 2 + nsbw * 4;
     uint4 *img = smem + wave * (wsz + NI * 64);
-    uint4 *srec = img + nsbw * 8 * T * 4;
+    uint4 *srec = img + nsbw * 8 * T * IMS;
     float *isc = (float *)(srec + nsbw * T * 2);
     uint4 *wb = img + wsz;
     float *red = (float *)(smem + NW * (wsz + NI * 64)); /* [NW][16 tokens][16 rows] */
@@ -456,7 +458,7 @@ __device__ __forceinline__ void mh_q4k_body(const MhArgs &a) {
         const int c = min(64 * i + lane, NCH - 1);
         const int col = c % CPR;
         ri[i] = c / CPR;
-        cb[i] = (col == 9 * P ? 0 : col) * 16;
+        cb[i] = (col >= 9 * P ? 0 : col) * 16; /* pad slots re-read chunk 0 (never past the super-block) */
     }
     uint4 R[NI];
     auto issue = [&](int tile, int s0) {
@@ -510,7 +512,7 @@ __device__ __forceinline__ void mh_q4k_body(const MhArgs &a) {
                 const float4 q = make_float4(v[u][1].x * sc, v[u][1].y * sc, v[u][1].z * sc, v[u][1].w * sc);
                 const le_h2 h0 = {(_Float16)p.x, (_Float16)p.z}, h1 = {(_Float16)p.y, (_Float16)p.w};
                 const le_h2 h2 = {(_Float16)q.x, (_Float16)q.z}, h3 = {(_Float16)q.y, (_Float16)q.w};
-                img[((l * 8 + (col >> 2)) * T + t) * 4 + (col & 3)] = make_uint4(as_u32(h0), as_u32(h1), as_u32(h2), as_u32(h3));
+                img[((l * 8 + (col >> 2)) * T + t) * IMS + (col & 3)] = make_uint4(as_u32(h0), as_u32(h1), as_u32(h2), as_u32(h3));
                 /* sums of the fp16-rounded values, so the mins term cancels the rounding the
                  * scale term sees (the error then scales with sum |w x|) */
                 float sm = (((float)h0.x + (float)h1.x) + ((float)h0.y + (float)h1.y)) +
@@ -555,8 +557,8 @@ __device__ __forceinline__ void mh_q4k_body(const MhArgs &a) {
                         const le_h2 v2 = {(_Float16)(0.0625f * sh), (_Float16)(0.0625f * sh)}, v3 = {(_Float16)(-64.f * sh), (_Float16)(-64.f * sh)};
                         le_v8h blo, bhi;
                         gm_q4k_frag(w, make_uint4(as_u32(v0), as_u32(v1), as_u32(v2), as_u32(v3)), blo, bhi);
-                        const le_v8h alo = __builtin_bit_cast(le_v8h, img[((l * 8 + 2 * g) * T + ta) * 4 + kq]);
-                        const le_v8h ahi = __builtin_bit_cast(le_v8h, img[((l * 8 + 2 * g + 1) * T + ta) * 4 + kq]);
+                        const le_v8h alo = __builtin_bit_cast(le_v8h, img[((l * 8 + 2 * g) * T + ta) * IMS + kq]);
+                        const le_v8h ahi = __builtin_bit_cast(le_v8h, img[((l * 8 + 2 * g + 1) * T + ta) * IMS + kq]);
                         d1 = __builtin_amdgcn_mfma_f32_16x16x32_f16(alo, blo, d1, 0, 0, 0);
                         d1 = __builtin_amdgcn_mfma_f32_16x16x32_f16(ahi, bhi, d1, 0, 0, 0);
                     }

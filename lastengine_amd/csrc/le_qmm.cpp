@@ -955,8 +955,10 @@ static int mh_launch(le_ctx *c, const void *w, const float *x, int m, float *y, 
     for (int i = 0; i < ncand; i++) {
         const int P = c->gm_mh_shape ? c->gm_mh_shape / 10 : cand[i][0], NW = c->gm_mh_shape ? c->gm_mh_shape % 10 : cand[i][1];
         if (P > c->ms_p || nsb % (NW * P)) continue;
-        const int ni = (16 * (9 * P + 1) + 63) / 64;
-        const size_t lds = (size_t)NW * ((size_t)(nsb / NW) * (T * 544 + 64) + (size_t)ni * 1024) + (size_t)NW * 2048;
+        /* per wave: per super-block T records of 8 x 5 16-byte image slots and 2 sum slots, 64 bytes
+         * of scales; the staging of 16 rows x (9P + 1, made odd) slots; the reduction area */
+        const int ni = (16 * ((9 * P + 1) | 1) + 63) / 64;
+        const size_t lds = (size_t)NW * ((size_t)(nsb / NW) * (T * 672 + 64) + (size_t)ni * 1024) + (size_t)NW * 2048;
         if (lds > c->lds_limit) continue;
         char name[48];
         snprintf(name, sizeof name, "le_mh_12_p%d_w%d_t%d", P, NW, T);
