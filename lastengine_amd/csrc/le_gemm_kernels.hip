@@ -74,17 +74,25 @@ __device__ __forceinline__ void gm_split2(float a, float b, u32 &hi, u32 &lo) {
  * nibbles) -> two B fragments of fp16 codes q*sc in the order 0,2,1,3 within each four. The
  * nibble at bits 0-3 (4-7) of a 16-bit half becomes fp16 1024+q (1024+16q) by the exponent
  * trick; one packed fma with (sc, -1024 sc) (or (sc/16, -64 sc)) gives q*sc exactly. */
+/* (x & m) | c in one v_and_or_b32 (a VOP3 instruction cannot carry the two literal constants, so
+ * the compiler would otherwise emit an and and an or); m and c stay in registers */
+__device__ __forceinline__ u32 gm_and_or(u32 x, u32 m, u32 c) {
+    u32 r;
+    __asm__("v_and_or_b32 %0, %1, %2, %3" : "=v"(r) : "v"(x), "v"(m), "v"(c));
+    return r;
+}
 __device__ __forceinline__ void gm_q4k_frag(uint2 w, uint4 k, le_v8h &lo, le_v8h &hi) {
     const le_h2 slo = as_h2(k.x), clo = as_h2(k.y), shi = as_h2(k.z), chi = as_h2(k.w);
+    const u32 mlo = 0x000F000Fu, mhi = 0x00F000F0u, c1024 = 0x64006400u;
     u32 l[4], h[4];
     const u32 ws[2] = {w.x, w.y};
 #pragma unroll
     for (int i = 0; i < 2; i++) {
         const u32 a = ws[i], a8 = a >> 8;
-        l[2 * i] = as_u32(__builtin_elementwise_fma(as_h2((a & 0x000F000Fu) | 0x64006400u), slo, clo));
-        l[2 * i + 1] = as_u32(__builtin_elementwise_fma(as_h2((a8 & 0x000F000Fu) | 0x64006400u), slo, clo));
-        h[2 * i] = as_u32(__builtin_elementwise_fma(as_h2((a & 0x00F000F0u) | 0x64006400u), shi, chi));
-        h[2 * i + 1] = as_u32(__builtin_elementwise_fma(as_h2((a8 & 0x00F000F0u) | 0x64006400u), shi, chi));
+        l[2 * i] = as_u32(__builtin_elementwise_fma(as_h2(gm_and_or(a, mlo, c1024)), slo, clo));
+        l[2 * i + 1] = as_u32(__builtin_elementwise_fma(as_h2(gm_and_or(a8, mlo, c1024)), slo, clo));
+        h[2 * i] = as_u32(__builtin_elementwise_fma(as_h2(gm_and_or(a, mhi, c1024)), shi, chi));
+        h[2 * i + 1] = as_u32(__builtin_elementwise_fma(as_h2(gm_and_or(a8, mhi, c1024)), shi, chi));
     }
     lo = __builtin_bit_cast(le_v8h, make_uint4(l[0], l[1], l[2], l[3]));
     hi = __builtin_bit_cast(le_v8h, make_uint4(h[0], h[1], h[2], h[3]));
