@@ -443,7 +443,7 @@ __device__ __forceinline__ void mh_q4k_body(const MhArgs &a) {
     const int K = a.cols, nsb = K >> 8, M = a.m;
     const int G = max(a.groups, 1), tok0 = T * (int)(blockIdx.x % G), bx = blockIdx.x / G, gx = max((int)gridDim.x / G, 1);
     const size_t rb = (size_t)nsb * 144;
-    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6); /* wave-uniform */
     const int n = lane & 15, kq = lane >> 4;
     const int nsbw = nsb / NW;
     /* wave-private LDS: the image [local sb][sub-block j][token][4 x 16 B], the sum records
@@ -476,65 +476,95 @@ __device__ __forceinline__ void mh_q4k_body(const MhArgs &a) {
             R[i] = ldg16(a.w + (size_t)row * rb + (size_t)s0 * 144 + cb[i]);
         }
     };
-    issue(min(bx, ntile - 1), active ? sfirst : 0);
-    /* the wave's activations, built here: chunk c = (local sb, token, 8-value column of the
-     * 256) -> 16 bytes of fp16 in the order 0,2,1,3 within each four (the order of the B
-     * fragments); the four lanes of a 32-value sub-block add their sums, which go into the
-     * token's record as fp16 high and low halves */
-    if (active) {
-        const int nch = nsbw * T * 32;
-        for (int c0 = 0; c0 < nch; c0 += 64 * 4) {
-            float4 v[4][2];
-#pragma unroll
-            for (int u = 0; u < 4; u++) {
-                const int c = min(c0 + 64 * u + lane, nch - 1), l = c / (T * 32), t = (c / 32) % T, col = c & 31;
-                const float *src = a.x + (size_t)min(tok0 + t, M - 1) * K + 256 * gsb(l) + 8 * col;
-                v[u][0] = *(const LE_GLOBAL float4 *)src;
-                v[u][1] = *(const LE_GLOBAL float4 *)(src + 4);
-            }
-#pragma unroll
-            for (int u = 0; u < 4; u++) {
-                if (c0 + 64 * u >= nch) break; /* wave-uniform: nch is a multiple of 64 */
-                const int c = c0 + 64 * u + lane, l = c / (T * 32), t = (c / 32) % T, col = c & 31;
-                /* the 32 lanes of each half-wave hold one (token, super-block) */
-                /* the largest magnitude as an integer maximum of the bit patterns without sign
-                 * (the float order for every non-NaN value); over the 32 lanes by DPP within
-                 * each row of 16 and one swizzle (xor 16) across */
-                const float4 v0 = v[u][0], v1 = v[u][1];
-                u32 mx = max(max(max(__float_as_uint(v0.x) & 0x7FFFFFFFu, __float_as_uint(v0.y) & 0x7FFFFFFFu),
-                             max(__float_as_uint(v0.z) & 0x7FFFFFFFu, __float_as_uint(v0.w) & 0x7FFFFFFFu)),
-                         max(max(__float_as_uint(v1.x) & 0x7FFFFFFFu, __float_as_uint(v1.y) & 0x7FFFFFFFu),
-                             max(__float_as_uint(v1.z) & 0x7FFFFFFFu, __float_as_uint(v1.w) & 0x7FFFFFFFu)));
-                mx = max(mx, (u32)__builtin_amdgcn_update_dpp(0, (int)mx, 0xB1, 0xF, 0xF, true));  /* quad_perm [1,0,3,2] */
-                mx = max(mx, (u32)__builtin_amdgcn_update_dpp(0, (int)mx, 0x4E, 0xF, 0xF, true));  /* quad_perm [2,3,0,1] */
-                mx = max(mx, (u32)__builtin_amdgcn_update_dpp(0, (int)mx, 0x141, 0xF, 0xF, true)); /* row_half_mirror */
-                mx = max(mx, (u32)__builtin_amdgcn_update_dpp(0, (int)mx, 0x140, 0xF, 0xF, true)); /* row_mirror */
-                mx = max(mx, (u32)__builtin_amdgcn_ds_swizzle((int)mx, 0x401F));
-                /* biased exponent b of the maximum: x 2^(136 - b) puts it in [512, 1024); the
-                 * factor is kept within 2^-118 .. 2^126 (zero or subnormal maxima, inf / NaN) */
-                const int be = (int)(mx >> 23);
-                const int sx = min(max(136 - be, -118), 126);
-                const float sc = __uint_as_float((u32)(127 + sx) << 23), inv = __uint_as_float((u32)(127 - sx) << 23);
-                if (col < 16 / T) isc[l * 16 + t + T * col] = inv; /* MFMA rows t, t + T, ... */
-                const float4 p = make_float4(v[u][0].x * sc, v[u][0].y * sc, v[u][0].z * sc, v[u][0].w * sc);
-                const float4 q = make_float4(v[u][1].x * sc, v[u][1].y * sc, v[u][1].z * sc, v[u][1].w * sc);
-                const le_h2 h0 = {(_Float16)p.x, (_Float16)p.z}, h1 = {(_Float16)p.y, (_Float16)p.w};
-                const le_h2 h2 = {(_Float16)q.x, (_Float16)q.z}, h3 = {(_Float16)q.y, (_Float16)q.w};
-                img[((l * 8 + (col >> 2)) * T + t) * IMS + (col & 3)] = make_uint4(as_u32(h0), as_u32(h1), as_u32(h2), as_u32(h3));
-                /* sums of the fp16-rounded values, so the mins term cancels the rounding the
-                 * scale term sees (the error then scales with sum |w x|) */
-                float sm = (((float)h0.x + (float)h1.x) + ((float)h0.y + (float)h1.y)) +
-                           (((float)h2.x + (float)h3.x) + ((float)h2.y + (float)h3.y));
-                sm += dpp_f<0xB1>(sm);
-                sm += dpp_f<0x4E>(sm);
-                if ((col & 3) == 0) {
-                    const _Float16 hi = (_Float16)sm, lo = (_Float16)(sm - (float)hi);
-                    _Float16 *rec = (_Float16 *)(srec + (l * T + t) * 2);
-                    rec[col >> 2] = hi;
-                    rec[8 + (col >> 2)] = lo;
-                }
-            }
+    /* the wave's activations, built here: 64-lane row k of its chunks holds (local sb l, token t)
+     * = (q / T, q % T) for q = 2k + lane / 32 and the 8-value column lane % 32 of the 256 ->
+     * 16 bytes of fp16 in the order 0,2,1,3 within each four (the order of the B fragments);
+     * the four lanes of a 32-value sub-block add their sums, which go into the token's record as
+     * fp16 high and low halves. The first XP rows are loaded before the first weight item: the
+     * memory wait counter retires in issue order, so activations loaded after the weights could
+     * not be used before the weights had landed. */
+    constexpr int LT = T == 4 ? 2 : T == 8 ? 3 : 4, XP = 8;
+    /* every wave has super-blocks: the host launches only shapes with nsb % (NW P) == 0 */
+    const int nk = nsbw * T / 2, hs32 = lane >> 5, col = lane & 31;
+    auto xsrc = [&](int k) {
+        const int q = 2 * k + hs32, l = q >> LT, t = q & (T - 1);
+        return a.x + (min(tok0 + t, M - 1) * K + 256 * gsb(l) + 8 * col);
+    };
+    /* the largest magnitude of a (token, super-block) as an integer maximum of the bit patterns
+     * without sign (the float order for every non-NaN value); over the 32 lanes by DPP within
+     * each row of 16 and one swizzle (xor 16) across */
+    auto amax = [&](const float4 &v0, const float4 &v1) {
+        const u32 am = 0x7FFFFFFFu;
+        u32 mx = max(max(__float_as_uint(v0.x) & am, __float_as_uint(v0.y) & am), __float_as_uint(v0.z) & am);
+        mx = max(max(mx, __float_as_uint(v0.w) & am), __float_as_uint(v1.x) & am);
+        mx = max(max(mx, __float_as_uint(v1.y) & am), __float_as_uint(v1.z) & am);
+        mx = max(mx, __float_as_uint(v1.w) & am);
+        mx = max(mx, (u32)__builtin_amdgcn_update_dpp(0, (int)mx, 0xB1, 0xF, 0xF, true));  /* quad_perm [1,0,3,2] */
+        mx = max(mx, (u32)__builtin_amdgcn_update_dpp(0, (int)mx, 0x4E, 0xF, 0xF, true));  /* quad_perm [2,3,0,1] */
+        mx = max(mx, (u32)__builtin_amdgcn_update_dpp(0, (int)mx, 0x141, 0xF, 0xF, true)); /* row_half_mirror */
+        mx = max(mx, (u32)__builtin_amdgcn_update_dpp(0, (int)mx, 0x140, 0xF, 0xF, true)); /* row_mirror */
+        return max(mx, (u32)__builtin_amdgcn_ds_swizzle((int)mx, 0x401F));
+    };
+    typedef _Float16 h2v __attribute__((ext_vector_type(2)));
+    auto emit = [&](int k, const float4 &v0, const float4 &v1, u32 mx) {
+        const int q = 2 * k + hs32, l = q >> LT, t = q & (T - 1);
+        /* biased exponent b of the maximum: x 2^(136 - b) puts it in [512, 1024); the factor is
+         * kept within 2^-118 .. 2^126 (zero or subnormal maxima, inf / NaN) */
+        const int sx = min(max(136 - (int)(mx >> 23), -118), 126);
+        const float sc = __uint_as_float((u32)(127 + sx) << 23);
+        if (col < 16 / T) isc[l * 16 + t + T * col] = __uint_as_float((u32)(127 - sx) << 23); /* MFMA rows t, t + T, ... */
+        const h2v e0 = {(_Float16)(v0.x * sc), (_Float16)(v0.z * sc)}, e1 = {(_Float16)(v0.y * sc), (_Float16)(v0.w * sc)};
+        const h2v e2 = {(_Float16)(v1.x * sc), (_Float16)(v1.z * sc)}, e3 = {(_Float16)(v1.y * sc), (_Float16)(v1.w * sc)};
+        img[((l * 8 + (col >> 2)) * T + t) * IMS + (col & 3)] =
+            make_uint4(__builtin_bit_cast(u32, e0), __builtin_bit_cast(u32, e1), __builtin_bit_cast(u32, e2), __builtin_bit_cast(u32, e3));
+        /* sums of the fp16-rounded values, so the mins term cancels the rounding the scale term
+         * sees (the error then scales with sum |w x|) */
+        const h2v one = {(_Float16)1.f, (_Float16)1.f};
+        float sm = __builtin_amdgcn_fdot2(e0, one, 0.f, false);
+        sm = __builtin_amdgcn_fdot2(e1, one, sm, false);
+        sm = __builtin_amdgcn_fdot2(e2, one, sm, false);
+        sm = __builtin_amdgcn_fdot2(e3, one, sm, false);
+        sm += dpp_f<0xB1>(sm);
+        sm += dpp_f<0x4E>(sm);
+        if ((col & 3) == 0) {
+            const _Float16 hi = (_Float16)sm, lo = (_Float16)(sm - (float)hi);
+            _Float16 *rec = (_Float16 *)(srec + (l * T + t) * 2);
+            rec[col >> 2] = hi;
+            rec[8 + (col >> 2)] = lo;
         }
+    };
+    {
+        float4 v[XP][2];
+#pragma unroll
+        for (int k = 0; k < XP; k++) {
+            const float *src = xsrc(min(k, nk - 1));
+            v[k][0] = *(const LE_GLOBAL float4 *)src;
+            v[k][1] = *(const LE_GLOBAL float4 *)(src + 4);
+        }
+        issue(min(bx, ntile - 1), active ? sfirst : 0);
+        __builtin_amdgcn_sched_barrier(0); /* the weight loads go out before any activation wait */
+        /* every row's maximum first, so the rows' cross-lane reductions overlap */
+        u32 mx[XP];
+#pragma unroll
+        for (int k = 0; k < XP; k++) mx[k] = amax(v[k][0], v[k][1]);
+#pragma unroll
+        for (int k = 0; k < XP; k++)
+            if (k < nk) emit(k, v[k][0], v[k][1], mx[k]); /* wave-uniform */
+    }
+    for (int k0 = XP; k0 < nk; k0 += 4) { /* T = 16, or more than 2 local super-blocks at T = 8: the rest, after the weights */
+        float4 v[4][2];
+#pragma unroll
+        for (int u = 0; u < 4; u++) {
+            const float *src = xsrc(min(k0 + u, nk - 1));
+            v[u][0] = *(const LE_GLOBAL float4 *)src;
+            v[u][1] = *(const LE_GLOBAL float4 *)(src + 4);
+        }
+        u32 mx[4];
+#pragma unroll
+        for (int u = 0; u < 4; u++) mx[u] = amax(v[u][0], v[u][1]);
+#pragma unroll
+        for (int u = 0; u < 4; u++)
+            if (k0 + u < nk) emit(k0 + u, v[u][0], v[u][1], mx[u]);
     }
     const int ta = n % T; /* this lane's A row (token); rows past T repeat earlier tokens */
     int par = 0;

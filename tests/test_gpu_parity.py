@@ -284,6 +284,27 @@ def test_gemm_few_tokens_staged(fresh_engine, path, m, rows, cols):
     check_close(y.cpu().numpy(), want, absmag(ty, q, rows, cols, xs))
 
 
+@pytest.mark.parametrize("shape", [14, 18, 24, 22])
+@pytest.mark.parametrize("m", [4, 8, 16])
+def test_gemm_few_tokens_every_shape(fresh_engine, shape, m):
+    """Every (P, waves) shape of the few-token f16 kernel (option gm_mh_shape = 10 P + waves), so a
+    wave builds 1 to 8 local super-blocks of activations (the rows loaded before its first weight
+    item and, past eight rows, the rows loaded after it), at 4, 8 and 16 (one group) tokens."""
+    import torch
+    engine = fresh_engine
+    engine.set_option("gm_min_m", 64)
+    engine.set_option("gm_mh_max", 16)
+    engine.set_option("gm_mh_t16", 1)
+    engine.set_option("gm_mh_shape", shape)
+    ty, rows, cols = le.Q4_K, 200, 4096
+    q, _ = weights(ty, rows, cols, seed=41 + shape)
+    xs = np.stack([acts(cols, 7000 + 13 * m + t) for t in range(m)])
+    y = torch.full((m, rows), float("nan"), dtype=torch.float32, device="cuda")
+    engine.gemm(ty, dev(q), dev(xs), m, y, rows, cols)
+    sync()
+    check_close(y.cpu().numpy(), oracle.matmat(ty, q, rows, cols, xs), absmag(ty, q, rows, cols, xs))
+
+
 @pytest.mark.parametrize("m", [16, 128])
 def test_gemm_activation_split(fresh_engine, m):
     """gm_split=1 carries each activation as two fp16 halves: the result then agrees with the fp64
