@@ -428,9 +428,10 @@ struct MhArgs {
     const float *x;
     float *y;
     int rows, cols, m;
-    int groups; /* token groups of T: block b takes group b % groups and every (gridDim.x / groups)-th
-                 * row tile from b / groups, so the groups of a tile stream its weights at the same
-                 * time (the second read is served by the memory-side cache) */
+    int groups; /* token groups of T: block b takes group (b / 8) % groups and every
+                 * (gridDim.x / groups)-th row tile from ((b / 8) / groups) * 8 + b % 8, so the groups
+                 * of a tile stream its weights at the same time on one XCD (the host makes
+                 * gridDim.x / groups a multiple of 8 when groups > 1) */
 };
 
 template <int P, int NW, int T>
@@ -441,7 +442,10 @@ __device__ __forceinline__ void mh_q4k_body(const MhArgs &a) {
      * banks; IMS: slots per (token, sub-block) image record, 5 so that the 8 tokens of a read do */
     constexpr int CPR = (9 * P + 1) | 1, NCH = 16 * CPR, NI = (NCH + 63) / 64, IMS = 5;
     const int K = a.cols, nsb = K >> 8, M = a.m;
-    const int G = max(a.groups, 1), tok0 = T * (int)(blockIdx.x % G), bx = blockIdx.x / G, gx = max((int)gridDim.x / G, 1);
+    /* token group and row-tile block: blocks b and b + 8 run on the same XCD (blocks go to the
+     * XCDs round-robin), so the groups of a row tile are blocks 8 apart and share that XCD's L2 */
+    const int G = max(a.groups, 1), rnd = (int)blockIdx.x >> 3;
+    const int tok0 = T * (rnd % G), bx = (rnd / G) * 8 + (int)(blockIdx.x & 7), gx = max((int)gridDim.x / G, 1);
     const size_t rb = (size_t)nsb * 144;
     const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6); /* wave-uniform */
     const int n = lane & 15, kq = lane >> 4;

@@ -970,6 +970,7 @@ static int mh_launch(le_ctx *c, const void *w, const float *x, int m, float *y, 
             const long long it = (gx + cap - 1) / cap;
             gx = (gx + it - 1) / it;
         }
+        if (G > 1) gx = (gx + 7) / 8 * 8; /* the kernel's group / row-tile mapping */
         struct {
             const void *w;
             const float *x;
