@@ -1035,20 +1035,22 @@ static int gq_launch(le_ctx *c, int ty, const void *w, const float *x, int m, fl
                      size_t ws_bytes, hipStream_t st) {
     /* block shapes: (WM, WN, TM, TN) -> BM = 32 TM WM tokens, BN = 32 TN WN rows */
     static const int cfgs[10][4] = {{1, 4, 1, 2}, {1, 4, 2, 2}, {1, 4, 4, 2}, {2, 2, 2, 2}, {1, 8, 2, 1}, {1, 8, 4, 1}, {1, 8, 1, 1}, {1, 4, 2, 1}, {1, 4, 1, 1}, {1, 4, 4, 1}};
-    /* block shape by token count and type, from a sweep of every type at its config shape
-     * (M = 17, 32, 48, 64): up to 32 tokens 32 x 128 tiles on 4 waves (Q4_K M=17 33.4 -> 26.4 us,
-     * Q6_K 39.4 -> 28.5, Q8_0 64.5 -> 55.8, IQ3_XXS 39.0 -> 28.7); 33..64 tokens 32 x 128 for Q4_K
-     * (two token tiles: 37.7 -> 32.6 us at M=64), 64 x 128 on 4 waves for Q6_K and IQ3_XXS,
-     * 64 x 256 on 8 waves for Q8_0 and IQ2_XXS; 65..128 tokens 64 x 128 on 4 waves for Q4_K (M=128
-     * 52.2 -> 45.6 us) and 128 x 128 on 4 waves for Q6_K and IQ3_XXS (74.0 -> 49.9, 55.6 -> 49.7);
-     * above, 128 x 256 on 4 waves for Q6_K
-     * (M=512 140.5 -> 128.5 us) and 128 x 256 on 8 waves otherwise */
+    /* block shape by token count and type, from sweeps of every type at its config shape
+     * (14336 x 4096; Q6_K and IQ3_XXS 4096 x 14336, Q8_0 32000 x 4096): up to 32 tokens 32 x 128
+     * tiles on 4 waves (Q4_K M=17 33.4 -> 26.4 us, Q6_K 39.4 -> 28.5, Q8_0 64.5 -> 55.8, IQ3_XXS
+     * 39.0 -> 28.7); 33..64 tokens 64 x 128 on 4 waves for Q6_K and IQ3_XXS, 64 x 256 on 8 waves
+     * otherwise (Q4_K M=64 32.9 -> 30.4 us against 32 x 128); 65..256 tokens 64 x 256 on 8 waves
+     * for Q4_K, Q5_K, Q6_K (and IQ3_XXS up to 128) (M=128: Q4_K 45.1 -> 41.1 us, Q5_K 54.8 -> 44.7,
+     * Q6_K 52.5 -> 48.1, IQ3_XXS 50.1 -> 45.5; M=256: Q4_K 65.9 -> 59.3, Q5_K 79.7 -> 65.5, Q6_K
+     * 81.1 -> 73.5), and so on up to 512 tokens for Q6_K (M=384 124.6 -> 115.3); everything else
+     * 128 x 256 on 8 waves (Q6_K above 512 tokens 128 x 256 on 4 waves) */
     int ci = 5;
+    const bool k4 = ty == LE_TYPE_Q4_K || ty == LE_TYPE_Q5_K || ty == LE_TYPE_Q6_K;
     if (m <= 32) ci = 8;
-    else if (m <= 64) ci = ty == LE_TYPE_Q4_K ? 8 : (ty == LE_TYPE_Q6_K || ty == LE_TYPE_IQ3_XXS) ? 7 : 4;
-    else if (m <= 128 && ty == LE_TYPE_Q4_K) ci = 7;
-    else if (m <= 128 && (ty == LE_TYPE_Q6_K || ty == LE_TYPE_IQ3_XXS)) ci = 9;
-    else if (ty == LE_TYPE_Q6_K) ci = 2;
+    else if (m <= 64) ci = (ty == LE_TYPE_Q6_K || ty == LE_TYPE_IQ3_XXS) ? 7 : 4;
+    else if (m <= 128 && (k4 || ty == LE_TYPE_IQ3_XXS)) ci = 4;
+    else if (m <= 256 && k4) ci = 4;
+    else if (ty == LE_TYPE_Q6_K) ci = m <= 512 ? 4 : 2;
     if (c->gq_cfg) ci = c->gq_cfg - 1;
     const int nsb = cols / 256, srec = gq_srec(ty);
     auto lds_of = [&](int i) {
