@@ -408,18 +408,39 @@ __device__ __forceinline__ void gq_xprep_body(const GqArgs &a, u8 *ws) {
     }
 }
 
+/* Direct-to-LDS loads (gfx950 global_load_lds_dwordx4): the load unit writes lane l's 16 bytes
+ * at M0 + 16 l, so a wave's 64 chunks land as one contiguous 1 KB run with no registers held
+ * while in flight. Issued from inline assembly so the compiler does not wait for them before
+ * every LDS read; the kernel waits for them explicitly (the memory counter retires loads in
+ * issue order). */
+#pragma clang diagnostic push
+#pragma clang diagnostic ignored "-Winline-asm"
+__device__ __forceinline__ void gq_lds_dma16(const u8 *g, u32 lds_addr) {
+    asm volatile("s_mov_b32 m0, %1\n\tglobal_load_lds_dwordx4 %0, off" ::"v"(g), "s"(lds_addr) : "memory", "m0");
+}
+#pragma clang diagnostic pop
+template <int N>
+__device__ __forceinline__ void gq_vm_wait() {
+    static_assert(N >= 0 && N < 64, "vmcnt range");
+    asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory");
+}
+__device__ __forceinline__ u32 gq_lds_addr(const void *p) { return (u32)(size_t)(const __attribute__((address_space(3))) void *)p; }
+
 /* ============================ main kernel ============================ */
-template <int TY, int WM, int WN, int TM, int TN, bool GR = false>
+/* AD: the activation fragments go straight to LDS (a ring of three step slots, loaded two steps
+ * ahead) instead of through registers; the weights keep the register staging. */
+template <int TY, int WM, int WN, int TM, int TN, bool GR = false, bool AD = false>
 __device__ __forceinline__ void gq_body(const GqArgs &a, const u8 *ws) {
     using F = GqF<TY>;
     constexpr int BM = 32 * TM * WM, BN = 32 * TN * WN, NT = 64 * WM * WN;
-    constexpr int WB = BN * F::SLOT, AB = BM * 256, BUF = WB + AB;
+    constexpr int WB = BN * F::SLOT, AB = BM * 256, BUF = AD ? WB : WB + AB, NA = AD ? 3 : 0;
     constexpr int SBYTES = F::SREC ? (BM / 32) * F::SREC : 0; /* per super-block */
     constexpr int NWC = (BN * F::NCH + NT - 1) / NT, NAC = AB / 16 / NT, NSC = (SBYTES / 16 + NT - 1) / NT;
     static_assert(AB / 16 % NT == 0, "activation chunks must divide over the threads");
     extern __shared__ uint4 smem[];
     u8 *lds = (u8 *)smem;
-    u8 *Sl = lds + 2 * BUF;            /* [2][SBYTES] sum records, by super-block parity */
+    u8 *Aring = lds + 2 * BUF;          /* AD: [3][AB] activation step slots */
+    u8 *Sl = lds + 2 * BUF + NA * AB;  /* [2][SBYTES] sum records, by super-block parity */
     u8 *tab = Sl + 2 * SBYTES;          /* IQ tables */
 
     const int K = a.cols, nsb = K >> 8;
@@ -457,7 +478,7 @@ __device__ __forceinline__ void gq_body(const GqArgs &a, const u8 *ws) {
     if constexpr (F::TAB > 0) gq_tables<TY>(tab);
 
     struct Set {
-        uint4 w[NWC], x[NAC], s[NSC > 0 ? NSC : 1];
+        uint4 w[NWC], x[AD ? 1 : NAC], s[NSC > 0 ? NSC : 1];
     };
     /* every load is unconditional (addresses clamped) so the waits before staging count exactly
      * the loads of the step being staged; steps past the slice re-read the last one. Even steps
@@ -491,9 +512,11 @@ __device__ __forceinline__ void gq_body(const GqArgs &a, const u8 *ws) {
             const u8 *p = w0 + (h ? wo1[i] : wo0[i]);
             R.w[i] = F::ALIGNED ? ldg16c(p) : ldg16u(p); /* cached: the next step reads the same lines */
         }
-        const u8 *x0 = Ag + (size_t)(sb * 16 + 8 * h) * 1024;
+        if constexpr (!AD) {
+            const u8 *x0 = Ag + (size_t)(sb * 16 + 8 * h) * 1024;
 #pragma unroll
-        for (int i = 0; i < NAC; i++) R.x[i] = ldg16c(x0 + xo[i]);
+            for (int i = 0; i < NAC; i++) R.x[i] = ldg16c(x0 + xo[i]);
+        }
         if (SBYTES > 0 && even) {
             const u8 *s0p = Sg + (size_t)sb * F::SREC;
 #pragma unroll
@@ -510,8 +533,10 @@ __device__ __forceinline__ void gq_body(const GqArgs &a, const u8 *ws) {
             const int row = c / F::NCH, k = c - row * F::NCH;
             *(uint4 *)(B + row * F::SLOT + F::loff(k)) = R.w[i];
         }
+        if constexpr (!AD) {
 #pragma unroll
-        for (int i = 0; i < NAC; i++) ((uint4 *)(B + WB))[tid + NT * i] = R.x[i];
+            for (int i = 0; i < NAC; i++) ((uint4 *)(B + WB))[tid + NT * i] = R.x[i];
+        }
         if constexpr (SBYTES > 0) {
             if (even) {
 #pragma unroll
@@ -521,6 +546,19 @@ __device__ __forceinline__ void gq_body(const GqArgs &a, const u8 *ws) {
                     ((uint4 *)(Sl + (sb & 1) * SBYTES))[c] = R.s[i];
                 }
             }
+        }
+    };
+
+    /* AD: step s_'s activation fragments into ring slot s_ % 3 (steps past the slice re-read the
+     * last one into a slot that is no longer read) */
+    auto dma = [&](int s_) {
+        if constexpr (AD) {
+            const int s = min(s_, nstep - 1), sb = s >> 1, h = s & 1;
+            const u8 *x0 = Ag + (size_t)(sb * 16 + 8 * h) * 1024;
+            u8 *dst = Aring + (s_ % 3) * AB + 64 * 16 * wave;
+#pragma unroll
+            for (int i = 0; i < NAC; i++) /* the LDS address is uniform over the wave (M0) */
+                gq_lds_dma16(x0 + xo[i], __builtin_amdgcn_readfirstlane(gq_lds_addr(dst + NT * 16 * i)));
         }
     };
 
@@ -539,9 +577,11 @@ __device__ __forceinline__ void gq_body(const GqArgs &a, const u8 *ws) {
     /* the loads must reach the memory pipeline in step order (RA's before RB's, as in the loop),
      * or the wait at the loop head would have to cover both sets: no reordering across issues */
     issue(s0, RB, true);
+    dma(s0);
     stage(s0, RB, true);
     issue(s0 + 1, RA, false);
     __builtin_amdgcn_sched_barrier(0);
+    dma(s0 + 1);
     issue(s0 + 2, RB, true);
     __builtin_amdgcn_sched_barrier(0);
 
@@ -549,8 +589,12 @@ __device__ __forceinline__ void gq_body(const GqArgs &a, const u8 *ws) {
 #pragma unroll
         for (int h = 0; h < 2; h++) {
             const int s = 2 * sb + h;
+            if constexpr (AD) { /* this step's activations: younger are the loads of steps s + 2 (weights) and s + 1 (activations) */
+                if (h == 0) gq_vm_wait<NWC + NAC + (SBYTES > 0 ? NSC : 0)>();
+                else gq_vm_wait<NWC + NAC>();
+            }
             gq_barrier(); /* step s is staged; every wave is done with step s-1's buffer */
-            const u8 *Wb = lds + h * BUF, *Ab = Wb + WB + (wm * TM) * 8192;
+            const u8 *Wb = lds + h * BUF, *Ab = (AD ? Aring + (s % 3) * AB : Wb + WB) + (wm * TM) * 8192;
             const u8 *rs[TN];
 #pragma unroll
             for (int k = 0; k < TN; k++) rs[k] = Wb + (wn * TN * 32 + 32 * k + n) * F::SLOT;
@@ -570,6 +614,7 @@ __device__ __forceinline__ void gq_body(const GqArgs &a, const u8 *ws) {
                 __builtin_amdgcn_sched_barrier(0);
                 if (h) issue(s + 3, RB, true);
                 else issue(s + 3, RA, false);
+                dma(s + 2); /* slot (s + 2) % 3 was last read in step s - 1 */
                 __builtin_amdgcn_sched_barrier(0);
             };
             if constexpr (TY == LE_TYPE_Q4_K) {
@@ -935,6 +980,7 @@ __device__ __forceinline__ void gq_body(const GqArgs &a, const u8 *ws) {
             }
         }
     }
+    if constexpr (AD) gq_vm_wait<0>(); /* no activation load may still be writing LDS */
     /* D lane l element e: token 8 (e / 4) + 4 (l / 32) + e % 4 of the tile, row l % 32; the
      * token scales of the padded tile are all loaded first (one memory round trip) */
     if constexpr (F::EPI == 2) {
@@ -974,7 +1020,7 @@ __device__ __forceinline__ void gq_body(const GqArgs &a, const u8 *ws) {
      * rows (a wave covers 1 KB of one output row) instead of 4-byte stores 32 to a row. */
     float *dst = (!GR && a.ksplit > 1) ? a.part + (size_t)blockIdx.y * a.m * a.rows : second ? a.y2 : a.y;
     constexpr int TS = BN + 8, NQ = BN / 4;
-    static_assert((size_t)WM * 32 * TS * 4 <= (size_t)2 * BUF, "output staging must fit the step buffers");
+    static_assert((size_t)WM * 32 * TS * 4 <= (size_t)2 * BUF + (size_t)NA * AB, "output staging must fit the step buffers");
     float *T = (float *)lds;
     const bool vec = (a.rows & 3) == 0 && ((size_t)dst & 15) == 0;
 #pragma unroll
@@ -1088,10 +1134,15 @@ extern "C" __global__ void __launch_bounds__(1024) le_gq_plan(GqArgs a, u8 *ws, 
     extern "C" __global__ void __launch_bounds__(WM * WN * 64) le_gqg_##TY##_w##WM##WN##_t##TM##TN(GqArgs a, const u8 *ws) { \
         gq_body<TY, WM, WN, TM, TN, true>(a, ws);                                                                        \
     }
+#define LE_GQA_(TY, WM, WN, TM, TN)                                                                                     \
+    extern "C" __global__ void __launch_bounds__(WM * WN * 64) le_gq_##TY##_w##WM##WN##_t##TM##TN##_ad(GqArgs a, const u8 *ws) { \
+        gq_body<TY, WM, WN, TM, TN, false, true>(a, ws);                                                                   \
+    }
 #define LE_GQ(TY) LE_GQ_(TY, 1, 4, 1, 2) LE_GQ_(TY, 1, 4, 2, 2) LE_GQ_(TY, 1, 4, 4, 2) LE_GQ_(TY, 2, 2, 2, 2) \
     LE_GQ_(TY, 1, 8, 2, 1) LE_GQ_(TY, 1, 8, 4, 1) LE_GQ_(TY, 1, 8, 1, 1) LE_GQ_(TY, 1, 4, 2, 1) LE_GQ_(TY, 1, 4, 1, 1) LE_GQ_(TY, 1, 4, 4, 1) LE_GQG_(TY, 1, 8, 2, 1) LE_GQG_(TY, 1, 8, 4, 1) LE_GQG_(TY, 2, 2, 2, 2) LE_GQG_(TY, 1, 8, 1, 1)
 #if LE_GQ_SET == 2
 LE_GQ(2) LE_GQ(11) LE_GQ(13) LE_GQ(22)
 #else
 LE_GQ(8) LE_GQ(12) LE_GQ(14) LE_GQ(16) LE_GQ(18)
+LE_GQ_(12, 2, 4, 2, 2) LE_GQ_(12, 2, 4, 2, 1) LE_GQA_(12, 1, 8, 4, 1) LE_GQA_(12, 1, 8, 2, 1) LE_GQA_(12, 2, 4, 2, 2) LE_GQA_(12, 2, 4, 2, 1)
 #endif

@@ -125,8 +125,10 @@ struct le_ctx {
     int gq_min_m = 9;        /* other types: smallest M on the matrix-core GEMM (below: vector kernels) */
     int gq_cfg = 0;          /* generic GEMM block shape (tokens x rows, waves): 0 auto, 1 (32x256, 4), 2 (64x256, 4),
                                 3 (128x256, 4), 4 (128x128, 4), 5 (64x256, 8), 6 (128x256, 8), 7 (32x256, 8),
-                                8 (64x128, 4), 9 (32x128, 4), 10 (128x128, 4) */
+                                8 (64x128, 4), 9 (32x128, 4), 10 (128x128, 4); Q4_K only: 11 (128x256, 2x4
+                                waves of 64x64), 12 (128x128, 2x4 waves of 64x32) */
     int gq_ksplit = 0;       /* generic GEMM K slices: 0 auto, else 1, 2, 4, 8 */
+    int gq_ad = 0;           /* generic GEMM, activations straight to LDS (the _ad kernels, Q4_K): 0 auto, 1 always, -1 never */
     std::vector<hipModule_t> mods;
     std::map<std::string, hipFunction_t> fns;
     std::string err;
@@ -555,8 +557,11 @@ int le_set_option(le_ctx *c, const char *name, int value) {
         if (value < 1) return c->fail(LE_ERR_ARG, "gq_min_m must be >= 1");
         c->gq_min_m = value;
     } else if (n == "gq_cfg") {
-        if (value < 0 || value > 10) return c->fail(LE_ERR_ARG, "gq_cfg must be 0..10");
+        if (value < 0 || value > 12) return c->fail(LE_ERR_ARG, "gq_cfg must be 0..12");
         c->gq_cfg = value;
+    } else if (n == "gq_ad") {
+        if (value < -1 || value > 1) return c->fail(LE_ERR_ARG, "gq_ad must be -1, 0 or 1");
+        c->gq_ad = value;
     } else if (n == "gq_ksplit") {
         if (value != 0 && value != 1 && value != 2 && value != 4 && value != 8)
             return c->fail(LE_ERR_ARG, "gq_ksplit must be 0, 1, 2, 4 or 8");
@@ -1034,7 +1039,7 @@ static int gq_tab(int ty) {
 static int gq_launch(le_ctx *c, int ty, const void *w, const float *x, int m, float *y, int rows, int cols, void *ws,
                      size_t ws_bytes, hipStream_t st) {
     /* block shapes: (WM, WN, TM, TN) -> BM = 32 TM WM tokens, BN = 32 TN WN rows */
-    static const int cfgs[10][4] = {{1, 4, 1, 2}, {1, 4, 2, 2}, {1, 4, 4, 2}, {2, 2, 2, 2}, {1, 8, 2, 1}, {1, 8, 4, 1}, {1, 8, 1, 1}, {1, 4, 2, 1}, {1, 4, 1, 1}, {1, 4, 4, 1}};
+    static const int cfgs[12][4] = {{1, 4, 1, 2}, {1, 4, 2, 2}, {1, 4, 4, 2}, {2, 2, 2, 2}, {1, 8, 2, 1}, {1, 8, 4, 1}, {1, 8, 1, 1}, {1, 4, 2, 1}, {1, 4, 1, 1}, {1, 4, 4, 1}, {2, 4, 2, 2}, {2, 4, 2, 1}};
     /* block shape by token count and type, from sweeps of every type at its config shape
      * (14336 x 4096; Q6_K and IQ3_XXS 4096 x 14336, Q8_0 32000 x 4096): up to 32 tokens 32 x 128
      * tiles on 4 waves (Q4_K M=17 33.4 -> 26.4 us, Q6_K 39.4 -> 28.5, Q8_0 64.5 -> 55.8, IQ3_XXS
@@ -1051,11 +1056,19 @@ static int gq_launch(le_ctx *c, int ty, const void *w, const float *x, int m, fl
     else if (m <= 128 && (k4 || ty == LE_TYPE_IQ3_XXS)) ci = 4;
     else if (m <= 256 && k4) ci = 4;
     else if (ty == LE_TYPE_Q6_K) ci = m <= 512 ? 4 : 2;
+    /* Q4_K above 128 tokens: activations straight to LDS (bit-identical results), 128 x 256 tiles
+     * on 8 waves up to 256 tokens and 2 x 4 waves of 64 x 64 above (half the LDS activation reads
+     * per MFMA: M=256 69.2 -> 65.9 us, M=512 107.5 -> 100.7) */
+    bool ad = c->gq_ad > 0;
+    if (ty == LE_TYPE_Q4_K && m > 128 && c->gq_ad == 0 && !c->gq_cfg) {
+        ad = true;
+        ci = m > 256 ? 10 : 5;
+    }
     if (c->gq_cfg) ci = c->gq_cfg - 1;
     const int nsb = cols / 256, srec = gq_srec(ty);
     auto lds_of = [&](int i) {
         const int BM = 32 * cfgs[i][0] * cfgs[i][2], BN = 32 * cfgs[i][1] * cfgs[i][3];
-        return (size_t)2 * (BN * gq_slot(ty) + BM * 256) + (size_t)2 * (BM / 32) * srec + gq_tab(ty);
+        return (size_t)2 * BN * gq_slot(ty) + (size_t)(ad ? 3 : 2) * BM * 256 + (size_t)2 * (BM / 32) * srec + gq_tab(ty);
     };
     if (lds_of(ci) > c->lds_limit && (ci == 2 || ci == 5)) ci = 3;
     const size_t lds = lds_of(ci);
@@ -1063,7 +1076,8 @@ static int gq_launch(le_ctx *c, int ty, const void *w, const float *x, int m, fl
     const int WM = cfgs[ci][0], WN = cfgs[ci][1], TM = cfgs[ci][2], TN = cfgs[ci][3];
     const int BM = 32 * TM * WM, BN = 32 * TN * WN, nthr = 64 * WM * WN;
     char name[48];
-    snprintf(name, sizeof name, "le_gq_%d_w%d%d_t%d%d", ty, WM, WN, TM, TN);
+    snprintf(name, sizeof name, "le_gq_%d_w%d%d_t%d%d%s", ty, WM, WN, TM, TN, ad ? "_ad" : "");
+    if (!c->fn(name)) return c->fail(LE_ERR_SHAPE, "GEMM kernel %s is not built", name);
     const long long ntr = (rows + BN - 1) / BN, mt = (m + BM - 1) / BM;
     const long long grid = (ntr >= 8 ? (ntr + 7) / 8 * 8 : ntr) * mt; /* block order: le_gq_kernels.hip */
     if (grid > 0x7FFFFFFFLL) return c->fail(LE_ERR_SHAPE, "GEMM grid too large");
