@@ -1138,11 +1138,15 @@ extern "C" __global__ void __launch_bounds__(1024) le_gq_plan(GqArgs a, u8 *ws, 
     extern "C" __global__ void __launch_bounds__(WM * WN * 64) le_gq_##TY##_w##WM##WN##_t##TM##TN##_ad(GqArgs a, const u8 *ws) { \
         gq_body<TY, WM, WN, TM, TN, false, true>(a, ws);                                                                   \
     }
+#define LE_GQGA_(TY, WM, WN, TM, TN)                                                                                    \
+    extern "C" __global__ void __launch_bounds__(WM * WN * 64) le_gqg_##TY##_w##WM##WN##_t##TM##TN##_ad(GqArgs a, const u8 *ws) { \
+        gq_body<TY, WM, WN, TM, TN, true, true>(a, ws);                                                                     \
+    }
 #define LE_GQ(TY) LE_GQ_(TY, 1, 4, 1, 2) LE_GQ_(TY, 1, 4, 2, 2) LE_GQ_(TY, 1, 4, 4, 2) LE_GQ_(TY, 2, 2, 2, 2) \
     LE_GQ_(TY, 1, 8, 2, 1) LE_GQ_(TY, 1, 8, 4, 1) LE_GQ_(TY, 1, 8, 1, 1) LE_GQ_(TY, 1, 4, 2, 1) LE_GQ_(TY, 1, 4, 1, 1) LE_GQ_(TY, 1, 4, 4, 1) LE_GQG_(TY, 1, 8, 2, 1) LE_GQG_(TY, 1, 8, 4, 1) LE_GQG_(TY, 2, 2, 2, 2) LE_GQG_(TY, 1, 8, 1, 1)
 #if LE_GQ_SET == 2
 LE_GQ(2) LE_GQ(11) LE_GQ(13) LE_GQ(22)
 #else
 LE_GQ(8) LE_GQ(12) LE_GQ(14) LE_GQ(16) LE_GQ(18)
-LE_GQ_(12, 2, 4, 2, 2) LE_GQ_(12, 2, 4, 2, 1) LE_GQA_(12, 1, 8, 4, 1) LE_GQA_(12, 1, 8, 2, 1) LE_GQA_(12, 2, 4, 2, 2) LE_GQA_(12, 2, 4, 2, 1)
+LE_GQ_(12, 2, 4, 2, 2) LE_GQ_(12, 2, 4, 2, 1) LE_GQA_(12, 1, 8, 4, 1) LE_GQA_(12, 1, 8, 2, 1) LE_GQA_(12, 2, 4, 2, 2) LE_GQA_(12, 2, 4, 2, 1) LE_GQGA_(12, 1, 8, 4, 1) LE_GQGA_(12, 1, 8, 2, 1)
 #endif

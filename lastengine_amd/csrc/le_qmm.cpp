@@ -1149,9 +1149,12 @@ static int mm_grouped(le_ctx *c, int ty, const void *const *ptrs, const void *w,
     static const int cfgs[7][4] = {{1, 4, 1, 2}, {1, 4, 2, 2}, {1, 4, 4, 2}, {2, 2, 2, 2}, {1, 8, 2, 1}, {1, 8, 4, 1}, {1, 8, 1, 1}};
     int ci = mmg_cfg(nslot, npair);
     const int srec = gq_srec(ty);
+    /* Q4_K on 128-pair tiles: activations straight to LDS, as le_gemm above 128 tokens (MoE
+     * prefill at 2048 tokens 764 -> 729 us; the 64-pair tiles gain nothing: gq_ad=1 forces it) */
+    const bool ad = ty == LE_TYPE_Q4_K && (ci == 5 || (ci == 4 && c->gq_ad > 0)) && c->gq_ad >= 0;
     auto lds_of = [&](int i) {
         const int BM = 32 * cfgs[i][0] * cfgs[i][2], BN = 32 * cfgs[i][1] * cfgs[i][3];
-        return (size_t)2 * (BN * gq_slot(ty) + BM * 256) + (size_t)2 * (BM / 32) * srec + gq_tab(ty);
+        return (size_t)2 * BN * gq_slot(ty) + (size_t)(ad ? 3 : 2) * BM * 256 + (size_t)2 * (BM / 32) * srec + gq_tab(ty);
     };
     if (lds_of(ci) > c->lds_limit) ci = 3; /* 128 x 128 on 4 waves */
     const int WM = cfgs[ci][0], WN = cfgs[ci][1], TM = cfgs[ci][2], TN = cfgs[ci][3];
@@ -1174,7 +1177,7 @@ static int mm_grouped(le_ctx *c, int ty, const void *const *ptrs, const void *w,
     snprintf(name, sizeof name, "le_gq_xprepg_%d", ty);
     rc = c->launch(name, dim3((unsigned)npair), 256, 0, (hipStream_t)stream, args); /* one block per pair */
     if (rc) return rc;
-    snprintf(name, sizeof name, "le_gqg_%d_w%d%d_t%d%d", ty, WM, WN, TM, TN);
+    snprintf(name, sizeof name, "le_gqg_%d_w%d%d_t%d%d%s", ty, WM, WN, TM, TN, ad && ci != 3 ? "_ad" : "");
     return c->launch(name, dim3((unsigned)grid), nthr, lds_of(ci), (hipStream_t)stream, args);
 }
 
