@@ -427,19 +427,25 @@ __device__ __forceinline__ void gq_vm_wait() {
 __device__ __forceinline__ u32 gq_lds_addr(const void *p) { return (u32)(size_t)(const __attribute__((address_space(3))) void *)p; }
 
 /* ============================ main kernel ============================ */
-/* AD: the activation fragments go straight to LDS (a ring of three step slots, loaded two steps
- * ahead) instead of through registers; the weights keep the register staging. */
-template <int TY, int WM, int WN, int TM, int TN, bool GR = false, bool AD = false>
+/* NA > 0: the activation fragments go straight to LDS, a ring of NA step slots (2: loaded one
+ * step ahead, issued as the step starts, in the LDS the register-staged form uses for them; 3:
+ * two steps ahead, with the weights' loads) instead of through registers; the weights keep the
+ * register staging. Every launched kernel uses NA = 2 (measured against registers at M=512: Q4_K
+ * 109 -> 95 us, Q6_K 147 -> 114, Q8_0 252 -> 230, IQ2_XXS 98 -> 92; the three-slot ring 100 us for
+ * Q4_K); the results are the same bits in every form. */
+template <int TY, int WM, int WN, int TM, int TN, bool GR = false, int NA = 0>
 __device__ __forceinline__ void gq_body(const GqArgs &a, const u8 *ws) {
     using F = GqF<TY>;
+    constexpr bool AD = NA > 0;
+    static_assert(NA == 0 || NA == 2 || NA == 3, "activation ring of 2 or 3 slots");
     constexpr int BM = 32 * TM * WM, BN = 32 * TN * WN, NT = 64 * WM * WN;
-    constexpr int WB = BN * F::SLOT, AB = BM * 256, BUF = AD ? WB : WB + AB, NA = AD ? 3 : 0;
+    constexpr int WB = BN * F::SLOT, AB = BM * 256, BUF = AD ? WB : WB + AB;
     constexpr int SBYTES = F::SREC ? (BM / 32) * F::SREC : 0; /* per super-block */
     constexpr int NWC = (BN * F::NCH + NT - 1) / NT, NAC = AB / 16 / NT, NSC = (SBYTES / 16 + NT - 1) / NT;
     static_assert(AB / 16 % NT == 0, "activation chunks must divide over the threads");
     extern __shared__ uint4 smem[];
     u8 *lds = (u8 *)smem;
-    u8 *Aring = lds + 2 * BUF;          /* AD: [3][AB] activation step slots */
+    u8 *Aring = lds + 2 * BUF;          /* NA > 0: [NA][AB] activation step slots */
     u8 *Sl = lds + 2 * BUF + NA * AB;  /* [2][SBYTES] sum records, by super-block parity */
     u8 *tab = Sl + 2 * SBYTES;          /* IQ tables */
 
@@ -549,13 +555,13 @@ __device__ __forceinline__ void gq_body(const GqArgs &a, const u8 *ws) {
         }
     };
 
-    /* AD: step s_'s activation fragments into ring slot s_ % 3 (steps past the slice re-read the
-     * last one into a slot that is no longer read) */
+    /* NA > 0: step s_'s activation fragments into ring slot s_ % NA (steps past the slice re-read
+     * the last one into a slot that is no longer read) */
     auto dma = [&](int s_) {
         if constexpr (AD) {
             const int s = min(s_, nstep - 1), sb = s >> 1, h = s & 1;
             const u8 *x0 = Ag + (size_t)(sb * 16 + 8 * h) * 1024;
-            u8 *dst = Aring + (s_ % 3) * AB + 64 * 16 * wave;
+            u8 *dst = Aring + (s_ % (NA > 0 ? NA : 1)) * AB + 64 * 16 * wave;
 #pragma unroll
             for (int i = 0; i < NAC; i++) /* the LDS address is uniform over the wave (M0) */
                 gq_lds_dma16(x0 + xo[i], __builtin_amdgcn_readfirstlane(gq_lds_addr(dst + NT * 16 * i)));
@@ -581,7 +587,7 @@ __device__ __forceinline__ void gq_body(const GqArgs &a, const u8 *ws) {
     stage(s0, RB, true);
     issue(s0 + 1, RA, false);
     __builtin_amdgcn_sched_barrier(0);
-    dma(s0 + 1);
+    if constexpr (NA == 3) dma(s0 + 1);
     issue(s0 + 2, RB, true);
     __builtin_amdgcn_sched_barrier(0);
 
@@ -589,12 +595,18 @@ __device__ __forceinline__ void gq_body(const GqArgs &a, const u8 *ws) {
 #pragma unroll
         for (int h = 0; h < 2; h++) {
             const int s = 2 * sb + h;
-            if constexpr (AD) { /* this step's activations: younger are the loads of steps s + 2 (weights) and s + 1 (activations) */
+            /* this step's activations: younger are the loads of steps s + 2 (weights) and, with
+             * three slots, s + 1 (activations) */
+            if constexpr (NA == 3) {
                 if (h == 0) gq_vm_wait<NWC + NAC + (SBYTES > 0 ? NSC : 0)>();
                 else gq_vm_wait<NWC + NAC>();
+            } else if constexpr (NA == 2) {
+                if (h == 0) gq_vm_wait<NWC + (SBYTES > 0 ? NSC : 0)>();
+                else gq_vm_wait<NWC>();
             }
             gq_barrier(); /* step s is staged; every wave is done with step s-1's buffer */
-            const u8 *Wb = lds + h * BUF, *Ab = (AD ? Aring + (s % 3) * AB : Wb + WB) + (wm * TM) * 8192;
+            if constexpr (NA == 2) dma(s + 1); /* slot (s + 1) % 2 was last read in step s - 1 */
+            const u8 *Wb = lds + h * BUF, *Ab = (AD ? Aring + (s % (NA > 0 ? NA : 1)) * AB : Wb + WB) + (wm * TM) * 8192;
             const u8 *rs[TN];
 #pragma unroll
             for (int k = 0; k < TN; k++) rs[k] = Wb + (wn * TN * 32 + 32 * k + n) * F::SLOT;
@@ -614,7 +626,7 @@ __device__ __forceinline__ void gq_body(const GqArgs &a, const u8 *ws) {
                 __builtin_amdgcn_sched_barrier(0);
                 if (h) issue(s + 3, RB, true);
                 else issue(s + 3, RA, false);
-                dma(s + 2); /* slot (s + 2) % 3 was last read in step s - 1 */
+                if constexpr (NA == 3) dma(s + 2); /* slot (s + 2) % 3 was last read in step s - 1 */
                 __builtin_amdgcn_sched_barrier(0);
             };
             if constexpr (TY == LE_TYPE_Q4_K) {
@@ -1128,19 +1140,11 @@ extern "C" __global__ void __launch_bounds__(1024) le_gq_plan(GqArgs a, u8 *ws, 
 
 #define LE_GQ_(TY, WM, WN, TM, TN)                                                                                     \
     extern "C" __global__ void __launch_bounds__(WM * WN * 64) le_gq_##TY##_w##WM##WN##_t##TM##TN(GqArgs a, const u8 *ws) { \
-        gq_body<TY, WM, WN, TM, TN>(a, ws);                                                                            \
+        gq_body<TY, WM, WN, TM, TN, false, 2>(a, ws);                                                                  \
     }
 #define LE_GQG_(TY, WM, WN, TM, TN)                                                                                     \
     extern "C" __global__ void __launch_bounds__(WM * WN * 64) le_gqg_##TY##_w##WM##WN##_t##TM##TN(GqArgs a, const u8 *ws) { \
-        gq_body<TY, WM, WN, TM, TN, true>(a, ws);                                                                        \
-    }
-#define LE_GQA_(TY, WM, WN, TM, TN)                                                                                     \
-    extern "C" __global__ void __launch_bounds__(WM * WN * 64) le_gq_##TY##_w##WM##WN##_t##TM##TN##_ad(GqArgs a, const u8 *ws) { \
-        gq_body<TY, WM, WN, TM, TN, false, true>(a, ws);                                                                   \
-    }
-#define LE_GQGA_(TY, WM, WN, TM, TN)                                                                                    \
-    extern "C" __global__ void __launch_bounds__(WM * WN * 64) le_gqg_##TY##_w##WM##WN##_t##TM##TN##_ad(GqArgs a, const u8 *ws) { \
-        gq_body<TY, WM, WN, TM, TN, true, true>(a, ws);                                                                     \
+        gq_body<TY, WM, WN, TM, TN, true, 2>(a, ws);                                                                     \
     }
 #define LE_GQ(TY) LE_GQ_(TY, 1, 4, 1, 2) LE_GQ_(TY, 1, 4, 2, 2) LE_GQ_(TY, 1, 4, 4, 2) LE_GQ_(TY, 2, 2, 2, 2) \
     LE_GQ_(TY, 1, 8, 2, 1) LE_GQ_(TY, 1, 8, 4, 1) LE_GQ_(TY, 1, 8, 1, 1) LE_GQ_(TY, 1, 4, 2, 1) LE_GQ_(TY, 1, 4, 1, 1) LE_GQ_(TY, 1, 4, 4, 1) LE_GQG_(TY, 1, 8, 2, 1) LE_GQG_(TY, 1, 8, 4, 1) LE_GQG_(TY, 2, 2, 2, 2) LE_GQG_(TY, 1, 8, 1, 1)
@@ -1148,5 +1152,5 @@ extern "C" __global__ void __launch_bounds__(1024) le_gq_plan(GqArgs a, u8 *ws, 
 LE_GQ(2) LE_GQ(11) LE_GQ(13) LE_GQ(22)
 #else
 LE_GQ(8) LE_GQ(12) LE_GQ(14) LE_GQ(16) LE_GQ(18)
-LE_GQ_(12, 2, 4, 2, 2) LE_GQ_(12, 2, 4, 2, 1) LE_GQA_(12, 1, 8, 4, 1) LE_GQA_(12, 1, 8, 2, 1) LE_GQA_(12, 2, 4, 2, 2) LE_GQA_(12, 2, 4, 2, 1) LE_GQGA_(12, 1, 8, 4, 1) LE_GQGA_(12, 1, 8, 2, 1)
+LE_GQ_(12, 2, 4, 2, 2) LE_GQ_(12, 2, 4, 2, 1)
 #endif

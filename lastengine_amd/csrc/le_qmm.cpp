@@ -128,7 +128,6 @@ struct le_ctx {
                                 8 (64x128, 4), 9 (32x128, 4), 10 (128x128, 4); Q4_K only: 11 (128x256, 2x4
                                 waves of 64x64), 12 (128x128, 2x4 waves of 64x32) */
     int gq_ksplit = 0;       /* generic GEMM K slices: 0 auto, else 1, 2, 4, 8 */
-    int gq_ad = 0;           /* generic GEMM, activations straight to LDS (the _ad kernels, Q4_K): 0 auto, 1 always, -1 never */
     std::vector<hipModule_t> mods;
     std::map<std::string, hipFunction_t> fns;
     std::string err;
@@ -559,9 +558,6 @@ int le_set_option(le_ctx *c, const char *name, int value) {
     } else if (n == "gq_cfg") {
         if (value < 0 || value > 12) return c->fail(LE_ERR_ARG, "gq_cfg must be 0..12");
         c->gq_cfg = value;
-    } else if (n == "gq_ad") {
-        if (value < -1 || value > 1) return c->fail(LE_ERR_ARG, "gq_ad must be -1, 0 or 1");
-        c->gq_ad = value;
     } else if (n == "gq_ksplit") {
         if (value != 0 && value != 1 && value != 2 && value != 4 && value != 8)
             return c->fail(LE_ERR_ARG, "gq_ksplit must be 0, 1, 2, 4 or 8");
@@ -1041,34 +1037,25 @@ static int gq_launch(le_ctx *c, int ty, const void *w, const float *x, int m, fl
     /* block shapes: (WM, WN, TM, TN) -> BM = 32 TM WM tokens, BN = 32 TN WN rows */
     static const int cfgs[12][4] = {{1, 4, 1, 2}, {1, 4, 2, 2}, {1, 4, 4, 2}, {2, 2, 2, 2}, {1, 8, 2, 1}, {1, 8, 4, 1}, {1, 8, 1, 1}, {1, 4, 2, 1}, {1, 4, 1, 1}, {1, 4, 4, 1}, {2, 4, 2, 2}, {2, 4, 2, 1}};
     /* block shape by token count and type, from sweeps of every type at its config shape
-     * (14336 x 4096; Q6_K and IQ3_XXS 4096 x 14336, Q8_0 32000 x 4096): up to 32 tokens 32 x 128
-     * tiles on 4 waves (Q4_K M=17 33.4 -> 26.4 us, Q6_K 39.4 -> 28.5, Q8_0 64.5 -> 55.8, IQ3_XXS
-     * 39.0 -> 28.7); 33..64 tokens 64 x 128 on 4 waves for Q6_K and IQ3_XXS, 64 x 256 on 8 waves
-     * otherwise (Q4_K M=64 32.9 -> 30.4 us against 32 x 128); 65..256 tokens 64 x 256 on 8 waves
-     * for Q4_K, Q5_K, Q6_K (and IQ3_XXS up to 128) (M=128: Q4_K 45.1 -> 41.1 us, Q5_K 54.8 -> 44.7,
-     * Q6_K 52.5 -> 48.1, IQ3_XXS 50.1 -> 45.5; M=256: Q4_K 65.9 -> 59.3, Q5_K 79.7 -> 65.5, Q6_K
-     * 81.1 -> 73.5), and so on up to 512 tokens for Q6_K (M=384 124.6 -> 115.3); everything else
-     * 128 x 256 on 8 waves (Q6_K above 512 tokens 128 x 256 on 4 waves) */
+     * (14336 x 4096; Q6_K and IQ3_XXS 4096 x 14336, Q8_0 32000 x 4096), activations loaded straight
+     * into LDS: up to 32 tokens 32 x 128 tiles on 4 waves; 33..64 tokens 64 x 128 on 4 waves for
+     * Q6_K and IQ3_XXS, 64 x 256 on 8 waves otherwise; 65..128 tokens 128 x 128 on 4 waves for
+     * Q6_K (M=128 47.6 -> 46.3 us against 64 x 256), 64 x 256 on 8 waves for Q4_K, Q5_K and
+     * IQ3_XXS (M=128 against 128 x 256: Q4_K 44.8 -> 40.9, Q5_K 46.1 -> 43.0); 129..256 tokens
+     * 64 x 256 on 8 waves for Q4_K and Q5_K; everything else 128 x 256 on 8 waves (Q6_K M=256 72.8
+     * -> 66.0 us and M=512 126.5 -> 107.8 against 64 x 256) */
     int ci = 5;
-    const bool k4 = ty == LE_TYPE_Q4_K || ty == LE_TYPE_Q5_K || ty == LE_TYPE_Q6_K;
+    const bool k45 = ty == LE_TYPE_Q4_K || ty == LE_TYPE_Q5_K;
     if (m <= 32) ci = 8;
     else if (m <= 64) ci = (ty == LE_TYPE_Q6_K || ty == LE_TYPE_IQ3_XXS) ? 7 : 4;
-    else if (m <= 128 && (k4 || ty == LE_TYPE_IQ3_XXS)) ci = 4;
-    else if (m <= 256 && k4) ci = 4;
-    else if (ty == LE_TYPE_Q6_K) ci = m <= 512 ? 4 : 2;
-    /* Q4_K above 128 tokens: activations straight to LDS (bit-identical results), 128 x 256 tiles
-     * on 8 waves up to 256 tokens and 2 x 4 waves of 64 x 64 above (half the LDS activation reads
-     * per MFMA: M=256 69.2 -> 65.9 us, M=512 107.5 -> 100.7) */
-    bool ad = c->gq_ad > 0;
-    if (ty == LE_TYPE_Q4_K && m > 128 && c->gq_ad == 0 && !c->gq_cfg) {
-        ad = true;
-        ci = m > 256 ? 10 : 5;
-    }
+    else if (m <= 128 && ty == LE_TYPE_Q6_K) ci = 9;
+    else if (m <= 128 && (k45 || ty == LE_TYPE_IQ3_XXS)) ci = 4;
+    else if (m <= 256 && k45) ci = 4;
     if (c->gq_cfg) ci = c->gq_cfg - 1;
     const int nsb = cols / 256, srec = gq_srec(ty);
     auto lds_of = [&](int i) {
         const int BM = 32 * cfgs[i][0] * cfgs[i][2], BN = 32 * cfgs[i][1] * cfgs[i][3];
-        return (size_t)2 * BN * gq_slot(ty) + (size_t)(ad ? 3 : 2) * BM * 256 + (size_t)2 * (BM / 32) * srec + gq_tab(ty);
+        return (size_t)2 * (BN * gq_slot(ty) + BM * 256) + (size_t)2 * (BM / 32) * srec + gq_tab(ty);
     };
     if (lds_of(ci) > c->lds_limit && (ci == 2 || ci == 5)) ci = 3;
     const size_t lds = lds_of(ci);
@@ -1076,7 +1063,7 @@ static int gq_launch(le_ctx *c, int ty, const void *w, const float *x, int m, fl
     const int WM = cfgs[ci][0], WN = cfgs[ci][1], TM = cfgs[ci][2], TN = cfgs[ci][3];
     const int BM = 32 * TM * WM, BN = 32 * TN * WN, nthr = 64 * WM * WN;
     char name[48];
-    snprintf(name, sizeof name, "le_gq_%d_w%d%d_t%d%d%s", ty, WM, WN, TM, TN, ad ? "_ad" : "");
+    snprintf(name, sizeof name, "le_gq_%d_w%d%d_t%d%d", ty, WM, WN, TM, TN);
     if (!c->fn(name)) return c->fail(LE_ERR_SHAPE, "GEMM kernel %s is not built", name);
     const long long ntr = (rows + BN - 1) / BN, mt = (m + BM - 1) / BM;
     const long long grid = (ntr >= 8 ? (ntr + 7) / 8 * 8 : ntr) * mt; /* block order: le_gq_kernels.hip */
@@ -1149,12 +1136,9 @@ static int mm_grouped(le_ctx *c, int ty, const void *const *ptrs, const void *w,
     static const int cfgs[7][4] = {{1, 4, 1, 2}, {1, 4, 2, 2}, {1, 4, 4, 2}, {2, 2, 2, 2}, {1, 8, 2, 1}, {1, 8, 4, 1}, {1, 8, 1, 1}};
     int ci = mmg_cfg(nslot, npair);
     const int srec = gq_srec(ty);
-    /* Q4_K on 128-pair tiles: activations straight to LDS, as le_gemm above 128 tokens (MoE
-     * prefill at 2048 tokens 764 -> 729 us; the 64-pair tiles gain nothing: gq_ad=1 forces it) */
-    const bool ad = ty == LE_TYPE_Q4_K && (ci == 5 || (ci == 4 && c->gq_ad > 0)) && c->gq_ad >= 0;
     auto lds_of = [&](int i) {
         const int BM = 32 * cfgs[i][0] * cfgs[i][2], BN = 32 * cfgs[i][1] * cfgs[i][3];
-        return (size_t)2 * BN * gq_slot(ty) + (size_t)(ad ? 3 : 2) * BM * 256 + (size_t)2 * (BM / 32) * srec + gq_tab(ty);
+        return (size_t)2 * (BN * gq_slot(ty) + BM * 256) + (size_t)2 * (BM / 32) * srec + gq_tab(ty);
     };
     if (lds_of(ci) > c->lds_limit) ci = 3; /* 128 x 128 on 4 waves */
     const int WM = cfgs[ci][0], WN = cfgs[ci][1], TM = cfgs[ci][2], TN = cfgs[ci][3];
@@ -1177,7 +1161,7 @@ static int mm_grouped(le_ctx *c, int ty, const void *const *ptrs, const void *w,
     snprintf(name, sizeof name, "le_gq_xprepg_%d", ty);
     rc = c->launch(name, dim3((unsigned)npair), 256, 0, (hipStream_t)stream, args); /* one block per pair */
     if (rc) return rc;
-    snprintf(name, sizeof name, "le_gqg_%d_w%d%d_t%d%d%s", ty, WM, WN, TM, TN, ad && ci != 3 ? "_ad" : "");
+    snprintf(name, sizeof name, "le_gqg_%d_w%d%d_t%d%d", ty, WM, WN, TM, TN);
     return c->launch(name, dim3((unsigned)grid), nthr, lds_of(ci), (hipStream_t)stream, args);
 }
 

@@ -334,11 +334,11 @@ def test_options_validated(fresh_engine):
     good = {"mv_block": 512, "mv_blocks_per_cu": 1, "mv_shape": 0, "mq": 1, "ms": 1, "mq_waves": 4, "mq_steps": 2,
             "mq_blocks_per_cu": 2, "mq_waves_auto": 1, "ms_p": 2, "ms_p6": 2, "ms_piq": 2, "mq6": 1, "mqiq": 1, "ms_t": 1, "gm_mh": 1, "gm_mh_shape": 0, "gm_mh_max": 16, "gm_min_m": 5,
             "gm_tile": 0, "gm_ksplit": 0, "gm_pc": 1, "gm_split": 0, "moe_mfma": 1, "moe_fused": 1, "moe_fused_min_tok": 3,
-            "moe_fast": 1, "gq": 1, "gq_min_m": 9, "gq_cfg": 0, "gq_ksplit": 0, "gq_ad": 0}
+            "moe_fast": 1, "gq": 1, "gq_min_m": 9, "gq_cfg": 0, "gq_ksplit": 0}
     engine = fresh_engine
     for k, v in good.items():
         engine.set_option(k, v)
-    for k, v in [("no_such_option", 1), ("gm_tile", 33), ("gm_ksplit", 3), ("gm_split", 2), ("gm_mh_shape", 13), ("gm_mh_max", 12), ("ms_p6", 4), ("ms_piq", 3), ("gq_cfg", 13), ("gq_ad", 2), ("gq_ksplit", 3), ("gq_min_m", 0)]:
+    for k, v in [("no_such_option", 1), ("gm_tile", 33), ("gm_ksplit", 3), ("gm_split", 2), ("gm_mh_shape", 13), ("gm_mh_max", 12), ("ms_p6", 4), ("ms_piq", 3), ("gq_cfg", 13), ("gq_ksplit", 3), ("gq_min_m", 0)]:
         with pytest.raises(le.LeError) as e:
             engine.set_option(k, v)
         assert e.value.code == -1, (k, v)
