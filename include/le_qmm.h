@@ -93,8 +93,9 @@ const char *le_last_error(const le_ctx *ctx);
  *     per MFMA pass), used by le_gemm below "gm_min_m" tokens
  *   GEMM: "gq" (0/1) Q4_K on the generic matrix-core GEMM (default) or the older le_gm kernels,
  *     "gq_min_m" smallest M of the other types on the matrix-core GEMM (below: vector kernels that
- *     read the weights once per 8 tokens), "gq_cfg" its block shape (0 auto; 1..6: 32x256, 64x256,
- *     128x256, 128x128 tokens x rows on 4 waves, 64x256 and 128x256 on 8 waves), "gq_ksplit" its K
+ *     read the weights once per 8 tokens), "gq_cfg" its block shape (0 auto; 1..10: 32x256, 64x256,
+ *     128x256, 128x128 tokens x rows on 4 waves, 64x256, 128x256, 32x256 on 8 waves, 64x128, 32x128,
+ *     128x128 on 4 waves; Q4_K only, 2 x 4 waves: 11 128x256, 12 128x128), "gq_ksplit" its K
  *     slices (0 auto, 1, 2, 4, 8);
  *     "gm_mh" (0/1) Q4_K with 3..16 tokens on the staged f16 MFMA kernel (tokens as MFMA rows),
  *     "gm_mh_max" its largest M (16, the default, where K <= 4096 fits its LDS; or 8),
