@@ -1799,8 +1799,14 @@ struct MoeArgs {
     const u8 *const *gptr, *const *uptr, *const *dptr;
 };
 /* Expert e's weights: its pointer-table entry, or its slab in the 3D tensor. */
+/* Expert e's weights: slab e of a 3D tensor, or entry e of a device pointer table. e is uniform
+ * over the wave at every call site, so the table entry is read with a scalar load: a vector load
+ * there made the compiler wait for every vector load in flight (activations, images) before the
+ * weight loads could be issued, on the slab path as well. */
 __device__ __forceinline__ const u8 *moe_w(const u8 *slab, const u8 *const *ptrs, int e, size_t expert_bytes) {
-    return ptrs ? ptrs[e] : slab + (size_t)e * expert_bytes;
+    if (!ptrs) return slab + (size_t)e * expert_bytes;
+    typedef const u8 *wptr;
+    return ((const __attribute__((address_space(4))) wptr *)ptrs)[__builtin_amdgcn_readfirstlane(e)];
 }
 /* Barrier area at the start of the workspace: a status word (sticky, nonzero after a wait gave
  * up; read and cleared by le_moe_check), the generation word, then one arrival flag per block. */
@@ -2784,15 +2790,6 @@ __device__ __forceinline__ void moe_gum_body(const MoeArgs &a) {
     if (z >= R.U) return; /* uniform over the block */
     const int e = R.grp_e[z];
     const int nmem = __popcll(R.mask[e]);
-    if (blockIdx.x == 0 && z == 0) {
-        for (int i = threadIdx.x; i < a.n_tok * a.k; i += blockDim.x) {
-            if (a.idx_out) a.idx_out[i] = R.topi[i];
-            if (a.w_out) a.w_out[i] = R.topw[i];
-        }
-        moe_rec_write(a, R, a.ws + (size_t)a.n_tok * a.k * LE_MOE_IMG(a.ff));
-        /* the down launch may split a row tile over two blocks that add into the output */
-        for (int i = threadIdx.x; i < a.n_tok * a.hidden; i += blockDim.x) a.out[i] = 0.f;
-    }
     /* 2. the four tiles of this wave's super-blocks (gate rows 32ux.., +16, up rows 32ux.., +16),
      * packed: chunk c = (tile, row, column) of 4 x 16 x CPR, all in flight at once */
     const size_t rb = (size_t)NSB * 144;
@@ -2804,6 +2801,17 @@ __device__ __forceinline__ void moe_gum_body(const MoeArgs &a) {
         const int c = min(64 * i + lane, NCH - 1), ti = c / (16 * CPR), rem = c % (16 * CPR), col = rem % CPR;
         Rg[i] = ldg16((ti < 2 ? Wg : Wu) + (size_t)(32 * ux + 16 * (ti & 1) + rem / CPR) * rb + (size_t)wave * P * 144 +
                       (col == 9 * P ? 0 : col) * 16);
+    }
+    /* block (0,0) also writes the routing outputs and record, and clears the output (the down
+     * launch may split a row tile over two blocks that add into it), after issuing its weights so
+     * those stores do not delay them */
+    if (blockIdx.x == 0 && z == 0) {
+        for (int i = threadIdx.x; i < a.n_tok * a.k; i += blockDim.x) {
+            if (a.idx_out) a.idx_out[i] = R.topi[i];
+            if (a.w_out) a.w_out[i] = R.topw[i];
+        }
+        moe_rec_write(a, R, a.ws + (size_t)a.n_tok * a.k * LE_MOE_IMG(a.ff));
+        for (int i = threadIdx.x; i < a.n_tok * a.hidden; i += blockDim.x) a.out[i] = 0.f;
     }
     /* 3. token images (the Q4_K slice map) and the group's members */
 #pragma unroll
@@ -2911,11 +2919,14 @@ __device__ __forceinline__ void moe_dnm_body(const MoeArgs &a) {
     uint4 iv[2][4];
     static_assert(LE_MOE_DN_IMGS * IMGC <= 8 * 64 * NW, "the image preload covers every image chunk");
     const int nci = npair * IMGC;
-    if (all_in) {
+    if (all_in) { /* only the rounds that hold image chunks (uniform over the block): clamped
+                     * re-reads of the last chunk had queued 4.5x the image bytes at one token
+                     * ahead of the weight loads */
 #pragma unroll
         for (int u = 0; u < 2; u++)
 #pragma unroll
-            for (int q = 0; q < 4; q++) iv[u][q] = ldg16c(a.ws + 16 * (size_t)min((int)threadIdx.x + 64 * NW * (4 * u + q), nci - 1));
+            for (int q = 0; q < 4; q++)
+                if (64 * NW * (4 * u + q) < nci) iv[u][q] = ldg16c(a.ws + 16 * (size_t)min((int)threadIdx.x + 64 * NW * (4 * u + q), nci - 1));
     }
     /* the routing of the gate/up launch (n_tok * k <= 64 <= blockDim.x, groups <= 64) */
     moe_rec_read(a, R, a.ws + (size_t)a.n_tok * a.k * IMG);
