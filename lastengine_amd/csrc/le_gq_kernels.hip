@@ -492,6 +492,7 @@ __device__ __forceinline__ void gq_body(const GqArgs &a, const u8 *ws) {
     /* per-thread 32-bit load offsets, computed once (the host keeps a slice's weights and the
      * activation planes below 4 GiB): so each load is a scalar base plus one of these */
     u32 wo0[NWC], wo1[NWC], xo[NAC], so[NSC > 0 ? NSC : 1];
+    bool xlive[NAC];
 #pragma unroll
     for (int i = 0; i < NWC; i++) {
         const int c = min(tid + NT * i, BN * F::NCH - 1), row = c / F::NCH, k = c - row * F::NCH;
@@ -503,6 +504,7 @@ __device__ __forceinline__ void gq_body(const GqArgs &a, const u8 *ws) {
     for (int i = 0; i < NAC; i++) {
         const int c = tid + NT * i, tl = c >> 9, off = c & 511; /* 512 chunks = 8 KB per 32-token tile */
         xo[i] = (u32)(mb / 32 + tl) * (u32)(K / 16) * 1024u + 16u * off;
+        xlive[i] = mb + 32 * tl + (off & 31) < M; /* fragment lane l holds token l % 32 */
     }
 #pragma unroll
     for (int i = 0; i < (NSC > 0 ? NSC : 1); i++) {
@@ -563,8 +565,13 @@ __device__ __forceinline__ void gq_body(const GqArgs &a, const u8 *ws) {
             const u8 *x0 = Ag + (size_t)(sb * 16 + 8 * h) * 1024;
             u8 *dst = Aring + (s_ % (NA > 0 ? NA : 1)) * AB + 64 * 16 * wave;
 #pragma unroll
-            for (int i = 0; i < NAC; i++) /* the LDS address is uniform over the wave (M0) */
-                gq_lds_dma16(x0 + xo[i], __builtin_amdgcn_readfirstlane(gq_lds_addr(dst + NT * 16 * i)));
+            for (int i = 0; i < NAC; i++) { /* the LDS address is uniform over the wave (M0) */
+                const u32 la = __builtin_amdgcn_readfirstlane(gq_lds_addr(dst + NT * 16 * i));
+                /* lanes of tokens past the tile's last one load nothing: their LDS bytes only
+                 * reach output rows that are never stored, and a 128-byte line holds 8 tokens,
+                 * so a sparse tile (grouped form) fetches a quarter of the lines per valid 8 */
+                if (xlive[i]) gq_lds_dma16(x0 + xo[i], la);
+            }
         }
     };
 
