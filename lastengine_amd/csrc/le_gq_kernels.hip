@@ -90,9 +90,58 @@ struct GqArgs {
  * (mp floats). */
 __host__ __device__ inline size_t gq_s_off(int mp, int K) { return (size_t)mp * K * 2; }
 __host__ __device__ inline size_t gq_t_off(int mp, int K, int srec) { return gq_s_off(mp, K) + (size_t)(mp / 32) * (K / 256) * srec; }
-/* grouped form: the tile list after the token scales: int count, pad to 16 B, int slot[maxt], int first[maxt],
- * then each slot's first tile, int tfirst[nslot] */
-__host__ __device__ inline size_t gq_l_off(int mp, int K, int srec) { return gq_t_off(mp, K, srec) + (size_t)mp * 4; }
+
+/* Tiles of the grouped form: slot s has off[s+1] - off[s] pairs, split into tiles of bm, listed
+ * slot by slot. Each wave derives what it needs from off itself (no planning launch): the slots'
+ * counts are loaded 256 at a time, all in flight together, then scanned across the wave. */
+__device__ __forceinline__ int gq_wave_scan(int v) { /* inclusive prefix sum over the wave, by DPP */
+    v += __builtin_amdgcn_update_dpp(0, v, 0x111, 0xF, 0xF, true); /* row_shr:1 (rows of 16 lanes) */
+    v += __builtin_amdgcn_update_dpp(0, v, 0x112, 0xF, 0xF, true); /* row_shr:2 */
+    v += __builtin_amdgcn_update_dpp(0, v, 0x114, 0xF, 0xF, true); /* row_shr:4 */
+    v += __builtin_amdgcn_update_dpp(0, v, 0x118, 0xF, 0xF, true); /* row_shr:8 */
+    v += __builtin_amdgcn_update_dpp(0, v, 0x142, 0xA, 0xF, false); /* row_bcast:15 into rows 1, 3 */
+    v += __builtin_amdgcn_update_dpp(0, v, 0x143, 0xC, 0xF, false); /* row_bcast:31 into rows 2, 3 */
+    return v;
+}
+/* Walk the slots 256 at a time (every load of a round in flight together), each lane holding one
+ * slot's first pair o0, its tile count c and the number of tiles before it; stop at the first
+ * slot for which hit(o0, o1, first, c) holds on some lane. Returns that slot (or -1) and, through
+ * the references, its first pair and first tile. Uniform over the wave. */
+template <class Hit>
+__device__ __forceinline__ int gq_slot_walk(const int *__restrict__ off, int nslot, int bm, Hit hit, int &o0_out, int &first_out) {
+    const int lane = threadIdx.x & 63;
+    int base = 0;
+    for (int s0 = 0; s0 < nslot; s0 += 256) {
+        int o0[4], o1[4];
+#pragma unroll
+        for (int q = 0; q < 4; q++) {
+            const int s = min(s0 + 64 * q + lane, nslot - 1);
+            o0[q] = off[s];
+            o1[q] = off[s + 1];
+        }
+#pragma unroll
+        for (int q = 0; q < 4; q++) {
+            const bool in = s0 + 64 * q + lane < nslot;
+            const int c = in ? (max(o1[q] - o0[q], 0) + bm - 1) / bm : 0, inc = gq_wave_scan(c), first = base + inc - c;
+            const unsigned long long h = __ballot(in && c > 0 && hit(o0[q], o1[q], first, c));
+            if (h) {
+                const int l = __ffsll((long long)h) - 1;
+                o0_out = __shfl(o0[q], l);
+                first_out = __shfl(first, l);
+                return s0 + 64 * q + l;
+            }
+            base += __shfl(inc, 63);
+        }
+    }
+    return -1;
+}
+/* tile mt: its slot and first pair (false past the last tile) */
+__device__ __forceinline__ bool gq_tile_of(const int *__restrict__ off, int nslot, int bm, int mt, int &slot, int &pair0) {
+    int o0, first;
+    slot = gq_slot_walk(off, nslot, bm, [mt](int, int, int f, int c) { return mt >= f && mt < f + c; }, o0, first);
+    pair0 = o0 + (mt - first) * bm;
+    return slot >= 0;
+}
 
 __device__ __forceinline__ le_h2 as_h2(u32 v) { return __builtin_bit_cast(le_h2, v); }
 __device__ __forceinline__ u32 as_u32(le_h2 v) { return __builtin_bit_cast(u32, v); }
@@ -272,24 +321,20 @@ __device__ __forceinline__ void gq_xprep_body(const GqArgs &a, u8 *ws) {
     bool live = t < a.m;
     size_t src = t;
     if constexpr (GR) {
-        /* one block per pair p: its slot s (off[s] <= p < off[s+1], by bisection), then its
-         * position tfirst[s] * bm + (p - off[s]) among the planned tiles */
-        constexpr int srec_ = SK == 1 ? 1024 : 0;
-        const int *lst = (const int *)(ws + gq_l_off(a.mp, K, srec_));
+        /* one block per pair p (the grid is npair blocks): its slot s (off[s] <= p < off[s+1]),
+         * then its position first_tile(s) * bm + (p - off[s]) among the tiles; the pair's token
+         * index loads with the slots' offsets */
         const int p = blockIdx.x;
+        const int srcp = a.in_idx[p];
         live = false;
-        if (p >= a.off[0] && p < a.off[a.nslot]) {
-            int lo = 0, hi = a.nslot;
-            while (hi - lo > 1) {
-                const int mid = (lo + hi) >> 1;
-                if (a.off[mid] <= p) lo = mid;
-                else hi = mid;
-            }
-            const int j = p - a.off[lo], tile = lst[4 + 2 * a.maxt + lo] + j / a.bm;
-            if (j >= 0 && p < a.off[lo + 1] && tile < lst[0]) {
+        int o0, first;
+        const int lo = gq_slot_walk(a.off, a.nslot, a.bm, [p](int b, int e, int, int) { return p >= b && p < e; }, o0, first);
+        if (lo >= 0) {
+            const int j = p - o0, tile = first + j / a.bm;
+            if (tile < a.maxt) {
                 live = true;
                 t = tile * a.bm + j % a.bm;
-                src = (size_t)a.in_idx[p];
+                src = (size_t)srcp;
             }
         }
     }
@@ -462,10 +507,8 @@ __device__ __forceinline__ void gq_body(const GqArgs &a, const u8 *ws) {
     int M = a.m, pair0 = 0;
     const u8 *Wsrc = a.w;
     if constexpr (GR) {
-        const int *lst = (const int *)(ws + gq_l_off(a.mp, K, F::SREC));
-        if (mt >= lst[0]) return; /* uniform: past the planned tiles */
-        const int sl = lst[4 + mt];
-        pair0 = lst[4 + a.maxt + mt];
+        int sl;
+        if (!gq_tile_of(a.off, a.nslot, a.bm, mt, sl, pair0)) return; /* uniform: past the last tile */
         M = mb + min(BM, a.off[sl + 1] - pair0); /* token t of the tile is valid while t < M */
         if (second)
             Wsrc = a.ptrs2 ? a.ptrs2[sl] : a.w2 + (size_t)sl * a.w_slot_bytes;
@@ -1112,37 +1155,6 @@ extern "C" __global__ void __launch_bounds__(256) le_gq_ksum(GqArgs a) {
     }
 }
 
-/* Plan of the grouped form: slot s has off[s+1] - off[s] pairs, split into tiles of bm; the
- * tiles are listed slot by slot (count, then slot and first pair of each) in the workspace. One
- * block of 1024 threads; slots are taken 1024 at a time with a running base. */
-extern "C" __global__ void __launch_bounds__(1024) le_gq_plan(GqArgs a, u8 *ws, int srec) {
-    __shared__ int scan[1024];
-    int *lst = (int *)(ws + gq_l_off(a.mp, a.cols, srec));
-    int base = 0;
-    for (int s0 = 0; s0 < a.nslot; s0 += 1024) {
-        const int s = s0 + (int)threadIdx.x;
-        const int n = s < a.nslot ? (max(a.off[s + 1] - a.off[s], 0) + a.bm - 1) / a.bm : 0;
-        scan[threadIdx.x] = n;
-        __syncthreads();
-        for (int o = 1; o < 1024; o <<= 1) { /* inclusive Hillis-Steele scan */
-            const int v = threadIdx.x >= (unsigned)o ? scan[threadIdx.x - o] : 0;
-            __syncthreads();
-            scan[threadIdx.x] += v;
-            __syncthreads();
-        }
-        const int first = base + scan[threadIdx.x] - n;
-        if (s < a.nslot) lst[4 + 2 * a.maxt + s] = first; /* the slot's first tile */
-        for (int q = 0; q < n; q++) {
-            if (first + q < a.maxt) {
-                lst[4 + first + q] = s;
-                lst[4 + a.maxt + first + q] = a.off[s] + q * a.bm;
-            }
-        }
-        base += scan[1023];
-        __syncthreads();
-    }
-    if (threadIdx.x == 0) lst[0] = min(base, a.maxt);
-}
 #endif
 
 #define LE_GQ_(TY, WM, WN, TM, TN)                                                                                     \

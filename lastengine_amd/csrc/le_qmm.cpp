@@ -1115,7 +1115,7 @@ static int mmg_maxt(int nslot, int npair) { const int bm = mmg_bm(nslot, npair);
 size_t le_mm_grouped_workspace_size(int ty, int nslot, int npair, int cols) {
     if (!supported_mv(ty) || nslot <= 0 || npair < 0 || cols <= 0 || cols % 256) return 0;
     const size_t maxt = (size_t)mmg_maxt(nslot, npair), mp = maxt * mmg_bm(nslot, npair);
-    return mp * cols * 2 + mp / 32 * (cols / 256) * gq_srec(ty) + mp * 4 + 16 + 8 * maxt + 4 * (size_t)nslot;
+    return mp * cols * 2 + mp / 32 * (cols / 256) * gq_srec(ty) + mp * 4;
 }
 
 /* Grouped matmul; with a second weight set (ptrs2 or w2, same type and shape) the same pairs are
@@ -1152,14 +1152,12 @@ static int mm_grouped(le_ctx *c, int ty, const void *const *ptrs, const void *w,
         return c->fail(LE_ERR_SHAPE, "grouped GEMM too large (32-bit weight or activation offsets)");
     GqHostArgs a{w, x, y, rows, cols, mp, mp, 1, ptrs, (unsigned long long)rows * le_row_bytes(ty, cols), off, in_idx,
                  out_idx, nslot, maxt, BM, 0, nullptr, ptrs2, w2, y2, dual ? 1 : 0, 0, up};
-    int srec_arg = srec;
-    void *pargs[] = {&a, &ws, &srec_arg};
-    int rc = c->launch("le_gq_plan", dim3(1), 1024, 0, (hipStream_t)stream, pargs);
-    if (rc) return rc;
+    /* the tiles (slots split into BM pairs, slot by slot) are derived from off inside the two
+     * launches, each block finding its own */
     void *args[] = {&a, &ws};
     char name[48];
     snprintf(name, sizeof name, "le_gq_xprepg_%d", ty);
-    rc = c->launch(name, dim3((unsigned)npair), 256, 0, (hipStream_t)stream, args); /* one block per pair */
+    int rc = c->launch(name, dim3((unsigned)npair), 256, 0, (hipStream_t)stream, args); /* one block per pair */
     if (rc) return rc;
     snprintf(name, sizeof name, "le_gqg_%d_w%d%d_t%d%d", ty, WM, WN, TM, TN);
     return c->launch(name, dim3((unsigned)grid), nthr, lds_of(ci), (hipStream_t)stream, args);
