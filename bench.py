@@ -232,7 +232,7 @@ def bench_moe(eng, n_tok, steps, warmup, n_exp=128, k=8, hidden=2048, ff=768, co
     h = torch.from_numpy(le.fill_normal(n_tok * hidden, 299)).cuda()
     out = torch.empty(n_tok * hidden, dtype=torch.float32, device="cuda")
     nws = eng.moe_workspace_size(n_tok, k, ff)
-    if n_tok >= 16:  # room for the grouped form, which takes 16 tokens and more
+    if n_tok >= 11:  # room for the grouped form, which takes 11 tokens and more
         nws = max(nws, eng.moe_prefill_workspace_size(n_tok, k, n_exp, hidden, ff))
     ws = torch.zeros(nws, dtype=torch.uint8, device="cuda")
     n_launch = copies * variants

@@ -229,12 +229,12 @@ int le_gemm_noalloc(le_ctx *ctx, int ty, const void *w, const float *x, int m, f
  * (IQ2_XXS, IQ2_XXS), (IQ3_XXS, IQ3_XXS) run the grouped form below at every token count and need
  * le_moe_prefill_workspace_size bytes).
  * Limits: n_tok <= 65536, k <= 16, n_exp <= 256, hidden and ff multiples of 256.
- * Prefill-sized calls (more than 64 tokens; from 16 tokens when ws holds
+ * Prefill-sized calls (more than 64 tokens; from 11 tokens when ws holds
  * le_moe_prefill_workspace_size bytes) route every token, group the (token, expert) pairs by
  * expert on the device (token order within an expert) and run the three projections as grouped
  * matrix-core matmuls (le_mm_grouped), so each expert's weights are streamed once per tile of up
  * to 128 of its pairs; ws must then hold le_moe_prefill_workspace_size bytes. Decode-sized calls
- * need le_moe_workspace_size bytes; 9..15 tokens (or up to 64 without the grouped form's workspace)
+ * need le_moe_workspace_size bytes; 9..10 tokens (or up to 64 without the grouped form's workspace)
  * run as consecutive calls of at most 8 tokens, each of which streams its own routed experts.
  * For 3..8 tokens at hidden 2048 the layer runs as one launch with a device-wide barrier between
  * gate/up and down. That launch sizes its grid to the blocks that fit on the device at once and

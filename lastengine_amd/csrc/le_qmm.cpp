@@ -109,9 +109,9 @@ struct le_ctx {
     int moe_fused_min_tok = 3; /* ... from this many tokens on (below, two launches are faster) */
     unsigned int moe_spin_limit = 1u << 20; /* polls before a barrier wait gives up (about a second); 0 fails it */
     int moe_prefill = 1;        /* grouped matrix-core form for larger token counts (forced above 64) */
-    int moe_prefill_min_tok = 16; /* ... from this many tokens, when the workspace is sized for it (config 4, 8-token
-                                     decode calls against the grouped form: 12 tokens 117 / 124 us, 16 tokens 137 / 131,
-                                     20 tokens 184 / 152, 24 tokens 203 / 164) */
+    int moe_prefill_min_tok = 11; /* ... from this many tokens, when the workspace is sized for it (config 4, 8-token
+                                     decode calls against the grouped form: 10 tokens 99.6 / 102.3 us, 12 tokens
+                                     116.8 / 109.0, 14 tokens 128.5 / 112.9, 16 tokens 117.7 / 116.8) */
     int moe_dn_split = 0;    /* down launch blocks per row tile: 0 auto, 1, 2 */
     std::map<std::string, int> occ; /* resident blocks per CU, by kernel name and LDS bytes */
     int gm_min_m = 5;        /* le_gemm uses the MFMA GEMM from this many tokens on (below: the
