@@ -194,7 +194,7 @@ int le_stream_read_sink_bytes(le_ctx *ctx);
  * ptrs is NULL, w + s * rows * row_bytes (expert slab s of a 3D tensor). off (nslot + 1 ints),
  * in_idx and out_idx (npair ints) are device arrays; npair = off[nslot] - off[0] is the caller's
  * bound on the pairs (the reference's host-side grouping knows it). Runs on the matrix cores for
- * every type, each slot's weights streamed once per tile of 64 or 128 of its pairs, with the
+ * every type, each slot's weights streamed once per tile of 32, 64 or 128 of its pairs, with the
  * same activation numerics as le_gemm. Output rows of different pairs must differ. ws: device
  * workspace of le_mm_grouped_workspace_size(ty, nslot, npair, cols) bytes. */
 size_t le_mm_grouped_workspace_size(int ty, int nslot, int npair, int cols);
