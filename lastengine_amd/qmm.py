@@ -226,7 +226,7 @@ class Engine:
         if ws is None:
             import torch
             n = self.moe_workspace_size(n_tok, k, ff)
-            if n_tok >= 16 or (ty_gate, ty_down) not in MOE_DECODE_PAIRS:
+            if n_tok >= 11 or (ty_gate, ty_down) not in MOE_DECODE_PAIRS:
                 n = max(n, self.moe_prefill_workspace_size(n_tok, k, n_exp, hidden, ff))
             ws = torch.zeros(max(16, n), dtype=torch.uint8, device="cuda")
         if ws_bytes is None:
@@ -241,7 +241,7 @@ class Engine:
         if ws is None:
             import torch
             n = self.moe_workspace_size(n_tok, k, ff)
-            if n_tok >= 16 or (ty_gate, ty_down) not in MOE_DECODE_PAIRS:
+            if n_tok >= 11 or (ty_gate, ty_down) not in MOE_DECODE_PAIRS:
                 n = max(n, self.moe_prefill_workspace_size(n_tok, k, n_exp, hidden, ff))
             ws = torch.zeros(max(16, n), dtype=torch.uint8, device="cuda")
         if ws_bytes is None:

@@ -100,3 +100,36 @@ def test_moe_pointer_tables(engine, n_tok):
     a, b = out1.cpu().numpy(), out2.cpu().numpy()
     assert np.all(np.isfinite(a))
     assert np.array_equal(a.view(np.uint32), b.view(np.uint32))
+
+
+@pytest.mark.parametrize("name", ["Q4_K", "Q6_K"])
+def test_mm_grouped_many_slots(engine, name):
+    """More slots than one round of the blocks' slot walk (256 per round): pairs only in a few
+    slots on both sides of the round and wave boundaries (63/64, 255/256), one slot spanning two
+    32-pair tiles, the rest empty."""
+    import torch
+    ty = le.MV_TYPES[name]
+    nslot, rows, cols, n_src = 300, 128, 512, 64
+    counts = [0] * nslot
+    for s, c in ((0, 3), (63, 1), (64, 9), (255, 2), (256, 40), (257, 1), (299, 5)):
+        counts[s] = c
+    print("mm_grouped many slots", name, flush=True)
+    q = wbytes(ty, nslot * rows, cols, seed=90 + ty)
+    xs = np.stack([acts(cols, 8800 + t) for t in range(n_src)])
+    off, in_idx, out_idx = grouping(counts, n_src, seed=ty)
+    npair = int(off[-1])
+    y = torch.full((npair, rows), float("nan"), dtype=torch.float32, device="cuda")
+    engine.mm_grouped(ty, dev(off), dev(in_idx), dev(out_idx), nslot, npair, dev(xs), y, rows, cols, w=dev(q))
+    torch.cuda.synchronize()
+    got = y.cpu().numpy()
+    rbs = le.row_bytes(ty, cols) * rows
+    for s in range(nslot):
+        lo, hi = off[s], off[s + 1]
+        if hi == lo:
+            continue
+        slab = q.reshape(-1)[s * rbs:(s + 1) * rbs]
+        xsel = xs[in_idx[lo:hi]]
+        want = oracle.matmat(ty, slab, rows, cols, xsel)
+        wf = oracle.dequant_rows(ty, slab, rows, cols).astype(np.float64)
+        mag = np.abs(xsel.astype(np.float64)) @ np.abs(wf).T
+        check_close(got[out_idx[lo:hi]], want, mag)

@@ -196,9 +196,10 @@ def test_moe_limits(engine):
     run(engine, le.Q4_K, le.Q6_K, 32, 16, 256, 256, 64, seed=700)
 
 
-@pytest.mark.parametrize("n_tok", [16, 64])
+@pytest.mark.parametrize("n_tok", [10, 12, 16, 23, 64])
 def test_moe_config4_more_tokens(engine, n_tok):
-    """Config 4 beyond the decode-shaped kernels (the vector member-chunk path)."""
+    """Config 4 beyond one call of the decode-shaped kernels: 8-token decode calls up to 10 tokens,
+    the grouped form (each routed expert streamed once per tile of its pairs) from 11."""
     run(engine, le.Q4_K, le.Q6_K, 128, 8, 2048, 768, n_tok, seed=720 + n_tok)
 
 
