@@ -947,9 +947,9 @@ static int mh_launch(le_ctx *c, const void *w, const float *x, int m, float *y, 
     /* above 8 tokens: groups of 8 tokens whose blocks stream the same row tiles side by side
      * (option gm_mh_t16 = 1: one 16-token group, whose images need 128 KB of LDS at K = 4096) */
     const int nsb = cols / 256, T = m <= 4 ? 4 : m <= 8 || !c->gm_mh_t16 ? 8 : 16, G = (m + T - 1) / T;
-    /* (P, NW) in order of preference, measured on 14336 x 4096 (T=4: 15.0 us with (2,4); T=8:
-     * 16.4 us with (1,8)) */
-    static const int k4[4][2] = {{2, 4}, {1, 4}, {1, 8}, {2, 2}}, k8[4][2] = {{1, 8}, {2, 4}, {1, 4}, {2, 2}};
+    /* (P, NW) in order of preference, measured on 14336 x 4096 (T=4, 3..4 tokens: 12.8 us with
+     * (1,8) against 13.2 with (2,4), 13.5 with (1,4); T=8: 14.0 us with (1,8)) */
+    static const int k4[4][2] = {{1, 8}, {2, 4}, {1, 4}, {2, 2}}, k8[4][2] = {{1, 8}, {2, 4}, {1, 4}, {2, 2}};
     static const int k16[4][2] = {{1, 4}, {1, 8}, {2, 4}, {2, 2}};
     const int(*cand)[2] = T == 4 ? k4 : T == 8 ? k8 : k16;
     const int ncand = 4;
