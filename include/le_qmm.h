@@ -236,7 +236,7 @@ int le_gemm_noalloc(le_ctx *ctx, int ty, const void *w, const float *x, int m, f
  * to 128 of its pairs; ws must then hold le_moe_prefill_workspace_size bytes. Decode-sized calls
  * need le_moe_workspace_size bytes; 9..10 tokens (or up to 64 without the grouped form's workspace)
  * run as consecutive calls of at most 8 tokens, each of which streams its own routed experts.
- * For 3..8 tokens at hidden 2048 the layer runs as one launch with a device-wide barrier between
+ * For 5..8 tokens at hidden 2048 the layer runs as one launch with a device-wide barrier between
  * gate/up and down. That launch sizes its grid to the blocks that fit on the device at once and
  * assumes nothing else occupies it: a concurrent kernel on another stream can make its bounded
  * waits (about a second, option "moe_spin_limit") give up, and the launch then writes NaN to out

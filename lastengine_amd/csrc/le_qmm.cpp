@@ -106,7 +106,8 @@ struct le_ctx {
     int moe_chunk = 1;       /* decode-form MoE above 8 tokens: consecutive calls of at most 8 tokens */
     int moe_mfma = 1;        /* decode-shaped MoE on the staged MFMA kernels where the types allow */
     int moe_fused = 1;       /* ... in one launch with a device-wide barrier where the grid fits */
-    int moe_fused_min_tok = 3; /* ... from this many tokens on (below, two launches are faster) */
+    int moe_fused_min_tok = 5; /* ... from this many tokens on (config 4, two launches against one: 3 / 4 tokens
+                                  41.5 / 47.1 us against 43.0 / 48.3, 5 tokens 61.2 against 55.1) */
     unsigned int moe_spin_limit = 1u << 20; /* polls before a barrier wait gives up (about a second); 0 fails it */
     int moe_prefill = 1;        /* grouped matrix-core form for larger token counts (forced above 64) */
     int moe_prefill_min_tok = 11; /* ... from this many tokens, when the workspace is sized for it (config 4, 8-token

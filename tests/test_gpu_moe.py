@@ -57,7 +57,7 @@ def run(engine, tg, td, n_exp, k, hidden, ff, n_tok, seed, lg=None, rand=False, 
     check_close(out.cpu().numpy(), want, mag)
 
 
-@pytest.mark.parametrize("n_tok", [1, 3, 8])
+@pytest.mark.parametrize("n_tok", [1, 3, 5, 8])
 def test_moe_small(engine, n_tok):
     run(engine, le.Q4_K, le.Q6_K, 16, 4, 256, 256, n_tok, seed=10 + n_tok)
 

@@ -1,4 +1,4 @@
-"""The one-launch MoE layer's device-wide barrier (3..8 tokens at hidden 2048): a forced give-up is
+"""The one-launch MoE layer's device-wide barrier (5..8 tokens at hidden 2048): a forced give-up is
 reported (NaN outputs, le_moe_check -> LE_ERR_TIMEOUT) and leaves nothing behind that breaks the
 next call; launches on different workspaces keep separate barrier state. The give-up is forced
 from the host with a zero spin limit, so every kernel still exits normally."""
@@ -35,7 +35,7 @@ def call(engine, g, u, d, h, lg, ws):
 def test_barrier_give_up_then_recover(fresh_engine):
     import torch
     engine = fresh_engine
-    n_tok = 4
+    n_tok = 5
     g, u, d, h, lg = inputs(n_tok, 500)
     dg, du, dd, dh, dl = dev(g), dev(u), dev(d), dev(h), dev(lg)
     ws = torch.empty(engine.moe_workspace_size(n_tok, K, FF), dtype=torch.uint8, device="cuda")
@@ -62,7 +62,7 @@ def test_barrier_separate_workspaces(fresh_engine):
     import torch
     engine = fresh_engine
     cases = []
-    for n_tok, seed in ((3, 600), (8, 610)):
+    for n_tok, seed in ((5, 600), (8, 610)):
         g, u, d, h, lg = inputs(n_tok, seed)
         ws = torch.empty(engine.moe_workspace_size(n_tok, K, FF), dtype=torch.uint8, device="cuda")
         want, _, _, mag = reference(TG, TD, g, u, d, N_EXP, K, HIDDEN, FF, h, lg)
@@ -82,7 +82,7 @@ def test_barrier_graph_replays(fresh_engine):
     would let the second replay's barrier pass at once and read the previous replay's images)."""
     import torch
     engine = fresh_engine
-    n_tok = 4
+    n_tok = 5
     g, u, d, h0, lg = inputs(n_tok, 700)
     dg, du, dd, dl = dev(g), dev(u), dev(d), dev(lg)
     dh = dev(h0)
