@@ -75,7 +75,7 @@ struct GqArgs {
     const u8 *const *ptrs;
     unsigned long long w_slot_bytes;
     const int *off, *in_idx, *out_idx;
-    int nslot, maxt, bm, pad;
+    int nslot, maxt, bm, npair; /* grouped form: npair pairs (the pre-pass's grid) */
     float *part; /* [ksplit][m][rows] partial results of the K slices, or null */
     /* grouped form, dual: a second weight set (ptrs2 or w2, same type and shape) applied to the same
      * pairs, written to y2 (the MoE gate and up projections in one launch) */
@@ -303,6 +303,48 @@ __device__ __forceinline__ void gq_tables(u8 *tab) {
 }
 
 /* ============================ activation pre-pass ============================ */
+/* pre-pass: group g (8 values 8g..8g+7 = chunk g / 2, half g & 1) of padded token t, scaled by sc,
+ * into the fp16 fragments A and (SK) the sum records S. The 2 or 4 lanes of one sum are g's
+ * neighbours in the same wave, all inside or all outside the row (K % 256 == 0). */
+template <int SK>
+__device__ __forceinline__ void gq_xconvert(int g, float4 p, float4 q, float sc, int t, int K, _Float16 *A, u8 *S) {
+    constexpr int SREC = SK == 1 ? 1024 : 2048;
+    const int nsb = K >> 8, tile = t >> 5, tl = t & 31;
+    float v[8] = {p.x * sc, p.y * sc, p.z * sc, p.w * sc, q.x * sc, q.y * sc, q.z * sc, q.w * sc};
+    const le_h2 h0 = {(_Float16)v[0], (_Float16)v[2]}, h1 = {(_Float16)v[1], (_Float16)v[3]};
+    const le_h2 h2 = {(_Float16)v[4], (_Float16)v[6]}, h3 = {(_Float16)v[5], (_Float16)v[7]};
+    const size_t off = ((((size_t)tile * (K / 16) + (g >> 1)) * 2 + (g & 1)) * 32 + tl) * 8;
+    *(LE_GLOBAL uint4 *)(A + off) = make_uint4(as_u32(h0), as_u32(h1), as_u32(h2), as_u32(h3));
+    if constexpr (SK != 0) {
+        /* g runs over consecutive lanes, so the groups of one sum are neighbouring lanes */
+        /* sums of the fp16-rounded values the MFMA sees, so that the mins term cancels the
+         * scale term's share of the rounding exactly: the result is then sum w * x~ with
+         * error relative to sum |w x|, not to sum |sc q x| */
+        float r[8];
+#pragma unroll
+        for (int i = 0; i < 8; i++) r[i] = (float)(_Float16)v[i];
+        float s = ((r[0] + r[1]) + (r[2] + r[3])) + ((r[4] + r[5]) + (r[6] + r[7]));
+        s += __shfl_xor(s, 1);
+        if constexpr (SK == 1) s += __shfl_xor(s, 2);
+        const int span = SK == 1 ? 4 : 2;
+        if ((g & (span - 1)) == 0) {
+            const int sb = g >> 5, j = (g & 31) / span; /* sum index within the super-block */
+            const _Float16 hi = (_Float16)s, lo = (_Float16)(s - (float)hi);
+            _Float16 *rec = (_Float16 *)(S + ((size_t)tile * nsb + sb) * SREC);
+            /* position P8(j % 8) (P8 is its own inverse), the order of the B2 operand */
+            const int pj = (j & 4) | ((j & 1) << 1) | ((j >> 1) & 1);
+            if constexpr (SK == 1) { /* [hs][token][8]: hs 0 high halves, hs 1 low halves */
+                rec[tl * 8 + pj] = hi;
+                rec[256 + tl * 8 + pj] = lo;
+            } else { /* [f][hs][token][8]: f 0 high, f 1 low; hs = j / 8 */
+                rec[((j >> 3) * 32 + tl) * 8 + pj] = hi;
+                rec[512 + ((j >> 3) * 32 + tl) * 8 + pj] = lo;
+            }
+        }
+    }
+}
+
+
 /* One block of 256 threads per (padded) token, or per pair in the grouped form. SK: 0 no sums, 1 per-32 sums (Q4_K), 2 per-16
  * sums (Q6_K). */
 template <int SK, bool GR = false>
@@ -387,45 +429,8 @@ __device__ __forceinline__ void gq_xprep_body(const GqArgs &a, u8 *ws) {
     }
     const float sc = live ? ldexpf(1.f, -ex) : 0.f;
     _Float16 *A = (_Float16 *)ws;
-    const int tile = t >> 5, tl = t & 31;
-    constexpr int SREC = SK == 1 ? 1024 : 2048;
     u8 *S = ws + gq_s_off(a.mp, K);
-    /* group g = 8 values 8g..8g+7 = chunk g/2, half g&1. ng % 32 == 0 (K % 256 == 0), so the 2 or
-     * 4 lanes of one sum below are all inside or all outside ng */
-    auto convert = [&](int g, float4 p, float4 q) {
-        float v[8] = {p.x * sc, p.y * sc, p.z * sc, p.w * sc, q.x * sc, q.y * sc, q.z * sc, q.w * sc};
-        const le_h2 h0 = {(_Float16)v[0], (_Float16)v[2]}, h1 = {(_Float16)v[1], (_Float16)v[3]};
-        const le_h2 h2 = {(_Float16)v[4], (_Float16)v[6]}, h3 = {(_Float16)v[5], (_Float16)v[7]};
-        const size_t off = ((((size_t)tile * (K / 16) + (g >> 1)) * 2 + (g & 1)) * 32 + tl) * 8;
-        *(LE_GLOBAL uint4 *)(A + off) = make_uint4(as_u32(h0), as_u32(h1), as_u32(h2), as_u32(h3));
-        if constexpr (SK != 0) {
-            /* g runs over consecutive lanes, so the groups of one sum are neighbouring lanes */
-            /* sums of the fp16-rounded values the MFMA sees, so that the mins term cancels the
-             * scale term's share of the rounding exactly: the result is then sum w * x~ with
-             * error relative to sum |w x|, not to sum |sc q x| */
-            float r[8];
-#pragma unroll
-            for (int i = 0; i < 8; i++) r[i] = (float)(_Float16)v[i];
-            float s = ((r[0] + r[1]) + (r[2] + r[3])) + ((r[4] + r[5]) + (r[6] + r[7]));
-            s += __shfl_xor(s, 1);
-            if constexpr (SK == 1) s += __shfl_xor(s, 2);
-            const int span = SK == 1 ? 4 : 2;
-            if ((g & (span - 1)) == 0) {
-                const int sb = g >> 5, j = (g & 31) / span; /* sum index within the super-block */
-                const _Float16 hi = (_Float16)s, lo = (_Float16)(s - (float)hi);
-                _Float16 *rec = (_Float16 *)(S + ((size_t)tile * nsb + sb) * SREC);
-                /* position P8(j % 8) (P8 is its own inverse), the order of the B2 operand */
-                const int pj = (j & 4) | ((j & 1) << 1) | ((j >> 1) & 1);
-                if constexpr (SK == 1) { /* [hs][token][8]: hs 0 high halves, hs 1 low halves */
-                    rec[tl * 8 + pj] = hi;
-                    rec[256 + tl * 8 + pj] = lo;
-                } else { /* [f][hs][token][8]: f 0 high, f 1 low; hs = j / 8 */
-                    rec[((j >> 3) * 32 + tl) * 8 + pj] = hi;
-                    rec[512 + ((j >> 3) * 32 + tl) * 8 + pj] = lo;
-                }
-            }
-        }
-    };
+    auto convert = [&](int g, float4 p, float4 q) { gq_xconvert<SK>(g, p, q, sc, t, K, A, S); };
     if (inreg) {
 #pragma unroll
         for (int i = 0; i < XG; i++) {
@@ -448,8 +453,65 @@ __device__ __forceinline__ void gq_xprep_body(const GqArgs &a, u8 *ws) {
         }
     }
     if (tid == 0) {
-        constexpr int srec = SK == 0 ? 0 : SREC;
+        constexpr int srec = SK == 0 ? 0 : SK == 1 ? 1024 : 2048;
         ((float *)(ws + gq_t_off(a.mp, K, srec)))[t] = live ? ldexpf(1.f, ex) : 0.f;
+    }
+}
+
+/* Grouped form, K <= 4096: one wave per pair (four per block), each lane holding up to 8 groups of
+ * the pair's row; the largest magnitude by a wave reduction (no block barrier), then the same
+ * conversion as gq_xprep_body, so the same bits. */
+template <int SK>
+__device__ __forceinline__ void gq_xprepw_body(const GqArgs &a, u8 *ws) {
+    const int K = a.cols, lane = threadIdx.x & 63;
+    const int p = (int)blockIdx.x * 4 + (int)(threadIdx.x >> 6);
+    if (p >= a.npair) return; /* wave-uniform; no block barrier below */
+    const int srcp = a.in_idx[p]; /* loads with the slots' offsets */
+    int o0, first;
+    const int lo = gq_slot_walk(a.off, a.nslot, a.bm, [p](int b, int e, int, int) { return p >= b && p < e; }, o0, first);
+    if (lo < 0) return;
+    const int j = p - o0, tile = first + j / a.bm;
+    if (tile >= a.maxt) return;
+    const int t = tile * a.bm + j % a.bm;
+    const LE_GLOBAL float *xr = (const LE_GLOBAL float *)(a.x + (size_t)srcp * K);
+    constexpr int XW = 8;
+    const int ng = K / 8;
+    float4 P[XW], Q[XW];
+    float am = 0.f;
+#pragma unroll
+    for (int i = 0; i < XW; i++) {
+        const int g = lane + 64 * i;
+        if (g < ng) {
+            P[i] = ((const LE_GLOBAL float4 *)xr)[2 * g];
+            Q[i] = ((const LE_GLOBAL float4 *)xr)[2 * g + 1];
+            if (a.up) {
+                const LE_GLOBAL float4 *ur = (const LE_GLOBAL float4 *)(a.up + (size_t)srcp * K);
+                P[i] = le_silu_mul4(P[i], ur[2 * g]);
+                Q[i] = le_silu_mul4(Q[i], ur[2 * g + 1]);
+            }
+        } else {
+            P[i] = Q[i] = make_float4(0.f, 0.f, 0.f, 0.f);
+        }
+        am = fmaxf(am, amax8(P[i], Q[i]));
+    }
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) am = fmaxf(am, __shfl_xor(am, o));
+    int ex = 0;
+    if (am > 0.f && am <= 3.0e38f) {
+        (void)frexpf(am, &ex); /* am = f 2^ex, f in [0.5, 1) */
+        ex = max(ex - 7, -100);
+    }
+    const float sc = ldexpf(1.f, -ex);
+    _Float16 *A = (_Float16 *)ws;
+    u8 *S = ws + gq_s_off(a.mp, K);
+#pragma unroll
+    for (int i = 0; i < XW; i++) {
+        const int g = lane + 64 * i;
+        if (g < ng) gq_xconvert<SK>(g, P[i], Q[i], sc, t, K, A, S); /* ng % 32 == 0: a sum's lanes are all in or all out */
+    }
+    if (lane == 0) {
+        constexpr int srec = SK == 0 ? 0 : SK == 1 ? 1024 : 2048;
+        ((float *)(ws + gq_t_off(a.mp, K, srec)))[t] = ldexpf(1.f, ex);
     }
 }
 
@@ -1116,7 +1178,8 @@ __device__ __forceinline__ void gq_body(const GqArgs &a, const u8 *ws) {
 
 #define LE_GQX(TY, SK) \
     extern "C" __global__ void __launch_bounds__(256) le_gq_xprep_##TY(GqArgs a, u8 *ws) { gq_xprep_body<SK>(a, ws); } \
-    extern "C" __global__ void __launch_bounds__(256) le_gq_xprepg_##TY(GqArgs a, u8 *ws) { gq_xprep_body<SK, true>(a, ws); }
+    extern "C" __global__ void __launch_bounds__(256) le_gq_xprepg_##TY(GqArgs a, u8 *ws) { gq_xprep_body<SK, true>(a, ws); } \
+    extern "C" __global__ void __launch_bounds__(256) le_gq_xprepw_##TY(GqArgs a, u8 *ws) { gq_xprepw_body<SK>(a, ws); }
 /* two code objects, compiled in parallel: the five types of the reference's mmq kernels, and the
  * four formats added beside them (LE_GQ_SET=2) */
 #if LE_GQ_SET == 2

@@ -129,6 +129,7 @@ struct le_ctx {
                                 8 (64x128, 4), 9 (32x128, 4), 10 (128x128, 4); Q4_K only: 11 (128x256, 2x4
                                 waves of 64x64), 12 (128x128, 2x4 waves of 64x32) */
     int gq_ksplit = 0;       /* generic GEMM K slices: 0 auto, else 1, 2, 4, 8 */
+    int mmg_xw = 1;          /* grouped pre-pass: one wave per pair (K <= 4096) instead of one block */
     std::vector<hipModule_t> mods;
     std::map<std::string, hipFunction_t> fns;
     std::string err;
@@ -559,6 +560,8 @@ int le_set_option(le_ctx *c, const char *name, int value) {
     } else if (n == "gq_cfg") {
         if (value < 0 || value > 12) return c->fail(LE_ERR_ARG, "gq_cfg must be 0..12");
         c->gq_cfg = value;
+    } else if (n == "mmg_xw") {
+        c->mmg_xw = value ? 1 : 0;
     } else if (n == "gq_ksplit") {
         if (value != 0 && value != 1 && value != 2 && value != 4 && value != 8)
             return c->fail(LE_ERR_ARG, "gq_ksplit must be 0, 1, 2, 4 or 8");
@@ -1007,7 +1010,7 @@ struct GqHostArgs {
     const void *const *ptrs;
     unsigned long long w_slot_bytes;
     const int *off, *in_idx, *out_idx;
-    int nslot, maxt, bm, pad;
+    int nslot, maxt, bm, npair;
     float *part;
     const void *const *ptrs2;
     const void *w2;
@@ -1152,13 +1155,22 @@ static int mm_grouped(le_ctx *c, int ty, const void *const *ptrs, const void *w,
         (unsigned long long)rows * le_row_bytes(ty, cols) >= (1ull << 32))
         return c->fail(LE_ERR_SHAPE, "grouped GEMM too large (32-bit weight or activation offsets)");
     GqHostArgs a{w, x, y, rows, cols, mp, mp, 1, ptrs, (unsigned long long)rows * le_row_bytes(ty, cols), off, in_idx,
-                 out_idx, nslot, maxt, BM, 0, nullptr, ptrs2, w2, y2, dual ? 1 : 0, 0, up};
+                 out_idx, nslot, maxt, BM, npair, nullptr, ptrs2, w2, y2, dual ? 1 : 0, 0, up};
     /* the tiles (slots split into BM pairs, slot by slot) are derived from off inside the two
      * launches, each block finding its own */
     void *args[] = {&a, &ws};
     char name[48];
-    snprintf(name, sizeof name, "le_gq_xprepg_%d", ty);
-    int rc = c->launch(name, dim3((unsigned)npair), 256, 0, (hipStream_t)stream, args); /* one block per pair */
+    /* from 256 pairs and up to K = 4096, one wave per pair (four pairs per block: 512 tokens
+     * 262 -> 248 us, 2048 tokens 668 -> 626 us a layer); else one block per pair, whose wider
+     * spread is ~1 us faster at 128 pairs */
+    int rc;
+    if (cols <= 4096 && npair >= 256 && c->mmg_xw) {
+        snprintf(name, sizeof name, "le_gq_xprepw_%d", ty);
+        rc = c->launch(name, dim3((unsigned)((npair + 3) / 4)), 256, 0, (hipStream_t)stream, args);
+    } else {
+        snprintf(name, sizeof name, "le_gq_xprepg_%d", ty);
+        rc = c->launch(name, dim3((unsigned)npair), 256, 0, (hipStream_t)stream, args);
+    }
     if (rc) return rc;
     snprintf(name, sizeof name, "le_gqg_%d_w%d%d_t%d%d", ty, WM, WN, TM, TN);
     return c->launch(name, dim3((unsigned)grid), nthr, lds_of(ci), (hipStream_t)stream, args);

@@ -133,3 +133,31 @@ def test_mm_grouped_many_slots(engine, name):
         wf = oracle.dequant_rows(ty, slab, rows, cols).astype(np.float64)
         mag = np.abs(xsel.astype(np.float64)) @ np.abs(wf).T
         check_close(got[out_idx[lo:hi]], want, mag)
+
+
+@pytest.mark.parametrize("name", ["Q4_K", "Q6_K", "Q8_0", "IQ2_XXS", "Q5_K"])
+@pytest.mark.parametrize("cols", [1024, 4096])
+def test_mm_grouped_prepass_forms(engine, name, cols):
+    """The activation pre-pass run one wave per pair (K <= 4096) and one block per pair give the
+    same bits: both take the row's max magnitude and convert every value the same way."""
+    import torch
+    ty = le.MV_TYPES[name]
+    counts = (0, 37, 200, 5, 64, 1)
+    nslot, rows, n_src = len(counts), 128, 90
+    print("mm_grouped prepass forms", name, cols, flush=True)
+    dq = dev(wbytes(ty, nslot * rows, cols, seed=80 + ty))
+    xs = dev(np.stack([acts(cols, 8100 + t) for t in range(n_src)]))
+    off, in_idx, out_idx = grouping(counts, n_src, seed=ty)
+    npair = int(off[-1])
+    outs = []
+    try:
+        for xw in (1, 0):
+            engine.set_option("mmg_xw", xw)
+            y = torch.full((npair, rows), float("nan"), dtype=torch.float32, device="cuda")
+            engine.mm_grouped(ty, dev(off), dev(in_idx), dev(out_idx), nslot, npair, xs, y, rows, cols, w=dq)
+            torch.cuda.synchronize()
+            outs.append(y.cpu().numpy())
+    finally:
+        engine.set_option("mmg_xw", 1)
+    assert np.isfinite(outs[0]).all()
+    assert np.array_equal(outs[0].view(np.uint32), outs[1].view(np.uint32))
