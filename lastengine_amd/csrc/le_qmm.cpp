@@ -810,8 +810,7 @@ static int moe_prefill(le_ctx *c, int ty_gate, int ty_down, const void *gate, co
     rc = mm_grouped(c, ty_down, dptr, down, nullptr, nullptr, off, out_idx, out_idx, n_exp, np, G, D, nullptr, hidden, ff, gws,
                     gws_bytes, st, U);
     if (rc) return rc;
-    long long no = (long long)n_tok * hidden;
-    const unsigned blocks = (unsigned)((no + 255) / 256 < 8192 ? (no + 255) / 256 : 8192);
+    const unsigned blocks = (unsigned)n_tok * (unsigned)((hidden + 1023) / 1024); /* (token, 1024 columns) */
     const float *Dc = D, *Wc = topw;
     void *cargs[] = {&Dc, &Wc, &out, &n_tok, &k, &hidden};
     return c->launch("le_moe_combine", dim3(blocks), 256, 0, st, cargs);

@@ -3434,64 +3434,93 @@ extern "C" __global__ void __launch_bounds__(512) le_moe_route_tok(MoePre a) {
     }
 }
 
-/* One block per expert e, two passes over the selection: the number of pairs routed to lower
- * experts (its offset), then its own pairs in pair (= token) order, so the grouping is
- * deterministic. The block for the last expert also writes off[n_exp]. */
+/* One block per expert e: its offset (the number of pairs routed to lower experts) and its own
+ * pairs in pair (= token) order, so the grouping is deterministic. A round covers 16384 pairs,
+ * 4096 per wave, the lane reading pair 64 j + lane at step j (coalesced), so that pair order is
+ * (wave, j, lane) order and a match's rank is a ballot's popcount below its lane. With more than
+ * 16384 pairs the offset takes a pass of its own first. The block for the last expert also writes
+ * off[n_exp]. */
 extern "C" __global__ void __launch_bounds__(256) le_moe_group(MoePre a) {
-    __shared__ int wsum[4];
+    __shared__ int wsum[4], wcnt[4];
     const int e = blockIdx.x, lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int npair = a.n_tok * a.k;
+    constexpr int R = 16384;
+    const bool one = npair <= R;
     int low = 0;
-    for (int p = threadIdx.x; p < npair; p += 256) low += a.topi[p] < e;
-    for (int o = 32; o > 0; o >>= 1) low += __shfl_xor(low, o);
-    if (lane == 0) wsum[wave] = low;
-    __syncthreads();
-    const int off = wsum[0] + wsum[1] + wsum[2] + wsum[3];
-    if (threadIdx.x == 0) a.off[e] = off;
-    int base = off;
-    __shared__ int wcnt[4];
-    /* 2048 pairs per round, 8 consecutive ones per thread: thread order is pair order, so an
-     * exclusive scan of the per-thread match counts gives each match its rank */
-    for (int p0 = 0; p0 < npair; p0 += 2048) {
-        const int pt = p0 + 8 * (int)threadIdx.x;
-        unsigned m = 0;
-#pragma unroll
-        for (int j = 0; j < 8; j++) m |= (pt + j < npair && a.topi[pt + j] == e ? 1u : 0u) << j;
-        const int cnt = __popc(m);
-        int incl = cnt;
-#pragma unroll
-        for (int o = 1; o < 64; o <<= 1) {
-            const int t = __shfl_up(incl, o);
-            if (lane >= o) incl += t;
+    if (!one)
+        for (int p = threadIdx.x; p < npair; p += 256) low += a.topi[p] < e;
+    const unsigned long long lt = (1ull << lane) - 1ull;
+    int off = 0, base = 0;
+    for (int r0 = 0; r0 < npair; r0 += R) {
+        const int pw = r0 + 4096 * wave + lane;
+        unsigned long long m = 0;
+#pragma unroll 16
+        for (int j = 0; j < 64; j++) {
+            const int p = pw + 64 * j;
+            const int v = p < npair ? a.topi[p] : 0x7fffffff;
+            if (one) low += v < e;
+            m |= (unsigned long long)(v == e) << j;
         }
-        if (lane == 63) wcnt[wave] = incl;
+        int c = __popcll(m);
+        for (int o = 32; o > 0; o >>= 1) c += __shfl_xor(c, o);
+        if (r0 == 0)
+            for (int o = 32; o > 0; o >>= 1) low += __shfl_xor(low, o);
+        if (lane == 0) {
+            wcnt[wave] = c;
+            if (r0 == 0) wsum[wave] = low;
+        }
         __syncthreads();
-        int before = 0;
-        for (int w = 0; w < wave; w++) before += wcnt[w];
-        int r = base + before + incl - cnt;
-#pragma unroll
-        for (int j = 0; j < 8; j++) {
-            if ((m >> j) & 1u) {
-                a.in_idx[r] = (pt + j) / a.k;
-                a.out_idx[r] = pt + j;
-                r++;
+        if (r0 == 0) {
+            off = wsum[0] + wsum[1] + wsum[2] + wsum[3];
+            if (threadIdx.x == 0) a.off[e] = off;
+        }
+        int r = off + base;
+        for (int w = 0; w < wave; w++) r += wcnt[w];
+        for (int j = 0; j < 64; j++) {
+            const bool hit = (m >> j) & 1ull;
+            const unsigned long long bj = __ballot(hit);
+            if (bj == 0ull) continue; /* uniform */
+            if (hit) {
+                const int p = pw + 64 * j, q = r + __popcll(bj & lt);
+                a.in_idx[q] = p / a.k;
+                a.out_idx[q] = p;
             }
+            r += __popcll(bj);
         }
         base += wcnt[0] + wcnt[1] + wcnt[2] + wcnt[3];
         __syncthreads();
     }
-    if (e == a.n_exp - 1 && threadIdx.x == 0) a.off[a.n_exp] = base;
+    if (e == a.n_exp - 1 && threadIdx.x == 0) a.off[a.n_exp] = off + base;
 }
 
-/* out[t][c] = sum over s < k of w[t k + s] * d[t k + s][c], added in selection order. */
+/* out[t][c] = sum over s < k of w[t k + s] * d[t k + s][c], added in selection order. Block
+ * (t, b) covers columns [1024 b, 1024 b + 1024) of token t, four per thread (as a float4 when the
+ * rows are 16-byte aligned). */
 extern "C" __global__ void __launch_bounds__(256) le_moe_combine(const float *d, const float *w, float *out, int n_tok, int k,
                                                                  int hidden) {
-    const long long n = (long long)n_tok * hidden;
-    for (long long i = (long long)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (long long)gridDim.x * blockDim.x) {
-        const int t = (int)(i / hidden), c = (int)(i - (long long)t * hidden);
-        float acc = 0.f;
-        for (int s = 0; s < k; s++) acc += w[t * k + s] * d[((size_t)t * k + s) * hidden + c];
-        out[i] = acc;
+    const int nb = (hidden + 1023) >> 10;
+    const int t = (int)blockIdx.x / nb, c0 = ((int)blockIdx.x - t * nb) * 1024 + 4 * (int)threadIdx.x;
+    if (t >= n_tok || c0 >= hidden) return;
+    const float *wt = w + (size_t)t * k;
+    const float *dt = d + (size_t)t * k * hidden;
+    float *o = out + (size_t)t * hidden;
+    if ((hidden & 3) == 0 && (((size_t)d | (size_t)out) & 15) == 0) {
+        float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
+        for (int s = 0; s < k; s++) {
+            const float ws = wt[s];
+            const float4 v = *(const float4 *)(dt + (size_t)s * hidden + c0);
+            acc.x += ws * v.x;
+            acc.y += ws * v.y;
+            acc.z += ws * v.z;
+            acc.w += ws * v.w;
+        }
+        *(float4 *)(o + c0) = acc;
+    } else {
+        for (int c = c0; c < c0 + 4 && c < hidden; c++) {
+            float acc = 0.f;
+            for (int s = 0; s < k; s++) acc += wt[s] * dt[(size_t)s * hidden + c];
+            o[c] = acc;
+        }
     }
 }
 #endif /* LE_PART_MOE */

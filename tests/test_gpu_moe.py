@@ -269,3 +269,9 @@ def test_moe_prefill_workspace(engine):
     with pytest.raises(le.LeError) as e:
         engine.moe(le.Q4_K, le.Q4_K, le.Q6_K, z, z, z, n_exp, k, hidden, ff, f, f, n_tok, f, ws=z, ws_bytes=need - 1)
     assert e.value.code == -7
+
+
+def test_moe_prefill_many_pairs(engine):
+    """More than 16384 pairs (the grouping kernel's round): 2100 tokens at k = 8, and a hidden size
+    that is not a multiple of the combine's 1024-column blocks."""
+    run(engine, le.Q8_0, le.Q8_0, 16, 8, 1280, 256, 2100, seed=930)
