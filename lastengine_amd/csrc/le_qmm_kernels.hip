@@ -3390,18 +3390,20 @@ struct MoePre {
     int n_tok, n_exp, k, pad;
 };
 
-/* One wave per token: k rounds of a wave-wide max (ties keep the lower expert), weights
- * exp(v - top) / sum in selection order, as the decode kernels compute them. */
-extern "C" __global__ void __launch_bounds__(512) le_moe_route_tok(MoePre a) {
-    const int lane = threadIdx.x & 63, t = blockIdx.x * 8 + (threadIdx.x >> 6);
-    if (t >= a.n_tok) return; /* uniform over the wave */
+/* Routing of one token by one wave: k rounds of a wave-wide max (ties keep the lower expert),
+ * weights exp(v - top) / sum in selection order, as the decode kernels compute them. Lane s < k
+ * ends with selection s's expert; the loads are split from the rounds so a wave can issue several
+ * tokens' loads first. */
+__device__ __forceinline__ void moe_route_load(const MoePre &a, int t, int lane, float (&vv)[MOE_LPASS]) {
     const int per = (a.n_exp + 63) >> 6;
-    float vv[MOE_LPASS];
 #pragma unroll
     for (int j = 0; j < MOE_LPASS; j++) {
         const int e = lane * per + j;
         vv[j] = j < per && e < a.n_exp ? a.logits[(size_t)t * a.n_exp + e] : -INFINITY;
     }
+}
+__device__ __forceinline__ int moe_route_pick(const MoePre &a, int t, int lane, float (&vv)[MOE_LPASS]) {
+    const int per = (a.n_exp + 63) >> 6;
     int my_e = 0;
     float my_v = 0.f;
     for (int r = 0; r < a.k; r++) {
@@ -3431,6 +3433,84 @@ extern "C" __global__ void __launch_bounds__(512) le_moe_route_tok(MoePre a) {
         a.topw[i] = ex / tot;
         if (a.idx_out) a.idx_out[i] = my_e;
         if (a.w_out) a.w_out[i] = ex / tot;
+    }
+    return my_e;
+}
+
+/* One wave per token. */
+extern "C" __global__ void __launch_bounds__(512) le_moe_route_tok(MoePre a) {
+    const int lane = threadIdx.x & 63, t = blockIdx.x * 8 + (threadIdx.x >> 6);
+    if (t >= a.n_tok) return; /* uniform over the wave */
+    float vv[MOE_LPASS];
+    moe_route_load(a, t, lane, vv);
+    (void)moe_route_pick(a, t, lane, vv);
+}
+
+/* Routing and grouping in one block of 16 waves for up to 64 tokens and 1024 pairs: wave w routes
+ * tokens w, w + 16, ... (all their logits loaded first), then thread p takes pair p: its rank
+ * among the pairs of its expert is the count of that expert in lower waves (per-wave histograms
+ * in LDS) plus the lower lanes of its own wave holding the same expert, so each expert's pairs
+ * come out in pair order, as le_moe_group orders them. */
+extern "C" __global__ void __launch_bounds__(1024) le_moe_route_group(MoePre a) {
+    __shared__ int hist[16][64 * MOE_LPASS];
+    __shared__ int sel[1024], base_e[64 * MOE_LPASS];
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int ne = a.n_exp, np = a.n_tok * a.k;
+    for (int i = tid; i < 16 * 64 * MOE_LPASS; i += 1024) (&hist[0][0])[i] = 0;
+    {
+        float vv[4][MOE_LPASS];
+#pragma unroll
+        for (int i = 0; i < 4; i++)
+            if (wave + 16 * i < a.n_tok) moe_route_load(a, wave + 16 * i, lane, vv[i]);
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            const int t = wave + 16 * i;
+            if (t < a.n_tok) {
+                const int e = moe_route_pick(a, t, lane, vv[i]);
+                if (lane < a.k) sel[t * a.k + lane] = e;
+            }
+        }
+    }
+    __syncthreads();
+    const int e = tid < np ? sel[tid] : -1;
+    int below = 0; /* lower lanes of this wave on the same expert */
+    for (int j = 0; j < 64; j++) below += j < lane && __builtin_amdgcn_readlane(e, j) == e ? 1 : 0;
+    if (e >= 0) atomicAdd(&hist[wave][e], 1);
+    __syncthreads();
+    if (wave == 0) { /* per-expert totals, exclusive scan over the experts, 4 per lane */
+        int c[MOE_LPASS], s = 0;
+#pragma unroll
+        for (int j = 0; j < MOE_LPASS; j++) {
+            const int x = lane * MOE_LPASS + j;
+            c[j] = 0;
+            if (x < ne)
+                for (int w = 0; w < 16; w++) c[j] += hist[w][x];
+            s += c[j];
+        }
+        int incl = s;
+#pragma unroll
+        for (int o = 1; o < 64; o <<= 1) {
+            const int y = __shfl_up(incl, o);
+            if (lane >= o) incl += y;
+        }
+        int run = incl - s;
+#pragma unroll
+        for (int j = 0; j < MOE_LPASS; j++) {
+            const int x = lane * MOE_LPASS + j;
+            if (x < ne) {
+                base_e[x] = run;
+                a.off[x] = run;
+            }
+            run += c[j];
+        }
+        if (lane == 63) a.off[ne] = incl;
+    }
+    __syncthreads();
+    if (e >= 0) {
+        int q = base_e[e] + below;
+        for (int w = 0; w < wave; w++) q += hist[w][e];
+        a.in_idx[q] = tid / a.k;
+        a.out_idx[q] = tid;
     }
 }
 

@@ -275,3 +275,37 @@ def test_moe_prefill_many_pairs(engine):
     """More than 16384 pairs (the grouping kernel's round): 2100 tokens at k = 8, and a hidden size
     that is not a multiple of the combine's 1024-column blocks."""
     run(engine, le.Q8_0, le.Q8_0, 16, 8, 1280, 256, 2100, seed=930)
+
+
+@pytest.mark.parametrize("n_tok,k,n_exp", [(11, 8, 128), (20, 16, 256), (32, 16, 64), (32, 8, 200), (33, 8, 128)])
+def test_moe_route_group_one_block(engine, n_tok, k, n_exp):
+    """Routing and grouping in one block (up to 32 tokens and 1024 pairs) give the same bits as the
+    per-token routing and per-expert grouping launches, including on tied logits."""
+    import torch
+    hidden, ff = 512, 256
+    g = wbytes(le.Q4_K, n_exp * ff, hidden, 940)
+    u = wbytes(le.Q4_K, n_exp * ff, hidden, 941)
+    d = wbytes(le.Q6_K, n_exp * hidden, ff, 942)
+    h = acts(n_tok * hidden, 943).reshape(n_tok, hidden)
+    lg = np.round(acts(n_tok * n_exp, 944).reshape(n_tok, n_exp) * 4) / 4  # many ties
+    ws = torch.empty(engine.moe_prefill_workspace_size(n_tok, k, n_exp, hidden, ff), dtype=torch.uint8, device="cuda")
+    outs = []
+    try:
+        for r1 in (1, 0):
+            engine.set_option("moe_route1", r1)
+            out = torch.empty(n_tok, hidden, dtype=torch.float32, device="cuda")
+            idx = torch.empty(n_tok, k, dtype=torch.int32, device="cuda")
+            w = torch.empty(n_tok, k, dtype=torch.float32, device="cuda")
+            engine.moe(le.Q4_K, le.Q4_K, le.Q6_K, dev(g), dev(u), dev(d), n_exp, k, hidden, ff, dev(lg), dev(h), n_tok,
+                       out, idx, w, ws=ws)
+            torch.cuda.synchronize()
+            outs.append((out.cpu().numpy(), idx.cpu().numpy(), w.cpu().numpy()))
+    finally:
+        engine.set_option("moe_route1", 1)
+    assert np.array_equal(outs[0][1], outs[1][1])
+    assert np.array_equal(outs[0][2].view(np.uint32), outs[1][2].view(np.uint32))
+    assert np.isfinite(outs[0][0]).all()
+    assert np.array_equal(outs[0][0].view(np.uint32), outs[1][0].view(np.uint32))
+    want, widx, _, mag = reference(le.Q4_K, le.Q6_K, g, u, d, n_exp, k, hidden, ff, h, lg)
+    assert np.array_equal(outs[0][1], widx)
+    check_close(outs[0][0], want, mag)
