@@ -3515,16 +3515,16 @@ extern "C" __global__ void __launch_bounds__(1024) le_moe_route_group(MoePre a) 
 }
 
 /* One block per expert e: its offset (the number of pairs routed to lower experts) and its own
- * pairs in pair (= token) order, so the grouping is deterministic. A round covers 16384 pairs,
- * 4096 per wave, the lane reading pair 64 j + lane at step j (coalesced), so that pair order is
- * (wave, j, lane) order and a match's rank is a ballot's popcount below its lane. With more than
- * 16384 pairs the offset takes a pass of its own first. The block for the last expert also writes
- * off[n_exp]. */
+ * pairs in pair (= token) order, so the grouping is deterministic. A round covers 256 J pairs
+ * (J = ceil(pairs / 256), at most 64), 64 J per wave, the lane reading pair 64 j + lane of its
+ * wave's run at step j (coalesced), so that pair order is (wave, j, lane) order and a match's rank
+ * is a ballot's popcount below its lane. With more than 16384 pairs the offset takes a pass of its
+ * own first. The block for the last expert also writes off[n_exp]. */
 extern "C" __global__ void __launch_bounds__(256) le_moe_group(MoePre a) {
     __shared__ int wsum[4], wcnt[4];
     const int e = blockIdx.x, lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int npair = a.n_tok * a.k;
-    constexpr int R = 16384;
+    const int J = min((npair + 255) >> 8, 64), R = 256 * J;
     const bool one = npair <= R;
     int low = 0;
     if (!one)
@@ -3532,10 +3532,10 @@ extern "C" __global__ void __launch_bounds__(256) le_moe_group(MoePre a) {
     const unsigned long long lt = (1ull << lane) - 1ull;
     int off = 0, base = 0;
     for (int r0 = 0; r0 < npair; r0 += R) {
-        const int pw = r0 + 4096 * wave + lane;
+        const int pw = r0 + 64 * J * wave + lane;
         unsigned long long m = 0;
 #pragma unroll 16
-        for (int j = 0; j < 64; j++) {
+        for (int j = 0; j < J; j++) {
             const int p = pw + 64 * j;
             const int v = p < npair ? a.topi[p] : 0x7fffffff;
             if (one) low += v < e;
@@ -3556,7 +3556,7 @@ extern "C" __global__ void __launch_bounds__(256) le_moe_group(MoePre a) {
         }
         int r = off + base;
         for (int w = 0; w < wave; w++) r += wcnt[w];
-        for (int j = 0; j < 64; j++) {
+        for (int j = 0; j < J; j++) {
             const bool hit = (m >> j) & 1ull;
             const unsigned long long bj = __ballot(hit);
             if (bj == 0ull) continue; /* uniform */
