@@ -277,7 +277,7 @@ def test_moe_prefill_many_pairs(engine):
     run(engine, le.Q8_0, le.Q8_0, 16, 8, 1280, 256, 2100, seed=930)
 
 
-@pytest.mark.parametrize("n_tok,k,n_exp", [(11, 8, 128), (20, 16, 256), (32, 16, 64), (32, 8, 200), (33, 8, 128)])
+@pytest.mark.parametrize("n_tok,k,n_exp", [(11, 8, 128), (20, 16, 256), (32, 16, 64), (32, 8, 200), (33, 8, 128), (12, 1, 3), (17, 2, 2)])
 def test_moe_route_group_one_block(engine, n_tok, k, n_exp):
     """Routing and grouping in one block (up to 32 tokens and 1024 pairs) give the same bits as the
     per-token routing and per-expert grouping launches, including on tied logits."""
@@ -309,3 +309,16 @@ def test_moe_route_group_one_block(engine, n_tok, k, n_exp):
     want, widx, _, mag = reference(le.Q4_K, le.Q6_K, g, u, d, n_exp, k, hidden, ff, h, lg)
     assert np.array_equal(outs[0][1], widx)
     check_close(outs[0][0], want, mag)
+
+
+@pytest.mark.parametrize("n_tok", [1, 5])
+def test_moe_grouped_form_few_tokens(engine, n_tok):
+    """The grouped form forced down to 1 and 5 tokens (one-block routing and grouping with most
+    waves holding no token) against the oracle."""
+    import torch
+    ws = torch.empty(engine.moe_prefill_workspace_size(n_tok, 8, 64, 512, 256), dtype=torch.uint8, device="cuda")
+    try:
+        engine.set_option("moe_prefill_min_tok", 1)
+        run(engine, le.Q4_K, le.Q6_K, 64, 8, 512, 256, n_tok, seed=960 + n_tok, ws=ws)
+    finally:
+        engine.set_option("moe_prefill_min_tok", 11)
