@@ -225,7 +225,7 @@ int le_gemm_noalloc(le_ctx *ctx, int ty, const void *w, const float *x, int m, f
  * weights renormalised over the k, out[t*hidden ...] = sum_s w_s * down_e(silu(gate_e h_t) * up_e h_t).
  * gate/up: n_exp slabs of ff x hidden (types ty_gate, ty_up), down: n_exp slabs of hidden x ff
  * (ty_down), slab e at e * rows * row_bytes. Routing and grouping by expert run on the device
- * (no host synchronisation); each routed expert's weights are read once per call (for 9..15
+ * (no host synchronisation); each routed expert's weights are read once per call (for 9..10
  * tokens once per 8-token chunk; in the grouped form once per tile of its pairs). idx_out/w_out
  * (n_tok*k, optional) receive the selection. ws: device workspace of le_moe_workspace_size bytes
  * (type pairs other than (Q4_K, Q6_K), (Q4_K, Q4_K), (Q6_K, Q6_K), (Q8_0, Q8_0), (IQ2_XXS, IQ3_XXS),
