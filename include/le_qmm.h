@@ -98,6 +98,8 @@ const char *le_last_error(const le_ctx *ctx);
  *     128x128 on 4 waves; Q4_K only, 2 x 4 waves: 11 128x256, 12 128x128), "gq_ksplit" its K
  *     slices (0 auto, 1, 2, 4, 8); "mmg_xw" (0/1) the grouped form's activation pre-pass one wave
  *     per pair from 256 pairs when K <= 4096 (default) or one block per pair (same results);
+ *     "mmg_w4" (0/1) grouped 32-pair tiles of Q6_K / Q8_0 / Q4_0 on 4-wave 32x128 blocks (default)
+ *     or 8-wave 32x256 ones (same results);
  *     "moe_route1" (0/1) the grouped MoE's routing and grouping in one block up to 32 tokens
  *     (default) or two launches (same results);
  *     "gm_mh" (0/1) Q4_K with 3..16 tokens on the staged f16 MFMA kernel (tokens as MFMA rows),

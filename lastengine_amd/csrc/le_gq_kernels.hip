@@ -1229,7 +1229,7 @@ extern "C" __global__ void __launch_bounds__(256) le_gq_ksum(GqArgs a) {
         gq_body<TY, WM, WN, TM, TN, true, 2>(a, ws);                                                                     \
     }
 #define LE_GQ(TY) LE_GQ_(TY, 1, 4, 1, 2) LE_GQ_(TY, 1, 4, 2, 2) LE_GQ_(TY, 1, 4, 4, 2) LE_GQ_(TY, 2, 2, 2, 2) \
-    LE_GQ_(TY, 1, 8, 2, 1) LE_GQ_(TY, 1, 8, 4, 1) LE_GQ_(TY, 1, 8, 1, 1) LE_GQ_(TY, 1, 4, 2, 1) LE_GQ_(TY, 1, 4, 1, 1) LE_GQ_(TY, 1, 4, 4, 1) LE_GQG_(TY, 1, 8, 2, 1) LE_GQG_(TY, 1, 8, 4, 1) LE_GQG_(TY, 2, 2, 2, 2) LE_GQG_(TY, 1, 8, 1, 1)
+    LE_GQ_(TY, 1, 8, 2, 1) LE_GQ_(TY, 1, 8, 4, 1) LE_GQ_(TY, 1, 8, 1, 1) LE_GQ_(TY, 1, 4, 2, 1) LE_GQ_(TY, 1, 4, 1, 1) LE_GQ_(TY, 1, 4, 4, 1) LE_GQG_(TY, 1, 8, 2, 1) LE_GQG_(TY, 1, 8, 4, 1) LE_GQG_(TY, 2, 2, 2, 2) LE_GQG_(TY, 1, 8, 1, 1) LE_GQG_(TY, 1, 4, 1, 1)
 #if LE_GQ_SET == 2
 LE_GQ(2) LE_GQ(11) LE_GQ(13) LE_GQ(22)
 #else

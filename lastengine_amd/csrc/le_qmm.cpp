@@ -130,6 +130,7 @@ struct le_ctx {
                                 waves of 64x64), 12 (128x128, 2x4 waves of 64x32) */
     int gq_ksplit = 0;       /* generic GEMM K slices: 0 auto, else 1, 2, 4, 8 */
     int moe_route1 = 1;      /* grouped MoE up to 32 tokens: routing and grouping in one block */
+    int mmg_w4 = 1;          /* grouped 32-pair tiles: 4-wave 32 x 128 blocks where 8-wave ones fill half the LDS */
     int mmg_xw = 1;          /* grouped pre-pass: one wave per pair (K <= 4096) instead of one block */
     std::vector<hipModule_t> mods;
     std::map<std::string, hipFunction_t> fns;
@@ -563,6 +564,8 @@ int le_set_option(le_ctx *c, const char *name, int value) {
         c->gq_cfg = value;
     } else if (n == "moe_route1") {
         c->moe_route1 = value ? 1 : 0;
+    } else if (n == "mmg_w4") {
+        c->mmg_w4 = value ? 1 : 0;
     } else if (n == "mmg_xw") {
         c->mmg_xw = value ? 1 : 0;
     } else if (n == "gq_ksplit") {
@@ -1146,7 +1149,7 @@ static int mm_grouped(le_ctx *c, int ty, const void *const *ptrs, const void *w,
     const size_t need = le_mm_grouped_workspace_size(ty, nslot, npair, cols);
     if (ws_bytes < need) return c->fail(LE_ERR_WORKSPACE, "workspace needs %zu bytes", need);
     if (npair == 0) return LE_OK;
-    static const int cfgs[7][4] = {{1, 4, 1, 2}, {1, 4, 2, 2}, {1, 4, 4, 2}, {2, 2, 2, 2}, {1, 8, 2, 1}, {1, 8, 4, 1}, {1, 8, 1, 1}};
+    static const int cfgs[8][4] = {{1, 4, 1, 2}, {1, 4, 2, 2}, {1, 4, 4, 2}, {2, 2, 2, 2}, {1, 8, 2, 1}, {1, 8, 4, 1}, {1, 8, 1, 1}, {1, 4, 1, 1}};
     int ci = mmg_cfg(nslot, npair);
     const int srec = gq_srec(ty);
     auto lds_of = [&](int i) {
@@ -1154,6 +1157,9 @@ static int mm_grouped(le_ctx *c, int ty, const void *const *ptrs, const void *w,
         return (size_t)2 * (BN * gq_slot(ty) + BM * 256) + (size_t)2 * (BM / 32) * srec + gq_tab(ty);
     };
     if (lds_of(ci) > c->lds_limit) ci = 3; /* 128 x 128 on 4 waves */
+    /* 32-pair tiles whose 8-wave block would hold more than half the LDS (Q6_K, Q8_0: one block
+     * per CU): 32 x 128 on 4 waves, several blocks per CU */
+    if (ci == 6 && c->mmg_w4 && 2 * lds_of(6) > c->lds_limit) ci = 7;
     const int WM = cfgs[ci][0], WN = cfgs[ci][1], TM = cfgs[ci][2], TN = cfgs[ci][3];
     const int BM = 32 * TM * WM, BN = 32 * TN * WN, nthr = 64 * WM * WN;
     if (BM != mmg_bm(nslot, npair) && !(ci == 3 && mmg_bm(nslot, npair) == 128))

@@ -161,3 +161,38 @@ def test_mm_grouped_prepass_forms(engine, name, cols):
         engine.set_option("mmg_xw", 1)
     assert np.isfinite(outs[0]).all()
     assert np.array_equal(outs[0].view(np.uint32), outs[1].view(np.uint32))
+
+
+@pytest.mark.parametrize("name", ["Q6_K", "Q8_0", "Q4_0"])
+def test_mm_grouped_four_wave_tiles(engine, name):
+    """Sparse slots (32-pair tiles) of the types whose 8-wave block fills half the LDS run on 4-wave
+    32 x 128 blocks; both give the same bits (a pair's sum runs over K in the same order)."""
+    import torch
+    ty = le.MV_TYPES[name]
+    counts = (3, 0, 17, 1, 40, 2, 9)
+    nslot, rows, cols, n_src = len(counts), 320, 768, 60
+    q = wbytes(ty, nslot * rows, cols, seed=95 + ty)
+    xs_h = np.stack([acts(cols, 8500 + t) for t in range(n_src)])
+    off, in_idx, out_idx = grouping(counts, n_src, seed=ty + 5)
+    npair = int(off[-1])
+    dq, xs = dev(q), dev(xs_h)
+    outs = []
+    try:
+        for w4 in (1, 0):
+            engine.set_option("mmg_w4", w4)
+            y = torch.full((npair, rows), float("nan"), dtype=torch.float32, device="cuda")
+            engine.mm_grouped(ty, dev(off), dev(in_idx), dev(out_idx), nslot, npair, xs, y, rows, cols, w=dq)
+            torch.cuda.synchronize()
+            outs.append(y.cpu().numpy())
+    finally:
+        engine.set_option("mmg_w4", 1)
+    assert np.isfinite(outs[0]).all()
+    assert np.array_equal(outs[0].view(np.uint32), outs[1].view(np.uint32))
+    rbs = le.row_bytes(ty, cols) * rows
+    for s in (2, 4):
+        lo, hi = off[s], off[s + 1]
+        slab = q.reshape(-1)[s * rbs:(s + 1) * rbs]
+        xsel = xs_h[in_idx[lo:hi]]
+        want = oracle.matmat(ty, slab, rows, cols, xsel)
+        wf = oracle.dequant_rows(ty, slab, rows, cols).astype(np.float64)
+        check_close(outs[0][out_idx[lo:hi]], want, np.abs(xsel.astype(np.float64)) @ np.abs(wf).T)
